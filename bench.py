@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X PJRT plugin's hot path (one GPU).
+
+Metric: "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak;
+fusion GB/s % HBM peak".
+
+  value      causal SDPA forward, bf16, B=4 H=16 D=128, S=8192 (config C3 at
+             the north_star target length), TFLOP/s with FLOPs = 2*B*H*S^2*D
+             (causal half of 4*B*H*S^2*D).  One step = one mk_sdpa_fwd launch
+             over inputs already resident in HBM.
+  sweep      the same for S in 512..16384
+  fusions    C2 LayerNorm / GELU / reduce_sum / argmax and C4 gather /
+             scatter-add, GB/s of algorithmic bytes and fraction of 8 TB/s
+  roofline   the dominant kernel (SDPA at S=8192): achieved TFLOP/s from HIP
+             events on the launch stream, against 2516.6 TFLOP/s bf16 dense
+  cpu_baseline  the float64 numpy oracle on a bounded sample of (b, h) pairs
+             of the same workload, extrapolated to all pairs
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only sdpa|fusions]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "mccl-jax_amd"))
+
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline"], default=None)
+    ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def dev_bf16(bits, torch, np):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def time_launches(torch, fn, steps, warmup):
+    """Average milliseconds per call of fn (one or more launches on torch's
+    current stream), HIP events around the whole timed region."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def sdpa_flops(B, H, S, D):
+    return 2.0 * B * H * S * S * D
+
+
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary
+    (profiles/<name>.txt, line 'traffic_bytes_per_launch: N'), else None."""
+    p = os.path.join(ROOT, "profiles", name + ".txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline_sdpa(np, S, budget_s):
+    """The oracle (float64 numpy) on (b, h) pairs of the C3 workload until the
+    time budget is used, extrapolated to all B*H = 64 pairs."""
+    from oracle import bf16, inputs, ops
+
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+        cores = len(os.sched_getaffinity(0))
+        limiter = threadpool_limits(limits=cores)
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        limiter, threads = None, 1
+    d = inputs.c3_sdpa(S)
+    B, H, D = 4, 16, 128
+    scale = 1 / math.sqrt(D)
+    done = 0
+    t0 = time.perf_counter()
+    for bh in range(B * H):
+        b, h = divmod(bh, H)
+        q, k, v = (bf16.from_bf16_bits(d[n][b, h]) for n in ("q", "k", "v"))
+        ops.sdpa(q, k, v, scale, causal=True)
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    per_pair = el / done
+    total_s = per_pair * B * H
+    return {
+        "value": round(sdpa_flops(B, H, S, D) / total_s / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"float64 numpy oracle (ops.sdpa) on {done} of {B*H} (b,h) pairs at S={S}, "
+                  f"{el:.1f}s, extrapolated x{B*H/done:.1f}; BLAS threads={threads}",
+    }
+
+
+def run_sdpa(torch, np, K, args):
+    from oracle import inputs
+
+    B, H, D = 4, 16, 128
+    scale = 1 / math.sqrt(D)
+    seqs = [args.seq] if args.only == "headline" else [512, 1024, 2048, 4096, 8192, 16384]
+    sweep = {}
+    head = None
+    for S in seqs:
+        d = inputs.c3_sdpa(S)
+        q, k, v = (dev_bf16(d[n], torch, np) for n in ("q", "k", "v"))
+        del d
+        o = torch.empty_like(q)
+        steps = args.steps if S == args.seq else max(5, min(args.steps, 20))
+        ms = time_launches(torch, lambda: K.sdpa_fwd(q, k, v, scale, True, out=o), steps, args.warmup)
+        tf = sdpa_flops(B, H, S, D) / (ms * 1e-3) / 1e12
+        sweep[str(S)] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+        log(f"sdpa S={S}: {ms:.3f} ms  {tf:.1f} TFLOP/s  ({100*tf/PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+        if S == args.seq:
+            head = (ms, tf, steps)
+        del q, k, v, o
+        torch.cuda.empty_cache()
+    return sweep, head
+
+
+def run_fusions(torch, np, K, args):
+    from oracle import inputs
+
+    res = {}
+
+    def rec(name, nbytes, fn, steps=20):
+        ms = time_launches(torch, fn, steps, 3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 5), "bytes": int(nbytes), "gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"{name}: {ms*1e3:.1f} us  {gbs:.0f} GB/s ({100*gbs/PEAK_HBM_GBS:.1f}% of HBM peak)")
+
+    d = inputs.c2_layernorm()
+    x, g, b = (dev_bf16(d[n], torch, np) for n in ("x", "gamma", "beta"))
+    rec("layernorm_8192x4096_bf16", 8192 * 4096 * 2 * 2 + 4096 * 2 * 2, lambda: K.layernorm(x, g, b, 1e-5))
+    del x, g, b, d
+    x = dev_bf16(inputs.c2_gelu()["x"], torch, np)
+    y = torch.empty_like(x)
+    rec("gelu_tanh_8192x16384_bf16", x.numel() * 4, lambda: K.gelu_tanh(x, out=y))
+    del x, y
+    x = dev_bf16(inputs.c2_reduce()["x"], torch, np)
+    rec("reduce_sum_65536x1024_bf16", x.numel() * 2 + 65536 * 4, lambda: K.row_reduce(x, "sum"))
+    rec("argmax_65536x1024_bf16", x.numel() * 2 + 65536 * 4, lambda: K.row_argmax(x, with_values=False))
+    del x
+    d = inputs.c4_indexing()
+    table = dev_bf16(d["table_bf16"], torch, np)
+    ids = torch.from_numpy(d["ids"]).cuda()
+    rec("gather_32x2048_from_50257x768_bf16", 65536 * 4 + 2 * 65536 * 768 * 2, lambda: K.gather_rows(table, ids))
+    tf = torch.from_numpy(d["table_f32"]).cuda()
+    gr = torch.from_numpy(d["grads"]).cuda()
+    out = torch.empty_like(tf)
+    ws = torch.empty(int(K.lib().mk_scatter_add_workspace_bytes(50257, 65536)), dtype=torch.uint8, device="cuda")
+    idf = ids.reshape(-1)
+    rec("scatter_add_65536x768_into_50257x768_f32", 65536 * 768 * 4 + 65536 * 4 + 2 * 50257 * 768 * 4,
+        lambda: K.scatter_add_rows(tf, idf, gr, out=out, workspace=ws))
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU: multi-GPU execution "
+                          "(RCCL collectives) is out of scope; run with --gpus 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device"}))
+        sys.exit(1)
+    from mi355x_pjrt import kernels as K
+
+    K.lib()
+    torch.cuda.init()
+    sweep, head, fusions = {}, None, {}
+    if args.only in (None, "sdpa", "headline"):
+        sweep, head = run_sdpa(torch, np, K, args)
+    if args.only in (None, "fusions"):
+        fusions = run_fusions(torch, np, K, args)
+    if head is None:
+        print(json.dumps({"fusions": fusions}))
+        return
+    ms, tf, steps = head
+    S = args.seq
+    cpu = None if args.no_cpu else cpu_baseline_sdpa(np, S, args.cpu_seconds)
+    traffic = read_traffic(f"sdpa_fwd_causal_b4h16d128_s{S}_traffic")
+    line = {
+        "metric": "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak; fusion GB/s % HBM peak",
+        "value": round(tf, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: numpy PCG64 N(0,1)/sqrt(128) bf16, seeds 3000-3002",
+        "config": {"workload": f"C3 causal SDPA forward B=4 H=16 S={S} D=128 bf16 (mk_sdpa_fwd)",
+                   "batch": 4, "heads": 16, "seq_len": S, "head_dim": 128, "causal": True,
+                   "flops_per_step": sdpa_flops(4, 16, S, 128)},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+        "fusions": fusions,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

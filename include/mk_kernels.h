@@ -1,0 +1,244 @@
+/*
+ * mk_kernels.h — C-ABI of the hand-written gfx950 (MI355X) HIP kernels.
+ *
+ * This is the "thin C-ABI" the jam compiler lowers StableHLO into.  Every
+ * entry point takes device pointers, explicit element counts / strides and a
+ * hipStream_t passed as `void*`; none of them allocates device memory except
+ * where a `workspace` argument is documented (callers size it with the
+ * matching *_workspace_bytes query).  All launches are asynchronous on the
+ * given stream.  Return value: MK_OK (0) or an MK_ERR_* code; the message for
+ * the last failure on the calling thread is available from mk_last_error().
+ *
+ * Each entry point replaces one group of MPSGraph calls of the reference
+ * (Lazarus-931/mccl-jax, Metal backend); the replaced call sites are cited as
+ * path:line into that repository.
+ */
+#ifndef MI355X_MK_KERNELS_H_
+#define MI355X_MK_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  Numeric values equal PJRT_Buffer_Type's so the plugin can
+ * pass them through unchanged (third_party/xla/pjrt/c/pjrt_c_api.h:626-660). */
+typedef enum mk_dtype {
+  MK_PRED = 1, MK_S8 = 2, MK_S16 = 3, MK_S32 = 4, MK_S64 = 5,
+  MK_U8 = 6, MK_U16 = 7, MK_U32 = 8, MK_U64 = 9,
+  MK_F16 = 10, MK_F32 = 11, MK_F64 = 12, MK_BF16 = 13
+} mk_dtype;
+
+enum {
+  MK_OK = 0,
+  MK_ERR_INVALID = 1,     /* bad shape / stride / pointer / dtype combination */
+  MK_ERR_UNSUPPORTED = 2, /* valid request this build has no kernel for       */
+  MK_ERR_LAUNCH = 3       /* hipLaunchKernel / hipGetLastError failure         */
+};
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* mk_last_error(void);
+/* ABI version of this header (bumped on incompatible change). */
+int mk_abi_version(void);
+/* Number of visible HIP devices (0 on a host without a GPU; never fails). */
+int mk_device_count(void);
+
+/* ------------------------------------------------------------------------
+ * a4  dot_general → batched GEMM on MFMA.
+ * Replaces: src/jam/ops/linalg.mm:98 (matrixMultiplicationWithPrimaryTensor)
+ *           and the operand transposes/reshapes at linalg.mm:34-45,68-90.
+ *
+ * C[b][m][n] = sum_k A[b][m][k] * B[b][k][n]  (+ bias[n]) (then ReLU)
+ *   A element (b,m,k) at  A + b*a_bs + m*a_ms + k*a_ks   (elements, not bytes)
+ *   B element (b,k,n) at  B + b*b_bs + k*b_ks + n*b_ns
+ *   C element (b,m,n) at  C + b*c_bs + m*c_ms + n        (row-major rows)
+ * One of (a_ms, a_ks) and one of (b_ks, b_ns) must be 1 (unit stride); the
+ * other operand stride is the leading dimension.  ab_type ∈ {MK_F32, MK_BF16,
+ * MK_F16}; c_type ∈ {MK_F32, MK_BF16, MK_F16}; accumulation is always fp32.
+ * epilogue: 0 none, 1 +bias, 2 +bias then max(.,0).  bias has c_type, may be
+ * NULL when epilogue == 0.
+ * ---------------------------------------------------------------------- */
+int mk_gemm(void* stream, int ab_type, int c_type,
+            int64_t batch, int64_t M, int64_t N, int64_t K,
+            const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,
+            const void* B, int64_t b_bs, int64_t b_ks, int64_t b_ns,
+            void* C, int64_t c_bs, int64_t c_ms,
+            const void* bias, int epilogue);
+
+/* ------------------------------------------------------------------------
+ * a5+a6  fused scaled-dot-product attention (flash attention, forward).
+ * Replaces the unfused chain the reference emits for the jnp attention
+ * pattern: linalg.mm:98 (Q·Kᵀ) → elementwise.mm:87 (softMaxWithTensor,
+ * matched by TrySoftmax elementwise.mm:71-89) → linalg.mm:98 (P·V), with the
+ * causal mask built by shape.mm:249-256 (iota), binary.mm:84-109 (compare)
+ * and binary.mm:77-82 (select).  The [S,S] score matrix never exists.
+ *
+ * O[b,h,i,:] = softmax_j( scale * Q[b,h,i,:]·K[b,h,j,:] , j ≤ i+Sk-Sq if causal ) · V[b,h,j,:]
+ * Tensors are bf16 with D contiguous; the other strides are in elements:
+ *   X element (b,h,s,d) at X + b*x_bs + h*x_hs + s*x_ss + d.
+ * D ∈ {64, 128}.  Accumulation fp32, online softmax in fp32.
+ * lse (optional, may be NULL): fp32 [B,H,Sq] row log-sum-exp (natural log) of
+ * the scaled, masked scores, written densely.
+ * ---------------------------------------------------------------------- */
+int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
+                const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,
+                const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ss,
+                void* o, int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                float scale, int causal, float* lse);
+
+/* ------------------------------------------------------------------------
+ * a8  row reduction over the innermost (contiguous) axis.
+ * Replaces: src/jam/ops/reduce.mm:97-106 (reductionSum/Max/Min/Product).
+ * y[r] = op_{c<cols} x[r*cols + c]; in_type ∈ {MK_BF16, MK_F16, MK_F32},
+ * out_type ∈ {MK_F32, MK_BF16, MK_F16}; fp32 accumulation.
+ * op: 0 sum, 1 max, 2 min, 3 product.  init is folded in (StableHLO reduce
+ * init operand; the reference ignores it, reduce.mm:79-108).
+ * ---------------------------------------------------------------------- */
+int mk_row_reduce(void* stream, int in_type, int out_type, int op,
+                  int64_t rows, int64_t cols, const void* x, float init, void* y);
+
+/* ------------------------------------------------------------------------
+ * a9  fused row max + argmax / min + argmin (bit-exact).
+ * Replaces: src/jam/ops/reduce.mm:29-43 (DetectArgReduce) and 61-66
+ * (reductionMaximum + reductionArgMaximum).  Semantics are XLA's variadic
+ * reduce as emitted by jnp.argmax: larger value wins (smaller for argmin),
+ * NaN beats every number, ties go to the lower index.
+ * in_type ∈ {MK_BF16, MK_F16, MK_F32}; values (same dtype as x) may be NULL;
+ * index_type ∈ {MK_S32, MK_S64}.
+ * ---------------------------------------------------------------------- */
+int mk_row_argmax(void* stream, int in_type, int is_min, int64_t rows, int64_t cols,
+                  const void* x, void* values, int index_type, void* indices);
+
+/* ------------------------------------------------------------------------
+ * a7+a8  fused LayerNorm over the innermost axis (one HBM pass).
+ * Replaces the reduce(reduce.mm:97-106) + elementwise(elementwise.mm:91-171)
+ * chain of the "LayerNorm" composition validated in docs/ops.md:79.
+ * y = (x - mean) * rsqrt(var + eps) * gamma + beta, stats in fp32 (two-pass
+ * in registers), x/gamma/beta/y of io_type ∈ {MK_BF16, MK_F32}.
+ * gamma / beta may be NULL (treated as 1 / 0).
+ * ---------------------------------------------------------------------- */
+int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t cols,
+                 const void* x, const void* gamma, const void* beta, float eps, void* y);
+
+/* ------------------------------------------------------------------------
+ * a7  fused GELU (tanh approximation), fp32 math, one rounding on store.
+ * Replaces the multiply/add/tanh chain of elementwise.mm:91-171 for the
+ * "GELU-tanh" composition (docs/ops.md:79).
+ * y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); io_type ∈ {MK_BF16, MK_F32}.
+ * ---------------------------------------------------------------------- */
+int mk_gelu_tanh(void* stream, int io_type, int64_t n, const void* x, void* y);
+
+/* ------------------------------------------------------------------------
+ * a7  generic fused elementwise program (register-resident interpreter).
+ * Replaces one MPSGraph node per elementwise op (elementwise.mm:91-171,
+ * binary.mm:65-109, shape.mm:270-293 convert, structural.mm:87-96 broadcast)
+ * with ONE launch per fused chain.  Every element of the output shape runs
+ * the same straight-line program over fp32 registers.
+ *
+ * Shapes: the output has `rank` ≤ 6 dims (`dims`); input t is addressed with
+ * element strides in_strides[t*6 + d] (0 for broadcast dims) — so
+ * broadcast_in_dim / transpose feeding the chain are folded into addressing.
+ * Program: n_instr instructions of 4 int32 {opcode, dst, a, b} plus a third
+ * operand for select/clamp packed in the high 16 bits of `b` (see
+ * mk_ew_op).  Registers 0..n_inputs-1 are preloaded with the inputs
+ * (converted to fp32 / int32 semantics per in_types); constants come from
+ * `consts` (fp32) via MK_EW_CONST.  Register `out_reg` is stored, converted
+ * to out_type.  At most 32 registers, 64 instructions, 8 inputs.
+ * ---------------------------------------------------------------------- */
+typedef enum mk_ew_op {
+  MK_EW_CONST = 0,  /* r[dst] = consts[a]                       */
+  MK_EW_ADD, MK_EW_SUB, MK_EW_MUL, MK_EW_DIV, MK_EW_MAX, MK_EW_MIN, MK_EW_POW,
+  MK_EW_NEG, MK_EW_EXP, MK_EW_LOG, MK_EW_TANH, MK_EW_SQRT, MK_EW_RSQRT, MK_EW_ABS,
+  MK_EW_LOGISTIC,
+  MK_EW_CMP_EQ, MK_EW_CMP_NE, MK_EW_CMP_LT, MK_EW_CMP_LE, MK_EW_CMP_GT, MK_EW_CMP_GE,
+  MK_EW_SELECT,     /* r[dst] = r[a] != 0 ? r[b & 0xffff] : r[b >> 16]          */
+  MK_EW_CLAMP,      /* r[dst] = min(max(r[b & 0xffff], r[a]), r[b >> 16])       */
+  MK_EW_ROUND_BF16, /* r[dst] = fp32(bf16_rne(r[a])) — per-op bf16 rounding    */
+  MK_EW_ROUND_F16,  /* r[dst] = fp32(f16_rne(r[a]))                            */
+  MK_EW_FLOOR, MK_EW_CEIL, MK_EW_SIGN,
+  MK_EW_AND, MK_EW_OR, MK_EW_NOT,   /* on 0/1 predicates                        */
+  MK_EW_MOV,
+  MK_EW_CMP_LT_S32, MK_EW_CMP_GE_S32, /* integer compares on raw int32 bits    */
+  MK_EW_ADD_S32, MK_EW_SUB_S32, MK_EW_MUL_S32,
+  MK_EW_S32_TO_F32, MK_EW_F32_TO_S32,  /* C-style truncation toward zero        */
+  MK_EW_ERF,
+  MK_EW_NUM_OPS
+} mk_ew_op;
+
+int mk_ew_program(void* stream, int rank, const int64_t* dims,
+                  int n_inputs, const void* const* inputs, const int* in_types,
+                  const int64_t* in_strides,
+                  int n_instr, const int32_t* program, const float* consts, int n_consts,
+                  int out_reg, int out_type, void* out);
+
+/* ------------------------------------------------------------------------
+ * a10  row gather (embedding lookup), bit-exact copy.
+ * Replaces: src/jam/ops/gather_scatter.mm:185-196 (gatherWithUpdatesTensor
+ * axis:0) including the index clamp to [0, n_rows-1] at 180-183.
+ * out[i, :] = table[clamp(ids[i], 0, n_rows-1), :]; row_bytes % 4 == 0.
+ * ids: int32 (index_type MK_S32) or int64 (MK_S64).
+ * ---------------------------------------------------------------------- */
+int mk_gather_rows(void* stream, int64_t n_rows, int64_t row_bytes, const void* table,
+                   int index_type, int64_t n_ids, const void* ids, void* out);
+
+/* ------------------------------------------------------------------------
+ * a11  deterministic scatter-add of rows (bit-exact vs in-order fp32).
+ * Replaces: src/jam/ops/gather_scatter.mm:322-327 (scatterNDWithDataTensor
+ * mode:Add), whose GPU accumulation order is unspecified.
+ * out[r, :] = table[r, :] + sum over i with ids[i]==r, in increasing i, of
+ *             updates[i, :]   (fp32 adds applied sequentially in that order)
+ * ids outside [0, n_rows) are dropped (StableHLO scatter semantics, JAX's
+ * FILL_OR_DROP mode).  table and out may alias (in-place).  dtype ∈ {MK_F32,
+ * MK_BF16}: bf16 rounds after every add, exactly as a sequential bf16 scatter.
+ * workspace: device memory of mk_scatter_add_workspace_bytes(n_rows, n_ids).
+ * ---------------------------------------------------------------------- */
+size_t mk_scatter_add_workspace_bytes(int64_t n_rows, int64_t n_ids);
+int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int64_t row_len,
+                        const void* table, int index_type, int64_t n_ids, const void* ids,
+                        const void* updates, void* out, void* workspace);
+
+/* ------------------------------------------------------------------------
+ * a6  iota.  Replaces src/jam/ops/shape.mm:249-256 (coordinateAlongAxis +
+ * castTensor).  out[idx] = idx[dim] for every index of the row-major shape.
+ * out_type ∈ {MK_S32, MK_S64, MK_F32, MK_BF16, MK_U32}.
+ * ---------------------------------------------------------------------- */
+int mk_iota(void* stream, int out_type, int rank, const int64_t* dims, int dim, void* out);
+
+/* ------------------------------------------------------------------------
+ * a12  strided copy (transpose / broadcast / slice materialisation).
+ * Replaces shape.mm:28-40 (transposeTensor), shape.mm:163-172 and
+ * structural.mm:87-96 (broadcastTensor) when the consumer cannot fold the
+ * layout into its own addressing.  out is dense row-major over `dims`;
+ * in element (i0..ir) at in + sum_d i_d * in_strides[d] (elements, may be 0).
+ * elem_bytes ∈ {1, 2, 4, 8}; rank ≤ 6.
+ * ---------------------------------------------------------------------- */
+int mk_copy_strided(void* stream, int elem_bytes, int rank, const int64_t* dims,
+                    const void* in, const int64_t* in_strides, void* out);
+
+/* ------------------------------------------------------------------------
+ * a5  standalone row softmax (fallback when the SDPA pattern does not match).
+ * Replaces src/jam/ops/elementwise.mm:87 (softMaxWithTensor).
+ * y[r,:] = softmax(x[r,:]); io_type ∈ {MK_BF16, MK_F32}; fp32 math.
+ * ---------------------------------------------------------------------- */
+int mk_softmax_rows(void* stream, int io_type, int64_t rows, int64_t cols,
+                    const void* x, void* y);
+
+/* ------------------------------------------------------------------------
+ * dtype conversion (a7 `convert`, shape.mm:270-293), element-wise, dense.
+ * Float→int truncates toward zero; unsigned sources convert as unsigned
+ * (the unsigned fix-up of shape.mm:280-291); float→bf16/f16 is RNE.
+ * ---------------------------------------------------------------------- */
+int mk_convert(void* stream, int in_type, int out_type, int64_t n, const void* in, void* out);
+
+/* Fill n elements of elem_bytes (1,2,4,8) with the bit pattern `pattern`
+ * (a kernel, so it is safe inside captured HIP graphs). */
+int mk_fill(void* stream, int elem_bytes, int64_t n, uint64_t pattern, void* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_MK_KERNELS_H_ */

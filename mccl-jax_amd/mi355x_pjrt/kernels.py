@@ -1,0 +1,267 @@
+"""Python entry to the gfx950 kernels through the C-ABI (include/mk_kernels.h).
+
+torch provides device memory and the current HIP stream; every call goes
+through ctypes into libmk_kernels.so.  There is no CPU or torch fallback:
+if the library is missing the call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+MK = dict(PRED=1, S8=2, S16=3, S32=4, S64=5, U8=6, U16=7, U32=8, U64=9,
+          F16=10, F32=11, F64=12, BF16=13)
+
+_TORCH_TO_MK = {
+    torch.bool: MK["PRED"], torch.int8: MK["S8"], torch.int16: MK["S16"],
+    torch.int32: MK["S32"], torch.int64: MK["S64"], torch.uint8: MK["U8"],
+    torch.float16: MK["F16"], torch.float32: MK["F32"], torch.float64: MK["F64"],
+    torch.bfloat16: MK["BF16"],
+}
+_MK_TO_TORCH = {v: k for k, v in _TORCH_TO_MK.items()}
+
+REDUCE_OP = {"sum": 0, "max": 1, "min": 2, "prod": 3}
+
+
+def mk_dtype(t: torch.dtype) -> int:
+    try:
+        return _TORCH_TO_MK[t]
+    except KeyError as e:
+        raise TypeError(f"no mk dtype for {t}") from e
+
+
+def lib():
+    return _lib.load_kernels()
+
+
+def _stream(stream=None) -> ctypes.c_void_p:
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _check(rc, what):
+    _lib.check(rc, what)
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("mk kernels take device tensors")
+
+
+# ------------------------------------------------------------------ a5 attention
+def sdpa_fwd(q, k, v, scale: float, causal: bool = True, out=None, lse=None, stream=None):
+    """O = softmax(scale Q Kᵀ [causal tril mask]) V on [B, H, S, D] bf16 views
+    (any B/H/S strides, D contiguous)."""
+    _require_cuda(q, k, v)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    for t in (q, k, v):
+        if t.dtype != torch.bfloat16 or t.stride(3) != 1:
+            raise ValueError("sdpa_fwd: bf16 tensors with contiguous head_dim")
+    if out is None:
+        out = torch.empty((B, H, Sq, D), dtype=torch.bfloat16, device=q.device)
+    rc = lib().mk_sdpa_fwd(
+        _stream(stream), B, H, Sq, Sk, D,
+        _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        float(scale), int(bool(causal)), _ptr(lse))
+    _check(rc, "mk_sdpa_fwd")
+    return out
+
+
+# ------------------------------------------------------------------ a4 GEMM
+def gemm(a, b, out_dtype=None, bias=None, relu=False, out=None, stream=None):
+    """C[b] = A[b] @ B[b] (+bias)(relu) for 2-D or 3-D views with a unit
+    stride along one dim of each operand (transposed views are free)."""
+    _require_cuda(a, b)
+    if a.dtype != b.dtype:
+        raise ValueError("gemm: operand dtypes differ")
+    squeeze = a.dim() == 2
+    a3 = a.unsqueeze(0) if squeeze else a
+    b3 = b.unsqueeze(0) if b.dim() == 2 else b
+    batch, M, K = a3.shape
+    _, K2, N = b3.shape
+    if K2 != K:
+        raise ValueError("gemm: inner dims differ")
+    out_dtype = out_dtype or a.dtype
+    if out is None:
+        out = torch.empty((batch, M, N), dtype=out_dtype, device=a.device)
+    o3 = out.unsqueeze(0) if out.dim() == 2 else out
+    b_bs = b3.stride(0) if b3.shape[0] == batch and b.dim() == 3 else 0
+    epi = 0 if bias is None else (2 if relu else 1)
+    rc = lib().mk_gemm(
+        _stream(stream), mk_dtype(a.dtype), mk_dtype(out_dtype), batch, M, N, K,
+        _ptr(a3), a3.stride(0), a3.stride(1), a3.stride(2),
+        _ptr(b3), b_bs, b3.stride(1), b3.stride(2),
+        _ptr(o3), o3.stride(0), o3.stride(1), _ptr(bias), epi)
+    _check(rc, "mk_gemm")
+    return out[0] if squeeze and out.dim() == 3 else out
+
+
+# ------------------------------------------------------------------ a8/a9 reductions
+def row_reduce(x, op="sum", out_dtype=torch.float32, init=None, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    rows = x.numel() // x.shape[-1] if x.numel() else 0
+    y = torch.empty(x.shape[:-1], dtype=out_dtype, device=x.device)
+    if init is None:
+        init = {"sum": 0.0, "max": float("-inf"), "min": float("inf"), "prod": 1.0}[op]
+    rc = lib().mk_row_reduce(_stream(stream), mk_dtype(x.dtype), mk_dtype(out_dtype),
+                             REDUCE_OP[op], rows, x.shape[-1], _ptr(x), float(init), _ptr(y))
+    _check(rc, "mk_row_reduce")
+    return y
+
+
+def row_argmax(x, is_min=False, index_dtype=torch.int32, with_values=True, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    rows = x.numel() // x.shape[-1] if x.numel() else 0
+    idx = torch.empty(x.shape[:-1], dtype=index_dtype, device=x.device)
+    vals = torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device) if with_values else None
+    rc = lib().mk_row_argmax(_stream(stream), mk_dtype(x.dtype), int(is_min), rows, x.shape[-1],
+                             _ptr(x), _ptr(vals), mk_dtype(index_dtype), _ptr(idx))
+    _check(rc, "mk_row_argmax")
+    return idx, vals
+
+
+def layernorm(x, gamma=None, beta=None, eps=1e-5, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    rows = x.numel() // x.shape[-1]
+    rc = lib().mk_layernorm(_stream(stream), mk_dtype(x.dtype), rows, x.shape[-1], _ptr(x),
+                            _ptr(gamma), _ptr(beta), float(eps), _ptr(y))
+    _check(rc, "mk_layernorm")
+    return y
+
+
+def softmax_rows(x, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    rows = x.numel() // x.shape[-1]
+    rc = lib().mk_softmax_rows(_stream(stream), mk_dtype(x.dtype), rows, x.shape[-1], _ptr(x), _ptr(y))
+    _check(rc, "mk_softmax_rows")
+    return y
+
+
+# ------------------------------------------------------------------ a7 elementwise
+def gelu_tanh(x, out=None, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    y = torch.empty_like(x) if out is None else out
+    rc = lib().mk_gelu_tanh(_stream(stream), mk_dtype(x.dtype), x.numel(), _ptr(x), _ptr(y))
+    _check(rc, "mk_gelu_tanh")
+    return y
+
+
+def convert(x, dtype, stream=None):
+    _require_cuda(x)
+    x = x.contiguous()
+    y = torch.empty(x.shape, dtype=dtype, device=x.device)
+    rc = lib().mk_convert(_stream(stream), mk_dtype(x.dtype), mk_dtype(dtype), x.numel(), _ptr(x), _ptr(y))
+    _check(rc, "mk_convert")
+    return y
+
+
+def fill(out, pattern: int, stream=None):
+    rc = lib().mk_fill(_stream(stream), out.element_size(), out.numel(), ctypes.c_uint64(pattern), _ptr(out))
+    _check(rc, "mk_fill")
+    return out
+
+
+def iota(shape, dim, dtype=torch.int32, device="cuda", stream=None):
+    out = torch.empty(shape, dtype=dtype, device=device)
+    dims = (ctypes.c_int64 * len(shape))(*shape)
+    rc = lib().mk_iota(_stream(stream), mk_dtype(dtype), len(shape), dims, dim, _ptr(out))
+    _check(rc, "mk_iota")
+    return out
+
+
+def copy_strided(x, stream=None):
+    """Materialise any strided view (transpose / broadcast via expand) densely."""
+    _require_cuda(x)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    r = x.dim()
+    dims = (ctypes.c_int64 * max(r, 1))(*x.shape)
+    strides = (ctypes.c_int64 * max(r, 1))(*x.stride())
+    rc = lib().mk_copy_strided(_stream(stream), x.element_size(), r, dims, _ptr(x), strides, _ptr(out))
+    _check(rc, "mk_copy_strided")
+    return out
+
+
+EW = dict(CONST=0, ADD=1, SUB=2, MUL=3, DIV=4, MAX=5, MIN=6, POW=7, NEG=8, EXP=9, LOG=10,
+          TANH=11, SQRT=12, RSQRT=13, ABS=14, LOGISTIC=15, CMP_EQ=16, CMP_NE=17, CMP_LT=18,
+          CMP_LE=19, CMP_GT=20, CMP_GE=21, SELECT=22, CLAMP=23, ROUND_BF16=24, ROUND_F16=25,
+          FLOOR=26, CEIL=27, SIGN=28, AND=29, OR=30, NOT=31, MOV=32, CMP_LT_S32=33,
+          CMP_GE_S32=34, ADD_S32=35, SUB_S32=36, MUL_S32=37, S32_TO_F32=38, F32_TO_S32=39, ERF=40)
+
+
+def ew_program(shape, inputs, program, consts, out_reg, out_dtype, stream=None):
+    """Run a fused elementwise program.  `inputs` are tensors broadcast (via
+    torch.expand views) to `shape`; `program` is a list of (op, dst, a, b)."""
+    rank = len(shape)
+    dev = inputs[0].device if inputs else "cuda"
+    out = torch.empty(shape, dtype=out_dtype, device=dev)
+    ptrs = (ctypes.c_void_p * max(len(inputs), 1))(*[t.data_ptr() for t in inputs])
+    types = (ctypes.c_int * max(len(inputs), 1))(*[mk_dtype(t.dtype) for t in inputs])
+    strides = (ctypes.c_int64 * (6 * max(len(inputs), 1)))()
+    for i, t in enumerate(inputs):
+        tt = t.expand(shape)
+        for d in range(rank):
+            strides[6 * i + d] = tt.stride(d)
+    prog = (ctypes.c_int32 * (4 * max(len(program), 1)))()
+    for p, ins in enumerate(program):
+        for j in range(4):
+            prog[4 * p + j] = int(ins[j])
+    cst = (ctypes.c_float * max(len(consts), 1))(*consts)
+    dims = (ctypes.c_int64 * max(rank, 1))(*shape)
+    rc = lib().mk_ew_program(_stream(stream), rank, dims, len(inputs), ptrs, types, strides,
+                             len(program), prog, cst, len(consts), out_reg, mk_dtype(out_dtype),
+                             _ptr(out))
+    _check(rc, "mk_ew_program")
+    return out
+
+
+# ------------------------------------------------------------------ a10/a11 indexing
+def gather_rows(table, ids, stream=None):
+    _require_cuda(table, ids)
+    table = table.contiguous()
+    ids_c = ids.contiguous()
+    out = torch.empty(tuple(ids.shape) + tuple(table.shape[1:]), dtype=table.dtype, device=table.device)
+    row_bytes = table[0].numel() * table.element_size() if table.shape[0] else 0
+    rc = lib().mk_gather_rows(_stream(stream), table.shape[0], row_bytes, _ptr(table),
+                              mk_dtype(ids.dtype), ids_c.numel(), _ptr(ids_c), _ptr(out))
+    _check(rc, "mk_gather_rows")
+    return out
+
+
+def scatter_add_rows(table, ids, updates, out=None, workspace=None, stream=None):
+    """out[r] = table[r] + sum_{i: ids[i]==r, in increasing i} updates[i]
+    (bit-exact sequential order); out may be `table` itself (in place)."""
+    _require_cuda(table, ids, updates)
+    ids_c = ids.contiguous().reshape(-1)
+    n_rows, row_len = table.shape[0], table[0].numel()
+    if out is None:
+        out = torch.empty_like(table)
+    nbytes = lib().mk_scatter_add_workspace_bytes(n_rows, ids_c.numel())
+    if workspace is None:
+        workspace = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=table.device)
+    elif workspace.numel() < nbytes:
+        raise ValueError("scatter_add_rows: workspace too small")
+    rc = lib().mk_scatter_add_rows(_stream(stream), mk_dtype(table.dtype), n_rows, row_len,
+                                   _ptr(table), mk_dtype(ids.dtype), ids_c.numel(), _ptr(ids_c),
+                                   _ptr(updates.contiguous()), _ptr(out), _ptr(workspace))
+    _check(rc, "mk_scatter_add_rows")
+    return out

@@ -1,0 +1,474 @@
+// Elementwise kernels: fused GELU(tanh), the generic fused elementwise
+// program, convert, fill, iota and strided copy (transpose / broadcast).
+//
+// Streaming kernels move 16 bytes per lane per access (dwordx4) and each
+// thread keeps kUnroll independent vectors in flight, so one wave has
+// 64 × 16 × kUnroll bytes outstanding — what HBM3E needs to approach peak.
+#include "mk_common.h"
+
+#include <cmath>
+
+namespace mk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3).
+// Using 1 + tanh(u) = 2 / (1 + exp(-2u)) gives gelu = x / (1 + exp(-2u)),
+// which has no cancellation for negative x and needs one exp2 + one rcp.
+// exp(-2u) = exp2(x * (c0 + c1 x^2)) with c0 = -2 sqrt(2/pi) log2(e).
+__device__ inline float gelu_tanh_f32(float x) {
+  constexpr float kC0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float kC1 = kC0 * 0.044715f;
+  const float t = x * fmaf(x * x, kC1, kC0);
+  const float e = exp2f(t);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+template <typename T> struct V16;
+template <> struct V16<uint16_t> { using V = u16x8; static constexpr int N = 8; };
+template <> struct V16<float> { using V = f32x4; static constexpr int N = 4; };
+
+template <typename T>
+__device__ inline float cvt_in(T v) {
+  if constexpr (sizeof(T) == 2) return bf16_to_f32(v);
+  else return v;
+}
+template <typename T>
+__device__ inline T cvt_out(float v) {
+  if constexpr (sizeof(T) == 2) return f32_to_bf16(v);
+  else return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gelu_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                          int64_t nvec) {
+  using V = typename V16<T>::V;
+  constexpr int N = V16<T>::N;
+  const V* xv = reinterpret_cast<const V*>(x);
+  V* yv = reinterpret_cast<V*>(y);
+  const int64_t base = int64_t(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+  V a[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    int64_t i = base + int64_t(u) * kBlock;
+    if (i < nvec) a[u] = ld_stream(&xv[i]);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    int64_t i = base + int64_t(u) * kBlock;
+    if (i < nvec) {
+      V o;
+#pragma unroll
+      for (int j = 0; j < N; ++j) o.v[j] = cvt_out<T>(gelu_tanh_f32(cvt_in<T>(a[u].v[j])));
+      st_stream(&yv[i], o);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gelu_scalar_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                             int64_t begin, int64_t n) {
+  int64_t i = begin + int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < n) y[i] = cvt_out<T>(gelu_tanh_f32(cvt_in<T>(x[i])));
+}
+
+// ------------------------------------------------------------------ ew program
+constexpr int kEwMaxRank = 6;
+constexpr int kEwMaxInputs = 8;
+constexpr int kEwMaxRegs = 32;
+constexpr int kEwMaxInstr = 64;
+constexpr int kEwMaxConsts = 64;
+
+struct EwArgs {
+  const void* in[kEwMaxInputs];
+  int in_type[kEwMaxInputs];
+  int in_mode[kEwMaxInputs];  // 0 scalar (offset 0), 1 dense (offset = i), 2 strided
+  int64_t in_stride[kEwMaxInputs][kEwMaxRank];
+  int64_t dims[kEwMaxRank];
+  int rank;
+  int n_inputs;
+  int n_instr;
+  int out_reg;
+  int out_type;
+  int need_index;  // some input is strided: decompose the linear index
+  int32_t prog[kEwMaxInstr][4];
+  float consts[kEwMaxConsts];
+};
+
+__device__ inline float as_f(int32_t i) { return __int_as_float(i); }
+__device__ inline int32_t as_i(float f) { return __float_as_int(f); }
+
+// Integer-typed inputs are kept as raw int32 bits in the fp32 register file
+// when the program uses the *_S32 opcodes; float-typed inputs are widened.
+__device__ inline float ew_load(const void* p, int64_t i, int t) {
+  if (t == MK_S32 || t == MK_U32) return as_f(reinterpret_cast<const int32_t*>(p)[i]);
+  if (t == MK_S64) return as_f(int32_t(reinterpret_cast<const int64_t*>(p)[i]));
+  if (t == MK_PRED || t == MK_U8) return float(reinterpret_cast<const uint8_t*>(p)[i]);
+  return load_as_f32(p, i, t);
+}
+__device__ inline void ew_store(void* p, int64_t i, int t, float v) {
+  if (t == MK_S32 || t == MK_U32) reinterpret_cast<int32_t*>(p)[i] = as_i(v);
+  else if (t == MK_S64) reinterpret_cast<int64_t*>(p)[i] = int64_t(as_i(v));
+  else store_from_f32(p, i, t, v);
+}
+
+__device__ inline float sign_f(float x) {
+  return x > 0.f ? 1.f : (x < 0.f ? -1.f : x);  // keeps ±0 and NaN
+}
+
+// The whole program block travels as a by-value kernel argument (< 2 KiB),
+// so a launch needs no device-side staging buffer.
+__global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n, void* out) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  float r[kEwMaxRegs];
+#pragma unroll
+  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
+  const int rank = A.rank;
+  int64_t idx[kEwMaxRank];
+  if (A.need_index) {
+    int64_t rem = i;
+    for (int d = rank - 1; d >= 0; --d) {
+      idx[d] = rem % A.dims[d];
+      rem /= A.dims[d];
+    }
+  }
+  for (int t = 0; t < A.n_inputs; ++t) {
+    int64_t off = 0;
+    if (A.in_mode[t] == 1) {
+      off = i;
+    } else if (A.in_mode[t] == 2) {
+      for (int d = 0; d < rank; ++d) off += idx[d] * A.in_stride[t][d];
+    }
+    r[t] = ew_load(A.in[t], off, A.in_type[t]);
+  }
+  for (int p = 0; p < A.n_instr; ++p) {
+    const int op = A.prog[p][0], dst = A.prog[p][1], a = A.prog[p][2], b = A.prog[p][3];
+    const float va = r[a];
+    const float vb = r[b & 0xffff];
+    float o;
+    switch (op) {
+      case MK_EW_CONST: o = A.consts[a]; break;
+      case MK_EW_ADD: o = va + vb; break;
+      case MK_EW_SUB: o = va - vb; break;
+      case MK_EW_MUL: o = va * vb; break;
+      case MK_EW_DIV: o = va / vb; break;
+      case MK_EW_MAX: o = (va != va || vb != vb) ? __builtin_nanf("") : fmaxf(va, vb); break;
+      case MK_EW_MIN: o = (va != va || vb != vb) ? __builtin_nanf("") : fminf(va, vb); break;
+      case MK_EW_POW: o = powf(va, vb); break;
+      case MK_EW_NEG: o = -va; break;
+      case MK_EW_EXP: o = expf(va); break;
+      case MK_EW_LOG: o = logf(va); break;
+      case MK_EW_TANH: o = tanhf(va); break;
+      case MK_EW_SQRT: o = sqrtf(va); break;
+      case MK_EW_RSQRT: o = 1.f / sqrtf(va); break;
+      case MK_EW_ABS: o = fabsf(va); break;
+      case MK_EW_LOGISTIC: o = 1.f / (1.f + expf(-va)); break;
+      case MK_EW_CMP_EQ: o = va == vb ? 1.f : 0.f; break;
+      case MK_EW_CMP_NE: o = va != vb ? 1.f : 0.f; break;
+      case MK_EW_CMP_LT: o = va < vb ? 1.f : 0.f; break;
+      case MK_EW_CMP_LE: o = va <= vb ? 1.f : 0.f; break;
+      case MK_EW_CMP_GT: o = va > vb ? 1.f : 0.f; break;
+      case MK_EW_CMP_GE: o = va >= vb ? 1.f : 0.f; break;
+      case MK_EW_SELECT: o = va != 0.f ? r[b & 0xffff] : r[(b >> 16) & 0xffff]; break;
+      case MK_EW_CLAMP: {
+        const float lo = r[b & 0xffff], hi = r[(b >> 16) & 0xffff];
+        o = fminf(fmaxf(va, lo), hi);
+        break;
+      }
+      case MK_EW_ROUND_BF16: o = bf16_to_f32(f32_to_bf16(va)); break;
+      case MK_EW_ROUND_F16: o = f16_to_f32(f32_to_f16(va)); break;
+      case MK_EW_FLOOR: o = floorf(va); break;
+      case MK_EW_CEIL: o = ceilf(va); break;
+      case MK_EW_SIGN: o = sign_f(va); break;
+      case MK_EW_AND: o = (va != 0.f && vb != 0.f) ? 1.f : 0.f; break;
+      case MK_EW_OR: o = (va != 0.f || vb != 0.f) ? 1.f : 0.f; break;
+      case MK_EW_NOT: o = va == 0.f ? 1.f : 0.f; break;
+      case MK_EW_MOV: o = va; break;
+      case MK_EW_CMP_LT_S32: o = as_i(va) < as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_CMP_GE_S32: o = as_i(va) >= as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_ADD_S32: o = as_f(as_i(va) + as_i(vb)); break;
+      case MK_EW_SUB_S32: o = as_f(as_i(va) - as_i(vb)); break;
+      case MK_EW_MUL_S32: o = as_f(as_i(va) * as_i(vb)); break;
+      case MK_EW_S32_TO_F32: o = float(as_i(va)); break;
+      case MK_EW_F32_TO_S32: o = as_f(int32_t(va)); break;
+      case MK_EW_ERF: o = erff(va); break;
+      default: o = 0.f; break;
+    }
+    r[dst] = o;
+  }
+  ew_store(out, i, A.out_type, r[A.out_reg]);
+}
+
+// ------------------------------------------------------------------ convert / fill / iota
+__global__ __launch_bounds__(kBlock) void convert_kernel(const void* __restrict__ in, int in_type,
+                                                         void* __restrict__ out, int out_type,
+                                                         int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const bool in_int = in_type == MK_S8 || in_type == MK_S16 || in_type == MK_S32 ||
+                      in_type == MK_S64 || in_type == MK_U8 || in_type == MK_U16 ||
+                      in_type == MK_U32 || in_type == MK_U64 || in_type == MK_PRED;
+  const bool out_int = out_type == MK_S8 || out_type == MK_S16 || out_type == MK_S32 ||
+                       out_type == MK_S64 || out_type == MK_U8 || out_type == MK_U16 ||
+                       out_type == MK_U32 || out_type == MK_U64;
+  if (in_int && out_int) {
+    int64_t v;
+    switch (in_type) {
+      case MK_S8: v = reinterpret_cast<const int8_t*>(in)[i]; break;
+      case MK_S16: v = reinterpret_cast<const int16_t*>(in)[i]; break;
+      case MK_S32: v = reinterpret_cast<const int32_t*>(in)[i]; break;
+      case MK_S64: v = reinterpret_cast<const int64_t*>(in)[i]; break;
+      case MK_U8: case MK_PRED: v = reinterpret_cast<const uint8_t*>(in)[i]; break;
+      case MK_U16: v = reinterpret_cast<const uint16_t*>(in)[i]; break;
+      case MK_U32: v = reinterpret_cast<const uint32_t*>(in)[i]; break;
+      default: v = int64_t(reinterpret_cast<const uint64_t*>(in)[i]); break;
+    }
+    switch (out_type) {
+      case MK_S8: reinterpret_cast<int8_t*>(out)[i] = int8_t(v); break;
+      case MK_S16: reinterpret_cast<int16_t*>(out)[i] = int16_t(v); break;
+      case MK_S32: reinterpret_cast<int32_t*>(out)[i] = int32_t(v); break;
+      case MK_S64: reinterpret_cast<int64_t*>(out)[i] = v; break;
+      case MK_U8: reinterpret_cast<uint8_t*>(out)[i] = uint8_t(v); break;
+      case MK_U16: reinterpret_cast<uint16_t*>(out)[i] = uint16_t(v); break;
+      case MK_U32: reinterpret_cast<uint32_t*>(out)[i] = uint32_t(v); break;
+      default: reinterpret_cast<uint64_t*>(out)[i] = uint64_t(v); break;
+    }
+    return;
+  }
+  if (out_type == MK_PRED) {
+    reinterpret_cast<uint8_t*>(out)[i] = load_as_f32(in, i, in_type) != 0.f;
+    return;
+  }
+  if (in_type == MK_F64 && out_type == MK_F32) {
+    reinterpret_cast<float*>(out)[i] = float(reinterpret_cast<const double*>(in)[i]);
+    return;
+  }
+  if (out_type == MK_F64) {
+    reinterpret_cast<double*>(out)[i] = in_type == MK_F64 ? reinterpret_cast<const double*>(in)[i]
+                                                          : double(load_as_f32(in, i, in_type));
+    return;
+  }
+  store_from_f32(out, i, out_type, load_as_f32(in, i, in_type));
+}
+
+template <typename W>
+__global__ __launch_bounds__(kBlock) void fill_kernel(W* __restrict__ out, W v, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+
+__global__ __launch_bounds__(kBlock) void iota_kernel(void* __restrict__ out, int out_type, int64_t n,
+                                                      int64_t inner, int64_t dim_size) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const int64_t c = (i / inner) % dim_size;
+  switch (out_type) {
+    case MK_S32: reinterpret_cast<int32_t*>(out)[i] = int32_t(c); break;
+    case MK_U32: reinterpret_cast<uint32_t*>(out)[i] = uint32_t(c); break;
+    case MK_S64: reinterpret_cast<int64_t*>(out)[i] = c; break;
+    default: store_from_f32(out, i, out_type, float(c)); break;
+  }
+}
+
+struct CopyArgs {
+  int64_t dims[kEwMaxRank];
+  int64_t strides[kEwMaxRank];
+  int rank;
+};
+
+template <typename W>
+__global__ __launch_bounds__(kBlock) void copy_strided_kernel(const W* __restrict__ in,
+                                                              W* __restrict__ out, int64_t n,
+                                                              CopyArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  int64_t rem = i, off = 0;
+  for (int d = a.rank - 1; d >= 0; --d) {
+    const int64_t q = rem / a.dims[d];
+    off += (rem - q * a.dims[d]) * a.strides[d];
+    rem = q;
+  }
+  out[i] = in[off];
+}
+
+inline unsigned blocks_for(int64_t n, int per_block) {
+  return unsigned((n + per_block - 1) / per_block);
+}
+
+}  // namespace
+}  // namespace mk
+
+using namespace mk;
+
+extern "C" int mk_gelu_tanh(void* stream, int io_type, int64_t n, const void* x, void* y) {
+  clear_error();
+  if (n < 0) return fail(MK_ERR_INVALID, "mk_gelu_tanh: negative n");
+  if (n == 0) return MK_OK;
+  if (!x || !y) return fail(MK_ERR_INVALID, "mk_gelu_tanh: null pointer");
+  hipStream_t s = as_stream(stream);
+  const bool al = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  if (io_type == MK_BF16 || io_type == MK_F32) {
+    const int N = io_type == MK_BF16 ? 8 : 4;
+    const int64_t nvec = al ? n / N : 0;
+    if (nvec > 0) {
+      dim3 g(blocks_for(nvec, kBlock * kUnroll));
+      if (io_type == MK_BF16)
+        hipLaunchKernelGGL(gelu_vec_kernel<uint16_t>, g, dim3(kBlock), 0, s, (const uint16_t*)x, (uint16_t*)y, nvec);
+      else
+        hipLaunchKernelGGL(gelu_vec_kernel<float>, g, dim3(kBlock), 0, s, (const float*)x, (float*)y, nvec);
+    }
+    const int64_t begin = nvec * N;
+    if (begin < n) {
+      dim3 g(blocks_for(n - begin, kBlock));
+      if (io_type == MK_BF16)
+        hipLaunchKernelGGL(gelu_scalar_kernel<uint16_t>, g, dim3(kBlock), 0, s, (const uint16_t*)x, (uint16_t*)y, begin, n);
+      else
+        hipLaunchKernelGGL(gelu_scalar_kernel<float>, g, dim3(kBlock), 0, s, (const float*)x, (float*)y, begin, n);
+    }
+    return check_launch("mk_gelu_tanh");
+  }
+  return fail(MK_ERR_UNSUPPORTED, "mk_gelu_tanh: io_type must be bf16/f32");
+}
+
+extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_inputs,
+                             const void* const* inputs, const int* in_types,
+                             const int64_t* in_strides, int n_instr, const int32_t* program,
+                             const float* consts, int n_consts, int out_reg, int out_type,
+                             void* out) {
+  clear_error();
+  if (rank < 0 || rank > kEwMaxRank) return fail(MK_ERR_INVALID, "mk_ew_program: rank > 6");
+  if (n_inputs < 0 || n_inputs > kEwMaxInputs) return fail(MK_ERR_INVALID, "mk_ew_program: > 8 inputs");
+  if (n_instr < 0 || n_instr > kEwMaxInstr) return fail(MK_ERR_INVALID, "mk_ew_program: > 64 instructions");
+  if (n_consts < 0 || n_consts > kEwMaxConsts) return fail(MK_ERR_INVALID, "mk_ew_program: > 64 constants");
+  if (out_reg < 0 || out_reg >= kEwMaxRegs) return fail(MK_ERR_INVALID, "mk_ew_program: bad out_reg");
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    if (dims[d] < 0) return fail(MK_ERR_INVALID, "mk_ew_program: negative dim");
+    n *= dims[d];
+  }
+  if (n == 0) return MK_OK;
+  if (!out) return fail(MK_ERR_INVALID, "mk_ew_program: null output");
+  EwArgs a{};
+  a.rank = rank;
+  a.n_inputs = n_inputs;
+  a.n_instr = n_instr;
+  a.out_reg = out_reg;
+  a.out_type = out_type;
+  for (int d = 0; d < rank; ++d) a.dims[d] = dims[d];
+  int need_index = 0;
+  for (int t = 0; t < n_inputs; ++t) {
+    if (!inputs[t]) return fail(MK_ERR_INVALID, "mk_ew_program: null input");
+    a.in[t] = inputs[t];
+    a.in_type[t] = in_types[t];
+    if (dtype_bytes(in_types[t]) == 0) return fail(MK_ERR_UNSUPPORTED, "mk_ew_program: bad input dtype");
+    int64_t expect = 1;
+    bool is_dense = true, is_scalar = true;
+    for (int d = rank - 1; d >= 0; --d) {
+      const int64_t st = in_strides[t * kEwMaxRank + d];
+      a.in_stride[t][d] = dims[d] == 1 ? 0 : st;  // size-1 dims never contribute
+      if (dims[d] != 1 && st != expect) is_dense = false;
+      if (dims[d] != 1 && st != 0) is_scalar = false;
+      expect *= dims[d];
+    }
+    a.in_mode[t] = is_scalar ? 0 : (is_dense ? 1 : 2);
+    need_index |= (a.in_mode[t] == 2);
+  }
+  for (int p = 0; p < n_instr; ++p) {
+    const int32_t* ins = program + 4 * p;
+    if (ins[0] < 0 || ins[0] >= MK_EW_NUM_OPS) return fail(MK_ERR_INVALID, "mk_ew_program: bad opcode");
+    if (ins[1] < 0 || ins[1] >= kEwMaxRegs) return fail(MK_ERR_INVALID, "mk_ew_program: bad dst register");
+    if (ins[0] == MK_EW_CONST) {
+      if (ins[2] < 0 || ins[2] >= n_consts) return fail(MK_ERR_INVALID, "mk_ew_program: bad constant index");
+    } else {
+      if (ins[2] < 0 || ins[2] >= kEwMaxRegs || (ins[3] & 0xffff) >= kEwMaxRegs ||
+          ((ins[3] >> 16) & 0xffff) >= kEwMaxRegs)
+        return fail(MK_ERR_INVALID, "mk_ew_program: bad source register");
+    }
+    for (int k = 0; k < 4; ++k) a.prog[p][k] = ins[k];
+  }
+  for (int c = 0; c < n_consts; ++c) a.consts[c] = consts[c];
+  a.need_index = need_index;
+  hipLaunchKernelGGL(ew_program_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
+                     as_stream(stream), a, n, out);
+  return check_launch("mk_ew_program");
+}
+
+extern "C" int mk_convert(void* stream, int in_type, int out_type, int64_t n, const void* in,
+                          void* out) {
+  clear_error();
+  if (n < 0) return fail(MK_ERR_INVALID, "mk_convert: negative n");
+  if (dtype_bytes(in_type) == 0 || dtype_bytes(out_type) == 0)
+    return fail(MK_ERR_UNSUPPORTED, "mk_convert: unsupported dtype");
+  if (n == 0) return MK_OK;
+  if (!in || !out) return fail(MK_ERR_INVALID, "mk_convert: null pointer");
+  hipLaunchKernelGGL(convert_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, as_stream(stream),
+                     in, in_type, out, out_type, n);
+  return check_launch("mk_convert");
+}
+
+extern "C" int mk_fill(void* stream, int elem_bytes, int64_t n, uint64_t pattern, void* out) {
+  clear_error();
+  if (n < 0) return fail(MK_ERR_INVALID, "mk_fill: negative n");
+  if (n == 0) return MK_OK;
+  if (!out) return fail(MK_ERR_INVALID, "mk_fill: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(blocks_for(n, kBlock)), b(kBlock);
+  switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(fill_kernel<uint8_t>, g, b, 0, s, (uint8_t*)out, uint8_t(pattern), n); break;
+    case 2: hipLaunchKernelGGL(fill_kernel<uint16_t>, g, b, 0, s, (uint16_t*)out, uint16_t(pattern), n); break;
+    case 4: hipLaunchKernelGGL(fill_kernel<uint32_t>, g, b, 0, s, (uint32_t*)out, uint32_t(pattern), n); break;
+    case 8: hipLaunchKernelGGL(fill_kernel<uint64_t>, g, b, 0, s, (uint64_t*)out, pattern, n); break;
+    default: return fail(MK_ERR_INVALID, "mk_fill: elem_bytes must be 1, 2, 4 or 8");
+  }
+  return check_launch("mk_fill");
+}
+
+extern "C" int mk_iota(void* stream, int out_type, int rank, const int64_t* dims, int dim, void* out) {
+  clear_error();
+  if (rank < 1 || rank > kEwMaxRank || dim < 0 || dim >= rank)
+    return fail(MK_ERR_INVALID, "mk_iota: need 1 <= rank <= 6 and 0 <= dim < rank");
+  if (out_type != MK_S32 && out_type != MK_S64 && out_type != MK_F32 && out_type != MK_BF16 &&
+      out_type != MK_U32 && out_type != MK_F16)
+    return fail(MK_ERR_UNSUPPORTED, "mk_iota: unsupported out_type");
+  int64_t n = 1, inner = 1;
+  for (int d = 0; d < rank; ++d) {
+    if (dims[d] < 0) return fail(MK_ERR_INVALID, "mk_iota: negative dim");
+    n *= dims[d];
+    if (d > dim) inner *= dims[d];
+  }
+  if (n == 0) return MK_OK;
+  if (!out) return fail(MK_ERR_INVALID, "mk_iota: null pointer");
+  hipLaunchKernelGGL(iota_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, as_stream(stream), out,
+                     out_type, n, inner, dims[dim]);
+  return check_launch("mk_iota");
+}
+
+extern "C" int mk_copy_strided(void* stream, int elem_bytes, int rank, const int64_t* dims,
+                               const void* in, const int64_t* in_strides, void* out) {
+  clear_error();
+  if (rank < 0 || rank > kEwMaxRank) return fail(MK_ERR_INVALID, "mk_copy_strided: rank > 6");
+  CopyArgs a{};
+  a.rank = rank;
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    if (dims[d] < 0) return fail(MK_ERR_INVALID, "mk_copy_strided: negative dim");
+    a.dims[d] = dims[d];
+    a.strides[d] = in_strides[d];
+    n *= dims[d];
+  }
+  if (n == 0) return MK_OK;
+  if (!in || !out) return fail(MK_ERR_INVALID, "mk_copy_strided: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(blocks_for(n, kBlock)), b(kBlock);
+  switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(copy_strided_kernel<uint8_t>, g, b, 0, s, (const uint8_t*)in, (uint8_t*)out, n, a); break;
+    case 2: hipLaunchKernelGGL(copy_strided_kernel<uint16_t>, g, b, 0, s, (const uint16_t*)in, (uint16_t*)out, n, a); break;
+    case 4: hipLaunchKernelGGL(copy_strided_kernel<uint32_t>, g, b, 0, s, (const uint32_t*)in, (uint32_t*)out, n, a); break;
+    case 8: hipLaunchKernelGGL(copy_strided_kernel<uint64_t>, g, b, 0, s, (const uint64_t*)in, (uint64_t*)out, n, a); break;
+    default: return fail(MK_ERR_INVALID, "mk_copy_strided: elem_bytes must be 1, 2, 4 or 8");
+  }
+  return check_launch("mk_copy_strided");
+}

@@ -1,0 +1,364 @@
+// Indexing kernels: row gather (embedding lookup) and deterministic
+// scatter-add.
+//
+// Scatter-add determinism: the result must equal applying the updates one
+// at a time in increasing update index (XLA:CPU's sequential scatter), so
+// for every destination row the fp32 adds happen in that order.  The plan:
+//   1. keys[i] = ids[i] (or n_rows for a dropped out-of-range id), vals[i] = i
+//   2. stable LSD radix sort of (key, val) by key, 8 bits per pass — stable,
+//      so equal keys keep increasing i
+//   3. bounds: first/last position of every key in the sorted array
+//   4. one wave per destination row: acc = table[r]; acc += updates[i] for the
+//      row's i in sorted (= increasing) order; store.
+// Step 4 is the HBM-bound part (reads updates once, table rows once, writes
+// output rows once); steps 1-3 touch only O(n_ids + n_rows) 4-byte words.
+#include "mk_common.h"
+
+namespace mk {
+namespace {
+
+constexpr int kBlock = 256;
+
+// ------------------------------------------------------------------ gather
+template <typename IdxT>
+__global__ __launch_bounds__(kBlock) void gather_rows16_kernel(const u32x4_t* __restrict__ table,
+                                                               int64_t n_rows, int64_t row_vecs,
+                                                               const IdxT* __restrict__ ids,
+                                                               int64_t n_ids,
+                                                               u32x4_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (i >= n_ids) return;
+  int64_t r = int64_t(ids[i]);
+  r = r < 0 ? 0 : (r >= n_rows ? n_rows - 1 : r);  // StableHLO gather clamps start indices
+  const u32x4_t* src = table + r * row_vecs;
+  u32x4_t* dst = out + i * row_vecs;
+  for (int64_t c = lane; c < row_vecs; c += 64) dst[c] = src[c];
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kBlock) void gather_rows4_kernel(const uint32_t* __restrict__ table,
+                                                              int64_t n_rows, int64_t row_words,
+                                                              const IdxT* __restrict__ ids,
+                                                              int64_t n_ids,
+                                                              uint32_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (i >= n_ids) return;
+  int64_t r = int64_t(ids[i]);
+  r = r < 0 ? 0 : (r >= n_rows ? n_rows - 1 : r);
+  const uint32_t* src = table + r * row_words;
+  uint32_t* dst = out + i * row_words;
+  for (int64_t c = lane; c < row_words; c += 64) dst[c] = src[c];
+}
+
+// ------------------------------------------------------------------ radix sort
+__global__ __launch_bounds__(kBlock) void fill_words(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kSortItems = 4;
+constexpr int kSortTile = kBlock * kSortItems;  // elements per block per pass
+
+template <typename IdxT>
+__global__ __launch_bounds__(kBlock) void scatter_prepare_kernel(const IdxT* __restrict__ ids,
+                                                                 int64_t n, int64_t n_rows,
+                                                                 uint32_t* __restrict__ keys,
+                                                                 uint32_t* __restrict__ vals) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const int64_t id = int64_t(ids[i]);
+  keys[i] = (id < 0 || id >= n_rows) ? uint32_t(n_rows) : uint32_t(id);
+  vals[i] = uint32_t(i);
+}
+
+// Per-block digit histogram, stored digit-major: hist[d * nb + block].
+__global__ __launch_bounds__(kBlock) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n,
+                                                            int shift, uint32_t* __restrict__ hist,
+                                                            int nb) {
+  __shared__ uint32_t h[256];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+#pragma unroll
+  for (int k = 0; k < kSortItems; ++k) {
+    const int64_t e = base + int64_t(k) * kBlock + threadIdx.x;
+    if (e < n) atomicAdd(&h[(keys[e] >> shift) & 255u], 1u);
+  }
+  __syncthreads();
+  hist[int64_t(threadIdx.x) * nb + blockIdx.x] = h[threadIdx.x];
+}
+
+// Exclusive scan of `total` words in place, one block of 1024 threads.
+constexpr int kScanBlock = 1024;
+__global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(uint32_t* __restrict__ data,
+                                                                    int64_t total) {
+  __shared__ uint32_t part[kScanBlock];
+  const int t = threadIdx.x;
+  const int64_t per = (total + kScanBlock - 1) / kScanBlock;
+  const int64_t b = t * per, e = (b + per < total) ? b + per : total;
+  uint32_t s = 0;
+  for (int64_t i = b; i < e; ++i) s += data[i];
+  part[t] = s;
+  __syncthreads();
+  // Hillis-Steele inclusive scan of the per-thread partial sums
+  for (int off = 1; off < kScanBlock; off <<= 1) {
+    uint32_t v = t >= off ? part[t - off] : 0u;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  uint32_t run = t > 0 ? part[t - 1] : 0u;
+  for (int64_t i = b; i < e; ++i) {
+    const uint32_t v = data[i];
+    data[i] = run;
+    run += v;
+  }
+}
+
+// Stable scatter of one radix pass.  Element order inside a tile is
+// k-major (e = base + k*256 + t), which is also the global order, so a rank
+// computed in that order is the stable rank.
+__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
+                                                               const uint32_t* __restrict__ vals_in,
+                                                               int64_t n, int shift,
+                                                               const uint32_t* __restrict__ offsets,
+                                                               int nb,
+                                                               uint32_t* __restrict__ keys_out,
+                                                               uint32_t* __restrict__ vals_out) {
+  __shared__ uint32_t running[256];            // same-digit elements already placed in this tile
+  __shared__ uint32_t wave_cnt[kBlock / 64][256];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  running[t] = 0;
+  const int64_t base = int64_t(blockIdx.x) * kSortTile;
+  const uint32_t my_off = offsets[int64_t(t) * nb + blockIdx.x];  // for digit t
+  __shared__ uint32_t block_off[256];
+  block_off[t] = my_off;
+  for (int k = 0; k < kSortItems; ++k) {
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) wave_cnt[w][t] = 0;
+    __syncthreads();
+    const int64_t e = base + int64_t(k) * kBlock + t;
+    const bool valid = e < n;
+    uint32_t key = 0, val = 0, d = 0;
+    if (valid) {
+      key = keys_in[e];
+      val = vals_in[e];
+      d = (key >> shift) & 255u;
+    }
+    // lanes of this wave holding the same digit
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t ones = __ballot(valid && ((d >> bit) & 1u));
+      peers &= ((d >> bit) & 1u) ? ones : ~ones;
+    }
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t rank_w = uint32_t(__popcll(peers & lt_mask));
+    if (valid && rank_w == 0) wave_cnt[wave][d] = uint32_t(__popcll(peers));
+    __syncthreads();
+    if (valid) {
+      uint32_t before = running[d];
+      for (int w = 0; w < wave; ++w) before += wave_cnt[w][d];
+      const uint32_t pos = block_off[d] + before + rank_w;
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+    uint32_t add = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / 64; ++w) add += wave_cnt[w][t];
+    running[t] += add;
+    __syncthreads();
+  }
+}
+
+// bounds[2r] / bounds[2r+1] = first / one-past-last sorted position of key r
+// (both 0 when r has no updates; zero-filled beforehand).
+__global__ __launch_bounds__(kBlock) void bucket_bounds_kernel(const uint32_t* __restrict__ keys,
+                                                               int64_t n, int64_t n_rows,
+                                                               uint32_t* __restrict__ bounds) {
+  const int64_t j = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (j >= n) return;
+  const uint32_t k = keys[j];
+  if (k >= uint32_t(n_rows)) return;  // dropped ids sort last
+  if (j == 0 || keys[j - 1] != k) bounds[2 * int64_t(k)] = uint32_t(j);
+  if (j == n - 1 || keys[j + 1] != k) bounds[2 * int64_t(k) + 1] = uint32_t(j + 1);
+}
+
+// One wave per destination row.  For fp32 the order of adds per element is
+// table, then updates in increasing index — exactly the sequential order.
+// For bf16 each add is rounded to bf16 as a bf16 scatter would.
+template <bool BF16>
+__global__ __launch_bounds__(kBlock) void scatter_accumulate_kernel(
+    const void* __restrict__ table, void* __restrict__ out, int64_t n_rows, int64_t row_len,
+    const void* __restrict__ updates, const uint32_t* __restrict__ vals,
+    const uint32_t* __restrict__ bounds, bool in_place, bool vec_ok) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (r >= n_rows) return;
+  const uint32_t b = bounds[2 * r], e = bounds[2 * r + 1];
+  if (in_place && b == e) return;  // untouched row already holds its value
+  if constexpr (!BF16) {
+    const float* tr = reinterpret_cast<const float*>(table) + r * row_len;
+    float* orow = reinterpret_cast<float*>(out) + r * row_len;
+    const float* up = reinterpret_cast<const float*>(updates);
+    if (vec_ok) {
+      const int64_t nv = row_len / 4;
+      for (int64_t c0 = lane; c0 < nv; c0 += 3 * 64) {
+        // up to three float4 columns per lane per sweep
+        f32x4 acc[3];
+        int64_t cs[3];
+        int m = 0;
+        for (; m < 3 && c0 + m * 64 < nv; ++m) {
+          cs[m] = c0 + m * 64;
+          acc[m] = reinterpret_cast<const f32x4*>(tr)[cs[m]];
+        }
+        for (uint32_t j = b; j < e; ++j) {
+          const f32x4* urow = reinterpret_cast<const f32x4*>(up + int64_t(vals[j]) * row_len);
+          for (int q = 0; q < m; ++q) {
+            const f32x4 u = urow[cs[q]];
+#pragma unroll
+            for (int z = 0; z < 4; ++z) acc[q].v[z] += u.v[z];
+          }
+        }
+        for (int q = 0; q < m; ++q) reinterpret_cast<f32x4*>(orow)[cs[q]] = acc[q];
+      }
+    } else {
+      for (int64_t c = lane; c < row_len; c += 64) {
+        float acc = tr[c];
+        for (uint32_t j = b; j < e; ++j) acc += up[int64_t(vals[j]) * row_len + c];
+        orow[c] = acc;
+      }
+    }
+  } else {
+    const uint16_t* tr = reinterpret_cast<const uint16_t*>(table) + r * row_len;
+    uint16_t* orow = reinterpret_cast<uint16_t*>(out) + r * row_len;
+    const uint16_t* up = reinterpret_cast<const uint16_t*>(updates);
+    for (int64_t c = lane; c < row_len; c += 64) {
+      float acc = bf16_to_f32(tr[c]);
+      for (uint32_t j = b; j < e; ++j)
+        acc = bf16_to_f32(f32_to_bf16(acc + bf16_to_f32(up[int64_t(vals[j]) * row_len + c])));
+      orow[c] = f32_to_bf16(acc);
+    }
+  }
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct ScatterWs {
+  uint32_t *keys0, *vals0, *keys1, *vals1, *hist, *bounds;
+  int nb;
+};
+
+inline ScatterWs carve(void* ws, int64_t n_rows, int64_t n_ids) {
+  ScatterWs w;
+  char* p = reinterpret_cast<char*>(ws);
+  const size_t idb = align256(size_t(n_ids) * 4);
+  w.nb = int((n_ids + kSortTile - 1) / kSortTile);
+  w.keys0 = reinterpret_cast<uint32_t*>(p); p += idb;
+  w.vals0 = reinterpret_cast<uint32_t*>(p); p += idb;
+  w.keys1 = reinterpret_cast<uint32_t*>(p); p += idb;
+  w.vals1 = reinterpret_cast<uint32_t*>(p); p += idb;
+  w.hist = reinterpret_cast<uint32_t*>(p); p += align256(size_t(256) * (w.nb > 0 ? w.nb : 1) * 4);
+  w.bounds = reinterpret_cast<uint32_t*>(p);
+  return w;
+}
+
+inline unsigned blocks_for(int64_t n, int per) { return unsigned((n + per - 1) / per); }
+
+}  // namespace
+}  // namespace mk
+
+using namespace mk;
+
+extern "C" int mk_gather_rows(void* stream, int64_t n_rows, int64_t row_bytes, const void* table,
+                              int index_type, int64_t n_ids, const void* ids, void* out) {
+  clear_error();
+  if (n_rows <= 0 || row_bytes < 0 || n_ids < 0)
+    return fail(MK_ERR_INVALID, "mk_gather_rows: need n_rows >= 1, row_bytes >= 0, n_ids >= 0");
+  if (row_bytes % 4 != 0) return fail(MK_ERR_UNSUPPORTED, "mk_gather_rows: row_bytes % 4 != 0");
+  if (index_type != MK_S32 && index_type != MK_S64)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gather_rows: index_type must be s32/s64");
+  if (n_ids == 0 || row_bytes == 0) return MK_OK;
+  if (!table || !ids || !out) return fail(MK_ERR_INVALID, "mk_gather_rows: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(blocks_for(n_ids, kBlock / 64)), b(kBlock);
+  const bool v16 = row_bytes % 16 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+  if (v16) {
+    if (index_type == MK_S32)
+      hipLaunchKernelGGL(gather_rows16_kernel<int32_t>, g, b, 0, s, (const u32x4_t*)table, n_rows,
+                         row_bytes / 16, (const int32_t*)ids, n_ids, (u32x4_t*)out);
+    else
+      hipLaunchKernelGGL(gather_rows16_kernel<int64_t>, g, b, 0, s, (const u32x4_t*)table, n_rows,
+                         row_bytes / 16, (const int64_t*)ids, n_ids, (u32x4_t*)out);
+  } else {
+    if (index_type == MK_S32)
+      hipLaunchKernelGGL(gather_rows4_kernel<int32_t>, g, b, 0, s, (const uint32_t*)table, n_rows,
+                         row_bytes / 4, (const int32_t*)ids, n_ids, (uint32_t*)out);
+    else
+      hipLaunchKernelGGL(gather_rows4_kernel<int64_t>, g, b, 0, s, (const uint32_t*)table, n_rows,
+                         row_bytes / 4, (const int64_t*)ids, n_ids, (uint32_t*)out);
+  }
+  return check_launch("mk_gather_rows");
+}
+
+extern "C" size_t mk_scatter_add_workspace_bytes(int64_t n_rows, int64_t n_ids) {
+  if (n_rows < 0 || n_ids < 0) return 0;
+  const int64_t nb = (n_ids + kSortTile - 1) / kSortTile;
+  return 4 * align256(size_t(n_ids) * 4) + align256(size_t(256) * size_t(nb > 0 ? nb : 1) * 4) +
+         align256(size_t(n_rows) * 8);
+}
+
+extern "C" int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int64_t row_len,
+                                   const void* table, int index_type, int64_t n_ids,
+                                   const void* ids, const void* updates, void* out,
+                                   void* workspace) {
+  clear_error();
+  if (n_rows < 0 || row_len < 0 || n_ids < 0) return fail(MK_ERR_INVALID, "mk_scatter_add_rows: negative size");
+  if (dtype != MK_F32 && dtype != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: dtype must be f32/bf16");
+  if (index_type != MK_S32 && index_type != MK_S64)
+    return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: index_type must be s32/s64");
+  if (n_rows >= (int64_t(1) << 31) || n_ids >= (int64_t(1) << 31))
+    return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: n_rows and n_ids must be < 2^31");
+  if (n_rows == 0 || row_len == 0) return MK_OK;
+  if (!table || !out || (n_ids > 0 && (!ids || !updates || !workspace)))
+    return fail(MK_ERR_INVALID, "mk_scatter_add_rows: null pointer");
+  hipStream_t s = as_stream(stream);
+  ScatterWs w = carve(workspace, n_rows, n_ids);
+  // bounds start at zero: rows without updates have an empty range
+  hipLaunchKernelGGL((fill_words), dim3(blocks_for(2 * n_rows, kBlock)), dim3(kBlock), 0, s, w.bounds, 2 * n_rows);
+  if (n_ids > 0) {
+    const unsigned gi = blocks_for(n_ids, kBlock);
+    if (index_type == MK_S32)
+      hipLaunchKernelGGL(scatter_prepare_kernel<int32_t>, dim3(gi), dim3(kBlock), 0, s, (const int32_t*)ids, n_ids, n_rows, w.keys0, w.vals0);
+    else
+      hipLaunchKernelGGL(scatter_prepare_kernel<int64_t>, dim3(gi), dim3(kBlock), 0, s, (const int64_t*)ids, n_ids, n_rows, w.keys0, w.vals0);
+    // keys are in [0, n_rows]: sort only the bits that can be set
+    int bits = 0;
+    while ((int64_t(1) << bits) <= n_rows) ++bits;
+    uint32_t *kin = w.keys0, *vin = w.vals0, *kout = w.keys1, *vout = w.vals1;
+    for (int shift = 0; shift < bits; shift += 8) {
+      hipLaunchKernelGGL(radix_hist_kernel, dim3(w.nb), dim3(kBlock), 0, s, kin, n_ids, shift, w.hist, w.nb);
+      hipLaunchKernelGGL(scan_exclusive_kernel, dim3(1), dim3(kScanBlock), 0, s, w.hist, int64_t(256) * w.nb);
+      hipLaunchKernelGGL(radix_scatter_kernel, dim3(w.nb), dim3(kBlock), 0, s, kin, vin, n_ids, shift, w.hist, w.nb, kout, vout);
+      uint32_t* tk = kin; kin = kout; kout = tk;
+      uint32_t* tv = vin; vin = vout; vout = tv;
+    }
+    hipLaunchKernelGGL(bucket_bounds_kernel, dim3(gi), dim3(kBlock), 0, s, kin, n_ids, n_rows, w.bounds);
+    w.vals0 = vin;  // sorted values
+  }
+  const bool in_place = table == out;
+  const bool vec_ok = dtype == MK_F32 && row_len % 4 == 0 &&
+                      ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out) |
+                        reinterpret_cast<uintptr_t>(updates)) & 15u) == 0;
+  dim3 g(blocks_for(n_rows, kBlock / 64));
+  if (dtype == MK_F32)
+    hipLaunchKernelGGL(scatter_accumulate_kernel<false>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, vec_ok);
+  else
+    hipLaunchKernelGGL(scatter_accumulate_kernel<true>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, false);
+  return check_launch("mk_scatter_add_rows");
+}

@@ -1,0 +1,160 @@
+// Shared device/host helpers for the gfx950 kernels behind include/mk_kernels.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "mk_kernels.h"
+
+namespace mk {
+
+// ---------------------------------------------------------------- errors
+// Per-thread last-error string; entry points return an MK_* code and leave
+// the human-readable reason here.
+void set_error(const std::string& msg);
+void clear_error();
+int fail(int code, const std::string& msg);
+// Checks hipGetLastError() after a launch; returns MK_OK or MK_ERR_LAUNCH.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- dtypes
+inline int dtype_bytes(int t) {
+  switch (t) {
+    case MK_PRED: case MK_S8: case MK_U8: return 1;
+    case MK_S16: case MK_U16: case MK_F16: case MK_BF16: return 2;
+    case MK_S32: case MK_U32: case MK_F32: return 4;
+    case MK_S64: case MK_U64: case MK_F64: return 8;
+    default: return 0;
+  }
+}
+
+// ---------------------------------------------------------------- bf16 / f16
+// bf16 is carried as raw uint16 bits.  Widening is exact; narrowing is
+// round-to-nearest-even with NaN kept quiet (sign preserved).
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  uint32_t u = uint32_t(h) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+__host__ __device__ inline uint16_t f32_to_bf16_sw(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+// On gfx950 the fptrunc lowers to v_cvt_pk_bf16_f32 (hardware RNE), one
+// instruction for two values; the host side uses the integer formulation.
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __bf16 b = static_cast<__bf16>(f);
+  uint16_t u;
+  __builtin_memcpy(&u, &b, 2);
+  return u;
+#else
+  return f32_to_bf16_sw(f);
+#endif
+}
+__device__ inline float f16_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return float(v);
+}
+__device__ inline uint16_t f32_to_f16(float f) {
+  _Float16 v = _Float16(f);  // RNE on AMDGPU (v_cvt_f16_f32)
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+// Generic scalar load/store through an element type known at run time (used
+// by the non-hot generic kernels only; hot kernels are templated).
+__device__ inline float load_as_f32(const void* p, int64_t i, int t) {
+  switch (t) {
+    case MK_F32: return reinterpret_cast<const float*>(p)[i];
+    case MK_BF16: return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    case MK_F16: return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    case MK_S32: return float(reinterpret_cast<const int32_t*>(p)[i]);
+    case MK_U32: return float(reinterpret_cast<const uint32_t*>(p)[i]);
+    case MK_S64: return float(reinterpret_cast<const int64_t*>(p)[i]);
+    case MK_U64: return float(reinterpret_cast<const uint64_t*>(p)[i]);
+    case MK_S8: return float(reinterpret_cast<const int8_t*>(p)[i]);
+    case MK_U8: case MK_PRED: return float(reinterpret_cast<const uint8_t*>(p)[i]);
+    case MK_S16: return float(reinterpret_cast<const int16_t*>(p)[i]);
+    case MK_U16: return float(reinterpret_cast<const uint16_t*>(p)[i]);
+    case MK_F64: return float(reinterpret_cast<const double*>(p)[i]);
+    default: return 0.f;
+  }
+}
+__device__ inline void store_from_f32(void* p, int64_t i, int t, float v) {
+  switch (t) {
+    case MK_F32: reinterpret_cast<float*>(p)[i] = v; break;
+    case MK_BF16: reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v); break;
+    case MK_F16: reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16(v); break;
+    case MK_S32: reinterpret_cast<int32_t*>(p)[i] = int32_t(v); break;
+    case MK_U32: reinterpret_cast<uint32_t*>(p)[i] = uint32_t(v); break;
+    case MK_S64: reinterpret_cast<int64_t*>(p)[i] = int64_t(v); break;
+    case MK_U64: reinterpret_cast<uint64_t*>(p)[i] = uint64_t(v); break;
+    case MK_S8: reinterpret_cast<int8_t*>(p)[i] = int8_t(v); break;
+    case MK_U8: reinterpret_cast<uint8_t*>(p)[i] = uint8_t(v); break;
+    case MK_PRED: reinterpret_cast<uint8_t*>(p)[i] = uint8_t(v != 0.f); break;
+    case MK_S16: reinterpret_cast<int16_t*>(p)[i] = int16_t(v); break;
+    case MK_U16: reinterpret_cast<uint16_t*>(p)[i] = uint16_t(v); break;
+    case MK_F64: reinterpret_cast<double*>(p)[i] = double(v); break;
+    default: break;
+  }
+}
+
+// ---------------------------------------------------------------- wave64
+constexpr int kWave = 64;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+__device__ inline float wave_min(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+__device__ inline float wave_prod(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v *= __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// 16-byte vector of 8 bf16 / 4 fp32 lanes for dwordx4 global traffic.
+struct alignas(16) u16x8 { uint16_t v[8]; };
+struct alignas(16) f32x4 { float v[4]; };
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) 16-byte load/store: data touched once should not
+// evict the L2 working set of other kernels.
+template <typename V>
+__device__ inline V ld_stream(const V* p) {
+  static_assert(sizeof(V) == 16, "16-byte vectors only");
+  u32x4_t r = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  V v;
+  __builtin_memcpy(&v, &r, 16);
+  return v;
+}
+template <typename V>
+__device__ inline void st_stream(V* p, const V& v) {
+  static_assert(sizeof(V) == 16, "16-byte vectors only");
+  u32x4_t r;
+  __builtin_memcpy(&r, &v, 16);
+  __builtin_nontemporal_store(r, reinterpret_cast<u32x4_t*>(p));
+}
+
+}  // namespace mk

@@ -1,0 +1,460 @@
+// Row-wise reductions over the innermost axis: reduce (sum/max/min/prod),
+// fused max+argmax (bit-exact), LayerNorm and softmax.
+//
+// Layout: x is [rows, cols] row-major.  One wave64 owns one row; each lane
+// reads 16-byte vectors (8 bf16 / 4 fp32) so a 2 KiB bf16 row is exactly two
+// dwordx4 loads per lane and every HBM line is fully used.  Cross-lane
+// combination is a 6-step butterfly.  Rows never interact, so the grid is
+// rows/4 workgroups of 4 waves — tens of thousands of waves for the C2
+// shapes, enough to keep all 256 CUs streaming.
+#include "mk_common.h"
+
+#include <cmath>
+
+namespace mk {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = kWavesPerBlock * kWave;
+
+template <typename T> struct Vec;
+template <> struct Vec<uint16_t> { static constexpr int N = 8; using V = u16x8; };
+template <> struct Vec<float> { static constexpr int N = 4; using V = f32x4; };
+
+template <typename T> __device__ inline float to_f32(T v);
+template <> __device__ inline float to_f32<float>(float v) { return v; }
+template <> __device__ inline float to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+
+// Input element types handled by the templated row kernels: bf16 (uint16_t
+// bits, IS_F16=false), f16 (uint16_t bits, IS_F16=true) and f32.
+template <typename T, bool IS_F16>
+__device__ inline float ld(T v) {
+  if constexpr (IS_F16) return f16_to_f32(v);
+  else return to_f32<T>(v);
+}
+
+template <int OP> __device__ inline float combine(float a, float b) {
+  if constexpr (OP == 0) return a + b;
+  else if constexpr (OP == 1) return fmaxf(a, b);
+  else if constexpr (OP == 2) return fminf(a, b);
+  else return a * b;
+}
+template <int OP> __device__ inline float wave_combine(float v) {
+  if constexpr (OP == 0) return wave_sum(v);
+  else if constexpr (OP == 1) return wave_max(v);
+  else if constexpr (OP == 2) return wave_min(v);
+  else return wave_prod(v);
+}
+template <int OP> __device__ inline float identity() {
+  if constexpr (OP == 0) return 0.f;
+  else if constexpr (OP == 1) return -INFINITY;
+  else if constexpr (OP == 2) return INFINITY;
+  else return 1.f;
+}
+
+// StableHLO max/min propagate NaN; fmaxf/fminf drop it, so NaN is tracked
+// separately for OP 1/2.
+template <typename T, bool IS_F16, int OP>
+__global__ __launch_bounds__(kBlock) void row_reduce_kernel(const T* __restrict__ x, int64_t rows,
+                                                            int64_t cols, float init, void* y,
+                                                            int out_type, bool vec_ok) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  float acc = identity<OP>();
+  bool nan = false;
+  constexpr int N = Vec<T>::N;
+  if (vec_ok) {
+    using V = typename Vec<T>::V;
+    const V* xv = reinterpret_cast<const V*>(xr);
+    const int64_t nv = cols / N;
+    int64_t i = lane;
+    // two vectors in flight per iteration
+    for (; i + kWave < nv; i += 2 * kWave) {
+      V a = xv[i], b = xv[i + kWave];
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float fa = ld<T, IS_F16>(a.v[j]);
+        nan |= (fa != fa);
+        acc = combine<OP>(acc, fa);
+      }
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float fb = ld<T, IS_F16>(b.v[j]);
+        nan |= (fb != fb);
+        acc = combine<OP>(acc, fb);
+      }
+    }
+    for (; i < nv; i += kWave) {
+      V a = xv[i];
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float fa = ld<T, IS_F16>(a.v[j]);
+        nan |= (fa != fa);
+        acc = combine<OP>(acc, fa);
+      }
+    }
+  } else {
+    for (int64_t c = lane; c < cols; c += kWave) {
+      float f = ld<T, IS_F16>(xr[c]);
+      nan |= (f != f);
+      acc = combine<OP>(acc, f);
+    }
+  }
+  acc = wave_combine<OP>(acc);
+  if (lane == 0) {
+    float r = combine<OP>(acc, init);
+    if constexpr (OP == 1 || OP == 2) {
+      bool any_nan = __any(nan) || (init != init);
+      if (any_nan) r = __builtin_nanf("");
+    }
+    store_from_f32(y, row, out_type, r);
+  }
+}
+
+// (value, index) pair compare for argmax/argmin with XLA semantics.
+template <bool IS_MIN>
+__device__ inline bool better(float a, int64_t ia, float b, int64_t ib) {
+  const bool an = a != a, bn = b != b;
+  if (an || bn) {
+    if (an && bn) return ia < ib;
+    return an;
+  }
+  if (a == b) return ia < ib;
+  return IS_MIN ? (a < b) : (a > b);
+}
+
+template <typename T> __device__ inline uint32_t raw_bits(T v) {
+  if constexpr (sizeof(T) == 4) {
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    return u;
+  } else {
+    return uint32_t(v);
+  }
+}
+template <typename T> __device__ inline T from_bits(uint32_t u) {
+  if constexpr (sizeof(T) == 4) {
+    T v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+  } else {
+    return T(u);
+  }
+}
+
+template <typename T, bool IS_F16, bool IS_MIN, typename IdxT>
+__global__ __launch_bounds__(kBlock) void row_argmax_kernel(const T* __restrict__ x, int64_t rows,
+                                                            int64_t cols, T* __restrict__ values,
+                                                            IdxT* __restrict__ indices, bool vec_ok) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  float best = 0.f;
+  int64_t bi = INT64_MAX;  // "no element yet": loses to any real element
+  uint32_t braw = 0;
+  constexpr int N = Vec<T>::N;
+  // Elements are visited in increasing index within a lane, so only a
+  // strictly better element may replace the current one.
+  auto consider = [&](T raw, int64_t idx) {
+    float f = ld<T, IS_F16>(raw);
+    if (bi == INT64_MAX || better<IS_MIN>(f, idx, best, bi)) {
+      best = f;
+      bi = idx;
+      braw = raw_bits<T>(raw);
+    }
+  };
+  if (vec_ok) {
+    using V = typename Vec<T>::V;
+    const V* xv = reinterpret_cast<const V*>(xr);
+    const int64_t nv = cols / N;
+    int64_t i = lane;
+    for (; i + kWave < nv; i += 2 * kWave) {
+      V a = xv[i], b = xv[i + kWave];
+#pragma unroll
+      for (int j = 0; j < N; ++j) consider(a.v[j], i * N + j);
+#pragma unroll
+      for (int j = 0; j < N; ++j) consider(b.v[j], (i + kWave) * N + j);
+    }
+    for (; i < nv; i += kWave) {
+      V a = xv[i];
+#pragma unroll
+      for (int j = 0; j < N; ++j) consider(a.v[j], i * N + j);
+    }
+  } else {
+    for (int64_t c = lane; c < cols; c += kWave) consider(xr[c], c);
+  }
+  // butterfly: every lane ends with the row winner
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(best, m, kWave);
+    const int64_t oi = __shfl_xor(bi, m, kWave);
+    const uint32_t oraw = __shfl_xor(braw, m, kWave);
+    if (oi != INT64_MAX && (bi == INT64_MAX || better<IS_MIN>(ob, oi, best, bi))) {
+      best = ob;
+      bi = oi;
+      braw = oraw;
+    }
+  }
+  if (lane == 0) {
+    if (values) values[row] = from_bits<T>(braw);
+    indices[row] = IdxT(bi == INT64_MAX ? 0 : bi);
+  }
+}
+
+// LayerNorm: one wave per row, the whole row held in registers (up to
+// kLnMaxPerLane fp32 per lane), two-pass mean/variance, single store.
+constexpr int kLnMaxVecs = 8;  // 8 × 8 bf16 = 64 elements per lane → cols ≤ 4096 in registers
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restrict__ x,
+                                                               const T* __restrict__ gamma,
+                                                               const T* __restrict__ beta,
+                                                               int64_t rows, int cols, float eps,
+                                                               T* __restrict__ y) {
+  using V = typename Vec<T>::V;
+  constexpr int N = Vec<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nv = cols / N;  // vectors per row; host guarantees nv ≤ kLnMaxVecs * 64
+  const V* xv = reinterpret_cast<const V*>(x + row * int64_t(cols));
+  float r[kLnMaxVecs][N];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < kLnMaxVecs; ++k) {
+    int i = lane + k * kWave;
+    if (i < nv) {
+      V a = xv[i];
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        r[k][j] = to_f32<T>(a.v[j]);
+        s += r[k][j];
+      }
+    }
+  }
+  const float inv_n = 1.f / float(cols);
+  const float mean = wave_sum(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < kLnMaxVecs; ++k) {
+    if (lane + k * kWave < nv) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float d = r[k][j] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) * inv_n;
+  const float rstd = 1.f / sqrtf(var + eps);
+  const V* gv = reinterpret_cast<const V*>(gamma);
+  const V* bv = reinterpret_cast<const V*>(beta);
+  V* yv = reinterpret_cast<V*>(y + row * int64_t(cols));
+#pragma unroll
+  for (int k = 0; k < kLnMaxVecs; ++k) {
+    int i = lane + k * kWave;
+    if (i < nv) {
+      V g{}, b{}, o;
+      if (gamma) g = gv[i];
+      if (beta) b = bv[i];
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float gj = gamma ? to_f32<T>(g.v[j]) : 1.f;
+        float bj = beta ? to_f32<T>(b.v[j]) : 0.f;
+        float v = (r[k][j] - mean) * rstd * gj + bj;
+        if constexpr (sizeof(T) == 2) o.v[j] = f32_to_bf16(v);
+        else o.v[j] = v;
+      }
+      yv[i] = o;
+    }
+  }
+}
+
+// Fallback LayerNorm for any width: three streaming passes over the row.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void layernorm_loop_kernel(const T* __restrict__ x,
+                                                                const T* __restrict__ gamma,
+                                                                const T* __restrict__ beta,
+                                                                int64_t rows, int64_t cols,
+                                                                float eps, T* __restrict__ y) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += kWave) s += to_f32<T>(xr[c]);
+  const float mean = wave_sum(s) / float(cols);
+  float q = 0.f;
+  for (int64_t c = lane; c < cols; c += kWave) {
+    float d = to_f32<T>(xr[c]) - mean;
+    q += d * d;
+  }
+  const float rstd = 1.f / sqrtf(wave_sum(q) / float(cols) + eps);
+  T* yr = y + row * cols;
+  for (int64_t c = lane; c < cols; c += kWave) {
+    float gj = gamma ? to_f32<T>(gamma[c]) : 1.f;
+    float bj = beta ? to_f32<T>(beta[c]) : 0.f;
+    float v = (to_f32<T>(xr[c]) - mean) * rstd * gj + bj;
+    if constexpr (sizeof(T) == 2) yr[c] = f32_to_bf16(v);
+    else yr[c] = v;
+  }
+}
+
+// Softmax over a row: max pass, sum-of-exp pass, normalise pass.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void softmax_kernel(const T* __restrict__ x, int64_t rows,
+                                                         int64_t cols, T* __restrict__ y) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  float m = -INFINITY;
+  for (int64_t c = lane; c < cols; c += kWave) m = fmaxf(m, to_f32<T>(xr[c]));
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += kWave) s += __expf(to_f32<T>(xr[c]) - m);
+  s = wave_sum(s);
+  const float inv = 1.f / s;
+  T* yr = y + row * cols;
+  for (int64_t c = lane; c < cols; c += kWave) {
+    float v = __expf(to_f32<T>(xr[c]) - m) * inv;
+    if constexpr (sizeof(T) == 2) yr[c] = f32_to_bf16(v);
+    else yr[c] = v;
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline unsigned grid_for_rows(int64_t rows) {
+  return unsigned((rows + kWavesPerBlock - 1) / kWavesPerBlock);
+}
+
+template <typename T, bool IS_F16>
+int launch_reduce(hipStream_t s, int op, int64_t rows, int64_t cols, const void* x, float init,
+                  void* y, int out_type) {
+  const bool vec_ok = aligned16(x) && (cols % Vec<T>::N) == 0;
+  const T* xp = reinterpret_cast<const T*>(x);
+  dim3 g(grid_for_rows(rows)), b(kBlock);
+  switch (op) {
+    case 0: hipLaunchKernelGGL((row_reduce_kernel<T, IS_F16, 0>), g, b, 0, s, xp, rows, cols, init, y, out_type, vec_ok); break;
+    case 1: hipLaunchKernelGGL((row_reduce_kernel<T, IS_F16, 1>), g, b, 0, s, xp, rows, cols, init, y, out_type, vec_ok); break;
+    case 2: hipLaunchKernelGGL((row_reduce_kernel<T, IS_F16, 2>), g, b, 0, s, xp, rows, cols, init, y, out_type, vec_ok); break;
+    case 3: hipLaunchKernelGGL((row_reduce_kernel<T, IS_F16, 3>), g, b, 0, s, xp, rows, cols, init, y, out_type, vec_ok); break;
+    default: return fail(MK_ERR_INVALID, "mk_row_reduce: op must be 0..3");
+  }
+  return check_launch("mk_row_reduce");
+}
+
+template <typename T, bool IS_F16, bool IS_MIN>
+int launch_argmax(hipStream_t s, int64_t rows, int64_t cols, const void* x, void* values,
+                  int index_type, void* indices) {
+  const bool vec_ok = aligned16(x) && (cols % Vec<T>::N) == 0;
+  dim3 g(grid_for_rows(rows)), b(kBlock);
+  const T* xp = reinterpret_cast<const T*>(x);
+  T* vp = reinterpret_cast<T*>(values);
+  if (index_type == MK_S32)
+    hipLaunchKernelGGL((row_argmax_kernel<T, IS_F16, IS_MIN, int32_t>), g, b, 0, s, xp, rows, cols,
+                       vp, reinterpret_cast<int32_t*>(indices), vec_ok);
+  else
+    hipLaunchKernelGGL((row_argmax_kernel<T, IS_F16, IS_MIN, int64_t>), g, b, 0, s, xp, rows, cols,
+                       vp, reinterpret_cast<int64_t*>(indices), vec_ok);
+  return check_launch("mk_row_argmax");
+}
+
+}  // namespace
+}  // namespace mk
+
+using namespace mk;
+
+extern "C" int mk_row_reduce(void* stream, int in_type, int out_type, int op, int64_t rows,
+                             int64_t cols, const void* x, float init, void* y) {
+  clear_error();
+  if (rows < 0 || cols < 0) return fail(MK_ERR_INVALID, "mk_row_reduce: negative shape");
+  if (out_type != MK_F32 && out_type != MK_BF16 && out_type != MK_F16)
+    return fail(MK_ERR_UNSUPPORTED, "mk_row_reduce: out_type must be f32/bf16/f16");
+  if (rows == 0) return MK_OK;
+  if (!x || !y) return fail(MK_ERR_INVALID, "mk_row_reduce: null pointer");
+  hipStream_t s = as_stream(stream);
+  switch (in_type) {
+    case MK_BF16: return launch_reduce<uint16_t, false>(s, op, rows, cols, x, init, y, out_type);
+    case MK_F16: return launch_reduce<uint16_t, true>(s, op, rows, cols, x, init, y, out_type);
+    case MK_F32: return launch_reduce<float, false>(s, op, rows, cols, x, init, y, out_type);
+    default: return fail(MK_ERR_UNSUPPORTED, "mk_row_reduce: in_type must be bf16/f16/f32");
+  }
+}
+
+extern "C" int mk_row_argmax(void* stream, int in_type, int is_min, int64_t rows, int64_t cols,
+                             const void* x, void* values, int index_type, void* indices) {
+  clear_error();
+  if (rows < 0 || cols <= 0)
+    return fail(MK_ERR_INVALID, "mk_row_argmax: need rows >= 0 and cols >= 1");
+  if (index_type != MK_S32 && index_type != MK_S64)
+    return fail(MK_ERR_UNSUPPORTED, "mk_row_argmax: index_type must be s32/s64");
+  if (rows == 0) return MK_OK;
+  if (!x || !indices) return fail(MK_ERR_INVALID, "mk_row_argmax: null pointer");
+  hipStream_t s = as_stream(stream);
+  switch (in_type) {
+    case MK_BF16:
+      return is_min ? launch_argmax<uint16_t, false, true>(s, rows, cols, x, values, index_type, indices)
+                    : launch_argmax<uint16_t, false, false>(s, rows, cols, x, values, index_type, indices);
+    case MK_F16:
+      return is_min ? launch_argmax<uint16_t, true, true>(s, rows, cols, x, values, index_type, indices)
+                    : launch_argmax<uint16_t, true, false>(s, rows, cols, x, values, index_type, indices);
+    case MK_F32:
+      return is_min ? launch_argmax<float, false, true>(s, rows, cols, x, values, index_type, indices)
+                    : launch_argmax<float, false, false>(s, rows, cols, x, values, index_type, indices);
+    default: return fail(MK_ERR_UNSUPPORTED, "mk_row_argmax: in_type must be bf16/f16/f32");
+  }
+}
+
+extern "C" int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                            const void* gamma, const void* beta, float eps, void* y) {
+  clear_error();
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_layernorm: bad shape");
+  if (rows == 0) return MK_OK;
+  if (!x || !y) return fail(MK_ERR_INVALID, "mk_layernorm: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(grid_for_rows(rows)), b(kBlock);
+  auto vec_ok = [&](int n) {
+    return (cols % n) == 0 && cols / n <= int64_t(kLnMaxVecs) * kWave && aligned16(x) &&
+           aligned16(y) && (!gamma || aligned16(gamma)) && (!beta || aligned16(beta));
+  };
+  if (io_type == MK_BF16) {
+    using T = uint16_t;
+    const T *xp = (const T*)x, *gp = (const T*)gamma, *bp = (const T*)beta;
+    if (vec_ok(8))
+      hipLaunchKernelGGL(layernorm_reg_kernel<T>, g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
+    else
+      hipLaunchKernelGGL(layernorm_loop_kernel<T>, g, b, 0, s, xp, gp, bp, rows, cols, eps, (T*)y);
+  } else if (io_type == MK_F32) {
+    using T = float;
+    const T *xp = (const T*)x, *gp = (const T*)gamma, *bp = (const T*)beta;
+    if (vec_ok(4))
+      hipLaunchKernelGGL(layernorm_reg_kernel<T>, g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
+    else
+      hipLaunchKernelGGL(layernorm_loop_kernel<T>, g, b, 0, s, xp, gp, bp, rows, cols, eps, (T*)y);
+  } else {
+    return fail(MK_ERR_UNSUPPORTED, "mk_layernorm: io_type must be bf16/f32");
+  }
+  return check_launch("mk_layernorm");
+}
+
+extern "C" int mk_softmax_rows(void* stream, int io_type, int64_t rows, int64_t cols,
+                               const void* x, void* y) {
+  clear_error();
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_softmax_rows: bad shape");
+  if (rows == 0) return MK_OK;
+  if (!x || !y) return fail(MK_ERR_INVALID, "mk_softmax_rows: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(grid_for_rows(rows)), b(kBlock);
+  if (io_type == MK_BF16)
+    hipLaunchKernelGGL(softmax_kernel<uint16_t>, g, b, 0, s, (const uint16_t*)x, rows, cols, (uint16_t*)y);
+  else if (io_type == MK_F32)
+    hipLaunchKernelGGL(softmax_kernel<float>, g, b, 0, s, (const float*)x, rows, cols, (float*)y);
+  else
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_rows: io_type must be bf16/f32");
+  return check_launch("mk_softmax_rows");
+}
