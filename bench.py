@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["sdpa", "fusions", "headline"], default=None)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -208,6 +208,14 @@ def main():
 
     K.lib()
     torch.cuda.init()
+    if args.only == "calib":
+        # plain copy of a known size: calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE
+        n = 128 << 20  # 128 Mi float32 = 512 MiB read + 512 MiB write per launch
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        ms = time_launches(torch, lambda: K.copy_strided(src), 5, 1)
+        print(json.dumps({"calib_copy_bytes_read": n * 4, "calib_copy_bytes_written": n * 4,
+                          "ms": round(ms, 4), "gbs": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}))
+        return
     sweep, head, fusions = {}, None, {}
     if args.only in (None, "sdpa", "headline"):
         sweep, head = run_sdpa(torch, np, K, args)

@@ -103,11 +103,12 @@ __global__ __launch_bounds__(kBlock) void row_reduce_kernel(const T* __restrict_
     }
   }
   acc = wave_combine<OP>(acc);
+  // the vote must run with the whole wave active, before the lane-0 branch
+  const bool any_nan = __any(nan);
   if (lane == 0) {
     float r = combine<OP>(acc, init);
     if constexpr (OP == 1 || OP == 2) {
-      bool any_nan = __any(nan) || (init != init);
-      if (any_nan) r = __builtin_nanf("");
+      if (any_nan || init != init) r = __builtin_nanf("");
     }
     store_from_f32(y, row, out_type, r);
   }

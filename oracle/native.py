@@ -52,7 +52,7 @@ def _ptr(a: np.ndarray):
 def scatter_add_f32(table, ids, updates) -> np.ndarray:
     out = np.array(table, dtype=np.float32, order="C", copy=True)
     ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
-    upd = np.ascontiguousarray(updates, dtype=np.float32).reshape(ids.size, -1)
+    upd = np.ascontiguousarray(updates, dtype=np.float32).reshape(ids.size, out.shape[1])
     load().oracle_scatter_add_f32(_ptr(out), out.shape[0], out.shape[1], _ptr(ids), ids.size, _ptr(upd))
     return out
 
@@ -60,7 +60,7 @@ def scatter_add_f32(table, ids, updates) -> np.ndarray:
 def scatter_add_bf16(table_bits, ids, updates_bits) -> np.ndarray:
     out = np.array(table_bits, dtype=np.uint16, order="C", copy=True)
     ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
-    upd = np.ascontiguousarray(updates_bits, dtype=np.uint16).reshape(ids.size, -1)
+    upd = np.ascontiguousarray(updates_bits, dtype=np.uint16).reshape(ids.size, out.shape[1])
     load().oracle_scatter_add_bf16(_ptr(out), out.shape[0], out.shape[1], _ptr(ids), ids.size, _ptr(upd))
     return out
 

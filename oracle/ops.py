@@ -205,7 +205,7 @@ def scatter_add_rows_f32(table, ids, updates):
     scatterNDWithDataTensor mode:Add of gather_scatter.mm:322-327."""
     out = np.array(table, dtype=np.float32, copy=True)
     ids = np.asarray(ids).reshape(-1).astype(np.int64)
-    upd = np.asarray(updates, dtype=np.float32).reshape(ids.shape[0], -1)
+    upd = np.asarray(updates, dtype=np.float32).reshape(ids.shape[0], out.shape[1])
     keep = (ids >= 0) & (ids < out.shape[0])
     np.add.at(out, ids[keep], upd[keep])
     return out
@@ -216,7 +216,7 @@ def scatter_add_rows_loop(table, ids, updates, round_fn=None):
     restates the bf16 variant: round_fn applied after every add)."""
     out = np.array(table, dtype=np.float32, copy=True)
     ids = np.asarray(ids).reshape(-1).astype(np.int64)
-    upd = np.asarray(updates, dtype=np.float32).reshape(ids.shape[0], -1)
+    upd = np.asarray(updates, dtype=np.float32).reshape(ids.shape[0], out.shape[1])
     for i, r in enumerate(ids):
         if 0 <= r < out.shape[0]:
             s = (out[r] + upd[i]).astype(np.float32)
