@@ -55,8 +55,9 @@ int mk_device_count(void);
  *   B element (b,k,n) at  B + b*b_bs + k*b_ks + n*b_ns
  *   C element (b,m,n) at  C + b*c_bs + m*c_ms + n        (row-major rows)
  * One of (a_ms, a_ks) and one of (b_ks, b_ns) must be 1 (unit stride); the
- * other operand stride is the leading dimension.  ab_type ∈ {MK_F32, MK_BF16,
- * MK_F16}; c_type ∈ {MK_F32, MK_BF16, MK_F16}; accumulation is always fp32.
+ * other operand stride is the leading dimension.  ab_type ∈ {MK_F32, MK_BF16}
+ * (MK_F16 returns MK_ERR_UNSUPPORTED); c_type ∈ {MK_F32, MK_BF16, MK_F16};
+ * accumulation is always fp32 (true fp32 MFMA for MK_F32 operands).
  * epilogue: 0 none, 1 +bias, 2 +bias then max(.,0).  bias has c_type, may be
  * NULL when epilogue == 0.
  * ---------------------------------------------------------------------- */
@@ -75,7 +76,9 @@ int mk_gemm(void* stream, int ab_type, int c_type,
  * causal mask built by shape.mm:249-256 (iota), binary.mm:84-109 (compare)
  * and binary.mm:77-82 (select).  The [S,S] score matrix never exists.
  *
- * O[b,h,i,:] = softmax_j( scale * Q[b,h,i,:]·K[b,h,j,:] , j ≤ i+Sk-Sq if causal ) · V[b,h,j,:]
+ * O[b,h,i,:] = softmax_j( scale * Q[b,h,i,:]·K[b,h,j,:] , j ≤ i if causal ) · V[b,h,j,:]
+ * (causal = jnp.tril of the [Sq, Sk] score matrix, top-left aligned; a row
+ * with no visible key yields NaN, as softmax over all -inf does).
  * Tensors are bf16 with D contiguous; the other strides are in elements:
  *   X element (b,h,s,d) at X + b*x_bs + h*x_hs + s*x_ss + d.
  * D ∈ {64, 128}.  Accumulation fp32, online softmax in fp32.
@@ -143,9 +146,11 @@ int mk_gelu_tanh(void* stream, int io_type, int64_t n, const void* x, void* y);
  * broadcast_in_dim / transpose feeding the chain are folded into addressing.
  * Program: n_instr instructions of 4 int32 {opcode, dst, a, b} plus a third
  * operand for select/clamp packed in the high 16 bits of `b` (see
- * mk_ew_op).  Registers 0..n_inputs-1 are preloaded with the inputs
- * (converted to fp32 / int32 semantics per in_types); constants come from
- * `consts` (fp32) via MK_EW_CONST.  Register `out_reg` is stored, converted
+ * mk_ew_op).  Registers 0..n_inputs-1 are preloaded with the inputs: float
+ * types widen to fp32, integer types are held as their int32 bit pattern
+ * (sign- or zero-extended; 64-bit truncated), predicates as 0.0f / 1.0f.
+ * Stores convert back the same way.  Constants come from `consts` (32-bit
+ * patterns, read as fp32) via MK_EW_CONST.  Register `out_reg` is stored, converted
  * to out_type.  At most 32 registers, 64 instructions, 8 inputs.
  * ---------------------------------------------------------------------- */
 typedef enum mk_ew_op {
@@ -165,6 +170,12 @@ typedef enum mk_ew_op {
   MK_EW_ADD_S32, MK_EW_SUB_S32, MK_EW_MUL_S32,
   MK_EW_S32_TO_F32, MK_EW_F32_TO_S32,  /* C-style truncation toward zero        */
   MK_EW_ERF,
+  MK_EW_CMP_EQ_S32, MK_EW_CMP_NE_S32, MK_EW_CMP_LE_S32, MK_EW_CMP_GT_S32,
+  MK_EW_MAX_S32, MK_EW_MIN_S32, MK_EW_NEG_S32,
+  MK_EW_AND_B32, MK_EW_OR_B32, MK_EW_XOR_B32, /* bitwise on raw 32-bit patterns */
+  MK_EW_PRED_TO_S32,                   /* 0/1 predicate -> int32 0/1            */
+  MK_EW_S32_TO_PRED,                   /* int32 != 0 -> predicate               */
+  MK_EW_U32_TO_F32,
   MK_EW_NUM_OPS
 } mk_ew_op;
 

@@ -201,11 +201,12 @@ def copy_strided(x, stream=None):
     return out
 
 
-EW = dict(CONST=0, ADD=1, SUB=2, MUL=3, DIV=4, MAX=5, MIN=6, POW=7, NEG=8, EXP=9, LOG=10,
-          TANH=11, SQRT=12, RSQRT=13, ABS=14, LOGISTIC=15, CMP_EQ=16, CMP_NE=17, CMP_LT=18,
-          CMP_LE=19, CMP_GT=20, CMP_GE=21, SELECT=22, CLAMP=23, ROUND_BF16=24, ROUND_F16=25,
-          FLOOR=26, CEIL=27, SIGN=28, AND=29, OR=30, NOT=31, MOV=32, CMP_LT_S32=33,
-          CMP_GE_S32=34, ADD_S32=35, SUB_S32=36, MUL_S32=37, S32_TO_F32=38, F32_TO_S32=39, ERF=40)
+_EW_NAMES = ("CONST ADD SUB MUL DIV MAX MIN POW NEG EXP LOG TANH SQRT RSQRT ABS LOGISTIC "
+             "CMP_EQ CMP_NE CMP_LT CMP_LE CMP_GT CMP_GE SELECT CLAMP ROUND_BF16 ROUND_F16 FLOOR "
+             "CEIL SIGN AND OR NOT MOV CMP_LT_S32 CMP_GE_S32 ADD_S32 SUB_S32 MUL_S32 S32_TO_F32 "
+             "F32_TO_S32 ERF CMP_EQ_S32 CMP_NE_S32 CMP_LE_S32 CMP_GT_S32 MAX_S32 MIN_S32 NEG_S32 "
+             "AND_B32 OR_B32 XOR_B32 PRED_TO_S32 S32_TO_PRED U32_TO_F32").split()
+EW = {n: i for i, n in enumerate(_EW_NAMES)}  # mirrors enum mk_ew_op in include/mk_kernels.h
 
 
 def ew_program(shape, inputs, program, consts, out_reg, out_dtype, stream=None):

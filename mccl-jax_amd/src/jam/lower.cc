@@ -1,0 +1,2251 @@
+// jam lowering: StableHLO IR -> launch plan over the mk_* C-ABI.
+//
+// Mirrors the role of the reference's Lower/WalkBlock (src/jam/lower.mm:
+// 208-314, 460-566): inline func.call (245-268), bind @main arguments
+// (477-487), dispatch every op, fail with "jam: unhandled op '<name>'" for
+// anything without a lowering (308-310).  Where the reference emits one
+// MPSGraph node per op, jam emits kernel launches:
+//   * layout ops (reshape, broadcast_in_dim, transpose, slice) become strided
+//     views and cost nothing until a consumer needs dense memory;
+//   * chains of elementwise ops (incl. convert, compare, select, clamp) are
+//     kept as expressions and compiled into ONE mk_ew_program launch each,
+//     with per-op bf16/f16 rounding where the StableHLO result type is
+//     bf16/f16 (what XLA:CPU computes);
+//   * pattern matchers replace whole subgraphs by a fused kernel: causal /
+//     full scaled-dot-product attention (QKᵀ -> scale -> mask -> softmax ->
+//     PV, cf. TrySoftmax elementwise.mm:71-89), arg-max/min reduces
+//     (DetectArgReduce reduce.mm:29-43), dot_general + bias (+ ReLU);
+//   * temporaries live in one arena per run, packed by liveness.
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <random>
+#include <set>
+#include <sstream>
+#include <unordered_map>
+
+#include "jam/ir.h"
+#include "jam/program.h"
+#include "mk_kernels.h"
+
+namespace mi::jam {
+
+const char* StepName(StepKind k) {
+  switch (k) {
+    case StepKind::kGemm: return "gemm";
+    case StepKind::kSdpa: return "sdpa";
+    case StepKind::kRowReduce: return "row_reduce";
+    case StepKind::kArgmax: return "argmax";
+    case StepKind::kLayerNorm: return "layernorm";
+    case StepKind::kGelu: return "gelu";
+    case StepKind::kEw: return "ew";
+    case StepKind::kGather: return "gather";
+    case StepKind::kScatterAdd: return "scatter_add";
+    case StepKind::kIota: return "iota";
+    case StepKind::kCopyStrided: return "copy_strided";
+    case StepKind::kSoftmax: return "softmax";
+    case StepKind::kConvert: return "convert";
+    case StepKind::kFill: return "fill";
+    case StepKind::kCopy: return "copy";
+  }
+  return "?";
+}
+
+std::string Program::Dump() const {
+  std::ostringstream os;
+  os << "program " << name << ": " << inputs.size() << " inputs, " << outputs.size()
+     << " outputs, " << steps.size() << " steps, arena " << arena_bytes << " B, " << consts.size()
+     << " consts\n";
+  for (const auto& p : patterns) os << "  pattern " << p << "\n";
+  for (size_t i = 0; i < steps.size(); ++i) {
+    os << "  [" << i << "] " << StepName(steps[i].kind);
+    if (!steps[i].note.empty()) os << " (" << steps[i].note << ")";
+    os << "\n";
+  }
+  return os.str();
+}
+
+CompileOptions OptionsFromEnv() {
+  CompileOptions o;
+  o.fuse_sdpa = getenv("JAM_NO_SDPA") == nullptr;
+  o.fuse_argmax = getenv("JAM_NO_ARGMAX") == nullptr;
+  o.fuse_gemm_epilogue = getenv("JAM_NO_GEMM_EPILOGUE") == nullptr;
+  o.fuse_layernorm = getenv("JAM_NO_LAYERNORM") == nullptr;
+  o.fuse_gelu = getenv("JAM_NO_GELU") == nullptr;
+  o.fuse_elementwise = getenv("JAM_NO_EW_FUSION") == nullptr;
+  return o;
+}
+
+namespace {
+
+// ------------------------------------------------------------------ constants
+uint16_t F32ToBf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+float Bf16ToF32(uint16_t h) {
+  uint32_t u = uint32_t(h) << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+// IEEE half, round to nearest even, with subnormals (the reference's
+// FloatToHalf, structural.mm:22-31, truncates and flushes; XLA rounds).
+uint16_t F32ToF16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return uint16_t(sign | 0x7e00u);
+  if (ax >= 0x477ff000u) return uint16_t(sign | 0x7c00u);  // rounds to >= 65520 -> inf
+  if (ax < 0x33000001u) return uint16_t(sign);             // < 2^-25 (+) -> 0
+  int e = int(ax >> 23) - 127;
+  uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+  int shift = e >= -14 ? 13 : 13 + (-14 - e);
+  uint32_t hm = m >> shift;
+  uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (hm & 1u))) ++hm;
+  uint32_t h = e >= -14 ? (uint32_t(e + 15) << 10) + (hm - 0x400u) : hm;
+  if (e >= -14 && hm >= 0x800u) h = (uint32_t(e + 16) << 10);  // mantissa overflow
+  return uint16_t(sign | h);
+}
+float F16ToF32(uint16_t h) {
+  const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t u;
+  if (e == 0) {
+    if (m == 0) u = s;
+    else {
+      float v = std::ldexp(float(m), -24);
+      memcpy(&u, &v, 4);
+      u |= s;
+    }
+  } else if (e == 31) {
+    u = s | 0x7f800000u | (m << 13);
+  } else {
+    u = s | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+double HexToValue(uint64_t bits, DType d) {
+  switch (d) {
+    case DType::kF32: {
+      uint32_t u = uint32_t(bits);
+      float f;
+      memcpy(&f, &u, 4);
+      return f;
+    }
+    case DType::kF64: {
+      double v;
+      memcpy(&v, &bits, 8);
+      return v;
+    }
+    case DType::kBF16: return Bf16ToF32(uint16_t(bits));
+    case DType::kF16: return F16ToF32(uint16_t(bits));
+    default: return double(int64_t(bits));
+  }
+}
+
+// Parse the body of dense<...> for a tensor type.  Fills fvals / ivals.
+bool ParseDense(Attr& a, const TensorType& t, std::string& err) {
+  std::string s = a.s;
+  const int64_t n = t.numel();
+  const bool fl = IsFloat(t.dtype);
+  a.fvals.clear();
+  a.ivals.clear();
+  auto trim = [](std::string x) {
+    size_t b = x.find_first_not_of(" \n\t"), e = x.find_last_not_of(" \n\t");
+    return b == std::string::npos ? std::string() : x.substr(b, e - b + 1);
+  };
+  s = trim(s);
+  if (s.size() >= 3 && s[0] == '"' && s[1] == '0' && (s[2] == 'x' || s[2] == 'X')) {
+    // raw little-endian element bytes
+    std::string hex = s.substr(3, s.size() - 4);
+    std::vector<uint8_t> bytes;
+    for (size_t i = 0; i + 1 < hex.size(); i += 2) bytes.push_back(uint8_t(strtoul(hex.substr(i, 2).c_str(), nullptr, 16)));
+    const int w = DTypeBytes(t.dtype);
+    if (w == 0 || bytes.size() % size_t(w) != 0) {
+      err = "jam: malformed dense hex constant";
+      return false;
+    }
+    const size_t cnt = bytes.size() / size_t(w);
+    for (size_t i = 0; i < cnt; ++i) {
+      uint64_t bits = 0;
+      memcpy(&bits, &bytes[i * w], w);
+      if (fl) a.fvals.push_back(HexToValue(bits, t.dtype));
+      else if (IsSigned(t.dtype)) {
+        int64_t v = int64_t(bits << (64 - 8 * w)) >> (64 - 8 * w);
+        a.ivals.push_back(v);
+      } else {
+        a.ivals.push_back(int64_t(bits));
+      }
+    }
+  } else {
+    std::string tok;
+    auto flush = [&]() {
+      if (tok.empty()) return;
+      if (tok == "true" || tok == "false") {
+        a.ivals.push_back(tok == "true");
+        a.fvals.push_back(tok == "true");
+      } else if (tok.size() > 2 && tok[0] == '0' && (tok[1] == 'x' || tok[1] == 'X')) {
+        uint64_t bits = strtoull(tok.c_str(), nullptr, 16);
+        if (fl) a.fvals.push_back(HexToValue(bits, t.dtype));
+        else a.ivals.push_back(int64_t(bits));
+      } else if (tok == "inf" || tok == "+inf") {
+        a.fvals.push_back(INFINITY);
+      } else if (tok == "-inf") {
+        a.fvals.push_back(-INFINITY);
+      } else if (tok == "nan") {
+        a.fvals.push_back(NAN);
+      } else {
+        if (fl) a.fvals.push_back(strtod(tok.c_str(), nullptr));
+        else a.ivals.push_back(strtoll(tok.c_str(), nullptr, 10));
+      }
+      tok.clear();
+    };
+    for (char c : s) {
+      if (c == '[' || c == ']' || c == ',' || c == ' ' || c == '\n' || c == '(' || c == ')') flush();
+      else tok.push_back(c);
+    }
+    flush();
+  }
+  const size_t cnt = fl ? a.fvals.size() : a.ivals.size();
+  if (cnt == 1 && n != 1) a.splat = true;
+  else if (int64_t(cnt) != n) {
+    err = "jam: dense constant has " + std::to_string(cnt) + " values for " + t.str();
+    return false;
+  } else {
+    a.splat = (n == 1);
+  }
+  if (fl && a.ivals.empty()) for (double v : a.fvals) a.ivals.push_back(int64_t(v));
+  if (!fl && a.fvals.empty()) for (int64_t v : a.ivals) a.fvals.push_back(double(v));
+  return true;
+}
+
+void EncodeElement(double v, int64_t iv, DType d, uint8_t* out) {
+  switch (d) {
+    case DType::kF32: { float f = float(v); memcpy(out, &f, 4); break; }
+    case DType::kF64: memcpy(out, &v, 8); break;
+    case DType::kBF16: { uint16_t h = F32ToBf16(float(v)); memcpy(out, &h, 2); break; }
+    case DType::kF16: { uint16_t h = F32ToF16(float(v)); memcpy(out, &h, 2); break; }
+    case DType::kPred: out[0] = iv != 0; break;
+    default: memcpy(out, &iv, size_t(DTypeBytes(d))); break;
+  }
+}
+
+// value of a scalar of type d as it lives in the ew register file (32 bits)
+uint32_t RegisterBits(double v, int64_t iv, DType d) {
+  float f;
+  if (IsFloat(d)) {
+    if (d == DType::kBF16) f = Bf16ToF32(F32ToBf16(float(v)));
+    else if (d == DType::kF16) f = F16ToF32(F32ToF16(float(v)));
+    else f = float(v);
+  } else if (d == DType::kPred) {
+    f = iv != 0 ? 1.f : 0.f;
+  } else {
+    int32_t i = int32_t(iv);
+    memcpy(&f, &i, 4);
+  }
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+// ------------------------------------------------------------------ views
+struct View {
+  BufRef buf;                     // base buffer (offset in bytes)
+  DType dtype = DType::kInvalid;
+  std::vector<int64_t> dims;
+  std::vector<int64_t> strides;   // elements
+  int64_t offset = 0;             // elements, added to buf.offset
+
+  int rank() const { return int(dims.size()); }
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t d : dims) n *= d;
+    return n;
+  }
+  bool dense() const {
+    int64_t e = 1;
+    for (int d = rank() - 1; d >= 0; --d) {
+      if (dims[d] != 1 && strides[d] != e) return false;
+      e *= dims[d];
+    }
+    return true;
+  }
+  BufRef at() const {
+    BufRef r = buf;
+    r.offset += offset * DTypeBytes(dtype);
+    return r;
+  }
+};
+
+std::vector<int64_t> DenseStrides(const std::vector<int64_t>& dims) {
+  std::vector<int64_t> s(dims.size());
+  int64_t e = 1;
+  for (int d = int(dims.size()) - 1; d >= 0; --d) {
+    s[d] = e;
+    e *= dims[d];
+  }
+  return s;
+}
+
+// ------------------------------------------------------------------ lowering state
+struct ValState {
+  enum Kind { kUnset, kView, kEw, kScalar } kind = kUnset;
+  View view;
+  double fval = 0;      // kScalar
+  int64_t ival = 0;
+  int op = -1;          // kEw: index of the producing op
+};
+
+struct Fused {
+  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu } kind;
+  std::vector<int> deps;  // value ids the fused step reads
+  // sdpa
+  int q = -1, k = -1, v = -1;
+  float scale = 1.f;
+  bool causal = false;
+  // argmax
+  int x = -1;
+  bool is_min = false;
+  int red_op = -1;
+  // gemm epilogue
+  int dot = -1, bias = -1;
+  bool relu = false;
+  // layernorm
+  int gamma = -1, beta = -1;
+  float eps = 0;
+  DType out_dtype = DType::kInvalid;
+};
+
+class Lowerer {
+ public:
+  Lowerer(Module& m, const CompileOptions& o) : m_(m), opts_(o) {}
+
+  std::shared_ptr<Program> Run(std::string& err) {
+    prog_ = std::make_shared<Program>();
+    try {
+      const Func* main = m_.find("main");
+      if (!main) {
+        for (const auto& f : m_.funcs)
+          if (f.is_public) main = &f;
+      }
+      if (!main) throw std::string("jam: module has no @main function");  // lower.mm:464-466
+      prog_->name = "jam." + (m_.name.empty() ? std::string("main") : m_.name);
+      // flatten: inline calls
+      std::unordered_map<int, int> remap;
+      for (int a : main->args) {
+        prog_->inputs.push_back(m_.types[a]);
+        ops_.reserve(64);
+      }
+      Inline(*main, main->args, outputs_, 0);
+      for (int o : outputs_) prog_->outputs.push_back(m_.types[o]);
+      state_.assign(m_.types.size(), ValState());
+      for (size_t i = 0; i < main->args.size(); ++i) {
+        ValState& s = state_[main->args[i]];
+        s.kind = ValState::kView;
+        s.view.buf = BufRef{Space::kInput, int(i), 0};
+        s.view.dtype = m_.types[main->args[i]].dtype;
+        s.view.dims = m_.types[main->args[i]].dims;
+        s.view.strides = DenseStrides(s.view.dims);
+      }
+      Analyze();
+      MatchPatterns();
+      Liveness();
+      Walk();
+      PackArena();
+      return prog_;
+    } catch (const std::string& e) {
+      err = e;
+      return nullptr;
+    }
+  }
+
+ private:
+  // -------------------------------------------------------------- inlining
+  // Appends the ops of `f` (with args bound to `actuals`) to ops_, renaming
+  // values; returns the values `f` returns in `results`.
+  void Inline(const Func& f, const std::vector<int>& actuals, std::vector<int>& results, int depth) {
+    if (depth > 32) throw std::string("jam: call depth exceeds 32 (recursive call?)");
+    std::unordered_map<int, int> ren;
+    for (size_t i = 0; i < f.args.size(); ++i) ren[f.args[i]] = actuals[i];
+    auto R = [&](int v) {
+      auto it = ren.find(v);
+      return it == ren.end() ? v : it->second;
+    };
+    for (const Op& op0 : f.body.ops) {
+      if (op0.name == "return") {
+        results.clear();
+        for (int v : op0.operands) results.push_back(R(v));
+        return;
+      }
+      if (op0.name == "func.call") {
+        const Attr* callee = op0.attr("callee");
+        const Func* g = callee ? m_.find(callee->s) : nullptr;
+        if (!g) throw std::string("jam: call to unknown function @" + (callee ? callee->s : "?"));
+        std::vector<int> acts, rets;
+        for (int v : op0.operands) acts.push_back(R(v));
+        Inline(*g, acts, rets, depth + 1);
+        if (rets.size() != op0.results.size()) throw std::string("jam: call result count mismatch");
+        for (size_t i = 0; i < rets.size(); ++i) ren[op0.results[i]] = rets[i];
+        continue;
+      }
+      if (op0.name == "stablehlo.optimization_barrier") {
+        for (size_t i = 0; i < op0.results.size(); ++i) ren[op0.results[i]] = R(op0.operands[i]);
+        continue;
+      }
+      Op op = op0;
+      for (int& v : op.operands) v = R(v);
+      // fresh result ids when a function is inlined more than once
+      if (inlined_once_.count(&f)) {
+        for (int& r : op.results) {
+          int nv = m_.new_value(m_.types[r]);
+          ren[r] = nv;
+          r = nv;
+        }
+      }
+      ops_.push_back(op);
+    }
+    inlined_once_.insert(&f);
+  }
+
+  // -------------------------------------------------------------- analysis
+  void Analyze() {
+    producer_.assign(m_.types.size(), -1);
+    uses_.assign(m_.types.size(), 0);
+    users_.assign(m_.types.size(), {});
+    for (size_t i = 0; i < ops_.size(); ++i) {
+      for (int r : ops_[i].results) producer_[r] = int(i);
+      for (int v : ops_[i].operands) {
+        ++uses_[v];
+        users_[v].push_back(int(i));
+      }
+    }
+    for (int o : outputs_) ++uses_[o];
+  }
+  const Op* prod(int v) const { return v >= 0 && producer_[v] >= 0 ? &ops_[producer_[v]] : nullptr; }
+  bool is(int v, const char* name) const {
+    const Op* p = prod(v);
+    return p && p->name == name;
+  }
+  int through_converts(int v, std::vector<int>* path = nullptr) const {
+    while (is(v, "stablehlo.convert") || is(v, "stablehlo.reshape")) {
+      if (path) path->push_back(producer_[v]);
+      v = prod(v)->operands[0];
+    }
+    return v;
+  }
+  // scalar value of a splat constant (possibly broadcast / reshaped / converted)
+  bool scalar_of(int v, double* out) const {
+    for (;;) {
+      const Op* p = prod(v);
+      if (!p) return false;
+      if (p->name == "stablehlo.broadcast_in_dim" || p->name == "stablehlo.reshape" ||
+          p->name == "stablehlo.convert" || p->name == "stablehlo.broadcast") {
+        v = p->operands[0];
+        continue;
+      }
+      if (p->name != "stablehlo.constant") return false;
+      Attr a = *p->attr("value");
+      std::string err;
+      if (!ParseDense(a, m_.types[v], err)) return false;
+      if (!a.splat && m_.types[v].numel() != 1) return false;
+      const DType d = m_.types[v].dtype;
+      double x = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
+      if (d == DType::kBF16) x = Bf16ToF32(F32ToBf16(float(x)));
+      else if (d == DType::kF16) x = F16ToF32(F32ToF16(float(x)));
+      else if (d == DType::kF32) x = float(x);
+      *out = x;
+      return true;
+    }
+  }
+  std::vector<int64_t> attr_ints(const Op& op, std::initializer_list<const char*> names) const {
+    for (const char* n : names)
+      if (const Attr* a = op.attr(n)) return a->ints();
+    return {};
+  }
+  struct DotDims {
+    std::vector<int64_t> lb, rb, lc, rc;
+  };
+  DotDims dot_dims(const Op& op) const {
+    DotDims d;
+    if (const Attr* dn = op.attr("dot_dimension_numbers")) {
+      if (const Attr* x = dn->get("lhs_batching_dimensions")) d.lb = x->ints();
+      if (const Attr* x = dn->get("rhs_batching_dimensions")) d.rb = x->ints();
+      if (const Attr* x = dn->get("lhs_contracting_dimensions")) d.lc = x->ints();
+      if (const Attr* x = dn->get("rhs_contracting_dimensions")) d.rc = x->ints();
+      return d;
+    }
+    if (const Attr* b = op.attr("batching_dims")) {
+      d.lb = b->list.at(0).ints();
+      d.rb = b->list.at(1).ints();
+    }
+    if (const Attr* c = op.attr("contracting_dims")) {
+      d.lc = c->list.at(0).ints();
+      d.rc = c->list.at(1).ints();
+    }
+    return d;
+  }
+  std::vector<int64_t> reduce_dims(const Op& op) const { return attr_ints(op, {"dimensions"}); }
+  std::string reduce_body_op(const Op& op) const {
+    if (op.regions.empty() || op.regions[0]->blocks.empty()) return "";
+    for (const Op& b : op.regions[0]->blocks[0].ops)
+      if (b.name != "return") return b.name;
+    return "";
+  }
+
+  // -------------------------------------------------------------- pattern matching
+  void MatchPatterns() {
+    for (size_t i = 0; i < ops_.size(); ++i) {
+      const Op& op = ops_[i];
+      if (op.name == "stablehlo.dot_general" && opts_.fuse_sdpa) TryMatchSdpa(int(i));
+      if (op.name == "stablehlo.reduce" && op.operands.size() == 4 && op.results.size() == 2 &&
+          opts_.fuse_argmax)
+        TryMatchArgmax(int(i));
+    }
+    if (opts_.fuse_gemm_epilogue)
+      for (size_t i = 0; i < ops_.size(); ++i)
+        if (ops_[i].name == "stablehlo.add" && !fused_.count(int(i))) TryMatchGemmEpilogue(int(i));
+    if (opts_.fuse_gelu)
+      for (size_t i = 0; i < ops_.size(); ++i)
+        if (ops_[i].name == "stablehlo.multiply" && !fused_.count(int(i))) TryMatchGelu(int(i));
+    if (opts_.fuse_layernorm)
+      for (size_t i = ops_.size(); i-- > 0;)
+        if (!fused_.count(int(i)) && (ops_[i].name == "stablehlo.add" || ops_[i].name == "stablehlo.multiply" ||
+                                      ops_[i].name == "stablehlo.convert"))
+          TryMatchLayerNorm(int(i));
+  }
+
+  // ---- small structural-matching helpers
+  bool IsConstNear(int v, double c, double rtol = 1e-6) const {
+    double x;
+    return scalar_of(v, &x) && std::fabs(x - c) <= rtol * std::max(1.0, std::fabs(c));
+  }
+  // commutative binary op `name` at v: f(a, b) for either operand order
+  template <typename F>
+  bool Comm(int v, const char* name, F f) const {
+    const Op* p = prod(v);
+    if (!p || p->name != name || p->operands.size() != 2) return false;
+    return f(p->operands[0], p->operands[1]) || f(p->operands[1], p->operands[0]);
+  }
+  template <typename F>
+  bool NonComm(int v, const char* name, F f) const {
+    const Op* p = prod(v);
+    if (!p || p->name != name || p->operands.size() != 2) return false;
+    return f(p->operands[0], p->operands[1]);
+  }
+  // v = broadcast/reshape chain of a 1-D vector [n] onto the last dim of a
+  // rank-r result; returns the vector (looking through one convert) or -1
+  int VectorOnLastDim(int v, int64_t n, std::set<int>* ops) const {
+    const TensorType& ot = m_.types[v];
+    int b = v;
+    std::vector<const Op*> chain;
+    while ((is(b, "stablehlo.broadcast_in_dim") || is(b, "stablehlo.reshape")) && m_.types[b].rank() != 1) {
+      chain.push_back(prod(b));
+      b = prod(b)->operands[0];
+    }
+    if (chain.empty() || m_.types[b].rank() != 1 || m_.types[b].dims[0] != n) return -1;
+    int pos = 0;
+    for (auto it = chain.rbegin(); it != chain.rend(); ++it) {
+      const Op* p = *it;
+      const auto& rd = m_.types[p->results[0]].dims;
+      if (p->name == "stablehlo.broadcast_in_dim") {
+        const auto dd = attr_ints(*p, {"dims", "broadcast_dimensions"});
+        if (pos >= int(dd.size())) return -1;
+        pos = int(dd[pos]);
+      } else {
+        int found = -1, nonunit = 0;
+        for (size_t k = 0; k < rd.size(); ++k)
+          if (rd[k] != 1) {
+            ++nonunit;
+            found = int(k);
+          }
+        if (nonunit != 1 || rd[found] != n) return -1;
+        pos = found;
+      }
+    }
+    if (pos != ot.rank() - 1) return -1;
+    if (ops)
+      for (const Op* p : chain) ops->insert(int(p - ops_.data()));
+    if (is(b, "stablehlo.convert")) {
+      if (ops) ops->insert(producer_[b]);
+      b = prod(b)->operands[0];
+    }
+    return b;
+  }
+  // v = broadcast chain of a row statistic: reduce_add over the last dim of
+  // `x_full` (rank r) kept as [rows..., 1] and broadcast back; returns the
+  // reduce input or -1.  scale: divide by n / multiply by 1/n folded in.
+  int RowMeanOf(int v, int64_t n, std::set<int>& ops) const {
+    int b = v;
+    while (is(b, "stablehlo.broadcast_in_dim") || is(b, "stablehlo.reshape")) {
+      ops.insert(producer_[b]);
+      b = prod(b)->operands[0];
+    }
+    // mean = sum / n  or  sum * (1/n)
+    int sum = -1;
+    if (NonComm(b, "stablehlo.divide", [&](int a, int c) {
+          if (!IsConstNear(c, double(n))) return false;
+          sum = a;
+          return true;
+        }) ||
+        Comm(b, "stablehlo.multiply", [&](int a, int c) {
+          if (!IsConstNear(c, 1.0 / double(n), 1e-6)) return false;
+          sum = a;
+          return true;
+        })) {
+      ops.insert(producer_[b]);
+    } else {
+      return -1;
+    }
+    while (is(sum, "stablehlo.broadcast_in_dim") || is(sum, "stablehlo.reshape")) {
+      ops.insert(producer_[sum]);
+      sum = prod(sum)->operands[0];
+    }
+    const Op* r = prod(sum);
+    if (!r || r->name != "stablehlo.reduce" || r->operands.size() != 2 || reduce_body_op(*r) != "stablehlo.add")
+      return -1;
+    double init;
+    if (!scalar_of(r->operands[1], &init) || init != 0.0) return -1;
+    const int in = r->operands[0];
+    const auto dims = reduce_dims(*r);
+    if (dims.size() != 1 || dims[0] != m_.types[in].rank() - 1 || m_.types[in].dims.back() != n) return -1;
+    ops.insert(producer_[sum]);
+    return in;
+  }
+
+  // all uses of `v` are by ops in `set` (and v is not a program output)
+  bool uses_within(int v, const std::set<int>& set) const {
+    for (int o : outputs_)
+      if (o == v) return false;
+    for (int u : users_[v])
+      if (!set.count(u)) return false;
+    return true;
+  }
+
+  // Point evaluation of a mask expression at index `idx`; false when the
+  // expression is not a static function of iota/constants.
+  bool EvalPoint(int v, const std::vector<int64_t>& idx, double* out, int depth = 0) const {
+    if (depth > 64) return false;
+    const Op* p = prod(v);
+    if (!p) return false;
+    const auto& od = m_.types[v].dims;
+    auto ev = [&](int w, const std::vector<int64_t>& ix, double* r) { return EvalPoint(w, ix, r, depth + 1); };
+    const std::string& n = p->name;
+    if (n == "stablehlo.iota") {
+      const auto dd = attr_ints(*p, {"dim", "iota_dimension"});
+      *out = double(idx.at(dd.empty() ? 0 : dd[0]));
+      return true;
+    }
+    if (n == "stablehlo.constant") {
+      Attr a = *p->attr("value");
+      std::string err;
+      if (!ParseDense(a, m_.types[v], err)) return false;
+      if (a.splat) {
+        *out = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
+        return true;
+      }
+      int64_t lin = 0;
+      for (size_t d = 0; d < od.size(); ++d) lin = lin * od[d] + idx[d];
+      *out = a.fvals.at(size_t(lin));
+      return true;
+    }
+    if (n == "stablehlo.broadcast_in_dim") {
+      const auto dims = attr_ints(*p, {"dims", "broadcast_dimensions"});
+      const auto& id = m_.types[p->operands[0]].dims;
+      std::vector<int64_t> ix(id.size());
+      for (size_t k = 0; k < id.size(); ++k) ix[k] = id[k] == 1 ? 0 : idx.at(dims.at(k));
+      return ev(p->operands[0], ix, out);
+    }
+    if (n == "stablehlo.reshape") {
+      int64_t lin = 0;
+      for (size_t d = 0; d < od.size(); ++d) lin = lin * od[d] + idx[d];
+      const auto& id = m_.types[p->operands[0]].dims;
+      std::vector<int64_t> ix(id.size());
+      for (int d = int(id.size()) - 1; d >= 0; --d) {
+        ix[d] = lin % id[d];
+        lin /= id[d];
+      }
+      return ev(p->operands[0], ix, out);
+    }
+    if (n == "stablehlo.transpose") {
+      const auto perm = attr_ints(*p, {"dims", "permutation"});
+      std::vector<int64_t> ix(perm.size());
+      for (size_t k = 0; k < perm.size(); ++k) ix[perm[k]] = idx[k];
+      return ev(p->operands[0], ix, out);
+    }
+    if (n == "stablehlo.convert") return ev(p->operands[0], idx, out);
+    double a = 0, b = 0, c = 0;
+    if (n == "stablehlo.compare") {
+      if (!ev(p->operands[0], idx, &a) || !ev(p->operands[1], idx, &b)) return false;
+      std::string dir;
+      if (const Attr* x = p->attr("comparison_direction")) dir = x->s;
+      else if (const Attr* x = p->attr("enum0")) dir = x->s;
+      if (dir == "GE") *out = a >= b;
+      else if (dir == "GT") *out = a > b;
+      else if (dir == "LE") *out = a <= b;
+      else if (dir == "LT") *out = a < b;
+      else if (dir == "EQ") *out = a == b;
+      else if (dir == "NE") *out = a != b;
+      else return false;
+      return true;
+    }
+    if (n == "stablehlo.select") {
+      if (!ev(p->operands[0], idx, &a)) return false;
+      return ev(p->operands[a != 0 ? 1 : 2], idx, out);
+    }
+    if (p->operands.size() == 2 && (n == "stablehlo.add" || n == "stablehlo.subtract" ||
+                                    n == "stablehlo.multiply" || n == "stablehlo.and" ||
+                                    n == "stablehlo.or")) {
+      if (!ev(p->operands[0], idx, &a) || !ev(p->operands[1], idx, &b)) return false;
+      if (n == "stablehlo.add") *out = a + b;
+      else if (n == "stablehlo.subtract") *out = a - b;
+      else if (n == "stablehlo.multiply") *out = a * b;
+      else if (n == "stablehlo.and") *out = (a != 0) && (b != 0);
+      else *out = (a != 0) || (b != 0);
+      return true;
+    }
+    if (n == "stablehlo.not") {
+      if (!ev(p->operands[0], idx, &c)) return false;
+      *out = c == 0;
+      return true;
+    }
+    return false;
+  }
+
+  // 1 = causal (key j visible iff j <= i), 0 = all visible, -1 = other/unknown
+  int ClassifyMask(int mask, int64_t B, int64_t H, int64_t Sq, int64_t Sk) const {
+    std::vector<std::pair<int64_t, int64_t>> pts;
+    if (Sq * Sk <= 4096) {
+      for (int64_t i = 0; i < Sq; ++i)
+        for (int64_t j = 0; j < Sk; ++j) pts.push_back({i, j});
+    } else {
+      for (int64_t i = 0; i < std::min(Sq, Sk); i += std::max<int64_t>(1, std::min(Sq, Sk) / 512)) {
+        pts.push_back({i, i});
+        if (i + 1 < Sk) pts.push_back({i, i + 1});
+        if (i > 0) pts.push_back({i, i - 1});
+      }
+      pts.push_back({0, Sk - 1});
+      pts.push_back({Sq - 1, 0});
+      pts.push_back({Sq - 1, Sk - 1});
+      std::mt19937_64 rng(12345);
+      for (int t = 0; t < 2000; ++t) pts.push_back({int64_t(rng() % uint64_t(Sq)), int64_t(rng() % uint64_t(Sk))});
+    }
+    bool all_true = true, causal = true;
+    for (int64_t b : {int64_t(0), B - 1})
+      for (int64_t h : {int64_t(0), H - 1})
+        for (auto& ij : pts) {
+          double r = 0;
+          if (!EvalPoint(mask, {b, h, ij.first, ij.second}, &r)) return -1;
+          const bool vis = r != 0;
+          all_true &= vis;
+          causal &= (vis == (ij.second <= ij.first));
+        }
+    if (all_true) return 0;
+    return causal ? 1 : -1;
+  }
+
+  bool is_reduce_over_last(int v, const char* body, int rank) const {
+    const Op* p = prod(v);
+    if (!p || p->name != "stablehlo.reduce" || p->operands.size() != 2) return false;
+    const auto dims = reduce_dims(*p);
+    return dims.size() == 1 && dims[0] == rank - 1 && reduce_body_op(*p) == body;
+  }
+
+  // softmax(S) along the last axis, as jax.nn.softmax lowers it:
+  //   M = reduce_max(S)            [optionally max(M, -inf) for `initial`]
+  //   E = exp(S - broadcast(M))
+  //   P = E / broadcast(reduce_sum(E))   [sum possibly on an f32 convert of E]
+  // returns S (the softmax input) and records the matched ops.
+  int MatchSoftmax(int P, std::set<int>& ops) const {
+    std::vector<int> path;
+    const Op* div = prod(P);
+    if (!div || div->name != "stablehlo.divide") return -1;
+    ops.insert(producer_[P]);
+    const int rank = m_.types[P].rank();
+    int E = div->operands[0];
+    int Z = div->operands[1];
+    // Z = broadcast(reshape?(convert?(reduce_sum(convert?(E)))))
+    int z = Z;
+    while (is(z, "stablehlo.broadcast_in_dim") || is(z, "stablehlo.reshape") || is(z, "stablehlo.convert")) {
+      ops.insert(producer_[z]);
+      z = prod(z)->operands[0];
+    }
+    if (!is_reduce_over_last(z, "stablehlo.add", rank)) return -1;
+    ops.insert(producer_[z]);
+    std::vector<int> p2;
+    int e_in_sum = through_converts(prod(z)->operands[0], &p2);
+    for (int o : p2) ops.insert(o);
+    int e_main = through_converts(E, &path);
+    for (int o : path) ops.insert(o);
+    if (e_in_sum != e_main) return -1;
+    const Op* ex = prod(e_main);
+    if (!ex || ex->name != "stablehlo.exponential") return -1;
+    ops.insert(producer_[e_main]);
+    const Op* sub = prod(ex->operands[0]);
+    if (!sub || sub->name != "stablehlo.subtract") return -1;
+    ops.insert(producer_[ex->operands[0]]);
+    const int S = sub->operands[0];
+    int m = sub->operands[1];
+    while (is(m, "stablehlo.broadcast_in_dim") || is(m, "stablehlo.reshape") || is(m, "stablehlo.convert") ||
+           is(m, "stablehlo.maximum")) {
+      ops.insert(producer_[m]);
+      const Op* q = prod(m);
+      if (q->name == "stablehlo.maximum") {
+        double c;
+        // max(M, -inf) (jnp.max `initial`): keep the non-constant side
+        if (scalar_of(q->operands[0], &c)) m = q->operands[1];
+        else if (scalar_of(q->operands[1], &c)) m = q->operands[0];
+        else return -1;
+        if (!(c < -1e30)) return -1;
+        continue;
+      }
+      m = q->operands[0];
+    }
+    if (!is_reduce_over_last(m, "stablehlo.maximum", rank)) return -1;
+    ops.insert(producer_[m]);
+    std::vector<int> p3;
+    if (through_converts(prod(m)->operands[0], &p3) != through_converts(S)) return -1;
+    for (int o : p3) ops.insert(o);
+    return S;
+  }
+
+  void TryMatchSdpa(int anchor) {
+    const Op& d2 = ops_[anchor];
+    const int P = d2.operands[0], V = d2.operands[1];
+    const TensorType& pt = m_.types[P];
+    const TensorType& vt = m_.types[V];
+    if (pt.rank() != 4 || vt.rank() != 4) return;
+    DotDims dd = dot_dims(d2);
+    if (dd.lb != std::vector<int64_t>{0, 1} || dd.rb != std::vector<int64_t>{0, 1} ||
+        dd.lc != std::vector<int64_t>{3} || dd.rc != std::vector<int64_t>{2})
+      return;
+    std::set<int> ops;
+    ops.insert(anchor);
+    std::vector<int> path;
+    const int Pin = through_converts(P, &path);
+    for (int o : path) ops.insert(o);
+    int S = MatchSoftmax(Pin, ops);
+    if (S < 0) return;
+    // mask: select(mask, scores, -inf)
+    int mask = -1;
+    int sc = S;
+    if (is(sc, "stablehlo.select")) {
+      const Op* sel = prod(sc);
+      double c;
+      if (!scalar_of(sel->operands[2], &c) || !(c < -1e30)) return;
+      mask = sel->operands[0];
+      ops.insert(producer_[sc]);
+      sc = sel->operands[1];
+    }
+    path.clear();
+    sc = through_converts(sc, &path);
+    for (int o : path) ops.insert(o);
+    // scale: multiply / divide by a splat constant (either side for multiply)
+    float scale = 1.f;
+    if (is(sc, "stablehlo.multiply") || is(sc, "stablehlo.divide")) {
+      const Op* s = prod(sc);
+      double c;
+      if (s->name == "stablehlo.multiply" && scalar_of(s->operands[1], &c)) {
+        scale = float(c);
+        ops.insert(producer_[sc]);
+        sc = s->operands[0];
+      } else if (s->name == "stablehlo.multiply" && scalar_of(s->operands[0], &c)) {
+        scale = float(c);
+        ops.insert(producer_[sc]);
+        sc = s->operands[1];
+      } else if (s->name == "stablehlo.divide" && scalar_of(s->operands[1], &c)) {
+        scale = float(1.0 / c);
+        ops.insert(producer_[sc]);
+        sc = s->operands[0];
+      }
+    }
+    path.clear();
+    sc = through_converts(sc, &path);
+    for (int o : path) ops.insert(o);
+    const Op* d1 = prod(sc);
+    if (!d1 || d1->name != "stablehlo.dot_general") return;
+    DotDims e = dot_dims(*d1);
+    if (e.lb != std::vector<int64_t>{0, 1} || e.rb != std::vector<int64_t>{0, 1} ||
+        e.lc != std::vector<int64_t>{3} || e.rc != std::vector<int64_t>{3})
+      return;
+    ops.insert(producer_[sc]);
+    const int Q = d1->operands[0], K = d1->operands[1];
+    const TensorType& qt = m_.types[Q];
+    const TensorType& kt = m_.types[K];
+    if (qt.dtype != DType::kBF16 || kt.dtype != DType::kBF16 || vt.dtype != DType::kBF16) return;
+    if (m_.types[d2.results[0]].dtype != DType::kBF16) return;
+    const int64_t D = qt.dims[3];
+    if ((D != 64 && D != 128) || vt.dims[3] != D) return;
+    bool causal = false;
+    if (mask >= 0) {
+      const int cls = ClassifyMask(mask, qt.dims[0], qt.dims[1], qt.dims[2], kt.dims[2]);
+      if (cls < 0) return;
+      causal = cls == 1;
+    }
+    // every intermediate result must stay inside the pattern
+    for (int o : ops)
+      for (int r : ops_[o].results)
+        if (o != anchor && !uses_within(r, ops)) return;
+    Fused f;
+    f.kind = Fused::kSdpa;
+    f.q = Q;
+    f.k = K;
+    f.v = V;
+    f.scale = scale;
+    f.causal = causal;
+    f.deps = {Q, K, V};
+    fused_[anchor] = f;
+    prog_->patterns.push_back(std::string("sdpa(") + (causal ? "causal" : "full") + ", scale=" +
+                              std::to_string(scale) + ")");
+  }
+
+  void TryMatchArgmax(int anchor) {
+    const Op& r = ops_[anchor];
+    const auto dims = reduce_dims(r);
+    if (dims.size() != 1) return;
+    // direction from the first compare in the body (reduce.mm:29-43)
+    int dir = 0;
+    if (!r.regions.empty())
+      for (const Op& b : r.regions[0]->blocks[0].ops)
+        if (b.name == "stablehlo.compare") {
+          std::string d;
+          if (const Attr* x = b.attr("comparison_direction")) d = x->s;
+          else if (const Attr* x = b.attr("enum0")) d = x->s;
+          dir = d == "GT" ? 1 : d == "LT" ? -1 : 0;
+          break;
+        }
+    if (dir == 0) return;
+    // second operand must be an iota along the reduced dimension
+    int ix = r.operands[1];
+    int dim_in_iota = int(dims[0]);
+    while (is(ix, "stablehlo.broadcast_in_dim")) {
+      const Op* b = prod(ix);
+      const auto bd = attr_ints(*b, {"dims", "broadcast_dimensions"});
+      auto it = std::find(bd.begin(), bd.end(), int64_t(dim_in_iota));
+      if (it == bd.end()) return;
+      dim_in_iota = int(it - bd.begin());
+      ix = b->operands[0];
+    }
+    if (!is(ix, "stablehlo.iota")) return;
+    const auto idim = attr_ints(*prod(ix), {"dim", "iota_dimension"});
+    if (idim.empty() || idim[0] != dim_in_iota) return;
+    const DType xt = m_.types[r.operands[0]].dtype;
+    if (xt != DType::kBF16 && xt != DType::kF32 && xt != DType::kF16) return;
+    const DType it_ = m_.types[r.results[1]].dtype;
+    if (it_ != DType::kI32 && it_ != DType::kI64) return;
+    Fused f;
+    f.kind = Fused::kArgmax;
+    f.x = r.operands[0];
+    f.is_min = dir < 0;
+    f.deps = {f.x};
+    fused_[anchor] = f;
+    prog_->patterns.push_back(dir > 0 ? "argmax" : "argmin");
+  }
+
+  // add(dot_general(a, b), broadcast_in_dim(bias, dims=[last])) [-> max(., 0)]
+  void TryMatchGemmEpilogue(int add_idx) {
+    const Op& add = ops_[add_idx];
+    for (int side = 0; side < 2; ++side) {
+      const int d = add.operands[side], bb = add.operands[1 - side];
+      const Op* dot = prod(d);
+      if (!dot || dot->name != "stablehlo.dot_general" || uses_[d] != 1 || fused_.count(producer_[d])) continue;
+      const TensorType& ot = m_.types[add.results[0]];
+      if (ot.rank() != 2) continue;
+      // bias: a chain of broadcast_in_dim / reshape from a 1-D [N] vector
+      // that places the vector on the last output dim
+      int b = bb;
+      std::vector<const Op*> chain;
+      while ((is(b, "stablehlo.broadcast_in_dim") || is(b, "stablehlo.reshape")) && m_.types[b].rank() >= 1 &&
+             !(m_.types[b].rank() == 1)) {
+        chain.push_back(prod(b));
+        b = prod(b)->operands[0];
+      }
+      bool ok = !chain.empty() && m_.types[b].rank() == 1 && m_.types[b].dims[0] == ot.dims[1];
+      int pos = 0;  // position of the vector's dim, innermost op outwards
+      for (auto it = chain.rbegin(); ok && it != chain.rend(); ++it) {
+        const Op* p = *it;
+        const auto& rd = m_.types[p->results[0]].dims;
+        if (p->name == "stablehlo.broadcast_in_dim") {
+          const auto dd = attr_ints(*p, {"dims", "broadcast_dimensions"});
+          ok = pos < int(dd.size());
+          if (ok) pos = int(dd[pos]);
+        } else {  // reshape that only adds / removes unit dims
+          int found = -1, nonunit = 0;
+          for (size_t k = 0; k < rd.size(); ++k)
+            if (rd[k] != 1) {
+              ++nonunit;
+              found = int(k);
+            }
+          ok = nonunit == 1 && rd[found] == ot.dims[1];
+          pos = found;
+        }
+      }
+      ok = ok && pos == ot.rank() - 1;
+      if (!ok || m_.types[b].dtype != ot.dtype) continue;
+      Fused f;
+      f.kind = Fused::kGemmEpi;
+      f.dot = producer_[d];
+      f.bias = b;
+      int anchor = add_idx;
+      // max(add, 0) -> relu
+      if (uses_[add.results[0]] == 1 && users_[add.results[0]].size() == 1) {
+        const int u = users_[add.results[0]][0];
+        const Op& mx = ops_[u];
+        if (mx.name == "stablehlo.maximum") {
+          const int other = mx.operands[0] == add.results[0] ? mx.operands[1] : mx.operands[0];
+          double c;
+          if (scalar_of(other, &c) && c == 0.0) {
+            f.relu = true;
+            anchor = u;
+          }
+        }
+      }
+      f.deps = {dot->operands[0], dot->operands[1], b};
+      fused_[anchor] = f;
+      absorbed_.insert(f.dot);
+      if (anchor != add_idx) absorbed_.insert(add_idx);
+      prog_->patterns.push_back(f.relu ? "gemm+bias+relu" : "gemm+bias");
+      return;
+    }
+  }
+
+  // gelu_tanh(X) = X * (0.5 * (1 + tanh(c * (X + 0.044715 * X^3)))) as
+  // jax.nn.gelu(approximate=True) lowers it (X^3 = X * (X * X)); either order
+  // of every commutative op.  X is f32 (optionally convert(bf16)); a
+  // convert-to-bf16 consumer is folded in so the kernel rounds once.
+  void TryMatchGelu(int mul_idx) {
+    const int M = ops_[mul_idx].results[0];
+    if (m_.types[M].dtype != DType::kF32) return;
+    int X = -1;
+    std::vector<int> interior;
+    const bool ok = Comm(M, "stablehlo.multiply", [&](int x, int h) {
+      interior.clear();
+      return Comm(h, "stablehlo.multiply", [&](int half, int t1) {
+        if (!IsConstNear(half, 0.5)) return false;
+        return Comm(t1, "stablehlo.add", [&](int one, int t) {
+          if (!IsConstNear(one, 1.0) || !is(t, "stablehlo.tanh")) return false;
+          const int u = prod(t)->operands[0];
+          return Comm(u, "stablehlo.multiply", [&](int c, int v) {
+            if (!IsConstNear(c, 0.7978845608028654, 1e-6)) return false;
+            return Comm(v, "stablehlo.add", [&](int x2, int w) {
+              if (x2 != x) return false;
+              return Comm(w, "stablehlo.multiply", [&](int c2, int c3) {
+                if (!IsConstNear(c2, 0.044715, 1e-6)) return false;
+                int sq = -1;
+                const bool cube = Comm(c3, "stablehlo.multiply", [&](int a, int b) {
+                  if (a != x) return false;
+                  return Comm(b, "stablehlo.multiply", [&](int p, int q) {
+                    if (p != x || q != x) return false;
+                    sq = b;
+                    return true;
+                  });
+                });
+                if (!cube) return false;
+                X = x;
+                interior = {h, t1, t, u, v, w, c3, sq};
+                return true;
+              });
+            });
+          });
+        });
+      });
+    });
+    if (!ok) return;
+    std::set<int> ops{mul_idx};
+    for (int v : interior) ops.insert(producer_[v]);
+    int anchor = mul_idx;
+    int out_v = M;
+    if (users_[M].size() == 1 && uses_[M] == 1 && ops_[users_[M][0]].name == "stablehlo.convert" &&
+        m_.types[ops_[users_[M][0]].results[0]].dtype == DType::kBF16) {
+      anchor = users_[M][0];
+      out_v = ops_[anchor].results[0];
+      ops.insert(anchor);
+    }
+    for (int v : interior)
+      if (!uses_within(v, ops)) return;
+    if (anchor != mul_idx && !uses_within(M, ops)) return;
+    int src = X;
+    if (is(X, "stablehlo.convert") && m_.types[prod(X)->operands[0]].dtype == DType::kBF16) src = prod(X)->operands[0];
+    const DType in_t = m_.types[src].dtype, out_t = m_.types[out_v].dtype;
+    if (in_t != out_t) return;  // kernel io is one dtype (bf16 -> bf16 or f32 -> f32)
+    Fused f;
+    f.kind = Fused::kGelu;
+    f.x = src;
+    f.out_dtype = out_t;
+    f.deps = {src};
+    fused_[anchor] = f;
+    for (int o : ops)
+      if (o != anchor) absorbed_.insert(o);
+    prog_->patterns.push_back(std::string("gelu_tanh(") + DTypeName(out_t) + ")");
+  }
+
+  // LayerNorm over the last dim, as the jnp two-pass formulation lowers:
+  //   XF = convert?(x); MEAN = sum(XF)/n; XC = XF - bcast(MEAN);
+  //   VAR = sum(XC*XC)/n; N = XC * bcast(rsqrt(VAR + eps));
+  //   Y = N [* bcast(gamma)] [+ bcast(beta)]  [-> convert to the storage type]
+  void TryMatchLayerNorm(int idx) {
+    int Y = ops_[idx].results[0];
+    int anchor = idx;
+    int out_v = Y;
+    if (ops_[idx].name == "stablehlo.convert") {  // output rounding folded in
+      Y = ops_[idx].operands[0];
+      if (users_[Y].size() != 1 || uses_[Y] != 1) return;
+    }
+    const TensorType& yt = m_.types[Y];
+    if (yt.dtype != DType::kF32 || yt.rank() < 1) return;
+    const int64_t n = yt.dims.back();
+    std::set<int> ops{idx};
+    int gamma = -1, beta = -1, N = Y;
+    // optional + beta
+    {
+      int rest = -1, bvec = -1;
+      std::set<int> bops;
+      if (Comm(Y, "stablehlo.add", [&](int a, int b) {
+            bops.clear();
+            int vec = VectorOnLastDim(b, n, &bops);
+            if (vec < 0) return false;
+            rest = a;
+            bvec = vec;
+            return true;
+          })) {
+        beta = bvec;
+        N = rest;
+        ops.insert(producer_[Y]);
+        ops.insert(bops.begin(), bops.end());
+      }
+    }
+    // optional * gamma
+    {
+      int rest = -1, gvec = -1;
+      std::set<int> gops;
+      int N2 = N;
+      if (Comm(N2, "stablehlo.multiply", [&](int a, int b) {
+            gops.clear();
+            int vec = VectorOnLastDim(b, n, &gops);
+            if (vec < 0) return false;
+            // the other side must itself be XC * bcast(rsqrt(...))
+            if (!is(a, "stablehlo.multiply")) return false;
+            rest = a;
+            gvec = vec;
+            return true;
+          })) {
+        gamma = gvec;
+        ops.insert(producer_[N2]);
+        ops.insert(gops.begin(), gops.end());
+        N = rest;
+      }
+    }
+    // N = XC * bcast(rsqrt(VAR + eps))
+    int XC = -1, XF = -1;
+    float eps = 0;
+    const bool core = Comm(N, "stablehlo.multiply", [&](int xc, int r) {
+      std::set<int> cops;
+      int rs = r;
+      while (is(rs, "stablehlo.broadcast_in_dim") || is(rs, "stablehlo.reshape")) {
+        cops.insert(producer_[rs]);
+        rs = prod(rs)->operands[0];
+      }
+      if (!is(rs, "stablehlo.rsqrt")) return false;
+      cops.insert(producer_[rs]);
+      int var = -1;
+      double e = 0;
+      if (!Comm(prod(rs)->operands[0], "stablehlo.add", [&](int a, int c) {
+            if (!scalar_of(c, &e)) return false;
+            var = a;
+            return true;
+          }))
+        return false;
+      cops.insert(producer_[prod(rs)->operands[0]]);
+      // XC = XF - bcast(MEAN(XF))
+      int xf = -1;
+      if (!NonComm(xc, "stablehlo.subtract", [&](int a, int m) {
+            std::set<int> mops;
+            int in = RowMeanOf(m, n, mops);
+            if (in < 0 || in != a) return false;
+            xf = a;
+            cops.insert(mops.begin(), mops.end());
+            return true;
+          }))
+        return false;
+      cops.insert(producer_[xc]);
+      // VAR = mean(XC * XC) over the same rows
+      std::set<int> vops;
+      int sq = RowMeanOf(var, n, vops);
+      if (sq < 0 || !is(sq, "stablehlo.multiply")) return false;
+      const Op* sqo = prod(sq);
+      if (sqo->operands[0] != xc || sqo->operands[1] != xc) return false;
+      vops.insert(producer_[sq]);
+      cops.insert(vops.begin(), vops.end());
+      ops.insert(producer_[N]);
+      ops.insert(cops.begin(), cops.end());
+      XC = xc;
+      XF = xf;
+      eps = float(e);
+      return true;
+    });
+    if (!core) return;
+    // every value computed inside the pattern stays inside it
+    for (int o : ops)
+      for (int r : ops_[o].results)
+        if (o != anchor && !uses_within(r, ops)) return;
+    int src = XF;
+    if (is(XF, "stablehlo.convert")) src = prod(XF)->operands[0];
+    const DType io = m_.types[out_v].dtype;
+    if (m_.types[src].dtype != io || (io != DType::kBF16 && io != DType::kF32)) return;
+    if ((gamma >= 0 && m_.types[gamma].dtype != io) || (beta >= 0 && m_.types[beta].dtype != io)) return;
+    (void)XC;
+    Fused f;
+    f.kind = Fused::kLayerNorm;
+    f.x = src;
+    f.gamma = gamma;
+    f.beta = beta;
+    f.eps = eps;
+    f.out_dtype = io;
+    f.deps = {src};
+    if (gamma >= 0) f.deps.push_back(gamma);
+    if (beta >= 0) f.deps.push_back(beta);
+    fused_[anchor] = f;
+    for (int o : ops)
+      if (o != anchor) absorbed_.insert(o);
+    prog_->patterns.push_back(std::string("layernorm(") + DTypeName(io) + ", eps=" + std::to_string(eps) + ")");
+  }
+
+  // -------------------------------------------------------------- liveness / DCE
+  void Liveness() {
+    live_.assign(ops_.size(), false);
+    std::vector<int> stack(outputs_.begin(), outputs_.end());
+    std::vector<bool> seen(m_.types.size(), false);
+    while (!stack.empty()) {
+      int v = stack.back();
+      stack.pop_back();
+      if (v < 0 || seen[v]) continue;
+      seen[v] = true;
+      int p = producer_[v];
+      if (p < 0) continue;
+      // a value computed inside a fused pattern is produced by the anchor
+      if (!live_[p]) live_[p] = true;
+      auto it = fused_.find(p);
+      const std::vector<int>& deps = it != fused_.end() ? it->second.deps : ops_[p].operands;
+      for (int d : deps) stack.push_back(d);
+    }
+    // absorbed ops (gemm epilogue internals) never run on their own
+    for (int a : absorbed_) live_[a] = false;
+  }
+
+  // -------------------------------------------------------------- arena
+  BufRef NewTemp(size_t bytes) {
+    BufRef r;
+    r.space = Space::kArena;
+    r.index = int(temps_.size());
+    r.offset = 0;
+    temps_.push_back({(bytes + 255) & ~size_t(255), -1, -1});
+    return r;
+  }
+  // final placement of the virtual arena buffers: linear scan over steps,
+  // first fit in a free list, so buffers with disjoint lifetimes share bytes
+  void PackArena() {
+    for (size_t s = 0; s < prog_->steps.size(); ++s)
+      for (const BufRef& b : prog_->steps[s].bufs)
+        if (b.space == Space::kArena) {
+          auto& t = temps_[b.index];
+          if (t.first < 0) t.first = int(s);
+          t.last = int(s);
+        }
+    struct Block {
+      size_t off, size;
+    };
+    std::vector<Block> free_list;
+    size_t top = 0;
+    std::vector<size_t> base(temps_.size(), 0);
+    std::vector<std::vector<int>> ends(prog_->steps.size() + 1);
+    std::vector<std::vector<int>> starts(prog_->steps.size() + 1);
+    for (size_t i = 0; i < temps_.size(); ++i)
+      if (temps_[i].first >= 0) {
+        starts[temps_[i].first].push_back(int(i));
+        ends[temps_[i].last].push_back(int(i));
+      }
+    for (size_t s = 0; s < prog_->steps.size(); ++s) {
+      for (int i : starts[s]) {
+        const size_t need = temps_[i].size;
+        bool placed = false;
+        for (size_t k = 0; k < free_list.size(); ++k)
+          if (free_list[k].size >= need) {
+            base[i] = free_list[k].off;
+            free_list[k].off += need;
+            free_list[k].size -= need;
+            if (free_list[k].size == 0) free_list.erase(free_list.begin() + long(k));
+            placed = true;
+            break;
+          }
+        if (!placed) {
+          base[i] = top;
+          top += need;
+        }
+      }
+      for (int i : ends[s]) free_list.push_back({base[i], temps_[i].size});
+    }
+    prog_->arena_bytes = top;
+    for (auto& st : prog_->steps)
+      for (BufRef& b : st.bufs)
+        if (b.space == Space::kArena) b.offset += int64_t(base[b.index]);
+  }
+
+  // -------------------------------------------------------------- materialization
+  // destination for the value `v` when it is materialized by a step
+  BufRef DestFor(int v) {
+    for (size_t k = 0; k < outputs_.size(); ++k)
+      if (outputs_[k] == v && !out_written_[k]) {
+        out_written_[k] = true;
+        return BufRef{Space::kOutput, int(k), 0};
+      }
+    return NewTemp(m_.types[v].bytes());
+  }
+  void SetDenseView(int v, BufRef where) {
+    ValState& s = state_[v];
+    s.kind = ValState::kView;
+    s.view.buf = where;
+    s.view.dtype = m_.types[v].dtype;
+    s.view.dims = m_.types[v].dims;
+    s.view.strides = DenseStrides(s.view.dims);
+    s.view.offset = 0;
+  }
+
+  // Guarantee that `v` is available as a view; emits steps as needed.
+  const View& NeedView(int v) {
+    ValState& s = state_[v];
+    if (s.kind == ValState::kView) return s.view;
+    if (s.kind == ValState::kUnset)
+      throw std::string("jam: value %" + std::to_string(v) + " used before it was lowered");
+    const TensorType& t = m_.types[v];
+    BufRef dst = DestFor(v);
+    if (s.kind == ValState::kScalar) {
+      Step st;
+      st.kind = StepKind::kFill;
+      st.bufs = {dst};
+      uint64_t pattern = 0;
+      uint8_t bytes[8] = {0};
+      EncodeElement(s.fval, s.ival, t.dtype, bytes);
+      memcpy(&pattern, bytes, size_t(DTypeBytes(t.dtype)));
+      st.i = {DTypeBytes(t.dtype), t.numel(), int64_t(pattern)};
+      st.note = "splat";
+      Emit(st);
+      SetDenseView(v, dst);
+      return state_[v].view;
+    }
+    EmitEw(v, dst);
+    SetDenseView(v, dst);
+    return state_[v].view;
+  }
+  // a dense copy of a view (for consumers that need row-major memory)
+  View Densify(const View& src, int64_t elem_bytes_hint = 0) {
+    if (src.dense()) return src;
+    View out;
+    out.dtype = src.dtype;
+    out.dims = src.dims;
+    out.strides = DenseStrides(src.dims);
+    out.buf = NewTemp(size_t(src.numel()) * DTypeBytes(src.dtype));
+    EmitCopy(src, out.buf);
+    return out;
+  }
+  void EmitCopy(const View& src, BufRef dst) {
+    if (src.dense()) {
+      Step st;
+      st.kind = StepKind::kCopy;
+      st.bufs = {src.at(), dst};
+      st.i = {int64_t(src.numel()) * DTypeBytes(src.dtype)};
+      Emit(st);
+      return;
+    }
+    if (src.rank() > 6) throw std::string("jam: rank > 6 layout copy is not supported");
+    Step st;
+    st.kind = StepKind::kCopyStrided;
+    st.bufs = {src.at(), dst};
+    st.i = {DTypeBytes(src.dtype), src.rank()};
+    for (int64_t d : src.dims) st.i.push_back(d);
+    st.strides = src.strides;
+    Emit(st);
+  }
+  void Emit(Step st) { prog_->steps.push_back(std::move(st)); }
+
+  // ---- elementwise expression compiler
+  static bool IsElementwise(const std::string& n) {
+    static const std::set<std::string> s = {
+        "stablehlo.add", "stablehlo.subtract", "stablehlo.multiply", "stablehlo.divide",
+        "stablehlo.maximum", "stablehlo.minimum", "stablehlo.power", "stablehlo.negate",
+        "stablehlo.exponential", "stablehlo.log", "stablehlo.tanh", "stablehlo.sqrt",
+        "stablehlo.rsqrt", "stablehlo.abs", "stablehlo.logistic", "stablehlo.compare",
+        "stablehlo.select", "stablehlo.clamp", "stablehlo.convert", "stablehlo.floor",
+        "stablehlo.ceil", "stablehlo.sign", "stablehlo.and", "stablehlo.or", "stablehlo.not",
+        "stablehlo.xor", "stablehlo.round_nearest_even"};
+    return s.count(n) > 0;
+  }
+
+  struct EwBuild {
+    std::vector<int> leaves;              // value ids loaded as inputs
+    std::vector<std::array<int32_t, 4>> prog;
+    std::vector<uint32_t> consts;
+    int next_reg = 0;
+    std::vector<int> free_regs;
+    std::unordered_map<int, int> memo;    // value id -> register holding it
+    std::unordered_map<int, int> refs;    // remaining in-expression references
+  };
+
+  int AllocReg(EwBuild& b) {
+    if (!b.free_regs.empty()) {
+      int r = b.free_regs.back();
+      b.free_regs.pop_back();
+      return r;
+    }
+    if (b.next_reg >= 32) throw 1;  // caller splits the expression
+    return b.next_reg++;
+  }
+  void FreeReg(EwBuild& b, int r) {
+    if (r >= int(b.leaves.size())) b.free_regs.push_back(r);
+  }
+  int ConstReg(EwBuild& b, uint32_t bits) {
+    int idx = -1;
+    for (size_t k = 0; k < b.consts.size(); ++k)
+      if (b.consts[k] == bits) idx = int(k);
+    if (idx < 0) {
+      if (b.consts.size() >= 64) throw 1;
+      b.consts.push_back(bits);
+      idx = int(b.consts.size()) - 1;
+    }
+    int r = AllocReg(b);
+    b.prog.push_back({MK_EW_CONST, r, idx, 0});
+    return r;
+  }
+  void Ins(EwBuild& b, int op, int dst, int a, int bb = 0) {
+    if (b.prog.size() >= 64) throw 1;
+    b.prog.push_back({op, dst, a, bb});
+  }
+
+  // An unmaterialized elementwise value is part of the expression being
+  // built (evaluated once per element, shared through a register); anything
+  // materialized is a leaf input.
+  bool InExpr(int v) const { return state_[v].kind == ValState::kEw; }
+
+  // First pass over the expression DAG: leaves and reference counts.
+  void CollectLeaves(int v, std::vector<int>& leaves, std::unordered_map<int, int>& refs,
+                     std::set<int>& seen) {
+    if (!seen.insert(v).second) return;
+    const ValState& s = state_[v];
+    if (s.kind == ValState::kScalar) return;
+    if (InExpr(v)) {
+      for (int o : ops_[s.op].operands) {
+        ++refs[o];
+        CollectLeaves(o, leaves, refs, seen);
+      }
+      return;
+    }
+    leaves.push_back(v);
+  }
+
+  void Release(EwBuild& b, int v) {
+    auto it = b.refs.find(v);
+    if (it == b.refs.end()) return;
+    if (--it->second == 0) {
+      auto m = b.memo.find(v);
+      if (m != b.memo.end()) FreeReg(b, m->second);
+    }
+  }
+
+  // Second pass: emit code for v, returns its register.
+  int Gen(EwBuild& b, int v, bool root) {
+    auto memo = b.memo.find(v);
+    if (memo != b.memo.end()) return memo->second;
+    const ValState& s = state_[v];
+    const DType t = m_.types[v].dtype;
+    if (s.kind == ValState::kScalar) {
+      int r = ConstReg(b, RegisterBits(s.fval, s.ival, t));
+      b.memo[v] = r;
+      return r;
+    }
+    if (!InExpr(v)) {
+      auto it = std::find(b.leaves.begin(), b.leaves.end(), v);
+      int r = int(it - b.leaves.begin());
+      b.memo[v] = r;
+      return r;
+    }
+    const Op& op = ops_[s.op];
+    const std::string& n = op.name;
+    std::vector<int> regs;
+    for (int o : op.operands) regs.push_back(Gen(b, o, false));
+    const DType in_t = m_.types[op.operands[0]].dtype;
+    const bool fl = IsFloat(in_t);
+    const bool in_int = !fl && in_t != DType::kPred;
+    int dst = -1;
+    auto unary = [&](int opc) {
+      dst = AllocReg(b);
+      Ins(b, opc, dst, regs[0]);
+    };
+    auto binary = [&](int opc) {
+      dst = AllocReg(b);
+      Ins(b, opc, dst, regs[0], regs[1]);
+    };
+    if (n == "stablehlo.add") binary(fl ? MK_EW_ADD : MK_EW_ADD_S32);
+    else if (n == "stablehlo.subtract") binary(fl ? MK_EW_SUB : MK_EW_SUB_S32);
+    else if (n == "stablehlo.multiply") binary(fl ? MK_EW_MUL : MK_EW_MUL_S32);
+    else if (n == "stablehlo.divide") {
+      if (!fl) throw std::string("jam: integer divide is not supported");
+      binary(MK_EW_DIV);
+    } else if (n == "stablehlo.maximum") binary(fl ? MK_EW_MAX : MK_EW_MAX_S32);
+    else if (n == "stablehlo.minimum") binary(fl ? MK_EW_MIN : MK_EW_MIN_S32);
+    else if (n == "stablehlo.power") binary(MK_EW_POW);
+    else if (n == "stablehlo.negate") unary(fl ? MK_EW_NEG : MK_EW_NEG_S32);
+    else if (n == "stablehlo.exponential") unary(MK_EW_EXP);
+    else if (n == "stablehlo.log") unary(MK_EW_LOG);
+    else if (n == "stablehlo.tanh") unary(MK_EW_TANH);
+    else if (n == "stablehlo.sqrt") unary(MK_EW_SQRT);
+    else if (n == "stablehlo.rsqrt") unary(MK_EW_RSQRT);
+    else if (n == "stablehlo.abs") unary(MK_EW_ABS);
+    else if (n == "stablehlo.logistic") unary(MK_EW_LOGISTIC);
+    else if (n == "stablehlo.floor") unary(MK_EW_FLOOR);
+    else if (n == "stablehlo.ceil") unary(MK_EW_CEIL);
+    else if (n == "stablehlo.sign") unary(MK_EW_SIGN);
+    else if (n == "stablehlo.round_nearest_even") throw std::string("jam: round_nearest_even is not supported");
+    else if (n == "stablehlo.not") {
+      if (in_t == DType::kPred) unary(MK_EW_NOT);
+      else {
+        int m1 = ConstReg(b, RegisterBits(-1, -1, DType::kI32));
+        dst = AllocReg(b);
+        Ins(b, MK_EW_XOR_B32, dst, regs[0], m1);
+        FreeReg(b, m1);
+      }
+    } else if (n == "stablehlo.and" || n == "stablehlo.or" || n == "stablehlo.xor") {
+      if (in_t == DType::kPred)
+        binary(n == "stablehlo.and" ? MK_EW_AND : n == "stablehlo.or" ? MK_EW_OR : MK_EW_CMP_NE);
+      else
+        binary(n == "stablehlo.and" ? MK_EW_AND_B32 : n == "stablehlo.or" ? MK_EW_OR_B32 : MK_EW_XOR_B32);
+    } else if (n == "stablehlo.compare") {
+      std::string dir;
+      if (const Attr* x = op.attr("comparison_direction")) dir = x->s;
+      else if (const Attr* x = op.attr("enum0")) dir = x->s;
+      int opc;
+      if (fl || in_t == DType::kPred) {
+        opc = dir == "EQ" ? MK_EW_CMP_EQ : dir == "NE" ? MK_EW_CMP_NE : dir == "LT" ? MK_EW_CMP_LT
+            : dir == "LE" ? MK_EW_CMP_LE : dir == "GT" ? MK_EW_CMP_GT : MK_EW_CMP_GE;
+      } else {
+        if (IsUnsigned(in_t)) throw std::string("jam: unsigned compare is not supported");
+        opc = dir == "EQ" ? MK_EW_CMP_EQ_S32 : dir == "NE" ? MK_EW_CMP_NE_S32 : dir == "LT" ? MK_EW_CMP_LT_S32
+            : dir == "LE" ? MK_EW_CMP_LE_S32 : dir == "GT" ? MK_EW_CMP_GT_S32 : MK_EW_CMP_GE_S32;
+      }
+      binary(opc);
+    } else if (n == "stablehlo.select") {
+      dst = AllocReg(b);
+      Ins(b, MK_EW_SELECT, dst, regs[0], regs[1] | (regs[2] << 16));
+    } else if (n == "stablehlo.clamp") {
+      // clamp(min, x, max)
+      const DType xt = m_.types[op.operands[1]].dtype;
+      dst = AllocReg(b);
+      if (IsFloat(xt)) {
+        Ins(b, MK_EW_CLAMP, dst, regs[1], regs[0] | (regs[2] << 16));
+      } else {
+        Ins(b, MK_EW_MAX_S32, dst, regs[1], regs[0]);
+        Ins(b, MK_EW_MIN_S32, dst, dst, regs[2]);
+      }
+    } else if (n == "stablehlo.convert") {
+      const DType ot = t;
+      dst = AllocReg(b);
+      if (IsFloat(in_t) && IsFloat(ot)) Ins(b, MK_EW_MOV, dst, regs[0]);
+      else if (in_int && IsFloat(ot)) Ins(b, IsUnsigned(in_t) ? MK_EW_U32_TO_F32 : MK_EW_S32_TO_F32, dst, regs[0]);
+      else if (in_t == DType::kPred && IsFloat(ot)) Ins(b, MK_EW_MOV, dst, regs[0]);
+      else if (IsFloat(in_t) && ot == DType::kPred) {
+        int z = ConstReg(b, 0);
+        Ins(b, MK_EW_CMP_NE, dst, regs[0], z);
+        FreeReg(b, z);
+      } else if (IsFloat(in_t)) Ins(b, MK_EW_F32_TO_S32, dst, regs[0]);
+      else if (in_t == DType::kPred) Ins(b, MK_EW_PRED_TO_S32, dst, regs[0]);
+      else if (ot == DType::kPred) Ins(b, MK_EW_S32_TO_PRED, dst, regs[0]);
+      else Ins(b, MK_EW_MOV, dst, regs[0]);
+    } else {
+      throw std::string("jam: no elementwise lowering for " + n);
+    }
+    // operands whose last in-expression reference this was give their register back
+    for (int o : op.operands) Release(b, o);
+    // per-op rounding: the StableHLO result type of an interior op is what
+    // XLA materialises
+    if (!root && (t == DType::kBF16 || t == DType::kF16))
+      Ins(b, t == DType::kBF16 ? MK_EW_ROUND_BF16 : MK_EW_ROUND_F16, dst, dst);
+    b.memo[v] = dst;
+    return dst;
+  }
+
+  void EmitEw(int v, BufRef dst) {
+    for (int attempt = 0; attempt < 64; ++attempt) {
+      std::vector<int> leaves;
+      std::unordered_map<int, int> refs;
+      std::set<int> seen;
+      CollectLeaves(v, leaves, refs, seen);
+      if (leaves.size() > 8) {
+        SplitLargestChild(v);
+        continue;
+      }
+      EwBuild b;
+      b.leaves = leaves;
+      b.refs = refs;
+      b.next_reg = int(leaves.size());
+      int out_reg;
+      try {
+        out_reg = Gen(b, v, true);
+      } catch (int) {
+        SplitLargestChild(v);
+        continue;
+      }
+      const TensorType& t = m_.types[v];
+      if (t.rank() > 6) throw std::string("jam: rank > 6 elementwise is not supported");
+      Step st;
+      st.kind = StepKind::kEw;
+      for (int l : leaves) {
+        const View& lv = NeedView(l);
+        if (lv.rank() != t.rank()) throw std::string("jam: elementwise operand rank mismatch");
+        st.bufs.push_back(lv.at());
+        st.types.push_back(int32_t(lv.dtype));
+        for (int d = 0; d < 6; ++d) st.strides.push_back(d < lv.rank() ? lv.strides[d] : 0);
+      }
+      st.bufs.push_back(dst);
+      st.i = {t.rank()};
+      for (int d = 0; d < 6; ++d) st.i.push_back(d < t.rank() ? t.dims[d] : 1);
+      st.i.push_back(int64_t(leaves.size()));
+      st.i.push_back(out_reg);
+      st.i.push_back(int64_t(t.dtype));
+      for (auto& ins : b.prog)
+        for (int k = 0; k < 4; ++k) st.prog.push_back(ins[k]);
+      for (uint32_t c : b.consts) {
+        float f;
+        memcpy(&f, &c, 4);
+        st.f.push_back(f);
+      }
+      st.note = ops_[state_[v].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
+                std::to_string(leaves.size()) + " inputs)";
+      Emit(st);
+      return;
+    }
+    throw std::string("jam: could not split an elementwise expression");
+  }
+
+  // materialize the biggest in-expression child of v so the expression shrinks
+  void SplitLargestChild(int v) {
+    std::function<int(int, std::set<int>&)> size = [&](int w, std::set<int>& seen) -> int {
+      if (!InExpr(w) || !seen.insert(w).second) return 0;
+      int s = 1;
+      for (int o : ops_[state_[w].op].operands) s += size(o, seen);
+      return s;
+    };
+    int best = -1, bs = 0;
+    for (int o : ops_[state_[v].op].operands) {
+      std::set<int> seen;
+      int s = size(o, seen);
+      if (s > bs) {
+        bs = s;
+        best = o;
+      }
+    }
+    if (best < 0) throw std::string("jam: elementwise expression has more than 8 distinct inputs");
+    BufRef d = NewTemp(m_.types[best].bytes());
+    EmitEw(best, d);
+    SetDenseView(best, d);
+  }
+
+  // -------------------------------------------------------------- the walk
+  void Walk() {
+    out_written_.assign(outputs_.size(), false);
+    for (size_t i = 0; i < ops_.size(); ++i) {
+      if (!live_[i]) continue;
+      auto f = fused_.find(int(i));
+      if (f != fused_.end()) {
+        EmitFused(int(i), f->second);
+        continue;
+      }
+      LowerOp(int(i));
+    }
+    // program outputs
+    for (size_t k = 0; k < outputs_.size(); ++k) {
+      if (out_written_[k] && state_[outputs_[k]].kind == ValState::kView &&
+          state_[outputs_[k]].view.buf.space == Space::kOutput && state_[outputs_[k]].view.buf.index == int(k))
+        continue;
+      const int v = outputs_[k];
+      if (state_[v].kind != ValState::kView) {
+        // materialize straight into this output
+        BufRef dst{Space::kOutput, int(k), 0};
+        out_written_[k] = true;
+        if (state_[v].kind == ValState::kEw) {
+          EmitEw(v, dst);
+        } else {
+          const TensorType& t = m_.types[v];
+          Step st;
+          st.kind = StepKind::kFill;
+          st.bufs = {dst};
+          uint64_t pattern = 0;
+          uint8_t bytes[8] = {0};
+          EncodeElement(state_[v].fval, state_[v].ival, t.dtype, bytes);
+          memcpy(&pattern, bytes, size_t(DTypeBytes(t.dtype)));
+          st.i = {DTypeBytes(t.dtype), t.numel(), int64_t(pattern)};
+          st.note = "splat output";
+          Emit(st);
+        }
+        SetDenseView(v, dst);
+        continue;
+      }
+      EmitCopy(state_[v].view, BufRef{Space::kOutput, int(k), 0});
+      out_written_[k] = true;
+    }
+  }
+
+  void LowerOp(int idx) {
+    const Op& op = ops_[idx];
+    const std::string& n = op.name;
+    auto res = [&](int k = 0) { return op.results.at(k); };
+    if (n == "stablehlo.constant") {
+      Attr a = *op.attr("value");
+      const TensorType& t = m_.types[res()];
+      std::string err;
+      if (!ParseDense(a, t, err)) throw err;
+      ValState& s = state_[res()];
+      if (a.splat || t.numel() == 1) {
+        s.kind = ValState::kScalar;
+        s.fval = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
+        s.ival = a.ivals.empty() ? int64_t(a.fvals[0]) : a.ivals[0];
+        return;
+      }
+      ConstBlob blob;
+      blob.type = t;
+      blob.bytes.resize(t.bytes());
+      const int w = DTypeBytes(t.dtype);
+      for (int64_t e = 0; e < t.numel(); ++e)
+        EncodeElement(a.fvals[size_t(e)], a.ivals[size_t(e)], t.dtype, &blob.bytes[size_t(e) * w]);
+      prog_->consts.push_back(std::move(blob));
+      s.kind = ValState::kView;
+      s.view.buf = BufRef{Space::kConst, int(prog_->consts.size()) - 1, 0};
+      s.view.dtype = t.dtype;
+      s.view.dims = t.dims;
+      s.view.strides = DenseStrides(t.dims);
+      return;
+    }
+    if (n == "stablehlo.broadcast_in_dim" || n == "stablehlo.broadcast") {
+      const int src = op.operands[0];
+      const TensorType& t = m_.types[res()];
+      if (state_[src].kind == ValState::kScalar) {
+        state_[res()] = state_[src];
+        return;
+      }
+      const View& sv = NeedView(src);
+      std::vector<int64_t> dims;
+      if (n == "stablehlo.broadcast") {  // legacy: prepend broadcast_sizes
+        const int lead = t.rank() - sv.rank();
+        for (int k = 0; k < sv.rank(); ++k) dims.push_back(lead + k);
+      } else {
+        dims = attr_ints(op, {"dims", "broadcast_dimensions"});
+      }
+      View v;
+      v.buf = sv.buf;
+      v.offset = sv.offset;
+      v.dtype = sv.dtype;
+      v.dims = t.dims;
+      v.strides.assign(t.rank(), 0);
+      for (size_t k = 0; k < dims.size(); ++k)
+        v.strides[dims[k]] = sv.dims[k] == 1 ? 0 : sv.strides[k];
+      SetView(res(), v);
+      return;
+    }
+    if (n == "stablehlo.reshape") {
+      const int src = op.operands[0];
+      if (state_[src].kind == ValState::kScalar) {
+        state_[res()] = state_[src];
+        return;
+      }
+      View sv = NeedView(src);
+      if (!sv.dense()) sv = Densify(sv);
+      View v = sv;
+      v.dims = m_.types[res()].dims;
+      v.strides = DenseStrides(v.dims);
+      SetView(res(), v);
+      return;
+    }
+    if (n == "stablehlo.transpose") {
+      const int src = op.operands[0];
+      if (state_[src].kind == ValState::kScalar) {
+        state_[res()] = state_[src];
+        return;
+      }
+      const View& sv = NeedView(src);
+      const auto perm = attr_ints(op, {"dims", "permutation"});
+      View v = sv;
+      for (size_t k = 0; k < perm.size(); ++k) {
+        v.dims[k] = sv.dims[perm[k]];
+        v.strides[k] = sv.strides[perm[k]];
+      }
+      SetView(res(), v);
+      return;
+    }
+    if (n == "stablehlo.slice") {
+      const View& sv = NeedView(op.operands[0]);
+      const auto st = attr_ints(op, {"start_indices"});
+      const auto sd = attr_ints(op, {"strides"});
+      View v = sv;
+      v.dims = m_.types[res()].dims;
+      for (int k = 0; k < sv.rank(); ++k) {
+        v.offset += st.at(k) * sv.strides[k];
+        v.strides[k] = sv.strides[k] * (sd.empty() ? 1 : sd[k]);
+      }
+      SetView(res(), v);
+      return;
+    }
+    if (IsElementwise(n)) {
+      ValState& s = state_[res()];
+      if (!opts_.fuse_elementwise) {
+        s.kind = ValState::kEw;
+        s.op = idx;
+        BufRef d = DestFor(res());
+        EmitEw(res(), d);
+        SetDenseView(res(), d);
+        return;
+      }
+      s.kind = ValState::kEw;
+      s.op = idx;  // evaluated inside the consumers' fused programs
+      return;
+    }
+    if (n == "stablehlo.iota") {
+      const TensorType& t = m_.types[res()];
+      const auto dd = attr_ints(op, {"dim", "iota_dimension"});
+      BufRef d = DestFor(res());
+      Step st;
+      st.kind = StepKind::kIota;
+      st.bufs = {d};
+      st.i = {int64_t(t.dtype), t.rank(), dd.empty() ? 0 : dd[0]};
+      for (int64_t x : t.dims) st.i.push_back(x);
+      Emit(st);
+      SetDenseView(res(), d);
+      return;
+    }
+    if (n == "stablehlo.reduce") {
+      LowerReduce(idx);
+      return;
+    }
+    if (n == "stablehlo.dot_general" || n == "stablehlo.dot") {
+      LowerDot(idx, nullptr);
+      return;
+    }
+    if (n == "stablehlo.gather") {
+      LowerGather(idx);
+      return;
+    }
+    if (n == "stablehlo.scatter") {
+      LowerScatter(idx);
+      return;
+    }
+    if (n == "stablehlo.concatenate") {
+      LowerConcat(idx);
+      return;
+    }
+    throw std::string("jam: unhandled op '" + n + "'");  // lower.mm:308-310
+  }
+
+  void SetView(int v, const View& view) {
+    ValState& s = state_[v];
+    s.kind = ValState::kView;
+    s.view = view;
+  }
+
+  // ---- reduce (generic single-operand; the arg-reduce pattern is fused)
+  void LowerReduce(int idx) {
+    const Op& op = ops_[idx];
+    if (op.operands.size() != 2 || op.results.size() != 1)
+      throw std::string("jam: variadic reduce other than arg-max/arg-min is not supported");
+    const std::string body = reduce_body_op(op);
+    int rop = body == "stablehlo.add" ? 0 : body == "stablehlo.maximum" ? 1 : body == "stablehlo.minimum" ? 2
+            : body == "stablehlo.multiply" ? 3 : -1;
+    if (rop < 0) throw std::string("jam: unsupported reduce body op '" + body + "'");  // reduce.mm:91
+    double init = 0;
+    if (!scalar_of(op.operands[1], &init)) throw std::string("jam: reduce init must be a constant");
+    int x = op.operands[0];
+    // reduce(convert(x_narrow -> f32)): the kernel widens while loading
+    if (state_[x].kind == ValState::kEw && is(x, "stablehlo.convert") &&
+        m_.types[x].dtype == DType::kF32) {
+      const int src = prod(x)->operands[0];
+      const DType st_ = m_.types[src].dtype;
+      if (st_ == DType::kBF16 || st_ == DType::kF16) x = src;
+    }
+    const DType xt = m_.types[x].dtype;
+    const DType ot = m_.types[op.results[0]].dtype;
+    if (!(xt == DType::kF32 || xt == DType::kBF16 || xt == DType::kF16))
+      throw std::string("jam: reduce over ") + DTypeName(xt) + " is not supported";
+    View xv = NeedView(x);
+    const auto dims = reduce_dims(op);
+    // move reduced dims last (a transposed view), then make it dense
+    std::vector<int> keep, red;
+    for (int d = 0; d < xv.rank(); ++d)
+      (std::find(dims.begin(), dims.end(), d) != dims.end() ? red : keep).push_back(d);
+    View pv = xv;
+    int k = 0;
+    int64_t rows = 1, cols = 1;
+    for (int d : keep) {
+      pv.dims[k] = xv.dims[d];
+      pv.strides[k++] = xv.strides[d];
+      rows *= xv.dims[d];
+    }
+    for (int d : red) {
+      pv.dims[k] = xv.dims[d];
+      pv.strides[k++] = xv.strides[d];
+      cols *= xv.dims[d];
+    }
+    pv = Densify(pv);
+    BufRef d = DestFor(op.results[0]);
+    Step st;
+    st.kind = StepKind::kRowReduce;
+    st.bufs = {pv.at(), d};
+    st.i = {int64_t(xt), int64_t(ot), rop, rows, cols};
+    st.f = {float(init)};
+    st.note = body;
+    Emit(st);
+    SetDenseView(op.results[0], d);
+  }
+
+  // Map a dot_general to mk_gemm; `epi` optionally carries bias / relu.
+  void LowerDot(int idx, const Fused* epi, int result_override = -1) {
+    const Op& op = ops_[idx];
+    const int res = result_override >= 0 ? result_override : op.results[0];
+    const int L = op.operands[0], Rv = op.operands[1];
+    DotDims dd = dot_dims(op);
+    if (op.name == "stablehlo.dot") {
+      dd.lc = {int64_t(m_.types[L].rank()) - 1};
+      dd.rc = {0};
+    }
+    View lv = NeedView(L), rv = NeedView(Rv);
+    const DType at = lv.dtype, bt = rv.dtype;
+    if (at != bt) throw std::string("jam: dot_general with mixed operand types");
+    if (at != DType::kF32 && at != DType::kBF16) throw std::string("jam: dot_general on ") + DTypeName(at) + " is not supported";
+    std::vector<int64_t> lf, rf;
+    for (int d = 0; d < lv.rank(); ++d)
+      if (!std::count(dd.lb.begin(), dd.lb.end(), d) && !std::count(dd.lc.begin(), dd.lc.end(), d)) lf.push_back(d);
+    for (int d = 0; d < rv.rank(); ++d)
+      if (!std::count(dd.rb.begin(), dd.rb.end(), d) && !std::count(dd.rc.begin(), dd.rc.end(), d)) rf.push_back(d);
+    // collapse a group of dims of a view into one (size, stride); false if
+    // their memory layout does not allow it
+    auto group = [](const View& v, const std::vector<int64_t>& ds, int64_t* size, int64_t* stride) {
+      *size = 1;
+      *stride = 0;
+      std::vector<int64_t> nz;
+      for (int64_t d : ds) {
+        *size *= v.dims[d];
+        if (v.dims[d] != 1) nz.push_back(d);
+      }
+      if (nz.empty()) {
+        *stride = 0;
+        return true;
+      }
+      for (size_t i = 0; i + 1 < nz.size(); ++i)
+        if (v.strides[nz[i]] != v.strides[nz[i + 1]] * v.dims[nz[i + 1]]) return false;
+      *stride = v.strides[nz.back()];
+      return true;
+    };
+    int64_t B = 1, M, N, K, K2, a_bs = 0, a_ms, a_ks, b_bs = 0, b_ks, b_ns, Bb = 1;
+    bool ok = group(lv, dd.lb, &B, &a_bs) && group(lv, lf, &M, &a_ms) && group(lv, dd.lc, &K, &a_ks) &&
+              group(rv, dd.rb, &Bb, &b_bs) && group(rv, rf, &N, &b_ns) && group(rv, dd.rc, &K2, &b_ks);
+    if (ok && (a_ms != 1 && a_ks != 1 && M != 1 && K != 1)) ok = false;
+    if (ok && (b_ks != 1 && b_ns != 1 && K != 1 && N != 1)) ok = false;
+    if (!ok) {
+      // materialise each operand as dense [batch..., free..., contract...]
+      auto canon = [&](View v, std::vector<int64_t> order) {
+        View p = v;
+        for (size_t k2 = 0; k2 < order.size(); ++k2) {
+          p.dims[k2] = v.dims[order[k2]];
+          p.strides[k2] = v.strides[order[k2]];
+        }
+        return Densify(p);
+      };
+      std::vector<int64_t> lo = dd.lb, ro = dd.rb;
+      lo.insert(lo.end(), lf.begin(), lf.end());
+      lo.insert(lo.end(), dd.lc.begin(), dd.lc.end());
+      ro.insert(ro.end(), dd.rc.begin(), dd.rc.end());
+      ro.insert(ro.end(), rf.begin(), rf.end());
+      lv = canon(lv, lo);
+      rv = canon(rv, ro);
+      const size_t nb = dd.lb.size(), nlf = lf.size(), nrc = dd.rc.size();
+      std::vector<int64_t> gb, gf, gc, rgb, rgc, rgf;
+      for (size_t i = 0; i < nb; ++i) gb.push_back(int64_t(i)), rgb.push_back(int64_t(i));
+      for (size_t i = 0; i < nlf; ++i) gf.push_back(int64_t(nb + i));
+      for (size_t i = 0; i < dd.lc.size(); ++i) gc.push_back(int64_t(nb + nlf + i));
+      for (size_t i = 0; i < nrc; ++i) rgc.push_back(int64_t(nb + i));
+      for (size_t i = 0; i < rf.size(); ++i) rgf.push_back(int64_t(nb + nrc + i));
+      if (!(group(lv, gb, &B, &a_bs) && group(lv, gf, &M, &a_ms) && group(lv, gc, &K, &a_ks) &&
+            group(rv, rgb, &Bb, &b_bs) && group(rv, rgc, &K2, &b_ks) && group(rv, rgf, &N, &b_ns)))
+        throw std::string("jam: dot_general operand layout could not be canonicalised");
+    }
+    if (K != K2 || B != Bb) throw std::string("jam: dot_general dimension mismatch");
+    if (M == 1) a_ms = a_ks == 1 ? K : 1;
+    if (K == 1) a_ks = 1;
+    if (N == 1) b_ns = b_ks == 1 ? K : 1;
+    if (B == 1) a_bs = b_bs = 0;
+    const DType ct = m_.types[res].dtype;
+    BufRef d = DestFor(res);
+    Step st;
+    st.kind = StepKind::kGemm;
+    st.bufs = {lv.at(), rv.at(), d};
+    int epilogue = 0;
+    if (epi) {
+      const View& bv = NeedView(epi->bias);
+      st.bufs.push_back(Densify(bv).at());
+      epilogue = epi->relu ? 2 : 1;
+    }
+    st.i = {int64_t(at), int64_t(ct), B, M, N, K, a_bs, a_ms, a_ks, b_bs, b_ks, b_ns, M * N, N, epilogue};
+    st.note = std::to_string(B) + "x" + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
+    Emit(st);
+    SetDenseView(res, d);
+  }
+
+  void LowerGather(int idx) {
+    const Op& op = ops_[idx];
+    const Attr* dn = op.attr("dimension_numbers");
+    if (!dn) throw std::string("jam: gather without dimension_numbers");
+    auto gi = [&](const char* k) {
+      const Attr* a = dn->get(k);
+      return a ? a->ints() : std::vector<int64_t>{};
+    };
+    const auto offset_dims = gi("offset_dims"), collapsed = gi("collapsed_slice_dims"),
+               start_map = gi("start_index_map");
+    const auto ivd = gi("index_vector_dim");
+    const auto slice = attr_ints(op, {"slice_sizes"});
+    const int tbl = op.operands[0], ids = op.operands[1];
+    const TensorType& tt = m_.types[tbl];
+    const TensorType& it = m_.types[ids];
+    const TensorType& ot = m_.types[op.results[0]];
+    // row gather: table[N, rest...], one collapsed dim 0, full slices elsewhere
+    bool row = collapsed == std::vector<int64_t>{0} && start_map == std::vector<int64_t>{0} &&
+               int(slice.size()) == tt.rank() && slice[0] == 1;
+    for (int d = 1; row && d < tt.rank(); ++d) row = slice[d] == tt.dims[d];
+    const int64_t ivdim = ivd.empty() ? it.rank() : ivd[0];
+    const int64_t batch_rank = ivdim == it.rank() ? it.rank() : it.rank() - 1;
+    if (row) {  // offset dims must be the trailing output dims
+      for (size_t k = 0; k < offset_dims.size(); ++k) row = row && offset_dims[k] == batch_rank + int64_t(k);
+    }
+    if (!row || (ivdim != it.rank() && it.dims[ivdim] != 1))
+      throw std::string("jam: only row gathers (embedding lookups) are supported");  // cf. gather_scatter.mm:135-207
+    const View& tv = NeedView(tbl);
+    const View tvd = Densify(tv);
+    const View iv = Densify(NeedView(ids));
+    if (it.dtype != DType::kI32 && it.dtype != DType::kI64)
+      throw std::string("jam: gather indices must be i32 or i64");
+    BufRef d = DestFor(op.results[0]);
+    int64_t row_elems = 1;
+    for (int k = 1; k < tt.rank(); ++k) row_elems *= tt.dims[k];
+    Step st;
+    st.kind = StepKind::kGather;
+    st.bufs = {tvd.at(), iv.at(), d};
+    st.i = {tt.dims[0], row_elems * DTypeBytes(tt.dtype), int64_t(it.dtype), ot.numel() / std::max<int64_t>(row_elems, 1)};
+    Emit(st);
+    SetDenseView(op.results[0], d);
+  }
+
+  void LowerScatter(int idx) {
+    const Op& op = ops_[idx];
+    if (op.operands.size() != 3) throw std::string("jam: variadic scatter is not supported");
+    const std::string body = op.regions.empty() ? "" : reduce_body_op(op);
+    if (body != "stablehlo.add") throw std::string("jam: only scatter-add is supported (body '" + body + "')");
+    const Attr* dn = op.attr("scatter_dimension_numbers");
+    if (!dn) throw std::string("jam: scatter without dimension numbers");
+    auto gi = [&](const char* k) {
+      const Attr* a = dn->get(k);
+      return a ? a->ints() : std::vector<int64_t>{};
+    };
+    const auto inserted = gi("inserted_window_dims"), todims = gi("scatter_dims_to_operand_dims"),
+               uwd = gi("update_window_dims");
+    const int tbl = op.operands[0], ids = op.operands[1], upd = op.operands[2];
+    const TensorType& tt = m_.types[tbl];
+    const TensorType& ut = m_.types[upd];
+    bool row = inserted == std::vector<int64_t>{0} && todims == std::vector<int64_t>{0};
+    int64_t row_elems = 1;
+    for (int k = 1; k < tt.rank(); ++k) row_elems *= tt.dims[k];
+    // update windows are the trailing update dims and cover whole rows
+    for (size_t k = 0; row && k < uwd.size(); ++k) row = uwd[k] == ut.rank() - int64_t(uwd.size()) + int64_t(k);
+    if (!row) throw std::string("jam: only row scatter-adds are supported");  // cf. gather_scatter.mm:262-335
+    const DType dt = tt.dtype;
+    if (dt != DType::kF32 && dt != DType::kBF16) throw std::string("jam: scatter-add on ") + DTypeName(dt) + " is not supported";
+    const View tv = Densify(NeedView(tbl));
+    const View iv = Densify(NeedView(ids));
+    const View uv = Densify(NeedView(upd));
+    const int64_t n_ids = ut.numel() / std::max<int64_t>(row_elems, 1);
+    BufRef d = DestFor(op.results[0]);
+    BufRef ws = NewTemp(mk_scatter_add_workspace_bytes(tt.dims[0], n_ids));
+    Step st;
+    st.kind = StepKind::kScatterAdd;
+    st.bufs = {tv.at(), iv.at(), uv.at(), d, ws};
+    st.i = {int64_t(dt), tt.dims[0], row_elems, int64_t(m_.types[ids].dtype), n_ids};
+    Emit(st);
+    SetDenseView(op.results[0], d);
+  }
+
+  void LowerConcat(int idx) {
+    const Op& op = ops_[idx];
+    const auto dd = attr_ints(op, {"dim", "dimension"});
+    const int64_t dim = dd.empty() ? 0 : dd[0];
+    const TensorType& t = m_.types[op.results[0]];
+    int64_t outer = 1;
+    for (int64_t k = 0; k < dim; ++k) outer *= t.dims[k];
+    if (outer != 1) throw std::string("jam: concatenate is supported along the outermost non-unit dim only");
+    BufRef d = DestFor(op.results[0]);
+    int64_t off = 0;
+    for (int v : op.operands) {
+      const View& sv = NeedView(v);
+      BufRef part = d;
+      part.offset += off;
+      EmitCopy(sv, part);
+      off += int64_t(m_.types[v].bytes());
+    }
+    SetDenseView(op.results[0], d);
+  }
+
+  // -------------------------------------------------------------- fused steps
+  void EmitFused(int anchor, const Fused& f) {
+    const Op& op = ops_[anchor];
+    if (f.kind == Fused::kSdpa) {
+      const View& q = NeedView(f.q);
+      const View& k = NeedView(f.k);
+      const View& v = NeedView(f.v);
+      auto ok = [](const View& x) { return x.strides[3] == 1 && x.dtype == DType::kBF16; };
+      View qv = ok(q) ? q : Densify(q), kv = ok(k) ? k : Densify(k), vv = ok(v) ? v : Densify(v);
+      const int res = op.results[0];
+      BufRef d = DestFor(res);
+      const auto& od = m_.types[res].dims;
+      Step st;
+      st.kind = StepKind::kSdpa;
+      st.bufs = {qv.at(), kv.at(), vv.at(), d};
+      st.i = {qv.dims[0], qv.dims[1], qv.dims[2], kv.dims[2], qv.dims[3],
+              qv.strides[0], qv.strides[1], qv.strides[2],
+              kv.strides[0], kv.strides[1], kv.strides[2],
+              vv.strides[0], vv.strides[1], vv.strides[2],
+              od[1] * od[2] * od[3], od[2] * od[3], od[3], f.causal ? 1 : 0};
+      st.f = {f.scale};
+      st.note = f.causal ? "causal" : "full";
+      Emit(st);
+      SetDenseView(res, d);
+      return;
+    }
+    if (f.kind == Fused::kArgmax) {
+      View x = NeedView(f.x);
+      const auto dims = reduce_dims(op);
+      const int rd = int(dims[0]);
+      // reduced dim last, dense rows
+      View pv = x;
+      int k = 0;
+      int64_t rows = 1;
+      for (int d = 0; d < x.rank(); ++d)
+        if (d != rd) {
+          pv.dims[k] = x.dims[d];
+          pv.strides[k++] = x.strides[d];
+          rows *= x.dims[d];
+        }
+      pv.dims[k] = x.dims[rd];
+      pv.strides[k] = x.strides[rd];
+      pv = Densify(pv);
+      const int rv = op.results[0], ri = op.results[1];
+      const bool need_vals = live_value(rv);
+      BufRef dv = need_vals ? DestFor(rv) : BufRef{};
+      BufRef di = DestFor(ri);
+      Step st;
+      st.kind = StepKind::kArgmax;
+      st.bufs = {pv.at(), dv, di};
+      st.i = {int64_t(x.dtype), f.is_min ? 1 : 0, rows, x.dims[rd], int64_t(m_.types[ri].dtype), need_vals ? 1 : 0};
+      Emit(st);
+      if (need_vals) SetDenseView(rv, dv);
+      SetDenseView(ri, di);
+      return;
+    }
+    if (f.kind == Fused::kGemmEpi) {
+      LowerDot(f.dot, &f, op.results[0]);
+      return;
+    }
+    if (f.kind == Fused::kGelu) {
+      const View x = Densify(NeedView(f.x));
+      const int res = op.results[0];
+      BufRef d = DestFor(res);
+      Step st;
+      st.kind = StepKind::kGelu;
+      st.bufs = {x.at(), d};
+      st.i = {int64_t(f.out_dtype), x.numel()};
+      Emit(st);
+      SetDenseView(res, d);
+      return;
+    }
+    if (f.kind == Fused::kLayerNorm) {
+      const View x = Densify(NeedView(f.x));
+      BufRef g{}, b{};
+      if (f.gamma >= 0) g = Densify(NeedView(f.gamma)).at();
+      if (f.beta >= 0) b = Densify(NeedView(f.beta)).at();
+      const int res = op.results[0];
+      BufRef d = DestFor(res);
+      const int64_t cols = x.dims.back();
+      Step st;
+      st.kind = StepKind::kLayerNorm;
+      st.bufs = {x.at(), g, b, d};
+      st.i = {int64_t(f.out_dtype), x.numel() / std::max<int64_t>(cols, 1), cols};
+      st.f = {f.eps};
+      Emit(st);
+      SetDenseView(res, d);
+      return;
+    }
+    throw std::string("jam: internal: unknown fused pattern");
+  }
+
+  bool live_value(int v) const {
+    for (int o : outputs_)
+      if (o == v) return true;
+    for (int u : users_[v])
+      if (live_[u]) return true;
+    return false;
+  }
+
+  struct Temp {
+    size_t size;
+    int first, last;
+  };
+
+  Module& m_;
+  CompileOptions opts_;
+  std::shared_ptr<Program> prog_;
+  std::vector<Op> ops_;
+  std::vector<int> outputs_;
+  std::set<const Func*> inlined_once_;
+  std::vector<int> producer_, uses_;
+  std::vector<std::vector<int>> users_;
+  std::vector<ValState> state_;
+  std::map<int, Fused> fused_;
+  std::set<int> absorbed_;
+  std::vector<bool> live_;
+  std::vector<Temp> temps_;
+  std::vector<bool> out_written_;
+};
+
+}  // namespace
+
+CompileResult Compile(const char* code, size_t size, const CompileOptions& opts) {
+  CompileResult r;
+  if (IsMlirBytecode(code, size)) {
+    r.error = "jam: MLIR bytecode (StableHLO portable artifact) input is not supported by this "
+              "build; pass the module as StableHLO text (PJRT_Program.format = \"mlir\")";
+    return r;
+  }
+  std::string err;
+  auto m = ParseText(code, size, err);
+  if (!m) {
+    r.error = err;
+    return r;
+  }
+  Lowerer L(*m, opts);
+  r.program = L.Run(err);
+  if (!r.program) r.error = err.empty() ? "jam: lowering failed" : err;
+  return r;
+}
+
+}  // namespace mi::jam

@@ -1,0 +1,93 @@
+// jam launch plan: what Compile produces and Run executes.
+//
+// The reference compiles a module into one MPSGraph (or graph segments plus
+// collective steps) and runs it synchronously (program_impl.h:14-51,
+// jam_run.mm:361-419).  jam instead produces a flat list of kernel launches
+// over the C-ABI of include/mk_kernels.h.  Every buffer a launch touches is a
+// BufRef resolved at run time: a program input, a program output, a slice
+// of the per-run arena (temporaries, liveness-packed at compile time) or a
+// constant uploaded once per device.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "jam/ir.h"
+
+namespace mi::jam {
+
+enum class Space : uint8_t { kInput, kOutput, kArena, kConst, kNone };
+
+struct BufRef {
+  Space space = Space::kNone;
+  int index = 0;        // input / output / const index (unused for arena)
+  int64_t offset = 0;   // byte offset (arena: absolute offset in the arena)
+};
+
+enum class StepKind : uint8_t {
+  kGemm, kSdpa, kRowReduce, kArgmax, kLayerNorm, kGelu, kEw, kGather, kScatterAdd,
+  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy,
+};
+
+const char* StepName(StepKind k);
+
+struct Step {
+  StepKind kind;
+  std::vector<BufRef> bufs;    // kernel-specific order (documented in run.cc)
+  std::vector<int64_t> i;      // integer parameters
+  std::vector<float> f;        // float parameters
+  std::vector<int32_t> prog;   // ew program (4 ints per instruction)
+  std::vector<int64_t> strides;  // ew per-input strides (6 per input) / copy strides
+  std::vector<int32_t> types;  // ew per-input dtypes
+  std::string note;            // provenance for dumps / errors
+};
+
+struct ConstBlob {
+  TensorType type;
+  std::vector<uint8_t> bytes;
+};
+
+class Program {
+ public:
+  std::vector<TensorType> inputs;
+  std::vector<TensorType> outputs;
+  std::vector<Step> steps;
+  std::vector<ConstBlob> consts;
+  size_t arena_bytes = 0;
+  std::vector<std::string> patterns;   // fused patterns recognised (for tests / dumps)
+  std::string name = "jam.main";
+
+  std::string Dump() const;
+
+  // device copies of `consts`, uploaded lazily once per device ordinal
+  std::vector<void*>* DeviceConsts(int ordinal);
+  ~Program();
+
+ private:
+  std::mutex mu_;
+  std::vector<std::vector<void*>> dev_consts_;
+};
+
+struct CompileOptions {
+  bool fuse_sdpa = true;        // env JAM_NO_SDPA disables
+  bool fuse_argmax = true;
+  bool fuse_gemm_epilogue = true;
+  bool fuse_layernorm = true;
+  bool fuse_gelu = true;
+  bool fuse_elementwise = true;
+};
+
+struct CompileResult {
+  std::shared_ptr<Program> program;
+  std::string error;
+};
+
+// Compile StableHLO (MLIR text) into a launch plan.  Mirrors
+// jam::Compile(bytes, size, num_processes) of the reference (jam.cc:8-24).
+CompileResult Compile(const char* code, size_t size, const CompileOptions& opts = CompileOptions());
+CompileOptions OptionsFromEnv();
+
+}  // namespace mi::jam

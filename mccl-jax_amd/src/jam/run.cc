@@ -1,0 +1,183 @@
+#include "jam/run.h"
+
+#include <cstring>
+
+#include "mk_kernels.h"
+
+namespace mi::jam {
+
+std::vector<void*>* Program::DeviceConsts(int ordinal) {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (dev_consts_.size() <= size_t(ordinal)) dev_consts_.resize(ordinal + 1);
+  auto& v = dev_consts_[ordinal];
+  if (v.size() == consts.size()) return &v;
+  std::string err;
+  exec::DeviceContext* dev = exec::DeviceContext::Get(ordinal, &err);
+  if (!dev) return nullptr;
+  for (size_t i = v.size(); i < consts.size(); ++i) {
+    void* p = dev->Alloc(consts[i].bytes.size(), &err);
+    if (!p && !consts[i].bytes.empty()) return nullptr;
+    if (!dev->CopyToDevice(p, consts[i].bytes.data(), consts[i].bytes.size(), &err)) return nullptr;
+    v.push_back(p);
+  }
+  return &v;
+}
+
+Program::~Program() {
+  for (size_t o = 0; o < dev_consts_.size(); ++o) {
+    if (dev_consts_[o].empty()) continue;
+    exec::DeviceContext* dev = exec::DeviceContext::Get(int(o), nullptr);
+    if (!dev) continue;
+    for (void* p : dev_consts_[o]) dev->Free(p);
+  }
+}
+
+namespace {
+
+struct Frame {
+  const std::vector<RunInput>* inputs;
+  std::vector<RunOutput>* outputs;
+  std::vector<void*>* consts;
+  char* arena;
+};
+
+void* Resolve(const BufRef& b, const Frame& f) {
+  switch (b.space) {
+    case Space::kInput: return const_cast<char*>(static_cast<const char*>((*f.inputs)[b.index].data)) + b.offset;
+    case Space::kOutput: return static_cast<char*>((*f.outputs)[b.index].data) + b.offset;
+    case Space::kArena: return f.arena + b.offset;
+    case Space::kConst: return static_cast<char*>((*f.consts)[b.index]) + b.offset;
+    case Space::kNone: return nullptr;
+  }
+  return nullptr;
+}
+
+// Step encodings (written by lower.cc):
+//   gemm     bufs A,B,C[,bias]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
+//   sdpa     bufs Q,K,V,O       i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
+//   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
+//   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
+//   layernorm bufs x,g,b,y      i io_type,rows,cols  f eps
+//   gelu     bufs x,y           i io_type,n
+//   ew       bufs in...,out     i rank,dims[6],n_inputs,out_reg,out_type  prog  strides[6n]  types[n]  f consts
+//   gather   bufs table,ids,out i n_rows,row_bytes,index_type,n_ids
+//   scatter_add bufs table,ids,updates,out,workspace  i dtype,n_rows,row_len,index_type,n_ids
+//   iota     bufs out           i out_type,rank,dim,dims...
+//   copy_strided bufs in,out    i elem_bytes,rank,dims...  strides
+//   softmax  bufs x,y           i io_type,rows,cols
+//   convert  bufs in,out        i in_type,out_type,n
+//   fill     bufs out           i elem_bytes,n,pattern
+//   copy     bufs in,out        i bytes
+int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
+  void* st = reinterpret_cast<void*>(stream);
+  auto P = [&](size_t k) { return Resolve(s.bufs[k], f); };
+  const auto& i = s.i;
+  switch (s.kind) {
+    case StepKind::kGemm:
+      return mk_gemm(st, int(i[0]), int(i[1]), i[2], i[3], i[4], i[5], P(0), i[6], i[7], i[8], P(1), i[9],
+                     i[10], i[11], P(2), i[12], i[13], s.bufs.size() > 3 ? P(3) : nullptr, int(i[14]));
+    case StepKind::kSdpa:
+      return mk_sdpa_fwd(st, i[0], i[1], i[2], i[3], i[4], P(0), i[5], i[6], i[7], P(1), i[8], i[9], i[10],
+                         P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], s.f[0], int(i[17]), nullptr);
+    case StepKind::kRowReduce:
+      return mk_row_reduce(st, int(i[0]), int(i[1]), int(i[2]), i[3], i[4], P(0), s.f[0], P(1));
+    case StepKind::kArgmax:
+      return mk_row_argmax(st, int(i[0]), int(i[1]), i[2], i[3], P(0), i[5] ? P(1) : nullptr, int(i[4]), P(2));
+    case StepKind::kLayerNorm:
+      return mk_layernorm(st, int(i[0]), i[1], i[2], P(0), P(1), P(2), s.f[0], P(3));
+    case StepKind::kGelu:
+      return mk_gelu_tanh(st, int(i[0]), i[1], P(0), P(1));
+    case StepKind::kEw: {
+      const int n_in = int(i[7]);
+      const void* ins[8];
+      int types[8];
+      for (int k = 0; k < n_in; ++k) {
+        ins[k] = P(size_t(k));
+        types[k] = s.types[size_t(k)];
+      }
+      return mk_ew_program(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
+                           s.prog.data(), s.f.data(), int(s.f.size()), int(i[8]), int(i[9]), P(size_t(n_in)));
+    }
+    case StepKind::kGather:
+      return mk_gather_rows(st, i[0], i[1], P(0), int(i[2]), i[3], P(1), P(2));
+    case StepKind::kScatterAdd:
+      return mk_scatter_add_rows(st, int(i[0]), i[1], i[2], P(0), int(i[3]), i[4], P(1), P(2), P(3), P(4));
+    case StepKind::kIota:
+      return mk_iota(st, int(i[0]), int(i[1]), &i[3], int(i[2]), P(0));
+    case StepKind::kCopyStrided:
+      return mk_copy_strided(st, int(i[0]), int(i[1]), &i[2], P(0), s.strides.data(), P(1));
+    case StepKind::kSoftmax:
+      return mk_softmax_rows(st, int(i[0]), i[1], i[2], P(0), P(1));
+    case StepKind::kConvert:
+      return mk_convert(st, int(i[0]), int(i[1]), i[2], P(0), P(1));
+    case StepKind::kFill:
+      return mk_fill(st, int(i[0]), i[1], uint64_t(i[2]), P(0));
+    case StepKind::kCopy: {
+      if (i[0] == 0) return MK_OK;
+      hipError_t e = hipMemcpyAsync(P(1), P(0), size_t(i[0]), hipMemcpyDeviceToDevice, stream);
+      return e == hipSuccess ? MK_OK : MK_ERR_LAUNCH;
+    }
+  }
+  return MK_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+
+std::string Run(Program& prog, exec::DeviceContext& dev, const std::vector<RunInput>& inputs,
+                std::vector<RunOutput>& outputs) {
+  if (inputs.size() != prog.inputs.size()) return "jam run: wrong number of inputs";  // jam_run.mm:364
+  for (size_t k = 0; k < inputs.size(); ++k) {
+    if (inputs[k].nbytes != prog.inputs[k].bytes()) return "jam run: input size mismatch";  // jam_run.mm:376
+    if (!inputs[k].data && inputs[k].nbytes != 0) return "jam run: null input buffer";
+  }
+  std::string err;
+  std::vector<void*>* consts = prog.DeviceConsts(dev.ordinal());
+  if (!consts) return "jam run: constant upload failed";
+  std::vector<RunOutput> outs(prog.outputs.size());
+  auto release = [&]() {
+    for (auto& o : outs) dev.Free(o.data);
+  };
+  for (size_t k = 0; k < outs.size(); ++k) {
+    outs[k].type = prog.outputs[k];
+    outs[k].nbytes = prog.outputs[k].bytes();
+    if (outs[k].nbytes == 0) continue;
+    outs[k].data = dev.Alloc(outs[k].nbytes, &err);
+    if (!outs[k].data) {
+      release();
+      return "jam run: output allocation failed: " + err;
+    }
+  }
+  char* arena = nullptr;
+  if (prog.arena_bytes) {
+    arena = static_cast<char*>(dev.Alloc(prog.arena_bytes, &err));
+    if (!arena) {
+      release();
+      return "jam run: arena allocation failed: " + err;
+    }
+  }
+  if (!exec::UseDevice(dev.ordinal(), &err)) {
+    release();
+    dev.Free(arena);
+    return "jam run: " + err;
+  }
+  Frame f{&inputs, &outs, consts, arena};
+  for (size_t k = 0; k < prog.steps.size(); ++k) {
+    const int rc = RunStep(prog.steps[k], f, dev.stream());
+    if (rc != MK_OK) {
+      std::string msg = "jam run: step " + std::to_string(k) + " (" + StepName(prog.steps[k].kind) + "): " +
+                        (rc == MK_ERR_LAUNCH && prog.steps[k].kind == StepKind::kCopy ? "hipMemcpyAsync failed"
+                                                                                       : mk_last_error());
+      (void)dev.Synchronize(nullptr);
+      release();
+      dev.Free(arena);
+      return msg;
+    }
+  }
+  // the arena goes back to the pool now: later work on the same stream is
+  // ordered after these launches
+  dev.Free(arena);
+  outputs = std::move(outs);
+  return "";
+}
+
+}  // namespace mi::jam

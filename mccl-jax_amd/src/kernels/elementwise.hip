@@ -100,18 +100,31 @@ struct EwArgs {
 __device__ inline float as_f(int32_t i) { return __int_as_float(i); }
 __device__ inline int32_t as_i(float f) { return __float_as_int(f); }
 
-// Integer-typed inputs are kept as raw int32 bits in the fp32 register file
-// when the program uses the *_S32 opcodes; float-typed inputs are widened.
+// Register file conventions: float types widen to fp32; integer types hold
+// their int32 bit pattern (sign- / zero-extended, 64-bit truncated);
+// predicates hold 0.0f / 1.0f.
 __device__ inline float ew_load(const void* p, int64_t i, int t) {
-  if (t == MK_S32 || t == MK_U32) return as_f(reinterpret_cast<const int32_t*>(p)[i]);
-  if (t == MK_S64) return as_f(int32_t(reinterpret_cast<const int64_t*>(p)[i]));
-  if (t == MK_PRED || t == MK_U8) return float(reinterpret_cast<const uint8_t*>(p)[i]);
-  return load_as_f32(p, i, t);
+  switch (t) {
+    case MK_PRED: return reinterpret_cast<const uint8_t*>(p)[i] ? 1.f : 0.f;
+    case MK_S8: return as_f(int32_t(reinterpret_cast<const int8_t*>(p)[i]));
+    case MK_U8: return as_f(int32_t(reinterpret_cast<const uint8_t*>(p)[i]));
+    case MK_S16: return as_f(int32_t(reinterpret_cast<const int16_t*>(p)[i]));
+    case MK_U16: return as_f(int32_t(reinterpret_cast<const uint16_t*>(p)[i]));
+    case MK_S32: case MK_U32: return as_f(reinterpret_cast<const int32_t*>(p)[i]);
+    case MK_S64: case MK_U64: return as_f(int32_t(reinterpret_cast<const int64_t*>(p)[i]));
+    default: return load_as_f32(p, i, t);
+  }
 }
 __device__ inline void ew_store(void* p, int64_t i, int t, float v) {
-  if (t == MK_S32 || t == MK_U32) reinterpret_cast<int32_t*>(p)[i] = as_i(v);
-  else if (t == MK_S64) reinterpret_cast<int64_t*>(p)[i] = int64_t(as_i(v));
-  else store_from_f32(p, i, t, v);
+  switch (t) {
+    case MK_PRED: reinterpret_cast<uint8_t*>(p)[i] = v != 0.f; break;
+    case MK_S8: case MK_U8: reinterpret_cast<uint8_t*>(p)[i] = uint8_t(as_i(v)); break;
+    case MK_S16: case MK_U16: reinterpret_cast<uint16_t*>(p)[i] = uint16_t(as_i(v)); break;
+    case MK_S32: case MK_U32: reinterpret_cast<int32_t*>(p)[i] = as_i(v); break;
+    case MK_S64: reinterpret_cast<int64_t*>(p)[i] = int64_t(as_i(v)); break;
+    case MK_U64: reinterpret_cast<uint64_t*>(p)[i] = uint64_t(uint32_t(as_i(v))); break;
+    default: store_from_f32(p, i, t, v); break;
+  }
 }
 
 __device__ inline float sign_f(float x) {
@@ -195,6 +208,19 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
       case MK_EW_S32_TO_F32: o = float(as_i(va)); break;
       case MK_EW_F32_TO_S32: o = as_f(int32_t(va)); break;
       case MK_EW_ERF: o = erff(va); break;
+      case MK_EW_CMP_EQ_S32: o = as_i(va) == as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_CMP_NE_S32: o = as_i(va) != as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_CMP_LE_S32: o = as_i(va) <= as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_CMP_GT_S32: o = as_i(va) > as_i(vb) ? 1.f : 0.f; break;
+      case MK_EW_MAX_S32: o = as_f(max(as_i(va), as_i(vb))); break;
+      case MK_EW_MIN_S32: o = as_f(min(as_i(va), as_i(vb))); break;
+      case MK_EW_NEG_S32: o = as_f(-as_i(va)); break;
+      case MK_EW_AND_B32: o = as_f(as_i(va) & as_i(vb)); break;
+      case MK_EW_OR_B32: o = as_f(as_i(va) | as_i(vb)); break;
+      case MK_EW_XOR_B32: o = as_f(as_i(va) ^ as_i(vb)); break;
+      case MK_EW_PRED_TO_S32: o = as_f(va != 0.f ? 1 : 0); break;
+      case MK_EW_S32_TO_PRED: o = as_i(va) != 0 ? 1.f : 0.f; break;
+      case MK_EW_U32_TO_F32: o = float(uint32_t(as_i(va))); break;
       default: o = 0.f; break;
     }
     r[dst] = o;

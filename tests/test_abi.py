@@ -16,7 +16,7 @@ LIB = os.path.join(ROOT, "mccl-jax_amd", "lib")
 def _declared(header: str, prefix: str):
     text = open(os.path.join(INCLUDE, header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"\w*)\s*\(", text)))
 
 
 def _exported(so: str):

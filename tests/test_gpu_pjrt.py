@@ -1,0 +1,190 @@
+"""End-to-end parity through the PJRT C API on the MI355X: the StableHLO of
+each BASELINE config is compiled by the plugin, inputs are uploaded with
+PJRT_Client_BufferFromHostBuffer, the executable runs, results come back
+with PJRT_Buffer_ToHostBuffer and are compared with the CPU oracle on the
+same seeded inputs — the path jaxlib drives (pjrt_c_api.cc:681-829)."""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+from mi355x_pjrt import modules, pjrt
+from oracle import bf16, inputs, native, ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def client():
+    p = pjrt.Plugin()
+    c = p.client()
+    if c.device_kind(c.devices()[0]) != "MI355X":
+        pytest.skip("no device")
+    yield c
+    c.close()
+
+
+def run(client, text, *args):
+    e = client.compile(text)
+    bufs = [client.put(a, code) for a, code in args]
+    outs = e.execute(bufs)
+    res = [o.to_numpy() for o in outs]
+    for b in bufs + outs:
+        b.destroy()
+    e.destroy()
+    return res
+
+
+def test_roundtrip_all_dtypes(client):
+    rng = np.random.default_rng(0)
+    for dt in (np.float32, np.int32, np.int8, np.uint8, np.int16, np.uint16, np.float16, np.bool_, np.int64):
+        a = (rng.standard_normal((3, 5, 7)) * 50).astype(dt)
+        b = client.put(a)
+        np.testing.assert_array_equal(b.to_numpy(), a)
+        b.destroy()
+    bits = bf16.to_bf16_bits(rng.standard_normal(1001).astype(np.float32))
+    b = client.put(bits, pjrt.BF16)
+    assert b.type == pjrt.BF16 and b.shape == (1001,)
+    np.testing.assert_array_equal(b.to_numpy(), bits)
+    b.destroy()
+
+
+def test_c1_mlp_fp32(client):
+    d = inputs.c1_mlp()
+    print("case: pjrt C1 mlp", flush=True)
+    (y,) = run(client, modules.mlp(), *[(d[k], None) for k in ("x", "w1", "b1", "w2", "b2")])
+    want = ops.mlp_forward(d["x"], d["w1"], d["b1"], d["w2"], d["b2"])
+    hh = np.maximum(np.abs(d["x"]).astype(np.float64) @ np.abs(d["w1"]) + np.abs(d["b1"]), 0)
+    norm = hh @ np.abs(d["w2"]) + np.abs(d["b2"])
+    assert np.max(np.abs(y - want) / norm) < 1e-5
+
+
+def test_c2_reduce_sum_and_argmax(client):
+    x = inputs.c2_reduce()["x"]
+    print("case: pjrt C2 reduce_sum / argmax", flush=True)
+    (s,) = run(client, modules.reduce_sum(), (x, pjrt.BF16))
+    ref = native.row_sum_bf16(x)
+    norm = native.row_sum_bf16(bf16.to_bf16_bits(np.abs(bf16.from_bf16_bits(x))))
+    assert np.max(np.abs(s - ref) / norm) < 1e-5
+    for is_min in (False, True):
+        (i,) = run(client, modules.argmax(is_min=is_min), (x, pjrt.BF16))
+        np.testing.assert_array_equal(i, native.argmax_rows_bf16(x, is_min)[0])
+
+
+def test_c2_layernorm(client):
+    d = inputs.c2_layernorm()
+    print("case: pjrt C2 layernorm", flush=True)
+    (y,) = run(client, modules.layernorm(), (d["x"], pjrt.BF16), (d["gamma"], pjrt.BF16), (d["beta"], pjrt.BF16))
+    x, g, b = (bf16.from_bf16_bits(d[n]) for n in ("x", "gamma", "beta"))
+    for r0 in range(0, 8192, 2048):
+        sl = slice(r0, r0 + 2048)
+        want = ops.layernorm(x[sl], g, b, 1e-5)
+        got = bf16.from_bf16_bits(y[sl]).astype(np.float64)
+        xs = np.asarray(x[sl], np.float64)
+        xh = np.abs(xs - xs.mean(-1, keepdims=True)) / np.sqrt(xs.var(-1, keepdims=True) + 1e-5)
+        scale = (xh + 1) * np.abs(g) + np.abs(b)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+        assert np.all(np.abs(got - want) <= ulp + 1e-5 * scale)
+
+
+def test_c2_gelu(client):
+    x = inputs.c2_gelu()["x"]
+    print("case: pjrt C2 gelu (fused)", flush=True)
+    (y,) = run(client, modules.gelu(), (x, pjrt.BF16))
+    for r0 in range(0, x.shape[0], 1024):
+        want = ops.round_to(ops.gelu_tanh(bf16.from_bf16_bits(x[r0:r0 + 1024])), "bf16")
+        dist = bf16.bf16_ulp_distance(y[r0:r0 + 1024], want)
+        assert dist.max() <= 1 and np.mean(dist == 0) > 0.99
+
+
+def test_c2_gelu_unfused_generic_path(client):
+    """JAM_NO_GELU: the jnp chain in the elementwise interpreter, fp32 per op
+    like XLA:CPU.  0.5*x*(1+tanh(u)) cancels for negative x in fp32, so the
+    bound is one bf16 ulp plus the fp32 cancellation term 2^-22 * |x|."""
+    x = inputs.c2_gelu(1024, 16384)["x"]
+    os.environ["JAM_NO_GELU"] = "1"
+    try:
+        (y,) = run(client, modules.gelu(1024, 16384), (x, pjrt.BF16))
+    finally:
+        del os.environ["JAM_NO_GELU"]
+    xf = bf16.from_bf16_bits(x).astype(np.float64)
+    want = ops.gelu_tanh(xf)
+    got = bf16.from_bf16_bits(y).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 2.0 ** -22 * np.abs(xf))
+
+
+def test_c2_layernorm_unfused_generic_path(client):
+    d = inputs.c2_layernorm(512, 4096)
+    os.environ["JAM_NO_LAYERNORM"] = "1"
+    try:
+        (y,) = run(client, modules.layernorm(512, 4096), (d["x"], pjrt.BF16), (d["gamma"], pjrt.BF16),
+                   (d["beta"], pjrt.BF16))
+    finally:
+        del os.environ["JAM_NO_LAYERNORM"]
+    x, g, b = (bf16.from_bf16_bits(d[n]) for n in ("x", "gamma", "beta"))
+    want = ops.layernorm(x, g, b, 1e-5)
+    got = bf16.from_bf16_bits(y).astype(np.float64)
+    xs = np.asarray(x, np.float64)
+    xh = np.abs(xs - xs.mean(-1, keepdims=True)) / np.sqrt(xs.var(-1, keepdims=True) + 1e-5)
+    scale = (xh + 1) * np.abs(g) + np.abs(b)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-5 * scale)
+
+
+@pytest.mark.parametrize("S,causal", [(512, True), (512, False), (2048, True)])
+def test_c3_sdpa_fused(client, S, causal):
+    d = inputs.c3_sdpa(S)
+    print(f"case: pjrt C3 sdpa S={S} causal={causal}", flush=True)
+    (o,) = run(client, modules.sdpa(4, 16, S, 128, causal), *[(d[k], pjrt.BF16) for k in ("q", "k", "v")])
+    scale = 1 / 11.3125  # the module divides by bf16(sqrt(128))
+    for b, h in [(0, 0), (2, 9), (3, 15)]:
+        want = ops.sdpa(*(bf16.from_bf16_bits(d[k][b, h]) for k in ("q", "k", "v")), scale, causal)
+        err = np.abs(bf16.from_bf16_bits(o[b, h]) - want)
+        assert err.max() < 2e-2 and err.max() < 2e-2 * np.abs(want).max()
+
+
+def test_c3_sdpa_unfused_generic_path(client):
+    """JAM_NO_SDPA: the same module through the generic lowering (batched
+    bf16 GEMMs, iota/compare mask, bf16 reduce-max, f32 sum, divide)."""
+    d = inputs.c3_sdpa(256, batch=2, heads=3)
+    os.environ["JAM_NO_SDPA"] = "1"
+    try:
+        (o,) = run(client, modules.sdpa(2, 3, 256, 128, True), *[(d[k], pjrt.BF16) for k in ("q", "k", "v")])
+    finally:
+        del os.environ["JAM_NO_SDPA"]
+    want = ops.sdpa(*(bf16.from_bf16_bits(d[k]) for k in ("q", "k", "v")), 1 / 11.3125, True)
+    err = np.abs(bf16.from_bf16_bits(o) - want)
+    assert err.max() < 2e-2
+
+
+def test_c4_gather_and_scatter_add(client):
+    d = inputs.c4_indexing()
+    print("case: pjrt C4 gather / scatter-add", flush=True)
+    (g,) = run(client, modules.gather(), (d["table_bf16"], pjrt.BF16), (d["ids"], None))
+    np.testing.assert_array_equal(g.reshape(-1, 768), native.gather_rows(d["table_bf16"], d["ids"]))
+    ids = d["ids"].reshape(-1)
+    (t,) = run(client, modules.scatter_add(), (d["table_f32"], None), (ids, None), (d["grads"], None))
+    np.testing.assert_array_equal(t, native.scatter_add_f32(d["table_f32"], ids, d["grads"]))
+
+
+def test_buffer_lifecycle_errors(client):
+    e = client.compile(modules.reduce_sum(4, 8))
+    x = client.put(np.ones((4, 8), np.uint16) * 0x3F80, pjrt.BF16)
+    (y,) = e.execute([x])
+    np.testing.assert_array_equal(y.to_numpy(), np.full(4, 8.0, np.float32))
+    x.delete()
+    with pytest.raises(pjrt.PjrtError) as ei:
+        e.execute([x])
+    assert "was deleted" in ei.value.message
+    with pytest.raises(pjrt.PjrtError):
+        x.to_numpy()
+    y2 = client.put(np.ones((4, 8), np.float32))
+    with pytest.raises(pjrt.PjrtError) as ei:
+        e.execute([y2])  # wrong byte size for a bf16 [4,8] input
+    assert "size mismatch" in ei.value.message
+    for b in (x, y, y2):
+        b.destroy()
+    e.destroy()

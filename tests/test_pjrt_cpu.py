@@ -1,0 +1,170 @@
+"""The PJRT plugin through its C API, without a GPU: the function table,
+platform identity, compile structure of every config module (fused patterns,
+launch counts) and the named-error surface (cf. the reference's
+pjrt_c_api.cc:124-127, 681-697, 753-829 and lower.mm:308-310)."""
+
+import os
+import subprocess
+
+import pytest
+
+from mi355x_pjrt import PJRT_LIBRARY, modules, pjrt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def plugin():
+    return pjrt.Plugin()
+
+
+@pytest.fixture(scope="module")
+def client(plugin):
+    c = plugin.client()
+    yield c
+    c.close()
+
+
+def test_api_table_complete(plugin):
+    assert plugin.version == (0, 55)
+    assert plugin.struct_size == 840          # sizeof(PJRT_Api) for v0.55
+    assert [s for s in pjrt.SLOTS if not plugin.slot(s)] == []
+
+
+def test_platform_identity(client):
+    assert client.platform_name == "mi355x"   # not rocm/cuda: no GPU custom_calls from JAX
+    assert "PJRT 0.55" in client.platform_version
+    devs = client.devices()
+    assert len(devs) >= 1
+    assert client.device_kind(devs[0]) == "MI355X"
+
+
+def _plan(client, text):
+    e = client.compile(text)
+    try:
+        return e.plan(), e.output_types(), e.output_shapes()
+    finally:
+        e.destroy()
+
+
+def test_compile_mlp_fuses_bias_relu(client):
+    plan, types, shapes = _plan(client, modules.mlp())
+    assert types == [pjrt.F32] and shapes == [(256, 1024)]
+    assert "pattern gemm+bias+relu" in plan and "pattern gemm+bias\n" in plan
+    assert plan.count("] gemm") == 2 and "] ew" not in plan
+
+
+def test_compile_sdpa_is_one_flash_launch(client):
+    for causal in (True, False):
+        plan, types, shapes = _plan(client, modules.sdpa(4, 16, 8192, 128, causal=causal))
+        assert shapes == [(4, 16, 8192, 128)] and types == [pjrt.BF16]
+        assert f"sdpa({'causal' if causal else 'full'}, scale=0.088398)" in plan  # 1/bf16(sqrt(128))
+        assert " 1 steps" in plan and "arena 0 B" in plan       # no [S,S] tensor anywhere
+
+
+def test_compile_sdpa_unfused_when_disabled(client):
+    os.environ["JAM_NO_SDPA"] = "1"
+    try:
+        plan, _, _ = _plan(client, modules.sdpa(1, 2, 64, 64))
+    finally:
+        del os.environ["JAM_NO_SDPA"]
+    assert "pattern sdpa" not in plan and plan.count("] gemm") == 2
+
+
+def test_compile_argmax_reduce_gelu(client):
+    plan, types, _ = _plan(client, modules.argmax())
+    assert "pattern argmax" in plan and " 1 steps" in plan and types == [pjrt.S32]
+    plan, _, _ = _plan(client, modules.argmax(is_min=True))
+    assert "pattern argmin" in plan
+    plan, _, _ = _plan(client, modules.reduce_sum())
+    assert " 1 steps" in plan and "row_reduce" in plan       # convert folded into the reduce load
+    plan, _, _ = _plan(client, modules.gelu())
+    assert "pattern gelu_tanh(bf16)" in plan and " 1 steps" in plan and "] gelu" in plan
+    os.environ["JAM_NO_GELU"] = "1"
+    try:
+        plan, _, _ = _plan(client, modules.gelu())
+    finally:
+        del os.environ["JAM_NO_GELU"]
+    assert " 1 steps" in plan and "] ew" in plan             # generic path: still one pass over HBM
+
+
+def test_compile_indexing(client):
+    plan, _, shapes = _plan(client, modules.gather())
+    assert "] gather" in plan and shapes == [(32, 2048, 768)]
+    plan, _, shapes = _plan(client, modules.scatter_add())
+    assert "] scatter_add" in plan and shapes == [(50257, 768)]
+
+
+def test_compile_layernorm(client):
+    plan, types, shapes = _plan(client, modules.layernorm(64, 256))
+    assert types == [pjrt.BF16] and shapes == [(64, 256)]
+    assert "pattern layernorm(bf16, eps=0.000010)" in plan and " 1 steps" in plan
+    os.environ["JAM_NO_LAYERNORM"] = "1"
+    try:
+        plan, _, _ = _plan(client, modules.layernorm(64, 256))
+    finally:
+        del os.environ["JAM_NO_LAYERNORM"]
+    assert "pattern layernorm" not in plan and plan.count("row_reduce") == 2
+
+
+BAD = {
+    "parse": ("module { func.func public @main( -> }", "parse error"),
+    "unhandled": ("""func.func public @main(%a: tensor<4x4xf32>) -> tensor<4x4xf32> {
+  %0 = stablehlo.cholesky %a, lower = true : tensor<4x4xf32>
+  return %0 : tensor<4x4xf32>
+}""", "unhandled op 'stablehlo.cholesky'"),
+    "no_main": ("""func.func private @helper(%a: tensor<f32>) -> tensor<f32> {
+  return %a : tensor<f32>
+}""", "no @main"),
+    "bytecode": ("ML\xefR\x00\x01garbage", "bytecode"),
+    "bad_type": ("""func.func public @main(%a: tensor<4xc64>) -> tensor<4xc64> {
+  return %a : tensor<4xc64>
+}""", "unsupported element type"),
+    "undefined": ("""func.func public @main(%a: tensor<4xf32>) -> tensor<4xf32> {
+  %0 = stablehlo.add %a, %b : tensor<4xf32>
+  return %0 : tensor<4xf32>
+}""", "undefined value %b"),
+}
+
+
+@pytest.mark.parametrize("case", sorted(BAD))
+def test_compile_errors_are_named(client, case):
+    text, needle = BAD[case]
+    with pytest.raises(pjrt.PjrtError) as ei:
+        client.compile(text.encode("latin-1"))
+    assert ei.value.code == "INVALID_ARGUMENT"
+    assert ei.value.message.startswith("jam compile: ")
+    assert needle in ei.value.message
+
+
+def test_unimplemented_slots_and_multinode(plugin, client):
+    with pytest.raises(pjrt.PjrtError) as ei:
+        plugin.client({"node_id": 0, "num_nodes": 2})
+    assert ei.value.code == "UNIMPLEMENTED"
+    # a stub slot answers UNIMPLEMENTED with its name
+    import ctypes
+    fn = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p)(plugin.slot("Executable_Serialize"))
+    err = fn(None)
+    e = plugin._error(err)
+    assert e.code == "UNIMPLEMENTED" and "PJRT_Executable_Serialize" in e.message
+
+
+def test_execute_argument_count_checked(client):
+    e = client.compile(modules.reduce_sum(4, 8))
+    with pytest.raises(pjrt.PjrtError) as ei:
+        e.execute([])
+    assert ei.value.code == "INVALID_ARGUMENT" and "expected 1 arguments" in ei.value.message
+    e.delete()
+    with pytest.raises(pjrt.PjrtError) as ei:
+        e.execute([])
+    assert "deleted executable" in ei.value.message
+    e.destroy()
+
+
+def test_cpp_driver_compiles(tmp_path):
+    mod = tmp_path / "sdpa.mlir"
+    mod.write_text(modules.sdpa(1, 2, 128, 64))
+    exe = os.path.join(ROOT, "mccl-jax_amd", "bin", "pjrt_e2e")
+    r = subprocess.run([exe, PJRT_LIBRARY, str(mod), "--compile-only"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "PJRT API 0.55" in r.stdout and "platform mi355x" in r.stdout and "compiled: 1 outputs" in r.stdout
