@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X PJRT plugin's hot path (one GPU).
 
-Metric (BASELINE.json): "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak;
+Metric: "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak;
 fusion GB/s % HBM peak".
 
   value      causal SDPA forward, bf16, B=4 H=16 D=128, S=8192 (config C3 at

@@ -4,7 +4,7 @@
   kernels   torch-tensor wrappers over the C-ABI of include/mk_kernels.h
   pjrt      ctypes driver of libpjrt_mi355x.so through the PJRT C API
             (the counterpart of the reference's pjrt_e2e harness)
-  modules   StableHLO text of the BASELINE config functions
+  modules   StableHLO text of the benchmark config functions
 """
 
 import os as _os

@@ -1,4 +1,4 @@
-"""StableHLO text of the BASELINE config functions, in the form jax.jit
+"""StableHLO text of the benchmark config functions, in the form jax.jit
 lowers them (``jax.jit(f).lower(*args).as_text()``): pretty-printed ops,
 ``func.call`` for nested jits (``@relu``), keepdims via ``broadcast_in_dim``,
 the iota/compare causal mask, generic-form gather/scatter.

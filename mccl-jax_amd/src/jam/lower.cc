@@ -231,12 +231,27 @@ bool ParseDense(Attr& a, const TensorType& t, std::string& err) {
   return true;
 }
 
+// A decimal literal is read as a double and rounded ONCE to the element
+// type (nearest, ties to even), as MLIR's APFloat conversion does; rounding
+// through float first could round twice.  p = significand bits, emin = the
+// smallest normal exponent (bf16: 8, -126; f16: 11, -14).  The result is
+// exactly representable as a float.
+double RoundToFormat(double v, int p, int emin) {
+  if (!std::isfinite(v) || v == 0) return v;
+  int e;
+  std::frexp(v, &e);
+  const double q = std::ldexp(1.0, std::max(e - 1, emin) - (p - 1));
+  return std::nearbyint(v / q) * q;
+}
+uint16_t F64ToBf16(double v) { return F32ToBf16(float(RoundToFormat(v, 8, -126))); }
+uint16_t F64ToF16(double v) { return F32ToF16(float(RoundToFormat(v, 11, -14))); }
+
 void EncodeElement(double v, int64_t iv, DType d, uint8_t* out) {
   switch (d) {
     case DType::kF32: { float f = float(v); memcpy(out, &f, 4); break; }
     case DType::kF64: memcpy(out, &v, 8); break;
-    case DType::kBF16: { uint16_t h = F32ToBf16(float(v)); memcpy(out, &h, 2); break; }
-    case DType::kF16: { uint16_t h = F32ToF16(float(v)); memcpy(out, &h, 2); break; }
+    case DType::kBF16: { uint16_t h = F64ToBf16(v); memcpy(out, &h, 2); break; }
+    case DType::kF16: { uint16_t h = F64ToF16(v); memcpy(out, &h, 2); break; }
     case DType::kPred: out[0] = iv != 0; break;
     default: memcpy(out, &iv, size_t(DTypeBytes(d))); break;
   }
@@ -246,8 +261,8 @@ void EncodeElement(double v, int64_t iv, DType d, uint8_t* out) {
 uint32_t RegisterBits(double v, int64_t iv, DType d) {
   float f;
   if (IsFloat(d)) {
-    if (d == DType::kBF16) f = Bf16ToF32(F32ToBf16(float(v)));
-    else if (d == DType::kF16) f = F16ToF32(F32ToF16(float(v)));
+    if (d == DType::kBF16) f = Bf16ToF32(F64ToBf16(v));
+    else if (d == DType::kF16) f = F16ToF32(F64ToF16(v));
     else f = float(v);
   } else if (d == DType::kPred) {
     f = iv != 0 ? 1.f : 0.f;
@@ -462,8 +477,8 @@ class Lowerer {
       if (!a.splat && m_.types[v].numel() != 1) return false;
       const DType d = m_.types[v].dtype;
       double x = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
-      if (d == DType::kBF16) x = Bf16ToF32(F32ToBf16(float(x)));
-      else if (d == DType::kF16) x = F16ToF32(F32ToF16(float(x)));
+      if (d == DType::kBF16) x = Bf16ToF32(F64ToBf16(x));
+      else if (d == DType::kF16) x = F16ToF32(F64ToF16(x));
       else if (d == DType::kF32) x = float(x);
       *out = x;
       return true;

@@ -10,7 +10,7 @@ loudly when their HIP build is missing instead of falling back here.
 The reference's numerical oracle is JAX's XLA:CPU backend running the same
 jitted StableHLO (docs/ops.md:7-10).  JAX/jaxlib are a third-party dependency
 that is absent from /root/reference and from this image, with no version
-pinned anywhere in the reference (SURVEY §8c), so the functions here restate
+pinned anywhere in the reference, so the functions here restate
 the published semantics of the StableHLO ops (and JAX's lowering of the
 config functions) in numpy: fp64 for floating-point truth, exact integer /
 bit arithmetic for bf16 rounding, argmax and indexing, and strictly

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configs (oracle; test
+"""Seeded synthetic inputs for the benchmark configs C1-C5 (oracle; test
 infrastructure only).
 
 Both sides of every parity check draw from numpy's PCG64
@@ -36,7 +36,7 @@ def uniform_ids(config: int, tensor: int, shape, high: int) -> np.ndarray:
     return rng(config, tensor).integers(0, high, size=shape, dtype=np.int32)
 
 
-# ---- the BASELINE configs (shapes from BASELINE.json "configs")
+# ---- the benchmark configs (C1 MLP, C2 fusions, C3 SDPA, C4 indexing)
 
 def c1_mlp():
     """C1: x[256,1024], W1[1024,4096], b1[4096], W2[4096,1024], b2[1024] ~ N(0, 0.02) fp32."""

@@ -1,11 +1,11 @@
 """Kernel parity on the MI355X: every mk_* entry point, called through the
 C-ABI (ctypes), against the CPU oracle on the same seeded inputs.
 
-Bars (BASELINE north_star): integer / index / copy work bit-exact; fp32
+Bars: integer / index / copy work bit-exact; fp32
 within 1e-5 relative (stated per test in its norm-scaled form); bf16 outputs
 within one bf16 ulp of the float64 oracle rounded once; attention within
 2e-2 absolute (the north_star bar) and a tighter relative bound.
-Full BASELINE sizes are used where the oracle finishes in seconds; the
+Full benchmark sizes are used where the oracle finishes in seconds; the
 attention sweep at full size is checked on sampled rows plus closed forms.
 """
 
@@ -279,7 +279,7 @@ def test_sdpa_strided_views(K):
 
 @pytest.mark.parametrize("S", [8192])
 def test_sdpa_c3_full_size_sampled_rows(K, S):
-    """C3 at its BASELINE shape: the kernel runs on all [4,16,S,128]; rows are
+    """C3 at its benchmark shape: the kernel runs on all [4,16,S,128]; rows are
     checked against the oracle on a sample (each row needs only its prefix),
     row 0 against the closed form O[0] = V[0] exactly."""
     d = inputs.c3_sdpa(S)

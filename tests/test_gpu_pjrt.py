@@ -1,5 +1,5 @@
 """End-to-end parity through the PJRT C API on the MI355X: the StableHLO of
-each BASELINE config is compiled by the plugin, inputs are uploaded with
+each benchmark config is compiled by the plugin, inputs are uploaded with
 PJRT_Client_BufferFromHostBuffer, the executable runs, results come back
 with PJRT_Buffer_ToHostBuffer and are compared with the CPU oracle on the
 same seeded inputs — the path jaxlib drives (pjrt_c_api.cc:681-829)."""
@@ -168,6 +168,31 @@ def test_c4_gather_and_scatter_add(client):
     ids = d["ids"].reshape(-1)
     (t,) = run(client, modules.scatter_add(), (d["table_f32"], None), (ids, None), (d["grads"], None))
     np.testing.assert_array_equal(t, native.scatter_add_f32(d["table_f32"], ids, d["grads"]))
+
+
+def test_constants_bf16_f16_rne(client):
+    """Dense decimal constants are rounded once from the literal's double
+    value to the element type, nearest-even, with subnormals and overflow to
+    inf (numpy's float64 -> float16 cast; the pinned oracle's f64 -> bf16).
+    Includes a value that rounds differently if it goes through f32 first."""
+    vals = [1 / 3, 0.1, 1 + 2 ** -8 + 2 ** -40, 1 + 2 ** -8, 6.0e-08, 65519.0, 65520.0, -2.5e-7,
+            1e-40, -3.0e38, 5e-324, 0.0]
+    n = len(vals)
+    txt = ", ".join(repr(float(v)) for v in vals)
+    text = f"""func.func public @main(%x: tensor<{n}xf32>) -> (tensor<{n}xbf16>, tensor<{n}xf16>, tensor<{n}xf32>) {{
+  %c = stablehlo.constant dense<[{txt}]> : tensor<{n}xbf16>
+  %h = stablehlo.constant dense<[{txt}]> : tensor<{n}xf16>
+  %cf = stablehlo.convert %c : (tensor<{n}xbf16>) -> tensor<{n}xf32>
+  %s = stablehlo.add %cf, %x : tensor<{n}xf32>
+  return %c, %h, %s : tensor<{n}xbf16>, tensor<{n}xf16>, tensor<{n}xf32>
+}}"""
+    x = np.arange(n, dtype=np.float32)
+    c, h, s = run(client, text, (x, None))
+    want_bf16 = bf16.to_bf16_bits_f64(np.array(vals, np.float64))
+    np.testing.assert_array_equal(c, want_bf16)
+    assert c[2] != bf16.to_bf16_bits(np.array([vals[2]], np.float32))[0]  # the double-rounding case
+    np.testing.assert_array_equal(h.view(np.uint16), np.array(vals, np.float64).astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(s, bf16.from_bf16_bits(want_bf16) + x)
 
 
 def test_buffer_lifecycle_errors(client):
