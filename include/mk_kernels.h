@@ -81,9 +81,13 @@ int mk_gemm(void* stream, int ab_type, int c_type,
  * with no visible key yields NaN, as softmax over all -inf does).
  * Tensors are bf16 with D contiguous; the other strides are in elements:
  *   X element (b,h,s,d) at X + b*x_bs + h*x_hs + s*x_ss + d.
- * D ∈ {64, 128}.  Accumulation fp32, online softmax in fp32.
+ * D ∈ {64, 128}; k_ss, v_ss in [D, 2^24) (any stride when the length is 1).
+ * Scores, running max and accumulation in fp32; the probabilities are
+ * rounded to bf16 (as XLA's bf16 softmax rounds exp) and the row sum adds
+ * those rounded values, so O = Σ bf16(p)·V / Σ bf16(p).
  * lse (optional, may be NULL): fp32 [B,H,Sq] row log-sum-exp (natural log) of
- * the scaled, masked scores, written densely.
+ * the scaled, masked scores, written densely: log of that same row sum plus
+ * the row max (within 2^-9 of the exact value).
  * ---------------------------------------------------------------------- */
 int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                 const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,

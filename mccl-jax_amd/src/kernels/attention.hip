@@ -20,7 +20,14 @@
 // (pairs of keys packed into one 32-bit LDS word per d).
 //
 // Online softmax runs in the log2 domain: s2 = s * scale * log2(e),
-// p = exp2(s2 - m), row statistics in fp32.
+// p = exp2(s2 - m) on v_exp_f32, row statistics in fp32.  The running max m
+// is raised (and O, l rescaled) only when some row's max grows by more than
+// kRescaleLog2; otherwise p <= 2^kRescaleLog2 stays far inside fp32/bf16
+// range and the rescale is skipped.  The row sum adds the bf16-rounded p
+// (the values the P.V product uses) with v_dot2_f32_bf16.
+//
+// K/V tiles are fetched with raw buffer loads whose descriptor ends at the
+// last valid key: rows past Sk read as zeros without a branch.
 #include "mk_common.h"
 
 #include <cmath>
@@ -29,11 +36,15 @@ namespace mk {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 128;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
 constexpr int kThreads = 256;
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
 
 struct SdpaArgs {
   const uint16_t* q;
@@ -55,6 +66,11 @@ __device__ inline bf16x8_t as_bf16x8(const u32x4_t& v) {
   bf16x8_t r;
   __builtin_memcpy(&r, &v, 16);
   return r;
+}
+
+// descriptor over [base, base + bytes): loads past the end return zeros
+__device__ inline __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, int(bytes), kBufferWord3);
 }
 
 template <int D, bool CAUSAL>
@@ -114,25 +130,25 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
 
   auto load_tile = [&](int tile) {
     const int kv0 = tile * kBN;
+    const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1)
+    // byte extent of the valid rows; rows are >= D elements apart
+    const __amdgpu_buffer_rsrc_t kr =
+        tile_rsrc(kb + int64_t(kv0) * p.k_ss, uint32_t((rows - 1) * p.k_ss + D) * 2u);
+    const __amdgpu_buffer_rsrc_t vr =
+        tile_rsrc(vb + int64_t(kv0) * p.v_ss, uint32_t((rows - 1) * p.v_ss + D) * 2u);
 #pragma unroll
     for (int i = 0; i < KCH_T; ++i) {
       const int ch = t + i * kThreads;
       const int row = ch / (D / 8), col = (ch % (D / 8)) * 8;
-      const int key = kv0 + row;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (key < p.Sk) v = *reinterpret_cast<const u32x4_t*>(kb + int64_t(key) * p.k_ss + col);
-      kreg[i] = v;
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, (row * int(p.k_ss) + col) * 2, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < VP_T; ++i) {
       const int task = t + i * kThreads;
       const int pr = task % (kBN / 2), d8 = task / (kBN / 2);
-      const int key = kv0 + 2 * pr;
-      u32x4_t v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
-      if (key < p.Sk) v0 = *reinterpret_cast<const u32x4_t*>(vb + int64_t(key) * p.v_ss + d8 * 8);
-      if (key + 1 < p.Sk) v1 = *reinterpret_cast<const u32x4_t*>(vb + int64_t(key + 1) * p.v_ss + d8 * 8);
-      vreg[i][0] = v0;
-      vreg[i][1] = v1;
+      const int off = (2 * pr * int(p.v_ss) + d8 * 8) * 2;
+      vreg[i][0] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
+      vreg[i][1] = __builtin_amdgcn_raw_buffer_load_b128(vr, off + int(p.v_ss) * 2, 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
@@ -201,37 +217,51 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
         }
     }
 
-    // ---- online softmax (log2 domain)
+    // ---- online softmax (log2 domain, lazy rescale)
     float mt = sacc[0][0];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb2][r]);
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt * p.scale_log2);
-    // m_new == -inf only while every key so far is masked for this row
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    m_run = m_new;
-    float lsum = 0.f;
-    bf16x8_t pf[2][2];
+    const float m_cand = fmaxf(m_run, mt * p.scale_log2);
+    // m_run == -inf until the row has seen an unmasked key, so the first
+    // such tile always rescales (alpha = exp2(-inf) = 0 on O = 0, l = 0)
+    if (__builtin_amdgcn_ballot_w64(m_cand > m_run + kRescaleLog2) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+      m_run = m_cand;
+      l_run *= alpha;
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float e = exp2f(fmaf(sacc[kb2][8 * j2 + i], p.scale_log2, -m_use));
-          lsum += e;
-          pf[kb2][j2][i] = static_cast<__bf16>(e);
-        }
-      }
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
     }
-    l_run = fmaf(l_run, alpha, lsum);
+    // m_run == -inf only while every key so far is masked for this row
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    // p = exp2(s2 - m), packed two keys per 32-bit word (v_cvt_pk_bf16_f32),
+    // summed from the packed words with v_dot2_f32_bf16
+    bf16x8_t pf[2][2];
+    {
+      const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+      float ls0 = 0.f, ls1 = 0.f;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+        for (int j2 = 0; j2 < 2; ++j2) {
+          u32x4_t w;
+#pragma unroll
+          for (int i = 0; i < 8; i += 2) {
+            const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(sacc[kb2][8 * j2 + i], p.scale_log2, -m_use)),
+                              __builtin_amdgcn_exp2f(fmaf(sacc[kb2][8 * j2 + i + 1], p.scale_log2, -m_use))};
+            const bf16x2_t pr = __builtin_convertvector(e, bf16x2_t);
+            w[i / 2] = __builtin_bit_cast(uint32_t, pr);
+            if (i & 2) ls1 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls1, false);
+            else ls0 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls0, false);
+          }
+          pf[kb2][j2] = as_bf16x8(w);
+        }
+      l_run += ls0 + ls1;
+    }
 
     // ---- Oᵀ += Vᵀ · Pᵀ
 #pragma unroll
@@ -293,12 +323,17 @@ extern "C" int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
     return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_fwd: sizes too large");
   if (B == 0 || H == 0 || Sq == 0) return MK_OK;
   if (!q || !k || !v || !o) return fail(MK_ERR_INVALID, "mk_sdpa_fwd: null pointer");
+  // a length-1 sequence axis may carry any stride; only row 0 is read
+  if (Sq == 1) q_ss = o_ss = D;
+  if (Sk == 1) k_ss = v_ss = D;
   // 16-byte vector access along d needs every row start 16-byte aligned
   const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
   const int64_t st = q_bs | q_hs | q_ss | k_bs | k_hs | k_ss | v_bs | v_hs | v_ss;
   if ((al & 15u) != 0 || (st & 7) != 0 || ((o_bs | o_hs | o_ss) & 3) != 0)
     return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_fwd: q/k/v need 16-byte aligned rows (strides % 8 == 0), o strides % 4 == 0");
+  if (k_ss < D || v_ss < D || k_ss >= (int64_t(1) << 24) || v_ss >= (int64_t(1) << 24))
+    return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_fwd: k/v sequence strides must be in [D, 2^24)");
   SdpaArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.o = (uint16_t*)o;
   a.lse = lse;

@@ -232,12 +232,17 @@ def test_scatter_add_edge_cases(K):
 
 
 # ------------------------------------------------------------------ C3 attention
-def _sdpa_case(K, B, H, S, D, causal, seed, Sk=None):
+def _sdpa_case(K, B, H, S, D, causal, seed, Sk=None, qk_std=1 / math.sqrt(128), k_ramp=0):
     rng = np.random.default_rng(seed)
     Sk = Sk or S
     s = 1 / math.sqrt(128)
-    q = bf16.to_bf16_bits((rng.standard_normal((B, H, S, D)) * s).astype(np.float32))
-    k = bf16.to_bf16_bits((rng.standard_normal((B, H, Sk, D)) * s).astype(np.float32))
+    qq = rng.standard_normal((B, H, S, D)) * qk_std
+    kk = rng.standard_normal((B, H, Sk, D)) * qk_std
+    if k_ramp:  # q, k > 0 and |k_j| grows like j / k_ramp: the row max keeps rising
+        qq = np.abs(qq)
+        kk = np.abs(kk) * (1 + np.arange(Sk) / k_ramp)[None, None, :, None]
+    q = bf16.to_bf16_bits(qq.astype(np.float32))
+    k = bf16.to_bf16_bits(kk.astype(np.float32))
     v = bf16.to_bf16_bits((rng.standard_normal((B, H, Sk, D)) * s).astype(np.float32))
     scale = 1 / math.sqrt(D)
     lse = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
@@ -248,7 +253,11 @@ def _sdpa_case(K, B, H, S, D, causal, seed, Sk=None):
     err = np.abs(got - want)
     assert err.max() <= 2e-2, err.max()                       # north_star bar
     assert err.max() <= 2e-2 * np.abs(want).max(), (err.max(), np.abs(want).max())
-    np.testing.assert_allclose(lse.cpu().numpy(), ops.sdpa_lse(qf, kf, scale, causal), atol=2e-4)
+    # the kernel's row sum adds the bf16-rounded probabilities (the values
+    # its P.V product uses, as XLA's bf16 softmax does): each carries <= 2^-9
+    # relative rounding, so log(sum) is within 2^-9 of the exact lse; the
+    # fp32 scores add ~2e-5 relative to the lse's own magnitude
+    np.testing.assert_allclose(lse.cpu().numpy(), ops.sdpa_lse(qf, kf, scale, causal), atol=2.0 ** -9, rtol=2e-5)
     return got, want
 
 
@@ -263,6 +272,18 @@ def test_sdpa_small_vs_oracle(K, S, D, causal):
 def test_sdpa_cross_lengths(K):
     _sdpa_case(K, 1, 2, 96, 128, False, seed=5, Sk=300)
     _sdpa_case(K, 1, 2, 300, 64, True, seed=6, Sk=320)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_large_scores_rescale(K, causal):
+    """Scores with a wide spread (q, k ~ N(0, 1)) and scores that keep growing
+    along the keys, by ~15 (k_ramp 8) and ~4 (k_ramp 32) log2 units per
+    64-key tile: the running max is raised on many tiles (O and l rescaled),
+    and between raises p reaches up to 2^8 against a stale max."""
+    print(f"case: sdpa large scores causal={causal}", flush=True)
+    _sdpa_case(K, 1, 2, 1024, 128, causal, seed=21, qk_std=1.0)
+    _sdpa_case(K, 1, 2, 700, 64, causal, seed=22, qk_std=0.5, k_ramp=8)
+    _sdpa_case(K, 1, 2, 700, 64, causal, seed=23, qk_std=0.5, k_ramp=32)
 
 
 def test_sdpa_strided_views(K):
