@@ -87,7 +87,7 @@ int mk_gemm(void* stream, int ab_type, int c_type,
  * those rounded values, so O = Σ bf16(p)·V / Σ bf16(p).
  * lse (optional, may be NULL): fp32 [B,H,Sq] row log-sum-exp (natural log) of
  * the scaled, masked scores, written densely: log of that same row sum plus
- * the row max (within 2^-9 of the exact value).
+ * the row max (within 2^-8 of the exact value).
  * ---------------------------------------------------------------------- */
 int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                 const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,

@@ -3,8 +3,7 @@
 //
 // Work split: one workgroup = 4 waves = BM = 128 query rows of one (b, h);
 // each wave owns 32 query rows for the whole key loop.  Key/value tiles of
-// BN = 64 rows are staged through LDS (double buffered; global loads for
-// tile t+1 are issued before tile t is computed).
+// BN = 64 rows pass through LDS.
 //
 // Register layouts (32x32 MFMA, lane l, g = l / 32, c = l % 32):
 //   A operand: row c, 8 consecutive k-slots of half g
@@ -15,16 +14,26 @@
 // in-lane reductions plus one exchange with lane l^32.  Those same
 // registers, converted to bf16, ARE the B operand of Oᵀ = Vᵀ · Pᵀ: the k-slot
 // (g, i) of P corresponds to key 16*j + 4*g + 8*(i/4) + i%4 of the 16-key
-// step j, and the A operand (Vᵀ) is read from LDS with the same key mapping,
-// so P never leaves registers.  Vᵀ is produced while staging V into LDS
-// (pairs of keys packed into one 32-bit LDS word per d).
+// step j.  V stays row-major in LDS; the A operand (Vᵀ) is read with
+// ds_read_b64_tr_b16, which hands each lane of a 16-lane group one column of
+// a 4-key x 16-d block: two such reads give the 8 k-slots of a lane.
+//
+// Pipeline (per tile t, one barrier): K runs one tile ahead of its use and
+// V one tile behind, so after the barrier of iteration t the workgroup stores
+// K[t+1] and V[t] (fetched into registers during iteration t-1) into the LDS
+// buffers that K[t-1] and V[t-2] have left, and issues the global loads of
+// K[t+2] and V[t+1].  Each wave computes S(t) = K[t]·Qᵀ and then issues the
+// MFMAs of O += P(t-1)·V[t-1] in the same instruction stream as the
+// exponentials of P(t), so the matrix cores work while the softmax runs.
 //
 // Online softmax runs in the log2 domain: s2 = s * scale * log2(e),
 // p = exp2(s2 - m) on v_exp_f32, row statistics in fp32.  The running max m
-// is raised (and O, l rescaled) only when some row's max grows by more than
-// kRescaleLog2; otherwise p <= 2^kRescaleLog2 stays far inside fp32/bf16
-// range and the rescale is skipped.  The row sum adds the bf16-rounded p
-// (the values the P.V product uses) with v_dot2_f32_bf16.
+// is raised only when some row's max grows by more than kRescaleLog2, and
+// then to an integer, so the rescale factor alpha = exp2(m_old - m_new) is a
+// power of two: O, l and the pending bf16 P(t-1) are scaled exactly.
+// Between raises p <= 2^kRescaleLog2 stays far inside fp32/bf16 range.  The
+// row sum adds the bf16-rounded p (the values the P.V product uses) with
+// v_dot2_f32_bf16.
 //
 // K/V tiles are fetched with raw buffer loads whose descriptor ends at the
 // last valid key: rows past Sk read as zeros without a branch.
@@ -39,6 +48,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 constexpr int kBM = 128;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
@@ -62,6 +73,11 @@ struct SdpaArgs {
   float scale_log2;  // scale * log2(e)
 };
 
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
+
 __device__ inline bf16x8_t as_bf16x8(const u32x4_t& v) {
   bf16x8_t r;
   __builtin_memcpy(&r, &v, 16);
@@ -73,20 +89,24 @@ __device__ inline __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* base, uint32_
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, int(bytes), kBufferWord3);
 }
 
+// 4 bf16 of one LDS column block (ds_read_b64_tr_b16), as two 32-bit words
+__device__ inline uint2 lds_read_tr(const uint16_t* p) {
+  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
-  constexpr int KS = D + 8;    // K row stride in LDS (elements): conflict-free b128 reads
-  constexpr int VS = kBN + 4;  // Vᵀ row stride (elements): conflict-free b64 reads
-  constexpr int KCH = kBN * D / 8;           // 16-byte chunks in a K tile
-  constexpr int KCH_T = KCH / kThreads;      // per thread
-  constexpr int VPAIRS = (kBN / 2) * (D / 8);  // (key pair, d-chunk) tasks in a V tile
-  constexpr int VP_T = VPAIRS / kThreads;
+  constexpr int KS = D + 8;   // K row stride in LDS (elements): conflict-free b128 reads
+  constexpr int VS = D + 32;  // V row stride in LDS (elements): conflict-free transposed reads
+  constexpr int CH = D / 8;   // 16-byte chunks per row
+  constexpr int CH_T = kBN * CH / kThreads;  // chunks per thread per K (or V) tile
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
-  static_assert(KCH % kThreads == 0 && VPAIRS % kThreads == 0, "tile/thread mismatch");
+  static_assert((kBN * CH) % kThreads == 0, "tile/thread mismatch");
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * VS];
 
   // heaviest (latest) query tiles first; consecutive ids walk over heads so
   // a head's tiles share an XCD when BH % 8 == 0
@@ -96,7 +116,8 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   const int b = bh / p.H, h = bh % p.H;
 
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int c = lane & 31, g = lane >> 5;
   const int q0 = qt * kBM + wave * 32;  // first query row of this wave
   const int qrow = q0 + c;               // the query this lane's columns belong to
@@ -118,59 +139,68 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   }
 
   int kv_end = p.Sk;
-  if (CAUSAL) {
-    const int last_q = min(qt * kBM + kBM, p.Sq);  // one past the block's last query
-    kv_end = min(kv_end, last_q);
-  }
+  if (CAUSAL) kv_end = min(kv_end, min(qt * kBM + kBM, p.Sq));  // one past the block's last query
   const int n_tiles = (kv_end + kBN - 1) / kBN;
+  // tiles this wave computes (causal: those holding a key <= its last query)
+  const int n_rel = CAUSAL ? min(n_tiles, (q0 + 31) / kBN + 1) : n_tiles;
 
-  // staging registers for the next tile
-  u32x4_t kreg[KCH_T];
-  u32x4_t vreg[VP_T][2];
-
-  auto load_tile = [&](int tile) {
+  // ---- staging: global -> registers -> LDS
+  u32x4_t kreg[CH_T], vreg[CH_T];
+  auto load_k = [&](int tile) {
     const int kv0 = tile * kBN;
-    const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1)
-    // byte extent of the valid rows; rows are >= D elements apart
-    const __amdgpu_buffer_rsrc_t kr =
+    const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
+    const __amdgpu_buffer_rsrc_t r =
         tile_rsrc(kb + int64_t(kv0) * p.k_ss, uint32_t((rows - 1) * p.k_ss + D) * 2u);
-    const __amdgpu_buffer_rsrc_t vr =
-        tile_rsrc(vb + int64_t(kv0) * p.v_ss, uint32_t((rows - 1) * p.v_ss + D) * 2u);
 #pragma unroll
-    for (int i = 0; i < KCH_T; ++i) {
+    for (int i = 0; i < CH_T; ++i) {
       const int ch = t + i * kThreads;
-      const int row = ch / (D / 8), col = (ch % (D / 8)) * 8;
-      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, (row * int(p.k_ss) + col) * 2, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < VP_T; ++i) {
-      const int task = t + i * kThreads;
-      const int pr = task % (kBN / 2), d8 = task / (kBN / 2);
-      const int off = (2 * pr * int(p.v_ss) + d8 * 8) * 2;
-      vreg[i][0] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
-      vreg[i][1] = __builtin_amdgcn_raw_buffer_load_b128(vr, off + int(p.v_ss) * 2, 0, 0);
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(r, ((ch / CH) * int(p.k_ss) + (ch % CH) * 8) * 2, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto load_v = [&](int tile) {
+    const int kv0 = tile * kBN;
+    const int rows = min(kBN, p.Sk - kv0);
+    const __amdgpu_buffer_rsrc_t r =
+        tile_rsrc(vb + int64_t(kv0) * p.v_ss, uint32_t((rows - 1) * p.v_ss + D) * 2u);
 #pragma unroll
-    for (int i = 0; i < KCH_T; ++i) {
+    for (int i = 0; i < CH_T; ++i) {
       const int ch = t + i * kThreads;
-      const int row = ch / (D / 8), col = (ch % (D / 8)) * 8;
-      *reinterpret_cast<u32x4_t*>(&Ks[buf][row * KS + col]) = kreg[i];
+      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(r, ((ch / CH) * int(p.v_ss) + (ch % CH) * 8) * 2, 0, 0);
     }
+  };
+  auto store_k = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < VP_T; ++i) {
-      const int task = t + i * kThreads;
-      const int pr = task % (kBN / 2), d8 = task / (kBN / 2);
-      const uint16_t* a = reinterpret_cast<const uint16_t*>(&vreg[i][0]);
-      const uint16_t* bq = reinterpret_cast<const uint16_t*>(&vreg[i][1]);
+    for (int i = 0; i < CH_T; ++i) {
+      const int ch = t + i * kThreads;
+      *reinterpret_cast<u32x4_t*>(&Ks[buf][(ch / CH) * KS + (ch % CH) * 8]) = kreg[i];
+    }
+  };
+  auto store_v = [&](int buf) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = uint32_t(a[e]) | (uint32_t(bq[e]) << 16);
-        *reinterpret_cast<uint32_t*>(&Vt[buf][(d8 * 8 + e) * VS + 2 * pr]) = w;
+    for (int i = 0; i < CH_T; ++i) {
+      const int ch = t + i * kThreads;
+      *reinterpret_cast<u32x4_t*>(&Vs[buf][(ch / CH) * VS + (ch % CH) * 8]) = vreg[i];
+    }
+  };
+
+  // ---- Sᵀ = K · Qᵀ for the 64 keys of an LDS K tile (two 32-key blocks)
+  auto qk = [&](int buf, f32x16_t(&s)[2]) {
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb2][r] = 0.f;
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        const bf16x8_t a =
+            as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Ks[buf][(kb2 * 32 + c) * KS + 16 * st + 8 * g]));
+        s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], s[kb2], 0, 0, 0);
       }
     }
   };
+
+  // lane's element offset in a V tile for the transposed reads: key 4g + r/4,
+  // d 16*hi + 4*(r%4) (r = lane % 16, hi = lane / 16 % 2)
+  const int vlane = (4 * g + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   f32x16_t o[NDB];
 #pragma unroll
@@ -180,67 +210,89 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   float m_run = -INFINITY;  // running max, log2 domain
   float l_run = 0.f;        // this lane's share of the running row sum
 
-  if (n_tiles > 0) load_tile(0);
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int buf = tile & 1;
-    store_tile(buf);
-    if (tile + 1 < n_tiles) load_tile(tile + 1);
-    __syncthreads();
-    const int kv0 = tile * kBN;
-    // a wave whose queries all precede the tile has nothing to do here
-    if (CAUSAL && kv0 > q0 + 31) continue;
-
-    // ---- Sᵀ = K · Qᵀ for 64 keys (two 32-key blocks)
-    f32x16_t sacc[2];
+  // ---- Oᵀ += Vᵀ · Pᵀ over the 64 keys of the LDS V tile in buffer vbuf
+  auto pv = [&](const bf16x8_t(&pf)[2][2], int vbuf) {
+    const uint16_t* vt = &Vs[vbuf][vlane];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb2][r] = 0.f;
+      for (int j2 = 0; j2 < 2; ++j2) {
+        const int kstep = kb2 * 32 + 16 * j2;
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) {
-        const bf16x8_t a =
-            as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Ks[buf][(kb2 * 32 + c) * KS + 16 * s + 8 * g]));
-        sacc[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[kb2], 0, 0, 0);
+        for (int db = 0; db < NDB; ++db) {
+          const uint2 lo = lds_read_tr(vt + kstep * VS + db * 32);
+          const uint2 hi = lds_read_tr(vt + (kstep + 8) * VS + db * 32);
+          const u32x4_t av = {lo.x, lo.y, hi.x, hi.y};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pf[kb2][j2], o[db], 0, 0, 0);
+        }
       }
     }
+  };
+
+  // One tile tt of this wave: S(tt) = K[tt]·Qᵀ, softmax statistics, then the
+  // exponentials of P(tt) interleaved with O += P(tt-1)·V[tt-1] (PREV).
+  // pf holds P(tt-1) on entry and P(tt) on exit.
+  auto step = [&](int tt, bf16x8_t(&pf)[2][2], auto prev) {
+    constexpr bool PREV = decltype(prev)::value;
+    const int kv0 = tt * kBN;
+    f32x16_t s[2];
+    qk(tt & 1, s);
 
     // ---- masking (diagonal / ragged tiles only)
-    const bool need_mask = (CAUSAL && kv0 + kBN - 1 > q0) || (kv0 + kBN > p.Sk);
-    if (need_mask) {
+    if ((CAUSAL && kv0 + kBN - 1 > q0) || kv0 + kBN > p.Sk) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kv0 + kb2 * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-          const bool masked = (key >= p.Sk) || (CAUSAL && key > qrow);
-          if (masked) sacc[kb2][r] = -INFINITY;
+          if (key >= p.Sk || (CAUSAL && key > qrow)) s[kb2][r] = -INFINITY;
         }
     }
 
-    // ---- online softmax (log2 domain, lazy rescale)
-    float mt = sacc[0][0];
+    // ---- online softmax statistics (log2 domain, lazy power-of-two rescale)
+    float mt = s[0][0];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb2][r]);
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb2][r]);
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_cand = fmaxf(m_run, mt * p.scale_log2);
     // m_run == -inf until the row has seen an unmasked key, so the first
-    // such tile always rescales (alpha = exp2(-inf) = 0 on O = 0, l = 0)
+    // such tile always rescales (alpha = 0 on O = 0, l = 0)
     if (__builtin_amdgcn_ballot_w64(m_cand > m_run + kRescaleLog2) != 0) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
-      m_run = m_cand;
+      const float m_new = ceilf(m_cand);  // integer: alpha is a power of two
+      // rows with no unmasked key yet keep m = -inf and alpha = 1
+      const float alpha = (m_new == m_run) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      if constexpr (PREV) {
+        // P(tt-1) still to be applied: bf16 * 2^k is exact
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int j2 = 0; j2 < 2; ++j2) {
+            u32x4_t w = __builtin_bit_cast(u32x4_t, pf[kb2][j2]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const f32x2_t e = {__builtin_bit_cast(float, w[i] << 16) * alpha,
+                                 __builtin_bit_cast(float, w[i] & 0xffff0000u) * alpha};
+              w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(e, bf16x2_t));
+            }
+            pf[kb2][j2] = as_bf16x8(w);
+          }
+      }
     }
     // m_run == -inf only while every key so far is masked for this row
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    // p = exp2(s2 - m), packed two keys per 32-bit word (v_cvt_pk_bf16_f32),
-    // summed from the packed words with v_dot2_f32_bf16
-    bf16x8_t pf[2][2];
+
+    // ---- P(tt) = exp2(s2 - m), packed two keys per 32-bit word
+    // (v_cvt_pk_bf16_f32), summed from the packed words with v_dot2_f32_bf16;
+    // the MFMAs of P(tt-1)·V[tt-1] run meanwhile
+    bf16x8_t pn[2][2];
     {
       const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
       float ls0 = 0.f, ls1 = 0.f;
@@ -251,35 +303,50 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
           u32x4_t w;
 #pragma unroll
           for (int i = 0; i < 8; i += 2) {
-            const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(sacc[kb2][8 * j2 + i], p.scale_log2, -m_use)),
-                              __builtin_amdgcn_exp2f(fmaf(sacc[kb2][8 * j2 + i + 1], p.scale_log2, -m_use))};
+            const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i], p.scale_log2, -m_use)),
+                               __builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i + 1], p.scale_log2, -m_use))};
             const bf16x2_t pr = __builtin_convertvector(e, bf16x2_t);
             w[i / 2] = __builtin_bit_cast(uint32_t, pr);
             if (i & 2) ls1 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls1, false);
             else ls0 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls0, false);
           }
-          pf[kb2][j2] = as_bf16x8(w);
+          pn[kb2][j2] = as_bf16x8(w);
         }
       l_run += ls0 + ls1;
     }
+    if constexpr (PREV) pv(pf, (tt - 1) & 1);
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) pf[kb2][j2] = pn[kb2][j2];
+  };
 
-    // ---- Oᵀ += Vᵀ · Pᵀ
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2) {
-        const int kbase = kb2 * 32 + 16 * j2 + 4 * g;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint16_t* row = &Vt[buf][(db * 32 + c) * VS + kbase];
-          u32x4_t av;
-          const uint2 lo = *reinterpret_cast<const uint2*>(row);
-          const uint2 hi = *reinterpret_cast<const uint2*>(row + 8);
-          av[0] = lo.x; av[1] = lo.y; av[2] = hi.x; av[3] = hi.y;
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pf[kb2][j2], o[db], 0, 0, 0);
-        }
-      }
+  // staging of iteration tt: K[tt+1] and V[tt] into LDS, loads of K[tt+2], V[tt+1]
+  auto stage = [&](int tt) {
+    if (tt + 1 < n_tiles) store_k((tt + 1) & 1);
+    store_v(tt & 1);
+    if (tt + 2 < n_tiles) load_k(tt + 2);
+    if (tt + 1 < n_tiles) load_v(tt + 1);
+  };
+
+  bf16x8_t pf[2][2];
+  if (n_tiles > 0) {
+    // prologue: K[0] in LDS, K[1] and V[0] in flight
+    load_k(0);
+    store_k(0);
+    if (n_tiles > 1) load_k(1);
+    load_v(0);
+    __syncthreads();
+    stage(0);
+    step(0, pf, Flag<false>{});  // every wave has n_rel >= 1
+    for (int tt = 1; tt < n_tiles; ++tt) {
+      __syncthreads();
+      stage(tt);
+      if (tt < n_rel) step(tt, pf, Flag<true>{});
+      else if (tt == n_rel) pv(pf, (tt - 1) & 1);  // the wave's last tile, V still resident
     }
+    __syncthreads();  // V[n_tiles-1] was stored in the last iteration
+    if (n_rel == n_tiles) pv(pf, (n_tiles - 1) & 1);
   }
 
   // ---- epilogue: normalise and store O (lane owns query qrow, 4 consecutive d per reg group)
@@ -292,9 +359,11 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = db * 32 + 8 * r4 + 4 * g;
+        const f32x2_t lo = {o[db][4 * r4 + 0] * inv, o[db][4 * r4 + 1] * inv};
+        const f32x2_t hi = {o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv};
         uint2 w;
-        w.x = uint32_t(f32_to_bf16(o[db][4 * r4 + 0] * inv)) | (uint32_t(f32_to_bf16(o[db][4 * r4 + 1] * inv)) << 16);
-        w.y = uint32_t(f32_to_bf16(o[db][4 * r4 + 2] * inv)) | (uint32_t(f32_to_bf16(o[db][4 * r4 + 3] * inv)) << 16);
+        w.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2_t));
+        w.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2_t));
         *reinterpret_cast<uint2*>(ob + d) = w;
       }
     }
