@@ -1,9 +1,10 @@
 // Causal / non-causal scaled-dot-product attention, forward (flash style)
 // for gfx950 on v_mfma_f32_32x32x16_bf16.
 //
-// Work split: one workgroup = 4 waves = BM = 128 query rows of one (b, h);
-// each wave owns 32 query rows for the whole key loop.  Key/value tiles of
-// BN = 64 rows pass through LDS.
+// Work split: one workgroup = 8 waves = BM = 256 query rows of one (b, h),
+// one workgroup per CU; wave w owns query rows 32 w .. 32 w + 31 for the
+// whole key loop.  Key/value tiles of BN = 64 rows pass through LDS and are
+// shared by the 8 waves.
 //
 // Register layouts (32x32 MFMA, lane l, g = l / 32, c = l % 32):
 //   A operand: row c, 8 consecutive k-slots of half g
@@ -18,25 +19,35 @@
 // ds_read_b64_tr_b16, which hands each lane of a 16-lane group one column of
 // a 4-key x 16-d block: two such reads give the 8 k-slots of a lane.
 //
-// Pipeline (per tile t, one barrier): K runs one tile ahead of its use and
-// V one tile behind, so after the barrier of iteration t the workgroup stores
-// K[t+1] and V[t] (fetched into registers during iteration t-1) into the LDS
-// buffers that K[t-1] and V[t-2] have left, and issues the global loads of
-// K[t+2] and V[t+1].  Each wave computes S(t) = K[t]·Qᵀ and then issues the
-// MFMAs of O += P(t-1)·V[t-1] in the same instruction stream as the
-// exponentials of P(t), so the matrix cores work while the softmax runs.
+// Ping-pong: waves 0-3 (group A) and 4-7 (group B) share the four SIMDs, one
+// of each per SIMD, and alternate between two phases separated by workgroup
+// barriers.  In its matrix phase M(t) a wave issues the 32 MFMAs of
+// S(t) = K[t]·Qᵀ and O += P(t-1)·V[t-1] back to back, with the LDS operand
+// reads running several MFMAs ahead; in its softmax phase X(t) it masks S(t),
+// updates the running max / sum and forms P(t).  Group A runs M(t) while
+// group B runs X(t-1), then the roles swap, so each SIMD's matrix core always
+// has one wave feeding it while the other wave does vector work.
+//
+// K and V tiles go from HBM/L2 straight into LDS (buffer_load_dwordx4 ... lds:
+// lane l of a wave writes bytes [16 l, 16 l + 16) of a 1 KB LDS block, from
+// any global address), so no registers stage them.  Rows are padded in LDS
+// (K by 16 bytes, V by 64 bytes) so that the K reads (32 rows, one chunk
+// each) and the transposed V reads (4 rows x 2 chunks per 16 lanes) hit
+// distinct banks; the lanes whose 16 bytes fall on padding fetch from an
+// out-of-range offset, which the buffer unit answers with zeros.  The
+// descriptor of a tile ends at its last valid key, so rows past Sk are zeros
+// too.  K[t+1] and V[t] are copied during phases 2t and 2t+1 into the
+// buffers that K[t-1] and V[t-2] have left, and waited for at the barrier of
+// phase 2t+2.  Each buffer is its own LDS object, named statically at every
+// use, so a copy in flight into one buffer never makes a read of another
+// wait for it.
 //
 // Online softmax runs in the log2 domain: s2 = s * scale * log2(e),
 // p = exp2(s2 - m) on v_exp_f32, row statistics in fp32.  The running max m
-// is raised only when some row's max grows by more than kRescaleLog2, and
-// then to an integer, so the rescale factor alpha = exp2(m_old - m_new) is a
-// power of two: O, l and the pending bf16 P(t-1) are scaled exactly.
-// Between raises p <= 2^kRescaleLog2 stays far inside fp32/bf16 range.  The
-// row sum adds the bf16-rounded p (the values the P.V product uses) with
-// v_dot2_f32_bf16.
-//
-// K/V tiles are fetched with raw buffer loads whose descriptor ends at the
-// last valid key: rows past Sk read as zeros without a branch.
+// is raised (and O, l rescaled) only when some row's max grows by more than
+// kRescaleLog2; between raises p <= 2^kRescaleLog2 stays far inside
+// fp32/bf16 range.  The row sum adds the bf16-rounded p (the values the P.V
+// product uses) with v_dot2_f32_bf16.
 #include "mk_common.h"
 
 #include <cmath>
@@ -50,11 +61,13 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kBM = 128;    // query rows per workgroup
+constexpr int kBM = 256;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
-constexpr int kThreads = 256;
-constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold (log2 units)
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
 
 struct SdpaArgs {
@@ -77,6 +90,10 @@ template <bool B>
 struct Flag {
   static constexpr bool value = B;
 };
+template <int N>
+struct Int {
+  static constexpr int value = N;
+};
 
 __device__ inline bf16x8_t as_bf16x8(const u32x4_t& v) {
   bf16x8_t r;
@@ -96,17 +113,26 @@ __device__ inline uint2 lds_read_tr(const uint16_t* p) {
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
-  constexpr int KS = D + 8;   // K row stride in LDS (elements): conflict-free b128 reads
-  constexpr int VS = D + 32;  // V row stride in LDS (elements): conflict-free transposed reads
-  constexpr int CH = D / 8;   // 16-byte chunks per row
-  constexpr int CH_T = kBN * CH / kThreads;  // chunks per thread per K (or V) tile
+__global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p) {
+  constexpr int CH = D / 8;      // 16-byte chunks of a row
+  constexpr int UK = CH + 1;     // K row stride in LDS, 16-byte units
+  constexpr int UV = CH + 4;     // V row stride in LDS, 16-byte units
+  constexpr int KS = UK * 8, VS = UV * 8;  // the same in elements
+  constexpr int NK = UK, NV = UV;          // 1 KB copies per tile (64 rows x U units / 64 lanes)
+  constexpr int NKW = (NK + kWaves - 1) / kWaves, NVW = (NV + kWaves - 1) / kWaves;
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
-  static_assert((kBN * CH) % kThreads == 0, "tile/thread mismatch");
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * VS];
+  __shared__ __attribute__((aligned(1024))) uint16_t K0[NK * 512];
+  __shared__ __attribute__((aligned(1024))) uint16_t K1[NK * 512];
+  __shared__ __attribute__((aligned(1024))) uint16_t V0[NV * 512];
+  __shared__ __attribute__((aligned(1024))) uint16_t V1[NV * 512];
+  auto kbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
+    if constexpr (decltype(i)::value == 0) return K0; else return K1;
+  };
+  auto vbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
+    if constexpr (decltype(i)::value == 0) return V0; else return V1;
+  };
 
   // heaviest (latest) query tiles first; consecutive ids walk over heads so
   // a head's tiles share an XCD when BH % 8 == 0
@@ -115,9 +141,9 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   const int bh = id % p.BH;
   const int b = bh / p.H, h = bh % p.H;
 
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0: group A, 1: group B (one phase later)
   const int c = lane & 31, g = lane >> 5;
   const int q0 = qt * kBM + wave * 32;  // first query row of this wave
   const int qrow = q0 + c;               // the query this lane's columns belong to
@@ -144,101 +170,103 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   // tiles this wave computes (causal: those holding a key <= its last query)
   const int n_rel = CAUSAL ? min(n_tiles, (q0 + 31) / kBN + 1) : n_tiles;
 
-  // ---- staging: global -> registers -> LDS
-  u32x4_t kreg[CH_T], vreg[CH_T];
-  auto load_k = [&](int tile) {
+  // ---- staging: global -> LDS.  Copy j (1 KB) of a tile is issued by wave
+  // j % 8 and covers LDS units 64 j + lane; unit u holds row u / U, chunk u % U.
+  int koff[NKW], voff[NVW];  // the lane's byte offsets within a tile (2^31: padding)
+#pragma unroll
+  for (int i = 0; i < NKW; ++i) {
+    const int u = 64 * (kWaves * i + wave) + lane, row = u / UK, ch = u % UK;
+    koff[i] = (ch < CH && row < kBN) ? (row * int(p.k_ss) + ch * 8) * 2 : int(0x80000000u);
+  }
+#pragma unroll
+  for (int i = 0; i < NVW; ++i) {
+    const int u = 64 * (kWaves * i + wave) + lane, row = u / UV, ch = u % UV;
+    voff[i] = (ch < CH && row < kBN) ? (row * int(p.v_ss) + ch * 8) * 2 : int(0x80000000u);
+  }
+  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
     const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
-    const __amdgpu_buffer_rsrc_t r =
-        tile_rsrc(kb + int64_t(kv0) * p.k_ss, uint32_t((rows - 1) * p.k_ss + D) * 2u);
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
 #pragma unroll
-    for (int i = 0; i < CH_T; ++i) {
-      const int ch = t + i * kThreads;
-      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(r, ((ch / CH) * int(p.k_ss) + (ch % CH) * 8) * 2, 0, 0);
-    }
+    for (int i = 0; i < nw; ++i)
+      if (kWaves * i + wave < n)  // wave-uniform
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (kWaves * i + wave) * 512), 16, off[i], 0, 0, 0);
   };
-  auto load_v = [&](int tile) {
-    const int kv0 = tile * kBN;
-    const int rows = min(kBN, p.Sk - kv0);
-    const __amdgpu_buffer_rsrc_t r =
-        tile_rsrc(vb + int64_t(kv0) * p.v_ss, uint32_t((rows - 1) * p.v_ss + D) * 2u);
-#pragma unroll
-    for (int i = 0; i < CH_T; ++i) {
-      const int ch = t + i * kThreads;
-      vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(r, ((ch / CH) * int(p.v_ss) + (ch % CH) * 8) * 2, 0, 0);
-    }
-  };
-  auto store_k = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CH_T; ++i) {
-      const int ch = t + i * kThreads;
-      *reinterpret_cast<u32x4_t*>(&Ks[buf][(ch / CH) * KS + (ch % CH) * 8]) = kreg[i];
-    }
-  };
-  auto store_v = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < CH_T; ++i) {
-      const int ch = t + i * kThreads;
-      *reinterpret_cast<u32x4_t*>(&Vs[buf][(ch / CH) * VS + (ch % CH) * 8]) = vreg[i];
-    }
-  };
-
-  // ---- Sᵀ = K · Qᵀ for the 64 keys of an LDS K tile (two 32-key blocks)
-  auto qk = [&](int buf, f32x16_t(&s)[2]) {
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb2][r] = 0.f;
-#pragma unroll
-      for (int st = 0; st < NKS; ++st) {
-        const bf16x8_t a =
-            as_bf16x8(*reinterpret_cast<const u32x4_t*>(&Ks[buf][(kb2 * 32 + c) * KS + 16 * st + 8 * g]));
-        s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[st], s[kb2], 0, 0, 0);
-      }
-    }
-  };
+  auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, NK, NKW, kbuf(buf), tile); };
+  auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, NV, NVW, vbuf(buf), tile); };
 
   // lane's element offset in a V tile for the transposed reads: key 4g + r/4,
   // d 16*hi + 4*(r%4) (r = lane % 16, hi = lane / 16 % 2)
   const int vlane = (4 * g + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int klane = c * KS + 8 * g;  // K row c, half g
 
   f32x16_t o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  f32x16_t s[2];            // S(t): from M(t) to X(t)
+  bf16x8_t pf[2][2];        // P(t): from X(t) to M(t+1)
   float m_run = -INFINITY;  // running max, log2 domain
   float l_run = 0.f;        // this lane's share of the running row sum
 
-  // ---- Oᵀ += Vᵀ · Pᵀ over the 64 keys of the LDS V tile in buffer vbuf
-  auto pv = [&](const bf16x8_t(&pf)[2][2], int vbuf) {
-    const uint16_t* vt = &Vs[vbuf][vlane];
+  // ---- matrix phase M(t): S(t) = K[t]·Qᵀ (QK) and O += P(t-1)·V[t-1] (PV).
+  // KB names K[t]'s buffer, VB V[t-1]'s.  The LDS reads are issued in the
+  // order their MFMAs use them and run ahead by LA MFMAs.
+  auto mphase = [&](auto kbi, auto vbi, auto do_qk, auto do_pv) __attribute__((always_inline)) {
+    constexpr bool QK = decltype(do_qk)::value, PV = decltype(do_pv)::value;
+    const uint16_t* ks = kbuf(kbi);
+    const uint16_t* vs = vbuf(vbi);
+    constexpr int NQ = QK ? 2 * NKS : 0;  // QK MFMAs (two 32-key chains)
+    constexpr int NP = PV ? 4 * NDB : 0;  // PV MFMAs
+    constexpr int N = NQ + NP;
+    constexpr int MQP = NQ < NP ? NQ : NP;
+    // MFMA order: QK and PV alternate while both remain, then the rest
+    auto is_qk = [](int n) __attribute__((always_inline)) {
+      return (QK && PV) ? ((n < 2 * MQP) ? (n % 2 == 0) : (NQ > NP)) : QK;
+    };
+    auto index = [](int n) __attribute__((always_inline)) {
+      return (QK && PV) ? ((n < 2 * MQP) ? n / 2 : MQP + (n - 2 * MQP)) : n;
+    };
+    // A operand of MFMA n: K rows (QK) or Vᵀ from two transposed reads (PV)
+    auto load_op = [&](int n) __attribute__((always_inline)) -> u32x4_t {
+      const int i = index(n);
+      if (is_qk(n)) return *reinterpret_cast<const u32x4_t*>(&ks[klane + (i & 1) * 32 * KS + 16 * (i >> 1)]);
+      const int kstep = 16 * (i / NDB), db = i % NDB;
+      const uint2 lo = lds_read_tr(&vs[vlane + kstep * VS + db * 32]);
+      const uint2 hi = lds_read_tr(&vs[vlane + (kstep + 8) * VS + db * 32]);
+      return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+    };
+    if constexpr (QK) {
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2) {
-        const int kstep = kb2 * 32 + 16 * j2;
+        for (int r = 0; r < 16; ++r) s[kb2][r] = 0.f;
+    }
+    // operands are read LA MFMAs ahead of their use (a ring of LA registers)
+    constexpr int LA = 4;
+    u32x4_t ring[LA];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint2 lo = lds_read_tr(vt + kstep * VS + db * 32);
-          const uint2 hi = lds_read_tr(vt + (kstep + 8) * VS + db * 32);
-          const u32x4_t av = {lo.x, lo.y, hi.x, hi.y};
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), pf[kb2][j2], o[db], 0, 0, 0);
+    for (int n = 0; n < LA && n < N; ++n) ring[n] = load_op(n);
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const u32x4_t a = ring[n % LA];
+      if (n + LA < N) ring[n % LA] = load_op(n + LA);
+      const int i = index(n);
+      if (is_qk(n)) {
+        if constexpr (QK) s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[i >> 1], s[i & 1], 0, 0, 0);
+      } else {
+        if constexpr (PV) {
+          const int kb2 = i / (2 * NDB), j2 = (i / NDB) % 2, db = i % NDB;
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf[kb2][j2], o[db], 0, 0, 0);
         }
       }
     }
   };
 
-  // One tile tt of this wave: S(tt) = K[tt]·Qᵀ, softmax statistics, then the
-  // exponentials of P(tt) interleaved with O += P(tt-1)·V[tt-1] (PREV).
-  // pf holds P(tt-1) on entry and P(tt) on exit.
-  auto step = [&](int tt, bf16x8_t(&pf)[2][2], auto prev) {
-    constexpr bool PREV = decltype(prev)::value;
+  // ---- softmax phase X(t): mask S(t), running max / rescale, P(t), row sum
+  auto xphase = [&](int tt) __attribute__((always_inline)) {
     const int kv0 = tt * kBN;
-    f32x16_t s[2];
-    qk(tt & 1, s);
-
-    // ---- masking (diagonal / ragged tiles only)
     if ((CAUSAL && kv0 + kBN - 1 > q0) || kv0 + kBN > p.Sk) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
@@ -248,8 +276,6 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
           if (key >= p.Sk || (CAUSAL && key > qrow)) s[kb2][r] = -INFINITY;
         }
     }
-
-    // ---- online softmax statistics (log2 domain, lazy power-of-two rescale)
     float mt = s[0][0];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2)
@@ -260,93 +286,107 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
     // m_run == -inf until the row has seen an unmasked key, so the first
     // such tile always rescales (alpha = 0 on O = 0, l = 0)
     if (__builtin_amdgcn_ballot_w64(m_cand > m_run + kRescaleLog2) != 0) {
-      const float m_new = ceilf(m_cand);  // integer: alpha is a power of two
       // rows with no unmasked key yet keep m = -inf and alpha = 1
-      const float alpha = (m_new == m_run) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
+      const float alpha = (m_cand == m_run) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_cand);
+      m_run = m_cand;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      if constexpr (PREV) {
-        // P(tt-1) still to be applied: bf16 * 2^k is exact
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int j2 = 0; j2 < 2; ++j2) {
-            u32x4_t w = __builtin_bit_cast(u32x4_t, pf[kb2][j2]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const f32x2_t e = {__builtin_bit_cast(float, w[i] << 16) * alpha,
-                                 __builtin_bit_cast(float, w[i] & 0xffff0000u) * alpha};
-              w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(e, bf16x2_t));
-            }
-            pf[kb2][j2] = as_bf16x8(w);
-          }
-      }
     }
     // m_run == -inf only while every key so far is masked for this row
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-
-    // ---- P(tt) = exp2(s2 - m), packed two keys per 32-bit word
-    // (v_cvt_pk_bf16_f32), summed from the packed words with v_dot2_f32_bf16;
-    // the MFMAs of P(tt-1)·V[tt-1] run meanwhile
-    bf16x8_t pn[2][2];
-    {
-      const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
-      float ls0 = 0.f, ls1 = 0.f;
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-        for (int j2 = 0; j2 < 2; ++j2) {
-          u32x4_t w;
-#pragma unroll
-          for (int i = 0; i < 8; i += 2) {
-            const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i], p.scale_log2, -m_use)),
-                               __builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i + 1], p.scale_log2, -m_use))};
-            const bf16x2_t pr = __builtin_convertvector(e, bf16x2_t);
-            w[i / 2] = __builtin_bit_cast(uint32_t, pr);
-            if (i & 2) ls1 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls1, false);
-            else ls0 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls0, false);
-          }
-          pn[kb2][j2] = as_bf16x8(w);
-        }
-      l_run += ls0 + ls1;
-    }
-    if constexpr (PREV) pv(pf, (tt - 1) & 1);
+    // p = exp2(s2 - m), packed two keys per 32-bit word (v_cvt_pk_bf16_f32),
+    // summed from the packed words with v_dot2_f32_bf16
+    const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+    float ls0 = 0.f, ls1 = 0.f;
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int j2 = 0; j2 < 2; ++j2) pf[kb2][j2] = pn[kb2][j2];
+      for (int j2 = 0; j2 < 2; ++j2) {
+        u32x4_t w;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i], p.scale_log2, -m_use)),
+                             __builtin_amdgcn_exp2f(fmaf(s[kb2][8 * j2 + i + 1], p.scale_log2, -m_use))};
+          const bf16x2_t pr = __builtin_convertvector(e, bf16x2_t);
+          w[i / 2] = __builtin_bit_cast(uint32_t, pr);
+          if (i & 2) ls1 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls1, false);
+          else ls0 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls0, false);
+        }
+        pf[kb2][j2] = as_bf16x8(w);
+      }
+    l_run += ls0 + ls1;
   };
 
-  // staging of iteration tt: K[tt+1] and V[tt] into LDS, loads of K[tt+2], V[tt+1]
-  auto stage = [&](int tt) {
-    if (tt + 1 < n_tiles) store_k((tt + 1) & 1);
-    store_v(tt & 1);
-    if (tt + 2 < n_tiles) load_k(tt + 2);
-    if (tt + 1 < n_tiles) load_v(tt + 1);
+  // M(t) for this wave: QK when t < n_rel, PV when 1 <= t <= n_rel.
+  // KP = t % 2 (K[t] in K<KP>, V[t-1] in V<1-KP>).
+  auto mstep = [&](int tt, auto kp) __attribute__((always_inline)) {
+    constexpr int KP = decltype(kp)::value;
+    const bool qk = tt < n_rel, pv = tt >= 1 && tt <= n_rel;
+    if (qk && pv) mphase(Int<KP>{}, Int<1 - KP>{}, Flag<true>{}, Flag<true>{});
+    else if (qk) mphase(Int<KP>{}, Int<1 - KP>{}, Flag<true>{}, Flag<false>{});
+    else if (pv) mphase(Int<KP>{}, Int<1 - KP>{}, Flag<false>{}, Flag<true>{});
+  };
+  auto xstep = [&](int tt) __attribute__((always_inline)) {
+    if (tt >= 0 && tt < n_rel) xphase(tt);
   };
 
-  bf16x8_t pf[2][2];
+  // Global phases: group A runs M(t) in phase 2t and X(t) in 2t+1, group B
+  // one phase later.  Each wave runs its own M(0) X(0) M(1) X(1) ... with a
+  // barrier before every phase; B waits out phase 0 first, so barriers pair
+  // up by count.  The barrier of an even phase 2t also waits for the copies
+  // started at phase 2t-2; after it every wave starts its share of K[t+1]
+  // and V[t].  Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
+  auto copies = [&](int t, auto kp) __attribute__((always_inline)) {  // kp = (t+1) % 2
+    constexpr int KP = decltype(kp)::value;
+    if (t + 1 < n_tiles) dma_k(t + 1, Int<KP>{});
+    if (t < n_tiles) dma_v(t, Int<1 - KP>{});
+  };
   if (n_tiles > 0) {
-    // prologue: K[0] in LDS, K[1] and V[0] in flight
-    load_k(0);
-    store_k(0);
-    if (n_tiles > 1) load_k(1);
-    load_v(0);
-    __syncthreads();
-    stage(0);
-    step(0, pf, Flag<false>{});  // every wave has n_rel >= 1
-    for (int tt = 1; tt < n_tiles; ++tt) {
+    dma_k(0, Int<0>{});
+    if (grp == 1) {  // phase 0 for group B: no work
       __syncthreads();
-      stage(tt);
-      if (tt < n_rel) step(tt, pf, Flag<true>{});
-      else if (tt == n_rel) pv(pf, (tt - 1) & 1);  // the wave's last tile, V still resident
+      copies(0, Int<1>{});
     }
-    __syncthreads();  // V[n_tiles-1] was stored in the last iteration
-    if (n_rel == n_tiles) pv(pf, (n_tiles - 1) & 1);
+    for (int t = 0; t <= n_tiles; t += 2) {
+      // ---- M(t), t even
+      if (grp == 0) {
+        __syncthreads();
+        copies(t, Int<1>{});
+      } else {
+        __builtin_amdgcn_s_barrier();
+      }
+      mstep(t, Int<0>{});
+      // ---- X(t)
+      if (t == n_tiles && grp == 1) break;  // B's last phase was M(n_tiles)
+      if (grp == 0) {
+        __builtin_amdgcn_s_barrier();
+      } else {
+        __syncthreads();
+        copies(t + 1, Int<0>{});
+      }
+      xstep(t);
+      if (t == n_tiles) break;
+      // ---- M(t+1), t+1 odd
+      if (grp == 0) {
+        __syncthreads();
+        copies(t + 1, Int<0>{});
+      } else {
+        __builtin_amdgcn_s_barrier();
+      }
+      mstep(t + 1, Int<1>{});
+      // ---- X(t+1)
+      if (t + 1 == n_tiles && grp == 1) break;
+      if (grp == 0) {
+        __builtin_amdgcn_s_barrier();
+      } else {
+        __syncthreads();
+        copies(t + 2, Int<1>{});
+      }
+      xstep(t + 1);
+    }
   }
 
   // ---- epilogue: normalise and store O (lane owns query qrow, 4 consecutive d per reg group)
