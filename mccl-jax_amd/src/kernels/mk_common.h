@@ -138,6 +138,8 @@ struct alignas(16) u16x8 { uint16_t v[8]; };
 struct alignas(16) f32x4 { float v[4]; };
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));  // converting f32x2_t to it is v_cvt_pk_bf16_f32 (RNE)
 
 // Streaming (non-temporal) 16-byte load/store: data touched once should not
 // evict the L2 working set of other kernels.

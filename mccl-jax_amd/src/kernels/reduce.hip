@@ -9,6 +9,7 @@
 // shapes, enough to keep all 256 CUs streaming.
 #include "mk_common.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace mk {
@@ -205,6 +206,65 @@ __global__ __launch_bounds__(kBlock) void row_argmax_kernel(const T* __restrict_
   }
 }
 
+// Argmax / argmin of 16-bit floats (bf16, f16) with a row of at most 65536
+// elements: each element becomes the 32-bit word (key << 16) | (0xFFFF - i),
+// where key orders the values as the XLA reducer does (larger value wins for
+// argmax, smaller for argmin, every NaN beats every number, -0 == +0), so
+// the row winner -- ties going to the lower index -- is the unsigned max of
+// the words.  Two elements are keyed at once with packed 16-bit integer ops.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+template <bool IS_MIN, uint32_t INF>
+__device__ inline uint32_t order_keys(uint32_t w) {
+  constexpr unsigned short kNan = INF + 1;  // smallest NaN magnitude
+  const u16x2_t mag = __builtin_bit_cast(u16x2_t, w & 0x7FFF7FFFu);
+  const u16x2_t magc = __builtin_elementwise_min(mag, u16x2_t{kNan, kNan});  // NaN -> kNan
+  // bit 15 of mag + (0x8000 - kNan) is set exactly for NaN halves
+  const uint32_t nanb =
+      __builtin_bit_cast(uint32_t, mag + u16x2_t{0x8000 - kNan, 0x8000 - kNan}) & 0x80008000u;
+  const uint32_t sgn = w & 0x80008000u;
+  // halves whose key is 0x8000 - magnitude: negative numbers for argmax,
+  // positive numbers for argmin; the other halves (NaN included) take
+  // 0x8000 + magnitude
+  const uint32_t low = IS_MIN ? (~(sgn | nanb) & 0x80008000u) : (sgn & ~nanb);
+  const uint32_t mask = (low >> 15) * 0xFFFFu;
+  const uint32_t kp = __builtin_bit_cast(uint32_t, magc + u16x2_t{0x8000, 0x8000});
+  const uint32_t kn = __builtin_bit_cast(uint32_t, u16x2_t{0x8000, 0x8000} - magc);
+  return (mask & kn) | (~mask & kp);
+}
+
+template <bool IS_F16, bool IS_MIN, typename IdxT>
+__global__ __launch_bounds__(kBlock) void row_argmax16_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                              int cols, uint16_t* __restrict__ values,
+                                                              IdxT* __restrict__ indices) {
+  constexpr uint32_t kInf = IS_F16 ? 0x7C00u : 0x7F80u;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * cols;
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xr);
+  const int nv = cols / 8;
+  uint32_t best = 0;  // below every element's word
+#pragma unroll 2
+  for (int i = lane; i < nv; i += kWave) {
+    const u32x4_t a = xv[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t k = order_keys<IS_MIN, kInf>(a[j]);
+      const uint32_t e = 0xFFFFu - uint32_t(8 * i + 2 * j);  // complement of the low half's index
+      const uint32_t p0 = (k << 16) | e, p1 = (k & 0xFFFF0000u) | (e - 1u);
+      best = max(best, max(p0, p1));
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) best = max(best, uint32_t(__shfl_xor(int(best), m, kWave)));
+  if (lane == 0) {
+    const int idx = int(0xFFFFu - (best & 0xFFFFu));
+    if (values) values[row] = xr[idx];  // the winner's own bits (NaN payloads included)
+    indices[row] = IdxT(idx);
+  }
+}
+
 // LayerNorm: one wave per row, the whole row held in registers (up to
 // kLnMaxPerLane fp32 per lane), two-pass mean/variance, single store.
 constexpr int kLnMaxVecs = 8;  // 8 × 8 bf16 = 64 elements per lane → cols ≤ 4096 in registers
@@ -268,6 +328,73 @@ __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restri
         float v = (r[k][j] - mean) * rstd * gj + bj;
         if constexpr (sizeof(T) == 2) o.v[j] = f32_to_bf16(v);
         else o.v[j] = v;
+      }
+      yv[i] = o;
+    }
+  }
+}
+
+// LayerNorm for bf16 rows of at most 4096 elements: the row stays packed in
+// registers (8 bf16 per 16-byte vector, 32 registers for 4096 columns) and
+// each pass widens its own copy.  The three passes spell the bf16 -> fp32
+// widening differently (shift, byte permute, funnel shift) so the compiler
+// cannot merge them into one widened copy of the row kept across the passes:
+// fewer registers, more rows in flight.  Statistics as layernorm_reg_kernel.
+__device__ inline float lo_a(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ inline float hi_a(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+__device__ inline float lo_b(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_perm(w, 0u, 0x05040C0Cu)); }
+__device__ inline float hi_b(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_perm(w, 0u, 0x07060C0Cu)); }
+__device__ inline float lo_c(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_alignbit(w, 0u, 16u)); }
+__device__ inline float hi_c(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, w, 0x03020C0Cu)); }
+
+__global__ __launch_bounds__(kBlock) void layernorm_bf16_packed_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+    int64_t rows, int cols, float eps, uint16_t* __restrict__ y) {
+  constexpr int KV = kLnMaxVecs;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nv = cols / 8;
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + row * cols);
+  u32x4_t v[KV];
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+    if (lane + k * kWave < nv) v[k] = xv[lane + k * kWave];
+  const float inv_n = 1.f / float(cols);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+    if (lane + k * kWave < nv)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += lo_a(v[k][j]) + hi_a(v[k][j]);
+  const float mean = wave_sum(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+    if (lane + k * kWave < nv)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d0 = lo_b(v[k][j]) - mean, d1 = hi_b(v[k][j]) - mean;
+        q += d0 * d0 + d1 * d1;
+      }
+  const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + eps);
+  u32x4_t* yv = reinterpret_cast<u32x4_t*>(y + row * cols);
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int i = lane + k * kWave;
+    // gamma / beta of two vectors at a time: the loads are not hoisted
+    // into one block of 64 registers
+    if (k % 2 == 0) asm volatile("" ::: "memory");
+    if (i < nv) {
+      const u32x4_t one4 = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+      const u32x4_t gk = gamma ? reinterpret_cast<const u32x4_t*>(gamma)[i] : one4;
+      const u32x4_t bk = beta ? reinterpret_cast<const u32x4_t*>(beta)[i] : u32x4_t{0u, 0u, 0u, 0u};
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x2_t e = {(lo_c(v[k][j]) - mean) * rstd * lo_a(gk[j]) + lo_a(bk[j]),
+                           (hi_c(v[k][j]) - mean) * rstd * hi_a(gk[j]) + hi_a(bk[j])};
+        o[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(e, bf16x2_t));
       }
       yv[i] = o;
     }
@@ -356,6 +483,17 @@ int launch_argmax(hipStream_t s, int64_t rows, int64_t cols, const void* x, void
   dim3 g(grid_for_rows(rows)), b(kBlock);
   const T* xp = reinterpret_cast<const T*>(x);
   T* vp = reinterpret_cast<T*>(values);
+  if constexpr (sizeof(T) == 2) {
+    if (vec_ok && cols <= 65536) {
+      if (index_type == MK_S32)
+        hipLaunchKernelGGL((row_argmax16_kernel<IS_F16, IS_MIN, int32_t>), g, b, 0, s, xp, rows, int(cols), vp,
+                           reinterpret_cast<int32_t*>(indices));
+      else
+        hipLaunchKernelGGL((row_argmax16_kernel<IS_F16, IS_MIN, int64_t>), g, b, 0, s, xp, rows, int(cols), vp,
+                           reinterpret_cast<int64_t*>(indices));
+      return check_launch("mk_row_argmax");
+    }
+  }
   if (index_type == MK_S32)
     hipLaunchKernelGGL((row_argmax_kernel<T, IS_F16, IS_MIN, int32_t>), g, b, 0, s, xp, rows, cols,
                        vp, reinterpret_cast<int32_t*>(indices), vec_ok);
@@ -427,7 +565,7 @@ extern "C" int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t col
     using T = uint16_t;
     const T *xp = (const T*)x, *gp = (const T*)gamma, *bp = (const T*)beta;
     if (vec_ok(8))
-      hipLaunchKernelGGL(layernorm_reg_kernel<T>, g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
+      hipLaunchKernelGGL(layernorm_bf16_packed_kernel, g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
     else
       hipLaunchKernelGGL(layernorm_loop_kernel<T>, g, b, 0, s, xp, gp, bp, rows, cols, eps, (T*)y);
   } else if (io_type == MK_F32) {

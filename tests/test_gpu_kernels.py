@@ -93,6 +93,44 @@ def test_row_argmax_ties_nan_dtypes(K):
             np.testing.assert_array_equal(gv32.cpu().numpy().view(np.uint32), wv32.view(np.uint32))
 
 
+def _argmax_ref_bits(bits, is_min, to_f32):
+    """Reference on raw 16-bit patterns: the pairwise-reducer oracle on the
+    exact fp32 values, values returned as the winner's own bits."""
+    idx, _ = ops.argmax_rows(to_f32(bits), is_min)
+    return idx, bits[np.arange(bits.shape[0]), idx]
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "f16"])
+def test_row_argmax_special_bit_patterns(K, fmt):
+    """16-bit keyed path: NaNs of both signs and several payloads (all beat
+    every number; the first NaN wins), +-inf, +-0 ties, subnormals, lowest
+    index on ties; int32 and int64 indices; values bit-exact."""
+    rng = np.random.default_rng(17)
+    if fmt == "bf16":
+        specials = np.array([0x7F80, 0xFF80, 0x7FC0, 0xFFC0, 0x7F81, 0xFFFF, 0x0000, 0x8000, 0x0001, 0x8001,
+                             0x3F80, 0xBF80], np.uint16)
+        to_f32, to_t = bf16.from_bf16_bits, (lambda b: dev_bf16(b))
+    else:
+        specials = np.array([0x7C00, 0xFC00, 0x7E00, 0xFE00, 0x7C01, 0xFFFF, 0x0000, 0x8000, 0x0001, 0x8001,
+                             0x3C00, 0xBC00], np.uint16)
+        to_f32 = lambda b: b.view(np.float16).astype(np.float32)
+        to_t = lambda b: torch.from_numpy(b.view(np.float16)).cuda()
+    for cols in (8, 64, 1024, 4096):
+        bits = rng.choice(specials, size=(300, cols)).astype(np.uint16)
+        bits[0] = specials[6]                       # all +0
+        bits[1] = specials[7]; bits[1, cols // 2] = specials[6]   # -0 / +0 tie -> index 0
+        bits[2] = specials[0]; bits[2, 3 % cols] = specials[3]    # +inf row with one negative NaN
+        finite = (to_f32(specials) == to_f32(specials))
+        bits[3] = rng.choice(specials[finite], size=cols)          # no NaN at all
+        for is_min in (False, True):
+            want_i, want_v = _argmax_ref_bits(bits, is_min, to_f32)
+            for it in (torch.int32, torch.int64):
+                gi, gv = K.row_argmax(to_t(bits), is_min=is_min, index_dtype=it)
+                np.testing.assert_array_equal(gi.cpu().numpy(), want_i, err_msg=f"{fmt} cols={cols} min={is_min}")
+                got_v = gv.cpu().view(torch.int16).numpy().view(np.uint16)
+                np.testing.assert_array_equal(got_v, want_v, err_msg=f"{fmt} values cols={cols}")
+
+
 # ------------------------------------------------------------------ C2a LayerNorm / C2b GELU
 def _ulp_check(got_bits, want_bits, exact_frac=0.999):
     d = bf16.bf16_ulp_distance(got_bits, want_bits)
