@@ -14,6 +14,8 @@
 // output rows once); steps 1-3 touch only O(n_ids + n_rows) 4-byte words.
 #include "mk_common.h"
 
+#include <algorithm>
+
 namespace mk {
 namespace {
 
@@ -61,12 +63,16 @@ __global__ __launch_bounds__(kBlock) void fill_words(uint32_t* __restrict__ p, i
 constexpr int kSortItems = 4;
 constexpr int kSortTile = kBlock * kSortItems;  // elements per block per pass
 
+// keys[i] = ids[i] (n_rows for an out-of-range id, sorted last and dropped),
+// vals[i] = i; threads also zero the 2 n_rows row bounds.
 template <typename IdxT>
 __global__ __launch_bounds__(kBlock) void scatter_prepare_kernel(const IdxT* __restrict__ ids,
                                                                  int64_t n, int64_t n_rows,
                                                                  uint32_t* __restrict__ keys,
-                                                                 uint32_t* __restrict__ vals) {
+                                                                 uint32_t* __restrict__ vals,
+                                                                 uint32_t* __restrict__ bounds) {
   const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < 2 * n_rows) bounds[i] = 0u;
   if (i >= n) return;
   const int64_t id = int64_t(ids[i]);
   keys[i] = (id < 0 || id >= n_rows) ? uint32_t(n_rows) : uint32_t(id);
@@ -90,30 +96,66 @@ __global__ __launch_bounds__(kBlock) void radix_hist_kernel(const uint32_t* __re
   hist[int64_t(threadIdx.x) * nb + blockIdx.x] = h[threadIdx.x];
 }
 
-// Exclusive scan of `total` words in place, one block of 1024 threads.
+// Exclusive scan of `total` words in place, one block of 1024 threads:
+// thread t owns the contiguous run [t*per, (t+1)*per); the run sums are
+// scanned with wave shuffles and one LDS exchange of the 16 wave totals.
 constexpr int kScanBlock = 1024;
+__device__ inline uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = uint32_t(__shfl_up(int(v), off, 64));
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+// The histogram is 256 x nb words (a multiple of 16): thread t owns runs of
+// 16 contiguous words, read and written as four 16-byte vectors and scanned
+// in registers; runs t, t + 1024, ... are handled in rounds, each round
+// carrying the total of the previous ones.
 __global__ __launch_bounds__(kScanBlock) void scan_exclusive_kernel(uint32_t* __restrict__ data,
                                                                     int64_t total) {
-  __shared__ uint32_t part[kScanBlock];
-  const int t = threadIdx.x;
-  const int64_t per = (total + kScanBlock - 1) / kScanBlock;
-  const int64_t b = t * per, e = (b + per < total) ? b + per : total;
-  uint32_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += data[i];
-  part[t] = s;
-  __syncthreads();
-  // Hillis-Steele inclusive scan of the per-thread partial sums
-  for (int off = 1; off < kScanBlock; off <<= 1) {
-    uint32_t v = t >= off ? part[t - off] : 0u;
+  __shared__ uint32_t wsum[kScanBlock / 64];
+  __shared__ uint32_t carry_s;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t runs = total / 16;
+  uint32_t carry = 0;  // sum of all earlier rounds
+  for (int64_t r0 = 0; r0 < runs; r0 += kScanBlock) {
+    const int64_t run = r0 + t;
+    u32x4_t v[4] = {};
+    if (run < runs) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = reinterpret_cast<const u32x4_t*>(data + run * 16)[k];
+    }
+    uint32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s += v[k][j];
+    const uint32_t incl = wave_incl_scan(s, lane);
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    part[t] += v;
+    if (wave == 0) {
+      const uint32_t w = lane < kScanBlock / 64 ? wsum[lane] : 0u;
+      const uint32_t wi = wave_incl_scan(w, lane);
+      if (lane < kScanBlock / 64) wsum[lane] = wi - w;  // exclusive prefix of wave totals
+      if (lane == kScanBlock / 64 - 1) carry_s = wi;    // this round's total
+    }
     __syncthreads();
-  }
-  uint32_t run = t > 0 ? part[t - 1] : 0u;
-  for (int64_t i = b; i < e; ++i) {
-    const uint32_t v = data[i];
-    data[i] = run;
-    run += v;
+    uint32_t acc = carry + wsum[wave] + incl - s;
+    if (run < runs) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          o[j] = acc;
+          acc += v[k][j];
+        }
+        reinterpret_cast<u32x4_t*>(data + run * 16)[k] = o;
+      }
+    }
+    carry += carry_s;
+    __syncthreads();  // wsum / carry_s are reused by the next round
   }
 }
 
@@ -197,7 +239,8 @@ __global__ __launch_bounds__(kBlock) void scatter_accumulate_kernel(
     const void* __restrict__ updates, const uint32_t* __restrict__ vals,
     const uint32_t* __restrict__ bounds, bool in_place, bool vec_ok) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  // wave-uniform row index, so the bounds and sorted update ids are scalar loads
+  const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (r >= n_rows) return;
   const uint32_t b = bounds[2 * r], e = bounds[2 * r + 1];
   if (in_place && b == e) return;  // untouched row already holds its value
@@ -206,25 +249,39 @@ __global__ __launch_bounds__(kBlock) void scatter_accumulate_kernel(
     float* orow = reinterpret_cast<float*>(out) + r * row_len;
     const float* up = reinterpret_cast<const float*>(updates);
     if (vec_ok) {
+      // up to four float4 columns per lane per sweep (row_len <= 1024 in one);
+      // the next update row is loaded while the current one is added
+      constexpr int Q = 4;
       const int64_t nv = row_len / 4;
-      for (int64_t c0 = lane; c0 < nv; c0 += 3 * 64) {
-        // up to three float4 columns per lane per sweep
-        f32x4 acc[3];
-        int64_t cs[3];
-        int m = 0;
-        for (; m < 3 && c0 + m * 64 < nv; ++m) {
-          cs[m] = c0 + m * 64;
-          acc[m] = reinterpret_cast<const f32x4*>(tr)[cs[m]];
-        }
-        for (uint32_t j = b; j < e; ++j) {
-          const f32x4* urow = reinterpret_cast<const f32x4*>(up + int64_t(vals[j]) * row_len);
-          for (int q = 0; q < m; ++q) {
-            const f32x4 u = urow[cs[q]];
+      const f32x4* t4 = reinterpret_cast<const f32x4*>(tr);
+      for (int64_t c0 = lane; c0 < nv; c0 += Q * 64) {
+        bool ok[Q];
+        f32x4 acc[Q], u[Q], un[Q];
 #pragma unroll
-            for (int z = 0; z < 4; ++z) acc[q].v[z] += u.v[z];
-          }
+        for (int q = 0; q < Q; ++q) {
+          ok[q] = c0 + q * 64 < nv;
+          if (ok[q]) acc[q] = t4[c0 + q * 64];
         }
-        for (int q = 0; q < m; ++q) reinterpret_cast<f32x4*>(orow)[cs[q]] = acc[q];
+        auto load_upd = [&](uint32_t j, f32x4(&dst)[Q]) __attribute__((always_inline)) {
+          const f32x4* urow = reinterpret_cast<const f32x4*>(up + int64_t(vals[j]) * row_len);
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+            if (ok[q]) dst[q] = urow[c0 + q * 64];
+        };
+        if (b < e) load_upd(b, u);
+        for (uint32_t j = b; j < e; ++j) {
+          if (j + 1 < e) load_upd(j + 1, un);
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+            if (ok[q])
+#pragma unroll
+              for (int z = 0; z < 4; ++z) acc[q].v[z] += u[q].v[z];
+#pragma unroll
+          for (int q = 0; q < Q; ++q) u[q] = un[q];
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+          if (ok[q]) reinterpret_cast<f32x4*>(orow)[c0 + q * 64] = acc[q];
       }
     } else {
       for (int64_t c = lane; c < row_len; c += 64) {
@@ -329,14 +386,17 @@ extern "C" int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int6
     return fail(MK_ERR_INVALID, "mk_scatter_add_rows: null pointer");
   hipStream_t s = as_stream(stream);
   ScatterWs w = carve(workspace, n_rows, n_ids);
-  // bounds start at zero: rows without updates have an empty range
-  hipLaunchKernelGGL((fill_words), dim3(blocks_for(2 * n_rows, kBlock)), dim3(kBlock), 0, s, w.bounds, 2 * n_rows);
+  // bounds start at zero (rows without updates have an empty range); the
+  // prepare kernel clears them
+  if (n_ids == 0)
+    hipLaunchKernelGGL((fill_words), dim3(blocks_for(2 * n_rows, kBlock)), dim3(kBlock), 0, s, w.bounds, 2 * n_rows);
   if (n_ids > 0) {
     const unsigned gi = blocks_for(n_ids, kBlock);
+    const unsigned gp = blocks_for(std::max<int64_t>(n_ids, 2 * n_rows), kBlock);
     if (index_type == MK_S32)
-      hipLaunchKernelGGL(scatter_prepare_kernel<int32_t>, dim3(gi), dim3(kBlock), 0, s, (const int32_t*)ids, n_ids, n_rows, w.keys0, w.vals0);
+      hipLaunchKernelGGL(scatter_prepare_kernel<int32_t>, dim3(gp), dim3(kBlock), 0, s, (const int32_t*)ids, n_ids, n_rows, w.keys0, w.vals0, w.bounds);
     else
-      hipLaunchKernelGGL(scatter_prepare_kernel<int64_t>, dim3(gi), dim3(kBlock), 0, s, (const int64_t*)ids, n_ids, n_rows, w.keys0, w.vals0);
+      hipLaunchKernelGGL(scatter_prepare_kernel<int64_t>, dim3(gp), dim3(kBlock), 0, s, (const int64_t*)ids, n_ids, n_rows, w.keys0, w.vals0, w.bounds);
     // keys are in [0, n_rows]: sort only the bits that can be set
     int bits = 0;
     while ((int64_t(1) << bits) <= n_rows) ++bits;
