@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   constexpr int UV = CH + 4;     // V row stride in LDS, 16-byte units
   constexpr int KS = UK * 8, VS = UV * 8;  // the same in elements
   constexpr int NK = UK, NV = UV;          // 1 KB copies per tile (64 rows x U units / 64 lanes)
-  constexpr int NKW = (NK + kWaves - 1) / kWaves, NVW = (NV + kWaves - 1) / kWaves;
+  constexpr int NKW = (NK + 3) / 4, NVW = (NV + 3) / 4;  // per wave: 4 waves of one group issue a tile
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
 
@@ -171,16 +171,17 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   const int n_rel = CAUSAL ? min(n_tiles, (q0 + 31) / kBN + 1) : n_tiles;
 
   // ---- staging: global -> LDS.  Copy j (1 KB) of a tile is issued by wave
-  // j % 8 and covers LDS units 64 j + lane; unit u holds row u / U, chunk u % U.
+  // j % 4 of the issuing group and covers LDS units 64 j + lane; unit u
+  // holds row u / U, chunk u % U.
   int koff[NKW], voff[NVW];  // the lane's byte offsets within a tile (2^31: padding)
 #pragma unroll
   for (int i = 0; i < NKW; ++i) {
-    const int u = 64 * (kWaves * i + wave) + lane, row = u / UK, ch = u % UK;
+    const int u = 64 * (4 * i + (wave & 3)) + lane, row = u / UK, ch = u % UK;
     koff[i] = (ch < CH && row < kBN) ? (row * int(p.k_ss) + ch * 8) * 2 : int(0x80000000u);
   }
 #pragma unroll
   for (int i = 0; i < NVW; ++i) {
-    const int u = 64 * (kWaves * i + wave) + lane, row = u / UV, ch = u % UV;
+    const int u = 64 * (4 * i + (wave & 3)) + lane, row = u / UV, ch = u % UV;
     voff[i] = (ch < CH && row < kBN) ? (row * int(p.v_ss) + ch * 8) * 2 : int(0x80000000u);
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
@@ -189,8 +190,8 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
     const __amdgpu_buffer_rsrc_t r = tile_rsrc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
 #pragma unroll
     for (int i = 0; i < nw; ++i)
-      if (kWaves * i + wave < n)  // wave-uniform
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (kWaves * i + wave) * 512), 16, off[i], 0, 0, 0);
+      if (4 * i + (wave & 3) < n)  // wave-uniform
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (4 * i + (wave & 3)) * 512), 16, off[i], 0, 0, 0);
   };
   auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, NK, NKW, kbuf(buf), tile); };
   auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, NV, NVW, vbuf(buf), tile); };
@@ -336,54 +337,54 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   // Global phases: group A runs M(t) in phase 2t and X(t) in 2t+1, group B
   // one phase later.  Each wave runs its own M(0) X(0) M(1) X(1) ... with a
   // barrier before every phase; B waits out phase 0 first, so barriers pair
-  // up by count.  The barrier of an even phase 2t also waits for the copies
-  // started at phase 2t-2; after it every wave starts its share of K[t+1]
-  // and V[t].  Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
-  auto copies = [&](int t, auto kp) __attribute__((always_inline)) {  // kp = (t+1) % 2
-    constexpr int KP = decltype(kp)::value;
-    if (t + 1 < n_tiles) dma_k(t + 1, Int<KP>{});
-    if (t < n_tiles) dma_v(t, Int<1 - KP>{});
-  };
+  // up by count.  Copies are started only by the group in its softmax phase,
+  // never by the group issuing MFMAs: B starts K[t+2] (into K<t%2>) at the
+  // beginning of X(t), phase 2t+2, and A starts V[t] (into V<t%2>) at the
+  // beginning of X(t), phase 2t+1.  The barrier of every even phase waits
+  // for the issuing waves' copies, so K[t+1] and V[t] are complete for
+  // A's M(t+1) in phase 2t+2.  Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
   if (n_tiles > 0) {
-    dma_k(0, Int<0>{});
-    if (grp == 1) {  // phase 0 for group B: no work
+    if (grp == 1) dma_k(0, Int<0>{});
+    if (grp == 1) {  // phase 0 for group B: start K[1], no softmax
       __syncthreads();
-      copies(0, Int<1>{});
+      if (1 < n_tiles) dma_k(1, Int<1>{});
+    } else {
+      __syncthreads();
     }
     for (int t = 0; t <= n_tiles; t += 2) {
       // ---- M(t), t even
       if (grp == 0) {
-        __syncthreads();
-        copies(t, Int<1>{});
+        if (t > 0) __syncthreads();  // phase 0's barrier was the one above
       } else {
         __builtin_amdgcn_s_barrier();
       }
       mstep(t, Int<0>{});
-      // ---- X(t)
       if (t == n_tiles && grp == 1) break;  // B's last phase was M(n_tiles)
+      // ---- X(t)
       if (grp == 0) {
         __builtin_amdgcn_s_barrier();
+        if (t < n_tiles) dma_v(t, Int<0>{});
       } else {
         __syncthreads();
-        copies(t + 1, Int<0>{});
+        if (t + 2 < n_tiles) dma_k(t + 2, Int<0>{});
       }
       xstep(t);
       if (t == n_tiles) break;
       // ---- M(t+1), t+1 odd
       if (grp == 0) {
         __syncthreads();
-        copies(t + 1, Int<0>{});
       } else {
         __builtin_amdgcn_s_barrier();
       }
       mstep(t + 1, Int<1>{});
-      // ---- X(t+1)
       if (t + 1 == n_tiles && grp == 1) break;
+      // ---- X(t+1)
       if (grp == 0) {
         __builtin_amdgcn_s_barrier();
+        if (t + 1 < n_tiles) dma_v(t + 1, Int<1>{});
       } else {
         __syncthreads();
-        copies(t + 2, Int<1>{});
+        if (t + 3 < n_tiles) dma_k(t + 3, Int<1>{});
       }
       xstep(t + 1);
     }
