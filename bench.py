@@ -16,7 +16,11 @@ fusion GB/s % HBM peak".
   cpu_baseline  the float64 numpy oracle on a bounded sample of (b, h) pairs
              of the same workload, extrapolated to all pairs
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only sdpa|fusions]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS] [--only sdpa|fusions]
+
+Before the first timed region the headline kernel runs untimed for --spinup
+seconds (default 1), so that no timed region includes the clocks' ramp from
+idle; then each workload runs W untimed and K timed launches.
 """
 
 from __future__ import annotations
@@ -44,7 +48,9 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--spinup", type=float, default=1.0,
+                    help="seconds of untimed headline launches before anything is timed (clocks settle)")
     ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -69,6 +75,24 @@ def time_launches(torch, fn, steps, warmup):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps
+
+
+def spin_up(torch, np, K, args):
+    """Untimed launches of the headline kernel for args.spinup seconds, so that
+    the GPU's clocks have left their idle state before the first timed region
+    (a cold MI355X runs the first tens of milliseconds of work slower)."""
+    if args.spinup <= 0:
+        return
+    B, H, S, D = 4, 16, 8192, 128
+    q = torch.zeros(B, H, S, D, dtype=torch.bfloat16, device="cuda")
+    o = torch.empty_like(q)
+    t0 = time.time()
+    while time.time() - t0 < args.spinup:
+        for _ in range(20):
+            K.sdpa_fwd(q, q, q, 1 / math.sqrt(D), True, out=o)
+        torch.cuda.synchronize()
+    del q, o
+    torch.cuda.empty_cache()
 
 
 def sdpa_flops(B, H, S, D):
@@ -217,6 +241,7 @@ def main():
                           "ms": round(ms, 4), "gbs": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}))
         return
     sweep, head, fusions = {}, None, {}
+    spin_up(torch, np, K, args)
     if args.only in (None, "sdpa", "headline"):
         sweep, head = run_sdpa(torch, np, K, args)
     if args.only in (None, "fusions"):
@@ -235,6 +260,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
+        "spinup_s": args.spinup,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",

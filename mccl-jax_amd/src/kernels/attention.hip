@@ -36,11 +36,12 @@
 // distinct banks; the lanes whose 16 bytes fall on padding fetch from an
 // out-of-range offset, which the buffer unit answers with zeros.  The
 // descriptor of a tile ends at its last valid key, so rows past Sk are zeros
-// too.  K[t+1] and V[t] are copied during phases 2t and 2t+1 into the
-// buffers that K[t-1] and V[t-2] have left, and waited for at the barrier of
-// phase 2t+2.  Each buffer is its own LDS object, named statically at every
-// use, so a copy in flight into one buffer never makes a read of another
-// wait for it.
+// too.  The copies are issued from inline assembly, so the compiler neither
+// knows nor waits for them: the issuing wave waits for its own copies
+// (s_waitcnt vmcnt(0)) right before the barrier that hands the data to the
+// other waves, and the barriers themselves order LDS only.  Q is waited for
+// before the key loop, so no wait the compiler places inside the loop can
+// stall on a copy in flight.
 //
 // Online softmax runs in the log2 domain: s2 = s * scale * log2(e),
 // p = exp2(s2 - m) on v_exp_f32, row statistics in fp32.  The running max m
@@ -61,7 +62,6 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kBM = 256;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
@@ -101,9 +101,47 @@ __device__ inline bf16x8_t as_bf16x8(const u32x4_t& v) {
   return r;
 }
 
-// descriptor over [base, base + bytes): loads past the end return zeros
-__device__ inline __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, int(bytes), kBufferWord3);
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// raw buffer descriptor over [base, base + bytes): loads past the end return
+// zeros (word1: base bits 47:32, stride 0; word2: size; word3: gfx9 format)
+__device__ inline i32x4_t tile_desc(const uint16_t* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xFFFFu), int(bytes), kBufferWord3};
+}
+
+// LDS byte address of a __shared__ location
+__device__ inline uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// One 1 KB copy HBM/L2 -> LDS: lane l loads 16 bytes at byte offset voff of
+// the descriptor's range and the buffer unit writes them to LDS bytes
+// [dst + 16 l, dst + 16 l + 16).  Issued from inline assembly so that the
+// compiler does not track it: it inserts no vmcnt wait of its own for these
+// copies, and the kernel waits for them explicitly (wait_copies) before the
+// barrier that hands the data to the other waves.  M0 holds the LDS address
+// (set by the compiler from the constraint); one wait state separates the M0
+// write from the copy.
+// The descriptor and the LDS address pass through readfirstlane here, at the
+// operand, so they are in SGPRs however the caller computed them.
+__device__ inline void copy_to_lds(const i32x4_t& rsrc, uint32_t dst, int voff) {
+  const i32x4_t r = {__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
+                     __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(r), "{m0}"(__builtin_amdgcn_readfirstlane(dst))
+               : "memory");
+}
+
+// wait until every copy this wave has issued has landed in LDS
+__device__ inline void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// workgroup barrier ordering LDS accesses only (waits for lgkmcnt, not vmcnt)
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // 4 bf16 of one LDS column block (ds_read_b64_tr_b16), as two 32-bit words
@@ -162,6 +200,10 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
       if (ok) v = *reinterpret_cast<const u32x4_t*>(qb + int64_t(qrow) * p.q_ss + 16 * s + 8 * g);
       qf[s] = as_bf16x8(v);
     }
+    // Q is in registers before the key loop starts.  Without this wait the
+    // compiler waits for Q (vmcnt(0)) at the first use inside the loop, on
+    // every trip, which would also wait out the K/V copies in flight.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched
   }
 
   int kv_end = p.Sk;
@@ -187,11 +229,11 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
     const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
-    const __amdgpu_buffer_rsrc_t r = tile_rsrc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
+    const i32x4_t r = tile_desc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
 #pragma unroll
     for (int i = 0; i < nw; ++i)
       if (4 * i + (wave & 3) < n)  // wave-uniform
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)(dst + (4 * i + (wave & 3)) * 512), 16, off[i], 0, 0, 0);
+        copy_to_lds(r, lds_addr(dst + (4 * i + (wave & 3)) * 512), off[i]);
   };
   auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, NK, NKW, kbuf(buf), tile); };
   auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, NV, NVW, vbuf(buf), tile); };
@@ -338,52 +380,58 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   // one phase later.  Each wave runs its own M(0) X(0) M(1) X(1) ... with a
   // barrier before every phase; B waits out phase 0 first, so barriers pair
   // up by count.  Copies are started only by the group in its softmax phase,
-  // never by the group issuing MFMAs: B starts K[t+2] (into K<t%2>) at the
-  // beginning of X(t), phase 2t+2, and A starts V[t] (into V<t%2>) at the
-  // beginning of X(t), phase 2t+1.  The barrier of every even phase waits
-  // for the issuing waves' copies, so K[t+1] and V[t] are complete for
-  // A's M(t+1) in phase 2t+2.  Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
+  // never by the group issuing MFMAs:
+  //   A starts V[t] (into V<t%2>, last read in phase 2t-1) at the start of
+  //     X(t), phase 2t+1, and waits for it before the barrier of phase 2t+2,
+  //     where M(t+1) first reads it;
+  //   B starts K[t+2] (into K<t%2>, last read in phase 2t+1) at the start of
+  //     X(t), phase 2t+2, and waits for it before the barrier of phase 2t+4,
+  //     where M(t+2) first reads it.
+  // Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
   if (n_tiles > 0) {
-    if (grp == 1) dma_k(0, Int<0>{});
-    if (grp == 1) {  // phase 0 for group B: start K[1], no softmax
-      __syncthreads();
+    if (grp == 1) {  // K[0] before phase 0, K[1] during it (B has no softmax yet)
+      dma_k(0, Int<0>{});
+      wait_copies();
+      lds_barrier();
       if (1 < n_tiles) dma_k(1, Int<1>{});
     } else {
-      __syncthreads();
+      lds_barrier();
     }
     for (int t = 0; t <= n_tiles; t += 2) {
-      // ---- M(t), t even
+      // ---- M(t), t even (A: phase 0's barrier was the one above)
       if (grp == 0) {
-        if (t > 0) __syncthreads();  // phase 0's barrier was the one above
+        if (t > 0) {
+          wait_copies();  // V[t-1] (started in X(t-1)) is read from this phase on
+          lds_barrier();
+        }
       } else {
-        __builtin_amdgcn_s_barrier();
+        lds_barrier();
       }
       mstep(t, Int<0>{});
       if (t == n_tiles && grp == 1) break;  // B's last phase was M(n_tiles)
       // ---- X(t)
       if (grp == 0) {
-        __builtin_amdgcn_s_barrier();
+        lds_barrier();
         if (t < n_tiles) dma_v(t, Int<0>{});
       } else {
-        __syncthreads();
+        wait_copies();  // K[t+1] (started in X(t-1)) is read from this phase on
+        lds_barrier();
         if (t + 2 < n_tiles) dma_k(t + 2, Int<0>{});
       }
       xstep(t);
       if (t == n_tiles) break;
       // ---- M(t+1), t+1 odd
-      if (grp == 0) {
-        __syncthreads();
-      } else {
-        __builtin_amdgcn_s_barrier();
-      }
+      if (grp == 0) wait_copies();  // V[t]
+      lds_barrier();
       mstep(t + 1, Int<1>{});
       if (t + 1 == n_tiles && grp == 1) break;
       // ---- X(t+1)
       if (grp == 0) {
-        __builtin_amdgcn_s_barrier();
+        lds_barrier();
         if (t + 1 < n_tiles) dma_v(t + 1, Int<1>{});
       } else {
-        __syncthreads();
+        wait_copies();  // K[t+2]
+        lds_barrier();
         if (t + 3 < n_tiles) dma_k(t + 3, Int<1>{});
       }
       xstep(t + 1);
