@@ -334,12 +334,11 @@ __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restri
   }
 }
 
-// LayerNorm for bf16 rows of at most 4096 elements: the row stays packed in
-// registers (8 bf16 per 16-byte vector, 32 registers for 4096 columns) and
-// each pass widens its own copy.  The three passes spell the bf16 -> fp32
-// widening differently (shift, byte permute, funnel shift) so the compiler
-// cannot merge them into one widened copy of the row kept across the passes:
-// fewer registers, more rows in flight.  Statistics as layernorm_reg_kernel.
+// bf16 -> fp32 widening of the low / high half of a packed word, spelled
+// three ways (shift, byte permute, funnel shift).  The LayerNorm passes each
+// use their own spelling, so the compiler cannot merge them into one widened
+// copy of the row kept live across the passes: the row stays packed (8 bf16
+// per 16-byte vector), fewer registers, more rows in flight.
 __device__ inline float lo_a(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float hi_a(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
 __device__ inline float lo_b(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_perm(w, 0u, 0x05040C0Cu)); }
@@ -347,44 +346,71 @@ __device__ inline float hi_b(uint32_t w) { return __builtin_bit_cast(float, __bu
 __device__ inline float lo_c(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_alignbit(w, 0u, 16u)); }
 __device__ inline float hi_c(uint32_t w) { return __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, w, 0x03020C0Cu)); }
 
-__global__ __launch_bounds__(kBlock) void layernorm_bf16_packed_kernel(
+// LayerNorm for bf16 rows split over WPR waves of a 256-thread workgroup
+// (4 / WPR rows per workgroup): lane t of the row's WPR*64 lanes holds the
+// 16-byte vectors t, t + 64 WPR, ... (KV of them), so a row of 4096 needs
+// 8 / WPR registers' worth of vectors per lane and many more waves fit on a
+// CU than with a whole row per wave.  The two row sums are combined across
+// the row's waves through LDS; mean and variance are two-pass as in
+// layernorm_reg_kernel.  Rows past the end still take part in the barriers.
+template <int WPR, int KV>
+__global__ __launch_bounds__(kBlock) void layernorm_bf16_split_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
     int64_t rows, int cols, float eps, uint16_t* __restrict__ y) {
-  constexpr int KV = kLnMaxVecs;
+  constexpr int RPB = kWavesPerBlock / WPR;  // rows per workgroup
+  __shared__ float red[2][kWavesPerBlock];
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int wave = threadIdx.x >> 6;
+  const int rloc = wave / WPR, part = wave % WPR;
+  const int64_t row = int64_t(blockIdx.x) * RPB + rloc;
+  const bool live = row < rows;
   const int nv = cols / 8;
-  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + row * cols);
+  const int t0 = part * kWave + lane;
+  constexpr int kStride = WPR * kWave;
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(x + (live ? row : 0) * cols);
   u32x4_t v[KV];
 #pragma unroll
   for (int k = 0; k < KV; ++k)
-    if (lane + k * kWave < nv) v[k] = xv[lane + k * kWave];
+    if (live && t0 + k * kStride < nv) v[k] = xv[t0 + k * kStride];
   const float inv_n = 1.f / float(cols);
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < KV; ++k)
-    if (lane + k * kWave < nv)
+    if (live && t0 + k * kStride < nv)
 #pragma unroll
       for (int j = 0; j < 4; ++j) s += lo_a(v[k][j]) + hi_a(v[k][j]);
-  const float mean = wave_sum(s) * inv_n;
+  s = wave_sum(s);
+  if constexpr (WPR > 1) {
+    if (lane == 0) red[0][wave] = s;
+    __syncthreads();
+    s = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) s += red[0][rloc * WPR + w];
+  }
+  const float mean = s * inv_n;
   float q = 0.f;
 #pragma unroll
   for (int k = 0; k < KV; ++k)
-    if (lane + k * kWave < nv)
+    if (live && t0 + k * kStride < nv)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float d0 = lo_b(v[k][j]) - mean, d1 = hi_b(v[k][j]) - mean;
         q += d0 * d0 + d1 * d1;
       }
-  const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + eps);
+  q = wave_sum(q);
+  if constexpr (WPR > 1) {
+    if (lane == 0) red[1][wave] = q;
+    __syncthreads();
+    q = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) q += red[1][rloc * WPR + w];
+  }
+  if (!live) return;
+  const float rstd = 1.f / sqrtf(q * inv_n + eps);
   u32x4_t* yv = reinterpret_cast<u32x4_t*>(y + row * cols);
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
-    const int i = lane + k * kWave;
-    // gamma / beta of two vectors at a time: the loads are not hoisted
-    // into one block of 64 registers
-    if (k % 2 == 0) asm volatile("" ::: "memory");
+    const int i = t0 + k * kStride;
     if (i < nv) {
       const u32x4_t one4 = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
       const u32x4_t gk = gamma ? reinterpret_cast<const u32x4_t*>(gamma)[i] : one4;
@@ -564,8 +590,17 @@ extern "C" int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t col
   if (io_type == MK_BF16) {
     using T = uint16_t;
     const T *xp = (const T*)x, *gp = (const T*)gamma, *bp = (const T*)beta;
-    if (vec_ok(8))
-      hipLaunchKernelGGL(layernorm_bf16_packed_kernel, g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
+    // rows of up to 4096 / 8192 / 16384 stay in registers over 1 / 2 / 4 waves
+    const bool vec = cols % 8 == 0 && cols <= 16384 && rows < (int64_t(1) << 31) && aligned16(x) &&
+                     aligned16(y) && (!gamma || aligned16(gamma)) && (!beta || aligned16(beta));
+    if (vec && cols <= 4096)
+      hipLaunchKernelGGL((layernorm_bf16_split_kernel<1, 8>), g, b, 0, s, xp, gp, bp, rows, int(cols), eps, (T*)y);
+    else if (vec && cols <= 8192)
+      hipLaunchKernelGGL((layernorm_bf16_split_kernel<2, 8>), dim3(unsigned((rows + 1) / 2)), b, 0, s, xp, gp,
+                         bp, rows, int(cols), eps, (T*)y);
+    else if (vec && cols <= 16384)
+      hipLaunchKernelGGL((layernorm_bf16_split_kernel<4, 8>), dim3(unsigned(rows)), b, 0, s, xp, gp, bp, rows,
+                         int(cols), eps, (T*)y);
     else
       hipLaunchKernelGGL(layernorm_loop_kernel<T>, g, b, 0, s, xp, gp, bp, rows, cols, eps, (T*)y);
   } else if (io_type == MK_F32) {

@@ -169,7 +169,7 @@ def test_layernorm_c2_full(K):
         _bf16_close(y[sl], ops.layernorm(x[sl], g, b, 1e-5), _ln_scale(x[sl], g, b))
 
 
-@pytest.mark.parametrize("cols", [1, 100, 768, 4096, 4104, 6000])
+@pytest.mark.parametrize("cols", [1, 100, 768, 4096, 4104, 6000, 12288, 16384, 16392])
 def test_layernorm_widths_f32_bf16(K, cols):
     rng = np.random.default_rng(cols)
     x = (rng.standard_normal((19, cols)) * 3 + 1).astype(np.float32)
@@ -321,15 +321,17 @@ def test_sdpa_large_scores_rescale(K, causal):
     and between raises p reaches up to 2^8 against a stale max."""
     print(f"case: sdpa large scores causal={causal}", flush=True)
     _sdpa_case(K, 1, 2, 1024, 128, causal, seed=21, qk_std=1.0)
-    _sdpa_case(K, 1, 2, 700, 64, causal, seed=22, qk_std=0.5, k_ramp=8)
-    _sdpa_case(K, 1, 2, 700, 64, causal, seed=23, qk_std=0.5, k_ramp=32)
+    for D in (64, 128):
+        _sdpa_case(K, 1, 2, 700, D, causal, seed=22, qk_std=0.5, k_ramp=8)
+        _sdpa_case(K, 1, 2, 700, D, causal, seed=23, qk_std=0.5, k_ramp=32)
 
 
-def test_sdpa_strided_views(K):
+@pytest.mark.parametrize("D", [64, 128])
+def test_sdpa_strided_views(K, D):
     """[B, S, H, D] storage (the layout a head split produces) passed as a
     permuted view: no copy, strides folded into addressing."""
     rng = np.random.default_rng(9)
-    B, S, H, D = 2, 200, 4, 64
+    B, S, H = 2, 200, 4
     x = [bf16.to_bf16_bits((rng.standard_normal((B, S, H, D)) / 8).astype(np.float32)) for _ in range(3)]
     q, k, v = (dev_bf16(a).permute(0, 2, 1, 3) for a in x)
     o = host_bf16(K.sdpa_fwd(q, k, v, 0.125, True))
