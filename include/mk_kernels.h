@@ -252,6 +252,86 @@ int mk_convert(void* stream, int in_type, int out_type, int64_t n, const void* i
  * (a kernel, so it is safe inside captured HIP graphs). */
 int mk_fill(void* stream, int elem_bytes, int64_t n, uint64_t pattern, void* out);
 
+/* ========================================================================
+ * Backward and optimizer kernels of the one-GPU training step (config C5:
+ * the jitted value_and_grad + Adam step of temp/dp_train.py:67-76 on a
+ * GPT-2-small decoder).  In the reference these ops reach MPSGraph through
+ * the same handlers as the forward (dot_general linalg.mm:47-105, reduce
+ * reduce.mm:79-108, elementwise elementwise.mm:91-171, scatter
+ * gather_scatter.mm:262-335) applied to the StableHLO that jax.grad emits;
+ * here each backward composition is one entry point.
+ * ====================================================================== */
+
+/* dx = dy * gelu_tanh'(x), gelu_tanh as mk_gelu_tanh; fp32 math, one rounding
+ * on store.  io_type ∈ {MK_BF16, MK_F32}.  dx may alias dy. */
+int mk_gelu_tanh_bwd(void* stream, int io_type, int64_t n, const void* x, const void* dy, void* dx);
+
+/* y[c] = sum_r x[r, c] (fp32 out, fp32 accumulation) — bias gradients, the
+ * reduce over the batch axis that jax.grad emits for a broadcast bias add
+ * (reduce.mm:97-106 over axis 0).  Deterministic: per-block partial rows in
+ * the workspace, then added in block order.  in_type ∈ {MK_BF16, MK_F32}. */
+size_t mk_col_sum_workspace_bytes(int64_t rows, int64_t cols);
+int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols, const void* x, float* y,
+               void* workspace);
+
+/* LayerNorm backward for y = (x - mean) rstd gamma + beta over rows of `cols`
+ * (mean / rstd recomputed from x as mk_layernorm computes them):
+ *   dx = rstd (g - mean(g) - xh mean(g xh)),  g = dy gamma, xh = (x - mean) rstd
+ *   dgamma = sum_rows dy xh,  dbeta = sum_rows dy   (fp32, deterministic)
+ * io_type ∈ {MK_BF16, MK_F32} for x, gamma, dy, dx; cols ≤ 2048; gamma may be
+ * NULL (1); dgamma / dbeta both NULL skips them (then no workspace needed). */
+size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                     const void* gamma, const void* dy, float eps, void* dx, float* dgamma,
+                     float* dbeta, void* workspace);
+
+/* Softmax cross-entropy over rows of logits, loss and gradient together:
+ *   lse_r = log sum_j exp(x[r, j]);  loss_rows[r] = lse_r - x[r, labels[r]]
+ *   dlogits[r, j] = (exp(x[r, j] - lse_r) - [j == labels[r]]) * grad_scale
+ * (grad_scale = 1/rows gives the gradient of the mean loss, as
+ * optax.softmax_cross_entropy_with_integer_labels(...).mean() under jax.grad).
+ * io_type ∈ {MK_BF16, MK_F32} for logits / dlogits (dlogits may alias logits);
+ * label_type ∈ {MK_S32, MK_S64}; a label outside [0, cols) gives loss NaN
+ * and no target term.  loss_rows (fp32 [rows]) may be NULL. */
+int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,
+                    int label_type, const void* labels, float grad_scale, float* loss_rows,
+                    void* dlogits);
+
+/* One Adam step, the update of temp/dp_train.py:71-75:
+ *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
+ *   p = p - lr (m / bc1) / (sqrt(v / bc2) + eps)       (bc1 = 1-b1^t, bc2 = 1-b2^t)
+ * computed in fp32; the hyperparameters come in as doubles and b1, 1-b1, b2,
+ * 1-b2, eps, lr, bc1, bc2 are each rounded once to fp32 (how JAX folds the
+ * Python-float constants of that loop).  With `master` (fp32) the update runs
+ * on the master copy and the bf16 param receives its RNE rounding
+ * (param_type MK_BF16); with master NULL the param is fp32 and updated in
+ * place.  grad_type ∈ {MK_F32, MK_BF16}; m, v fp32; all arrays n elements. */
+int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type,
+                   const void* grad, float* m, float* v, double lr, double b1, double b2, double eps,
+                   double bc1, double bc2);
+
+/* Attention backward for O = softmax(scale Q Kᵀ [causal]) V (mk_sdpa_fwd's
+ * convention, lse from its forward): with P = exp(scale S - lse) (0 where
+ * masked), D_r = dO_r · O_r and dS = scale P (dO Vᵀ - D):
+ *   dV = Pᵀ dO,  dQ = dS K,  dK = dSᵀ Q     (bf16 out, fp32 accumulation)
+ * — the transposed dot_generals, select and reduce that jax.grad emits for
+ * the attention pattern.  S, dP (fp32) and P, dS (bf16) are materialised per
+ * (b, h) in the workspace of mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk); the
+ * products run on mk_gemm.  Strides as mk_sdpa_fwd (elements, D contiguous);
+ * o and dout rows 16-byte aligned; D a multiple of 8, ≤ 256. */
+size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
+int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
+                const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,
+                const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ss,
+                const void* o, int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                const void* dout, int64_t do_bs, int64_t do_hs, int64_t do_ss,
+                const float* lse,
+                void* dq, int64_t dq_bs, int64_t dq_hs, int64_t dq_ss,
+                void* dk, int64_t dk_bs, int64_t dk_hs, int64_t dk_ss,
+                void* dv, int64_t dv_bs, int64_t dv_hs, int64_t dv_ss,
+                float scale, int causal, void* workspace);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,17 @@ SIGNATURES = {
     "mk_softmax_rows": (_I, [_P, _I, _I64, _I64, _P, _P]),
     "mk_convert": (_I, [_P, _I, _I, _I64, _P, _P]),
     "mk_fill": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
+    "mk_gelu_tanh_bwd": (_I, [_P, _I, _I64, _P, _P, _P]),
+    "mk_col_sum_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "mk_col_sum": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
+    "mk_layernorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "mk_layernorm_bwd": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _F, _P, _P, _P, _P]),
+    "mk_softmax_xent": (_I, [_P, _I, _I64, _I64, _P, _I, _P, _F, _P, _P]),
+    "mk_adam_update": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P] + [ctypes.c_double] * 6),
+    "mk_sdpa_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64]),
+    "mk_sdpa_bwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64]
+                    + [_P, _I64, _I64, _I64] * 5 + [_P]
+                    + [_P, _I64, _I64, _I64] * 3 + [_F, _I, _P]),
 }
 
 _kernels = None

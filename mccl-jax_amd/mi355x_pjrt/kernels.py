@@ -266,3 +266,94 @@ def scatter_add_rows(table, ids, updates, out=None, workspace=None, stream=None)
                                    _ptr(updates.contiguous()), _ptr(out), _ptr(workspace))
     _check(rc, "mk_scatter_add_rows")
     return out
+
+
+# ------------------------------------------------------------------ C5 training step
+def _ws(nbytes, device, workspace):
+    if workspace is None:
+        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    if workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError("workspace too small")
+    return workspace
+
+
+def gelu_tanh_bwd(x, dy, out=None, stream=None):
+    """dx = dy * gelu_tanh'(x) (same dtype as x; out may be dy)."""
+    _require_cuda(x, dy)
+    out = torch.empty_like(x) if out is None else out
+    rc = lib().mk_gelu_tanh_bwd(_stream(stream), mk_dtype(x.dtype), x.numel(), _ptr(x), _ptr(dy), _ptr(out))
+    _check(rc, "mk_gelu_tanh_bwd")
+    return out
+
+
+def col_sum(x, out=None, workspace=None, stream=None):
+    """fp32 column sums of a 2-D (rows, cols) contiguous tensor."""
+    _require_cuda(x)
+    rows, cols = x.shape
+    out = torch.empty(cols, dtype=torch.float32, device=x.device) if out is None else out
+    ws = _ws(lib().mk_col_sum_workspace_bytes(rows, cols), x.device, workspace)
+    rc = lib().mk_col_sum(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(out), _ptr(ws))
+    _check(rc, "mk_col_sum")
+    return out
+
+
+def layernorm_bwd(x, gamma, dy, eps=1e-5, dx=None, dgamma=None, dbeta=None, workspace=None, want_params=True,
+                  stream=None):
+    """(dx, dgamma, dbeta) of LayerNorm over the last axis (fp32 dgamma/dbeta)."""
+    _require_cuda(x, dy)
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    dx = torch.empty_like(x) if dx is None else dx
+    if want_params:
+        dgamma = torch.empty(cols, dtype=torch.float32, device=x.device) if dgamma is None else dgamma
+        dbeta = torch.empty(cols, dtype=torch.float32, device=x.device) if dbeta is None else dbeta
+    ws = _ws(lib().mk_layernorm_bwd_workspace_bytes(rows, cols), x.device, workspace)
+    rc = lib().mk_layernorm_bwd(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(gamma), _ptr(dy),
+                                float(eps), _ptr(dx), _ptr(dgamma if want_params else None),
+                                _ptr(dbeta if want_params else None), _ptr(ws))
+    _check(rc, "mk_layernorm_bwd")
+    return dx, dgamma, dbeta
+
+
+def softmax_xent(logits, labels, grad_scale, loss_rows=None, dlogits=None, stream=None):
+    """Per-row softmax cross-entropy loss (fp32) and the logit gradient
+    (dlogits may be logits itself)."""
+    _require_cuda(logits, labels)
+    cols = logits.shape[-1]
+    rows = logits.numel() // cols
+    loss_rows = torch.empty(rows, dtype=torch.float32, device=logits.device) if loss_rows is None else loss_rows
+    dlogits = torch.empty_like(logits) if dlogits is None else dlogits
+    rc = lib().mk_softmax_xent(_stream(stream), mk_dtype(logits.dtype), rows, cols, _ptr(logits),
+                               mk_dtype(labels.dtype), _ptr(labels), float(grad_scale), _ptr(loss_rows),
+                               _ptr(dlogits))
+    _check(rc, "mk_softmax_xent")
+    return loss_rows, dlogits
+
+
+def adam_update(param, grad, m, v, lr, b1, b2, eps, bc1, bc2, master=None, stream=None):
+    """One Adam step in place (temp/dp_train.py:71-75 semantics)."""
+    rc = lib().mk_adam_update(_stream(stream), param.numel(), mk_dtype(param.dtype), _ptr(param), _ptr(master),
+                              mk_dtype(grad.dtype), _ptr(grad), _ptr(m), _ptr(v), float(lr), float(b1),
+                              float(b2), float(eps), float(bc1), float(bc2))
+    _check(rc, "mk_adam_update")
+
+
+def sdpa_bwd(q, k, v, o, dout, lse, scale, causal=True, dq=None, dk=None, dv=None, workspace=None, stream=None):
+    """(dq, dk, dv) of mk_sdpa_fwd on [B, H, S, D] bf16 views."""
+    _require_cuda(q, k, v, o, dout, lse)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    ws = _ws(lib().mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk), q.device, workspace)
+    args = [_stream(stream), B, H, Sq, Sk, D]
+    for t in (q, k, v, o, dout):
+        args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+    args += [_ptr(lse)]
+    for t in (dq, dk, dv):
+        args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+    args += [float(scale), int(bool(causal)), _ptr(ws)]
+    rc = lib().mk_sdpa_bwd(*args)
+    _check(rc, "mk_sdpa_bwd")
+    return dq, dk, dv

@@ -1,0 +1,568 @@
+// Backward and optimizer kernels of the one-GPU training step (config C5,
+// a GPT-2-small decoder): LayerNorm and GELU(tanh) backward, column sums
+// (bias gradients), fused softmax cross-entropy (loss and logit gradient in
+// one pass pair), attention backward and the Adam update of the reference's
+// training loop.
+//
+// Every reduction here is deterministic: column sums go through per-block
+// partial rows in a workspace and a second pass that adds the partials in
+// block order, so the same inputs give the same bits on every run.
+#include "mk_common.h"
+
+#include <cmath>
+
+namespace mk {
+namespace {
+
+constexpr int kBlock = 256;
+
+typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ inline float lo16(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ inline float hi16(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+__device__ inline uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+template <typename T> __device__ inline float ldf(const T* p, int64_t i);
+template <> __device__ inline float ldf<float>(const float* p, int64_t i) { return p[i]; }
+template <> __device__ inline float ldf<uint16_t>(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+template <typename T> __device__ inline void stf(T* p, int64_t i, float v);
+template <> __device__ inline void stf<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <> __device__ inline void stf<uint16_t>(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+
+inline int64_t align256(int64_t n) { return (n + 255) & ~int64_t(255); }
+
+// ---------------------------------------------------------------- GELU bwd
+// gelu(x) = x * s, s = 1 / (1 + exp(-2u)), u = c (x + k x^3) (the forward's
+// form); gelu'(x) = s + x s (1 - s) 2c (1 + 3k x^2).
+__device__ inline float gelu_tanh_grad_f32(float x) {
+  constexpr float kC = 0.7978845608028654f, kK = 0.044715f;
+  constexpr float kC0 = -2.0f * kC * 1.4426950408889634f;
+  const float x2 = x * x;
+  const float e = exp2f(x * fmaf(x2, kC0 * kK, kC0));
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  return s * fmaf(x * (1.0f - s), (2.0f * kC) * fmaf(3.0f * kK, x2, 1.0f), 1.0f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gelu_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                        T* __restrict__ dx, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+    stf<T>(dx, i, ldf<T>(dy, i) * gelu_tanh_grad_f32(ldf<T>(x, i)));
+}
+
+// bf16, 8 elements per thread per trip
+__global__ __launch_bounds__(kBlock) void gelu_bwd_bf16x8_kernel(const u32x4_t* __restrict__ x,
+                                                                const u32x4_t* __restrict__ dy,
+                                                                u32x4_t* __restrict__ dx, int64_t nvec) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
+    const u32x4_t a = x[i], d = dy[i];
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16(lo16(d[j]) * gelu_tanh_grad_f32(lo16(a[j])), hi16(d[j]) * gelu_tanh_grad_f32(hi16(a[j])));
+    dx[i] = o;
+  }
+}
+
+// ---------------------------------------------------------------- column sums
+// Pass 1: block b sums rows [b*rpb, (b+1)*rpb) of every column into its
+// partial row; thread t owns columns t, t + 256, ... and adds its rows in
+// order.  Pass 2: y[c] = sum over blocks, in block order.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void col_partial_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                           int64_t rpb, float* __restrict__ part) {
+  const int64_t r0 = int64_t(blockIdx.x) * rpb, r1 = min(rows, r0 + rpb);
+  for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
+    float acc = 0.f;
+    for (int64_t r = r0; r < r1; ++r) acc += ldf<T>(x, r * cols + c);
+    part[int64_t(blockIdx.x) * cols + c] = acc;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void col_final_kernel(const float* __restrict__ part, int64_t nparts,
+                                                         int64_t cols, float* __restrict__ y) {
+  const int64_t c = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) acc += part[p * cols + c];
+  y[c] = acc;
+}
+
+inline int64_t col_parts(int64_t rows) { return std::min<int64_t>(512, std::max<int64_t>(1, (rows + 15) / 16)); }
+
+// ---------------------------------------------------------------- LayerNorm bwd
+// One wave per row (rows of up to 64 * 8 * KV columns held in registers as
+// fp32); the row's mean / rstd are recomputed from x exactly as the forward
+// computes them (two-pass).  With xh = (x - mean) rstd and g = dy * gamma:
+//   dx = rstd (g - mean(g) - xh mean(g xh)),
+// and the wave adds dy * xh and dy into its lanes' dgamma / dbeta partials
+// over the rows it visits (rows w, w + W, ... for W waves in the grid), which
+// go to the workspace as one partial row per wave.
+template <typename T, int KV>
+__global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
+                                                             const T* __restrict__ dy, int64_t rows, int cols,
+                                                             float eps, T* __restrict__ dx,
+                                                             float* __restrict__ part_g, float* __restrict__ part_b) {
+  constexpr int NV = 8;  // columns per lane per vector step
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  const int64_t nwaves = int64_t(gridDim.x) * (kBlock / 64);
+  const float inv_n = 1.f / float(cols);
+  float gam[KV][NV], accg[KV][NV], accb[KV][NV];
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (k * 64 + lane) * NV + j;
+      gam[k][j] = (c < cols) ? (gamma ? ldf<T>(gamma, c) : 1.f) : 0.f;
+      accg[k][j] = 0.f;
+      accb[k][j] = 0.f;
+    }
+  for (int64_t r = wave; r < rows; r += nwaves) {
+    const T* xr = x + r * cols;
+    const T* dr = dy + r * cols;
+    float xv[KV][NV], dv[KV][NV];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        xv[k][j] = (c < cols) ? ldf<T>(xr, c) : 0.f;
+        dv[k][j] = (c < cols) ? ldf<T>(dr, c) : 0.f;
+        s += xv[k][j];
+      }
+    const float mean = wave_sum(s) * inv_n;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        const float d = (c < cols) ? xv[k][j] - mean : 0.f;
+        q += d * d;
+      }
+    const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + eps);
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        const float xh = (c < cols) ? (xv[k][j] - mean) * rstd : 0.f;
+        const float g = dv[k][j] * gam[k][j];
+        sg += g;
+        sgx += g * xh;
+        accg[k][j] += dv[k][j] * xh;
+        accb[k][j] += dv[k][j];
+        xv[k][j] = xh;
+      }
+    const float mg = wave_sum(sg) * inv_n, mgx = wave_sum(sgx) * inv_n;
+    T* dxr = dx + r * cols;
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        if (c < cols) stf<T>(dxr, c, rstd * (dv[k][j] * gam[k][j] - mg - xv[k][j] * mgx));
+      }
+  }
+  if (part_g) {
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        if (c < cols) {
+          part_g[wave * cols + c] = accg[k][j];
+          part_b[wave * cols + c] = accb[k][j];
+        }
+      }
+  }
+}
+
+constexpr int64_t kLnBwdWaves = 2048;
+
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};  // partial rows (and waves) of the LayerNorm backward
+
+// ---------------------------------------------------------------- softmax xent
+// One workgroup per row.  Pass 1: running (max, sum of exp) per thread,
+// combined across the workgroup; lse = max + log(sum).  loss = lse - x[label].
+// Pass 2: dlogits = (exp(x - lse) - [j == label]) * grad_scale.
+template <typename T, typename L>
+__global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restrict__ logits, int64_t cols,
+                                                            const L* __restrict__ labels, float grad_scale,
+                                                            float* __restrict__ loss, T* __restrict__ dlogits) {
+  __shared__ float sm[kBlock / 64], ss[kBlock / 64];
+  const int64_t row = blockIdx.x;
+  const T* xr = logits + row * cols;
+  float m = -INFINITY, s = 0.f;
+  for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
+    const float v = ldf<T>(xr, j);
+    if (v > m) {
+      s = s * __expf(m - v) + 1.f;
+      m = v;
+    } else if (m != -INFINITY) {
+      s += __expf(v - m);
+    }
+  }
+  // combine (m, s) over the wave, then over the 4 waves
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float mo = __shfl_xor(m, off, 64), so = __shfl_xor(s, off, 64);
+    const float mn = fmaxf(m, mo);
+    s = (mn == -INFINITY) ? 0.f : s * __expf(m - mn) + so * __expf(mo - mn);
+    m = mn;
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) {
+    sm[wv] = m;
+    ss[wv] = s;
+  }
+  __syncthreads();
+  float M = sm[0];
+#pragma unroll
+  for (int w = 1; w < kBlock / 64; ++w) M = fmaxf(M, sm[w]);
+  float S = 0.f;
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) S += (sm[w] == -INFINITY) ? 0.f : ss[w] * __expf(sm[w] - M);
+  const float lse = M + __logf(S);
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  if (threadIdx.x == 0 && loss) loss[row] = lab_ok ? lse - ldf<T>(xr, lab) : __builtin_nanf("");
+  T* dr = dlogits + row * cols;
+  for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
+    const float p = __expf(ldf<T>(xr, j) - lse);
+    stf<T>(dr, j, (p - (j == lab ? 1.f : 0.f)) * grad_scale);
+  }
+}
+
+// ---------------------------------------------------------------- Adam
+// dp_train.py body(): m = b1 m + (1-b1) g; v = b2 v + (1-b2) g g;
+// p = p - lr (m / bc1) / (sqrt(v / bc2) + eps), in fp32 with the constants
+// b1, 1-b1, b2, 1-b2, eps each one fp32 rounding of the double value (as
+// JAX folds the Python-float expressions).  With a master copy the update
+// runs on the fp32 master and the bf16 parameter receives its RNE rounding;
+// without one the fp32 parameter is updated in place.
+template <typename G>
+__global__ __launch_bounds__(kBlock) void adam_kernel(int64_t n, float* __restrict__ p32, uint16_t* __restrict__ p16,
+                                                    const G* __restrict__ grad, float* __restrict__ m,
+                                                    float* __restrict__ v, float lr, float b1, float omb1, float b2,
+                                                    float omb2, float eps, float bc1, float bc2) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    const float g = ldf<G>(grad, i);
+    const float mi = b1 * m[i] + omb1 * g;
+    const float vi = b2 * v[i] + omb2 * g * g;
+    m[i] = mi;
+    v[i] = vi;
+    const float p = p32[i] - lr * (mi / bc1) / (sqrtf(vi / bc2) + eps);
+    p32[i] = p;
+    if (p16) p16[i] = f32_to_bf16(p);
+  }
+}
+
+// ---------------------------------------------------------------- attention bwd
+// D[r] = sum_d dO[r, d] O[r, d] for every query row r = (b, h, i)
+__global__ __launch_bounds__(kBlock) void attn_rowdot_kernel(const uint16_t* __restrict__ o, int64_t o_bs, int64_t o_hs,
+                                                           int64_t o_ss, const uint16_t* __restrict__ dout,
+                                                           int64_t d_bs, int64_t d_hs, int64_t d_ss, int64_t H,
+                                                           int64_t S, int64_t D, int64_t nrows,
+                                                           float* __restrict__ out) {
+  const int64_t r = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (r >= nrows) return;
+  const int64_t bh = r / S, i = r % S, b = bh / H, h = bh % H;
+  const uint16_t* orow = o + b * o_bs + h * o_hs + i * o_ss;
+  const uint16_t* drow = dout + b * d_bs + h * d_hs + i * d_ss;
+  float acc = 0.f;
+  for (int64_t d = 0; d < D; d += 8) {
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(orow + d);
+    const u32x4_t c = *reinterpret_cast<const u32x4_t*>(drow + d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += lo16(a[j]) * lo16(c[j]) + hi16(a[j]) * hi16(c[j]);
+  }
+  out[r] = acc;
+}
+
+// P[bh, i, j] = exp(scale * S[bh, i, j] - lse[bh, i]) (0 where masked), bf16
+__global__ __launch_bounds__(kBlock) void attn_probs_kernel(const float* __restrict__ s, const float* __restrict__ lse,
+                                                          int64_t Sq, int64_t Sk, float scale, int causal,
+                                                          uint16_t* __restrict__ p, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < n; e += stride) {
+    const int64_t j = e % Sk, row = e / Sk, i = row % Sq;
+    const float v = (causal && j > i) ? 0.f : __expf(scale * s[e] - lse[row]);
+    p[e] = f32_to_bf16(v);
+  }
+}
+
+// dS = scale * P * (dP - D[row]), bf16, written over P
+__global__ __launch_bounds__(kBlock) void attn_dscores_kernel(const float* __restrict__ dp, const float* __restrict__ dsum,
+                                                            int64_t Sk, float scale, uint16_t* __restrict__ p,
+                                                            int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < n; e += stride) {
+    const float pv = bf16_to_f32(p[e]);
+    p[e] = f32_to_bf16(scale * pv * (dp[e] - dsum[e / Sk]));
+  }
+}
+
+inline unsigned grid_for(int64_t n, int64_t per_block = kBlock) {
+  return unsigned(std::min<int64_t>((n + per_block - 1) / per_block, 65536));
+}
+
+}  // namespace
+}  // namespace mk
+
+using namespace mk;
+
+extern "C" int mk_gelu_tanh_bwd(void* stream, int io_type, int64_t n, const void* x, const void* dy, void* dx) {
+  clear_error();
+  if (n < 0) return fail(MK_ERR_INVALID, "mk_gelu_tanh_bwd: negative n");
+  if (n == 0) return MK_OK;
+  if (!x || !dy || !dx) return fail(MK_ERR_INVALID, "mk_gelu_tanh_bwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  if (io_type == MK_BF16) {
+    const bool vec = (n % 8) == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
+                                       reinterpret_cast<uintptr_t>(dx)) & 15) == 0;
+    if (vec)
+      hipLaunchKernelGGL(gelu_bwd_bf16x8_kernel, dim3(grid_for(n / 8)), dim3(kBlock), 0, s, (const u32x4_t*)x,
+                         (const u32x4_t*)dy, (u32x4_t*)dx, n / 8);
+    else
+      hipLaunchKernelGGL(gelu_bwd_kernel<uint16_t>, dim3(grid_for(n)), dim3(kBlock), 0, s, (const uint16_t*)x,
+                         (const uint16_t*)dy, (uint16_t*)dx, n);
+  } else if (io_type == MK_F32) {
+    hipLaunchKernelGGL(gelu_bwd_kernel<float>, dim3(grid_for(n)), dim3(kBlock), 0, s, (const float*)x,
+                       (const float*)dy, (float*)dx, n);
+  } else {
+    return fail(MK_ERR_UNSUPPORTED, "mk_gelu_tanh_bwd: io_type must be bf16/f32");
+  }
+  return check_launch("mk_gelu_tanh_bwd");
+}
+
+extern "C" size_t mk_col_sum_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return size_t(align256(col_parts(rows) * cols * 4));
+}
+
+extern "C" int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols, const void* x, float* y,
+                          void* workspace) {
+  clear_error();
+  if (rows < 0 || cols < 0) return fail(MK_ERR_INVALID, "mk_col_sum: negative shape");
+  if (cols == 0) return MK_OK;
+  if (!y) return fail(MK_ERR_INVALID, "mk_col_sum: null output");
+  hipStream_t s = as_stream(stream);
+  if (rows == 0) return mk_fill(stream, 4, cols, 0, y);
+  if (!x || !workspace) return fail(MK_ERR_INVALID, "mk_col_sum: null input or workspace");
+  const int64_t np = col_parts(rows), rpb = (rows + np - 1) / np;
+  float* part = static_cast<float*>(workspace);
+  if (in_type == MK_BF16)
+    hipLaunchKernelGGL(col_partial_kernel<uint16_t>, dim3(unsigned(np)), dim3(kBlock), 0, s, (const uint16_t*)x,
+                       rows, cols, rpb, part);
+  else if (in_type == MK_F32)
+    hipLaunchKernelGGL(col_partial_kernel<float>, dim3(unsigned(np)), dim3(kBlock), 0, s, (const float*)x, rows,
+                       cols, rpb, part);
+  else
+    return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: in_type must be bf16/f32");
+  hipLaunchKernelGGL(col_final_kernel, dim3(unsigned((cols + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, part, np,
+                     cols, y);
+  return check_launch("mk_col_sum");
+}
+
+extern "C" size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return size_t(2 * align256(kLnBwdWaves * cols * 4));
+}
+
+extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                                const void* gamma, const void* dy, float eps, void* dx, float* dgamma,
+                                float* dbeta, void* workspace) {
+  clear_error();
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_layernorm_bwd: bad shape");
+  if (cols > 64 * 8 * 4) return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: rows of at most 2048 columns");
+  if ((dgamma == nullptr) != (dbeta == nullptr))
+    return fail(MK_ERR_INVALID, "mk_layernorm_bwd: dgamma and dbeta are both given or both NULL");
+  if (rows == 0) {
+    if (dgamma) {
+      if (int rc = mk_fill(stream, 4, cols, 0, dgamma)) return rc;
+      return mk_fill(stream, 4, cols, 0, dbeta);
+    }
+    return MK_OK;
+  }
+  if (!x || !dy || !dx || (dgamma && !workspace)) return fail(MK_ERR_INVALID, "mk_layernorm_bwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  const int64_t waves = std::min<int64_t>(kLnBwdWaves, rows);
+  const unsigned blocks = unsigned((waves + 3) / 4);
+  const int64_t nparts = int64_t(blocks) * 4;  // every wave of the grid writes a partial row
+  float* pg = dgamma ? static_cast<float*>(workspace) : nullptr;
+  float* pb = dgamma ? reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(kLnBwdWaves * cols * 4))
+                     : nullptr;
+  const int kv = int((cols + 511) / 512);
+  auto launch = [&](auto tag, auto kvt) {
+    using T = decltype(tag);
+    constexpr int KV = decltype(kvt)::value;
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, KV>), dim3(blocks), dim3(kBlock), 0, s, (const T*)x,
+                       (const T*)gamma, (const T*)dy, rows, int(cols), eps, (T*)dx, pg, pb);
+  };
+  auto dispatch = [&](auto tag) {
+    if (kv == 1) launch(tag, IntC<1>{});
+    else if (kv == 2) launch(tag, IntC<2>{});
+    else launch(tag, IntC<4>{});
+  };
+  if (io_type == MK_BF16) dispatch(uint16_t{});
+  else if (io_type == MK_F32) dispatch(float{});
+  else return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: io_type must be bf16/f32");
+  if (dgamma) {
+    const dim3 g(unsigned((cols + kBlock - 1) / kBlock));
+    hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pg, nparts, cols, dgamma);
+    hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pb, nparts, cols, dbeta);
+  }
+  return check_launch("mk_layernorm_bwd");
+}
+
+extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,
+                               int label_type, const void* labels, float grad_scale, float* loss_rows,
+                               void* dlogits) {
+  clear_error();
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_softmax_xent: bad shape");
+  if (rows == 0) return MK_OK;
+  if (rows >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: too many rows");
+  if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent: null pointer");
+  hipStream_t s = as_stream(stream);
+  const dim3 g{unsigned(rows)}, b{unsigned(kBlock)};
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    if (label_type == MK_S32)
+      hipLaunchKernelGGL((softmax_xent_kernel<T, int32_t>), g, b, 0, s, (const T*)logits, cols,
+                         (const int32_t*)labels, grad_scale, loss_rows, (T*)dlogits);
+    else
+      hipLaunchKernelGGL((softmax_xent_kernel<T, int64_t>), g, b, 0, s, (const T*)logits, cols,
+                         (const int64_t*)labels, grad_scale, loss_rows, (T*)dlogits);
+  };
+  if (label_type != MK_S32 && label_type != MK_S64)
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: labels must be s32/s64");
+  if (io_type == MK_BF16) go(uint16_t{});
+  else if (io_type == MK_F32) go(float{});
+  else return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: io_type must be bf16/f32");
+  return check_launch("mk_softmax_xent");
+}
+
+extern "C" int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type,
+                              const void* grad, float* m, float* v, double lr, double b1, double b2, double eps,
+                              double bc1, double bc2) {
+  clear_error();
+  if (n < 0) return fail(MK_ERR_INVALID, "mk_adam_update: negative n");
+  if (n == 0) return MK_OK;
+  if (!param || !grad || !m || !v) return fail(MK_ERR_INVALID, "mk_adam_update: null pointer");
+  float* p32;
+  uint16_t* p16 = nullptr;
+  if (master) {
+    if (param_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_adam_update: a master copy needs a bf16 param");
+    p32 = master;
+    p16 = static_cast<uint16_t*>(param);
+  } else {
+    if (param_type != MK_F32) return fail(MK_ERR_UNSUPPORTED, "mk_adam_update: without a master copy the param is f32");
+    p32 = static_cast<float*>(param);
+  }
+  hipStream_t s = as_stream(stream);
+  const dim3 g(grid_for(n)), b(kBlock);
+  const float f_lr = float(lr), f_b1 = float(b1), f_omb1 = float(1.0 - b1), f_b2 = float(b2),
+              f_omb2 = float(1.0 - b2), f_eps = float(eps), f_bc1 = float(bc1), f_bc2 = float(bc2);
+  if (grad_type == MK_F32)
+    hipLaunchKernelGGL(adam_kernel<float>, g, b, 0, s, n, p32, p16, (const float*)grad, m, v, f_lr, f_b1, f_omb1,
+                       f_b2, f_omb2, f_eps, f_bc1, f_bc2);
+  else if (grad_type == MK_BF16)
+    hipLaunchKernelGGL(adam_kernel<uint16_t>, g, b, 0, s, n, p32, p16, (const uint16_t*)grad, m, v, f_lr, f_b1,
+                       f_omb1, f_b2, f_omb2, f_eps, f_bc1, f_bc2);
+  else
+    return fail(MK_ERR_UNSUPPORTED, "mk_adam_update: grad_type must be bf16/f32");
+  return check_launch("mk_adam_update");
+}
+
+extern "C" size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0) return 0;
+  const int64_t n = B * H * Sq * Sk;
+  return size_t(align256(n * 4) + align256(n * 2) + align256(B * H * Sq * 4));
+}
+
+extern "C" int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                           const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
+                           const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,
+                           const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ss,
+                           const void* o, int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                           const void* dout, int64_t do_bs, int64_t do_hs, int64_t do_ss,
+                           const float* lse,
+                           void* dq, int64_t dq_bs, int64_t dq_hs, int64_t dq_ss,
+                           void* dk, int64_t dk_bs, int64_t dk_hs, int64_t dk_ss,
+                           void* dv, int64_t dv_bs, int64_t dv_hs, int64_t dv_ss,
+                           float scale, int causal, void* workspace) {
+  clear_error();
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return fail(MK_ERR_INVALID, "mk_sdpa_bwd: negative shape");
+  if (D <= 0 || D % 8 != 0 || D > 256) return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: head_dim must be a multiple of 8, <= 256");
+  if (B == 0 || H == 0 || Sq == 0 || Sk == 0) return MK_OK;
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !workspace)
+    return fail(MK_ERR_INVALID, "mk_sdpa_bwd: null pointer");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(dout);
+  if ((al & 15) != 0 || ((o_bs | o_hs | o_ss | do_bs | do_hs | do_ss) & 7) != 0)
+    return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: o and dO rows must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const int64_t n = B * H * Sq * Sk;
+  float* F = static_cast<float*>(workspace);  // scores, then dP
+  uint16_t* P = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + align256(n * 4));  // P, then dS
+  float* Dsum = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(n * 4) + align256(n * 2));
+  const int64_t nrows = B * H * Sq;
+  hipLaunchKernelGGL(attn_rowdot_kernel, dim3(unsigned((nrows + kBlock - 1) / kBlock)), dim3(kBlock), 0, s,
+                     (const uint16_t*)o, o_bs, o_hs, o_ss, (const uint16_t*)dout, do_bs, do_hs, do_ss, H, Sq, D,
+                     nrows, Dsum);
+  if (int rc = check_launch("mk_sdpa_bwd")) return rc;
+  const int64_t SS = Sq * Sk;
+  // per batch index: H heads as one batched GEMM (head stride), S / dP rows of Sk
+  for (int64_t b = 0; b < B; ++b) {
+    const uint16_t* qb = static_cast<const uint16_t*>(q) + b * q_bs;
+    const uint16_t* kb = static_cast<const uint16_t*>(k) + b * k_bs;
+    float* Fb = F + b * H * SS;
+    // S = Q Kᵀ  [Sq x Sk], fp32
+    if (int rc = mk_gemm(stream, MK_BF16, MK_F32, H, Sq, Sk, D, qb, q_hs, q_ss, 1, kb, k_hs, 1, k_ss, Fb, SS, Sk,
+                         nullptr, 0))
+      return rc;
+  }
+  hipLaunchKernelGGL(attn_probs_kernel, dim3(grid_for(n)), dim3(kBlock), 0, s, F, lse, Sq, Sk, scale, causal, P, n);
+  if (int rc = check_launch("mk_sdpa_bwd")) return rc;
+  for (int64_t b = 0; b < B; ++b) {
+    const uint16_t* db = static_cast<const uint16_t*>(dout) + b * do_bs;
+    const uint16_t* vb = static_cast<const uint16_t*>(v) + b * v_bs;
+    const uint16_t* Pb = P + b * H * SS;
+    float* Fb = F + b * H * SS;
+    // dV = Pᵀ dO  [Sk x D]
+    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, db, do_hs, do_ss, 1,
+                         static_cast<uint16_t*>(dv) + b * dv_bs, dv_hs, dv_ss, nullptr, 0))
+      return rc;
+    // dP = dO Vᵀ  [Sq x Sk], fp32 (over the scores)
+    if (int rc = mk_gemm(stream, MK_BF16, MK_F32, H, Sq, Sk, D, db, do_hs, do_ss, 1, vb, v_hs, 1, v_ss, Fb, SS, Sk,
+                         nullptr, 0))
+      return rc;
+  }
+  hipLaunchKernelGGL(attn_dscores_kernel, dim3(grid_for(n)), dim3(kBlock), 0, s, F, Dsum, Sk, scale, P, n);
+  if (int rc = check_launch("mk_sdpa_bwd")) return rc;
+  for (int64_t b = 0; b < B; ++b) {
+    const uint16_t* qb = static_cast<const uint16_t*>(q) + b * q_bs;
+    const uint16_t* kb = static_cast<const uint16_t*>(k) + b * k_bs;
+    const uint16_t* Pb = P + b * H * SS;
+    // dQ = dS K  [Sq x D]
+    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sq, D, Sk, Pb, SS, Sk, 1, kb, k_hs, k_ss, 1,
+                         static_cast<uint16_t*>(dq) + b * dq_bs, dq_hs, dq_ss, nullptr, 0))
+      return rc;
+    // dK = dSᵀ Q  [Sk x D]
+    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, qb, q_hs, q_ss, 1,
+                         static_cast<uint16_t*>(dk) + b * dk_bs, dk_hs, dk_ss, nullptr, 0))
+      return rc;
+  }
+  return MK_OK;
+}

@@ -1,0 +1,231 @@
+"""Backward and optimizer kernels of the C5 training step through the C-ABI,
+against torch float64 autograd on the CPU (the gradient the jitted
+value_and_grad of temp/dp_train.py:67-76 computes, in exact arithmetic).
+
+Float tolerances: fp32 I/O paths are held to fp32 rounding of the fp64
+result (relative to the scale of the quantity); bf16 paths to bf16 rounding
+(2^-8 relative) plus the fp32 accumulation terms."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K(cuda):
+    from mi355x_pjrt import kernels
+
+    kernels.lib()
+    return kernels
+
+
+def _f64(t):
+    return t.detach().to("cpu", torch.float64)
+
+
+def _rel(got, want):
+    got, want = _f64(got), _f64(want)
+    return float((got - want).norm() / max(float(want.norm()), 1e-30))
+
+
+# ------------------------------------------------------------------ GELU backward
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gelu_tanh_bwd(K, dtype):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4099, generator=g) * 3
+    x[:8] = torch.tensor([0.0, -0.0, 10.0, -10.0, 30.0, -30.0, 1e-20, -1e-3])
+    dy = torch.randn(4099, generator=g)
+    xd, dyd = x.to(dtype).cuda(), dy.to(dtype).cuda()
+    got = K.gelu_tanh_bwd(xd, dyd)
+    xr = _f64(xd).requires_grad_(True)
+    torch.nn.functional.gelu(xr, approximate="tanh").backward(_f64(dyd))
+    want = xr.grad
+    if dtype == torch.float32:
+        np.testing.assert_allclose(_f64(got), want, rtol=2e-5, atol=2e-6 * float(want.abs().max()))
+    else:
+        np.testing.assert_allclose(_f64(got), want, rtol=2 ** -7, atol=1e-6)
+    # the bf16 vector path (length a multiple of 8, aligned)
+    x8 = xd[:4096]
+    got8 = K.gelu_tanh_bwd(x8, dyd[:4096])
+    np.testing.assert_array_equal(_f64(got8), _f64(got[:4096]))
+
+
+# ------------------------------------------------------------------ column sums
+@pytest.mark.parametrize("rows,cols", [(1, 1), (19, 768), (8192, 768), (8, 786432), (1000, 257)])
+def test_col_sum(K, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(rows, cols, generator=g)
+    for dtype in (torch.float32, torch.bfloat16):
+        xd = x.to(dtype).cuda()
+        got = K.col_sum(xd)
+        want = _f64(xd).sum(0)
+        scale = _f64(xd).abs().sum(0)
+        assert float(((_f64(got) - want).abs() / (scale + 1e-30)).max()) < 1e-6
+    # deterministic: same bits twice
+    a, b = K.col_sum(xd), K.col_sum(xd)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ LayerNorm backward
+@pytest.mark.parametrize("cols", [1, 100, 768, 1000, 2048])
+def test_layernorm_bwd_f32(K, cols):
+    g = torch.Generator().manual_seed(cols)
+    rows = 37
+    x = torch.randn(rows, cols, generator=g) * 2 + 0.5
+    gamma = torch.randn(cols, generator=g)
+    beta = torch.randn(cols, generator=g)
+    dy = torch.randn(rows, cols, generator=g)
+    dx, dgam, dbet = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5)
+    xr = x.double().requires_grad_(True)
+    gr = gamma.double().requires_grad_(True)
+    br = beta.double().requires_grad_(True)
+    torch.nn.functional.layer_norm(xr, (cols,), gr, br, 1e-5).backward(dy.double())
+    # dx is rstd times an O(|dy gamma|) combination: fp32 rounding relative to
+    # that scale (a one-column row has dx = 0 exactly)
+    rstd = 1 / torch.sqrt(x.double().var(-1, unbiased=False, keepdim=True) + 1e-5)
+    scale = float((rstd * (dy.double() * gamma.double()).abs()).max())
+    assert float((_f64(dx) - xr.grad).abs().max()) < 5e-5 * scale
+    assert _rel(dgam, gr.grad) < 2e-5 or cols == 1
+    assert float((_f64(dgam) - gr.grad).abs().max()) < 1e-5 * float((dy.double() * (x.double() - x.double().mean(-1, keepdim=True)) * rstd).abs().sum(0).max() + 1)
+    assert _rel(dbet, br.grad) < 2e-6
+
+
+def test_layernorm_bwd_bf16_c5_rows(K):
+    g = torch.Generator().manual_seed(7)
+    rows, cols = 8192, 768
+    x = (torch.randn(rows, cols, generator=g) * 1.5).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16()
+    dy = torch.randn(rows, cols, generator=g).bfloat16()
+    dx, dgam, dbet = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5)
+    xr = x.double().requires_grad_(True)
+    gr = gamma.double().requires_grad_(True)
+    br = torch.zeros(cols, dtype=torch.float64, requires_grad=True)
+    torch.nn.functional.layer_norm(xr, (cols,), gr, br, 1e-5).backward(dy.double())
+    assert _rel(dx, xr.grad) < 6e-3  # bf16 output rounding
+    assert _rel(dgam, gr.grad) < 1e-5
+    assert _rel(dbet, br.grad) < 1e-6
+    # dx alone (no parameter gradients, no workspace needed)
+    dx2, _, _ = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5, want_params=False)
+    assert torch.equal(dx2, dx)
+
+
+# ------------------------------------------------------------------ softmax cross-entropy
+@pytest.mark.parametrize("rows,cols", [(64, 257), (5, 1), (3, 50257)])
+def test_softmax_xent_f32(K, rows, cols):
+    g = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=g) * 4
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int32)
+    loss, dl = K.softmax_xent(x.cuda(), lab.cuda(), 1.0 / rows)
+    xr = x.double().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xr, lab.long(), reduction="none")
+    ref.mean().backward()
+    np.testing.assert_allclose(_f64(loss), _f64(ref), rtol=1e-5, atol=1e-5)
+    assert _rel(dl, xr.grad) < 1e-5
+
+
+def test_softmax_xent_bf16_in_place(K):
+    g = torch.Generator().manual_seed(3)
+    rows, cols = 16, 50257
+    x = (torch.randn(rows, cols, generator=g) * 3).bfloat16()
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int64)
+    xd = x.cuda()
+    loss, dl = K.softmax_xent(xd, lab.cuda(), 1.0 / rows, dlogits=xd)
+    assert dl.data_ptr() == xd.data_ptr()
+    xr = x.double().requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xr, lab, reduction="none")
+    ref.mean().backward()
+    np.testing.assert_allclose(_f64(loss), _f64(ref), rtol=1e-5, atol=1e-5)
+    assert _rel(dl, xr.grad) < 4e-3
+
+
+# ------------------------------------------------------------------ Adam
+def _adam_ref(p, g, m, v, lr, b1, b2, eps, bc1, bc2):
+    m = b1 * m + (1 - b1) * g
+    v = b2 * v + (1 - b2) * g * g
+    return p - lr * (m / bc1) / (np.sqrt(v / bc2) + eps), m, v
+
+
+def test_adam_update_f32_and_master(K):
+    rng = np.random.default_rng(0)
+    n = 100003
+    p = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    m = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    v = np.abs(rng.standard_normal(n) * 0.01).astype(np.float32)
+    hp = dict(lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, bc1=1 - 0.9 ** 3, bc2=1 - 0.999 ** 3)
+    wp, wm, wv = _adam_ref(p.astype(np.float64), g.astype(np.float64), m.astype(np.float64),
+                           v.astype(np.float64), **hp)
+    pd, gd, md, vd = (torch.from_numpy(a.copy()).cuda() for a in (p, g, m, v))
+    K.adam_update(pd, gd, md, vd, **hp)
+    # fp32 rounding of each update, bounded by the magnitudes of its terms
+    # (m = b1 m + (1-b1) g can cancel, so a relative bound on m alone is wrong)
+    e32 = 2.0 ** -23
+    m64, g64, v64, p64 = (a.astype(np.float64) for a in (m, g, v, p))
+    m_scale = np.abs(hp["b1"] * m64) + np.abs((1 - hp["b1"]) * g64)
+    assert np.all(np.abs(md.cpu().numpy() - wm) <= 3 * e32 * m_scale + 1e-30)
+    assert np.all(np.abs(vd.cpu().numpy() - wv) <= 4 * e32 * wv + 1e-30)
+    step = hp["lr"] * (np.abs(wm) / hp["bc1"] + 3 * e32 * m_scale / hp["bc1"]) / (np.sqrt(wv / hp["bc2"]) + hp["eps"])
+    assert np.all(np.abs(pd.cpu().numpy() - wp) <= 2 * e32 * np.abs(p64) + 8 * e32 * step + 1e-30)
+    # bf16 parameter with an fp32 master copy and a bf16 gradient
+    master = torch.from_numpy(p.copy()).cuda()
+    pb = master.bfloat16()
+    gb = torch.from_numpy(g).bfloat16().cuda()
+    md, vd = torch.from_numpy(m.copy()).cuda(), torch.from_numpy(v.copy()).cuda()
+    K.adam_update(pb, gb, md, vd, master=master, **hp)
+    wp2, _, _ = _adam_ref(p.astype(np.float64), gb.cpu().double().numpy(), m.astype(np.float64),
+                          v.astype(np.float64), **hp)
+    assert np.all(np.abs(master.cpu().numpy() - wp2) <= 2 * e32 * np.abs(p64) + 8 * e32 * step * 2 + 1e-30)
+    assert torch.equal(pb, master.bfloat16())
+
+
+# ------------------------------------------------------------------ attention backward
+def _attn_ref(q, k, v, scale, causal):
+    s = (q @ k.transpose(-1, -2)) * scale
+    if causal:
+        Sq, Sk = s.shape[-2:]
+        mask = torch.ones(Sq, Sk, dtype=torch.bool).tril()
+        s = s.masked_fill(~mask, float("-inf"))
+    return torch.softmax(s, -1) @ v
+
+
+@pytest.mark.parametrize("B,H,S,D,causal", [(2, 3, 128, 64, True), (1, 2, 100, 128, True),
+                                            (2, 2, 96, 64, False), (1, 1, 1, 64, True)])
+def test_sdpa_bwd(K, B, H, S, D, causal):
+    g = torch.Generator().manual_seed(S + D)
+    q, k, v = ((torch.randn(B, H, S, D, generator=g) * (1.0 if i < 2 else 0.5)).bfloat16() for i in range(3))
+    do = torch.randn(B, H, S, D, generator=g).bfloat16()
+    scale = 1 / math.sqrt(D)
+    qd, kd, vd, dod = (t.cuda() for t in (q, k, v, do))
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    o = K.sdpa_fwd(qd, kd, vd, scale, causal, lse=lse)
+    dq, dk, dv = K.sdpa_bwd(qd, kd, vd, o, dod, lse, scale, causal)
+    qr, kr, vr = (t.double().requires_grad_(True) for t in (q, k, v))
+    _attn_ref(qr, kr, vr, scale, causal).backward(do.double())
+    # bf16 operands, bf16 P / dS and bf16 outputs: relative L2 error of a few 2^-8
+    for got, want, name in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv")):
+        assert _rel(got, want) < 2.5e-2, name
+
+
+def test_sdpa_bwd_strided_head_split(K):
+    """q, k, v as column slices of one [B*S, 3*H*D] projection (the GPT-2
+    layout), dq/dk/dv written into the same layout."""
+    g = torch.Generator().manual_seed(11)
+    B, S, H, D = 2, 64, 2, 64
+    qkv = (torch.randn(B, S, 3, H, D, generator=g) * 0.7).bfloat16()
+    do = torch.randn(B, S, H, D, generator=g).bfloat16()
+    dev = qkv.cuda()
+    q, k, v = (dev[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    dod = do.cuda().permute(0, 2, 1, 3)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    o = K.sdpa_fwd(q, k, v, 0.125, True, lse=lse)
+    dqkv = torch.empty_like(dev)
+    dq, dk, dv = (dqkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    K.sdpa_bwd(q, k, v, o, dod, lse, 0.125, True, dq=dq, dk=dk, dv=dv)
+    qr, kr, vr = (qkv[:, :, i].permute(0, 2, 1, 3).double().requires_grad_(True) for i in range(3))
+    _attn_ref(qr, kr, vr, 0.125, True).backward(do.permute(0, 2, 1, 3).double())
+    for i, r in enumerate((qr, kr, vr)):
+        assert _rel(dqkv[:, :, i].permute(0, 2, 1, 3), r.grad) < 2.5e-2
