@@ -71,26 +71,55 @@ __global__ __launch_bounds__(kBlock) void gelu_bwd_bf16x8_kernel(const u32x4_t* 
 // ---------------------------------------------------------------- column sums
 // Pass 1: block b sums rows [b*rpb, (b+1)*rpb) of every column into its
 // partial row; thread t owns columns t, t + 256, ... and adds its rows in
-// order.  Pass 2: y[c] = sum over blocks, in block order.
+// order.  Pass 2 (col_final_kernel) adds the partial rows.
+constexpr int64_t kColChunk = 8 * kBlock;  // columns per block along grid y
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void col_partial_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
                                                            int64_t rpb, float* __restrict__ part) {
   const int64_t r0 = int64_t(blockIdx.x) * rpb, r1 = min(rows, r0 + rpb);
-  for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
+  const int64_t c1 = min(cols, int64_t(blockIdx.y + 1) * kColChunk);
+  for (int64_t c = int64_t(blockIdx.y) * kColChunk + threadIdx.x; c < c1; c += kBlock) {
     float acc = 0.f;
     for (int64_t r = r0; r < r1; ++r) acc += ldf<T>(x, r * cols + c);
     part[int64_t(blockIdx.x) * cols + c] = acc;
   }
 }
 
+// y[c] = sum over nparts partial rows.  A block covers 32 columns with 8
+// groups of threads; group j adds partials j, j + 8, ... in order (eight
+// loads in flight per thread), then the 8 group sums are added in group
+// order: a fixed summation tree, so the result is deterministic.
+constexpr int kFinCols = 32, kFinGroups = kBlock / kFinCols;
+
 __global__ __launch_bounds__(kBlock) void col_final_kernel(const float* __restrict__ part, int64_t nparts,
                                                          int64_t cols, float* __restrict__ y) {
-  const int64_t c = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (c >= cols) return;
+  __shared__ float red[kFinGroups][kFinCols];
+  const int cl = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
+  const int64_t c = int64_t(blockIdx.x) * kFinCols + cl;
   float acc = 0.f;
-  for (int64_t p = 0; p < nparts; ++p) acc += part[p * cols + c];
-  y[c] = acc;
+  if (c < cols) {
+    int64_t p = grp;
+    for (; p + 7 * kFinGroups < nparts; p += 8 * kFinGroups) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(p + u * kFinGroups) * cols + c];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; p < nparts; p += kFinGroups) acc += part[p * cols + c];
+  }
+  red[grp][cl] = acc;
+  __syncthreads();
+  if (grp == 0 && c < cols) {
+    float t = red[0][cl];
+#pragma unroll
+    for (int j = 1; j < kFinGroups; ++j) t += red[j][cl];
+    y[c] = t;
+  }
 }
+
+inline unsigned final_blocks(int64_t cols) { return unsigned((cols + kFinCols - 1) / kFinCols); }
 
 inline int64_t col_parts(int64_t rows) { return std::min<int64_t>(512, std::max<int64_t>(1, (rows + 15) / 16)); }
 
@@ -363,16 +392,16 @@ extern "C" int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols,
   if (!x || !workspace) return fail(MK_ERR_INVALID, "mk_col_sum: null input or workspace");
   const int64_t np = col_parts(rows), rpb = (rows + np - 1) / np;
   float* part = static_cast<float*>(workspace);
+  const dim3 g(unsigned(np), unsigned((cols + kColChunk - 1) / kColChunk));
+  if (g.y > 65535) return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: too many columns");
   if (in_type == MK_BF16)
-    hipLaunchKernelGGL(col_partial_kernel<uint16_t>, dim3(unsigned(np)), dim3(kBlock), 0, s, (const uint16_t*)x,
-                       rows, cols, rpb, part);
+    hipLaunchKernelGGL(col_partial_kernel<uint16_t>, g, dim3(kBlock), 0, s, (const uint16_t*)x, rows, cols, rpb,
+                       part);
   else if (in_type == MK_F32)
-    hipLaunchKernelGGL(col_partial_kernel<float>, dim3(unsigned(np)), dim3(kBlock), 0, s, (const float*)x, rows,
-                       cols, rpb, part);
+    hipLaunchKernelGGL(col_partial_kernel<float>, g, dim3(kBlock), 0, s, (const float*)x, rows, cols, rpb, part);
   else
     return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: in_type must be bf16/f32");
-  hipLaunchKernelGGL(col_final_kernel, dim3(unsigned((cols + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, part, np,
-                     cols, y);
+  hipLaunchKernelGGL(col_final_kernel, dim3(final_blocks(cols)), dim3(kBlock), 0, s, part, np, cols, y);
   return check_launch("mk_col_sum");
 }
 
@@ -420,7 +449,7 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
   else if (io_type == MK_F32) dispatch(float{});
   else return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: io_type must be bf16/f32");
   if (dgamma) {
-    const dim3 g(unsigned((cols + kBlock - 1) / kBlock));
+    const dim3 g(final_blocks(cols));
     hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pg, nparts, cols, dgamma);
     hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pb, nparts, cols, dbeta);
   }
