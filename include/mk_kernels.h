@@ -68,6 +68,20 @@ int mk_gemm(void* stream, int ab_type, int c_type,
             void* C, int64_t c_bs, int64_t c_ms,
             const void* bias, int epilogue);
 
+/* Plain GEMM through rocBLAS (the linear layers of the training step and
+ * their gradients: no epilogue to fuse, so the library GEMM is used, as the
+ * brief for this build allows for plain GEMMs).  Same operand convention as
+ * mk_gemm (row-major C with row stride c_ms, one unit stride per operand),
+ * C = alpha A B + beta C; no bias.  ab_type ∈ {MK_BF16 (c_type MK_BF16 /
+ * MK_F16 / MK_F32), MK_F32 (c_type MK_F32)}, fp32 accumulation.  Operands
+ * with overlapping rows (leading stride below the row length) are rejected.
+ * Replaces, for these products: src/jam/ops/linalg.mm:98. */
+int mk_gemm_blas(void* stream, int ab_type, int c_type,
+                 int64_t batch, int64_t M, int64_t N, int64_t K,
+                 const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,
+                 const void* B, int64_t b_bs, int64_t b_ks, int64_t b_ns,
+                 void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
+
 /* ------------------------------------------------------------------------
  * a5+a6  fused scaled-dot-product attention (flash attention, forward).
  * Replaces the unfused chain the reference emits for the jnp attention
@@ -262,6 +276,14 @@ int mk_fill(void* stream, int elem_bytes, int64_t n, uint64_t pattern, void* out
  * here each backward composition is one entry point.
  * ====================================================================== */
 
+/* out[r, c] = a[r, c] + b[r, c] + bias[c] over a dense [rows, cols] array,
+ * fp32 math and one rounding (b and / or bias may be NULL; out may alias a
+ * or b).  The residual and bias adds of the step: the broadcast add of a
+ * bias (structural.mm:87-96 broadcast feeding elementwise.mm add) and the
+ * residual add, folded into one pass.  io_type ∈ {MK_BF16, MK_F32}. */
+int mk_add_rows(void* stream, int io_type, int64_t rows, int64_t cols, const void* a, const void* b,
+                const void* bias, void* out);
+
 /* dx = dy * gelu_tanh'(x), gelu_tanh as mk_gelu_tanh; fp32 math, one rounding
  * on store.  io_type ∈ {MK_BF16, MK_F32}.  dx may alias dy. */
 int mk_gelu_tanh_bwd(void* stream, int io_type, int64_t n, const void* x, const void* dy, void* dx);
@@ -317,7 +339,7 @@ int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* 
  * — the transposed dot_generals, select and reduce that jax.grad emits for
  * the attention pattern.  S, dP (fp32) and P, dS (bf16) are materialised per
  * (b, h) in the workspace of mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk); the
- * products run on mk_gemm.  Strides as mk_sdpa_fwd (elements, D contiguous);
+ * products run on the rocBLAS GEMM of mk_gemm_blas.  Strides as mk_sdpa_fwd (elements, D contiguous);
  * o and dout rows 16-byte aligned; D a multiple of 8, ≤ 256. */
 size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
 int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,

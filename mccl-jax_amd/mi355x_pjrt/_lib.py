@@ -35,6 +35,10 @@ SIGNATURES = {
                      _P, _I64, _I64, _I64,
                      _P, _I64, _I64, _I64,
                      _P, _I64, _I64, _P, _I]),
+    "mk_gemm_blas": (_I, [_P, _I, _I, _I64, _I64, _I64, _I64,
+                          _P, _I64, _I64, _I64,
+                          _P, _I64, _I64, _I64,
+                          _P, _I64, _I64, _F, _F]),
     "mk_sdpa_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64,
                          _P, _I64, _I64, _I64,
                          _P, _I64, _I64, _I64,
@@ -55,6 +59,7 @@ SIGNATURES = {
     "mk_convert": (_I, [_P, _I, _I, _I64, _P, _P]),
     "mk_fill": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
     "mk_gelu_tanh_bwd": (_I, [_P, _I, _I64, _P, _P, _P]),
+    "mk_add_rows": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P]),
     "mk_col_sum_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "mk_col_sum": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
     "mk_layernorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),

@@ -8,9 +8,9 @@ lines 71-75), for a pre-LayerNorm decoder with tied input/output embeddings,
 GELU(tanh) MLP and causal attention, without the pmean (one GPU).  Every
 operation is a call through the C-ABI of include/mk_kernels.h:
 
-  forward   gather + position add, per layer LN -> QKV GEMM (+bias) -> causal
-            attention -> output GEMM (+bias) -> residual add -> LN -> FC GEMM
-            (+bias) -> GELU -> projection GEMM (+bias) -> residual add; final
+  forward   gather + position add, per layer LN -> QKV GEMM, bias add -> causal
+            attention -> output GEMM -> residual + bias add -> LN -> FC GEMM,
+            bias add -> GELU -> projection GEMM -> residual + bias add; final
             LN, logits GEMM against the embedding table, fused softmax
             cross-entropy (loss rows and the logit gradient, in place)
   backward  the transposed GEMMs (weight gradients straight to fp32), column
@@ -20,7 +20,9 @@ operation is a call through the C-ABI of include/mk_kernels.h:
   update    one Adam launch over all parameters (fp32 master, m, v; bf16
             working copy rewritten)
 
-All parameters live in five flat buffers (fp32 master, bf16 working copy,
+The GEMMs have no epilogue here (the biases join the elementwise pass that
+follows), so they are plain library GEMMs (mk_gemm_blas, rocBLAS); every other
+operation is a hand-written kernel.  All parameters live in five flat buffers (fp32 master, bf16 working copy,
 fp32 gradient, fp32 m, fp32 v), each parameter a 64-element-aligned slice, so
 the optimizer is a single launch and every gradient is written in place.  The
 step is prepared once as a list of bound calls (device pointers and shapes
@@ -47,7 +49,6 @@ _F = ctypes.c_float
 _D = ctypes.c_double
 
 BF16, F32, S32 = K.MK["BF16"], K.MK["F32"], K.MK["S32"]
-EW_ADD = K.EW["ADD"]
 
 
 @dataclass(frozen=True)
@@ -226,24 +227,17 @@ class GPT2TrainStep:
         def G(name):
             return P(self.view(self.grad, name))
 
-        def gemm(ab, ct, M, N, Kd, a, a_ms, a_ks, b, b_ks, b_ns, cptr, c_ms, bias=None, tag="gemm"):
-            calls.append(_Call(lib.mk_gemm, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
-                                             a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
-                                             _I64(b_ns), cptr, _I64(0), _I64(c_ms),
-                                             bias if bias is not None else _P(0), _I(0 if bias is None else 1)],
-                               "mk_gemm " + tag))
+        def gemm(ab, ct, M, N, Kd, a, a_ms, a_ks, b, b_ks, b_ns, cptr, c_ms, tag="gemm"):
+            # plain GEMM (no epilogue) through rocBLAS
+            calls.append(_Call(lib.mk_gemm_blas, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
+                                                  a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
+                                                  _I64(b_ns), cptr, _I64(0), _I64(c_ms), _F(1.0), _F(0.0)],
+                               "mk_gemm_blas " + tag))
 
-        def add(out, a, b, n):
-            # out = a + b over n bf16 elements (mk_ew_program, one ADD)
-            dims = (_I64 * 1)(n)
-            ptrs = (_P * 2)(a.value, b.value)
-            types = (_I * 2)(BF16, BF16)
-            strides = (_I64 * 12)(*([1, 0, 0, 0, 0, 0] * 2))
-            prog = (ctypes.c_int32 * 4)(EW_ADD, 2, 0, 1)
-            cst = (_F * 1)(0.0)
-            # the argument tuple keeps the ctypes arrays alive with the call
-            calls.append(_Call(lib.mk_ew_program, [st, _I(1), dims, _I(2), ptrs, types, strides, _I(1), prog, cst,
-                                                   _I(0), _I(2), _I(BF16), out], "mk_ew_program add"))
+        def add_rows(out, rows, cols, a, b=None, bias=None, tag="add"):
+            """out = a (+ b) (+ bias broadcast over rows), one mk_add_rows pass"""
+            calls.append(_Call(lib.mk_add_rows, [st, _I(BF16), _I64(rows), _I64(cols), a, b or _P(0),
+                                                 bias or _P(0), out], "mk_add_rows " + tag))
 
         def layernorm(x, gname, bname, y):
             calls.append(_Call(lib.mk_layernorm, [st, _I(BF16), _I64(T), _I64(d), x, W(gname), W(bname),
@@ -262,36 +256,28 @@ class GPT2TrainStep:
         calls.append(_Call(lib.mk_gather_rows, [st, _I64(V), _I64(d * 2), W("wte"), _I(S32), _I64(T),
                                                 P(self.ids), P(self.x[0])], "mk_gather_rows"))
         # x0 += wpe broadcast over the batch: [B, S*d] + [S*d]
-        dims = (_I64 * 2)(B, S * d)
-        ptrs = (_P * 2)(self.x[0].data_ptr(), self.view(self.param, "wpe").data_ptr())
-        types = (_I * 2)(BF16, BF16)
-        strides = (_I64 * 12)(S * d, 1, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0)
-        prog = (ctypes.c_int32 * 4)(EW_ADD, 2, 0, 1)
-        cst = (_F * 1)(0.0)
-        calls.append(_Call(lib.mk_ew_program, [st, _I(2), dims, _I(2), ptrs, types, strides, _I(1), prog, cst,
-                                               _I(0), _I(2), _I(BF16), P(self.x[0])], "mk_ew_program pos"))
+        add_rows(P(self.x[0]), B, S * d, P(self.x[0]), bias=W("wpe"), tag="pos")
         for l in range(L):
             p = f"h{l}."
             layernorm(P(self.x[l]), p + "ln1_g", p + "ln1_b", P(self.h1[l]))
             gemm(BF16, BF16, T, 3 * d, d, P(self.h1[l]), d, 1, W(p + "w_qkv"), 3 * d, 1, P(self.qkv[l]), 3 * d,
-                 bias=W(p + "b_qkv"), tag="qkv")
+                 tag="qkv")
+            add_rows(P(self.qkv[l]), T, 3 * d, P(self.qkv[l]), bias=W(p + "b_qkv"), tag="bias")
             q, k, v = (P(self.qkv[l], i * d) for i in range(3))
             strides_qkv = [_I64(S * 3 * d), _I64(hd), _I64(3 * d)]
             calls.append(_Call(lib.mk_sdpa_fwd, [st, _I64(B), _I64(H), _I64(S), _I64(S), _I64(hd),
                                                  q, *strides_qkv, k, *strides_qkv, v, *strides_qkv,
                                                  P(self.att[l]), _I64(S * d), _I64(hd), _I64(d),
                                                  _F(scale), _I(1), P(self.lse[l])], "mk_sdpa_fwd"))
-            gemm(BF16, BF16, T, d, d, P(self.att[l]), d, 1, W(p + "w_o"), d, 1, P(self.tmp), d,
-                 bias=W(p + "b_o"), tag="o")
-            add(P(self.xm[l]), P(self.x[l]), P(self.tmp), T * d)
+            gemm(BF16, BF16, T, d, d, P(self.att[l]), d, 1, W(p + "w_o"), d, 1, P(self.tmp), d, tag="o")
+            add_rows(P(self.xm[l]), T, d, P(self.x[l]), P(self.tmp), W(p + "b_o"), tag="residual")
             layernorm(P(self.xm[l]), p + "ln2_g", p + "ln2_b", P(self.h2[l]))
-            gemm(BF16, BF16, T, F, d, P(self.h2[l]), d, 1, W(p + "w_fc"), F, 1, P(self.f[l]), F,
-                 bias=W(p + "b_fc"), tag="fc")
+            gemm(BF16, BF16, T, F, d, P(self.h2[l]), d, 1, W(p + "w_fc"), F, 1, P(self.f[l]), F, tag="fc")
+            add_rows(P(self.f[l]), T, F, P(self.f[l]), bias=W(p + "b_fc"), tag="bias")
             calls.append(_Call(lib.mk_gelu_tanh, [st, _I(BF16), _I64(T * F), P(self.f[l]), P(self.g[l])],
                                "mk_gelu_tanh"))
-            gemm(BF16, BF16, T, d, F, P(self.g[l]), F, 1, W(p + "w_pr"), d, 1, P(self.tmp), d,
-                 bias=W(p + "b_pr"), tag="proj")
-            add(P(self.x[l + 1]), P(self.xm[l]), P(self.tmp), T * d)
+            gemm(BF16, BF16, T, d, F, P(self.g[l]), F, 1, W(p + "w_pr"), d, 1, P(self.tmp), d, tag="proj")
+            add_rows(P(self.x[l + 1]), T, d, P(self.xm[l]), P(self.tmp), W(p + "b_pr"), tag="residual")
         layernorm(P(self.x[L]), "lnf_g", "lnf_b", P(self.hf))
         # logits = hf @ wteᵀ, then loss rows and dlogits (over the logits)
         gemm(BF16, BF16, T, V, d, P(self.hf), d, 1, W("wte"), 1, d, P(self.logits), V, tag="logits")
@@ -317,7 +303,7 @@ class GPT2TrainStep:
             colsum(P(self.dff), T, F, G(p + "b_fc"))
             gemm(BF16, BF16, T, d, F, P(self.dff), F, 1, W(p + "w_fc"), 1, F, P(self.dh), d, tag="dh2")
             ln_bwd(P(self.xm[l]), p + "ln2_g", P(self.dh), P(self.dln), p + "ln2")
-            add(P(self.dx), P(self.dx), P(self.dln), T * d)
+            add_rows(P(self.dx), T, d, P(self.dx), P(self.dln))
             # attention branch of xm = x[l] + o(attn(ln1(x[l])))
             gemm(BF16, F32, d, d, T, P(self.att[l]), 1, d, P(self.dx), d, 1, G(p + "w_o"), d, tag="dw_o")
             colsum(P(self.dx), T, d, G(p + "b_o"))
@@ -336,7 +322,7 @@ class GPT2TrainStep:
             gemm(BF16, BF16, T, d, 3 * d, P(self.dqkv), 3 * d, 1, W(p + "w_qkv"), 1, 3 * d, P(self.dh), d,
                  tag="dh1")
             ln_bwd(P(self.x[l]), p + "ln1_g", P(self.dh), P(self.dln), p + "ln1")
-            add(P(self.dx), P(self.dx), P(self.dln), T * d)
+            add_rows(P(self.dx), T, d, P(self.dx), P(self.dln))
         # embeddings: position gradient = sum over the batch; token gradient
         # scattered (in token order) into the head's embedding gradient
         colsum(P(self.dx), B, S * d, G("wpe"))

@@ -277,6 +277,26 @@ def _ws(nbytes, device, workspace):
     return workspace
 
 
+def add_rows(a, b=None, bias=None, out=None, stream=None):
+    """out = a + b + bias (bias broadcast over the rows of a 2-D a), one pass
+    with fp32 math and one rounding; b and bias are optional, out may be a or b."""
+    _require_cuda(a)
+    rows, cols = a.shape
+    for t in (b, bias):
+        if t is not None:
+            _require_cuda(t)
+            if t.dtype != a.dtype or not t.is_contiguous():
+                raise ValueError("add_rows: operands must share a's dtype and be contiguous")
+    if b is not None and b.shape != a.shape:
+        raise ValueError("add_rows: b must have a's shape")
+    if bias is not None and bias.numel() != cols:
+        raise ValueError("add_rows: bias must have one value per column")
+    out = torch.empty_like(a) if out is None else out
+    rc = lib().mk_add_rows(_stream(stream), mk_dtype(a.dtype), rows, cols, _ptr(a), _ptr(b), _ptr(bias), _ptr(out))
+    _check(rc, "mk_add_rows")
+    return out
+
+
 def gelu_tanh_bwd(x, dy, out=None, stream=None):
     """dx = dy * gelu_tanh'(x) (same dtype as x; out may be dy)."""
     _require_cuda(x, dy)

@@ -1,0 +1,112 @@
+// Plain (unfused) GEMMs through rocBLAS: the linear layers of the training
+// step and their gradients, which have no epilogue worth fusing.  The
+// row-major, element-strided operand convention of mk_gemm is mapped onto
+// rocBLAS's column-major gemm: C[M,N] = A[M,K] B[K,N] is the column-major
+// product C^T[N,M] = B^T[N,K] A^T[K,M], and each operand is passed as stored
+// (no copies), transposed where its unit stride says so.
+#include "mk_common.h"
+
+#include <rocblas/rocblas.h>
+
+#include <mutex>
+#include <vector>
+
+namespace mk {
+namespace {
+
+std::mutex g_blas_mu;
+std::vector<rocblas_handle> g_handles;  // one per device, kept for the process
+
+rocblas_handle handle_for_current_device(int* err) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    *err = fail(MK_ERR_LAUNCH, "mk_gemm_blas: hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_blas_mu);
+  if (int(g_handles.size()) <= dev) g_handles.resize(dev + 1, nullptr);
+  if (!g_handles[dev]) {
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success) {
+      *err = fail(MK_ERR_LAUNCH, "mk_gemm_blas: rocblas_create_handle failed");
+      return nullptr;
+    }
+    rocblas_set_pointer_mode(h, rocblas_pointer_mode_host);
+    g_handles[dev] = h;
+  }
+  return g_handles[dev];
+}
+
+bool blas_type(int t, rocblas_datatype* out) {
+  if (t == MK_BF16) *out = rocblas_datatype_bf16_r;
+  else if (t == MK_F32) *out = rocblas_datatype_f32_r;
+  else if (t == MK_F16) *out = rocblas_datatype_f16_r;
+  else return false;
+  return true;
+}
+
+}  // namespace
+
+// shared with the attention backward (train.hip)
+int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
+              const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
+              int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0) return fail(MK_ERR_INVALID, "mk_gemm_blas: negative shape");
+  if (batch == 0 || M == 0 || N == 0) return MK_OK;
+  if (!A || !B || !C) return fail(MK_ERR_INVALID, "mk_gemm_blas: null pointer");
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX || batch > INT32_MAX)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: dimensions beyond int32");
+  rocblas_datatype ab, ct;
+  if (!blas_type(ab_type, &ab) || !blas_type(c_type, &ct) || ab_type == MK_F16 ||
+      (ab_type == MK_F32 && c_type != MK_F32))
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: operands bf16 (out bf16/f16/f32) or f32 (out f32)");
+  // rocBLAS "A" = our Bᵀ as an N x K column-major matrix
+  rocblas_operation op_a;
+  int64_t lda;
+  if (b_ns == 1) { op_a = rocblas_operation_none; lda = b_ks; }
+  else if (b_ks == 1) { op_a = rocblas_operation_transpose; lda = b_ns; }
+  else return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: B needs a unit stride along k or n");
+  // rocBLAS "B" = our Aᵀ as a K x M column-major matrix
+  rocblas_operation op_b;
+  int64_t ldb;
+  if (a_ks == 1) { op_b = rocblas_operation_none; ldb = a_ms; }
+  else if (a_ms == 1) { op_b = rocblas_operation_transpose; ldb = a_ks; }
+  else return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: A needs a unit stride along m or k");
+  // a stored matrix's leading dimension must cover its rows; where it has a
+  // single column the stride is never used and is set to the row count
+  auto fix_ld = [](int64_t& ld, int64_t rows, int64_t cols) {
+    if (cols == 1 && ld < rows) ld = rows;
+    return ld >= rows;
+  };
+  int64_t ldc = c_ms;
+  if (!fix_ld(lda, op_a == rocblas_operation_none ? N : K, op_a == rocblas_operation_none ? K : N) ||
+      !fix_ld(ldb, op_b == rocblas_operation_none ? K : M, op_b == rocblas_operation_none ? M : K) ||
+      !fix_ld(ldc, N, M))
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: overlapping rows (leading stride below the row length)");
+  if (lda > INT32_MAX || ldb > INT32_MAX || ldc > INT32_MAX)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas: leading dimension beyond int32");
+  int err = MK_OK;
+  rocblas_handle h = handle_for_current_device(&err);
+  if (!h) return err;
+  if (rocblas_set_stream(h, stream) != rocblas_status_success)
+    return fail(MK_ERR_LAUNCH, "mk_gemm_blas: rocblas_set_stream failed");
+  const rocblas_status st = rocblas_gemm_strided_batched_ex(
+      h, op_a, op_b, rocblas_int(N), rocblas_int(M), rocblas_int(K), &alpha, B, ab, rocblas_int(lda), b_bs, A, ab,
+      rocblas_int(ldb), a_bs, &beta, C, ct, rocblas_int(ldc), c_bs, C, ct, rocblas_int(ldc), c_bs,
+      rocblas_int(batch), rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success)
+    return fail(MK_ERR_LAUNCH, std::string("mk_gemm_blas: rocblas_gemm_strided_batched_ex: ") +
+                                   rocblas_status_to_string(st));
+  return MK_OK;
+}
+
+}  // namespace mk
+
+extern "C" int mk_gemm_blas(void* stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
+                            const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,
+                            const void* B, int64_t b_bs, int64_t b_ks, int64_t b_ns,
+                            void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta) {
+  mk::clear_error();
+  return mk::gemm_blas(mk::as_stream(stream), ab_type, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks,
+                       b_ns, C, c_bs, c_ms, alpha, beta);
+}

@@ -20,6 +20,11 @@ int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// rocBLAS GEMM behind mk_gemm_blas (blas.hip), same operand convention.
+int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
+              const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
+              int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
+
 // ---------------------------------------------------------------- dtypes
 inline int dtype_bytes(int t) {
   switch (t) {

@@ -343,6 +343,39 @@ __global__ __launch_bounds__(kBlock) void attn_dscores_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------- row adds
+// out[r, c] = a[r, c] (+ b[r, c]) (+ bias[c]), fp32 math, one rounding.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void add_rows_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                        const T* __restrict__ bias, int64_t rows, int64_t cols,
+                                                        T* __restrict__ out) {
+  const int64_t n = rows * cols, stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+    float v = ldf<T>(a, i);
+    if (b) v += ldf<T>(b, i);
+    if (bias) v += ldf<T>(bias, i % cols);
+    stf<T>(out, i, v);
+  }
+}
+
+// bf16, 8 columns per thread per trip (cols % 8 == 0, 16-byte aligned rows)
+__global__ __launch_bounds__(kBlock) void add_rows_bf16x8_kernel(const u32x4_t* __restrict__ a,
+                                                               const u32x4_t* __restrict__ b,
+                                                               const u32x4_t* __restrict__ bias, int64_t nvec,
+                                                               int64_t cvec, u32x4_t* __restrict__ out) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
+    const u32x4_t x = a[i];
+    const u32x4_t y = b ? b[i] : u32x4_t{0u, 0u, 0u, 0u};
+    const u32x4_t z = bias ? bias[i % cvec] : u32x4_t{0u, 0u, 0u, 0u};
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack_bf16(lo16(x[j]) + lo16(y[j]) + lo16(z[j]), hi16(x[j]) + hi16(y[j]) + hi16(z[j]));
+    out[i] = o;
+  }
+}
+
 inline unsigned grid_for(int64_t n, int64_t per_block = kBlock) {
   return unsigned(std::min<int64_t>((n + per_block - 1) / per_block, 65536));
 }
@@ -558,8 +591,7 @@ extern "C" int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
     const uint16_t* kb = static_cast<const uint16_t*>(k) + b * k_bs;
     float* Fb = F + b * H * SS;
     // S = Q Kᵀ  [Sq x Sk], fp32
-    if (int rc = mk_gemm(stream, MK_BF16, MK_F32, H, Sq, Sk, D, qb, q_hs, q_ss, 1, kb, k_hs, 1, k_ss, Fb, SS, Sk,
-                         nullptr, 0))
+    if (int rc = gemm_blas(s, MK_BF16, MK_F32, H, Sq, Sk, D, qb, q_hs, q_ss, 1, kb, k_hs, 1, k_ss, Fb, SS, Sk, 1.f, 0.f))
       return rc;
   }
   hipLaunchKernelGGL(attn_probs_kernel, dim3(grid_for(n)), dim3(kBlock), 0, s, F, lse, Sq, Sk, scale, causal, P, n);
@@ -570,12 +602,11 @@ extern "C" int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
     const uint16_t* Pb = P + b * H * SS;
     float* Fb = F + b * H * SS;
     // dV = Pᵀ dO  [Sk x D]
-    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, db, do_hs, do_ss, 1,
-                         static_cast<uint16_t*>(dv) + b * dv_bs, dv_hs, dv_ss, nullptr, 0))
+    if (int rc = gemm_blas(s, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, db, do_hs, do_ss, 1,
+                           static_cast<uint16_t*>(dv) + b * dv_bs, dv_hs, dv_ss, 1.f, 0.f))
       return rc;
     // dP = dO Vᵀ  [Sq x Sk], fp32 (over the scores)
-    if (int rc = mk_gemm(stream, MK_BF16, MK_F32, H, Sq, Sk, D, db, do_hs, do_ss, 1, vb, v_hs, 1, v_ss, Fb, SS, Sk,
-                         nullptr, 0))
+    if (int rc = gemm_blas(s, MK_BF16, MK_F32, H, Sq, Sk, D, db, do_hs, do_ss, 1, vb, v_hs, 1, v_ss, Fb, SS, Sk, 1.f, 0.f))
       return rc;
   }
   hipLaunchKernelGGL(attn_dscores_kernel, dim3(grid_for(n)), dim3(kBlock), 0, s, F, Dsum, Sk, scale, P, n);
@@ -585,13 +616,39 @@ extern "C" int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
     const uint16_t* kb = static_cast<const uint16_t*>(k) + b * k_bs;
     const uint16_t* Pb = P + b * H * SS;
     // dQ = dS K  [Sq x D]
-    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sq, D, Sk, Pb, SS, Sk, 1, kb, k_hs, k_ss, 1,
-                         static_cast<uint16_t*>(dq) + b * dq_bs, dq_hs, dq_ss, nullptr, 0))
+    if (int rc = gemm_blas(s, MK_BF16, MK_BF16, H, Sq, D, Sk, Pb, SS, Sk, 1, kb, k_hs, k_ss, 1,
+                           static_cast<uint16_t*>(dq) + b * dq_bs, dq_hs, dq_ss, 1.f, 0.f))
       return rc;
     // dK = dSᵀ Q  [Sk x D]
-    if (int rc = mk_gemm(stream, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, qb, q_hs, q_ss, 1,
-                         static_cast<uint16_t*>(dk) + b * dk_bs, dk_hs, dk_ss, nullptr, 0))
+    if (int rc = gemm_blas(s, MK_BF16, MK_BF16, H, Sk, D, Sq, Pb, SS, 1, Sk, qb, q_hs, q_ss, 1,
+                           static_cast<uint16_t*>(dk) + b * dk_bs, dk_hs, dk_ss, 1.f, 0.f))
       return rc;
   }
   return MK_OK;
+}
+
+extern "C" int mk_add_rows(void* stream, int io_type, int64_t rows, int64_t cols, const void* a, const void* b,
+                           const void* bias, void* out) {
+  clear_error();
+  if (rows < 0 || cols < 0) return fail(MK_ERR_INVALID, "mk_add_rows: negative shape");
+  if (rows == 0 || cols == 0) return MK_OK;
+  if (!a || !out) return fail(MK_ERR_INVALID, "mk_add_rows: null pointer");
+  hipStream_t s = as_stream(stream);
+  const int64_t n = rows * cols;
+  if (io_type == MK_BF16) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                         reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(out);
+    if (cols % 8 == 0 && (al & 15) == 0)
+      hipLaunchKernelGGL(add_rows_bf16x8_kernel, dim3(grid_for(n / 8)), dim3(kBlock), 0, s, (const u32x4_t*)a,
+                         (const u32x4_t*)b, (const u32x4_t*)bias, n / 8, cols / 8, (u32x4_t*)out);
+    else
+      hipLaunchKernelGGL(add_rows_kernel<uint16_t>, dim3(grid_for(n)), dim3(kBlock), 0, s, (const uint16_t*)a,
+                         (const uint16_t*)b, (const uint16_t*)bias, rows, cols, (uint16_t*)out);
+  } else if (io_type == MK_F32) {
+    hipLaunchKernelGGL(add_rows_kernel<float>, dim3(grid_for(n)), dim3(kBlock), 0, s, (const float*)a,
+                       (const float*)b, (const float*)bias, rows, cols, (float*)out);
+  } else {
+    return fail(MK_ERR_UNSUPPORTED, "mk_add_rows: io_type must be bf16/f32");
+  }
+  return check_launch("mk_add_rows");
 }

@@ -54,6 +54,28 @@ def test_gelu_tanh_bwd(K, dtype):
     np.testing.assert_array_equal(_f64(got8), _f64(got[:4096]))
 
 
+# ------------------------------------------------------------------ row adds
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8192, 768), (33, 2304)])
+def test_add_rows(K, dtype, rows, cols):
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    a, b = (torch.randn(rows, cols, generator=g).to(dtype).cuda() for _ in range(2))
+    bias = torch.randn(cols, generator=g).to(dtype).cuda()
+    exact = _f64(a) + _f64(b) + _f64(bias)
+    tol = dict(rtol=0, atol=1e-6) if dtype == torch.float32 else dict(rtol=2 ** -8, atol=1e-6)
+    got = K.add_rows(a, b, bias)
+    np.testing.assert_allclose(_f64(got), exact, **tol)
+    # the kernel adds left to right in fp32 and rounds once: bit-exact with the same order on the CPU
+    af, bf, cf = (t.cpu().float() for t in (a, b, bias))
+    np.testing.assert_array_equal(_f64(got), _f64(((af + bf) + cf).to(dtype)))
+    np.testing.assert_array_equal(_f64(K.add_rows(a, None, bias)), _f64((af + cf).to(dtype)))
+    np.testing.assert_array_equal(_f64(K.add_rows(a, b)), _f64((af + bf).to(dtype)))
+    # in place over a, as the step's residual adds run
+    a2 = a.clone()
+    K.add_rows(a2, b, bias, out=a2)
+    np.testing.assert_array_equal(_f64(a2), _f64(got))
+
+
 # ------------------------------------------------------------------ column sums
 @pytest.mark.parametrize("rows,cols", [(1, 1), (19, 768), (8192, 768), (8, 786432), (1000, 257)])
 def test_col_sum(K, rows, cols):
@@ -205,9 +227,13 @@ def test_sdpa_bwd(K, B, H, S, D, causal):
     dq, dk, dv = K.sdpa_bwd(qd, kd, vd, o, dod, lse, scale, causal)
     qr, kr, vr = (t.double().requires_grad_(True) for t in (q, k, v))
     _attn_ref(qr, kr, vr, scale, causal).backward(do.double())
-    # bf16 operands, bf16 P / dS and bf16 outputs: relative L2 error of a few 2^-8
+    # bf16 operands, bf16 P / dS and bf16 outputs: relative L2 error of a few
+    # 2^-8.  With one key dq = dk = 0 exactly (dP equals D), so the error is
+    # measured against max(|grad|, 1e-3 |dO|) rather than |grad| alone.
+    floor = 1e-3 * float(do.double().norm())
     for got, want, name in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv")):
-        assert _rel(got, want) < 2.5e-2, name
+        err = float((_f64(got) - want).norm()) / max(float(want.norm()), floor)
+        assert err < 2.5e-2, (name, err)
 
 
 def test_sdpa_bwd_strided_head_split(K):
