@@ -337,11 +337,15 @@ int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* 
  * masked), D_r = dO_r · O_r and dS = scale P (dO Vᵀ - D):
  *   dV = Pᵀ dO,  dQ = dS K,  dK = dSᵀ Q     (bf16 out, fp32 accumulation)
  * — the transposed dot_generals, select and reduce that jax.grad emits for
- * the attention pattern.  S, dP (fp32) and P, dS (bf16) are materialised per
- * (b, h) in the workspace of mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk); the
- * products run on the rocBLAS GEMM of mk_gemm_blas.  Strides as mk_sdpa_fwd (elements, D contiguous);
- * o and dout rows 16-byte aligned; D a multiple of 8, ≤ 256. */
-size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
+ * the attention pattern.  D ∈ {64, 128}: flash style on MFMA kernels, P and
+ * dS recomputed per tile from lse, nothing Sq x Sk in memory, deterministic
+ * (no atomics); the workspace holds D_r and lse per row (B H Sq 8 bytes,
+ * rounded up to 64-row tiles); q/k/v/o/dout rows 16-byte aligned, dq/dk/dv
+ * strides multiples of 4.  Other D (a multiple of 8, ≤ 256): S, dP (fp32)
+ * and P, dS (bf16) materialised for all heads in the workspace, products on
+ * the rocBLAS GEMM of mk_gemm_blas; o and dout rows 16-byte aligned.
+ * Strides as mk_sdpa_fwd (elements, D contiguous). */
+size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D);
 int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                 const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
                 const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,

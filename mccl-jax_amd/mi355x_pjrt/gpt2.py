@@ -205,7 +205,7 @@ class GPT2TrainStep:
         lib = self.lib
         ws = max(lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
                  lib.mk_layernorm_bwd_workspace_bytes(T, d),
-                 lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq),
+                 lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),
                  lib.mk_scatter_add_workspace_bytes(c.vocab, T))
         self.ws = torch.empty(int(ws), dtype=torch.uint8, device=dev)
 

@@ -366,7 +366,7 @@ def sdpa_bwd(q, k, v, o, dout, lse, scale, causal=True, dq=None, dk=None, dv=Non
     dq = torch.empty_like(q) if dq is None else dq
     dk = torch.empty_like(k) if dk is None else dk
     dv = torch.empty_like(v) if dv is None else dv
-    ws = _ws(lib().mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk), q.device, workspace)
+    ws = _ws(lib().mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk, D), q.device, workspace)
     args = [_stream(stream), B, H, Sq, Sk, D]
     for t in (q, k, v, o, dout):
         args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]

@@ -6,10 +6,7 @@
 // whole key loop.  Key/value tiles of BN = 64 rows pass through LDS and are
 // shared by the 8 waves.
 //
-// Register layouts (32x32 MFMA, lane l, g = l / 32, c = l % 32):
-//   A operand: row c, 8 consecutive k-slots of half g
-//   B operand: col c, 8 consecutive k-slots of half g
-//   C/D:       reg r holds row 8*(r/4) + 4*g + (r%4), col c
+// Register layouts: those of the 32x32 MFMA (attn_common.h).
 // S is computed transposed, Sᵀ = K · Qᵀ, so every lane holds one query's
 // scores (column c) for 32 of the tile's keys: the row max / row sum are
 // in-lane reductions plus one exchange with lane l^32.  Those same
@@ -49,26 +46,20 @@
 // kRescaleLog2; between raises p <= 2^kRescaleLog2 stays far inside
 // fp32/bf16 range.  The row sum adds the bf16-rounded p (the values the P.V
 // product uses) with v_dot2_f32_bf16.
-#include "mk_common.h"
+#include "attn_common.h"
 
 #include <cmath>
 
 namespace mk {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+using namespace attn;
 
 constexpr int kBM = 256;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
-constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
 
 struct SdpaArgs {
   const uint16_t* q;
@@ -85,70 +76,6 @@ struct SdpaArgs {
   int BH;
   float scale_log2;  // scale * log2(e)
 };
-
-template <bool B>
-struct Flag {
-  static constexpr bool value = B;
-};
-template <int N>
-struct Int {
-  static constexpr int value = N;
-};
-
-__device__ inline bf16x8_t as_bf16x8(const u32x4_t& v) {
-  bf16x8_t r;
-  __builtin_memcpy(&r, &v, 16);
-  return r;
-}
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// raw buffer descriptor over [base, base + bytes): loads past the end return
-// zeros (word1: base bits 47:32, stride 0; word2: size; word3: gfx9 format)
-__device__ inline i32x4_t tile_desc(const uint16_t* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return i32x4_t{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xFFFFu), int(bytes), kBufferWord3};
-}
-
-// LDS byte address of a __shared__ location
-__device__ inline uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
-}
-
-// One 1 KB copy HBM/L2 -> LDS: lane l loads 16 bytes at byte offset voff of
-// the descriptor's range and the buffer unit writes them to LDS bytes
-// [dst + 16 l, dst + 16 l + 16).  Issued from inline assembly so that the
-// compiler does not track it: it inserts no vmcnt wait of its own for these
-// copies, and the kernel waits for them explicitly (wait_copies) before the
-// barrier that hands the data to the other waves.  M0 holds the LDS address
-// (set by the compiler from the constraint); one wait state separates the M0
-// write from the copy.
-// The descriptor and the LDS address pass through readfirstlane here, at the
-// operand, so they are in SGPRs however the caller computed them.
-__device__ inline void copy_to_lds(const i32x4_t& rsrc, uint32_t dst, int voff) {
-  const i32x4_t r = {__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
-                     __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(r), "{m0}"(__builtin_amdgcn_readfirstlane(dst))
-               : "memory");
-}
-
-// wait until every copy this wave has issued has landed in LDS
-__device__ inline void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// workgroup barrier ordering LDS accesses only (waits for lgkmcnt, not vmcnt)
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// 4 bf16 of one LDS column block (ds_read_b64_tr_b16), as two 32-bit words
-__device__ inline uint2 lds_read_tr(const uint16_t* p) {
-  const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p));
-  return __builtin_bit_cast(uint2, v);
-}
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p) {

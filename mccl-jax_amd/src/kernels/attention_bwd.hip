@@ -1,0 +1,541 @@
+// Attention backward (flash style) for gfx950 on v_mfma_f32_32x32x16_bf16:
+// the gradient of O = softmax(scale Q Kᵀ [causal]) V that mk_sdpa_fwd
+// computes, from its lse, without materialising any Sq x Sk matrix.
+//
+// With P = exp(scale S - lse) (0 where masked), D_r = dO_r · O_r and
+// dS = P ∘ (dO Vᵀ - D):
+//   dV = Pᵀ dO,  dK = scale dSᵀ Q,  dQ = scale dS K.
+// Three launches, none with atomics, so results are deterministic:
+//   stats  D_r and lse_r · log2(e) per query row, packed per 64-row tile
+//          ([bh][tile][lse2 x 64 | D x 64]; rows past Sq: +inf, 0, which
+//          makes their P and dS exactly 0);
+//   kv     one workgroup per 128 keys of one (b, h), wave w owning keys
+//          32 w .. 32 w + 31: dVᵀ and dKᵀ accumulate in registers while
+//          64-query tiles of Q, dO and the stats stream through LDS;
+//   q      one workgroup per 128 queries, wave w owning 32 of them: dQᵀ
+//          accumulates while 64-key tiles of K and V stream through LDS.
+// Each recomputes P (and dP) for its pairs, so the kv pass runs four
+// products per tile and the q pass three.
+//
+// kv: S = Q Kᵀ is formed with the wave's keys as columns (K, V fragments are
+// the B operands, kept in registers), so a lane owns one key and its
+// registers P, dS double as the B operands of dVᵀ = dOᵀ P and dKᵀ = Qᵀ dS;
+// the A operands dOᵀ, Qᵀ are transposed LDS reads (ds_read_b64_tr_b16).
+// Query rows vary across a lane's registers, so their lse2 / D come from
+// LDS as broadcast 16-byte reads.
+// q: Sᵀ = K Qᵀ with the wave's queries as columns (Q, dO fragments in
+// registers), a lane owns one query (one lse2 and D in registers), and
+// dSᵀ is the B operand of dQᵀ = Kᵀ dSᵀ (Kᵀ read transposed from LDS).
+//
+// Tiles are copied HBM -> LDS with buffer_load ... lds, double-buffered: the
+// copy of tile t+1 is issued before tile t is computed, and each wave waits
+// for its own copies before the barrier that ends the step.  LDS rows are
+// padded by 16 bytes, so the row-wise operand reads are conflict-free.
+#include "attn_common.h"
+
+#include <cmath>
+
+namespace mk {
+namespace {
+
+using namespace attn;
+
+constexpr int kWavesB = 4;
+constexpr int kThreadsB = 64 * kWavesB;
+constexpr int kBlkRows = 128;  // keys (kv) / queries (q) per workgroup
+constexpr int kTile = 64;      // rows per streamed tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct BwdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dout;
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  const float* stats;
+  int64_t q_bs, q_hs, q_ss;
+  int64_t k_bs, k_hs, k_ss;
+  int64_t v_bs, v_hs, v_ss;
+  int64_t do_bs, do_hs, do_ss;
+  int64_t dq_bs, dq_hs, dq_ss;
+  int64_t dk_bs, dk_hs, dk_ss;
+  int64_t dv_bs, dv_hs, dv_ss;
+  int H, Sq, Sk, BH;
+  int n_qt;     // 64-row query tiles (stats tiles)
+  int n_blk;    // 128-row blocks per (b, h) of the launch
+  float scale_log2;
+  float scale;
+};
+
+// ---------------------------------------------------------------- stats
+__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdArgs p, const uint16_t* __restrict__ o,
+                                                            int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                                                            const float* __restrict__ lse, int D,
+                                                            float* __restrict__ stats) {
+  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t per = int64_t(p.n_qt) * kTile;
+  if (t >= int64_t(p.BH) * per) return;
+  const int64_t bh = t / per;
+  const int row = int(t % per);
+  float l2 = INFINITY, dsum = 0.f;
+  if (row < p.Sq) {
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const uint16_t* orow = o + b * o_bs + h * o_hs + row * o_ss;
+    const uint16_t* drow = p.dout + b * p.do_bs + h * p.do_hs + row * p.do_ss;
+    for (int d = 0; d < D; d += 8) {
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(orow + d);
+      const u32x4_t c = *reinterpret_cast<const u32x4_t*>(drow + d);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dsum += __builtin_bit_cast(float, a[j] << 16) * __builtin_bit_cast(float, c[j] << 16);
+        dsum += __builtin_bit_cast(float, a[j] & 0xFFFF0000u) * __builtin_bit_cast(float, c[j] & 0xFFFF0000u);
+      }
+    }
+    l2 = lse[bh * p.Sq + row] * kLog2e;
+  }
+  float* st = stats + (bh * p.n_qt + row / kTile) * (2 * kTile);
+  st[row % kTile] = l2;
+  st[kTile + row % kTile] = dsum;
+}
+
+// ---------------------------------------------------------------- tile copies
+// A tile = 64 rows of D bf16 in LDS with a row stride of U = D/8 + 1 units
+// of 16 bytes; copy j (1 KB) covers units 64 j .. 64 j + 63 (unit u: row
+// u / U, chunk u % U, the last chunk of a row being padding).  Copy j is
+// issued by wave j % 4.
+template <int D>
+struct TileCopy {
+  static constexpr int CH = D / 8;
+  static constexpr int U = CH + 1;
+  static constexpr int RS = U * 8;              // row stride, elements
+  static constexpr int NC = U;                  // copies per tile
+  static constexpr int NCW = (NC + kWavesB - 1) / kWavesB;
+  static constexpr int ELEMS = NC * 512;        // LDS elements per tile
+  int off[NCW];                                 // this lane's byte offsets (2^31: padding)
+  __device__ void init(int64_t ss, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < NCW; ++i) {
+      const int u = 64 * (kWavesB * i + wave) + lane, row = u / U, ch = u % U;
+      off[i] = (ch < CH) ? (row * int(ss) + ch * 8) * 2 : int(0x80000000u);
+    }
+  }
+  // rows [r0, r0 + 64) of a [rows_total, D] matrix with row stride ss
+  __device__ void issue(const uint16_t* base, int64_t ss, int r0, int rows_total, uint16_t* dst, int wave) const {
+    const int rows = min(kTile, rows_total - r0);  // >= 1
+    const i32x4_t r = tile_desc(base + int64_t(r0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
+#pragma unroll
+    for (int i = 0; i < NCW; ++i)
+      if (kWavesB * i + wave < NC)  // wave-uniform
+        copy_to_lds(r, lds_addr(dst + (kWavesB * i + wave) * 512), off[i]);
+  }
+};
+
+// store 32 rows' worth of a transposed accumulator: lane (c, g) owns row
+// `row` of the output and d = 32 db + 8 r4 + 4 g + 0..3 in acc[db][4 r4 ..]
+template <int NDB>
+__device__ inline void store_rows(uint16_t* out_row, const f32x16_t (&acc)[NDB], float mul, int g) {
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int d = db * 32 + 8 * r4 + 4 * g;
+      const f32x2_t lo = {acc[db][4 * r4 + 0] * mul, acc[db][4 * r4 + 1] * mul};
+      const f32x2_t hi = {acc[db][4 * r4 + 2] * mul, acc[db][4 * r4 + 3] * mul};
+      uint2 w;
+      w.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2_t));
+      w.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2_t));
+      *reinterpret_cast<uint2*>(out_row + d) = w;
+    }
+}
+
+// ---------------------------------------------------------------- dK, dV
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreadsB) void sdpa_bwd_kv_kernel(const BwdArgs p) {
+  using TC = TileCopy<D>;
+  constexpr int RS = TC::RS;
+  constexpr int NKS = D / 16;  // k-steps over d
+  constexpr int NDB = D / 32;  // 32-wide d blocks of dKᵀ / dVᵀ
+
+  __shared__ __attribute__((aligned(1024))) uint16_t Qs[2][TC::ELEMS];
+  __shared__ __attribute__((aligned(1024))) uint16_t Ds[2][TC::ELEMS];
+  __shared__ __attribute__((aligned(1024))) float Ss[2][256];  // lse2[64], D[64], then the zeros of the copy
+
+  // earliest key blocks (most queries) first; consecutive ids walk the heads
+  const int id = blockIdx.x;
+  const int kb = id / p.BH, bh = id % p.BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int kw0 = kb * kBlkRows + wave * 32;  // the wave's first key
+  const int key = kw0 + c;                     // this lane's key (column of S)
+
+  const uint16_t* qb = p.q + b * p.q_bs + h * p.q_hs;
+  const uint16_t* dob = p.dout + b * p.do_bs + h * p.do_hs;
+  const float* stb = p.stats + int64_t(bh) * p.n_qt * (2 * kTile);
+
+  // K, V fragments (B operands of S = Q Kᵀ and dP = dO Vᵀ): row `key`, d = 16 s + 8 g + 0..7
+  bf16x8_t kf[NKS], vf[NKS];
+  {
+    const bool ok = key < p.Sk;
+    const uint16_t* kr = p.k + b * p.k_bs + h * p.k_hs + int64_t(key) * p.k_ss;
+    const uint16_t* vr = p.v + b * p.v_bs + h * p.v_hs + int64_t(key) * p.v_ss;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      u32x4_t a = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
+      if (ok) {
+        a = *reinterpret_cast<const u32x4_t*>(kr + 16 * s + 8 * g);
+        w = *reinterpret_cast<const u32x4_t*>(vr + 16 * s + 8 * g);
+      }
+      kf[s] = as_bf16x8(a);
+      vf[s] = as_bf16x8(w);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no compiler wait inside the loop meets a copy in flight
+  }
+
+  TC qc, dc;
+  qc.init(p.q_ss, wave, lane);
+  dc.init(p.do_ss, wave, lane);
+  const int stat_off = lane < 32 ? lane * 16 : int(0x80000000u);
+  auto issue = [&](int t, int buf) __attribute__((always_inline)) {
+    qc.issue(qb, p.q_ss, t * kTile, p.Sq, Qs[buf], wave);
+    dc.issue(dob, p.do_ss, t * kTile, p.Sq, Ds[buf], wave);
+    if (wave == kWavesB - 1)
+      copy_to_lds(tile_desc(stb + int64_t(t) * (2 * kTile), 2 * kTile * 4), lds_addr(Ss[buf]), stat_off);
+  };
+
+  // lane offsets: row reads (row c, half g) and transposed reads (4-row x 16-col blocks)
+  const int rlane = c * RS + 8 * g;
+  const int tlane = (4 * g + ((lane & 15) >> 2)) * RS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  f32x16_t dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+
+  // first query tile holding a query >= the block's first key
+  const int t0 = CAUSAL ? (kb * kBlkRows) / kTile : 0;
+  const int t_end = p.n_qt;
+
+  auto step = [&](int t, const uint16_t* Q, const uint16_t* DO, const float* st) __attribute__((always_inline)) {
+    bf16x8_t pf[2][2], sf[2][2];
+    bool live[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int qm0 = t * kTile + 32 * mt;
+      live[mt] = qm0 < p.Sq && (!CAUSAL || qm0 + 31 >= kw0);  // wave-uniform
+      if (!live[mt]) continue;
+      f32x16_t s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&Q[rlane + 32 * mt * RS + 16 * ks]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), kf[ks], s, 0, 0, 0);
+      }
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&DO[rlane + 32 * mt * RS + 16 * ks]);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), vf[ks], dp, 0, 0, 0);
+      }
+      // rows of reg r: query qm0 + 8 (r/4) + 4 g + r%4
+      float pr[16], ds[16];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int row = 32 * mt + 8 * r4 + 4 * g;
+        const float4 l2 = *reinterpret_cast<const float4*>(&st[row]);
+        const float4 dd = *reinterpret_cast<const float4*>(&st[kTile + row]);
+        const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * r4 + i;
+          float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -lv[i]));
+          if (CAUSAL && key > t * kTile + row + i) pv = 0.f;
+          pr[r] = pv;
+          ds[r] = pv * (dp[r] - dv4[i]);
+        }
+      }
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) {
+        const int o = 8 * j2;
+        pf[mt][j2] = pack8(pr[o], pr[o + 1], pr[o + 2], pr[o + 3], pr[o + 4], pr[o + 5], pr[o + 6], pr[o + 7]);
+        sf[mt][j2] = pack8(ds[o], ds[o + 1], ds[o + 2], ds[o + 3], ds[o + 4], ds[o + 5], ds[o + 6], ds[o + 7]);
+      }
+    }
+    // dVᵀ += dOᵀ P, dKᵀ += Qᵀ dS over the tile's queries (k-step (mt, j2):
+    // k-slot (g, i) is query 32 mt + 16 j2 + 8 (i/4) + 4 g + i%4)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      if (!live[mt]) continue;
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int off = tlane + (32 * mt + 16 * j2) * RS + db * 32;
+          const uint2 dlo = lds_read_tr(&DO[off]), dhi = lds_read_tr(&DO[off + 8 * RS]);
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u32x4_t{dlo.x, dlo.y, dhi.x, dhi.y}),
+                                                           pf[mt][j2], dv[db], 0, 0, 0);
+          const uint2 qlo = lds_read_tr(&Q[off]), qhi = lds_read_tr(&Q[off + 8 * RS]);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u32x4_t{qlo.x, qlo.y, qhi.x, qhi.y}),
+                                                           sf[mt][j2], dk[db], 0, 0, 0);
+        }
+    }
+  };
+
+  if (t0 < t_end) {
+    issue(t0, 0);
+    wait_copies();
+    lds_barrier();
+    for (int t = t0; t < t_end; t += 2) {
+      if (t + 1 < t_end) issue(t + 1, 1);
+      step(t, Qs[0], Ds[0], Ss[0]);
+      wait_copies();
+      lds_barrier();
+      if (t + 1 >= t_end) break;
+      if (t + 2 < t_end) issue(t + 2, 0);
+      step(t + 1, Qs[1], Ds[1], Ss[1]);
+      wait_copies();
+      lds_barrier();
+    }
+  }
+
+  if (key < p.Sk) {
+    store_rows<NDB>(p.dv + b * p.dv_bs + h * p.dv_hs + int64_t(key) * p.dv_ss, dv, 1.f, g);
+    store_rows<NDB>(p.dk + b * p.dk_bs + h * p.dk_hs + int64_t(key) * p.dk_ss, dk, p.scale, g);
+  }
+}
+
+// ---------------------------------------------------------------- dQ
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreadsB) void sdpa_bwd_q_kernel(const BwdArgs p) {
+  using TC = TileCopy<D>;
+  constexpr int RS = TC::RS;
+  constexpr int NKS = D / 16;
+  constexpr int NDB = D / 32;
+
+  __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][TC::ELEMS];
+  __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][TC::ELEMS];
+
+  // latest query blocks (most keys) first
+  const int id = blockIdx.x;
+  const int qblk = CAUSAL ? (p.n_blk - 1 - id / p.BH) : (id / p.BH);
+  const int bh = id % p.BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int q0 = qblk * kBlkRows + wave * 32;
+  const int qrow = q0 + c;
+
+  const uint16_t* kb = p.k + b * p.k_bs + h * p.k_hs;
+  const uint16_t* vb = p.v + b * p.v_bs + h * p.v_hs;
+
+  // Q, dO fragments (B operands of Sᵀ = K Qᵀ and dPᵀ = V dOᵀ) and the row's stats
+  bf16x8_t qf[NKS], df[NKS];
+  float l2 = INFINITY, dsum = 0.f;
+  {
+    const bool ok = qrow < p.Sq;
+    const uint16_t* qr = p.q + b * p.q_bs + h * p.q_hs + int64_t(qrow) * p.q_ss;
+    const uint16_t* dr = p.dout + b * p.do_bs + h * p.do_hs + int64_t(qrow) * p.do_ss;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      u32x4_t a = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
+      if (ok) {
+        a = *reinterpret_cast<const u32x4_t*>(qr + 16 * s + 8 * g);
+        w = *reinterpret_cast<const u32x4_t*>(dr + 16 * s + 8 * g);
+      }
+      qf[s] = as_bf16x8(a);
+      df[s] = as_bf16x8(w);
+    }
+    if (ok) {
+      const float* st = p.stats + (int64_t(bh) * p.n_qt + qrow / kTile) * (2 * kTile) + qrow % kTile;
+      l2 = st[0];
+      dsum = st[kTile];
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  }
+
+  int kv_end = p.Sk;
+  if (CAUSAL) kv_end = min(kv_end, min(qblk * kBlkRows + kBlkRows, p.Sq));
+  const int n_tiles = (kv_end + kTile - 1) / kTile;
+  // tiles this wave computes (causal: those holding a key <= its last query)
+  const int n_rel = CAUSAL ? min(n_tiles, (q0 + 31) / kTile + 1) : n_tiles;
+
+  TC kc, vc;
+  kc.init(p.k_ss, wave, lane);
+  vc.init(p.v_ss, wave, lane);
+  auto issue = [&](int t, int buf) __attribute__((always_inline)) {
+    kc.issue(kb, p.k_ss, t * kTile, p.Sk, Ks[buf], wave);
+    vc.issue(vb, p.v_ss, t * kTile, p.Sk, Vs[buf], wave);
+  };
+
+  const int rlane = c * RS + 8 * g;
+  const int tlane = (4 * g + ((lane & 15) >> 2)) * RS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  f32x16_t dq[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+
+  auto step = [&](int t, const uint16_t* K, const uint16_t* V) __attribute__((always_inline)) {
+    if (t >= n_rel) return;  // wave-uniform
+    bf16x8_t sf[2][2];
+    bool live[2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      const int kk0 = t * kTile + 32 * kb2;
+      live[kb2] = kk0 < p.Sk && (!CAUSAL || kk0 <= q0 + 31);  // wave-uniform
+      if (!live[kb2]) continue;
+      f32x16_t s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&K[rlane + 32 * kb2 * RS + 16 * ks]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[ks], s, 0, 0, 0);
+      }
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&V[rlane + 32 * kb2 * RS + 16 * ks]);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), df[ks], dp, 0, 0, 0);
+      }
+      // rows of reg r: key kk0 + 8 (r/4) + 4 g + r%4
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = kk0 + 8 * (r / 4) + 4 * g + (r % 4);
+        float pv = __builtin_amdgcn_exp2f(fmaf(s[r], p.scale_log2, -l2));
+        if (kk >= p.Sk || (CAUSAL && kk > qrow)) pv = 0.f;
+        ds[r] = pv * (dp[r] - dsum);
+      }
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) {
+        const int o = 8 * j2;
+        sf[kb2][j2] = pack8(ds[o], ds[o + 1], ds[o + 2], ds[o + 3], ds[o + 4], ds[o + 5], ds[o + 6], ds[o + 7]);
+      }
+    }
+    // dQᵀ += Kᵀ dSᵀ (k-step (kb2, j2): k-slot (g, i) is key 32 kb2 + 16 j2 + 8 (i/4) + 4 g + i%4)
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      if (!live[kb2]) continue;
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int off = tlane + (32 * kb2 + 16 * j2) * RS + db * 32;
+          const uint2 lo = lds_read_tr(&K[off]), hi = lds_read_tr(&K[off + 8 * RS]);
+          dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y}),
+                                                           sf[kb2][j2], dq[db], 0, 0, 0);
+        }
+    }
+  };
+
+  if (n_tiles > 0) {
+    issue(0, 0);
+    wait_copies();
+    lds_barrier();
+    for (int t = 0; t < n_tiles; t += 2) {
+      if (t + 1 < n_tiles) issue(t + 1, 1);
+      step(t, Ks[0], Vs[0]);
+      wait_copies();
+      lds_barrier();
+      if (t + 1 >= n_tiles) break;
+      if (t + 2 < n_tiles) issue(t + 2, 0);
+      step(t + 1, Ks[1], Vs[1]);
+      wait_copies();
+      lds_barrier();
+    }
+  }
+
+  if (qrow < p.Sq) store_rows<NDB>(p.dq + b * p.dq_bs + h * p.dq_hs + int64_t(qrow) * p.dq_ss, dq, p.scale, g);
+}
+
+}  // namespace
+
+size_t sdpa_bwd_flash_workspace(int64_t B, int64_t H, int64_t Sq) {
+  return size_t(B * H * ((Sq + kTile - 1) / kTile) * (2 * kTile) * 4);
+}
+
+// Caller (mk_sdpa_bwd) has checked shapes, D in {64, 128}, pointers and the
+// workspace size; here: alignment and the ranges the kernels index with int.
+int sdpa_bwd_flash(hipStream_t s, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                   const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
+                   const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,
+                   const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ss,
+                   const void* o, int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                   const void* dout, int64_t do_bs, int64_t do_hs, int64_t do_ss, const float* lse,
+                   void* dq, int64_t dq_bs, int64_t dq_hs, int64_t dq_ss,
+                   void* dk, int64_t dk_bs, int64_t dk_hs, int64_t dk_ss,
+                   void* dv, int64_t dv_bs, int64_t dv_hs, int64_t dv_ss,
+                   float scale, int causal, void* workspace) {
+  if (Sq >= (int64_t(1) << 30) || Sk >= (int64_t(1) << 30) || B * H >= (int64_t(1) << 30))
+    return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: sizes too large");
+  // a length-1 sequence axis may carry any stride; only row 0 is read
+  if (Sq == 1) q_ss = o_ss = do_ss = dq_ss = D;
+  if (Sk == 1) k_ss = v_ss = dk_ss = dv_ss = D;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                       reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o) |
+                       reinterpret_cast<uintptr_t>(dout);
+  const int64_t st = q_bs | q_hs | q_ss | k_bs | k_hs | k_ss | v_bs | v_hs | v_ss | o_bs | o_hs | o_ss | do_bs |
+                     do_hs | do_ss;
+  const uintptr_t oal = reinterpret_cast<uintptr_t>(dq) | reinterpret_cast<uintptr_t>(dk) |
+                        reinterpret_cast<uintptr_t>(dv);
+  const int64_t ost = dq_bs | dq_hs | dq_ss | dk_bs | dk_hs | dk_ss | dv_bs | dv_hs | dv_ss;
+  if ((al & 15u) != 0 || (st & 7) != 0 || (oal & 7u) != 0 || (ost & 3) != 0)
+    return fail(MK_ERR_UNSUPPORTED,
+                "mk_sdpa_bwd: q/k/v/o/dO need 16-byte aligned rows (strides % 8 == 0), dq/dk/dv strides % 4 == 0");
+  if (q_ss < D || k_ss < D || v_ss < D || do_ss < D || q_ss >= (int64_t(1) << 24) || k_ss >= (int64_t(1) << 24) ||
+      v_ss >= (int64_t(1) << 24) || do_ss >= (int64_t(1) << 24))
+    return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: q/k/v/dO sequence strides must be in [D, 2^24)");
+  BwdArgs a;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.dout = (const uint16_t*)dout;
+  a.dq = (uint16_t*)dq; a.dk = (uint16_t*)dk; a.dv = (uint16_t*)dv;
+  a.stats = static_cast<const float*>(workspace);
+  a.q_bs = q_bs; a.q_hs = q_hs; a.q_ss = q_ss;
+  a.k_bs = k_bs; a.k_hs = k_hs; a.k_ss = k_ss;
+  a.v_bs = v_bs; a.v_hs = v_hs; a.v_ss = v_ss;
+  a.do_bs = do_bs; a.do_hs = do_hs; a.do_ss = do_ss;
+  a.dq_bs = dq_bs; a.dq_hs = dq_hs; a.dq_ss = dq_ss;
+  a.dk_bs = dk_bs; a.dk_hs = dk_hs; a.dk_ss = dk_ss;
+  a.dv_bs = dv_bs; a.dv_hs = dv_hs; a.dv_ss = dv_ss;
+  a.H = int(H); a.Sq = int(Sq); a.Sk = int(Sk); a.BH = int(B * H);
+  a.n_qt = int((Sq + kTile - 1) / kTile);
+  a.scale_log2 = scale * kLog2e;
+  a.scale = scale;
+
+  const int64_t nstat = int64_t(a.BH) * a.n_qt * kTile;
+  hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3(unsigned((nstat + 255) / 256)), dim3(256), 0, s, a,
+                     (const uint16_t*)o, o_bs, o_hs, o_ss, lse, int(D), static_cast<float*>(workspace));
+  if (int rc = check_launch("mk_sdpa_bwd")) return rc;
+
+  const int n_kb = int((Sk + kBlkRows - 1) / kBlkRows), n_qb = int((Sq + kBlkRows - 1) / kBlkRows);
+  if (int64_t(n_kb) * a.BH >= (int64_t(1) << 31) || int64_t(n_qb) * a.BH >= (int64_t(1) << 31))
+    return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: grid too large");
+  const dim3 bl{unsigned(kThreadsB)};
+  a.n_blk = n_kb;
+  const dim3 gkv{unsigned(int64_t(n_kb) * a.BH)};
+  if (D == 128) {
+    if (causal) hipLaunchKernelGGL((sdpa_bwd_kv_kernel<128, true>), gkv, bl, 0, s, a);
+    else hipLaunchKernelGGL((sdpa_bwd_kv_kernel<128, false>), gkv, bl, 0, s, a);
+  } else {
+    if (causal) hipLaunchKernelGGL((sdpa_bwd_kv_kernel<64, true>), gkv, bl, 0, s, a);
+    else hipLaunchKernelGGL((sdpa_bwd_kv_kernel<64, false>), gkv, bl, 0, s, a);
+  }
+  if (int rc = check_launch("mk_sdpa_bwd")) return rc;
+  a.n_blk = n_qb;
+  const dim3 gq{unsigned(int64_t(n_qb) * a.BH)};
+  if (D == 128) {
+    if (causal) hipLaunchKernelGGL((sdpa_bwd_q_kernel<128, true>), gq, bl, 0, s, a);
+    else hipLaunchKernelGGL((sdpa_bwd_q_kernel<128, false>), gq, bl, 0, s, a);
+  } else {
+    if (causal) hipLaunchKernelGGL((sdpa_bwd_q_kernel<64, true>), gq, bl, 0, s, a);
+    else hipLaunchKernelGGL((sdpa_bwd_q_kernel<64, false>), gq, bl, 0, s, a);
+  }
+  return check_launch("mk_sdpa_bwd");
+}
+
+}  // namespace mk

@@ -25,6 +25,20 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
               const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
 
+// Flash attention backward behind mk_sdpa_bwd for head_dim 64 / 128
+// (attention_bwd.hip); workspace: the per-row statistics.
+size_t sdpa_bwd_flash_workspace(int64_t B, int64_t H, int64_t Sq);
+int sdpa_bwd_flash(hipStream_t s, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                   const void* q, int64_t q_bs, int64_t q_hs, int64_t q_ss,
+                   const void* k, int64_t k_bs, int64_t k_hs, int64_t k_ss,
+                   const void* v, int64_t v_bs, int64_t v_hs, int64_t v_ss,
+                   const void* o, int64_t o_bs, int64_t o_hs, int64_t o_ss,
+                   const void* dout, int64_t do_bs, int64_t do_hs, int64_t do_ss, const float* lse,
+                   void* dq, int64_t dq_bs, int64_t dq_hs, int64_t dq_ss,
+                   void* dk, int64_t dk_bs, int64_t dk_hs, int64_t dk_ss,
+                   void* dv, int64_t dv_bs, int64_t dv_hs, int64_t dv_ss,
+                   float scale, int causal, void* workspace);
+
 // ---------------------------------------------------------------- dtypes
 inline int dtype_bytes(int t) {
   switch (t) {

@@ -548,8 +548,9 @@ extern "C" int mk_adam_update(void* stream, int64_t n, int param_type, void* par
   return check_launch("mk_adam_update");
 }
 
-extern "C" size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
+extern "C" size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
   if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0) return 0;
+  if (D == 64 || D == 128) return sdpa_bwd_flash_workspace(B, H, Sq);
   const int64_t n = B * H * Sq * Sk;
   return size_t(align256(n * 4) + align256(n * 2) + align256(B * H * Sq * 4));
 }
@@ -571,6 +572,10 @@ extern "C" int mk_sdpa_bwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
   if (B == 0 || H == 0 || Sq == 0 || Sk == 0) return MK_OK;
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !workspace)
     return fail(MK_ERR_INVALID, "mk_sdpa_bwd: null pointer");
+  if (D == 64 || D == 128)
+    return sdpa_bwd_flash(as_stream(stream), B, H, Sq, Sk, D, q, q_bs, q_hs, q_ss, k, k_bs, k_hs, k_ss, v, v_bs, v_hs,
+                          v_ss, o, o_bs, o_hs, o_ss, dout, do_bs, do_hs, do_ss, lse, dq, dq_bs, dq_hs, dq_ss, dk, dk_bs,
+                          dk_hs, dk_ss, dv, dv_bs, dv_hs, dv_ss, scale, causal, workspace);
   const uintptr_t al = reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(dout);
   if ((al & 15) != 0 || ((o_bs | o_hs | o_ss | do_bs | do_hs | do_ss) & 7) != 0)
     return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_bwd: o and dO rows must be 16-byte aligned");

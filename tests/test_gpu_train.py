@@ -236,6 +236,55 @@ def test_sdpa_bwd(K, B, H, S, D, causal):
         assert err < 2.5e-2, (name, err)
 
 
+def _bwd_vs_float64(K, B, H, Sq, Sk, D, causal, seed):
+    """mk_sdpa_bwd on bf16 inputs with o, lse of the float64 forward, against
+    float64 autograd; returns the GPU gradients."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Sq, D, generator=g).bfloat16()
+    k = torch.randn(B, H, Sk, D, generator=g).bfloat16()
+    v = (torch.randn(B, H, Sk, D, generator=g) * 0.5).bfloat16()
+    do = torch.randn(B, H, Sq, D, generator=g).bfloat16()
+    scale = 1 / math.sqrt(D)
+    qr, kr, vr = (t.double().requires_grad_(True) for t in (q, k, v))
+    s = (qr @ kr.transpose(-1, -2)) * scale
+    if causal:
+        s = s.masked_fill(~torch.ones(Sq, Sk, dtype=torch.bool).tril(), float("-inf"))
+    o = torch.softmax(s, -1) @ vr
+    o.backward(do.double())
+    lse = torch.logsumexp(s.detach(), -1).float().cuda()
+    dq, dk, dv = K.sdpa_bwd(q.cuda(), k.cuda(), v.cuda(), o.detach().bfloat16().cuda(), do.cuda(), lse, scale, causal)
+    floor = 1e-3 * float(do.double().norm())
+    for got, want, name in ((dq, qr.grad, "dq"), (dk, kr.grad, "dk"), (dv, vr.grad, "dv")):
+        err = float((_f64(got) - want).norm()) / max(float(want.norm()), floor)
+        assert err < 2.5e-2, (name, err)
+        assert bool(torch.isfinite(got).all()), name
+    return dq, dk, dv
+
+
+# flash path (D 64 / 128): ragged tiles, Sq != Sk both ways, the C5 sequence
+# length; D 96: the materialised path
+@pytest.mark.parametrize("B,H,Sq,Sk,D,causal", [
+    (1, 2, 1024, 1024, 64, True), (1, 1, 200, 200, 64, True), (2, 1, 300, 300, 128, False),
+    (1, 2, 70, 200, 64, False), (1, 1, 200, 70, 64, True), (1, 1, 70, 200, 128, True),
+    (1, 1, 129, 129, 128, True), (1, 2, 65, 33, 64, False), (1, 2, 100, 100, 96, True)])
+def test_sdpa_bwd_vs_float64(K, B, H, Sq, Sk, D, causal):
+    print(f"case: sdpa_bwd B{B} H{H} Sq{Sq} Sk{Sk} D{D} causal={causal}", flush=True)
+    _bwd_vs_float64(K, B, H, Sq, Sk, D, causal, seed=Sq * 7 + Sk + D)
+
+
+def test_sdpa_bwd_deterministic(K):
+    """No atomics: two runs give identical bits."""
+    g = torch.Generator().manual_seed(4)
+    B, H, S, D = 2, 3, 320, 64
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g).bfloat16().cuda() for _ in range(4))
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    o = K.sdpa_fwd(q, k, v, 0.125, True, lse=lse)
+    r1 = K.sdpa_bwd(q, k, v, o, do, lse, 0.125, True)
+    r2 = K.sdpa_bwd(q, k, v, o, do, lse, 0.125, True)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
 def test_sdpa_bwd_strided_head_split(K):
     """q, k, v as column slices of one [B*S, 3*H*D] projection (the GPT-2
     layout), dq/dk/dv written into the same layout."""
