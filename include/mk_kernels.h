@@ -296,16 +296,27 @@ size_t mk_col_sum_workspace_bytes(int64_t rows, int64_t cols);
 int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols, const void* x, float* y,
                void* workspace);
 
+/* mk_gelu_tanh_bwd over a dense [rows, cols] array fused with mk_col_sum of
+ * its output: dx = dy * gelu_tanh'(x) and dx_colsum[c] = sum_r dx[r, c] (the
+ * MLP bias gradient) in one pass over x and dy.  Workspace as mk_col_sum's;
+ * dx may alias dy. */
+int mk_gelu_tanh_bwd_colsum(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                            const void* dy, void* dx, float* dx_colsum, void* workspace);
+
 /* LayerNorm backward for y = (x - mean) rstd gamma + beta over rows of `cols`
  * (mean / rstd recomputed from x as mk_layernorm computes them):
- *   dx = rstd (g - mean(g) - xh mean(g xh)),  g = dy gamma, xh = (x - mean) rstd
- *   dgamma = sum_rows dy xh,  dbeta = sum_rows dy   (fp32, deterministic)
- * io_type ∈ {MK_BF16, MK_F32} for x, gamma, dy, dx; cols ≤ 2048; gamma may be
- * NULL (1); dgamma / dbeta both NULL skips them (then no workspace needed). */
+ *   dx = rstd (g - mean(g) - xh mean(g xh)) + dres,  g = dy gamma, xh = (x - mean) rstd
+ *   dgamma = sum_rows dy xh,  dbeta = sum_rows dy,  dx_colsum = sum_rows dx
+ * (fp32, deterministic).  dres (may be NULL; may alias dx) is the residual
+ * branch's gradient, so the pre-LN block's dx = dres + LN'(dy) is one pass;
+ * dx_colsum (may be NULL) is the bias gradient of the preceding projection.
+ * io_type ∈ {MK_BF16, MK_F32} for x, gamma, dy, dres, dx; cols ≤ 2048; gamma
+ * may be NULL (1); dgamma / dbeta both NULL skips them; the workspace is
+ * needed when dgamma or dx_colsum is given. */
 size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
-                     const void* gamma, const void* dy, float eps, void* dx, float* dgamma,
-                     float* dbeta, void* workspace);
+                     const void* gamma, const void* dy, const void* dres, float eps, void* dx,
+                     float* dgamma, float* dbeta, float* dx_colsum, void* workspace);
 
 /* Softmax cross-entropy over rows of logits, loss and gradient together:
  *   lse_r = log sum_j exp(x[r, j]);  loss_rows[r] = lse_r - x[r, labels[r]]

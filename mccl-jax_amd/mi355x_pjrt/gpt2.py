@@ -196,7 +196,6 @@ class GPT2TrainStep:
         self.tmp = torch.empty(T, d, **bf)
         self.dx = torch.empty(T, d, **bf)
         self.dh = torch.empty(T, d, **bf)
-        self.dln = torch.empty(T, d, **bf)
         self.dff = torch.empty(T, c.d_ff, **bf)
         self.dqkv = torch.empty(T, 3 * d, **bf)
         self.dx32 = torch.empty(T, d, dtype=torch.float32, device=dev)
@@ -246,9 +245,12 @@ class GPT2TrainStep:
         def colsum(x, rows, cols, out):
             calls.append(_Call(lib.mk_col_sum, [st, _I(BF16), _I64(rows), _I64(cols), x, out, ws], "mk_col_sum"))
 
-        def ln_bwd(x, gname, dy, dx, prefix):
+        def ln_bwd(x, gname, dy, dres, dx, prefix, colsum_out):
+            """dx = dres + LN'(dy), its LN parameter gradients and (when
+            colsum_out is given) the column sums of dx in one pass"""
             calls.append(_Call(lib.mk_layernorm_bwd, [st, _I(BF16), _I64(T), _I64(d), x, W(gname), dy,
-                                                      _F(c.ln_eps), dx, G(prefix + "_g"), G(prefix + "_b"), ws],
+                                                      dres or _P(0), _F(c.ln_eps), dx, G(prefix + "_g"),
+                                                      G(prefix + "_b"), colsum_out or _P(0), ws],
                                "mk_layernorm_bwd"))
 
         scale = 1.0 / math.sqrt(hd)
@@ -290,23 +292,23 @@ class GPT2TrainStep:
         dlog = P(self.logits)
         gemm(BF16, BF16, T, d, V, dlog, V, 1, W("wte"), d, 1, P(self.dh), d, tag="dhf")
         gemm(BF16, F32, V, d, T, dlog, 1, V, P(self.hf), d, 1, G("wte"), d, tag="dwte")
-        ln_bwd(P(self.x[L]), "lnf_g", P(self.dh), P(self.dx), "lnf")
+        # the bias gradient of each residual projection is the column sum of
+        # the residual-stream gradient, produced by the LayerNorm backward
+        # that writes it
+        ln_bwd(P(self.x[L]), "lnf_g", P(self.dh), None, P(self.dx), "lnf", G(f"h{L - 1}.b_pr"))
         for l in reversed(range(L)):
             p = f"h{l}."
             # MLP branch of x[l+1] = xm + proj(gelu(fc(ln2(xm))))
             gemm(BF16, F32, F, d, T, P(self.g[l]), 1, F, P(self.dx), d, 1, G(p + "w_pr"), d, tag="dw_pr")
-            colsum(P(self.dx), T, d, G(p + "b_pr"))
             gemm(BF16, BF16, T, F, d, P(self.dx), d, 1, W(p + "w_pr"), 1, d, P(self.dff), F, tag="dg")
-            calls.append(_Call(lib.mk_gelu_tanh_bwd, [st, _I(BF16), _I64(T * F), P(self.f[l]), P(self.dff),
-                                                      P(self.dff)], "mk_gelu_tanh_bwd"))
+            calls.append(_Call(lib.mk_gelu_tanh_bwd_colsum, [st, _I(BF16), _I64(T), _I64(F), P(self.f[l]),
+                                                             P(self.dff), P(self.dff), G(p + "b_fc"), ws],
+                               "mk_gelu_tanh_bwd_colsum"))
             gemm(BF16, F32, d, F, T, P(self.h2[l]), 1, d, P(self.dff), F, 1, G(p + "w_fc"), F, tag="dw_fc")
-            colsum(P(self.dff), T, F, G(p + "b_fc"))
             gemm(BF16, BF16, T, d, F, P(self.dff), F, 1, W(p + "w_fc"), 1, F, P(self.dh), d, tag="dh2")
-            ln_bwd(P(self.xm[l]), p + "ln2_g", P(self.dh), P(self.dln), p + "ln2")
-            add_rows(P(self.dx), T, d, P(self.dx), P(self.dln))
+            ln_bwd(P(self.xm[l]), p + "ln2_g", P(self.dh), P(self.dx), P(self.dx), p + "ln2", G(p + "b_o"))
             # attention branch of xm = x[l] + o(attn(ln1(x[l])))
             gemm(BF16, F32, d, d, T, P(self.att[l]), 1, d, P(self.dx), d, 1, G(p + "w_o"), d, tag="dw_o")
-            colsum(P(self.dx), T, d, G(p + "b_o"))
             gemm(BF16, BF16, T, d, d, P(self.dx), d, 1, W(p + "w_o"), 1, d, P(self.dh), d, tag="datt")
             q, k, v = (P(self.qkv[l], i * d) for i in range(3))
             dq, dk, dv = (P(self.dqkv, i * d) for i in range(3))
@@ -321,8 +323,8 @@ class GPT2TrainStep:
             colsum(P(self.dqkv), T, 3 * d, G(p + "b_qkv"))
             gemm(BF16, BF16, T, d, 3 * d, P(self.dqkv), 3 * d, 1, W(p + "w_qkv"), 1, 3 * d, P(self.dh), d,
                  tag="dh1")
-            ln_bwd(P(self.x[l]), p + "ln1_g", P(self.dh), P(self.dln), p + "ln1")
-            add_rows(P(self.dx), T, d, P(self.dx), P(self.dln))
+            ln_bwd(P(self.x[l]), p + "ln1_g", P(self.dh), P(self.dx), P(self.dx), p + "ln1",
+                   G(f"h{l - 1}.b_pr") if l > 0 else None)
         # embeddings: position gradient = sum over the batch; token gradient
         # scattered (in token order) into the head's embedding gradient
         colsum(P(self.dx), B, S * d, G("wpe"))

@@ -318,8 +318,9 @@ def col_sum(x, out=None, workspace=None, stream=None):
 
 
 def layernorm_bwd(x, gamma, dy, eps=1e-5, dx=None, dgamma=None, dbeta=None, workspace=None, want_params=True,
-                  stream=None):
-    """(dx, dgamma, dbeta) of LayerNorm over the last axis (fp32 dgamma/dbeta)."""
+                  dres=None, want_colsum=False, stream=None):
+    """(dx, dgamma, dbeta[, dx_colsum]) of LayerNorm over the last axis (fp32
+    dgamma/dbeta/colsum); dx = LN'(dy) + dres when dres is given."""
     _require_cuda(x, dy)
     cols = x.shape[-1]
     rows = x.numel() // cols
@@ -327,12 +328,26 @@ def layernorm_bwd(x, gamma, dy, eps=1e-5, dx=None, dgamma=None, dbeta=None, work
     if want_params:
         dgamma = torch.empty(cols, dtype=torch.float32, device=x.device) if dgamma is None else dgamma
         dbeta = torch.empty(cols, dtype=torch.float32, device=x.device) if dbeta is None else dbeta
+    colsum = torch.empty(cols, dtype=torch.float32, device=x.device) if want_colsum else None
     ws = _ws(lib().mk_layernorm_bwd_workspace_bytes(rows, cols), x.device, workspace)
     rc = lib().mk_layernorm_bwd(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(gamma), _ptr(dy),
-                                float(eps), _ptr(dx), _ptr(dgamma if want_params else None),
-                                _ptr(dbeta if want_params else None), _ptr(ws))
+                                _ptr(dres), float(eps), _ptr(dx), _ptr(dgamma if want_params else None),
+                                _ptr(dbeta if want_params else None), _ptr(colsum), _ptr(ws))
     _check(rc, "mk_layernorm_bwd")
-    return dx, dgamma, dbeta
+    return (dx, dgamma, dbeta, colsum) if want_colsum else (dx, dgamma, dbeta)
+
+
+def gelu_tanh_bwd_colsum(x, dy, out=None, workspace=None, stream=None):
+    """(dx, dx column sums in fp32) of dx = dy * gelu_tanh'(x) on 2-D x."""
+    _require_cuda(x, dy)
+    rows, cols = x.shape
+    out = torch.empty_like(x) if out is None else out
+    colsum = torch.empty(cols, dtype=torch.float32, device=x.device)
+    ws = _ws(lib().mk_col_sum_workspace_bytes(rows, cols), x.device, workspace)
+    rc = lib().mk_gelu_tanh_bwd_colsum(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(dy), _ptr(out),
+                                       _ptr(colsum), _ptr(ws))
+    _check(rc, "mk_gelu_tanh_bwd_colsum")
+    return out, colsum
 
 
 def softmax_xent(logits, labels, grad_scale, loss_rows=None, dlogits=None, stream=None):

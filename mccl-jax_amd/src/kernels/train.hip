@@ -10,6 +10,8 @@
 #include "mk_common.h"
 
 #include <cmath>
+#include <initializer_list>
+#include <type_traits>
 
 namespace mk {
 namespace {
@@ -69,10 +71,136 @@ __global__ __launch_bounds__(kBlock) void gelu_bwd_bf16x8_kernel(const u32x4_t* 
 }
 
 // ---------------------------------------------------------------- column sums
-// Pass 1: block b sums rows [b*rpb, (b+1)*rpb) of every column into its
-// partial row; thread t owns columns t, t + 256, ... and adds its rows in
-// order.  Pass 2 (col_final_kernel) adds the partial rows.
-constexpr int64_t kColChunk = 8 * kBlock;  // columns per block along grid y
+// Row data moves as 16-byte vectors: NV elements of T, widened to fp32.
+template <typename T> struct RowVec;
+template <> struct RowVec<uint16_t> {
+  static constexpr int NV = 8;
+  __device__ static void unpack(const u32x4_t& v, float (&f)[NV]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[2 * j] = lo16(v[j]);
+      f[2 * j + 1] = hi16(v[j]);
+    }
+  }
+  __device__ static u32x4_t pack(const float (&f)[NV]) {
+    u32x4_t v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = pack_bf16(f[2 * j], f[2 * j + 1]);
+    return v;
+  }
+};
+template <> struct RowVec<float> {
+  static constexpr int NV = 4;
+  __device__ static void unpack(const u32x4_t& v, float (&f)[NV]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = v[j];  // bit_cast of the vector element itself reads element 0 (hipcc)
+      f[j] = __builtin_bit_cast(float, w);
+    }
+  }
+  __device__ static u32x4_t pack(const float (&f)[NV]) {
+    u32x4_t v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = __builtin_bit_cast(uint32_t, f[j]);
+    return v;
+  }
+};
+
+// Pass 1, column partials over 16-byte vectors.  Block (bx, by) covers rows
+// [bx rpb, bx rpb + rpb) and the 64 NV columns from by 64 NV: thread t owns
+// column vector t % 64 and visits rows r0 + t / 64, + 4, ..., loading four
+// of its rows before using any (Op::load), then Op::apply turns each into NV
+// values (computing and storing whatever the pass writes).  The four row
+// lanes are added in lane order through LDS into partial row bx.
+constexpr int kRowLanes = kBlock / 64;
+
+template <typename T, class Op>
+__device__ inline void col_partial_body(const Op& op, int64_t rows, int64_t cols, int64_t rpb,
+                                        float* __restrict__ part) {
+  constexpr int NV = RowVec<T>::NV, BC = 64 * NV, UNR = 4;
+  __shared__ float red[kRowLanes][BC];
+  const int cv = threadIdx.x & 63, rl = threadIdx.x >> 6;
+  const int64_t r0 = int64_t(blockIdx.x) * rpb, r1 = min(rows, r0 + rpb);
+  const int64_t cb = int64_t(blockIdx.y) * BC, c = cb + cv * NV;
+  float acc[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) acc[j] = 0.f;
+  if (c < cols) {
+    for (int64_t r = r0 + rl; r < r1; r += UNR * kRowLanes) {
+      typename Op::Raw raw[UNR];
+#pragma unroll
+      for (int u = 0; u < UNR; ++u)
+        if (r + u * kRowLanes < r1) raw[u] = op.load(r + u * kRowLanes, c);
+#pragma unroll
+      for (int u = 0; u < UNR; ++u)
+        if (r + u * kRowLanes < r1) {
+          float f[NV];
+          op.apply(r + u * kRowLanes, c, raw[u], f);
+#pragma unroll
+          for (int j = 0; j < NV; ++j) acc[j] += f[j];
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) red[rl][cv * NV + j] = acc[j];
+  __syncthreads();
+  for (int i = threadIdx.x; i < BC; i += kBlock)
+    if (cb + i < cols) {
+      float t = red[0][i];
+#pragma unroll
+      for (int l = 1; l < kRowLanes; ++l) t += red[l][i];
+      part[int64_t(blockIdx.x) * cols + cb + i] = t;
+    }
+}
+
+template <typename T>
+struct SumOp {
+  using Raw = u32x4_t;
+  const T* x;
+  int64_t cols;
+  __device__ Raw load(int64_t r, int64_t c) const { return *reinterpret_cast<const u32x4_t*>(x + r * cols + c); }
+  __device__ void apply(int64_t, int64_t, const Raw& v, float (&f)[RowVec<T>::NV]) const { RowVec<T>::unpack(v, f); }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void col_partial_vec_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                               int64_t rpb, float* __restrict__ part) {
+  col_partial_body<T>(SumOp<T>{x, cols}, rows, cols, rpb, part);
+}
+
+// dx = dy * gelu_tanh'(x), stored, and its column partials
+template <typename T>
+struct GeluBwdOp {
+  struct Raw {
+    u32x4_t x, dy;
+  };
+  const T* x;
+  const T* dy;
+  T* dx;
+  int64_t cols;
+  __device__ Raw load(int64_t r, int64_t c) const {
+    return Raw{*reinterpret_cast<const u32x4_t*>(x + r * cols + c), *reinterpret_cast<const u32x4_t*>(dy + r * cols + c)};
+  }
+  __device__ void apply(int64_t r, int64_t c, const Raw& v, float (&f)[RowVec<T>::NV]) const {
+    constexpr int NV = RowVec<T>::NV;
+    float xf[NV], df[NV];
+    RowVec<T>::unpack(v.x, xf);
+    RowVec<T>::unpack(v.dy, df);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) f[j] = df[j] * gelu_tanh_grad_f32(xf[j]);
+    *reinterpret_cast<u32x4_t*>(dx + r * cols + c) = RowVec<T>::pack(f);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gelu_bwd_cols_kernel(const T* x, const T* dy, T* dx, int64_t rows,
+                                                             int64_t cols, int64_t rpb, float* __restrict__ part) {
+  col_partial_body<T>(GeluBwdOp<T>{x, dy, dx, cols}, rows, cols, rpb, part);
+}
+
+// Scalar pass 1 for rows that are not whole 16-byte vectors: block b sums
+// rows [b rpb, b rpb + rpb) of columns by 2048 + t, + 256, ... in row order.
+constexpr int64_t kColChunk = 8 * kBlock;
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void col_partial_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
@@ -86,15 +214,21 @@ __global__ __launch_bounds__(kBlock) void col_partial_kernel(const T* __restrict
   }
 }
 
-// y[c] = sum over nparts partial rows.  A block covers 32 columns with 8
-// groups of threads; group j adds partials j, j + 8, ... in order (eight
-// loads in flight per thread), then the 8 group sums are added in group
-// order: a fixed summation tree, so the result is deterministic.
-constexpr int kFinCols = 32, kFinGroups = kBlock / kFinCols;
+// Pass 2: y[c] = sum of the nparts partial rows, for up to three (partials,
+// output) pairs (grid y).  A block covers 16 columns with 16 groups of
+// threads; group j adds partials j, j + 16, ... in order (eight loads in
+// flight), then the group sums are added in group order: a fixed summation
+// tree, so the result is deterministic.
+constexpr int kFinCols = 16, kFinGroups = kBlock / kFinCols;
 
-__global__ __launch_bounds__(kBlock) void col_final_kernel(const float* __restrict__ part, int64_t nparts,
-                                                         int64_t cols, float* __restrict__ y) {
+struct FinalJob {
+  const float* part[3];
+  float* out[3];
+};
+
+__global__ __launch_bounds__(kBlock) void col_final_kernel(const FinalJob job, int64_t nparts, int64_t cols) {
   __shared__ float red[kFinGroups][kFinCols];
+  const float* __restrict__ part = job.part[blockIdx.y];
   const int cl = threadIdx.x % kFinCols, grp = threadIdx.x / kFinCols;
   const int64_t c = int64_t(blockIdx.x) * kFinCols + cl;
   float acc = 0.f;
@@ -115,57 +249,117 @@ __global__ __launch_bounds__(kBlock) void col_final_kernel(const float* __restri
     float t = red[0][cl];
 #pragma unroll
     for (int j = 1; j < kFinGroups; ++j) t += red[j][cl];
-    y[c] = t;
+    job.out[blockIdx.y][c] = t;
   }
 }
 
-inline unsigned final_blocks(int64_t cols) { return unsigned((cols + kFinCols - 1) / kFinCols); }
-
 inline int64_t col_parts(int64_t rows) { return std::min<int64_t>(512, std::max<int64_t>(1, (rows + 15) / 16)); }
 
+// launches pass 2 for n pairs
+int col_final(hipStream_t s, int n, const float* const* parts, float* const* outs, int64_t nparts, int64_t cols) {
+  FinalJob job{};
+  for (int i = 0; i < n; ++i) {
+    job.part[i] = parts[i];
+    job.out[i] = outs[i];
+  }
+  const dim3 g(unsigned((cols + kFinCols - 1) / kFinCols), unsigned(n));
+  hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, job, nparts, cols);
+  return check_launch("column sum final pass");
+}
+
 // ---------------------------------------------------------------- LayerNorm bwd
-// One wave per row (rows of up to 64 * 8 * KV columns held in registers as
-// fp32); the row's mean / rstd are recomputed from x exactly as the forward
-// computes them (two-pass).  With xh = (x - mean) rstd and g = dy * gamma:
-//   dx = rstd (g - mean(g) - xh mean(g xh)),
-// and the wave adds dy * xh and dy into its lanes' dgamma / dbeta partials
-// over the rows it visits (rows w, w + W, ... for W waves in the grid), which
-// go to the workspace as one partial row per wave.
-template <typename T, int KV>
-__global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
-                                                             const T* __restrict__ dy, int64_t rows, int cols,
-                                                             float eps, T* __restrict__ dx,
-                                                             float* __restrict__ part_g, float* __restrict__ part_b) {
-  constexpr int NV = 8;  // columns per lane per vector step
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
-  const int64_t nwaves = int64_t(gridDim.x) * (kBlock / 64);
+// One wave per row (rows of up to 64 NV KV columns held in registers as
+// fp32, NV consecutive columns per lane per step); the row's mean / rstd are
+// recomputed from x exactly as the forward computes them (two-pass).  With
+// xh = (x - mean) rstd and g = dy gamma:
+//   dx = rstd (g - mean(g) - xh mean(g xh))  (+ dres, the residual branch),
+// Block b owns rows [b rpb, b rpb + rpb), its wave w rows r0 + w, + 4, ...;
+// on the vector path the next row's loads are issued before the current
+// row's arithmetic.  Each lane adds dy xh, dy and the stored dx into
+// per-column accumulators, which the block adds in wave order through LDS
+// into its partial rows of dgamma, dbeta and colsum(dx).
+struct LnBwdArgs {
+  const void* x;
+  const void* gamma;
+  const void* dy;
+  const void* dres;
+  void* dx;
+  int64_t rows, rpb;
+  int cols;
+  float eps;
+  float* part_g;
+  float* part_b;
+  float* part_s;
+};
+
+constexpr int kLnBwdMaxCols = 2048;
+
+template <typename T, int KV, bool VEC>
+__global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a) {
+  using RV = RowVec<T>;
+  constexpr int NV = RV::NV;
+  __shared__ float red[kLnBwdMaxCols];
+  const T* __restrict__ x = static_cast<const T*>(a.x);
+  const T* __restrict__ gamma = static_cast<const T*>(a.gamma);
+  const T* __restrict__ dy = static_cast<const T*>(a.dy);
+  const T* dres = static_cast<const T*>(a.dres);
+  T* dx = static_cast<T*>(a.dx);
+  const int cols = a.cols;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const float inv_n = 1.f / float(cols);
-  float gam[KV][NV], accg[KV][NV], accb[KV][NV];
+  float gam[KV][NV], accg[KV][NV], accb[KV][NV], accs[KV][NV];
 #pragma unroll
   for (int k = 0; k < KV; ++k)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int c = (k * 64 + lane) * NV + j;
       gam[k][j] = (c < cols) ? (gamma ? ldf<T>(gamma, c) : 1.f) : 0.f;
-      accg[k][j] = 0.f;
-      accb[k][j] = 0.f;
+      accg[k][j] = accb[k][j] = accs[k][j] = 0.f;
     }
-  for (int64_t r = wave; r < rows; r += nwaves) {
-    const T* xr = x + r * cols;
-    const T* dr = dy + r * cols;
-    float xv[KV][NV], dv[KV][NV];
-    float s = 0.f;
+  const int64_t r0 = int64_t(blockIdx.x) * a.rpb, r1 = min(a.rows, r0 + a.rpb);
+  u32x4_t xr[KV], dr[KV], rr[KV];
+  auto fetch = [&](int64_t r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      const int c0 = (k * 64 + lane) * NV;
+      xr[k] = dr[k] = rr[k] = u32x4_t{0u, 0u, 0u, 0u};
+      if (r < r1 && c0 < cols) {
+        xr[k] = *reinterpret_cast<const u32x4_t*>(x + r * cols + c0);
+        dr[k] = *reinterpret_cast<const u32x4_t*>(dy + r * cols + c0);
+        if (dres) rr[k] = *reinterpret_cast<const u32x4_t*>(dres + r * cols + c0);
+      }
+    }
+  };
+  int64_t r = r0 + wid;
+  if constexpr (VEC) fetch(r);
+  for (; r < r1; r += kRowLanes) {
+    float xv[KV][NV], dv[KV][NV], rv[KV][NV];
+    if constexpr (VEC) {
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        RV::unpack(xr[k], xv[k]);
+        RV::unpack(dr[k], dv[k]);
+        RV::unpack(rr[k], rv[k]);
+      }
+      fetch(r + kRowLanes);
+    } else {
+#pragma unroll
+      for (int k = 0; k < KV; ++k)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const int c = (k * 64 + lane) * NV + j;
+          const bool ok = c < cols;
+          xv[k][j] = ok ? ldf<T>(x, r * cols + c) : 0.f;
+          dv[k][j] = ok ? ldf<T>(dy, r * cols + c) : 0.f;
+          rv[k][j] = (ok && dres) ? ldf<T>(dres, r * cols + c) : 0.f;
+        }
+    }
+    float sx = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const int c = (k * 64 + lane) * NV + j;
-        xv[k][j] = (c < cols) ? ldf<T>(xr, c) : 0.f;
-        dv[k][j] = (c < cols) ? ldf<T>(dr, c) : 0.f;
-        s += xv[k][j];
-      }
-    const float mean = wave_sum(s) * inv_n;
+      for (int j = 0; j < NV; ++j) sx += xv[k][j];
+    const float mean = wave_sum(sx) * inv_n;
     float q = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
@@ -175,7 +369,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const T* __restri
         const float d = (c < cols) ? xv[k][j] - mean : 0.f;
         q += d * d;
       }
-    const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + eps);
+    const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + a.eps);
     float sg = 0.f, sgx = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
@@ -191,35 +385,54 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const T* __restri
         xv[k][j] = xh;
       }
     const float mg = wave_sum(sg) * inv_n, mgx = wave_sum(sgx) * inv_n;
-    T* dxr = dx + r * cols;
 #pragma unroll
-    for (int k = 0; k < KV; ++k)
-#pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const int c = (k * 64 + lane) * NV + j;
-        if (c < cols) stf<T>(dxr, c, rstd * (dv[k][j] * gam[k][j] - mg - xv[k][j] * mgx));
-      }
-  }
-  if (part_g) {
-#pragma unroll
-    for (int k = 0; k < KV; ++k)
+    for (int k = 0; k < KV; ++k) {
+      float o[NV];
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int c = (k * 64 + lane) * NV + j;
-        if (c < cols) {
-          part_g[wave * cols + c] = accg[k][j];
-          part_b[wave * cols + c] = accb[k][j];
-        }
+        o[j] = rstd * (dv[k][j] * gam[k][j] - mg - xv[k][j] * mgx) + rv[k][j];
+        accs[k][j] += o[j];
       }
+      const int c0 = (k * 64 + lane) * NV;
+      if constexpr (VEC) {
+        if (c0 < cols) *reinterpret_cast<u32x4_t*>(dx + r * cols + c0) = RV::pack(o);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+          if (c0 + j < cols) stf<T>(dx, r * cols + c0 + j, o[j]);
+      }
+    }
   }
+  // block partial rows, the four waves added in wave order
+  auto block_rows = [&](const float (&acc)[KV][NV], float* part) __attribute__((always_inline)) {
+    for (int w = 0; w < kRowLanes; ++w) {
+      if (wid == w) {
+#pragma unroll
+        for (int k = 0; k < KV; ++k)
+#pragma unroll
+          for (int j = 0; j < NV; ++j) {
+            const int c = (k * 64 + lane) * NV + j;
+            if (c < cols) red[c] = (w == 0) ? acc[k][j] : red[c] + acc[k][j];
+          }
+      }
+      __syncthreads();
+    }
+    for (int c = threadIdx.x; c < cols; c += kBlock) part[int64_t(blockIdx.x) * cols + c] = red[c];
+    __syncthreads();
+  };
+  if (a.part_g) {
+    block_rows(accg, a.part_g);
+    block_rows(accb, a.part_b);
+  }
+  if (a.part_s) block_rows(accs, a.part_s);
 }
 
-constexpr int64_t kLnBwdWaves = 2048;
+constexpr int64_t kLnBwdBlocks = 512;  // partial rows of the LayerNorm backward
 
 template <int N>
 struct IntC {
   static constexpr int value = N;
-};  // partial rows (and waves) of the LayerNorm backward
+};
 
 // ---------------------------------------------------------------- softmax xent
 // One workgroup per row.  Pass 1: running (max, sum of exp) per thread,
@@ -414,6 +627,35 @@ extern "C" size_t mk_col_sum_workspace_bytes(int64_t rows, int64_t cols) {
   return size_t(align256(col_parts(rows) * cols * 4));
 }
 
+namespace {
+// rows of `cols` elements of T as whole 16-byte vectors at every row start
+template <typename T>
+bool rows_are_vectors(int64_t cols, std::initializer_list<const void*> ptrs) {
+  uintptr_t al = 0;
+  for (const void* p : ptrs) al |= reinterpret_cast<uintptr_t>(p);
+  return (cols * int64_t(sizeof(T))) % 16 == 0 && (al & 15) == 0;
+}
+
+template <typename T>
+int col_sum_launch(hipStream_t s, int64_t rows, int64_t cols, const T* x, float* y, float* part) {
+  const int64_t np = col_parts(rows), rpb = (rows + np - 1) / np, nb = (rows + rpb - 1) / rpb;
+  if (rows_are_vectors<T>(cols, {x})) {
+    constexpr int64_t BC = 64 * RowVec<T>::NV;
+    const dim3 g(unsigned(nb), unsigned((cols + BC - 1) / BC));
+    if (g.y > 65535) return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: too many columns");
+    hipLaunchKernelGGL(col_partial_vec_kernel<T>, g, dim3(kBlock), 0, s, x, rows, cols, rpb, part);
+  } else {
+    const dim3 g(unsigned(nb), unsigned((cols + kColChunk - 1) / kColChunk));
+    if (g.y > 65535) return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: too many columns");
+    hipLaunchKernelGGL(col_partial_kernel<T>, g, dim3(kBlock), 0, s, x, rows, cols, rpb, part);
+  }
+  if (int rc = check_launch("mk_col_sum")) return rc;
+  const float* parts[1] = {part};
+  float* outs[1] = {y};
+  return col_final(s, 1, parts, outs, nb, cols);
+}
+}  // namespace
+
 extern "C" int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols, const void* x, float* y,
                           void* workspace) {
   clear_error();
@@ -423,70 +665,113 @@ extern "C" int mk_col_sum(void* stream, int in_type, int64_t rows, int64_t cols,
   hipStream_t s = as_stream(stream);
   if (rows == 0) return mk_fill(stream, 4, cols, 0, y);
   if (!x || !workspace) return fail(MK_ERR_INVALID, "mk_col_sum: null input or workspace");
-  const int64_t np = col_parts(rows), rpb = (rows + np - 1) / np;
   float* part = static_cast<float*>(workspace);
-  const dim3 g(unsigned(np), unsigned((cols + kColChunk - 1) / kColChunk));
-  if (g.y > 65535) return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: too many columns");
-  if (in_type == MK_BF16)
-    hipLaunchKernelGGL(col_partial_kernel<uint16_t>, g, dim3(kBlock), 0, s, (const uint16_t*)x, rows, cols, rpb,
-                       part);
-  else if (in_type == MK_F32)
-    hipLaunchKernelGGL(col_partial_kernel<float>, g, dim3(kBlock), 0, s, (const float*)x, rows, cols, rpb, part);
-  else
-    return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: in_type must be bf16/f32");
-  hipLaunchKernelGGL(col_final_kernel, dim3(final_blocks(cols)), dim3(kBlock), 0, s, part, np, cols, y);
-  return check_launch("mk_col_sum");
+  if (in_type == MK_BF16) return col_sum_launch(s, rows, cols, static_cast<const uint16_t*>(x), y, part);
+  if (in_type == MK_F32) return col_sum_launch(s, rows, cols, static_cast<const float*>(x), y, part);
+  return fail(MK_ERR_UNSUPPORTED, "mk_col_sum: in_type must be bf16/f32");
+}
+
+extern "C" int mk_gelu_tanh_bwd_colsum(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                                       const void* dy, void* dx, float* dx_colsum, void* workspace) {
+  clear_error();
+  if (rows < 0 || cols < 0) return fail(MK_ERR_INVALID, "mk_gelu_tanh_bwd_colsum: negative shape");
+  if (cols == 0) return MK_OK;
+  if (!dx_colsum) return fail(MK_ERR_INVALID, "mk_gelu_tanh_bwd_colsum: null column-sum output");
+  if (rows == 0) return mk_fill(stream, 4, cols, 0, dx_colsum);
+  if (!x || !dy || !dx || !workspace) return fail(MK_ERR_INVALID, "mk_gelu_tanh_bwd_colsum: null pointer");
+  if (io_type != MK_BF16 && io_type != MK_F32)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gelu_tanh_bwd_colsum: io_type must be bf16/f32");
+  hipStream_t s = as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+  auto run = [&](auto tag) -> int {
+    using T = decltype(tag);
+    if (!rows_are_vectors<T>(cols, {x, dy, dx})) {  // two passes: elementwise, then the column sum of dx
+      if (int rc = mk_gelu_tanh_bwd(stream, io_type, rows * cols, x, dy, dx)) return rc;
+      return col_sum_launch(s, rows, cols, static_cast<const T*>(dx), dx_colsum, part);
+    }
+    const int64_t np = col_parts(rows), rpb = (rows + np - 1) / np, nb = (rows + rpb - 1) / rpb;
+    constexpr int64_t BC = 64 * RowVec<T>::NV;
+    const dim3 g(unsigned(nb), unsigned((cols + BC - 1) / BC));
+    if (g.y > 65535) return fail(MK_ERR_UNSUPPORTED, "mk_gelu_tanh_bwd_colsum: too many columns");
+    hipLaunchKernelGGL(gelu_bwd_cols_kernel<T>, g, dim3(kBlock), 0, s, static_cast<const T*>(x),
+                       static_cast<const T*>(dy), static_cast<T*>(dx), rows, cols, rpb, part);
+    if (int rc = check_launch("mk_gelu_tanh_bwd_colsum")) return rc;
+    const float* parts[1] = {part};
+    float* outs[1] = {dx_colsum};
+    return col_final(s, 1, parts, outs, nb, cols);
+  };
+  return io_type == MK_BF16 ? run(uint16_t{}) : run(float{});
 }
 
 extern "C" size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  return size_t(2 * align256(kLnBwdWaves * cols * 4));
+  return size_t(3 * align256(kLnBwdBlocks * cols * 4));
 }
 
 extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
-                                const void* gamma, const void* dy, float eps, void* dx, float* dgamma,
-                                float* dbeta, void* workspace) {
+                                const void* gamma, const void* dy, const void* dres, float eps, void* dx,
+                                float* dgamma, float* dbeta, float* dx_colsum, void* workspace) {
   clear_error();
   if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_layernorm_bwd: bad shape");
-  if (cols > 64 * 8 * 4) return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: rows of at most 2048 columns");
+  if (cols > kLnBwdMaxCols) return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: rows of at most 2048 columns");
   if ((dgamma == nullptr) != (dbeta == nullptr))
     return fail(MK_ERR_INVALID, "mk_layernorm_bwd: dgamma and dbeta are both given or both NULL");
+  if (io_type != MK_BF16 && io_type != MK_F32)
+    return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: io_type must be bf16/f32");
   if (rows == 0) {
     if (dgamma) {
       if (int rc = mk_fill(stream, 4, cols, 0, dgamma)) return rc;
-      return mk_fill(stream, 4, cols, 0, dbeta);
+      if (int rc = mk_fill(stream, 4, cols, 0, dbeta)) return rc;
     }
+    if (dx_colsum) return mk_fill(stream, 4, cols, 0, dx_colsum);
     return MK_OK;
   }
-  if (!x || !dy || !dx || (dgamma && !workspace)) return fail(MK_ERR_INVALID, "mk_layernorm_bwd: null pointer");
+  if (!x || !dy || !dx || ((dgamma || dx_colsum) && !workspace))
+    return fail(MK_ERR_INVALID, "mk_layernorm_bwd: null pointer");
   hipStream_t s = as_stream(stream);
-  const int64_t waves = std::min<int64_t>(kLnBwdWaves, rows);
-  const unsigned blocks = unsigned((waves + 3) / 4);
-  const int64_t nparts = int64_t(blocks) * 4;  // every wave of the grid writes a partial row
-  float* pg = dgamma ? static_cast<float*>(workspace) : nullptr;
-  float* pb = dgamma ? reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(kLnBwdWaves * cols * 4))
-                     : nullptr;
-  const int kv = int((cols + 511) / 512);
-  auto launch = [&](auto tag, auto kvt) {
+  const int64_t np = std::min<int64_t>(kLnBwdBlocks, std::max<int64_t>(1, (rows + 15) / 16));
+  const int64_t rpb = (rows + np - 1) / np, nb = (rows + rpb - 1) / rpb;
+  const int64_t slab = align256(kLnBwdBlocks * cols * 4);
+  char* ws = static_cast<char*>(workspace);
+  LnBwdArgs a;
+  a.x = x; a.gamma = gamma; a.dy = dy; a.dres = dres; a.dx = dx;
+  a.rows = rows; a.rpb = rpb; a.cols = int(cols); a.eps = eps;
+  a.part_g = dgamma ? reinterpret_cast<float*>(ws) : nullptr;
+  a.part_b = dgamma ? reinterpret_cast<float*>(ws + slab) : nullptr;
+  a.part_s = dx_colsum ? reinterpret_cast<float*>(ws + 2 * slab) : nullptr;
+  auto launch = [&](auto tag, auto kvt, auto vect) {
     using T = decltype(tag);
     constexpr int KV = decltype(kvt)::value;
-    hipLaunchKernelGGL((layernorm_bwd_kernel<T, KV>), dim3(blocks), dim3(kBlock), 0, s, (const T*)x,
-                       (const T*)gamma, (const T*)dy, rows, int(cols), eps, (T*)dx, pg, pb);
+    constexpr bool VEC = decltype(vect)::value;
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, KV, VEC>), dim3(unsigned(nb)), dim3(kBlock), 0, s, a);
   };
   auto dispatch = [&](auto tag) {
-    if (kv == 1) launch(tag, IntC<1>{});
-    else if (kv == 2) launch(tag, IntC<2>{});
-    else launch(tag, IntC<4>{});
+    using T = decltype(tag);
+    constexpr int NV = RowVec<T>::NV;
+    const int64_t kv = (cols + 64 * NV - 1) / (64 * NV);
+    auto with_kv = [&](auto vect) {
+      if (kv == 1) launch(tag, IntC<1>{}, vect);
+      else if (kv == 2) launch(tag, IntC<2>{}, vect);
+      else if (kv <= 4) launch(tag, IntC<4>{}, vect);
+      else if constexpr (NV == 4) launch(tag, IntC<8>{}, vect);  // fp32 only: bf16 rows fit KV 4
+    };
+    if (rows_are_vectors<T>(cols, {x, dy, dres, dx})) with_kv(std::true_type{});
+    else with_kv(std::false_type{});
   };
   if (io_type == MK_BF16) dispatch(uint16_t{});
-  else if (io_type == MK_F32) dispatch(float{});
-  else return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: io_type must be bf16/f32");
+  else dispatch(float{});
+  if (int rc = check_launch("mk_layernorm_bwd")) return rc;
+  const float* parts[3];
+  float* outs[3];
+  int n = 0;
   if (dgamma) {
-    const dim3 g(final_blocks(cols));
-    hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pg, nparts, cols, dgamma);
-    hipLaunchKernelGGL(col_final_kernel, g, dim3(kBlock), 0, s, pb, nparts, cols, dbeta);
+    parts[n] = a.part_g; outs[n++] = dgamma;
+    parts[n] = a.part_b; outs[n++] = dbeta;
   }
-  return check_launch("mk_layernorm_bwd");
+  if (dx_colsum) {
+    parts[n] = a.part_s; outs[n++] = dx_colsum;
+  }
+  return n ? col_final(s, n, parts, outs, nb, cols) : MK_OK;
 }
 
 extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,

@@ -135,6 +135,58 @@ def test_layernorm_bwd_bf16_c5_rows(K):
     assert torch.equal(dx2, dx)
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(torch.bfloat16, 8192, 768), (torch.bfloat16, 50, 1000),
+                                             (torch.float32, 37, 1000), (torch.float32, 9, 2048),
+                                             (torch.bfloat16, 5, 100)])
+def test_layernorm_bwd_residual_and_colsum(K, dtype, rows, cols):
+    """dx = dres + LN'(dy) in place over dres, with dgamma, dbeta and the
+    column sums of dx from the same pass (the pre-LN residual block)."""
+    g = torch.Generator().manual_seed(rows * 3 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 1.5 + 0.2).to(dtype)
+    gamma = (1 + 0.1 * torch.randn(cols, generator=g)).to(dtype)
+    dy = torch.randn(rows, cols, generator=g).to(dtype)
+    dres = torch.randn(rows, cols, generator=g).to(dtype)
+    buf = dres.cuda()
+    dx, dgam, dbet, csum = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5, dx=buf, dres=buf,
+                                           want_colsum=True)
+    assert dx.data_ptr() == buf.data_ptr()
+    xr = x.double().requires_grad_(True)
+    gr = gamma.double().requires_grad_(True)
+    br = torch.zeros(cols, dtype=torch.float64, requires_grad=True)
+    torch.nn.functional.layer_norm(xr, (cols,), gr, br, 1e-5).backward(dy.double())
+    want = xr.grad + dres.double()
+    tol = 6e-3 if dtype == torch.bfloat16 else 2e-5
+    assert _rel(dx, want) < tol
+    assert _rel(dgam, gr.grad) < 1e-5
+    assert _rel(dbet, br.grad) < 1e-6
+    # column sums of the stored dx, to its rounding
+    assert _rel(csum, want.sum(0)) < (1e-2 if dtype == torch.bfloat16 else 2e-5)
+    np.testing.assert_allclose(_f64(csum), _f64(dx).sum(0), rtol=0,
+                               atol=(2 ** -8 if dtype == torch.bfloat16 else 1e-5) * float(_f64(dx).abs().sum(0).max()))
+    # deterministic
+    buf2 = dres.cuda()
+    _, _, _, csum2 = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5, dx=buf2, dres=buf2, want_colsum=True)
+    assert torch.equal(buf2, dx) and torch.equal(csum2, csum)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(torch.bfloat16, 8192, 3072), (torch.bfloat16, 33, 100),
+                                             (torch.float32, 300, 256), (torch.bfloat16, 7, 13)])
+def test_gelu_tanh_bwd_colsum(K, dtype, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(dtype).cuda()
+    dy = torch.randn(rows, cols, generator=g).to(dtype).cuda()
+    dx, csum = K.gelu_tanh_bwd_colsum(x, dy)
+    np.testing.assert_array_equal(_f64(dx), _f64(K.gelu_tanh_bwd(x, dy)))  # same values as the plain pass
+    want = _f64(dx).sum(0)
+    scale = _f64(dx).abs().sum(0)
+    tol = 2 ** -7 if dtype == torch.bfloat16 else 1e-6  # bf16: the sum runs over the unrounded products
+    assert float(((_f64(csum) - want).abs() / (scale + 1e-30)).max()) < tol
+    # in place over dy
+    dy2 = dy.clone()
+    dx2, csum2 = K.gelu_tanh_bwd_colsum(x, dy2, out=dy2)
+    assert torch.equal(dx2, dx) and torch.equal(csum2, csum)
+
+
 # ------------------------------------------------------------------ softmax cross-entropy
 @pytest.mark.parametrize("rows,cols", [(64, 257), (5, 1), (3, 50257)])
 def test_softmax_xent_f32(K, rows, cols):
