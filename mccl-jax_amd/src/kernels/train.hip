@@ -486,6 +486,96 @@ __global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restric
   }
 }
 
+// bf16 rows held in registers: one workgroup of kXentThreads per row, the
+// row's 16-byte-aligned body as vectors (thread t: vectors t, t + 512, ...,
+// NVT of them), the unaligned head and tail (under 8 elements each) as one
+// scalar on threads 0..7 and 8..15.  The row is read once: max, sum of
+// exp(x - max), then dlogits = (exp(x - lse) - [j == label]) * grad_scale
+// written from the same registers (so dlogits may be logits).
+constexpr int kXentThreads = 512;
+constexpr uint32_t kBf16NegInfPair = 0xFF80FF80u;
+
+template <int NVT, typename L>
+__global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const uint16_t* logits, int64_t cols,
+                                                                       const L* __restrict__ labels,
+                                                                       float grad_scale, float* __restrict__ loss,
+                                                                       uint16_t* dlogits) {
+  constexpr int NW = kXentThreads / 64;
+  constexpr float kL2e = 1.4426950408889634f;
+  __shared__ float red[NW];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const uint16_t* xr = logits + row * cols;
+  uint16_t* dr = dlogits + row * cols;
+  const int64_t head = min<int64_t>(cols, int64_t(((16u - (reinterpret_cast<uintptr_t>(xr) & 15u)) & 15u) / 2u));
+  const int64_t nv = (cols - head) / 8, tail = cols - head - nv * 8;
+  const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xr + head);
+  u32x4_t v[NVT];
+#pragma unroll
+  for (int i = 0; i < NVT; ++i) {
+    const int64_t idx = t + int64_t(i) * kXentThreads;
+    v[i] = idx < nv ? xv[idx] : u32x4_t{kBf16NegInfPair, kBf16NegInfPair, kBf16NegInfPair, kBf16NegInfPair};
+  }
+  // this thread's scalar element, if any: head element t (t < 8) or tail element t - 8
+  int64_t ej = -1;
+  if (t < head) ej = t;
+  else if (t >= 8 && t - 8 < tail) ej = head + nv * 8 + (t - 8);
+  const float ex = ej >= 0 ? bf16_to_f32(xr[ej]) : -INFINITY;
+
+  auto block_reduce = [&](float x, bool is_max) __attribute__((always_inline)) {
+    x = is_max ? wave_max(x) : wave_sum(x);
+    if (lane == 0) red[wv] = x;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    __syncthreads();
+    return r;
+  };
+  float m = ex;
+#pragma unroll
+  for (int i = 0; i < NVT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(lo16(v[i][j]), hi16(v[i][j])));
+  // exponents from x - max (exact at the max), so a row's largest p is
+  // exactly 1 / S and a one-class row has p = 1, gradient 0
+  const float M = block_reduce(m, true);
+  float sum = ej >= 0 ? __builtin_amdgcn_exp2f((ex - M) * kL2e) : 0.f;
+#pragma unroll
+  for (int i = 0; i < NVT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      sum += __builtin_amdgcn_exp2f((lo16(v[i][j]) - M) * kL2e) + __builtin_amdgcn_exp2f((hi16(v[i][j]) - M) * kL2e);
+  const float S = block_reduce(sum, false);
+  const float lse = M + __logf(S);
+  const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xr[lab]) : __builtin_nanf("");
+  // gradient, from the registers (every read of the row is done: in place is safe)
+  u32x4_t* dv = reinterpret_cast<u32x4_t*>(dr + head);
+#pragma unroll
+  for (int i = 0; i < NVT; ++i) {
+    const int64_t idx = t + int64_t(i) * kXentThreads;
+    if (idx < nv) {
+      const int64_t j0 = head + idx * 8;
+      u32x4_t o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(lo16(v[i][j]) - M, kL2e, -ls2)) - (j0 + 2 * j == lab ? 1.f : 0.f);
+        const float p1 =
+            __builtin_amdgcn_exp2f(fmaf(hi16(v[i][j]) - M, kL2e, -ls2)) - (j0 + 2 * j + 1 == lab ? 1.f : 0.f);
+        o[j] = pack_bf16(p0 * grad_scale, p1 * grad_scale);
+      }
+      dv[idx] = o;
+    }
+  }
+  if (ej >= 0) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(ex - M, kL2e, -ls2)) - (ej == lab ? 1.f : 0.f);
+    dr[ej] = f32_to_bf16(p * grad_scale);
+  }
+}
+
 // ---------------------------------------------------------------- Adam
 // dp_train.py body(): m = b1 m + (1-b1) g; v = b2 v + (1-b2) g g;
 // p = p - lr (m / bc1) / (sqrt(v / bc2) + eps), in fp32 with the constants
@@ -784,6 +874,26 @@ extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t 
   if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent: null pointer");
   hipStream_t s = as_stream(stream);
   const dim3 g{unsigned(rows)}, b{unsigned(kBlock)};
+  // bf16 rows of up to 64K columns: the register-resident kernel
+  if (io_type == MK_BF16 && cols <= int64_t(kXentThreads) * 8 * 16) {
+    const int64_t nvt = (cols / 8 + kXentThreads - 1) / kXentThreads;  // vectors per thread (bound)
+    auto launch = [&](auto nt, auto ltag) {
+      constexpr int NVT = decltype(nt)::value;
+      using L = decltype(ltag);
+      hipLaunchKernelGGL((softmax_xent_bf16_kernel<NVT, L>), g, dim3(kXentThreads), 0, s, (const uint16_t*)logits,
+                         cols, (const L*)labels, grad_scale, loss_rows, (uint16_t*)dlogits);
+    };
+    auto with_labels = [&](auto nt) {
+      if (label_type == MK_S32) launch(nt, int32_t{});
+      else if (label_type == MK_S64) launch(nt, int64_t{});
+    };
+    if (label_type != MK_S32 && label_type != MK_S64)
+      return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: labels must be s32/s64");
+    if (nvt <= 4) with_labels(IntC<4>{});
+    else if (nvt <= 8) with_labels(IntC<8>{});
+    else with_labels(IntC<16>{});
+    return check_launch("mk_softmax_xent");
+  }
   auto go = [&](auto tag) {
     using T = decltype(tag);
     if (label_type == MK_S32)
