@@ -343,6 +343,14 @@ int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* 
                    const void* grad, float* m, float* v, double lr, double b1, double b2, double eps,
                    double bc1, double bc2);
 
+/* mk_adam_update with lr, bc1, bc2 read from device memory, hyper = {lr, bc1,
+ * bc2} (fp32): the step's scalar inputs of temp/dp_train.py:93-95 (host
+ * computed, passed as replicated f32 device scalars), so a captured launch
+ * sequence takes new values on every replay. */
+int mk_adam_update_dev(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type,
+                       const void* grad, float* m, float* v, const float* hyper, double b1, double b2,
+                       double eps);
+
 /* Attention backward for O = softmax(scale Q Kᵀ [causal]) V (mk_sdpa_fwd's
  * convention, lse from its forward): with P = exp(scale S - lse) (0 where
  * masked), D_r = dO_r · O_r and dS = scale P (dO Vᵀ - D):

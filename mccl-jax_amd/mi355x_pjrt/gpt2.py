@@ -13,12 +13,15 @@ operation is a call through the C-ABI of include/mk_kernels.h:
             bias add -> GELU -> projection GEMM -> residual + bias add; final
             LN, logits GEMM against the embedding table, fused softmax
             cross-entropy (loss rows and the logit gradient, in place)
-  backward  the transposed GEMMs (weight gradients straight to fp32), column
-            sums for the biases, GELU / LayerNorm / attention backward,
-            residual adds, position-embedding column sum, deterministic
-            scatter-add of the token gradient into the embedding gradient
+  backward  the transposed GEMMs (weight gradients straight to fp32), flash
+            attention backward, GELU backward fused with the MLP bias column
+            sums, LayerNorm backward fused with the residual add and the
+            projection-bias column sums, position-embedding column sum,
+            deterministic scatter-add of the token gradient into the
+            embedding gradient
   update    one Adam launch over all parameters (fp32 master, m, v; bf16
-            working copy rewritten)
+            working copy rewritten), lr and bias corrections read from a
+            device buffer so the whole step can be replayed as a HIP graph
 
 The GEMMs have no epilogue here (the biases join the elementwise pass that
 follows), so they are plain library GEMMs (mk_gemm_blas, rocBLAS); every other
@@ -154,6 +157,8 @@ class GPT2TrainStep:
         self.grad = torch.zeros(off, **f32)
         self.m = torch.zeros(off, **f32)
         self.v = torch.zeros(off, **f32)
+        self.hyper = torch.zeros(3, **f32)  # lr, bc1, bc2 of the current step (device scalars)
+        self.graph = None
         self.load(params if params is not None else init_params(cfg, seed))
         self._alloc()
         self.ids = torch.zeros(cfg.tokens, dtype=torch.int32, device=self.dev)
@@ -347,21 +352,53 @@ class GPT2TrainStep:
             call()
         return self.loss_sum
 
-    def adam(self, t=None):
-        """One Adam update of every parameter (temp/dp_train.py:71-75)."""
+    def set_step_scalars(self, t=None):
+        """Advance the step count and write the step's scalar inputs (lr and
+        the bias corrections bc1 = 1-b1^t, bc2 = 1-b2^t, host-computed in
+        double and rounded to fp32: temp/dp_train.py:91-95) to the device."""
         self.t = self.t + 1 if t is None else t
         bc1, bc2 = 1 - self.b1 ** self.t, 1 - self.b2 ** self.t
-        rc = self.lib.mk_adam_update(_P(self.stream.cuda_stream), self.n_flat, BF16, _P(self.param.data_ptr()),
-                                     _P(self.master.data_ptr()), F32, _P(self.grad.data_ptr()),
-                                     _P(self.m.data_ptr()), _P(self.v.data_ptr()), self.lr, self.b1, self.b2,
-                                     self.adam_eps, bc1, bc2)
-        K._check(rc, "mk_adam_update")
+        with torch.cuda.stream(self.stream):
+            self.hyper.copy_(torch.tensor([self.lr, bc1, bc2], dtype=torch.float32))
+
+    def _adam_launch(self):
+        rc = self.lib.mk_adam_update_dev(_P(self.stream.cuda_stream), self.n_flat, BF16, _P(self.param.data_ptr()),
+                                         _P(self.master.data_ptr()), F32, _P(self.grad.data_ptr()),
+                                         _P(self.m.data_ptr()), _P(self.v.data_ptr()), _P(self.hyper.data_ptr()),
+                                         self.b1, self.b2, self.adam_eps)
+        K._check(rc, "mk_adam_update_dev")
+
+    def adam(self, t=None):
+        """One Adam update of every parameter (temp/dp_train.py:71-75)."""
+        self.set_step_scalars(t)
+        self._adam_launch()
 
     def step(self):
         """forward + backward + Adam; returns the (pre-update) mean loss as a
         device tensor of one element (sum of loss rows / tokens)."""
         self.forward_backward()
         self.adam()
+        return self.loss_sum
+
+    def capture(self):
+        """Record forward + backward + the Adam launch as one HIP graph on the
+        step's stream (which must not be the default stream).  Run one eager
+        step first: library handles are created on first use, outside any
+        capture.  The graph reads the step scalars from device memory, so each
+        replay() takes that step's lr and bias corrections."""
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            with torch.cuda.graph(self.graph, stream=self.stream):
+                for call in self.calls:
+                    call()
+                self._adam_launch()
+        return self.graph
+
+    def replay(self):
+        """One training step by graph replay (after capture())."""
+        self.set_step_scalars()
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()
         return self.loss_sum
 
     def loss_value(self) -> float:

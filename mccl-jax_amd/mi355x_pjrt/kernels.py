@@ -373,6 +373,14 @@ def adam_update(param, grad, m, v, lr, b1, b2, eps, bc1, bc2, master=None, strea
     _check(rc, "mk_adam_update")
 
 
+def adam_update_dev(param, grad, m, v, hyper, b1, b2, eps, master=None, stream=None):
+    """adam_update with hyper = device fp32 tensor [lr, bc1, bc2]."""
+    rc = lib().mk_adam_update_dev(_stream(stream), param.numel(), mk_dtype(param.dtype), _ptr(param), _ptr(master),
+                                  mk_dtype(grad.dtype), _ptr(grad), _ptr(m), _ptr(v), _ptr(hyper), float(b1),
+                                  float(b2), float(eps))
+    _check(rc, "mk_adam_update_dev")
+
+
 def sdpa_bwd(q, k, v, o, dout, lse, scale, causal=True, dq=None, dk=None, dv=None, workspace=None, stream=None):
     """(dq, dk, dv) of mk_sdpa_fwd on [B, H, S, D] bf16 views."""
     _require_cuda(q, k, v, o, dout, lse)

@@ -587,7 +587,13 @@ template <typename G>
 __global__ __launch_bounds__(kBlock) void adam_kernel(int64_t n, float* __restrict__ p32, uint16_t* __restrict__ p16,
                                                     const G* __restrict__ grad, float* __restrict__ m,
                                                     float* __restrict__ v, float lr, float b1, float omb1, float b2,
-                                                    float omb2, float eps, float bc1, float bc2) {
+                                                    float omb2, float eps, float bc1, float bc2,
+                                                    const float* __restrict__ hyper) {
+  if (hyper) {  // lr, bc1, bc2 as device scalars (inputs of the step)
+    lr = hyper[0];
+    bc1 = hyper[1];
+    bc2 = hyper[2];
+  }
   const int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
     const float g = ldf<G>(grad, i);
@@ -911,10 +917,10 @@ extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t 
   return check_launch("mk_softmax_xent");
 }
 
-extern "C" int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type,
-                              const void* grad, float* m, float* v, double lr, double b1, double b2, double eps,
-                              double bc1, double bc2) {
-  clear_error();
+namespace {
+int adam_launch(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type, const void* grad,
+                float* m, float* v, double lr, double b1, double b2, double eps, double bc1, double bc2,
+                const float* hyper) {
   if (n < 0) return fail(MK_ERR_INVALID, "mk_adam_update: negative n");
   if (n == 0) return MK_OK;
   if (!param || !grad || !m || !v) return fail(MK_ERR_INVALID, "mk_adam_update: null pointer");
@@ -934,13 +940,29 @@ extern "C" int mk_adam_update(void* stream, int64_t n, int param_type, void* par
               f_omb2 = float(1.0 - b2), f_eps = float(eps), f_bc1 = float(bc1), f_bc2 = float(bc2);
   if (grad_type == MK_F32)
     hipLaunchKernelGGL(adam_kernel<float>, g, b, 0, s, n, p32, p16, (const float*)grad, m, v, f_lr, f_b1, f_omb1,
-                       f_b2, f_omb2, f_eps, f_bc1, f_bc2);
+                       f_b2, f_omb2, f_eps, f_bc1, f_bc2, hyper);
   else if (grad_type == MK_BF16)
     hipLaunchKernelGGL(adam_kernel<uint16_t>, g, b, 0, s, n, p32, p16, (const uint16_t*)grad, m, v, f_lr, f_b1,
-                       f_omb1, f_b2, f_omb2, f_eps, f_bc1, f_bc2);
+                       f_omb1, f_b2, f_omb2, f_eps, f_bc1, f_bc2, hyper);
   else
     return fail(MK_ERR_UNSUPPORTED, "mk_adam_update: grad_type must be bf16/f32");
   return check_launch("mk_adam_update");
+}
+}  // namespace
+
+extern "C" int mk_adam_update(void* stream, int64_t n, int param_type, void* param, float* master, int grad_type,
+                              const void* grad, float* m, float* v, double lr, double b1, double b2, double eps,
+                              double bc1, double bc2) {
+  clear_error();
+  return adam_launch(stream, n, param_type, param, master, grad_type, grad, m, v, lr, b1, b2, eps, bc1, bc2, nullptr);
+}
+
+extern "C" int mk_adam_update_dev(void* stream, int64_t n, int param_type, void* param, float* master,
+                                  int grad_type, const void* grad, float* m, float* v, const float* hyper, double b1,
+                                  double b2, double eps) {
+  clear_error();
+  if (!hyper) return fail(MK_ERR_INVALID, "mk_adam_update_dev: null hyperparameter pointer");
+  return adam_launch(stream, n, param_type, param, master, grad_type, grad, m, v, 0.0, b1, b2, eps, 1.0, 1.0, hyper);
 }
 
 extern "C" size_t mk_sdpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {

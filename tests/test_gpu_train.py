@@ -283,6 +283,24 @@ def test_adam_update_f32_and_master(K):
     assert torch.equal(pb, master.bfloat16())
 
 
+def test_adam_update_dev_matches_host_scalars(K):
+    """lr, bc1, bc2 from a device buffer give the same bits as the same
+    values passed as host scalars (both rounded once to fp32)."""
+    rng = np.random.default_rng(1)
+    n = 70001
+    p, g, m = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    v = np.abs(rng.standard_normal(n)).astype(np.float32) * 0.01
+    lr, b1, b2, eps, t = 3e-4, 0.9, 0.95, 1e-8, 7
+    bc1, bc2 = 1 - b1 ** t, 1 - b2 ** t
+    a = [torch.from_numpy(x.copy()).cuda() for x in (p, g, m, v)]
+    b = [torch.from_numpy(x.copy()).cuda() for x in (p, g, m, v)]
+    K.adam_update(a[0], a[1], a[2], a[3], lr, b1, b2, eps, bc1, bc2)
+    hyper = torch.tensor([lr, bc1, bc2], dtype=torch.float32).cuda()
+    K.adam_update_dev(b[0], b[1], b[2], b[3], hyper, b1, b2, eps)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
 # ------------------------------------------------------------------ attention backward
 def _attn_ref(q, k, v, scale, causal):
     s = (q @ k.transpose(-1, -2)) * scale
