@@ -15,8 +15,12 @@ fusion GB/s % HBM peak".
              events on the launch stream, against 2516.6 TFLOP/s bf16 dense
   cpu_baseline  the float64 numpy oracle on a bounded sample of (b, h) pairs
              of the same workload, extrapolated to all pairs
+  training_step  config C5: one GPT-2-small training step (forward, backward,
+             Adam; 12 layers, d 768, 12 heads, seq 1024, batch 8, vocab
+             50257, bf16 activations, fp32 Adam) replayed as one HIP graph;
+             ms/step, tokens/s, model TFLOP/s (3x forward FLOPs) and MFU
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS] [--only sdpa|fusions]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS] [--only sdpa|fusions|c5]
 
 Before the first timed region the headline kernel runs untimed for --spinup
 seconds (default 1), so that no timed region includes the clocks' ramp from
@@ -51,7 +55,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--spinup", type=float, default=1.0,
                     help="seconds of untimed headline launches before anything is timed (clocks settle)")
-    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib"], default=None)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -216,6 +220,47 @@ def run_fusions(torch, np, K, args):
     return res
 
 
+def run_c5(torch, np, args):
+    """C5 training step, graph-replayed: W untimed replays, then K timed
+    replays between HIP events on the step's stream."""
+    from mi355x_pjrt import gpt2
+
+    cfg = gpt2.GPT2Config()
+    stream = torch.cuda.Stream()
+    step = gpt2.GPT2TrainStep(cfg, seed=0, stream=stream)
+    rng = np.random.default_rng(5000)
+    ids = rng.integers(0, cfg.vocab, (cfg.batch, cfg.seq))
+    step.set_batch(ids, np.roll(ids, -1, axis=1))
+    step.step()  # eager first step (library handles), then capture
+    torch.cuda.synchronize()
+    loss_first = step.loss_value()
+    step.capture()
+    for _ in range(args.warmup):
+        step.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    fl = cfg.flops_per_step()
+    res = {"workload": "C5 GPT-2-small training step (forward + backward + Adam), B=8 S=1024 d=768 L=12 H=12 "
+                       "V=50257, bf16 activations, fp32 master/Adam, one HIP graph per step",
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(cfg.tokens / (ms * 1e-3), 1),
+           "model_tflops": round(fl / (ms * 1e-3) / 1e12, 2), "flops_per_step": fl,
+           "mfu": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "steps": args.steps,
+           "warmup": args.warmup, "loss_step1": round(loss_first, 4),
+           "loss_last": round(step.loss_value(), 4), "params": step.n_params,
+           "data": "synthetic: numpy PCG64 token ids U[0,V), labels = ids shifted by one; N(0,0.02) init"}
+    log(f"C5 step: {ms:.3f} ms, {res['tokens_per_s']:.0f} tokens/s, {res['model_tflops']:.1f} TFLOP/s, "
+        f"MFU {100 * res['mfu']:.1f}%")
+    del step
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -240,6 +285,9 @@ def main():
         print(json.dumps({"calib_copy_bytes_read": n * 4, "calib_copy_bytes_written": n * 4,
                           "ms": round(ms, 4), "gbs": round(2 * n * 4 / (ms * 1e-3) / 1e9, 1)}))
         return
+    if args.only == "c5":
+        print(json.dumps({"training_step": run_c5(torch, np, args)}))
+        return
     sweep, head, fusions = {}, None, {}
     spin_up(torch, np, K, args)
     if args.only in (None, "sdpa", "headline"):
@@ -249,6 +297,7 @@ def main():
     if head is None:
         print(json.dumps({"fusions": fusions}))
         return
+    c5 = run_c5(torch, np, args) if args.only is None else None
     ms, tf, steps = head
     S = args.seq
     cpu = None if args.no_cpu else cpu_baseline_sdpa(np, S, args.cpu_seconds)
@@ -275,6 +324,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "fusions": fusions,
+        "training_step": c5,
     }
     print(json.dumps(line))
 
