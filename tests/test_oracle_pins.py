@@ -325,3 +325,70 @@ def test_inputs_are_deterministic():
     for key in a:
         np.testing.assert_array_equal(a[key], b[key])
     assert a["q"].dtype == np.uint16 and a["q"].shape == (1, 2, 64, 128)
+
+
+# ------------------------------------------------------------------ C5 training-step oracle
+def _tiny_gpt2_params(rng, V=11, S=4, d=8, L=1, F=32):
+    p = {"wte": rng.standard_normal((V, d)) * 0.5, "wpe": rng.standard_normal((S, d)) * 0.5}
+    for l in range(L):
+        q = f"h{l}."
+        p.update({q + "ln1_g": 1 + 0.1 * rng.standard_normal(d), q + "ln1_b": 0.1 * rng.standard_normal(d),
+                  q + "w_qkv": rng.standard_normal((d, 3 * d)) * 0.4, q + "b_qkv": 0.1 * rng.standard_normal(3 * d),
+                  q + "w_o": rng.standard_normal((d, d)) * 0.4, q + "b_o": 0.1 * rng.standard_normal(d),
+                  q + "ln2_g": 1 + 0.1 * rng.standard_normal(d), q + "ln2_b": 0.1 * rng.standard_normal(d),
+                  q + "w_fc": rng.standard_normal((d, F)) * 0.4, q + "b_fc": 0.1 * rng.standard_normal(F),
+                  q + "w_pr": rng.standard_normal((F, d)) * 0.3, q + "b_pr": 0.1 * rng.standard_normal(d)})
+    p.update({"lnf_g": 1 + 0.1 * rng.standard_normal(d), "lnf_b": 0.1 * rng.standard_normal(d)})
+    return p
+
+
+def test_gpt2_ref_gradients_match_finite_differences():
+    """oracle/gpt2_ref.py: the float64 autograd gradients of every parameter
+    agree with central finite differences of the loss (torch gradcheck), and
+    loss_and_grads returns exactly those gradients."""
+    from oracle import gpt2_ref
+
+    rng = np.random.default_rng(0)
+    p = _tiny_gpt2_params(rng)
+    ids = rng.integers(0, 11, (2, 4))
+    labels = rng.integers(0, 11, (2, 4))
+    names = sorted(p)
+    ts = tuple(torch.tensor(p[n], dtype=torch.float64, requires_grad=True) for n in names)
+
+    def f(*args):
+        return gpt2_ref.forward_loss(dict(zip(names, args)), ids, labels, 1, 2)
+
+    assert torch.autograd.gradcheck(f, ts, eps=1e-6, atol=1e-6, rtol=1e-4)
+    loss, grads = gpt2_ref.loss_and_grads(p, ids, labels, 1, 2)
+    auto = torch.autograd.grad(f(*ts), ts)
+    for n, g in zip(names, auto):
+        np.testing.assert_array_equal(grads[n], g.numpy())
+    assert loss == float(f(*ts).detach())
+
+
+def test_gpt2_ref_zero_head_gives_uniform_loss():
+    """With the (tied) embedding table all zero every logit is 0: the loss is
+    ln(V) for any labels, and the head's bias gradient dL/d lnf_b is 0."""
+    from oracle import gpt2_ref
+
+    rng = np.random.default_rng(1)
+    p = _tiny_gpt2_params(rng)
+    p["wte"] = np.zeros_like(p["wte"])
+    ids = rng.integers(0, 11, (2, 4))
+    labels = rng.integers(0, 11, (2, 4))
+    loss, grads = gpt2_ref.loss_and_grads(p, ids, labels, 1, 2)
+    assert abs(loss - math.log(11)) < 1e-14
+    np.testing.assert_array_equal(grads["lnf_b"], 0.0)
+
+
+def test_gpt2_ref_adam_first_step_closed_form():
+    """From m = v = 0 at t = 1 the bias corrections cancel: p - lr g / (|g| + eps)."""
+    from oracle import gpt2_ref
+
+    rng = np.random.default_rng(2)
+    p, g = rng.standard_normal(1000), rng.standard_normal(1000)
+    lr, eps = 1e-3, 1e-8
+    p1, m1, v1 = gpt2_ref.adam(p, g, np.zeros(1000), np.zeros(1000), 1, lr, eps=eps)
+    np.testing.assert_allclose(p1, p - lr * g / (np.abs(g) + eps), rtol=1e-14, atol=1e-18)
+    np.testing.assert_allclose(m1, 0.1 * g, rtol=1e-15)
+    np.testing.assert_allclose(v1, 0.001 * g * g, rtol=1e-13)
