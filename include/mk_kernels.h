@@ -69,8 +69,7 @@ int mk_gemm(void* stream, int ab_type, int c_type,
             const void* bias, int epilogue);
 
 /* Plain GEMM through rocBLAS (the linear layers of the training step and
- * their gradients: no epilogue to fuse, so the library GEMM is used, as the
- * brief for this build allows for plain GEMMs).  Same operand convention as
+ * their gradients: with no epilogue to fuse, a library GEMM does the work).  Same operand convention as
  * mk_gemm (row-major C with row stride c_ms, one unit stride per operand),
  * C = alpha A B + beta C; no bias.  ab_type ∈ {MK_BF16 (c_type MK_BF16 /
  * MK_F16 / MK_F32), MK_F32 (c_type MK_F32)}, fp32 accumulation.  Operands
@@ -81,6 +80,19 @@ int mk_gemm_blas(void* stream, int ab_type, int c_type,
                  const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,
                  const void* B, int64_t b_bs, int64_t b_ks, int64_t b_ns,
                  void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
+
+/* Split-K form of mk_gemm_blas for fp32 outputs with few output tiles and a
+ * long contraction (the weight gradients dW = Xᵀ dY of the training step,
+ * linalg.mm:47-105's dot_general with the token axis contracted): the K axis
+ * is cut into `splits` equal slices, one batched GEMM writes the slices'
+ * products to the workspace (splits x M x N fp32) and a second pass adds
+ * them in slice order into C (deterministic).  K % splits == 0; N and c_ms
+ * multiples of 4; C and workspace 16-byte aligned; beta 0 (C overwritten).
+ * splits == 1 is a plain mk_gemm_blas call (no workspace). */
+size_t mk_gemm_blas_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits);
+int mk_gemm_blas_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A,
+                        int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C,
+                        int64_t c_ms, int64_t splits, void* workspace);
 
 /* ------------------------------------------------------------------------
  * a5+a6  fused scaled-dot-product attention (flash attention, forward).

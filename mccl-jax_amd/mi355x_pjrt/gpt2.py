@@ -132,6 +132,12 @@ class _Call:
 class GPT2TrainStep:
     """Buffers, parameters and the prepared launch list of one training step."""
 
+    # K-slices of the fp32 weight-gradient GEMMs (dW = Xᵀ dY, K = tokens):
+    # their few output tiles leave most CUs idle unless K is split.  Counts
+    # measured at C5 on one MI355X (per GEMM: plain vs split, slices summed
+    # by mk_gemm_blas_splitk's second pass).
+    DW_SPLITS = {"dw_o": 8, "dw_qkv": 2, "dw_fc": 4, "dw_pr": 4}
+
     def __init__(self, cfg: GPT2Config, params: dict | None = None, seed: int = 0, lr: float = 3e-4,
                  b1: float = 0.9, b2: float = 0.999, adam_eps: float = 1e-8, device="cuda", stream=None):
         if cfg.head_dim not in (64, 128):
@@ -207,7 +213,10 @@ class GPT2TrainStep:
         self.loss_rows = torch.empty(T, dtype=torch.float32, device=dev)
         self.loss_sum = torch.empty(1, dtype=torch.float32, device=dev)
         lib = self.lib
-        ws = max(lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
+        sk = [lib.mk_gemm_blas_splitk_workspace_bytes(d, n, self.DW_SPLITS[t])
+              for t, n in (("dw_o", d), ("dw_qkv", 3 * d), ("dw_fc", c.d_ff))]
+        sk.append(lib.mk_gemm_blas_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS["dw_pr"]))
+        ws = max(*sk, lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
                  lib.mk_layernorm_bwd_workspace_bytes(T, d),
                  lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),
                  lib.mk_scatter_add_workspace_bytes(c.vocab, T))
@@ -232,7 +241,14 @@ class GPT2TrainStep:
             return P(self.view(self.grad, name))
 
         def gemm(ab, ct, M, N, Kd, a, a_ms, a_ks, b, b_ks, b_ns, cptr, c_ms, tag="gemm"):
-            # plain GEMM (no epilogue) through rocBLAS
+            # plain GEMM (no epilogue) through rocBLAS; the fp32 weight
+            # gradients (few output tiles, K = tokens) split along K
+            sp = self.DW_SPLITS.get(tag, 1)
+            if sp > 1 and ct == F32 and Kd % sp == 0:
+                calls.append(_Call(lib.mk_gemm_blas_splitk, [st, _I(ab), _I64(M), _I64(N), _I64(Kd), a, _I64(a_ms),
+                                                             _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr, _I64(c_ms),
+                                                             _I64(sp), ws], "mk_gemm_blas_splitk " + tag))
+                return
             calls.append(_Call(lib.mk_gemm_blas, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
                                                   a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
                                                   _I64(b_ns), cptr, _I64(0), _I64(c_ms), _F(1.0), _F(0.0)],

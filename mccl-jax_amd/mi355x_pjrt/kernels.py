@@ -277,6 +277,46 @@ def _ws(nbytes, device, workspace):
     return workspace
 
 
+def _mat_strides(t):
+    """(batch stride, row stride, column stride) of a 2-D or 3-D view."""
+    if t.dim() == 2:
+        return 0, t.stride(0), t.stride(1)
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def gemm_blas(a, b, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
+    """out = alpha a @ b + beta out through rocBLAS (mk_gemm_blas); a [.., M, K],
+    b [.., K, N] views with one unit stride each (either orientation)."""
+    _require_cuda(a, b)
+    M, Kd = a.shape[-2:]
+    N = b.shape[-1]
+    batch = a.shape[0] if a.dim() == 3 else 1
+    if out is None:
+        shape = (batch, M, N) if a.dim() == 3 else (M, N)
+        out = torch.zeros(shape, dtype=out_dtype or a.dtype, device=a.device)
+    a_bs, a_ms, a_ks = _mat_strides(a)
+    b_bs, b_ks, b_ns = _mat_strides(b)
+    c_bs, c_ms, _ = _mat_strides(out)
+    rc = lib().mk_gemm_blas(_stream(stream), mk_dtype(a.dtype), mk_dtype(out.dtype), batch, M, N, Kd, _ptr(a), a_bs,
+                            a_ms, a_ks, _ptr(b), b_bs, b_ks, b_ns, _ptr(out), c_bs, c_ms, float(alpha), float(beta))
+    _check(rc, "mk_gemm_blas")
+    return out
+
+
+def gemm_blas_splitk(a, b, splits, out=None, workspace=None, stream=None):
+    """fp32 out = a @ b with the contraction cut into `splits` slices
+    (mk_gemm_blas_splitk); a [M, K], b [K, N] 2-D views."""
+    _require_cuda(a, b)
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = torch.empty(M, N, dtype=torch.float32, device=a.device) if out is None else out
+    ws = _ws(lib().mk_gemm_blas_splitk_workspace_bytes(M, N, splits), a.device, workspace)
+    rc = lib().mk_gemm_blas_splitk(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
+                                   _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), splits, _ptr(ws))
+    _check(rc, "mk_gemm_blas_splitk")
+    return out
+
+
 def add_rows(a, b=None, bias=None, out=None, stream=None):
     """out = a + b + bias (bias broadcast over the rows of a 2-D a), one pass
     with fp32 math and one rounding; b and bias are optional, out may be a or b."""

@@ -8,6 +8,7 @@
 
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -100,7 +101,57 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
   return MK_OK;
 }
 
+namespace {
+// C[m, n] = sum over slices s of W[s][m][n] (dense M x N slices), slices added
+// in order: the result does not depend on scheduling.
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ w, int64_t splits, int64_t M,
+                                                        int64_t N, float* __restrict__ c, int64_t c_ms) {
+  const int64_t nvec = M * N / 4, slab = M * N / 4;
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  const f32x4* wv = reinterpret_cast<const f32x4*>(w);
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < nvec; i += stride) {
+    f32x4 a = wv[i];
+    for (int64_t s = 1; s < splits; ++s) {
+      const f32x4 b = wv[s * slab + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a.v[j] += b.v[j];
+    }
+    const int64_t e = i * 4, m = e / N, n = e % N;
+    *reinterpret_cast<f32x4*>(c + m * c_ms + n) = a;
+  }
+}
+}  // namespace
+
 }  // namespace mk
+
+extern "C" size_t mk_gemm_blas_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {
+  if (M <= 0 || N <= 0 || splits <= 1) return 0;
+  return size_t(M * N * splits * 4);
+}
+
+extern "C" int mk_gemm_blas_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A,
+                                   int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C,
+                                   int64_t c_ms, int64_t splits, void* workspace) {
+  mk::clear_error();
+  if (splits < 1 || K < 0 || M < 0 || N < 0) return mk::fail(MK_ERR_INVALID, "mk_gemm_blas_splitk: bad shape or splits");
+  hipStream_t s = mk::as_stream(stream);
+  if (splits == 1 || M == 0 || N == 0)
+    return mk::gemm_blas(s, ab_type, MK_F32, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, 1.f, 0.f);
+  if (K % splits != 0) return mk::fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas_splitk: K must be a multiple of splits");
+  if (!workspace || !C) return mk::fail(MK_ERR_INVALID, "mk_gemm_blas_splitk: null workspace or output");
+  if ((N % 4) != 0 || (c_ms % 4) != 0 || ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(workspace)) & 15))
+    return mk::fail(MK_ERR_UNSUPPORTED, "mk_gemm_blas_splitk: N and c_ms multiples of 4, 16-byte aligned C and workspace");
+  const int64_t ks = K / splits;
+  // slice s reads A[:, s ks : (s+1) ks] and B[s ks : (s+1) ks, :] (element strides along k) and writes W[s]
+  float* W = static_cast<float*>(workspace);
+  if (int rc = mk::gemm_blas(s, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns,
+                             W, M * N, N, 1.f, 0.f))
+    return rc;
+  const int64_t nvec = M * N / 4;
+  const unsigned blocks = unsigned(std::min<int64_t>((nvec + 255) / 256, 4096));
+  hipLaunchKernelGGL(mk::splitk_sum_kernel, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  return mk::check_launch("mk_gemm_blas_splitk");
+}
 
 extern "C" int mk_gemm_blas(void* stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
                             const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,

@@ -577,6 +577,35 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
 }
 
 // ---------------------------------------------------------------- Adam
+// fp32 gradient, four parameters per thread per trip (16-byte loads and
+// stores; the bf16 copy as one 8-byte store); same arithmetic as adam_kernel.
+__global__ __launch_bounds__(kBlock) void adam_vec4_kernel(int64_t nvec, f32x4* __restrict__ p32,
+                                                         uint2* __restrict__ p16, const f32x4* __restrict__ grad,
+                                                         f32x4* __restrict__ m, f32x4* __restrict__ v, float lr,
+                                                         float b1, float omb1, float b2, float omb2, float eps,
+                                                         float bc1, float bc2, const float* __restrict__ hyper) {
+  if (hyper) {
+    lr = hyper[0];
+    bc1 = hyper[1];
+    bc2 = hyper[2];
+  }
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
+    const f32x4 g = grad[i], m0 = m[i], v0 = v[i], p0 = p32[i];
+    f32x4 m1, v1, p1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m1.v[j] = b1 * m0.v[j] + omb1 * g.v[j];
+      v1.v[j] = b2 * v0.v[j] + omb2 * g.v[j] * g.v[j];
+      p1.v[j] = p0.v[j] - lr * (m1.v[j] / bc1) / (sqrtf(v1.v[j] / bc2) + eps);
+    }
+    m[i] = m1;
+    v[i] = v1;
+    p32[i] = p1;
+    if (p16) p16[i] = uint2{pack_bf16(p1.v[0], p1.v[1]), pack_bf16(p1.v[2], p1.v[3])};
+  }
+}
+
 // dp_train.py body(): m = b1 m + (1-b1) g; v = b2 v + (1-b2) g g;
 // p = p - lr (m / bc1) / (sqrt(v / bc2) + eps), in fp32 with the constants
 // b1, 1-b1, b2, 1-b2, eps each one fp32 rounding of the double value (as
@@ -938,7 +967,13 @@ int adam_launch(void* stream, int64_t n, int param_type, void* param, float* mas
   const dim3 g(grid_for(n)), b(kBlock);
   const float f_lr = float(lr), f_b1 = float(b1), f_omb1 = float(1.0 - b1), f_b2 = float(b2),
               f_omb2 = float(1.0 - b2), f_eps = float(eps), f_bc1 = float(bc1), f_bc2 = float(bc2);
-  if (grad_type == MK_F32)
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p32) | reinterpret_cast<uintptr_t>(grad) |
+                       reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v);
+  if (grad_type == MK_F32 && n % 4 == 0 && (al & 15) == 0 && (reinterpret_cast<uintptr_t>(p16) & 7) == 0)
+    hipLaunchKernelGGL(adam_vec4_kernel, dim3(grid_for(n / 4)), b, 0, s, n / 4, (f32x4*)p32, (uint2*)p16,
+                       (const f32x4*)grad, (f32x4*)m, (f32x4*)v, f_lr, f_b1, f_omb1, f_b2, f_omb2, f_eps, f_bc1,
+                       f_bc2, hyper);
+  else if (grad_type == MK_F32)
     hipLaunchKernelGGL(adam_kernel<float>, g, b, 0, s, n, p32, p16, (const float*)grad, m, v, f_lr, f_b1, f_omb1,
                        f_b2, f_omb2, f_eps, f_bc1, f_bc2, hyper);
   else if (grad_type == MK_BF16)

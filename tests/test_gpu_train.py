@@ -54,6 +54,61 @@ def test_gelu_tanh_bwd(K, dtype):
     np.testing.assert_array_equal(_f64(got8), _f64(got[:4096]))
 
 
+# ------------------------------------------------------------------ library GEMM
+def _gemm_err(got, a, b, ref):
+    """max |got - ref| relative to sum_k |a||b| (the fp32 accumulation bound)."""
+    scale = _f64(a).abs() @ _f64(b).abs()
+    return float(((_f64(got) - ref).abs() / (scale + 1e-30)).max())
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_blas_layouts(K, ta, tb, out_dtype):
+    """Every operand orientation the step uses (A or B stored transposed),
+    bf16 operands, fp32 / bf16 output, against float64."""
+    g = torch.Generator().manual_seed(int(ta) * 2 + int(tb))
+    M, N, Kd = 200, 136, 328
+    a_st = torch.randn(Kd, M, generator=g) if ta else torch.randn(M, Kd, generator=g)
+    b_st = torch.randn(N, Kd, generator=g) if tb else torch.randn(Kd, N, generator=g)
+    a = (a_st.bfloat16().cuda().t() if ta else a_st.bfloat16().cuda())
+    b = (b_st.bfloat16().cuda().t() if tb else b_st.bfloat16().cuda())
+    got = K.gemm_blas(a, b, out_dtype=out_dtype)
+    ref = _f64(a) @ _f64(b)
+    tol = 1e-5 if out_dtype == torch.float32 else 2 ** -8
+    if out_dtype == torch.float32:
+        assert _gemm_err(got, a, b, ref) < tol
+    else:
+        np.testing.assert_allclose(_f64(got), ref, rtol=2 ** -8, atol=1e-5 * float((_f64(a).abs() @ _f64(b).abs()).max()))
+
+
+def test_gemm_blas_batched_alpha_beta_and_f32(K):
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(3, 40, 24, generator=g).cuda()
+    b = torch.randn(3, 24, 56, generator=g).cuda()
+    c0 = torch.randn(3, 40, 56, generator=g).cuda()
+    got = K.gemm_blas(a, b, out=c0.clone(), alpha=0.5, beta=2.0)
+    ref = 0.5 * (_f64(a) @ _f64(b)) + 2.0 * _f64(c0)
+    assert float((_f64(got) - ref).abs().max()) < 1e-4
+
+
+@pytest.mark.parametrize("M,N,Kd,splits", [(768, 3072, 8192, 4), (96, 64, 512, 8), (64, 32, 64, 1)])
+def test_gemm_blas_splitk(K, M, N, Kd, splits):
+    """Weight-gradient form (A = Xᵀ stored [K, M]): split-K agrees with the
+    plain GEMM to fp32 accumulation and is bit-reproducible."""
+    g = torch.Generator().manual_seed(M + N + splits)
+    x = (torch.randn(Kd, M, generator=g)).bfloat16().cuda()
+    dy = torch.randn(Kd, N, generator=g).bfloat16().cuda()
+    a = x.t()
+    got = K.gemm_blas_splitk(a, dy, splits)
+    if M * N * Kd <= 96 * 64 * 512:
+        ref = _f64(a) @ _f64(dy)
+    else:
+        ref = _f64(K.gemm_blas(a, dy, out_dtype=torch.float32))
+    scale = float((_f64(x).abs().t() @ _f64(dy).abs()).max())
+    assert float((_f64(got) - ref).abs().max()) < 2e-6 * scale
+    assert torch.equal(got, K.gemm_blas_splitk(a, dy, splits))
+
+
 # ------------------------------------------------------------------ row adds
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8192, 768), (33, 2304)])
@@ -250,9 +305,9 @@ def _adam_ref(p, g, m, v, lr, b1, b2, eps, bc1, bc2):
     return p - lr * (m / bc1) / (np.sqrt(v / bc2) + eps), m, v
 
 
-def test_adam_update_f32_and_master(K):
+@pytest.mark.parametrize("n", [100003, 100000])  # scalar kernel; four-wide kernel (n % 4 == 0)
+def test_adam_update_f32_and_master(K, n):
     rng = np.random.default_rng(0)
-    n = 100003
     p = rng.standard_normal(n).astype(np.float32)
     g = rng.standard_normal(n).astype(np.float32)
     m = (rng.standard_normal(n) * 0.1).astype(np.float32)
