@@ -245,3 +245,79 @@ def scatter_add(n=65536, vocab=50257, dim=768) -> str:
 
 ALL = {"mlp": mlp, "layernorm": layernorm, "gelu": gelu, "reduce_sum": reduce_sum,
        "argmax": argmax, "sdpa": sdpa, "gather": gather, "scatter_add": scatter_add}
+
+
+def adam_update(n=1 << 20, b1=0.9, b2=0.999, eps=1e-8) -> str:
+    """The per-parameter Adam update of temp/dp_train.py:71-75 as its own
+    jit with the state donated, ``jax.jit(upd, donate_argnums=(0, 1, 2))``:
+    upd(p, m, v, g, bc1, bc2, lr) -> (p - lr (m'/bc1) / (sqrt(v'/bc2) + eps),
+    m' = b1 m + (1-b1) g, v' = b2 v + (1-b2) g g).  JAX marks each donated
+    argument with the output it aliases (``tf.aliasing_output``); the
+    Python-float constants fold to f32."""
+    t, s = _t((n,), "f32"), "tensor<f32>"
+
+    def c(x):
+        return f"{float(x):.9e}"
+
+    def bc(v):
+        return f"stablehlo.broadcast_in_dim {v}, dims = [] : ({s}) -> {t}"
+    return f"""module @jit_upd attributes {{mhlo.num_partitions = 1 : i32, mhlo.num_replicas = 1 : i32}} {{
+  func.func public @main(%arg0: {t} {{tf.aliasing_output = 0 : i32}}, %arg1: {t} {{tf.aliasing_output = 1 : i32}}, %arg2: {t} {{tf.aliasing_output = 2 : i32}}, %arg3: {t}, %arg4: {s}, %arg5: {s}, %arg6: {s}) -> ({t} {{jax.result_info = "[0]"}}, {t} {{jax.result_info = "[1]"}}, {t} {{jax.result_info = "[2]"}}) {{
+    %cst = stablehlo.constant dense<{c(b1)}> : {s}
+    %0 = {bc("%cst")}
+    %1 = stablehlo.multiply %0, %arg1 : {t}
+    %cst_0 = stablehlo.constant dense<{c(1 - b1)}> : {s}
+    %2 = {bc("%cst_0")}
+    %3 = stablehlo.multiply %2, %arg3 : {t}
+    %4 = stablehlo.add %1, %3 : {t}
+    %cst_1 = stablehlo.constant dense<{c(b2)}> : {s}
+    %5 = {bc("%cst_1")}
+    %6 = stablehlo.multiply %5, %arg2 : {t}
+    %cst_2 = stablehlo.constant dense<{c(1 - b2)}> : {s}
+    %7 = {bc("%cst_2")}
+    %8 = stablehlo.multiply %7, %arg3 : {t}
+    %9 = stablehlo.multiply %8, %arg3 : {t}
+    %10 = stablehlo.add %6, %9 : {t}
+    %11 = {bc("%arg4")}
+    %12 = stablehlo.divide %4, %11 : {t}
+    %13 = {bc("%arg6")}
+    %14 = stablehlo.multiply %13, %12 : {t}
+    %15 = {bc("%arg5")}
+    %16 = stablehlo.divide %10, %15 : {t}
+    %17 = stablehlo.sqrt %16 : {t}
+    %cst_3 = stablehlo.constant dense<{c(eps)}> : {s}
+    %18 = {bc("%cst_3")}
+    %19 = stablehlo.add %17, %18 : {t}
+    %20 = stablehlo.divide %14, %19 : {t}
+    %21 = stablehlo.subtract %arg0, %20 : {t}
+    return %21, %4, %10 : {t}, {t}, {t}
+  }}
+}}
+"""
+
+
+def donated(kind: str, n=64) -> str:
+    """Small donation cases: 'matmul' (x @ w with x donated: the GEMM reads
+    x while writing, so no in-place alias), 'transpose_add' (x.T + y with x
+    donated: read in another layout), 'donor_add' (x + y with x marked
+    ``jax.buffer_donor``: output chosen by type, in place)."""
+    t = _t((n, n), "f32")
+    if kind == "matmul":
+        body = f"%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0] : ({t}, {t}) -> {t}"
+        attr = "{tf.aliasing_output = 0 : i32}"
+    elif kind == "transpose_add":
+        body = (f"%t = stablehlo.transpose %arg0, dims = [1, 0] : ({t}) -> {t}\n"
+                f"    %0 = stablehlo.add %t, %arg1 : {t}")
+        attr = "{tf.aliasing_output = 0 : i32}"
+    elif kind == "donor_add":
+        body = f"%0 = stablehlo.add %arg0, %arg1 : {t}"
+        attr = "{jax.buffer_donor = true}"
+    else:
+        raise ValueError(kind)
+    return f"""module @jit_donated attributes {{mhlo.num_partitions = 1 : i32, mhlo.num_replicas = 1 : i32}} {{
+  func.func public @main(%arg0: {t} {attr}, %arg1: {t}) -> ({t} {{jax.result_info = ""}}) {{
+    {body}
+    return %0 : {t}
+  }}
+}}
+"""

@@ -79,6 +79,12 @@ class NamedValue(_c.Structure):
                 ("type", _c.c_int), ("value", _c.c_int64), ("value_size", _SZ)]
 
 
+class ExecuteOptions(_c.Structure):
+    _fields_ = [("struct_size", _SZ), ("extension_start", _P), ("send_callbacks", _P), ("recv_callbacks", _P),
+                ("num_send_ops", _SZ), ("num_recv_ops", _SZ), ("launch_id", _c.c_int),
+                ("non_donatable_input_indices", _P), ("num_non_donatable_input_indices", _SZ)]
+
+
 class Program(_c.Structure):
     _fields_ = [("struct_size", _SZ), ("extension_start", _P), ("code", _P), ("code_size", _SZ),
                 ("format", _c.c_char_p), ("format_size", _SZ)]
@@ -121,6 +127,8 @@ A = {
     "Buffer_ToHostBuffer": _args("BufferToHostBuffer", [("src", _P), ("host_layout", _P), ("dst", _P),
                                                         ("dst_size", _SZ), ("event", _P)]),
     "Buffer_ReadyEvent": _args("BufferReadyEvent", [("buffer", _P), ("event", _P)]),
+    "Buffer_IsDeleted": _args("BufferIsDeleted", [("buffer", _P), ("is_deleted", _c.c_bool)]),
+    "Buffer_UnsafePointer": _args("BufferUnsafePointer", [("buffer", _P), ("buffer_pointer", _c.c_size_t)]),
     "LoadedExecutable_Destroy": _args("LoadedDestroy", [("executable", _P)]),
     "LoadedExecutable_Delete": _args("LoadedDelete", [("executable", _P)]),
     "LoadedExecutable_GetExecutable": _args("LoadedGetExecutable", [("loaded_executable", _P),
@@ -314,6 +322,14 @@ class Buffer:
     def delete(self):
         self.c.p.call("Buffer_Delete", buffer=self.h)
 
+    @property
+    def is_deleted(self) -> bool:
+        return bool(self.c.p.call("Buffer_IsDeleted", buffer=self.h).is_deleted)
+
+    @property
+    def device_pointer(self) -> int:
+        return int(self.c.p.call("Buffer_UnsafePointer", buffer=self.h).buffer_pointer)
+
     def destroy(self):
         if self.h:
             self.c.p.call("Buffer_Destroy", buffer=self.h)
@@ -357,14 +373,24 @@ class Executable:
         self.c.p.call("Executable_OptimizedProgram", executable=self.e, program=_c.pointer(prog))
         return buf.raw[:prog.code_size].decode()
 
-    def execute(self, args, wait=True):
+    def execute(self, args, wait=True, non_donatable=None):
+        """Run on one device; inputs the program aliases to outputs are
+        donated unless listed in non_donatable."""
         n = self.num_outputs
+        opts = None
+        if non_donatable is not None:
+            idx = (_c.c_int64 * max(len(non_donatable), 1))(*non_donatable)
+            o = ExecuteOptions()
+            o.struct_size = _c.sizeof(ExecuteOptions)
+            o.non_donatable_input_indices = _c.addressof(idx)
+            o.num_non_donatable_input_indices = len(non_donatable)
+            opts = _c.addressof(o)
         arg_arr = (_c.c_void_p * max(len(args), 1))(*[b.h for b in args])
         arg_lists = (_c.c_void_p * 1)(_c.addressof(arg_arr))
         out_arr = (_c.c_void_p * max(n, 1))()
         out_lists = (_c.c_void_p * 1)(_c.addressof(out_arr))
         events = (_c.c_void_p * 1)()
-        self.c.p.call("LoadedExecutable_Execute", executable=self.h, options=None,
+        self.c.p.call("LoadedExecutable_Execute", executable=self.h, options=opts,
                       argument_lists=_c.addressof(arg_lists), num_devices=1, num_args=len(args),
                       output_lists=_c.addressof(out_lists), device_complete_events=_c.addressof(events),
                       execute_device=None)

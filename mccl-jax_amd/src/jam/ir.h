@@ -94,6 +94,11 @@ struct Func {
   std::string name;
   bool is_public = true;
   std::vector<int> args;
+  // per argument: `tf.aliasing_output = k` (the output a donated argument may
+  // share memory with; -1 none) and `jax.buffer_donor` (donated, output
+  // chosen by type)
+  std::vector<int> arg_alias;
+  std::vector<bool> arg_donor;
   std::vector<TensorType> result_types;
   Block body;
 };

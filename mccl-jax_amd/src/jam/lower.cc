@@ -61,6 +61,7 @@ std::string Program::Dump() const {
      << " outputs, " << steps.size() << " steps, arena " << arena_bytes << " B, " << consts.size()
      << " consts\n";
   for (const auto& p : patterns) os << "  pattern " << p << "\n";
+  for (const auto& a : alias_notes) os << "  alias " << a << "\n";
   for (size_t i = 0; i < steps.size(); ++i) {
     os << "  [" << i << "] " << StepName(steps[i].kind);
     if (!steps[i].note.empty()) os << " (" << steps[i].note << ")";
@@ -379,6 +380,7 @@ class Lowerer {
       Liveness();
       Walk();
       PackArena();
+      Aliases(*main);
       return prog_;
     } catch (const std::string& e) {
       err = e;
@@ -387,6 +389,128 @@ class Lowerer {
   }
 
  private:
+  // -------------------------------------------------------------- donation
+  // Buffer indices a step writes (the rest it reads), per the encodings in
+  // run.cc.
+  static std::vector<size_t> WrittenBufs(const Step& s) {
+    switch (s.kind) {
+      case StepKind::kGemm: return {2};
+      case StepKind::kSdpa: return {3};
+      case StepKind::kRowReduce: return {1};
+      case StepKind::kArgmax: return {1, 2};
+      case StepKind::kLayerNorm: return {3};
+      case StepKind::kGelu: return {1};
+      case StepKind::kEw: return {size_t(s.i[7])};
+      case StepKind::kGather: return {2};
+      case StepKind::kScatterAdd: return {3, 4};
+      case StepKind::kIota: return {0};
+      case StepKind::kCopyStrided: return {1};
+      case StepKind::kSoftmax: return {1};
+      case StepKind::kConvert: return {1};
+      case StepKind::kFill: return {0};
+      case StepKind::kCopy: return {1};
+    }
+    return {};
+  }
+
+  // Can output `o` be computed straight into input `in`'s memory?
+  bool InPlaceSafe(int in, int o, std::string& why) const {
+    const auto& steps = prog_->steps;
+    auto is_in = [&](const BufRef& b) { return b.space == Space::kInput && b.index == in; };
+    auto is_out = [&](const BufRef& b) { return b.space == Space::kOutput && b.index == o; };
+    int first = -1;
+    for (size_t k = 0; k < steps.size() && first < 0; ++k)
+      for (size_t w : WrittenBufs(steps[k]))
+        if (w < steps[k].bufs.size() && is_out(steps[k].bufs[w])) first = int(k);
+    if (first < 0) {
+      why = "output never written";
+      return false;
+    }
+    for (size_t k = size_t(first) + 1; k < steps.size(); ++k)
+      for (const BufRef& b : steps[k].bufs)
+        if (is_in(b)) {
+          why = "input read after the output is first written (step " + std::to_string(k) + ")";
+          return false;
+        }
+    const Step& s = steps[size_t(first)];
+    const std::vector<size_t> wr = WrittenBufs(s);
+    std::vector<size_t> reads;
+    for (size_t j = 0; j < s.bufs.size(); ++j)
+      if (is_in(s.bufs[j]) && std::find(wr.begin(), wr.end(), j) == wr.end()) reads.push_back(j);
+    if (reads.empty()) return true;
+    // the writer reads the input too: only element-for-element in place
+    const BufRef& out = s.bufs[wr.front()];
+    for (size_t j : reads)
+      if (s.bufs[j].offset != 0 || out.offset != 0) {
+        why = "writer reads the input at an offset";
+        return false;
+      }
+    switch (s.kind) {
+      case StepKind::kGelu:
+        return true;
+      case StepKind::kConvert:
+        if (DTypeBytes(DType(s.i[0])) == DTypeBytes(DType(s.i[1]))) return true;
+        why = "convert changes the element width";
+        return false;
+      case StepKind::kEw: {
+        const int rank = int(s.i[0]);
+        std::vector<int64_t> dims(s.i.begin() + 1, s.i.begin() + 1 + rank);
+        const std::vector<int64_t> dense = DenseStrides(dims);
+        const int out_type = int(s.i[9]);
+        for (size_t j : reads) {
+          if (DTypeBytes(DType(s.types[j])) != DTypeBytes(DType(out_type))) {
+            why = "elementwise input and output widths differ";
+            return false;
+          }
+          for (int d = 0; d < rank; ++d)
+            if (dims[size_t(d)] > 1 && s.strides[j * 6 + size_t(d)] != dense[size_t(d)]) {
+              why = "elementwise input read in another layout (broadcast / transpose)";
+              return false;
+            }
+        }
+        return true;
+      }
+      default:
+        why = std::string("writer is ") + StepName(s.kind) + ", not element-for-element";
+        return false;
+    }
+  }
+
+  void Aliases(const Func& main) {
+    const size_t n_in = prog_->inputs.size(), n_out = prog_->outputs.size();
+    prog_->input_alias.assign(n_in, -1);
+    std::vector<bool> claimed(n_out, false);
+    auto consider = [&](size_t i, int o, const char* how) {
+      std::string why;
+      if (o < 0 || size_t(o) >= n_out) {
+        why = "no such output";
+      } else if (claimed[size_t(o)]) {
+        why = "output already aliased";
+      } else if (prog_->inputs[i].bytes() != prog_->outputs[size_t(o)].bytes()) {
+        why = "sizes differ";
+      } else if (InPlaceSafe(int(i), o, why)) {
+        prog_->input_alias[i] = o;
+        claimed[size_t(o)] = true;
+        prog_->alias_notes.push_back("input " + std::to_string(i) + " -> output " + std::to_string(o) +
+                                     " in place (" + how + ")");
+        return;
+      }
+      prog_->alias_notes.push_back("input " + std::to_string(i) + " -> output " + std::to_string(o) +
+                                   " not in place (" + how + "): " + why);
+    };
+    for (size_t i = 0; i < n_in && i < main.arg_alias.size(); ++i)
+      if (main.arg_alias[i] >= 0) consider(i, main.arg_alias[i], "tf.aliasing_output");
+    // donors without an explicit output: the first unclaimed output of the same type
+    for (size_t i = 0; i < n_in && i < main.arg_donor.size(); ++i) {
+      if (!main.arg_donor[i] || prog_->input_alias[i] >= 0 || main.arg_alias[i] >= 0) continue;
+      int match = -1;
+      for (size_t o = 0; o < n_out && match < 0; ++o)
+        if (!claimed[o] && prog_->outputs[o] == prog_->inputs[i]) match = int(o);
+      if (match >= 0) consider(i, match, "jax.buffer_donor");
+      else prog_->alias_notes.push_back("input " + std::to_string(i) + " donated: no output of its type");
+    }
+  }
+
   // -------------------------------------------------------------- inlining
   // Appends the ops of `f` (with args bound to `actuals`) to ops_, renaming
   // values; returns the values `f` returns in `results`.

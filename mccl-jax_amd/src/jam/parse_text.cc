@@ -590,11 +590,22 @@ class Parser {
       advance();
       expect(":");
       TensorType t = parse_type();
-      skip_attr_dict_opt();
+      int alias = -1;
+      bool donor = false;
+      if (is_punct("{")) {
+        const Attr ad = parse_attr_dict();
+        if (const Attr* al = ad.get("tf.aliasing_output")) {
+          if (al->kind != Attr::kInt) fail("tf.aliasing_output must be an integer");
+          alias = int(al->i);
+        }
+        if (const Attr* d = ad.get("jax.buffer_donor")) donor = d->kind == Attr::kBool ? d->i != 0 : true;
+      }
       skip_loc();
       int id = m_.new_value(t, name);
       define(name, {id});
       f.args.push_back(id);
+      f.arg_alias.push_back(alias);
+      f.arg_donor.push_back(donor);
       if (is_punct(",")) advance();
     }
     advance();

@@ -57,6 +57,13 @@ class Program {
   std::vector<Step> steps;
   std::vector<ConstBlob> consts;
   size_t arena_bytes = 0;
+  // Donation: per input, the output whose launches may write straight into
+  // this input's memory when the caller donates it (-1: none).  Set only
+  // where the plan allows it: no launch reads the input after the output's
+  // first writer, which reads it (if at all) element for element in the
+  // same layout.
+  std::vector<int> input_alias;
+  std::vector<std::string> alias_notes;  // why a requested alias was or was not taken (dumps)
   std::vector<std::string> patterns;   // fused patterns recognised (for tests / dumps)
   std::string name = "jam.main";
 

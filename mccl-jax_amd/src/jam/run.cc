@@ -113,7 +113,7 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     case StepKind::kFill:
       return mk_fill(st, int(i[0]), i[1], uint64_t(i[2]), P(0));
     case StepKind::kCopy: {
-      if (i[0] == 0) return MK_OK;
+      if (i[0] == 0 || P(0) == P(1)) return MK_OK;  // same memory: an output written over its donated input
       hipError_t e = hipMemcpyAsync(P(1), P(0), size_t(i[0]), hipMemcpyDeviceToDevice, stream);
       return e == hipSuccess ? MK_OK : MK_ERR_LAUNCH;
     }
@@ -124,7 +124,7 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
 }  // namespace
 
 std::string Run(Program& prog, exec::DeviceContext& dev, const std::vector<RunInput>& inputs,
-                std::vector<RunOutput>& outputs) {
+                std::vector<RunOutput>& outputs, const std::vector<void*>* preset) {
   if (inputs.size() != prog.inputs.size()) return "jam run: wrong number of inputs";  // jam_run.mm:364
   for (size_t k = 0; k < inputs.size(); ++k) {
     if (inputs[k].nbytes != prog.inputs[k].bytes()) return "jam run: input size mismatch";  // jam_run.mm:376
@@ -133,14 +133,22 @@ std::string Run(Program& prog, exec::DeviceContext& dev, const std::vector<RunIn
   std::string err;
   std::vector<void*>* consts = prog.DeviceConsts(dev.ordinal());
   if (!consts) return "jam run: constant upload failed";
+  if (preset && preset->size() != prog.outputs.size()) return "jam run: preset output list has the wrong length";
   std::vector<RunOutput> outs(prog.outputs.size());
+  std::vector<bool> owned(outs.size(), true);
   auto release = [&]() {
-    for (auto& o : outs) dev.Free(o.data);
+    for (size_t k = 0; k < outs.size(); ++k)
+      if (owned[k]) dev.Free(outs[k].data);
   };
   for (size_t k = 0; k < outs.size(); ++k) {
     outs[k].type = prog.outputs[k];
     outs[k].nbytes = prog.outputs[k].bytes();
     if (outs[k].nbytes == 0) continue;
+    if (preset && (*preset)[k]) {
+      outs[k].data = (*preset)[k];
+      owned[k] = false;
+      continue;
+    }
     outs[k].data = dev.Alloc(outs[k].nbytes, &err);
     if (!outs[k].data) {
       release();

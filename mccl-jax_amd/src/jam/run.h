@@ -26,8 +26,11 @@ struct RunOutput {
 };
 
 // Queue every step of `prog` on dev.stream().  On error, returns a message
-// prefixed "jam run:" and frees anything it allocated.
+// prefixed "jam run:" and frees anything it allocated.  `preset` (optional,
+// one entry per output) gives memory an output is written into instead of a
+// fresh allocation: a donated input's buffer, for an output
+// prog.input_alias names.  Run neither allocates nor frees preset memory.
 std::string Run(Program& prog, exec::DeviceContext& dev, const std::vector<RunInput>& inputs,
-                std::vector<RunOutput>& outputs);
+                std::vector<RunOutput>& outputs, const std::vector<void*>* preset = nullptr);
 
 }  // namespace mi::jam

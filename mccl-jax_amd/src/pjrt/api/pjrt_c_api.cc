@@ -21,12 +21,14 @@
 
 #include <atomic>
 #include <condition_variable>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <memory>
 #include <mutex>
+#include <set>
 #include <string>
 #include <thread>
 #include <utility>
@@ -1029,6 +1031,35 @@ PJRT_Error* LoadedExecute(PJRT_LoadedExecutable_Execute_Args* a) {
     std::vector<mi::jam::RunInput> ins;
     ins.reserve(a->num_args);
     std::vector<std::shared_ptr<Storage>> keep;  // inputs stay alive until launches are queued
+    // Donation: an input the program may overwrite with an output
+    // (prog->input_alias) gives that output its memory, unless the caller
+    // lists it in non_donatable_input_indices, or its storage is shared
+    // (external references, another buffer, or passed twice).
+    std::vector<void*> preset(prog->outputs.size(), nullptr);
+    std::vector<std::pair<size_t, int>> donated;  // (argument, output)
+    {
+      std::set<int64_t> keep_args;
+      const PJRT_ExecuteOptions* opt = a->options;
+      const size_t need = offsetof(PJRT_ExecuteOptions, num_non_donatable_input_indices) + sizeof(size_t);
+      if (opt && opt->struct_size < need)
+        return Err(PJRT_Error_Code_INVALID_ARGUMENT, "Execute: PJRT_ExecuteOptions struct_size too small");
+      if (opt && opt->non_donatable_input_indices)
+        for (size_t k = 0; k < opt->num_non_donatable_input_indices; ++k)
+          keep_args.insert(opt->non_donatable_input_indices[k]);
+      for (size_t i = 0; i < a->num_args && i < prog->input_alias.size(); ++i) {
+        const int o = prog->input_alias[i];
+        PJRT_Buffer* b = a->argument_lists[d][i];
+        if (o < 0 || keep_args.count(int64_t(i)) || !b || b->deleted || !b->storage || b->storage->host ||
+            b->storage->dev != ctx || b->external_refs != 0 || b->storage.use_count() != 1)
+          continue;
+        bool twice = false;
+        for (size_t j = 0; j < a->num_args; ++j)
+          if (j != i && a->argument_lists[d][j] == b) twice = true;
+        if (twice) continue;
+        preset[size_t(o)] = b->storage->data;
+        donated.emplace_back(i, o);
+      }
+    }
     for (size_t i = 0; i < a->num_args; ++i) {
       PJRT_Buffer* b = a->argument_lists[d][i];
       if (!b || b->deleted || !b->storage)
@@ -1042,12 +1073,20 @@ PJRT_Error* LoadedExecute(PJRT_LoadedExecutable_Execute_Args* a) {
       keep.push_back(b->storage);
     }
     std::vector<mi::jam::RunOutput> outs;
-    err = mi::jam::Run(*prog, *ctx, ins, outs);
+    err = mi::jam::Run(*prog, *ctx, ins, outs, &preset);
     if (!err.empty()) return Err(PJRT_Error_Code_INTERNAL, err);
     std::shared_ptr<EventState> done = RecordEvent(ctx, &err);
     if (!done) return Err(PJRT_Error_Code_INTERNAL, "Execute: " + err);
+    // donated inputs hand their storage to the output and are deleted
+    std::vector<std::shared_ptr<Storage>> from_input(outs.size());
+    for (const auto& [arg, o] : donated) {
+      PJRT_Buffer* b = a->argument_lists[d][arg];
+      keep.clear();  // drop the extra references taken above
+      from_input[size_t(o)] = std::move(b->storage);
+      b->deleted = true;
+    }
     for (size_t i = 0; i < outs.size(); ++i) {
-      auto s = std::make_shared<Storage>();
+      std::shared_ptr<Storage> s = from_input[i] ? from_input[i] : std::make_shared<Storage>();
       s->data = outs[i].data;
       s->nbytes = outs[i].nbytes;
       s->dev = ctx;

@@ -168,3 +168,19 @@ def test_cpp_driver_compiles(tmp_path):
     r = subprocess.run([exe, PJRT_LIBRARY, str(mod), "--compile-only"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     assert "PJRT API 0.55" in r.stdout and "platform mi355x" in r.stdout and "compiled: 1 outputs" in r.stdout
+
+
+def test_donation_aliases_in_plan(client):
+    """tf.aliasing_output / jax.buffer_donor on @main's arguments: the plan
+    writes an output over its donated input only where that is safe
+    (element-for-element, no later reader), and says why otherwise."""
+    plan, _, shapes = _plan(client, modules.adam_update(4096))
+    assert shapes == [(4096,)] * 3
+    for i in range(3):
+        assert f"alias input {i} -> output {i} in place (tf.aliasing_output)" in plan, plan
+    plan, _, _ = _plan(client, modules.donated("matmul"))
+    assert "alias input 0 -> output 0 not in place (tf.aliasing_output): writer is gemm" in plan
+    plan, _, _ = _plan(client, modules.donated("transpose_add"))
+    assert "alias input 0 -> output 0 not in place" in plan and "layout" in plan
+    plan, _, _ = _plan(client, modules.donated("donor_add"))
+    assert "alias input 0 -> output 0 in place (jax.buffer_donor)" in plan
