@@ -15,6 +15,7 @@
 #include "mk_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mk {
 namespace {
@@ -303,6 +304,75 @@ __global__ __launch_bounds__(kBlock) void scatter_accumulate_kernel(
   }
 }
 
+// fp32 rows as float4 vectors, one wave per destination row, all of a row's
+// loads in flight together: the bucket's sorted update indices come in with
+// one vector load (64 at a time) and are broadcast with v_readlane; the table
+// row and up to kScatterU update rows are loaded before any add, and the adds
+// run in bucket order (= increasing update index), so the result is the
+// sequential one bit for bit.  Columns go in blocks of 64 * RV float4.
+constexpr int kScatterU = 4;
+
+template <int RV>
+__global__ __launch_bounds__(kBlock) void scatter_accumulate_vec_kernel(
+    const f32x4* __restrict__ table, f32x4* __restrict__ out, int64_t n_rows, int64_t nv,
+    const f32x4* __restrict__ updates, const uint32_t* __restrict__ vals, const uint32_t* __restrict__ bounds,
+    bool in_place) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (r >= n_rows) return;
+  const uint32_t b = bounds[2 * r], e = bounds[2 * r + 1];
+  if (in_place && b == e) return;  // untouched row already holds its value
+  for (int64_t cb = 0; cb < nv; cb += 64 * RV) {
+    // lanes past the row end load its last vector (always in bounds) and
+    // store nothing, so no load needs a per-lane predicate
+    int64_t col[RV];
+    bool ok[RV];
+#pragma unroll
+    for (int q = 0; q < RV; ++q) {
+      const int64_t c = cb + q * 64 + lane;
+      ok[q] = c < nv;
+      col[q] = ok[q] ? c : nv - 1;
+    }
+    uint32_t myv = (uint32_t(lane) < e - b) ? vals[b + lane] : 0u;  // first chunk of bucket indices
+    f32x4 acc[RV];
+#pragma unroll
+    for (int q = 0; q < RV; ++q) acc[q] = table[r * nv + col[q]];
+    for (uint32_t j0 = b; j0 < e; j0 += 64) {
+      const uint32_t cnt = min(64u, e - j0);
+      if (j0 != b) myv = (uint32_t(lane) < cnt) ? vals[j0 + lane] : 0u;
+      for (uint32_t k0 = 0; k0 < cnt; k0 += kScatterU) {
+        const uint32_t g = min(uint32_t(kScatterU), cnt - k0);  // wave-uniform group size
+        int64_t row[kScatterU];
+#pragma unroll
+        for (int t = 0; t < kScatterU; ++t)
+          row[t] = int64_t(__builtin_amdgcn_readlane(myv, int(k0 + min(uint32_t(t), g - 1))));
+        f32x4 u[kScatterU][RV];
+        // loads of the group (g rows), then the adds in order
+        auto run = [&](auto gn) __attribute__((always_inline)) {
+          constexpr int G = decltype(gn)::value;
+#pragma unroll
+          for (int t = 0; t < G; ++t)
+#pragma unroll
+            for (int q = 0; q < RV; ++q) u[t][q] = updates[row[t] * nv + col[q]];
+#pragma unroll
+          for (int t = 0; t < G; ++t)
+#pragma unroll
+            for (int q = 0; q < RV; ++q)
+#pragma unroll
+              for (int z = 0; z < 4; ++z) acc[q].v[z] += u[t][q].v[z];
+        };
+        if (g == 4) run(std::integral_constant<int, 4>{});
+        else if (g == 3) run(std::integral_constant<int, 3>{});
+        else if (g == 2) run(std::integral_constant<int, 2>{});
+        else run(std::integral_constant<int, 1>{});
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < RV; ++q)
+      if (ok[q]) out[r * nv + col[q]] = acc[q];
+  }
+}
+
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct ScatterWs {
@@ -416,7 +486,17 @@ extern "C" int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int6
                       ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out) |
                         reinterpret_cast<uintptr_t>(updates)) & 15u) == 0;
   dim3 g(blocks_for(n_rows, kBlock / 64));
-  if (dtype == MK_F32)
+  if (dtype == MK_F32 && vec_ok) {
+    const int64_t nv = row_len / 4;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, g, dim3(kBlock), 0, s, (const f32x4*)table, (f32x4*)out, n_rows, nv,
+                         (const f32x4*)updates, w.vals0, w.bounds, in_place);
+    };
+    if (nv <= 64) go(scatter_accumulate_vec_kernel<1>);
+    else if (nv <= 128) go(scatter_accumulate_vec_kernel<2>);
+    else if (nv <= 192) go(scatter_accumulate_vec_kernel<3>);
+    else go(scatter_accumulate_vec_kernel<4>);
+  } else if (dtype == MK_F32)
     hipLaunchKernelGGL(scatter_accumulate_kernel<false>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, vec_ok);
   else
     hipLaunchKernelGGL(scatter_accumulate_kernel<true>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, false);
