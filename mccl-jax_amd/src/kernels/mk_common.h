@@ -136,6 +136,31 @@ __device__ inline float wave_sum(float v) {
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
+// The same sum through DPP lane moves instead of ds_bpermute round trips:
+// xor 1 and xor 2 (quad_perm), then row_half_mirror and row_mirror (which
+// act as xor 4 / xor 8 once the groups below them hold equal values), then
+// the four 16-lane row totals read with v_readlane and added.  A fixed order
+// (deterministic, though not the butterfly's), and a few VALU cycles per
+// step instead of an LDS round trip.
+__device__ inline float dpp_f(float v, int ctrl) {
+  switch (ctrl) {  // the control word must be a constant
+    case 0xB1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    case 0x4E: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    case 0x141: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  }
+}
+__device__ inline float wave_sum_dpp(float v) {
+  v += dpp_f(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += dpp_f(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += dpp_f(v, 0x141);  // row_half_mirror
+  v += dpp_f(v, 0x140);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
 __device__ inline float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));

@@ -359,7 +359,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
     for (int k = 0; k < KV; ++k)
 #pragma unroll
       for (int j = 0; j < NV; ++j) sx += xv[k][j];
-    const float mean = wave_sum(sx) * inv_n;
+    const float mean = wave_sum_dpp(sx) * inv_n;
     float q = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
         const float d = (c < cols) ? xv[k][j] - mean : 0.f;
         q += d * d;
       }
-    const float rstd = 1.f / sqrtf(wave_sum(q) * inv_n + a.eps);
+    const float rstd = 1.f / sqrtf(wave_sum_dpp(q) * inv_n + a.eps);
     float sg = 0.f, sgx = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
         accb[k][j] += dv[k][j];
         xv[k][j] = xh;
       }
-    const float mg = wave_sum(sg) * inv_n, mgx = wave_sum(sgx) * inv_n;
+    const float mg = wave_sum_dpp(sg) * inv_n, mgx = wave_sum_dpp(sgx) * inv_n;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
       float o[NV];
