@@ -296,6 +296,25 @@ int mk_fill(void* stream, int elem_bytes, int64_t n, uint64_t pattern, void* out
 int mk_add_rows(void* stream, int io_type, int64_t rows, int64_t cols, const void* a, const void* b,
                 const void* bias, void* out);
 
+/* Residual add and LayerNorm in one pass, bf16 rows:
+ *   sum = a + b + bias[c]      (fp32 adds, one RNE rounding; as mk_add_rows)
+ *   y   = (sum - mean) rstd gamma + beta over each row of the rounded sum
+ *         (two-pass mean / variance, as mk_layernorm)
+ * The pre-LN block's `x + proj(h) + bias` feeding the next LayerNorm
+ * (elementwise.mm add, then the LayerNorm pattern of reduce.mm:79-108),
+ * both results stored (the sum is the residual stream the backward reads).
+ * b, bias, gamma (1), beta (0) may be NULL; cols % 4 == 0, cols <= 2048;
+ * 8-byte aligned operands. */
+int mk_add_layernorm(void* stream, int64_t rows, int64_t cols, const void* a, const void* b,
+                     const void* bias, const void* gamma, const void* beta, float eps, void* sum_out,
+                     void* y);
+
+/* pre = x + bias[c] (bf16, one rounding) and y = gelu_tanh(pre) (as
+ * mk_gelu_tanh on the stored pre) in one pass: the MLP's bias add and
+ * activation (elementwise.mm add + the GELU chain).  pre may alias x. */
+int mk_bias_gelu(void* stream, int64_t rows, int64_t cols, const void* x, const void* bias, void* pre_out,
+                 void* y);
+
 /* dx = dy * gelu_tanh'(x), gelu_tanh as mk_gelu_tanh; fp32 math, one rounding
  * on store.  io_type ∈ {MK_BF16, MK_F32}.  dx may alias dy. */
 int mk_gelu_tanh_bwd(void* stream, int io_type, int64_t n, const void* x, const void* dy, void* dx);

@@ -60,6 +60,8 @@ SIGNATURES = {
     "mk_fill": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
     "mk_gelu_tanh_bwd": (_I, [_P, _I, _I64, _P, _P, _P]),
     "mk_add_rows": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P]),
+    "mk_add_layernorm": (_I, [_P, _I64, _I64, _P, _P, _P, _P, _P, _F, _P, _P]),
+    "mk_bias_gelu": (_I, [_P, _I64, _I64, _P, _P, _P, _P]),
     "mk_col_sum_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "mk_col_sum": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
     "mk_layernorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),

@@ -263,6 +263,11 @@ class GPT2TrainStep:
             calls.append(_Call(lib.mk_layernorm, [st, _I(BF16), _I64(T), _I64(d), x, W(gname), W(bname),
                                                   _F(c.ln_eps), y], "mk_layernorm"))
 
+        def add_layernorm(a, b, bias, ln, sum_out, y):
+            """sum_out = a + b + bias, y = LayerNorm(sum_out) with ln's parameters"""
+            calls.append(_Call(lib.mk_add_layernorm, [st, _I64(T), _I64(d), a, b, bias, W(ln + "_g"), W(ln + "_b"),
+                                                      _F(c.ln_eps), sum_out, y], "mk_add_layernorm"))
+
         def colsum(x, rows, cols, out):
             calls.append(_Call(lib.mk_col_sum, [st, _I(BF16), _I64(rows), _I64(cols), x, out, ws], "mk_col_sum"))
 
@@ -280,9 +285,11 @@ class GPT2TrainStep:
                                                 P(self.ids), P(self.x[0])], "mk_gather_rows"))
         # x0 += wpe broadcast over the batch: [B, S*d] + [S*d]
         add_rows(P(self.x[0]), B, S * d, P(self.x[0]), bias=W("wpe"), tag="pos")
+        # LN1 of layer 0 stands alone; every later LayerNorm (LN1 of the next
+        # layer, LN2, the final LN) is fused with the residual add before it
+        layernorm(P(self.x[0]), "h0.ln1_g", "h0.ln1_b", P(self.h1[0]))
         for l in range(L):
             p = f"h{l}."
-            layernorm(P(self.x[l]), p + "ln1_g", p + "ln1_b", P(self.h1[l]))
             gemm(BF16, BF16, T, 3 * d, d, P(self.h1[l]), d, 1, W(p + "w_qkv"), 3 * d, 1, P(self.qkv[l]), 3 * d,
                  tag="qkv")
             add_rows(P(self.qkv[l]), T, 3 * d, P(self.qkv[l]), bias=W(p + "b_qkv"), tag="bias")
@@ -293,15 +300,13 @@ class GPT2TrainStep:
                                                  P(self.att[l]), _I64(S * d), _I64(hd), _I64(d),
                                                  _F(scale), _I(1), P(self.lse[l])], "mk_sdpa_fwd"))
             gemm(BF16, BF16, T, d, d, P(self.att[l]), d, 1, W(p + "w_o"), d, 1, P(self.tmp), d, tag="o")
-            add_rows(P(self.xm[l]), T, d, P(self.x[l]), P(self.tmp), W(p + "b_o"), tag="residual")
-            layernorm(P(self.xm[l]), p + "ln2_g", p + "ln2_b", P(self.h2[l]))
+            add_layernorm(P(self.x[l]), P(self.tmp), W(p + "b_o"), p + "ln2", P(self.xm[l]), P(self.h2[l]))
             gemm(BF16, BF16, T, F, d, P(self.h2[l]), d, 1, W(p + "w_fc"), F, 1, P(self.f[l]), F, tag="fc")
-            add_rows(P(self.f[l]), T, F, P(self.f[l]), bias=W(p + "b_fc"), tag="bias")
-            calls.append(_Call(lib.mk_gelu_tanh, [st, _I(BF16), _I64(T * F), P(self.f[l]), P(self.g[l])],
-                               "mk_gelu_tanh"))
+            calls.append(_Call(lib.mk_bias_gelu, [st, _I64(T), _I64(F), P(self.f[l]), W(p + "b_fc"), P(self.f[l]),
+                                                  P(self.g[l])], "mk_bias_gelu"))
             gemm(BF16, BF16, T, d, F, P(self.g[l]), F, 1, W(p + "w_pr"), d, 1, P(self.tmp), d, tag="proj")
-            add_rows(P(self.x[l + 1]), T, d, P(self.xm[l]), P(self.tmp), W(p + "b_pr"), tag="residual")
-        layernorm(P(self.x[L]), "lnf_g", "lnf_b", P(self.hf))
+            nxt, y = (f"h{l + 1}.ln1", P(self.h1[l + 1])) if l + 1 < L else ("lnf", P(self.hf))
+            add_layernorm(P(self.xm[l]), P(self.tmp), W(p + "b_pr"), nxt, P(self.x[l + 1]), y)
         # logits = hf @ wteᵀ, then loss rows and dlogits (over the logits)
         gemm(BF16, BF16, T, V, d, P(self.hf), d, 1, W("wte"), 1, d, P(self.logits), V, tag="logits")
         calls.append(_Call(lib.mk_softmax_xent, [st, _I(BF16), _I64(T), _I64(V), P(self.logits), _I(S32),

@@ -337,6 +337,29 @@ def add_rows(a, b=None, bias=None, out=None, stream=None):
     return out
 
 
+def add_layernorm(a, b, bias, gamma, beta, eps=1e-5, sum_out=None, y=None, stream=None):
+    """(a + b + bias, LayerNorm of that sum) for bf16 [rows, cols] a, b."""
+    _require_cuda(a)
+    rows, cols = a.shape
+    sum_out = torch.empty_like(a) if sum_out is None else sum_out
+    y = torch.empty_like(a) if y is None else y
+    rc = lib().mk_add_layernorm(_stream(stream), rows, cols, _ptr(a), _ptr(b), _ptr(bias), _ptr(gamma), _ptr(beta),
+                                float(eps), _ptr(sum_out), _ptr(y))
+    _check(rc, "mk_add_layernorm")
+    return sum_out, y
+
+
+def bias_gelu(x, bias, pre_out=None, y=None, stream=None):
+    """(x + bias, gelu_tanh of that sum) for bf16 [rows, cols] x."""
+    _require_cuda(x, bias)
+    rows, cols = x.shape
+    pre_out = torch.empty_like(x) if pre_out is None else pre_out
+    y = torch.empty_like(x) if y is None else y
+    rc = lib().mk_bias_gelu(_stream(stream), rows, cols, _ptr(x), _ptr(bias), _ptr(pre_out), _ptr(y))
+    _check(rc, "mk_bias_gelu")
+    return pre_out, y
+
+
 def gelu_tanh_bwd(x, dy, out=None, stream=None):
     """dx = dy * gelu_tanh'(x) (same dtype as x; out may be dy)."""
     _require_cuda(x, dy)

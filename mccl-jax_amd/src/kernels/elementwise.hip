@@ -18,13 +18,6 @@ constexpr int kUnroll = 4;
 // Using 1 + tanh(u) = 2 / (1 + exp(-2u)) gives gelu = x / (1 + exp(-2u)),
 // which has no cancellation for negative x and needs one exp2 + one rcp.
 // exp(-2u) = exp2(x * (c0 + c1 x^2)) with c0 = -2 sqrt(2/pi) log2(e).
-__device__ inline float gelu_tanh_f32(float x) {
-  constexpr float kC0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
-  constexpr float kC1 = kC0 * 0.044715f;
-  const float t = x * fmaf(x * x, kC1, kC0);
-  const float e = exp2f(t);
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
-}
 
 template <typename T> struct V16;
 template <> struct V16<uint16_t> { using V = u16x8; static constexpr int N = 8; };

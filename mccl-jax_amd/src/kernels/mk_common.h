@@ -128,6 +128,18 @@ __device__ inline void store_from_f32(void* p, int64_t i, int t, float v) {
   }
 }
 
+// ---------------------------------------------------------------- GELU
+// gelu_tanh(x) = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3),
+// written as x / (1 + exp(-2u)) with exp2; shared by every kernel that
+// evaluates it, so fused and unfused paths give the same bits.
+__device__ inline float gelu_tanh_f32(float x) {
+  constexpr float kC0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  constexpr float kC1 = kC0 * 0.044715f;
+  const float t = x * fmaf(x * x, kC1, kC0);
+  const float e = exp2f(t);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // ---------------------------------------------------------------- wave64
 constexpr int kWave = 64;
 

@@ -681,6 +681,88 @@ __global__ __launch_bounds__(kBlock) void attn_dscores_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------- fused forward rows
+// sum = a + b + bias (fp32 adds, one bf16 rounding: the stored residual
+// stream, as mk_add_rows stores it) and y = LayerNorm(sum) over the rounded
+// values, two-pass mean / variance as mk_layernorm; one wave per row, four
+// bf16 per lane per step (8-byte vectors), KV steps per row.
+template <int KV>
+__global__ __launch_bounds__(kBlock) void add_layernorm_kernel(const uint2* __restrict__ a, const uint2* b,
+                                                             const uint2* __restrict__ bias,
+                                                             const uint2* __restrict__ gamma,
+                                                             const uint2* __restrict__ beta, int64_t rows, int cols4,
+                                                             float eps, uint2* sum_out, uint2* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;  // whole waves
+  const float inv_n = 1.f / float(cols4 * 4);
+  float v[KV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int c = k * 64 + lane;
+    if (c < cols4) {
+      const uint2 x = a[r * cols4 + c];
+      const uint2 y2 = b ? b[r * cols4 + c] : uint2{0u, 0u};
+      const uint2 z = bias ? bias[c] : uint2{0u, 0u};
+      const uint32_t w0 = pack_bf16(lo16(x.x) + lo16(y2.x) + lo16(z.x), hi16(x.x) + hi16(y2.x) + hi16(z.x));
+      const uint32_t w1 = pack_bf16(lo16(x.y) + lo16(y2.y) + lo16(z.y), hi16(x.y) + hi16(y2.y) + hi16(z.y));
+      sum_out[r * cols4 + c] = uint2{w0, w1};
+      v[k][0] = lo16(w0);
+      v[k][1] = hi16(w0);
+      v[k][2] = lo16(w1);
+      v[k][3] = hi16(w1);
+    } else {
+      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0.f;
+    }
+    s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+  }
+  const float mean = wave_sum_dpp(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+    if (k * 64 + lane < cols4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d = v[k][j] - mean;
+        q += d * d;
+      }
+  const float rstd = 1.f / sqrtf(wave_sum_dpp(q) * inv_n + eps);
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int c = k * 64 + lane;
+    if (c < cols4) {
+      const uint2 g = gamma ? gamma[c] : uint2{0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+      const uint2 be = beta ? beta[c] : uint2{0u, 0u};
+      const float o0 = (v[k][0] - mean) * rstd * lo16(g.x) + lo16(be.x);
+      const float o1 = (v[k][1] - mean) * rstd * hi16(g.x) + hi16(be.x);
+      const float o2 = (v[k][2] - mean) * rstd * lo16(g.y) + lo16(be.y);
+      const float o3 = (v[k][3] - mean) * rstd * hi16(g.y) + hi16(be.y);
+      y[r * cols4 + c] = uint2{pack_bf16(o0, o1), pack_bf16(o2, o3)};
+    }
+  }
+}
+
+// pre = x + bias (one bf16 rounding, stored: the activation's input that the
+// backward needs) and y = gelu_tanh(pre) from the rounded value; 8 bf16 per
+// thread per trip.  pre may alias x.
+__global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const u32x4_t* x, const u32x4_t* __restrict__ bias,
+                                                         int64_t nvec, int64_t cvec, u32x4_t* pre,
+                                                         u32x4_t* __restrict__ y) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
+    const u32x4_t a = x[i], b = bias[i % cvec];
+    u32x4_t p, o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[j] = pack_bf16(lo16(a[j]) + lo16(b[j]), hi16(a[j]) + hi16(b[j]));
+      o[j] = pack_bf16(gelu_tanh_f32(lo16(p[j])), gelu_tanh_f32(hi16(p[j])));
+    }
+    pre[i] = p;
+    y[i] = o;
+  }
+}
+
 // ---------------------------------------------------------------- row adds
 // out[r, c] = a[r, c] (+ b[r, c]) (+ bias[c]), fp32 math, one rounding.
 template <typename T>
@@ -1108,4 +1190,54 @@ extern "C" int mk_add_rows(void* stream, int io_type, int64_t rows, int64_t cols
     return fail(MK_ERR_UNSUPPORTED, "mk_add_rows: io_type must be bf16/f32");
   }
   return check_launch("mk_add_rows");
+}
+
+extern "C" int mk_add_layernorm(void* stream, int64_t rows, int64_t cols, const void* a, const void* b,
+                                const void* bias, const void* gamma, const void* beta, float eps, void* sum_out,
+                                void* y) {
+  clear_error();
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_add_layernorm: bad shape");
+  if (rows == 0) return MK_OK;
+  if (!a || !sum_out || !y) return fail(MK_ERR_INVALID, "mk_add_layernorm: null pointer");
+  if (cols % 4 != 0 || cols > 2048)
+    return fail(MK_ERR_UNSUPPORTED, "mk_add_layernorm: cols must be a multiple of 4, at most 2048");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(gamma) |
+                       reinterpret_cast<uintptr_t>(beta) | reinterpret_cast<uintptr_t>(sum_out) |
+                       reinterpret_cast<uintptr_t>(y);
+  if (al & 7) return fail(MK_ERR_UNSUPPORTED, "mk_add_layernorm: 8-byte aligned operands");
+  hipStream_t s = as_stream(stream);
+  const int cols4 = int(cols / 4), kv = (cols4 + 63) / 64;
+  const dim3 g(unsigned((rows + 3) / 4));
+  auto go = [&](auto kvt) {
+    constexpr int KV = decltype(kvt)::value;
+    hipLaunchKernelGGL((add_layernorm_kernel<KV>), g, dim3(kBlock), 0, s, (const uint2*)a, (const uint2*)b,
+                       (const uint2*)bias, (const uint2*)gamma, (const uint2*)beta, rows, cols4, eps,
+                       (uint2*)sum_out, (uint2*)y);
+  };
+  if (kv == 1) go(IntC<1>{});
+  else if (kv == 2) go(IntC<2>{});
+  else if (kv == 3) go(IntC<3>{});
+  else if (kv == 4) go(IntC<4>{});
+  else go(IntC<8>{});
+  return check_launch("mk_add_layernorm");
+}
+
+extern "C" int mk_bias_gelu(void* stream, int64_t rows, int64_t cols, const void* x, const void* bias,
+                            void* pre_out, void* y) {
+  clear_error();
+  if (rows < 0 || cols < 0) return fail(MK_ERR_INVALID, "mk_bias_gelu: negative shape");
+  if (rows == 0 || cols == 0) return MK_OK;
+  if (!x || !bias || !pre_out || !y) return fail(MK_ERR_INVALID, "mk_bias_gelu: null pointer");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(bias) |
+                       reinterpret_cast<uintptr_t>(pre_out) | reinterpret_cast<uintptr_t>(y);
+  hipStream_t s = as_stream(stream);
+  if (cols % 8 != 0 || (al & 15) != 0) {  // two passes: the bias add, then GELU of the stored sum
+    if (int rc = mk_add_rows(stream, MK_BF16, rows, cols, x, nullptr, bias, pre_out)) return rc;
+    return mk_gelu_tanh(stream, MK_BF16, rows * cols, pre_out, y);
+  }
+  const int64_t nvec = rows * cols / 8;
+  hipLaunchKernelGGL(bias_gelu_kernel, dim3(grid_for(nvec)), dim3(kBlock), 0, s, (const u32x4_t*)x,
+                     (const u32x4_t*)bias, nvec, cols / 8, (u32x4_t*)pre_out, (u32x4_t*)y);
+  return check_launch("mk_bias_gelu");
 }

@@ -131,6 +131,44 @@ def test_add_rows(K, dtype, rows, cols):
     np.testing.assert_array_equal(_f64(a2), _f64(got))
 
 
+# ------------------------------------------------------------------ fused forward rows
+@pytest.mark.parametrize("rows,cols", [(8192, 768), (37, 100), (5, 2048), (3, 260)])
+def test_add_layernorm(K, rows, cols):
+    """The stored sum equals mk_add_rows bit for bit; the LayerNorm of it is
+    within bf16 rounding of the float64 LayerNorm of the rounded sum (and of
+    mk_layernorm on that sum)."""
+    g = torch.Generator().manual_seed(rows + cols)
+    a, b = ((torch.randn(rows, cols, generator=g) * 2).bfloat16().cuda() for _ in range(2))
+    bias = (0.1 * torch.randn(cols, generator=g)).bfloat16().cuda()
+    gamma = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16().cuda()
+    beta = (0.1 * torch.randn(cols, generator=g)).bfloat16().cuda()
+    s, y = K.add_layernorm(a, b, bias, gamma, beta, 1e-5)
+    assert torch.equal(s, K.add_rows(a, b, bias))
+    want = torch.nn.functional.layer_norm(_f64(s), (cols,), _f64(gamma), _f64(beta), 1e-5)
+    np.testing.assert_allclose(_f64(y), want, rtol=2 ** -7, atol=2 ** -8)
+    y2 = K.layernorm(s, gamma, beta, 1e-5)
+    assert float((_f64(y) - _f64(y2)).abs().max()) <= 2 ** -7 * float(_f64(y2).abs().max())
+    # no second operand, no bias
+    s1, y1 = K.add_layernorm(a, None, None, gamma, beta, 1e-5)
+    assert torch.equal(s1, a)
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 3072), (33, 100)])
+def test_bias_gelu(K, rows, cols):
+    """pre equals mk_add_rows and y equals mk_gelu_tanh of pre, bit for bit
+    (the second shape takes the two-pass path); in place over x."""
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).bfloat16().cuda()
+    bias = (0.5 * torch.randn(cols, generator=g)).bfloat16().cuda()
+    pre, y = K.bias_gelu(x, bias)
+    want_pre = K.add_rows(x, None, bias)
+    assert torch.equal(pre, want_pre)
+    assert torch.equal(y, K.gelu_tanh(want_pre))
+    x2 = x.clone()
+    K.bias_gelu(x2, bias, pre_out=x2)
+    assert torch.equal(x2, pre)
+
+
 # ------------------------------------------------------------------ column sums
 @pytest.mark.parametrize("rows,cols", [(1, 1), (19, 768), (8192, 768), (8, 786432), (1000, 257)])
 def test_col_sum(K, rows, cols):
