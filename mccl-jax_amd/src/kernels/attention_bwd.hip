@@ -70,9 +70,10 @@ struct BwdArgs {
 };
 
 // ---------------------------------------------------------------- stats
+template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdArgs p, const uint16_t* __restrict__ o,
                                                             int64_t o_bs, int64_t o_hs, int64_t o_ss,
-                                                            const float* __restrict__ lse, int D,
+                                                            const float* __restrict__ lse,
                                                             float* __restrict__ stats) {
   const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t per = int64_t(p.n_qt) * kTile;
@@ -84,9 +85,15 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdArgs p, co
     const int64_t b = bh / p.H, h = bh % p.H;
     const uint16_t* orow = o + b * o_bs + h * o_hs + row * o_ss;
     const uint16_t* drow = p.dout + b * p.do_bs + h * p.do_hs + row * p.do_ss;
-    for (int d = 0; d < D; d += 8) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(orow + d);
-      const u32x4_t c = *reinterpret_cast<const u32x4_t*>(drow + d);
+    u32x4_t av[D / 8], cv[D / 8];  // all of the row's loads in flight before any use
+#pragma unroll
+    for (int k = 0; k < D / 8; ++k) {
+      av[k] = *reinterpret_cast<const u32x4_t*>(orow + 8 * k);
+      cv[k] = *reinterpret_cast<const u32x4_t*>(drow + 8 * k);
+    }
+#pragma unroll
+    for (int k = 0; k < D / 8; ++k) {
+      const u32x4_t a = av[k], c = cv[k];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         dsum += __builtin_bit_cast(float, a[j] << 16) * __builtin_bit_cast(float, c[j] << 16);
@@ -508,8 +515,12 @@ int sdpa_bwd_flash(hipStream_t s, int64_t B, int64_t H, int64_t Sq, int64_t Sk, 
   a.scale = scale;
 
   const int64_t nstat = int64_t(a.BH) * a.n_qt * kTile;
-  hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3(unsigned((nstat + 255) / 256)), dim3(256), 0, s, a,
-                     (const uint16_t*)o, o_bs, o_hs, o_ss, lse, int(D), static_cast<float*>(workspace));
+  if (D == 128)
+    hipLaunchKernelGGL(attn_bwd_stats_kernel<128>, dim3(unsigned((nstat + 255) / 256)), dim3(256), 0, s, a,
+                       (const uint16_t*)o, o_bs, o_hs, o_ss, lse, static_cast<float*>(workspace));
+  else
+    hipLaunchKernelGGL(attn_bwd_stats_kernel<64>, dim3(unsigned((nstat + 255) / 256)), dim3(256), 0, s, a,
+                       (const uint16_t*)o, o_bs, o_hs, o_ss, lse, static_cast<float*>(workspace));
   if (int rc = check_launch("mk_sdpa_bwd")) return rc;
 
   const int n_kb = int((Sk + kBlkRows - 1) / kBlkRows), n_qb = int((Sq + kBlkRows - 1) / kBlkRows);

@@ -74,6 +74,7 @@ __global__ __launch_bounds__(kBlock) void gelu_bwd_bf16x8_kernel(const u32x4_t* 
 // Row data moves as 16-byte vectors: NV elements of T, widened to fp32.
 template <typename T> struct RowVec;
 template <> struct RowVec<uint16_t> {
+  using Raw = u32x4_t;
   static constexpr int NV = 8;
   __device__ static void unpack(const u32x4_t& v, float (&f)[NV]) {
 #pragma unroll
@@ -90,6 +91,7 @@ template <> struct RowVec<uint16_t> {
   }
 };
 template <> struct RowVec<float> {
+  using Raw = u32x4_t;
   static constexpr int NV = 4;
   __device__ static void unpack(const u32x4_t& v, float (&f)[NV]) {
 #pragma unroll
@@ -104,6 +106,20 @@ template <> struct RowVec<float> {
     for (int j = 0; j < 4; ++j) v[j] = __builtin_bit_cast(uint32_t, f[j]);
     return v;
   }
+};
+
+// bf16 rows as 8-byte vectors (4 values per lane per step): a 768-column
+// row is exactly three steps of 64 lanes.
+struct Bf16x4 {
+  using Raw = uint2;
+  static constexpr int NV = 4;
+  __device__ static void unpack(const uint2& v, float (&f)[NV]) {
+    f[0] = lo16(v.x);
+    f[1] = hi16(v.x);
+    f[2] = lo16(v.y);
+    f[3] = hi16(v.y);
+  }
+  __device__ static uint2 pack(const float (&f)[NV]) { return uint2{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3])}; }
 };
 
 // Pass 1, column partials over 16-byte vectors.  Block (bx, by) covers rows
@@ -294,9 +310,9 @@ struct LnBwdArgs {
 
 constexpr int kLnBwdMaxCols = 2048;
 
-template <typename T, int KV, bool VEC>
+template <typename T, typename RV, int KV, bool VEC>
 __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a) {
-  using RV = RowVec<T>;
+  using Raw = typename RV::Raw;
   constexpr int NV = RV::NV;
   __shared__ float red[kLnBwdMaxCols];
   const T* __restrict__ x = static_cast<const T*>(a.x);
@@ -317,16 +333,16 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
       accg[k][j] = accb[k][j] = accs[k][j] = 0.f;
     }
   const int64_t r0 = int64_t(blockIdx.x) * a.rpb, r1 = min(a.rows, r0 + a.rpb);
-  u32x4_t xr[KV], dr[KV], rr[KV];
+  Raw xr[KV], dr[KV], rr[KV];
   auto fetch = [&](int64_t r) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
       const int c0 = (k * 64 + lane) * NV;
-      xr[k] = dr[k] = rr[k] = u32x4_t{0u, 0u, 0u, 0u};
+      xr[k] = dr[k] = rr[k] = Raw{};
       if (r < r1 && c0 < cols) {
-        xr[k] = *reinterpret_cast<const u32x4_t*>(x + r * cols + c0);
-        dr[k] = *reinterpret_cast<const u32x4_t*>(dy + r * cols + c0);
-        if (dres) rr[k] = *reinterpret_cast<const u32x4_t*>(dres + r * cols + c0);
+        xr[k] = *reinterpret_cast<const Raw*>(x + r * cols + c0);
+        dr[k] = *reinterpret_cast<const Raw*>(dy + r * cols + c0);
+        if (dres) rr[k] = *reinterpret_cast<const Raw*>(dres + r * cols + c0);
       }
     }
   };
@@ -395,7 +411,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
       }
       const int c0 = (k * 64 + lane) * NV;
       if constexpr (VEC) {
-        if (c0 < cols) *reinterpret_cast<u32x4_t*>(dx + r * cols + c0) = RV::pack(o);
+        if (c0 < cols) *reinterpret_cast<Raw*>(dx + r * cols + c0) = RV::pack(o);
       } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j)
@@ -950,9 +966,25 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     using T = decltype(tag);
     constexpr int KV = decltype(kvt)::value;
     constexpr bool VEC = decltype(vect)::value;
-    hipLaunchKernelGGL((layernorm_bwd_kernel<T, KV, VEC>), dim3(unsigned(nb)), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, RowVec<T>, KV, VEC>), dim3(unsigned(nb)), dim3(kBlock), 0, s, a);
   };
-  auto dispatch = [&](auto tag) {
+  // bf16 rows of at most 1024 columns in 8-byte vectors: fewer registers per
+  // lane (more rows in flight) and no idle lanes at 768 columns
+  const uintptr_t al8 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
+                        reinterpret_cast<uintptr_t>(dres) | reinterpret_cast<uintptr_t>(dx);
+  if (io_type == MK_BF16 && cols % 4 == 0 && cols <= 1024 && (al8 & 7) == 0) {
+    const int64_t kv = (cols + 255) / 256;
+    auto go = [&](auto kvt) {
+      constexpr int KV = decltype(kvt)::value;
+      hipLaunchKernelGGL((layernorm_bwd_kernel<uint16_t, Bf16x4, KV, true>), dim3(unsigned(nb)), dim3(kBlock), 0, s,
+                         a);
+    };
+    if (kv == 1) go(IntC<1>{});
+    else if (kv == 2) go(IntC<2>{});
+    else if (kv == 3) go(IntC<3>{});
+    else go(IntC<4>{});
+  } else {
+    auto dispatch = [&](auto tag) {
     using T = decltype(tag);
     constexpr int NV = RowVec<T>::NV;
     const int64_t kv = (cols + 64 * NV - 1) / (64 * NV);
@@ -964,9 +996,10 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     };
     if (rows_are_vectors<T>(cols, {x, dy, dres, dx})) with_kv(std::true_type{});
     else with_kv(std::false_type{});
-  };
-  if (io_type == MK_BF16) dispatch(uint16_t{});
-  else dispatch(float{});
+    };
+    if (io_type == MK_BF16) dispatch(uint16_t{});
+    else dispatch(float{});
+  }
   if (int rc = check_launch("mk_layernorm_bwd")) return rc;
   const float* parts[3];
   float* outs[3];
