@@ -55,10 +55,7 @@ namespace {
 
 using namespace attn;
 
-constexpr int kBM = 256;    // query rows per workgroup
 constexpr int kBN = 64;     // keys per tile
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
 
 struct SdpaArgs {
@@ -77,14 +74,18 @@ struct SdpaArgs {
   float scale_log2;  // scale * log2(e)
 };
 
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p) {
+// NW waves per workgroup (8: 256 query rows, one workgroup per CU; 4: 128
+// rows, two workgroups per CU, for short sequences), in two groups of GW.
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArgs p) {
+  constexpr int GW = NW / 2;       // waves per group
+  constexpr int kBM = 32 * NW;     // query rows per workgroup
   constexpr int CH = D / 8;      // 16-byte chunks of a row
   constexpr int UK = CH + 1;     // K row stride in LDS, 16-byte units
   constexpr int UV = CH + 4;     // V row stride in LDS, 16-byte units
   constexpr int KS = UK * 8, VS = UV * 8;  // the same in elements
   constexpr int NK = UK, NV = UV;          // 1 KB copies per tile (64 rows x U units / 64 lanes)
-  constexpr int NKW = (NK + 3) / 4, NVW = (NV + 3) / 4;  // per wave: 4 waves of one group issue a tile
+  constexpr int NKW = (NK + GW - 1) / GW, NVW = (NV + GW - 1) / GW;  // per wave: the GW waves of one group issue a tile
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
 
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2;  // 0: group A, 1: group B (one phase later)
+  const int grp = wave / GW;  // 0: group A, 1: group B (one phase later)
   const int c = lane & 31, g = lane >> 5;
   const int q0 = qt * kBM + wave * 32;  // first query row of this wave
   const int qrow = q0 + c;               // the query this lane's columns belong to
@@ -142,28 +143,33 @@ __global__ __launch_bounds__(kThreads, 1) void sdpa_fwd_kernel(const SdpaArgs p)
   // ---- staging: global -> LDS.  Copy j (1 KB) of a tile is issued by wave
   // j % 4 of the issuing group and covers LDS units 64 j + lane; unit u
   // holds row u / U, chunk u % U.
-  int koff[NKW], voff[NVW];  // the lane's byte offsets within a tile (2^31: padding)
+  // the lane's byte offset within a tile for copy i (2^31: padding).  With
+  // 8 waves they are kept in registers; the 4-wave variant issues twice as
+  // many copies per wave and recomputes them at each copy instead (a few
+  // integer ops), which keeps it within 256 VGPRs.
+  auto lane_off = [&](int i, int U, int64_t ss) __attribute__((always_inline)) {
+    const int u = 64 * (GW * i + (wave % GW)) + lane, row = u / U, ch = u % U;
+    return (ch < CH && row < kBN) ? (row * int(ss) + ch * 8) * 2 : int(0x80000000u);
+  };
+  constexpr bool kKeepOff = NW == 8;
+  int koff[kKeepOff ? NKW : 1], voff[kKeepOff ? NVW : 1];
+  if constexpr (kKeepOff) {
 #pragma unroll
-  for (int i = 0; i < NKW; ++i) {
-    const int u = 64 * (4 * i + (wave & 3)) + lane, row = u / UK, ch = u % UK;
-    koff[i] = (ch < CH && row < kBN) ? (row * int(p.k_ss) + ch * 8) * 2 : int(0x80000000u);
-  }
+    for (int i = 0; i < NKW; ++i) koff[i] = lane_off(i, UK, p.k_ss);
 #pragma unroll
-  for (int i = 0; i < NVW; ++i) {
-    const int u = 64 * (4 * i + (wave & 3)) + lane, row = u / UV, ch = u % UV;
-    voff[i] = (ch < CH && row < kBN) ? (row * int(p.v_ss) + ch * 8) * 2 : int(0x80000000u);
+    for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, UV, p.v_ss);
   }
-  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
+  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int U, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
     const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
     const i32x4_t r = tile_desc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
 #pragma unroll
     for (int i = 0; i < nw; ++i)
-      if (4 * i + (wave & 3) < n)  // wave-uniform
-        copy_to_lds(r, lds_addr(dst + (4 * i + (wave & 3)) * 512), off[i]);
+      if (GW * i + (wave % GW) < n)  // wave-uniform
+        copy_to_lds(r, lds_addr(dst + (GW * i + (wave % GW)) * 512), kKeepOff ? off[i] : lane_off(i, U, ss));
   };
-  auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, NK, NKW, kbuf(buf), tile); };
-  auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, NV, NVW, vbuf(buf), tile); };
+  auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, UK, NK, NKW, kbuf(buf), tile); };
+  auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, UV, NV, NVW, vbuf(buf), tile); };
 
   // lane's element offset in a V tile for the transposed reads: key 4g + r/4,
   // d 16*hi + 4*(r%4) (r = lane % 16, hi = lane / 16 % 2)
@@ -427,19 +433,28 @@ extern "C" int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
   a.v_bs = v_bs; a.v_hs = v_hs; a.v_ss = v_ss;
   a.o_bs = o_bs; a.o_hs = o_hs; a.o_ss = o_ss;
   a.H = int(H); a.Sq = int(Sq); a.Sk = int(Sk);
-  a.n_qtiles = int((Sq + kBM - 1) / kBM);
   a.BH = int(B * H);
   a.scale_log2 = scale * 1.4426950408889634f;
+  // 8 waves (256 query rows per workgroup) unless that grid would leave
+  // the GPU short of workgroups: then 4 waves (128 rows, two per CU)
+  const int64_t blocks8 = ((Sq + 255) / 256) * a.BH;
+  const int nw = blocks8 < 2 * 256 ? 4 : 8;  // 256 CUs
+  a.n_qtiles = int((Sq + 32 * nw - 1) / (32 * nw));
   const int64_t blocks = int64_t(a.n_qtiles) * a.BH;
   if (blocks >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_fwd: grid too large");
   hipStream_t s = as_stream(stream);
-  const dim3 g{unsigned(blocks)}, bl{unsigned(kThreads)};
-  if (D == 128) {
-    if (causal) hipLaunchKernelGGL((sdpa_fwd_kernel<128, true>), g, bl, 0, s, a);
-    else hipLaunchKernelGGL((sdpa_fwd_kernel<128, false>), g, bl, 0, s, a);
-  } else {
-    if (causal) hipLaunchKernelGGL((sdpa_fwd_kernel<64, true>), g, bl, 0, s, a);
-    else hipLaunchKernelGGL((sdpa_fwd_kernel<64, false>), g, bl, 0, s, a);
-  }
+  const dim3 g{unsigned(blocks)}, bl{unsigned(64 * nw)};
+  auto go = [&](auto nwt) {
+    constexpr int NW = decltype(nwt)::value;
+    if (D == 128) {
+      if (causal) hipLaunchKernelGGL((sdpa_fwd_kernel<128, true, NW>), g, bl, 0, s, a);
+      else hipLaunchKernelGGL((sdpa_fwd_kernel<128, false, NW>), g, bl, 0, s, a);
+    } else {
+      if (causal) hipLaunchKernelGGL((sdpa_fwd_kernel<64, true, NW>), g, bl, 0, s, a);
+      else hipLaunchKernelGGL((sdpa_fwd_kernel<64, false, NW>), g, bl, 0, s, a);
+    }
+  };
+  if (nw == 4) go(Int<4>{});
+  else go(Int<8>{});
   return check_launch("mk_sdpa_fwd");
 }
