@@ -89,6 +89,9 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
   int err = MK_OK;
   rocblas_handle h = handle_for_current_device(&err);
   if (!h) return err;
+  // a device's handle is shared: binding the stream and queueing the GEMM
+  // happen under one lock, so concurrent callers cannot swap streams between
+  std::lock_guard<std::mutex> lk(g_blas_mu);
   if (rocblas_set_stream(h, stream) != rocblas_status_success)
     return fail(MK_ERR_LAUNCH, "mk_gemm_blas: rocblas_set_stream failed");
   const rocblas_status st = rocblas_gemm_strided_batched_ex(

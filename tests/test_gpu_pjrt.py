@@ -254,3 +254,46 @@ def test_donation_reuses_input_memory(client):
     np.testing.assert_allclose(vr, v1, rtol=2e-7, atol=1e-12)
     np.testing.assert_allclose(pr, p1, rtol=1e-6, atol=1e-9)
     e.destroy()
+
+
+def test_concurrent_execute_from_threads(client):
+    """Several Python threads run one compiled executable at once (ctypes
+    releases the GIL, so the plugin sees concurrent PJRT_LoadedExecutable_Execute
+    and buffer transfers): every thread gets its own inputs' result, equal
+    to a single-threaded run of the same inputs."""
+    import threading
+
+    e = client.compile(modules.sdpa(1, 2, 256, 128, causal=True))
+    rng = np.random.default_rng(11)
+    cases = [[bf16.to_bf16_bits((rng.standard_normal((1, 2, 256, 128)) / math.sqrt(128)).astype(np.float32))
+              for _ in range(3)] for _ in range(4)]
+
+    def run_once(qkv):
+        bufs = [client.put(a, pjrt.BF16) for a in qkv]
+        (o,) = e.execute(bufs)
+        res = o.to_numpy()
+        for b in bufs + [o]:
+            b.destroy()
+        return res
+
+    want = [run_once(c) for c in cases]
+    errors, got = [], [[None] * 5 for _ in cases]
+
+    def worker(t):
+        try:
+            for it in range(5):
+                got[t][it] = run_once(cases[t])
+        except Exception as ex:  # noqa: BLE001 - reported below
+            errors.append(repr(ex))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(len(cases))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads), "a worker did not finish"
+    assert not errors, errors
+    for t in range(len(cases)):
+        for it in range(5):
+            np.testing.assert_array_equal(got[t][it], want[t])
+    e.destroy()
