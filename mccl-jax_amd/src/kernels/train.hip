@@ -607,7 +607,8 @@ __global__ __launch_bounds__(kBlock) void adam_vec4_kernel(int64_t nvec, f32x4* 
   }
   const int64_t stride = int64_t(gridDim.x) * kBlock;
   for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
-    const f32x4 g = grad[i], m0 = m[i], v0 = v[i], p0 = p32[i];
+    // every array is touched once per step: streaming loads and stores
+    const f32x4 g = ld_stream(&grad[i]), m0 = ld_stream(&m[i]), v0 = ld_stream(&v[i]), p0 = ld_stream(&p32[i]);
     f32x4 m1, v1, p1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -615,9 +616,9 @@ __global__ __launch_bounds__(kBlock) void adam_vec4_kernel(int64_t nvec, f32x4* 
       v1.v[j] = b2 * v0.v[j] + omb2 * g.v[j] * g.v[j];
       p1.v[j] = p0.v[j] - lr * (m1.v[j] / bc1) / (sqrtf(v1.v[j] / bc2) + eps);
     }
-    m[i] = m1;
-    v[i] = v1;
-    p32[i] = p1;
+    st_stream(&m[i], m1);
+    st_stream(&v[i], v1);
+    st_stream(&p32[i], p1);
     if (p16) p16[i] = uint2{pack_bf16(p1.v[0], p1.v[1]), pack_bf16(p1.v[2], p1.v[3])};
   }
 }
