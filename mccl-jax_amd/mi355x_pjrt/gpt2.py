@@ -213,9 +213,9 @@ class GPT2TrainStep:
         self.loss_rows = torch.empty(T, dtype=torch.float32, device=dev)
         self.loss_sum = torch.empty(1, dtype=torch.float32, device=dev)
         lib = self.lib
-        sk = [lib.mk_gemm_blas_splitk_workspace_bytes(d, n, self.DW_SPLITS[t])
+        sk = [lib.mk_gemm_blas_splitk_workspace_bytes(d, n, self.DW_SPLITS.get(t, 1))
               for t, n in (("dw_o", d), ("dw_qkv", 3 * d), ("dw_fc", c.d_ff))]
-        sk.append(lib.mk_gemm_blas_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS["dw_pr"]))
+        sk.append(lib.mk_gemm_blas_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS.get("dw_pr", 1)))
         ws = max(*sk, lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
                  lib.mk_layernorm_bwd_workspace_bytes(T, d),
                  lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),

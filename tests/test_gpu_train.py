@@ -81,6 +81,27 @@ def test_gemm_blas_layouts(K, ta, tb, out_dtype):
         np.testing.assert_allclose(_f64(got), ref, rtol=2 ** -8, atol=1e-5 * float((_f64(a).abs() @ _f64(b).abs()).max()))
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("M,N,Kd", [(77, 1001, 133), (1, 9, 5), (130, 3, 1031)])
+def test_gemm_blas_ragged(K, M, N, Kd, ta, tb, out_dtype):
+    """Sizes and row strides that are no multiple of the kernels' vector
+    widths (the vocabulary axis of the logits GEMMs is one), against float64."""
+    g = torch.Generator().manual_seed(M * 7 + N + Kd + 2 * int(ta) + int(tb))
+    a_st = torch.randn(Kd, M, generator=g) if ta else torch.randn(M, Kd, generator=g)
+    b_st = torch.randn(N, Kd, generator=g) if tb else torch.randn(Kd, N, generator=g)
+    a = (a_st.bfloat16().cuda().t() if ta else a_st.bfloat16().cuda())
+    b = (b_st.bfloat16().cuda().t() if tb else b_st.bfloat16().cuda())
+    got = K.gemm_blas(a, b, out_dtype=out_dtype)
+    ref = _f64(a) @ _f64(b)
+    scale = float((_f64(a).abs() @ _f64(b).abs()).max())
+    if out_dtype == torch.float32:
+        assert float((_f64(got) - ref).abs().max()) < 1e-5 * scale
+    else:
+        np.testing.assert_allclose(_f64(got), ref, rtol=2 ** -8, atol=1e-5 * scale)
+    assert torch.equal(got, K.gemm_blas(a, b, out_dtype=out_dtype))
+
+
 def test_gemm_blas_batched_alpha_beta_and_f32(K):
     g = torch.Generator().manual_seed(9)
     a = torch.randn(3, 40, 24, generator=g).cuda()
