@@ -9,7 +9,8 @@
 // Register layouts: those of the 32x32 MFMA (attn_common.h).
 // S is computed transposed, Sᵀ = K · Qᵀ, so every lane holds one query's
 // scores (column c) for 32 of the tile's keys: the row max / row sum are
-// in-lane reductions plus one exchange with lane l^32.  Those same
+// in-lane reductions plus one exchange with lane l^32 (v_permlane32_swap,
+// a VALU op: no LDS round trip on the softmax's critical path).  Those same
 // registers, converted to bf16, ARE the B operand of Oᵀ = Vᵀ · Pᵀ: the k-slot
 // (g, i) of P corresponds to key 16*j + 4*g + 8*(i/4) + i%4 of the 16-key
 // step j.  V stays row-major in LDS; the A operand (Vᵀ) is read with
@@ -257,7 +258,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb2][r]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    {
+      float lo, hi;
+      lane_halves(mt, lo, hi);
+      mt = fmaxf(lo, hi);
+    }
     const float m_cand = fmaxf(m_run, mt * p.scale_log2);
     // m_run == -inf until the row has seen an unmasked key, so the first
     // such tile always rescales (alpha = 0 on O = 0, l = 0)
@@ -372,7 +377,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   }
 
   // ---- epilogue: normalise and store O (lane owns query qrow, 4 consecutive d per reg group)
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  float l_lo, l_hi;
+  lane_halves(l_run, l_lo, l_hi);
+  const float l_tot = l_lo + l_hi;
   if (qrow < p.Sq) {
     const float inv = (l_tot > 0.f) ? 1.f / l_tot : __builtin_nanf("");
     uint16_t* ob = p.o + b * p.o_bs + h * p.o_hs + int64_t(qrow) * p.o_ss;

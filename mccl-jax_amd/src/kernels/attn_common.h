@@ -94,5 +94,18 @@ __device__ inline uint2 lds_read_tr(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
+// Values of lanes l and l ^ 32 in one VALU op, without the LDS path of
+// ds_bpermute: v_permlane32_swap on two copies of v leaves v[l % 32] in the
+// first result and v[l % 32 + 32] in the second, in every lane.  The empty
+// asm keeps the optimiser from treating the two operands as one value.
+__device__ inline void lane_halves(float v, float& lo, float& hi) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, v);
+  uint32_t b = a;
+  asm volatile("" : "+v"(b));
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  lo = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
+  hi = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 }  // namespace attn
 }  // namespace mk
