@@ -63,14 +63,18 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // compiler does not track it: it inserts no vmcnt wait of its own for these
 // copies, and the kernel waits for them explicitly (wait_copies) before the
 // barrier that hands the data to the other waves.  M0 holds the LDS address
-// (set by the compiler from the constraint); one wait state separates the M0
-// write from the copy.
+// (set by the compiler from the constraint).
 // The descriptor and the LDS address pass through readfirstlane here, at the
-// operand, so they are in SGPRs however the caller computed them.
+// operand, so they are in SGPRs however the caller computed them.  A VALU
+// write of an SGPR (v_readfirstlane) needs 5 wait states before a VMEM
+// instruction reads that SGPR, and the compiler's hazard pass does not look
+// inside inline assembly, so the copy is preceded by s_nop 4 (5 wait states;
+// this also covers the one the M0 write needs).  Without it a descriptor
+// word written just before the copy can be read stale.
 __device__ inline void copy_to_lds(const i32x4_t& rsrc, uint32_t dst, int voff) {
   const i32x4_t r = {__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
                      __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(r), "{m0}"(__builtin_amdgcn_readfirstlane(dst))
                : "memory");
