@@ -310,11 +310,15 @@ struct LnBwdArgs {
 
 constexpr int kLnBwdMaxCols = 2048;
 
-template <typename T, typename RV, int KV, bool VEC>
-__global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a) {
+// W waves per block; rows r0 + w, r0 + w + W, ... go to wave w, each wave
+// requesting its next row before it reduces the current one.  (Measured at
+// 8192 x 768: 4 waves per block is fastest; 6, 8 and 16 were 1.5-3x slower,
+// and keeping two rows of a wave in flight gained nothing.)
+template <typename T, typename RV, int KV, bool VEC, int W>
+__global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a) {
   using Raw = typename RV::Raw;
   constexpr int NV = RV::NV;
-  __shared__ float red[kLnBwdMaxCols];
+  __shared__ float red[3][kLnBwdMaxCols];
   const T* __restrict__ x = static_cast<const T*>(a.x);
   const T* __restrict__ gamma = static_cast<const T*>(a.gamma);
   const T* __restrict__ dy = static_cast<const T*>(a.dy);
@@ -346,30 +350,10 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
       }
     }
   };
-  int64_t r = r0 + wid;
-  if constexpr (VEC) fetch(r);
-  for (; r < r1; r += kRowLanes) {
-    float xv[KV][NV], dv[KV][NV], rv[KV][NV];
-    if constexpr (VEC) {
-#pragma unroll
-      for (int k = 0; k < KV; ++k) {
-        RV::unpack(xr[k], xv[k]);
-        RV::unpack(dr[k], dv[k]);
-        RV::unpack(rr[k], rv[k]);
-      }
-      fetch(r + kRowLanes);
-    } else {
-#pragma unroll
-      for (int k = 0; k < KV; ++k)
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          const int c = (k * 64 + lane) * NV + j;
-          const bool ok = c < cols;
-          xv[k][j] = ok ? ldf<T>(x, r * cols + c) : 0.f;
-          dv[k][j] = ok ? ldf<T>(dy, r * cols + c) : 0.f;
-          rv[k][j] = (ok && dres) ? ldf<T>(dres, r * cols + c) : 0.f;
-        }
-    }
+  // one row: statistics, dx = rstd (dy g - mean(dy g) - xhat mean(dy g xhat)) + dres,
+  // and the column partials
+  auto process = [&](int64_t r, float (&xv)[KV][NV], const float (&dv)[KV][NV],
+                     const float (&rv)[KV][NV]) __attribute__((always_inline)) {
     float sx = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k)
@@ -418,29 +402,81 @@ __global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(const LnBwdArgs a
           if (c0 + j < cols) stf<T>(dx, r * cols + c0 + j, o[j]);
       }
     }
-  }
-  // block partial rows, the four waves added in wave order
-  auto block_rows = [&](const float (&acc)[KV][NV], float* part) __attribute__((always_inline)) {
-    for (int w = 0; w < kRowLanes; ++w) {
-      if (wid == w) {
-#pragma unroll
-        for (int k = 0; k < KV; ++k)
-#pragma unroll
-          for (int j = 0; j < NV; ++j) {
-            const int c = (k * 64 + lane) * NV + j;
-            if (c < cols) red[c] = (w == 0) ? acc[k][j] : red[c] + acc[k][j];
-          }
-      }
-      __syncthreads();
-    }
-    for (int c = threadIdx.x; c < cols; c += kBlock) part[int64_t(blockIdx.x) * cols + c] = red[c];
-    __syncthreads();
   };
-  if (a.part_g) {
-    block_rows(accg, a.part_g);
-    block_rows(accb, a.part_b);
+  if constexpr (VEC) {
+    // the next row's loads are issued before the current row is reduced
+    int64_t r = r0 + wid;
+    fetch(r);
+    for (; r < r1; r += W) {
+      float xv[KV][NV], dv[KV][NV], rv[KV][NV];
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        RV::unpack(xr[k], xv[k]);
+        RV::unpack(dr[k], dv[k]);
+        RV::unpack(rr[k], rv[k]);
+      }
+      fetch(r + W);
+      process(r, xv, dv, rv);
+    }
+  } else {
+    for (int64_t r = r0 + wid; r < r1; r += W) {
+      float xv[KV][NV], dv[KV][NV], rv[KV][NV];
+#pragma unroll
+      for (int k = 0; k < KV; ++k)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const int c = (k * 64 + lane) * NV + j;
+          const bool ok = c < cols;
+          xv[k][j] = ok ? ldf<T>(x, r * cols + c) : 0.f;
+          dv[k][j] = ok ? ldf<T>(dy, r * cols + c) : 0.f;
+          rv[k][j] = (ok && dres) ? ldf<T>(dres, r * cols + c) : 0.f;
+        }
+      process(r, xv, dv, rv);
+    }
   }
-  if (a.part_s) block_rows(accs, a.part_s);
+  // block partial rows: the W waves added in wave order, the three sums in
+  // the same rounds.  In its round a wave reads every value it adds to
+  // before it writes any, so a round costs one LDS round trip rather than
+  // one per value.
+  const bool want_gb = a.part_g != nullptr, want_s = a.part_s != nullptr;
+  if (!want_gb && !want_s) return;
+  for (int w = 0; w < W; ++w) {
+    if (wid == w) {
+      float cur[3][KV][NV];
+#pragma unroll
+      for (int k = 0; k < KV; ++k)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const int c = (k * 64 + lane) * NV + j;
+          const bool ok = w > 0 && c < cols;
+          cur[0][k][j] = (ok && want_gb) ? red[0][c] : 0.f;
+          cur[1][k][j] = (ok && want_gb) ? red[1][c] : 0.f;
+          cur[2][k][j] = (ok && want_s) ? red[2][c] : 0.f;
+        }
+#pragma unroll
+      for (int k = 0; k < KV; ++k)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const int c = (k * 64 + lane) * NV + j;
+          if (c < cols) {
+            if (want_gb) {
+              red[0][c] = (w == 0) ? accg[k][j] : cur[0][k][j] + accg[k][j];
+              red[1][c] = (w == 0) ? accb[k][j] : cur[1][k][j] + accb[k][j];
+            }
+            if (want_s) red[2][c] = (w == 0) ? accs[k][j] : cur[2][k][j] + accs[k][j];
+          }
+        }
+    }
+    __syncthreads();
+  }
+  for (int c = threadIdx.x; c < cols; c += 64 * W) {
+    const int64_t o = int64_t(blockIdx.x) * cols + c;
+    if (want_gb) {
+      a.part_g[o] = red[0][c];
+      a.part_b[o] = red[1][c];
+    }
+    if (want_s) a.part_s[o] = red[2][c];
+  }
 }
 
 constexpr int64_t kLnBwdBlocks = 512;  // partial rows of the LayerNorm backward
@@ -967,7 +1003,7 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     using T = decltype(tag);
     constexpr int KV = decltype(kvt)::value;
     constexpr bool VEC = decltype(vect)::value;
-    hipLaunchKernelGGL((layernorm_bwd_kernel<T, RowVec<T>, KV, VEC>), dim3(unsigned(nb)), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL((layernorm_bwd_kernel<T, RowVec<T>, KV, VEC, kRowLanes>), dim3(unsigned(nb)), dim3(kBlock), 0, s, a);
   };
   // bf16 rows of at most 1024 columns in 8-byte vectors: fewer registers per
   // lane (more rows in flight) and no idle lanes at 768 columns
@@ -977,8 +1013,8 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     const int64_t kv = (cols + 255) / 256;
     auto go = [&](auto kvt) {
       constexpr int KV = decltype(kvt)::value;
-      hipLaunchKernelGGL((layernorm_bwd_kernel<uint16_t, Bf16x4, KV, true>), dim3(unsigned(nb)), dim3(kBlock), 0, s,
-                         a);
+      hipLaunchKernelGGL((layernorm_bwd_kernel<uint16_t, Bf16x4, KV, true, kRowLanes>), dim3(unsigned(nb)), dim3(kBlock),
+                         0, s, a);
     };
     if (kv == 1) go(IntC<1>{});
     else if (kv == 2) go(IntC<2>{});
