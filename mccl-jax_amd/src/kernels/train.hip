@@ -309,16 +309,21 @@ struct LnBwdArgs {
 };
 
 constexpr int kLnBwdMaxCols = 2048;
+constexpr int kLnBwdSliceCols = 1024;
 
 // W waves per block; rows r0 + w, r0 + w + W, ... go to wave w, each wave
-// requesting its next row before it reduces the current one.  (Measured at
-// 8192 x 768: 4 waves per block is fastest; 6, 8 and 16 were 1.5-3x slower,
-// and keeping two rows of a wave in flight gained nothing.)
-template <typename T, typename RV, int KV, bool VEC, int W>
+// requesting its next row before it reduces the current one.  The column
+// partials are merged after the rows, so their cost grows with W: 4 waves
+// per block was fastest at 8192 x 768.
+template <typename T, typename RV, int KV, bool VEC, int W, bool SLICES = false>
 __global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a) {
   using Raw = typename RV::Raw;
   constexpr int NV = RV::NV;
-  __shared__ float red[3][kLnBwdMaxCols];
+  // SLICES (rows of at most kLnBwdSliceCols columns): one LDS slice per wave;
+  // otherwise one shared slice merged in wave rounds.  Columns past the
+  // slice width are a sink for lanes past the row end.
+  constexpr int SC = SLICES ? kLnBwdSliceCols : kLnBwdMaxCols;
+  __shared__ __attribute__((aligned(16))) float red[SLICES ? W : 1][3][SC + 8];
   const T* __restrict__ x = static_cast<const T*>(a.x);
   const T* __restrict__ gamma = static_cast<const T*>(a.gamma);
   const T* __restrict__ dy = static_cast<const T*>(a.dy);
@@ -328,26 +333,48 @@ __global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const float inv_n = 1.f / float(cols);
   float gam[KV][NV], accg[KV][NV], accb[KV][NV], accs[KV][NV];
+  // gamma: clamped addresses rather than per-element guards, so the loads
+  // are issued together and waited for once (a guarded load per element is
+  // a memory round trip each, in series, before the first row)
+  if (gamma) {
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (k * 64 + lane) * NV + j;
+        gam[k][j] = ldf<T>(gamma, c < cols ? c : cols - 1);
+      }
+  } else {
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) gam[k][j] = 1.f;
+  }
 #pragma unroll
   for (int k = 0; k < KV; ++k)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int c = (k * 64 + lane) * NV + j;
-      gam[k][j] = (c < cols) ? (gamma ? ldf<T>(gamma, c) : 1.f) : 0.f;
+      if (c >= cols) gam[k][j] = 0.f;
       accg[k][j] = accb[k][j] = accs[k][j] = 0.f;
     }
   const int64_t r0 = int64_t(blockIdx.x) * a.rpb, r1 = min(a.rows, r0 + a.rpb);
+  // Row loads are unconditional: a row past the block's end reloads the
+  // block's last row, a column past the row end loads column 0, and without
+  // a residual x stands in for it; the values are discarded or zeroed after
+  // unpacking.  Guarded loads would sit in branches, and the compiler then
+  // waits for every load in flight (the next row's too) at the joins.
   Raw xr[KV], dr[KV], rr[KV];
+  const T* __restrict__ res_src = dres ? dres : x;
   auto fetch = [&](int64_t r) __attribute__((always_inline)) {
+    const int64_t rc = r < r1 ? r : r1 - 1;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
       const int c0 = (k * 64 + lane) * NV;
-      xr[k] = dr[k] = rr[k] = Raw{};
-      if (r < r1 && c0 < cols) {
-        xr[k] = *reinterpret_cast<const Raw*>(x + r * cols + c0);
-        dr[k] = *reinterpret_cast<const Raw*>(dy + r * cols + c0);
-        if (dres) rr[k] = *reinterpret_cast<const Raw*>(dres + r * cols + c0);
-      }
+      const int cs = c0 < cols ? c0 : 0;
+      xr[k] = *reinterpret_cast<const Raw*>(x + rc * cols + cs);
+      dr[k] = *reinterpret_cast<const Raw*>(dy + rc * cols + cs);
+      rr[k] = *reinterpret_cast<const Raw*>(res_src + rc * cols + cs);
     }
   };
   // one row: statistics, dx = rstd (dy g - mean(dy g) - xhat mean(dy g xhat)) + dres,
@@ -414,6 +441,13 @@ __global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a
         RV::unpack(xr[k], xv[k]);
         RV::unpack(dr[k], dv[k]);
         RV::unpack(rr[k], rv[k]);
+        const bool in_row = (k * 64 + lane) * NV < cols;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          xv[k][j] = in_row ? xv[k][j] : 0.f;
+          dv[k][j] = in_row ? dv[k][j] : 0.f;
+          rv[k][j] = (in_row && dres) ? rv[k][j] : 0.f;
+        }
       }
       fetch(r + W);
       process(r, xv, dv, rv);
@@ -435,47 +469,83 @@ __global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a
     }
   }
   // block partial rows: the W waves added in wave order, the three sums in
-  // the same rounds.  In its round a wave reads every value it adds to
-  // before it writes any, so a round costs one LDS round trip rather than
-  // one per value.
+  // the same rounds.  The rounds are branch-free (lanes past the row end use
+  // the sink column), so a wave issues all of its LDS reads of a round
+  // before its first add: per-element guards would put each read in its own
+  // branch and serialise the round trips (about 2 us per round at 768
+  // columns).
   const bool want_gb = a.part_g != nullptr, want_s = a.part_s != nullptr;
   if (!want_gb && !want_s) return;
-  for (int w = 0; w < W; ++w) {
-    if (wid == w) {
-      float cur[3][KV][NV];
+  int addr[KV][NV];
 #pragma unroll
-      for (int k = 0; k < KV; ++k)
+  for (int k = 0; k < KV; ++k)
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          const int c = (k * 64 + lane) * NV + j;
-          const bool ok = w > 0 && c < cols;
-          cur[0][k][j] = (ok && want_gb) ? red[0][c] : 0.f;
-          cur[1][k][j] = (ok && want_gb) ? red[1][c] : 0.f;
-          cur[2][k][j] = (ok && want_s) ? red[2][c] : 0.f;
-        }
-#pragma unroll
-      for (int k = 0; k < KV; ++k)
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-          const int c = (k * 64 + lane) * NV + j;
-          if (c < cols) {
-            if (want_gb) {
-              red[0][c] = (w == 0) ? accg[k][j] : cur[0][k][j] + accg[k][j];
-              red[1][c] = (w == 0) ? accb[k][j] : cur[1][k][j] + accb[k][j];
-            }
-            if (want_s) red[2][c] = (w == 0) ? accs[k][j] : cur[2][k][j] + accs[k][j];
-          }
-        }
+    for (int j = 0; j < NV; ++j) {
+      const int c0 = (k * 64 + lane) * NV, c = c0 + j;
+      // vector path (cols % NV == 0): a lane's NV columns stay contiguous,
+      // in range or in the sink, so the compiler can use 16-byte LDS ops
+      if constexpr (VEC) addr[k][j] = ((c0 < cols) ? c0 : SC) + j;
+      else addr[k][j] = (c < cols) ? c : SC;
     }
+  if constexpr (SLICES) {
+    // every wave writes its own slice at once; after one barrier the
+    // threads add the slices per column in wave order (the same order as
+    // the rounds below, so the same bits)
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        red[wid][0][addr[k][j]] = accg[k][j];
+        red[wid][1][addr[k][j]] = accb[k][j];
+        red[wid][2][addr[k][j]] = accs[k][j];
+      }
     __syncthreads();
-  }
-  for (int c = threadIdx.x; c < cols; c += 64 * W) {
-    const int64_t o = int64_t(blockIdx.x) * cols + c;
-    if (want_gb) {
-      a.part_g[o] = red[0][c];
-      a.part_b[o] = red[1][c];
+    for (int c = threadIdx.x; c < cols; c += 64 * W) {
+      float g = red[0][0][c], b = red[0][1][c], sm = red[0][2][c];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        g += red[w][0][c];
+        b += red[w][1][c];
+        sm += red[w][2][c];
+      }
+      const int64_t o = int64_t(blockIdx.x) * cols + c;
+      if (want_gb) {
+        a.part_g[o] = g;
+        a.part_b[o] = b;
+      }
+      if (want_s) a.part_s[o] = sm;
     }
-    if (want_s) a.part_s[o] = red[2][c];
+  } else {
+    for (int w = 0; w < W; ++w) {
+      if (wid == w) {
+        float cur[3][KV][NV];
+#pragma unroll
+        for (int k = 0; k < KV; ++k)
+#pragma unroll
+          for (int j = 0; j < NV; ++j) {
+            cur[0][k][j] = w > 0 ? red[0][0][addr[k][j]] : 0.f;
+            cur[1][k][j] = w > 0 ? red[0][1][addr[k][j]] : 0.f;
+            cur[2][k][j] = w > 0 ? red[0][2][addr[k][j]] : 0.f;
+          }
+#pragma unroll
+        for (int k = 0; k < KV; ++k)
+#pragma unroll
+          for (int j = 0; j < NV; ++j) {
+            red[0][0][addr[k][j]] = cur[0][k][j] + accg[k][j];
+            red[0][1][addr[k][j]] = cur[1][k][j] + accb[k][j];
+            red[0][2][addr[k][j]] = cur[2][k][j] + accs[k][j];
+          }
+      }
+      __syncthreads();
+    }
+    for (int c = threadIdx.x; c < cols; c += 64 * W) {
+      const int64_t o = int64_t(blockIdx.x) * cols + c;
+      if (want_gb) {
+        a.part_g[o] = red[0][0][c];
+        a.part_b[o] = red[0][1][c];
+      }
+      if (want_s) a.part_s[o] = red[0][2][c];
+    }
   }
 }
 
@@ -1013,8 +1083,8 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     const int64_t kv = (cols + 255) / 256;
     auto go = [&](auto kvt) {
       constexpr int KV = decltype(kvt)::value;
-      hipLaunchKernelGGL((layernorm_bwd_kernel<uint16_t, Bf16x4, KV, true, kRowLanes>), dim3(unsigned(nb)), dim3(kBlock),
-                         0, s, a);
+      hipLaunchKernelGGL((layernorm_bwd_kernel<uint16_t, Bf16x4, KV, true, kRowLanes, true>), dim3(unsigned(nb)),
+                         dim3(kBlock), 0, s, a);
     };
     if (kv == 1) go(IntC<1>{});
     else if (kv == 2) go(IntC<2>{});
