@@ -819,44 +819,56 @@ __global__ __launch_bounds__(kBlock) void add_layernorm_kernel(const uint2* __re
   const int64_t r = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
   if (r >= rows) return;  // whole waves
   const float inv_n = 1.f / float(cols4 * 4);
+  // Every load is issued up front from an in-range address (column 0 for
+  // lanes past the row end, a standing in for an absent b, column vectors
+  // for absent bias / gamma / beta) and replaced after the loads: guarded
+  // loads would sit in branches, each waited for before the next is issued.
+  const uint2* bsrc = b ? b : a;
+  uint2 xa[KV], xb[KV], zb[KV], gg[KV], bb[KV];
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int c = k * 64 + lane, cs = c < cols4 ? c : 0;
+    xa[k] = a[r * cols4 + cs];
+    xb[k] = bsrc[r * cols4 + cs];
+    zb[k] = bias ? bias[cs] : uint2{0u, 0u};
+    gg[k] = gamma ? gamma[cs] : uint2{0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+    bb[k] = beta ? beta[cs] : uint2{0u, 0u};
+  }
   float v[KV][4];
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
     const int c = k * 64 + lane;
-    if (c < cols4) {
-      const uint2 x = a[r * cols4 + c];
-      const uint2 y2 = b ? b[r * cols4 + c] : uint2{0u, 0u};
-      const uint2 z = bias ? bias[c] : uint2{0u, 0u};
-      const uint32_t w0 = pack_bf16(lo16(x.x) + lo16(y2.x) + lo16(z.x), hi16(x.x) + hi16(y2.x) + hi16(z.x));
-      const uint32_t w1 = pack_bf16(lo16(x.y) + lo16(y2.y) + lo16(z.y), hi16(x.y) + hi16(y2.y) + hi16(z.y));
-      sum_out[r * cols4 + c] = uint2{w0, w1};
-      v[k][0] = lo16(w0);
-      v[k][1] = hi16(w0);
-      v[k][2] = lo16(w1);
-      v[k][3] = hi16(w1);
-    } else {
-      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0.f;
-    }
+    const uint2 x = xa[k];
+    const uint2 y2 = b ? xb[k] : uint2{0u, 0u};
+    const uint2 z = zb[k];
+    const uint32_t w0 = pack_bf16(lo16(x.x) + lo16(y2.x) + lo16(z.x), hi16(x.x) + hi16(y2.x) + hi16(z.x));
+    const uint32_t w1 = pack_bf16(lo16(x.y) + lo16(y2.y) + lo16(z.y), hi16(x.y) + hi16(y2.y) + hi16(z.y));
+    const bool in_row = c < cols4;
+    if (in_row) sum_out[r * cols4 + c] = uint2{w0, w1};
+    v[k][0] = in_row ? lo16(w0) : 0.f;
+    v[k][1] = in_row ? hi16(w0) : 0.f;
+    v[k][2] = in_row ? lo16(w1) : 0.f;
+    v[k][3] = in_row ? hi16(w1) : 0.f;
     s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
   }
   const float mean = wave_sum_dpp(s) * inv_n;
   float q = 0.f;
 #pragma unroll
-  for (int k = 0; k < KV; ++k)
-    if (k * 64 + lane < cols4)
+  for (int k = 0; k < KV; ++k) {
+    const bool in_row = k * 64 + lane < cols4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float d = v[k][j] - mean;
-        q += d * d;
-      }
+    for (int j = 0; j < 4; ++j) {
+      const float d = in_row ? v[k][j] - mean : 0.f;
+      q += d * d;
+    }
+  }
   const float rstd = 1.f / sqrtf(wave_sum_dpp(q) * inv_n + eps);
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
     const int c = k * 64 + lane;
     if (c < cols4) {
-      const uint2 g = gamma ? gamma[c] : uint2{0x3F803F80u, 0x3F803F80u};  // bf16 1.0
-      const uint2 be = beta ? beta[c] : uint2{0u, 0u};
+      const uint2 g = gg[k], be = bb[k];
       const float o0 = (v[k][0] - mean) * rstd * lo16(g.x) + lo16(be.x);
       const float o1 = (v[k][1] - mean) * rstd * hi16(g.x) + hi16(be.x);
       const float o2 = (v[k][2] - mean) * rstd * lo16(g.y) + lo16(be.y);
