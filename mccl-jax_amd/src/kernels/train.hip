@@ -632,6 +632,12 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   const int64_t head = min<int64_t>(cols, int64_t(((16u - (reinterpret_cast<uintptr_t>(xr) & 15u)) & 15u) / 2u));
   const int64_t nv = (cols - head) / 8, tail = cols - head - nv * 8;
   const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xr + head);
+  // the label's logit (for the loss) is loaded with the row, by every lane
+  // from one in-range address, rather than by one thread after the
+  // reductions, where its round trip would end every workgroup
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  const uint16_t xlab_bits = xr[lab_ok ? lab : 0];
   u32x4_t v[NVT];
 #pragma unroll
   for (int i = 0; i < NVT; ++i) {
@@ -671,9 +677,7 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   const float S = block_reduce(sum, false);
   const float lse = M + __logf(S);
   const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
-  const int64_t lab = int64_t(labels[row]);
-  const bool lab_ok = lab >= 0 && lab < cols;
-  if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xr[lab]) : __builtin_nanf("");
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xlab_bits) : __builtin_nanf("");
   // gradient, from the registers (every read of the row is done: in place is safe)
   u32x4_t* dv = reinterpret_cast<u32x4_t*>(dr + head);
 #pragma unroll
