@@ -66,6 +66,26 @@ struct TileLoader {
 
   __device__ inline void load(const T* src, int64_t rs, int64_t ks, int64_t row0, int64_t rows,
                               int64_t k0, int64_t K, bool vec) {
+    // Interior tile (the whole ROWS x BK block in range) with vector access:
+    // every chunk is one 16-byte load, issued without a per-chunk bounds
+    // branch.  (Loads inside such branches are each waited for before the
+    // next is issued.)  The condition is uniform over the workgroup.
+    if (vec && row0 + ROWS <= rows && k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < PER_T; ++i) {
+        const int ch = threadIdx.x + i * kThreads;
+        if constexpr (KC) {
+          const int r = ch / (BK / VEC), kc = (ch % (BK / VEC)) * VEC;
+          reg[i][0] = *reinterpret_cast<const u32x4_t*>(src + (row0 + r) * rs + (k0 + kc));
+        } else {
+          const int rc = (ch % (ROWS / VEC)) * VEC, kp = (ch / (ROWS / VEC)) * KPAIR;
+#pragma unroll
+          for (int q = 0; q < KPAIR; ++q)
+            reg[i][q] = *reinterpret_cast<const u32x4_t*>(src + (k0 + kp + q) * ks + (row0 + rc));
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int ch = threadIdx.x + i * kThreads;
