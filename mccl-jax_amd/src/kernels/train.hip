@@ -889,8 +889,13 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const u32x4_t* x, con
                                                          int64_t nvec, int64_t cvec, u32x4_t* pre,
                                                          u32x4_t* __restrict__ y) {
   const int64_t stride = int64_t(gridDim.x) * kBlock;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
-    const u32x4_t a = x[i], b = bias[i % cvec];
+  // bias column of vector i, advanced with i (no 64-bit division per trip)
+  const int64_t i0 = int64_t(blockIdx.x) * kBlock + threadIdx.x, step = stride % cvec;
+  int64_t ci = i0 % cvec;
+  for (int64_t i = i0; i < nvec; i += stride) {
+    const u32x4_t a = x[i], b = bias[ci];
+    ci += step;
+    if (ci >= cvec) ci -= cvec;
     u32x4_t p, o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -923,10 +928,15 @@ __global__ __launch_bounds__(kBlock) void add_rows_bf16x8_kernel(const u32x4_t* 
                                                                const u32x4_t* __restrict__ bias, int64_t nvec,
                                                                int64_t cvec, u32x4_t* __restrict__ out) {
   const int64_t stride = int64_t(gridDim.x) * kBlock;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < nvec; i += stride) {
+  // bias column of vector i, advanced with i (no 64-bit division per trip)
+  const int64_t i0 = int64_t(blockIdx.x) * kBlock + threadIdx.x, step = stride % cvec;
+  int64_t ci = i0 % cvec;
+  for (int64_t i = i0; i < nvec; i += stride) {
     const u32x4_t x = a[i];
     const u32x4_t y = b ? b[i] : u32x4_t{0u, 0u, 0u, 0u};
-    const u32x4_t z = bias ? bias[i % cvec] : u32x4_t{0u, 0u, 0u, 0u};
+    const u32x4_t z = bias ? bias[ci] : u32x4_t{0u, 0u, 0u, 0u};
+    ci += step;
+    if (ci >= cvec) ci -= cvec;
     u32x4_t o;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
