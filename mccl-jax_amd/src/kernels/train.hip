@@ -613,7 +613,8 @@ __global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restric
 // NVT of them), the unaligned head and tail (under 8 elements each) as one
 // scalar on threads 0..7 and 8..15.  The row is read once: max, sum of
 // exp(x - max), then dlogits = (exp(x - lse) - [j == label]) * grad_scale
-// written from the same registers (so dlogits may be logits).
+// written from the same registers (so dlogits may be logits); the label's
+// element is rewritten by one thread after a barrier.
 constexpr int kXentThreads = 512;
 constexpr uint32_t kBf16NegInfPair = 0xFF80FF80u;
 
@@ -684,21 +685,29 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   for (int i = 0; i < NVT; ++i) {
     const int64_t idx = t + int64_t(i) * kXentThreads;
     if (idx < nv) {
-      const int64_t j0 = head + idx * 8;
       u32x4_t o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(lo16(v[i][j]) - M, kL2e, -ls2)) - (j0 + 2 * j == lab ? 1.f : 0.f);
-        const float p1 =
-            __builtin_amdgcn_exp2f(fmaf(hi16(v[i][j]) - M, kL2e, -ls2)) - (j0 + 2 * j + 1 == lab ? 1.f : 0.f);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(lo16(v[i][j]) - M, kL2e, -ls2));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(hi16(v[i][j]) - M, kL2e, -ls2));
         o[j] = pack_bf16(p0 * grad_scale, p1 * grad_scale);
       }
       dv[idx] = o;
     }
   }
   if (ej >= 0) {
-    const float p = __builtin_amdgcn_exp2f(fmaf(ex - M, kL2e, -ls2)) - (ej == lab ? 1.f : 0.f);
+    const float p = __builtin_amdgcn_exp2f(fmaf(ex - M, kL2e, -ls2));
     dr[ej] = f32_to_bf16(p * grad_scale);
+  }
+  // the one-hot term touches one element: after every store above, thread 0
+  // rewrites it as (p - 1) * grad_scale, p from the label's logit (the same
+  // value and rounding as the element's own store)
+  if (lab_ok) {
+    __syncthreads();
+    if (t == 0) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(bf16_to_f32(xlab_bits) - M, kL2e, -ls2)) - 1.f;
+      dr[lab] = f32_to_bf16(p * grad_scale);
+    }
   }
 }
 
