@@ -107,17 +107,33 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
 namespace {
 // C[m, n] = sum over slices s of W[s][m][n] (dense M x N slices), slices added
 // in order: the result does not depend on scheduling.
+// S > 0: the slice count is a compile-time constant, so a vector's S loads
+// are issued together (with a runtime count each load is waited for before
+// the next); S == 0: any count.  Same order of adds either way.
+template <int S>
 __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ w, int64_t splits, int64_t M,
                                                         int64_t N, float* __restrict__ c, int64_t c_ms) {
   const int64_t nvec = M * N / 4, slab = M * N / 4;
   const int64_t stride = int64_t(gridDim.x) * 256;
   const f32x4* wv = reinterpret_cast<const f32x4*>(w);
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < nvec; i += stride) {
-    f32x4 a = wv[i];
-    for (int64_t s = 1; s < splits; ++s) {
-      const f32x4 b = wv[s * slab + i];
+    f32x4 a;
+    if constexpr (S > 0) {
+      f32x4 b[S];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) a.v[j] += b.v[j];
+      for (int s = 0; s < S; ++s) b[s] = wv[s * slab + i];
+      a = b[0];
+#pragma unroll
+      for (int s = 1; s < S; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a.v[j] += b[s].v[j];
+    } else {
+      a = wv[i];
+      for (int64_t s = 1; s < splits; ++s) {
+        const f32x4 b = wv[s * slab + i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a.v[j] += b.v[j];
+      }
     }
     const int64_t e = i * 4, m = e / N, n = e % N;
     *reinterpret_cast<f32x4*>(c + m * c_ms + n) = a;
@@ -152,7 +168,10 @@ extern "C" int mk_gemm_blas_splitk(void* stream, int ab_type, int64_t M, int64_t
     return rc;
   const int64_t nvec = M * N / 4;
   const unsigned blocks = unsigned(std::min<int64_t>((nvec + 255) / 256, 4096));
-  hipLaunchKernelGGL(mk::splitk_sum_kernel, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  if (splits == 2) hipLaunchKernelGGL(mk::splitk_sum_kernel<2>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else if (splits == 4) hipLaunchKernelGGL(mk::splitk_sum_kernel<4>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else if (splits == 8) hipLaunchKernelGGL(mk::splitk_sum_kernel<8>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else hipLaunchKernelGGL(mk::splitk_sum_kernel<0>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
   return mk::check_launch("mk_gemm_blas_splitk");
 }
 
