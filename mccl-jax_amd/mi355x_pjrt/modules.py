@@ -157,11 +157,14 @@ def argmax(rows=65536, cols=1024, is_min=False) -> str:
 """
 
 
-def sdpa(b=4, h=16, s=8192, d=128, causal=True) -> str:
+def sdpa(b=4, h=16, s=8192, d=128, causal=True, mask_ops=None) -> str:
     """C3: s = einsum('bhqd,bhkd->bhqk', q, k) / sqrt(d) (bf16, the constant
     rounded to bf16); s = where(tril(ones((S, S), bool)), s, -inf);
     p = jax.nn.softmax(s, -1) (max, exp, sum in f32 via convert, divide);
-    o = einsum('bhqk,bhkd->bhqd', p, v)."""
+    o = einsum('bhqk,bhkd->bhqd', p, v).
+
+    ``mask_ops``: StableHLO lines that define ``%6``, the [b,h,s,s] i1 mask
+    (any form), in place of the iota/compare causal mask."""
     q = _t((b, h, s, d), "bf16")
     sc = _t((b, h, s, s), "bf16")
     sf = _t((b, h, s, s), "f32")
@@ -172,7 +175,13 @@ def sdpa(b=4, h=16, s=8192, d=128, causal=True) -> str:
     sqrt_d = float(d) ** 0.5
     mask = ""
     use = "%2"
-    if causal:
+    if mask_ops is not None:
+        mask = mask_ops + f"""    %cst_1 = stablehlo.constant dense<0xFF80> : tensor<bf16>
+    %7 = stablehlo.broadcast_in_dim %cst_1, dims = [] : (tensor<bf16>) -> {sc}
+    %8 = stablehlo.select %6, %2, %7 : {m4}, {sc}
+"""
+        use = "%8"
+    elif causal:
         mask = f"""    %3 = stablehlo.iota dim = 0 : {i2}
     %4 = stablehlo.iota dim = 1 : {i2}
     %5 = stablehlo.compare  GE, %3, %4,  SIGNED : ({i2}, {i2}) -> {m2}

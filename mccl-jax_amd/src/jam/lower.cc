@@ -595,12 +595,10 @@ class Lowerer {
         continue;
       }
       if (p->name != "stablehlo.constant") return false;
-      Attr a = *p->attr("value");
-      std::string err;
-      if (!ParseDense(a, m_.types[v], err)) return false;
-      if (!a.splat && m_.types[v].numel() != 1) return false;
+      const Attr* a = ParsedConst(v);
+      if (!a || (!a->splat && m_.types[v].numel() != 1)) return false;
       const DType d = m_.types[v].dtype;
-      double x = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
+      double x = a->fvals.empty() ? double(a->ivals[0]) : a->fvals[0];
       if (d == DType::kBF16) x = Bf16ToF32(F64ToBf16(x));
       else if (d == DType::kF16) x = F16ToF32(F64ToF16(x));
       else if (d == DType::kF32) x = float(x);
@@ -772,125 +770,475 @@ class Lowerer {
     return true;
   }
 
-  // Point evaluation of a mask expression at index `idx`; false when the
-  // expression is not a static function of iota/constants.
-  bool EvalPoint(int v, const std::vector<int64_t>& idx, double* out, int depth = 0) const {
-    if (depth > 64) return false;
+  // ---- the attention mask, proven rather than sampled
+  //
+  // A mask sub-expression is read symbolically over its own index axes:
+  //   * an integer affine form c0 + Σ c[k]·idx[k] (iota, integer-valued splat
+  //     constants, add/subtract/negate, multiply by a constant, and converts
+  //     that are exact over the value's range),
+  //   * a predicate: a boolean formula (and/or/not/xor) over half-planes
+  //     `affine >= 0` (from compare of two affine forms, select between
+  //     constant booleans, constant booleans),
+  //   * a dense constant read through an index map (broadcast / transpose /
+  //     unit reshape), optionally compared with a splat constant.
+  // Layout ops remap the axes.  Anything else makes the mask "unknown" and
+  // the attention stays on the generic path.
+  struct MaskAff {
+    int64_t c0 = 0;
+    std::vector<int64_t> c;  // one coefficient per axis of the value
+  };
+  struct MaskNode {
+    enum Kind { kLeaf, kConst, kAnd, kOr, kXor, kNot } kind = kConst;
+    MaskAff aff;   // kLeaf: aff >= 0
+    bool val = false;
+    int a = -1, b = -1;
+  };
+  struct MaskSym {
+    enum Kind { kNone, kAff, kPred, kTable } kind = kNone;
+    MaskAff aff;
+    std::vector<MaskNode> nodes;
+    int root = -1;
+    // kTable: element at idx = table[toff + Σ tstride[k]·idx[k]], then the
+    // converts in `conv`, then (if cmp set) compared with cmp_val
+    const Attr* table = nullptr;
+    DType table_dtype = DType::kInvalid;
+    std::vector<int64_t> tstride;
+    int64_t toff = 0;
+    std::vector<DType> conv;
+    std::string cmp;
+    double cmp_val = 0;
+  };
+
+  const Attr* ParsedConst(int v) const {
+    const int pi = v >= 0 ? producer_[v] : -1;
+    if (pi < 0 || ops_[pi].name != "stablehlo.constant") return nullptr;
+    auto it = const_cache_.find(pi);
+    if (it != const_cache_.end()) return it->second.get();
+    auto a = std::make_shared<Attr>(*ops_[pi].attr("value"));
+    std::string err;
+    if (!ParseDense(*a, m_.types[v], err)) a.reset();
+    return (const_cache_[pi] = a).get();
+  }
+
+  static int64_t AffBound(const MaskAff& f, const std::vector<int64_t>& dims) {
+    // max |value| over the index box (saturating)
+    double m = std::fabs(double(f.c0));
+    for (size_t k = 0; k < f.c.size(); ++k) m += std::fabs(double(f.c[k])) * double(std::max<int64_t>(dims[k] - 1, 0));
+    return m > 9e18 ? INT64_MAX : int64_t(m);
+  }
+  static bool ExactIn(int64_t bound, DType d) {
+    switch (d) {
+      case DType::kBF16: return bound <= (int64_t(1) << 8);
+      case DType::kF16: return bound <= (int64_t(1) << 11);
+      case DType::kF32: return bound <= (int64_t(1) << 24);
+      case DType::kF64: return bound <= (int64_t(1) << 53);
+      case DType::kI8: case DType::kU8: return bound < (int64_t(1) << 7);
+      case DType::kI16: case DType::kU16: return bound < (int64_t(1) << 15);
+      case DType::kI32: case DType::kU32: return bound < (int64_t(1) << 31);
+      case DType::kI64: case DType::kU64: return bound < INT64_MAX;
+      default: return false;
+    }
+  }
+  static double ConvertScalar(double x, DType d) {
+    switch (d) {
+      case DType::kPred: return x != 0 ? 1.0 : 0.0;
+      case DType::kBF16: return std::isnan(x) ? x : Bf16ToF32(F64ToBf16(x));
+      case DType::kF16: return std::isnan(x) ? x : F16ToF32(F64ToF16(x));
+      case DType::kF32: return double(float(x));
+      case DType::kF64: return x;
+      default: return std::isfinite(x) ? std::trunc(x) : 0.0;  // float -> int truncates
+    }
+  }
+  static bool CompareDir(const std::string& dir, double a, double b, bool* ok) {
+    *ok = true;
+    if (dir == "GE") return a >= b;
+    if (dir == "GT") return a > b;
+    if (dir == "LE") return a <= b;
+    if (dir == "LT") return a < b;
+    if (dir == "EQ") return a == b;
+    if (dir == "NE") return a != b;
+    *ok = false;
+    return false;
+  }
+  static std::string CompareDirOf(const Op& p) {
+    if (const Attr* x = p.attr("comparison_direction")) return x->s;
+    if (const Attr* x = p.attr("enum0")) return x->s;
+    return "";
+  }
+
+  // Remap the axes of a symbolic value: new axis k takes the old axis
+  // from[k] (-1: a new axis the value does not depend on); old axes of size
+  // 1 that are dropped read index 0.
+  static void RemapAff(MaskAff& f, const std::vector<int>& from) {
+    std::vector<int64_t> c(from.size(), 0);
+    for (size_t k = 0; k < from.size(); ++k)
+      if (from[k] >= 0) c[k] = f.c[size_t(from[k])];
+    f.c = std::move(c);
+  }
+  static void RemapSym(MaskSym& s, const std::vector<int>& from) {
+    if (s.kind == MaskSym::kAff) RemapAff(s.aff, from);
+    if (s.kind == MaskSym::kPred)
+      for (auto& n : s.nodes)
+        if (n.kind == MaskNode::kLeaf) RemapAff(n.aff, from);
+    if (s.kind == MaskSym::kTable) {
+      std::vector<int64_t> st(from.size(), 0);
+      for (size_t k = 0; k < from.size(); ++k)
+        if (from[k] >= 0) st[k] = s.tstride[size_t(from[k])];
+      s.tstride = std::move(st);
+    }
+  }
+  static MaskSym PredConst(bool v) {
+    MaskSym s;
+    s.kind = MaskSym::kPred;
+    MaskNode n;
+    n.kind = MaskNode::kConst;
+    n.val = v;
+    s.nodes.push_back(n);
+    s.root = 0;
+    return s;
+  }
+  static MaskSym PredCombine(MaskNode::Kind k, const MaskSym& x, const MaskSym* y) {
+    MaskSym s;
+    s.kind = MaskSym::kPred;
+    s.nodes = x.nodes;
+    const int ra = x.root;
+    int rb = -1;
+    if (y) {
+      const int off = int(s.nodes.size());
+      for (MaskNode n : y->nodes) {
+        if (n.a >= 0) n.a += off;
+        if (n.b >= 0) n.b += off;
+        s.nodes.push_back(n);
+      }
+      rb = y->root + off;
+    }
+    MaskNode n;
+    n.kind = k;
+    n.a = ra;
+    n.b = rb;
+    s.nodes.push_back(n);
+    s.root = int(s.nodes.size()) - 1;
+    return s;
+  }
+
+  MaskSym MaskSymOf(int v, int depth = 0) const {
+    MaskSym none;
+    if (depth > 64) return none;
     const Op* p = prod(v);
-    if (!p) return false;
-    const auto& od = m_.types[v].dims;
-    auto ev = [&](int w, const std::vector<int64_t>& ix, double* r) { return EvalPoint(w, ix, r, depth + 1); };
+    if (!p) return none;
+    const TensorType& t = m_.types[v];
+    const int r = t.rank();
     const std::string& n = p->name;
+    auto sub = [&](int w) { return MaskSymOf(w, depth + 1); };
     if (n == "stablehlo.iota") {
       const auto dd = attr_ints(*p, {"dim", "iota_dimension"});
-      *out = double(idx.at(dd.empty() ? 0 : dd[0]));
-      return true;
+      const int64_t d = dd.empty() ? 0 : dd[0];
+      if (d < 0 || d >= r || !ExactIn(t.dims[size_t(d)] - 1, t.dtype)) return none;
+      MaskSym s;
+      s.kind = MaskSym::kAff;
+      s.aff.c.assign(size_t(r), 0);
+      s.aff.c[size_t(d)] = 1;
+      return s;
     }
     if (n == "stablehlo.constant") {
-      Attr a = *p->attr("value");
-      std::string err;
-      if (!ParseDense(a, m_.types[v], err)) return false;
-      if (a.splat) {
-        *out = a.fvals.empty() ? double(a.ivals[0]) : a.fvals[0];
-        return true;
+      const Attr* a = ParsedConst(v);
+      if (!a) return none;
+      if (a->splat || t.numel() == 1) {
+        if (t.dtype == DType::kPred) return PredConst(a->ivals.at(0) != 0);
+        const double x = a->fvals.empty() ? double(a->ivals.at(0)) : a->fvals.at(0);
+        if (!(std::fabs(x) < 9e15) || x != std::trunc(x)) return none;
+        MaskSym s;
+        s.kind = MaskSym::kAff;
+        s.aff.c0 = int64_t(x);
+        s.aff.c.assign(size_t(r), 0);
+        return s;
       }
-      int64_t lin = 0;
-      for (size_t d = 0; d < od.size(); ++d) lin = lin * od[d] + idx[d];
-      *out = a.fvals.at(size_t(lin));
-      return true;
+      MaskSym s;
+      s.kind = MaskSym::kTable;
+      s.table = a;
+      s.table_dtype = t.dtype;
+      s.tstride = DenseStrides(t.dims);
+      for (int k = 0; k < r; ++k)
+        if (t.dims[size_t(k)] == 1) s.tstride[size_t(k)] = 0;
+      return s;
     }
     if (n == "stablehlo.broadcast_in_dim") {
       const auto dims = attr_ints(*p, {"dims", "broadcast_dimensions"});
       const auto& id = m_.types[p->operands[0]].dims;
-      std::vector<int64_t> ix(id.size());
-      for (size_t k = 0; k < id.size(); ++k) ix[k] = id[k] == 1 ? 0 : idx.at(dims.at(k));
-      return ev(p->operands[0], ix, out);
-    }
-    if (n == "stablehlo.reshape") {
-      int64_t lin = 0;
-      for (size_t d = 0; d < od.size(); ++d) lin = lin * od[d] + idx[d];
-      const auto& id = m_.types[p->operands[0]].dims;
-      std::vector<int64_t> ix(id.size());
-      for (int d = int(id.size()) - 1; d >= 0; --d) {
-        ix[d] = lin % id[d];
-        lin /= id[d];
+      if (dims.size() != id.size()) return none;
+      MaskSym s = sub(p->operands[0]);
+      if (s.kind == MaskSym::kNone) return none;
+      std::vector<int> from(size_t(r), -1);
+      for (size_t k = 0; k < id.size(); ++k) {
+        if (dims[k] < 0 || dims[k] >= r) return none;
+        if (id[k] != 1) from[size_t(dims[k])] = int(k);
       }
-      return ev(p->operands[0], ix, out);
+      RemapSym(s, from);
+      return s;
     }
     if (n == "stablehlo.transpose") {
       const auto perm = attr_ints(*p, {"dims", "permutation"});
-      std::vector<int64_t> ix(perm.size());
-      for (size_t k = 0; k < perm.size(); ++k) ix[perm[k]] = idx[k];
-      return ev(p->operands[0], ix, out);
+      if (int(perm.size()) != r) return none;
+      MaskSym s = sub(p->operands[0]);
+      if (s.kind == MaskSym::kNone) return none;
+      std::vector<int> from(static_cast<size_t>(r));
+      for (int k = 0; k < r; ++k) from[size_t(k)] = int(perm[size_t(k)]);
+      RemapSym(s, from);
+      return s;
     }
-    if (n == "stablehlo.convert") return ev(p->operands[0], idx, out);
-    double a = 0, b = 0, c = 0;
-    if (n == "stablehlo.compare") {
-      if (!ev(p->operands[0], idx, &a) || !ev(p->operands[1], idx, &b)) return false;
-      std::string dir;
-      if (const Attr* x = p->attr("comparison_direction")) dir = x->s;
-      else if (const Attr* x = p->attr("enum0")) dir = x->s;
-      if (dir == "GE") *out = a >= b;
-      else if (dir == "GT") *out = a > b;
-      else if (dir == "LE") *out = a <= b;
-      else if (dir == "LT") *out = a < b;
-      else if (dir == "EQ") *out = a == b;
-      else if (dir == "NE") *out = a != b;
-      else return false;
-      return true;
+    if (n == "stablehlo.reshape") {
+      // only insertion / removal of unit axes
+      const auto& id = m_.types[p->operands[0]].dims;
+      std::vector<int> in_nu, out_nu;
+      for (size_t k = 0; k < id.size(); ++k)
+        if (id[k] != 1) in_nu.push_back(int(k));
+      for (int k = 0; k < r; ++k)
+        if (t.dims[size_t(k)] != 1) out_nu.push_back(k);
+      if (in_nu.size() != out_nu.size()) return none;
+      std::vector<int> from(size_t(r), -1);
+      for (size_t k = 0; k < in_nu.size(); ++k) {
+        if (id[size_t(in_nu[k])] != t.dims[size_t(out_nu[k])]) return none;
+        from[size_t(out_nu[k])] = in_nu[k];
+      }
+      MaskSym s = sub(p->operands[0]);
+      if (s.kind == MaskSym::kNone) return none;
+      RemapSym(s, from);
+      return s;
     }
-    if (n == "stablehlo.select") {
-      if (!ev(p->operands[0], idx, &a)) return false;
-      return ev(p->operands[a != 0 ? 1 : 2], idx, out);
+    if (n == "stablehlo.convert") {
+      const int w = p->operands[0];
+      MaskSym s = sub(w);
+      const DType to = t.dtype;
+      if (s.kind == MaskSym::kAff) {
+        if (to == DType::kPred || !ExactIn(AffBound(s.aff, t.dims), to)) return none;
+        return s;
+      }
+      if (s.kind == MaskSym::kPred) return to == DType::kPred ? s : none;
+      if (s.kind == MaskSym::kTable && s.cmp.empty()) {
+        s.conv.push_back(to);
+        return s;
+      }
+      return none;
     }
-    if (p->operands.size() == 2 && (n == "stablehlo.add" || n == "stablehlo.subtract" ||
-                                    n == "stablehlo.multiply" || n == "stablehlo.and" ||
-                                    n == "stablehlo.or")) {
-      if (!ev(p->operands[0], idx, &a) || !ev(p->operands[1], idx, &b)) return false;
-      if (n == "stablehlo.add") *out = a + b;
-      else if (n == "stablehlo.subtract") *out = a - b;
-      else if (n == "stablehlo.multiply") *out = a * b;
-      else if (n == "stablehlo.and") *out = (a != 0) && (b != 0);
-      else *out = (a != 0) || (b != 0);
-      return true;
+    if (n == "stablehlo.negate") {
+      MaskSym s = sub(p->operands[0]);
+      if (s.kind != MaskSym::kAff || IsUnsigned(t.dtype)) return none;
+      s.aff.c0 = -s.aff.c0;
+      for (auto& c : s.aff.c) c = -c;
+      return s;
     }
     if (n == "stablehlo.not") {
-      if (!ev(p->operands[0], idx, &c)) return false;
-      *out = c == 0;
-      return true;
+      MaskSym s = sub(p->operands[0]);
+      if (s.kind == MaskSym::kPred) return PredCombine(MaskNode::kNot, s, nullptr);
+      return none;
     }
-    return false;
+    if ((n == "stablehlo.and" || n == "stablehlo.or" || n == "stablehlo.xor") && p->operands.size() == 2) {
+      if (t.dtype != DType::kPred) return none;
+      MaskSym a = sub(p->operands[0]), b = sub(p->operands[1]);
+      if (a.kind != MaskSym::kPred || b.kind != MaskSym::kPred) return none;
+      return PredCombine(n == "stablehlo.and" ? MaskNode::kAnd : n == "stablehlo.or" ? MaskNode::kOr : MaskNode::kXor,
+                         a, &b);
+    }
+    if ((n == "stablehlo.add" || n == "stablehlo.subtract" || n == "stablehlo.multiply") && p->operands.size() == 2) {
+      if (t.dtype == DType::kPred) return none;
+      MaskSym a = sub(p->operands[0]), b = sub(p->operands[1]);
+      if (a.kind != MaskSym::kAff || b.kind != MaskSym::kAff) return none;
+      MaskSym s;
+      s.kind = MaskSym::kAff;
+      s.aff.c.assign(size_t(r), 0);
+      if (n == "stablehlo.multiply") {
+        const bool a_const = std::all_of(a.aff.c.begin(), a.aff.c.end(), [](int64_t c) { return c == 0; });
+        const bool b_const = std::all_of(b.aff.c.begin(), b.aff.c.end(), [](int64_t c) { return c == 0; });
+        if (!a_const && !b_const) return none;
+        const MaskAff& f = a_const ? b.aff : a.aff;
+        const int64_t m = a_const ? a.aff.c0 : b.aff.c0;
+        if (std::llabs(m) > (int64_t(1) << 20)) return none;
+        s.aff.c0 = f.c0 * m;
+        for (size_t k = 0; k < f.c.size(); ++k) s.aff.c[k] = f.c[k] * m;
+      } else {
+        const int64_t sg = n == "stablehlo.add" ? 1 : -1;
+        s.aff.c0 = a.aff.c0 + sg * b.aff.c0;
+        for (size_t k = 0; k < s.aff.c.size(); ++k) s.aff.c[k] = a.aff.c[k] + sg * b.aff.c[k];
+      }
+      // every intermediate value must be exact in the op's own type
+      if (!ExactIn(AffBound(s.aff, t.dims), t.dtype)) return none;
+      if (IsUnsigned(t.dtype)) return none;  // wrap-around is not affine
+      return s;
+    }
+    if (n == "stablehlo.compare" && p->operands.size() == 2) {
+      const std::string dir = CompareDirOf(*p);
+      MaskSym a = sub(p->operands[0]), b = sub(p->operands[1]);
+      if (a.kind == MaskSym::kAff && b.kind == MaskSym::kAff) {
+        // d = a - b; integer-valued, so GT d >= 1, LT -d >= 1
+        MaskAff d;
+        d.c.assign(size_t(r), 0);
+        d.c0 = a.aff.c0 - b.aff.c0;
+        for (size_t k = 0; k < d.c.size(); ++k) d.c[k] = a.aff.c[k] - b.aff.c[k];
+        auto leaf = [&](MaskAff f) {
+          MaskSym s;
+          s.kind = MaskSym::kPred;
+          MaskNode x;
+          x.kind = MaskNode::kLeaf;
+          x.aff = std::move(f);
+          s.nodes.push_back(x);
+          s.root = 0;
+          return s;
+        };
+        MaskAff neg = d;
+        neg.c0 = -neg.c0;
+        for (auto& c : neg.c) c = -c;
+        if (dir == "GE") return leaf(d);
+        if (dir == "LE") return leaf(neg);
+        if (dir == "GT") { d.c0 -= 1; return leaf(d); }
+        if (dir == "LT") { neg.c0 -= 1; return leaf(neg); }
+        if (dir == "EQ" || dir == "NE") {
+          // d == 0  <=>  d >= 0 and -d >= 0
+          MaskSym ge = leaf(d), le = leaf(neg);
+          MaskSym eq = PredCombine(MaskNode::kAnd, ge, &le);
+          return dir == "EQ" ? eq : PredCombine(MaskNode::kNot, eq, nullptr);
+        }
+        return none;
+      }
+      // table OP splat constant (either side)
+      double c = 0;
+      bool ok = false;
+      if (a.kind == MaskSym::kTable && a.cmp.empty() && scalar_of(p->operands[1], &c)) {
+        CompareDir(dir, 0, 0, &ok);
+        if (!ok) return none;
+        a.cmp = dir;
+        a.cmp_val = c;
+        return a;
+      }
+      if (b.kind == MaskSym::kTable && b.cmp.empty() && scalar_of(p->operands[0], &c)) {
+        static const std::map<std::string, std::string> flip = {{"GE", "LE"}, {"LE", "GE"}, {"GT", "LT"},
+                                                                  {"LT", "GT"}, {"EQ", "EQ"}, {"NE", "NE"}};
+        auto it = flip.find(dir);
+        if (it == flip.end()) return none;
+        b.cmp = it->second;
+        b.cmp_val = c;
+        return b;
+      }
+      return none;
+    }
+    if (n == "stablehlo.select" && p->operands.size() == 3 && t.dtype == DType::kPred) {
+      // select(p, true, false) = p ; select(p, false, true) = not p
+      MaskSym c = sub(p->operands[0]);
+      MaskSym x = sub(p->operands[1]), y = sub(p->operands[2]);
+      auto const_of = [](const MaskSym& s, bool* v) {
+        if (s.kind != MaskSym::kPred || s.nodes.size() != 1 || s.nodes[0].kind != MaskNode::kConst) return false;
+        *v = s.nodes[0].val;
+        return true;
+      };
+      bool xv, yv;
+      if (c.kind != MaskSym::kPred || !const_of(x, &xv) || !const_of(y, &yv)) return none;
+      if (xv == yv) return PredConst(xv);
+      return xv ? c : PredCombine(MaskNode::kNot, c, nullptr);
+    }
+    return none;
   }
 
-  // 1 = causal (key j visible iff j <= i), 0 = all visible, -1 = other/unknown
-  int ClassifyMask(int mask, int64_t B, int64_t H, int64_t Sq, int64_t Sk) const {
-    std::vector<std::pair<int64_t, int64_t>> pts;
-    if (Sq * Sk <= 4096) {
-      for (int64_t i = 0; i < Sq; ++i)
-        for (int64_t j = 0; j < Sk; ++j) pts.push_back({i, j});
-    } else {
-      for (int64_t i = 0; i < std::min(Sq, Sk); i += std::max<int64_t>(1, std::min(Sq, Sk) / 512)) {
-        pts.push_back({i, i});
-        if (i + 1 < Sk) pts.push_back({i, i + 1});
-        if (i > 0) pts.push_back({i, i - 1});
-      }
-      pts.push_back({0, Sk - 1});
-      pts.push_back({Sq - 1, 0});
-      pts.push_back({Sq - 1, Sk - 1});
-      std::mt19937_64 rng(12345);
-      for (int t = 0; t < 2000; ++t) pts.push_back({int64_t(rng() % uint64_t(Sq)), int64_t(rng() % uint64_t(Sk))});
+  // Visible keys of row i under a predicate formula, as sorted disjoint
+  // half-open intervals [lo, hi) within [0, Sk).  Only axes 2 (query) and 3
+  // (key) may carry coefficients; the caller checks that.
+  using Ivals = std::vector<std::pair<int64_t, int64_t>>;
+  static Ivals IvUnion(const Ivals& a, const Ivals& b) {
+    Ivals all = a;
+    all.insert(all.end(), b.begin(), b.end());
+    std::sort(all.begin(), all.end());
+    Ivals out;
+    for (auto& iv : all) {
+      if (iv.first >= iv.second) continue;
+      if (!out.empty() && iv.first <= out.back().second) out.back().second = std::max(out.back().second, iv.second);
+      else out.push_back(iv);
     }
-    bool all_true = true, causal = true;
-    for (int64_t b : {int64_t(0), B - 1})
-      for (int64_t h : {int64_t(0), H - 1})
-        for (auto& ij : pts) {
-          double r = 0;
-          if (!EvalPoint(mask, {b, h, ij.first, ij.second}, &r)) return -1;
-          const bool vis = r != 0;
-          all_true &= vis;
-          causal &= (vis == (ij.second <= ij.first));
+    return out;
+  }
+  static Ivals IvComplement(const Ivals& a, int64_t Sk) {
+    Ivals out;
+    int64_t at = 0;
+    for (auto& iv : a) {
+      if (iv.first > at) out.push_back({at, iv.first});
+      at = std::max(at, iv.second);
+    }
+    if (at < Sk) out.push_back({at, Sk});
+    return out;
+  }
+  static Ivals IvIntersect(const Ivals& a, const Ivals& b, int64_t Sk) {
+    return IvComplement(IvUnion(IvComplement(a, Sk), IvComplement(b, Sk)), Sk);
+  }
+  static int64_t FloorDiv(int64_t a, int64_t b) {
+    int64_t q = a / b;
+    if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+    return q;
+  }
+  static Ivals RowVisible(const std::vector<MaskNode>& nodes, int at, int64_t i, int64_t Sk) {
+    const MaskNode& n = nodes[size_t(at)];
+    switch (n.kind) {
+      case MaskNode::kConst: return n.val ? Ivals{{0, Sk}} : Ivals{};
+      case MaskNode::kLeaf: {
+        // c0 + ci*i + cj*j >= 0
+        const int64_t ci = n.aff.c.size() > 2 ? n.aff.c[2] : 0, cj = n.aff.c.size() > 3 ? n.aff.c[3] : 0;
+        const int64_t base = n.aff.c0 + ci * i;
+        if (cj == 0) return base >= 0 ? Ivals{{0, Sk}} : Ivals{};
+        if (cj > 0) {  // j >= ceil(-base / cj)
+          const int64_t lo = -FloorDiv(base, cj);
+          return IvUnion({{std::max<int64_t>(lo, 0), Sk}}, {});
         }
-    if (all_true) return 0;
+        const int64_t hi = FloorDiv(base, -cj);  // j <= floor(base / -cj)
+        return IvUnion({{0, std::min<int64_t>(hi + 1, Sk)}}, {});
+      }
+      case MaskNode::kNot: return IvComplement(RowVisible(nodes, n.a, i, Sk), Sk);
+      case MaskNode::kAnd: return IvIntersect(RowVisible(nodes, n.a, i, Sk), RowVisible(nodes, n.b, i, Sk), Sk);
+      case MaskNode::kOr: return IvUnion(RowVisible(nodes, n.a, i, Sk), RowVisible(nodes, n.b, i, Sk));
+      case MaskNode::kXor: {
+        const Ivals x = RowVisible(nodes, n.a, i, Sk), y = RowVisible(nodes, n.b, i, Sk);
+        return IvUnion(IvIntersect(x, IvComplement(y, Sk), Sk), IvIntersect(IvComplement(x, Sk), y, Sk));
+      }
+    }
+    return {};
+  }
+
+  // 1 = causal (key j visible iff j <= i), 0 = all visible, -1 = anything
+  // else.  Exact: every query row (and every (b, h) a dense table varies
+  // over) is checked, never a sample.
+  int ClassifyMask(int mask, int64_t B, int64_t H, int64_t Sq, int64_t Sk) const {
+    const TensorType& mt = m_.types[mask];
+    if (mt.rank() != 4 || mt.dims != std::vector<int64_t>{B, H, Sq, Sk}) return -1;
+    MaskSym s = MaskSymOf(mask);
+    bool causal = true, all = true;
+    if (s.kind == MaskSym::kPred) {
+      for (const auto& n : s.nodes)
+        if (n.kind == MaskNode::kLeaf && ((B > 1 && n.aff.c[0] != 0) || (H > 1 && n.aff.c[1] != 0))) return -1;
+      for (int64_t i = 0; i < Sq && (causal || all); ++i) {
+        const Ivals v = RowVisible(s.nodes, s.root, i, Sk);
+        const Ivals full{{0, Sk}};
+        const Ivals tri{{0, std::min(i + 1, Sk)}};
+        all &= v == full;
+        causal &= v == tri;
+      }
+    } else if (s.kind == MaskSym::kTable) {
+      const Attr& a = *s.table;
+      const bool fl = IsFloat(s.table_dtype);
+      const int64_t nb = s.tstride[0] ? B : 1, nh = s.tstride[1] ? H : 1;
+      for (int64_t b = 0; b < nb; ++b)
+        for (int64_t h = 0; h < nh; ++h)
+          for (int64_t i = 0; i < Sq && (causal || all); ++i)
+            for (int64_t j = 0; j < Sk; ++j) {
+              const int64_t e = s.toff + b * s.tstride[0] + h * s.tstride[1] + i * s.tstride[2] + j * s.tstride[3];
+              double x = fl ? a.fvals.at(size_t(e)) : double(a.ivals.at(size_t(e)));
+              for (DType d : s.conv) x = ConvertScalar(x, d);
+              bool vis = x != 0;
+              if (!s.cmp.empty()) {
+                bool ok;
+                vis = CompareDir(s.cmp, x, s.cmp_val, &ok);
+              }
+              all &= vis;
+              causal &= vis == (j <= i);
+            }
+    } else {
+      return -1;
+    }
+    if (all) return 0;
     return causal ? 1 : -1;
   }
 
@@ -1847,10 +2195,15 @@ class Lowerer {
     const std::string& n = op.name;
     auto res = [&](int k = 0) { return op.results.at(k); };
     if (n == "stablehlo.constant") {
-      Attr a = *op.attr("value");
       const TensorType& t = m_.types[res()];
-      std::string err;
-      if (!ParseDense(a, t, err)) throw err;
+      const Attr* ap = ParsedConst(res());
+      if (!ap) {
+        Attr a = *op.attr("value");
+        std::string err;
+        ParseDense(a, t, err);
+        throw err;
+      }
+      const Attr& a = *ap;
       ValState& s = state_[res()];
       if (a.splat || t.numel() == 1) {
         s.kind = ValState::kScalar;
@@ -2358,6 +2711,9 @@ class Lowerer {
   std::set<const Func*> inlined_once_;
   std::vector<int> producer_, uses_;
   std::vector<std::vector<int>> users_;
+  // constant op index -> its parsed dense value (each constant is parsed
+  // once per Compile, however often the matchers look at it)
+  mutable std::unordered_map<int, std::shared_ptr<Attr>> const_cache_;
   std::vector<ValState> state_;
   std::map<int, Fused> fused_;
   std::set<int> absorbed_;

@@ -339,29 +339,50 @@ def test_sdpa_strided_views(K, D):
     assert np.abs(bf16.from_bf16_bits(o) - want).max() < 2e-3
 
 
-@pytest.mark.parametrize("S", [8192])
+@pytest.mark.parametrize("S", [512, 1024, 2048, 4096, 8192, 16384])
 def test_sdpa_c3_full_size_sampled_rows(K, S):
-    """C3 at its benchmark shape: the kernel runs on all [4,16,S,128]; rows are
-    checked against the oracle on a sample (each row needs only its prefix),
-    row 0 against the closed form O[0] = V[0] exactly."""
+    """C3 at its benchmark shape, every length of the sweep: the kernel runs
+    on all [4,16,S,128].  Row 0 must equal V[0] exactly (a single visible
+    key).  For S <= 2048 every row of every (b,h) is checked against the
+    float64 oracle; above, 8 (b,h) pairs including the last are checked on
+    ~70 rows each (each row needs only its prefix), the last row among them."""
     d = inputs.c3_sdpa(S)
     print(f"case: sdpa C3 full S={S}", flush=True)
     qd, kd, vd = dev_bf16(d["q"]), dev_bf16(d["k"]), dev_bf16(d["v"])
     scale = 1 / math.sqrt(128)
     o = host_bf16(K.sdpa_fwd(qd, kd, vd, scale, True))
     np.testing.assert_array_equal(o[:, :, 0, :], d["v"][:, :, 0, :])
-    rng = np.random.default_rng(10)
-    rows = sorted(set([1, 63, 64, 127, 128, 4095, S - 1] + list(rng.integers(0, S, 24))))
-    for b, h in [(0, 0), (1, 7), (3, 15)]:
+    if S <= 2048:
+        pairs = [(b, h) for b in range(4) for h in range(16)]
+        rows = np.arange(S)
+    else:
+        pairs = [(0, 0), (0, 15), (1, 3), (1, 7), (2, 9), (2, 12), (3, 0), (3, 15)]
+        rng = np.random.default_rng(10 + S)
+        rows = np.array(sorted(set([1, 63, 64, 127, 128, 255, 256, S // 2 - 1, S // 2, S - 2, S - 1] +
+                                   list(rng.integers(0, S, 60)))))
+    worst = 0.0
+    for b, h in pairs:
         qf = bf16.from_bf16_bits(d["q"][b, h]).astype(np.float64)
         kf = bf16.from_bf16_bits(d["k"][b, h]).astype(np.float64)
         vf = bf16.from_bf16_bits(d["v"][b, h]).astype(np.float64)
-        for i in rows:
-            s = kf[: i + 1] @ qf[i] * scale
-            p = np.exp(s - s.max())
-            want = (p @ vf[: i + 1]) / p.sum()
-            got = bf16.from_bf16_bits(o[b, h, i]).astype(np.float64)
-            assert np.abs(got - want).max() < 2e-3, (b, h, i)
+        for r0 in range(0, len(rows), 256):
+            rr = rows[r0:r0 + 256]
+            kmax = int(rr.max()) + 1
+            sc = (qf[rr] @ kf[:kmax].T) * scale
+            sc[np.arange(kmax)[None, :] > rr[:, None]] = -np.inf
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            want = (p @ vf[:kmax]) / p.sum(axis=1, keepdims=True)
+            # the kernel multiplies bf16-rounded probabilities (relative
+            # error <= 2^-9 each, so the normalised weights move by <= 2^-8
+            # of themselves) and rounds O to bf16 (<= 2^-9 relative)
+            wabs = (p @ np.abs(vf[:kmax])) / p.sum(axis=1, keepdims=True)
+            got = bf16.from_bf16_bits(o[b, h, rr]).astype(np.float64)
+            e = np.abs(got - want)
+            worst = max(worst, float(e.max()))
+            assert e.max() <= 2e-2, (b, h, e.max())        # north_star bar
+            bad = e > 2.0 ** -8 * wabs + 2.0 ** -9 * np.abs(want) + 1e-6
+            assert not bad.any(), (b, h, rr[np.nonzero(bad)[0][:5]], e[bad][:5])
+    print(f"case: sdpa C3 full S={S} max abs err {worst:.2e} over {len(pairs)} (b,h) x {len(rows)} rows", flush=True)
 
 
 def test_sdpa_prefix_mean_closed_form(K):

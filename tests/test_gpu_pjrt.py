@@ -134,7 +134,7 @@ def test_c2_layernorm_unfused_generic_path(client):
     assert np.all(np.abs(got - want) <= ulp + 1e-5 * scale)
 
 
-@pytest.mark.parametrize("S,causal", [(512, True), (512, False), (2048, True)])
+@pytest.mark.parametrize("S,causal", [(512, True), (512, False), (1024, True), (2048, True), (4096, True)])
 def test_c3_sdpa_fused(client, S, causal):
     d = inputs.c3_sdpa(S)
     print(f"case: pjrt C3 sdpa S={S} causal={causal}", flush=True)
