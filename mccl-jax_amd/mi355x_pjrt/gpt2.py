@@ -164,6 +164,11 @@ class GPT2TrainStep:
         self.m = torch.zeros(off, **f32)
         self.v = torch.zeros(off, **f32)
         self.hyper = torch.zeros(3, **f32)  # lr, bc1, bc2 of the current step (device scalars)
+        # pinned staging for those scalars: a ring, so a step's upload never
+        # waits for the stream (a buffer is reused only after the copy that
+        # last read it has run, four steps back)
+        self._hyper_host = [torch.zeros(3, dtype=torch.float32, pin_memory=True) for _ in range(4)]
+        self._hyper_done = [None] * 4
         self.graph = None
         self.load(params if params is not None else init_params(cfg, seed))
         self._alloc()
@@ -379,8 +384,16 @@ class GPT2TrainStep:
         double and rounded to fp32: temp/dp_train.py:91-95) to the device."""
         self.t = self.t + 1 if t is None else t
         bc1, bc2 = 1 - self.b1 ** self.t, 1 - self.b2 ** self.t
+        k = self.t % len(self._hyper_host)
+        if self._hyper_done[k] is not None:
+            self._hyper_done[k].synchronize()
+        host = self._hyper_host[k]
+        host[0], host[1], host[2] = self.lr, bc1, bc2
         with torch.cuda.stream(self.stream):
-            self.hyper.copy_(torch.tensor([self.lr, bc1, bc2], dtype=torch.float32))
+            self.hyper.copy_(host, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+        self._hyper_done[k] = ev
 
     def _adam_launch(self):
         rc = self.lib.mk_adam_update_dev(_P(self.stream.cuda_stream), self.n_flat, BF16, _P(self.param.data_ptr()),

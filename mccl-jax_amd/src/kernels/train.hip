@@ -1166,8 +1166,13 @@ extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t 
   if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent: null pointer");
   hipStream_t s = as_stream(stream);
   const dim3 g{unsigned(rows)}, b{unsigned(kBlock)};
-  // bf16 rows of up to 64K columns: the register-resident kernel
-  if (io_type == MK_BF16 && cols <= int64_t(kXentThreads) * 8 * 16) {
+  // bf16 rows of up to 64K columns: the register-resident kernel.  It takes
+  // the unaligned head of a row from the logits' 16-byte phase and stores
+  // dlogits with 16-byte vectors at the same offsets, so both must share
+  // that phase; otherwise the element-wise kernel below runs.
+  const bool same_phase =
+      ((reinterpret_cast<uintptr_t>(logits) ^ reinterpret_cast<uintptr_t>(dlogits)) & 15u) == 0;
+  if (io_type == MK_BF16 && same_phase && cols <= int64_t(kXentThreads) * 8 * 16) {
     const int64_t nvt = (cols / 8 + kXentThreads - 1) / kXentThreads;  // vectors per thread (bound)
     auto launch = [&](auto nt, auto ltag) {
       constexpr int NVT = decltype(nt)::value;

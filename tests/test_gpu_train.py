@@ -357,6 +357,29 @@ def test_softmax_xent_bf16_shapes(K, rows, cols):
     np.testing.assert_allclose(_f64(dl), want_grad, rtol=2 ** -7, atol=1e-30)
 
 
+def test_softmax_xent_bf16_dlogits_offset_view(K):
+    """dlogits in a different 16-byte phase from logits (an offset view):
+    the launcher must not use the register-resident kernel's vector stores,
+    whose offsets follow the logits' phase."""
+    g = torch.Generator().manual_seed(11)
+    rows, cols = 6, 4099
+    x = (torch.randn(rows, cols, generator=g) * 3).bfloat16()
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int32)
+    buf = torch.zeros(rows * cols + 8, dtype=torch.bfloat16, device="cuda")
+    for off in (1, 3):
+        buf.zero_()
+        xd = x.cuda()
+        dl = buf[off:off + rows * cols].view(rows, cols)
+        assert (dl.data_ptr() - xd.data_ptr()) % 16 != 0
+        loss, dl = K.softmax_xent(xd, lab.cuda(), 1.0 / rows, dlogits=dl)
+        xr = x.double().requires_grad_(True)
+        ref = torch.nn.functional.cross_entropy(xr, lab.long(), reduction="none")
+        ref.mean().backward()
+        np.testing.assert_allclose(_f64(loss), _f64(ref), rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(_f64(dl), _f64(xr.grad), rtol=2 ** -7, atol=1e-30)
+        assert float(buf[:off].abs().sum()) == 0.0 and float(buf[off + rows * cols:].abs().sum()) == 0.0
+
+
 # ------------------------------------------------------------------ Adam
 def _adam_ref(p, g, m, v, lr, b1, b2, eps, bc1, bc2):
     m = b1 * m + (1 - b1) * g
