@@ -145,7 +145,38 @@ A = {
         ("executable", _P), ("output_types", _P), ("num_output_types", _SZ)]),
     "Executable_OutputDimensions": _args("ExecutableOutputDimensions", [
         ("executable", _P), ("num_outputs", _SZ), ("dims", _P), ("dim_sizes", _P)]),
+    "Plugin_Attributes": _args("PluginAttributes", [("attributes", _P), ("num_attributes", _SZ)]),
+    "DeviceDescription_Attributes": _args("DescAttributes", [("device_description", _P),
+                                                             ("num_attributes", _SZ), ("attributes", _P)]),
+    "DeviceDescription_ToString": _args("DescToString", [("device_description", _P), ("to_string", _P),
+                                                         ("to_string_size", _SZ)]),
+    "Executable_Serialize": _args("ExecutableSerialize", [
+        ("executable", _P), ("serialized_bytes", _P), ("serialized_bytes_size", _SZ),
+        ("serialized_executable", _P), ("serialized_executable_deleter", _c.CFUNCTYPE(None, _P))]),
+    "Executable_DeserializeAndLoad": _args("ExecutableDeserializeAndLoad", [
+        ("client", _P), ("serialized_executable", _P), ("serialized_executable_size", _SZ),
+        ("loaded_executable", _P)]),
+    "Event_OnReady": _args("EventOnReady", [("event", _P), ("callback", _P), ("user_arg", _P)]),
 }
+
+
+def named_values(ptr, n) -> dict:
+    """Decode a PJRT_NamedValue array into {name: value}."""
+    out = {}
+    for i in range(n):
+        v = NamedValue.from_address(ptr + i * _c.sizeof(NamedValue))
+        name = _c.string_at(v.name, v.name_size).decode()
+        if v.type == 0:  # kString
+            out[name] = _c.string_at(v.value, v.value_size).decode()
+        elif v.type == 1:  # kInt64
+            out[name] = int(v.value)
+        elif v.type == 2:  # kInt64List
+            out[name] = list((_c.c_int64 * v.value_size).from_address(v.value)) if v.value_size else []
+        elif v.type == 4:  # kBool
+            out[name] = bool(v.value & 0xFF)
+        else:
+            out[name] = v.value
+    return out
 
 
 class PjrtError(RuntimeError):
@@ -213,6 +244,21 @@ class Plugin:
         self._fn("Error_Destroy")(_c.addressof(d))
         return PjrtError(code, msg)
 
+    def event_ready(self, ev) -> bool:
+        return bool(self.call("Event_IsReady", event=ev).is_ready)
+
+    def on_ready(self, ev, fn):
+        """Register fn(error_or_None) with PJRT_Event_OnReady; returns the
+        ctypes callback, which the caller keeps alive until it has fired."""
+        proto = _c.CFUNCTYPE(None, _P, _P)
+
+        def trampoline(err, _user):
+            fn(self._error(err) if err else None)
+
+        cb = proto(trampoline)
+        self.call("Event_OnReady", event=ev, callback=_c.cast(cb, _P), user_arg=None)
+        return cb
+
     def await_event(self, ev):
         if not ev:
             return
@@ -220,6 +266,10 @@ class Plugin:
             self.call("Event_Await", event=ev)
         finally:
             self.call("Event_Destroy", event=ev)
+
+    def attributes(self) -> dict:
+        a = self.call("Plugin_Attributes")
+        return named_values(a.attributes, a.num_attributes)
 
     def client(self, options: dict | None = None) -> "Client":
         opts = options or {}
@@ -269,6 +319,23 @@ class Client:
         k = self.p.call("DeviceDescription_Kind", device_description=d.device_description)
         return _c.string_at(k.device_kind, k.device_kind_size).decode()
 
+    def device_attributes(self, dev) -> dict:
+        d = self.p.call("Device_GetDescription", device=dev)
+        a = self.p.call("DeviceDescription_Attributes", device_description=d.device_description)
+        return named_values(a.attributes, a.num_attributes)
+
+    def device_string(self, dev) -> str:
+        d = self.p.call("Device_GetDescription", device=dev)
+        t = self.p.call("DeviceDescription_ToString", device_description=d.device_description)
+        return _c.string_at(t.to_string, t.to_string_size).decode()
+
+    def deserialize(self, blob: bytes) -> "Executable":
+        """PJRT_Executable_DeserializeAndLoad of bytes from Executable.serialize()."""
+        buf = _c.create_string_buffer(blob, len(blob))
+        a = self.p.call("Executable_DeserializeAndLoad", client=self.h, serialized_executable=_c.addressof(buf),
+                        serialized_executable_size=len(blob))
+        return Executable(self, a.loaded_executable)
+
     def compile(self, text: str | bytes) -> "Executable":
         code = text.encode() if isinstance(text, str) else bytes(text)
         buf = _c.create_string_buffer(code, len(code))
@@ -311,13 +378,22 @@ class Buffer:
         a = self.c.p.call("Buffer_ReadyEvent", buffer=self.h)
         self.c.p.await_event(a.event)
 
-    def to_numpy(self) -> np.ndarray:
+    def to_numpy_async(self):
+        """Start PJRT_Buffer_ToHostBuffer; returns (array, event).  The array
+        holds the data once the event is ready."""
         dt = _PJRT_TO_NP[self.type]
         out = np.empty(self.shape, dtype=dt)
         a = self.c.p.call("Buffer_ToHostBuffer", src=self.h, host_layout=None, dst=out.ctypes.data,
                           dst_size=out.nbytes)
-        self.c.p.await_event(a.event)
+        return out, a.event
+
+    def to_numpy(self) -> np.ndarray:
+        out, ev = self.to_numpy_async()
+        self.c.p.await_event(ev)
         return out
+
+    def ready_event(self):
+        return self.c.p.call("Buffer_ReadyEvent", buffer=self.h).event
 
     def delete(self):
         self.c.p.call("Buffer_Delete", buffer=self.h)
@@ -375,7 +451,8 @@ class Executable:
 
     def execute(self, args, wait=True, non_donatable=None):
         """Run on one device; inputs the program aliases to outputs are
-        donated unless listed in non_donatable."""
+        donated unless listed in non_donatable.  wait=True awaits the
+        completion event, False drops it, "event" returns (outputs, event)."""
         n = self.num_outputs
         opts = None
         if non_donatable is not None:
@@ -394,11 +471,20 @@ class Executable:
                       argument_lists=_c.addressof(arg_lists), num_devices=1, num_args=len(args),
                       output_lists=_c.addressof(out_lists), device_complete_events=_c.addressof(events),
                       execute_device=None)
+        outs = [Buffer(self.c, out_arr[i]) for i in range(n)]
+        if wait == "event":
+            return outs, events[0]
         if wait:
             self.c.p.await_event(events[0])
         else:
             self.c.p.call("Event_Destroy", event=events[0])
-        return [Buffer(self.c, out_arr[i]) for i in range(n)]
+        return outs
+
+    def serialize(self) -> bytes:
+        a = self.c.p.call("Executable_Serialize", executable=self.e)
+        blob = _c.string_at(a.serialized_bytes, a.serialized_bytes_size)
+        a.serialized_executable_deleter(a.serialized_executable)
+        return blob
 
     def delete(self):
         self.c.p.call("LoadedExecutable_Delete", executable=self.h)

@@ -1,5 +1,8 @@
 #include "execution/device.h"
 
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
 #include <memory>
 
 namespace mi::exec {
@@ -53,19 +56,33 @@ DeviceContext* DeviceContext::Get(int ordinal, std::string* error) {
   return v[ordinal].get();
 }
 
-bool DeviceContext::Init(std::string* error) {
-  if (!UseDevice(ordinal_, error)) return false;
+bool DeviceContext::Probe(int ordinal, GpuProps* out, std::string* error) {
   hipDeviceProp_t prop;
-  hipError_t e = hipGetDeviceProperties(&prop, ordinal_);
+  hipError_t e = hipGetDeviceProperties(&prop, ordinal);
   if (e != hipSuccess) {
+    (void)hipGetLastError();
     if (error) *error = HipMsg("hipGetDeviceProperties", e);
     return false;
   }
-  name_ = prop.gcnArchName;
-  cus_ = prop.multiProcessorCount;
-  stats_.bytes_limit = int64_t(prop.totalGlobalMem);
+  out->arch = prop.gcnArchName;
+  out->name = prop.name;
+  out->compute_units = prop.multiProcessorCount;
+  out->hbm_bytes = int64_t(prop.totalGlobalMem);
+  out->clock_khz = prop.clockRate;
+  char bus[32];
+  snprintf(bus, sizeof(bus), "%04x:%02x:%02x.0", unsigned(prop.pciDomainID), unsigned(prop.pciBusID),
+           unsigned(prop.pciDeviceID));
+  out->pci_bus_id = bus;
+  return true;
+}
+
+bool DeviceContext::Init(std::string* error) {
+  if (!UseDevice(ordinal_, error)) return false;
+  if (!Probe(ordinal_, &props_, error)) return false;
+  stats_.bytes_limit = props_.hbm_bytes;
   // default priority, non-blocking with respect to the legacy null stream
-  e = hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking);
+  hipError_t e = hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&upload_, hipStreamNonBlocking);
   if (e != hipSuccess) {
     if (error) *error = HipMsg("hipStreamCreate", e);
     return false;
@@ -142,6 +159,7 @@ void DeviceContext::Trim() {
   }
   if (release.empty()) return;
   (void)UseDevice(ordinal_, nullptr);
+  (void)hipStreamSynchronize(upload_);
   (void)hipStreamSynchronize(stream_);
   for (void* p : release) (void)hipFree(p);
 }
@@ -151,13 +169,118 @@ MemoryStats DeviceContext::Stats() {
   return stats_;
 }
 
-bool DeviceContext::CopyToDevice(void* dst, const void* src, size_t bytes, std::string* error) {
-  if (bytes == 0) return true;
-  (void)UseDevice(ordinal_, nullptr);
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream_);
-  if (e == hipSuccess) e = hipStreamSynchronize(stream_);
+namespace {
+constexpr size_t kStagePiece = size_t(8) << 20;       // upload staging granule
+constexpr size_t kPinnedCacheBytes = size_t(512) << 20;  // cached idle pinned chunks
+constexpr size_t kPinnedBusyBytes = size_t(1) << 30;   // in-flight staging before waiting
+}  // namespace
+
+void DeviceContext::ReapPinnedLocked() {
+  // busy chunks retire in stream order: stop at the first still in flight
+  while (!pin_busy_.empty()) {
+    Busy& b = pin_busy_.front();
+    hipError_t q = hipEventQuery(b.until);
+    if (q == hipErrorNotReady) break;
+    (void)hipEventDestroy(b.until);
+    const size_t cls = pin_size_[b.p];
+    if (pin_cached_ + cls <= kPinnedCacheBytes) {
+      pin_free_.emplace(cls, b.p);
+      pin_cached_ += cls;
+    } else {
+      pin_size_.erase(b.p);
+      (void)hipHostFree(b.p);
+    }
+    pin_busy_.pop_front();
+  }
+}
+
+void* DeviceContext::TakePinned(size_t bytes, std::string* error) {
+  const size_t cls = SizeClass(bytes ? bytes : 1);
+  std::lock_guard<std::mutex> lk(pin_mu_);
+  ReapPinnedLocked();
+  auto it = pin_free_.find(cls);
+  if (it != pin_free_.end()) {
+    void* p = it->second;
+    pin_free_.erase(it);
+    pin_cached_ -= cls;
+    return p;
+  }
+  size_t busy = 0;
+  for (const Busy& b : pin_busy_) busy += pin_size_[b.p];
+  while (busy > kPinnedBusyBytes && !pin_busy_.empty()) {  // bound the staging in flight
+    (void)hipEventSynchronize(pin_busy_.front().until);
+    busy -= pin_size_[pin_busy_.front().p];
+    ReapPinnedLocked();
+  }
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, cls, hipHostMallocDefault);
   if (e != hipSuccess) {
-    if (error) *error = HipMsg("host-to-device copy", e);
+    (void)hipGetLastError();
+    if (error) *error = HipMsg("hipHostMalloc", e);
+    return nullptr;
+  }
+  pin_size_[p] = cls;
+  return p;
+}
+
+void DeviceContext::ReturnPinned(void* p, hipEvent_t busy_until) {
+  if (!p) return;
+  std::lock_guard<std::mutex> lk(pin_mu_);
+  if (busy_until) {
+    pin_busy_.push_back({p, busy_until});
+    return;
+  }
+  const size_t cls = pin_size_[p];
+  if (pin_cached_ + cls <= kPinnedCacheBytes) {
+    pin_free_.emplace(cls, p);
+    pin_cached_ += cls;
+  } else {
+    pin_size_.erase(p);
+    (void)hipHostFree(p);
+  }
+}
+
+hipEvent_t DeviceContext::Upload(void* dst, const void* src, size_t bytes, std::string* error) {
+  if (!UseDevice(ordinal_, error)) return nullptr;
+  std::lock_guard<std::mutex> lk(upload_mu_);
+  for (size_t off = 0; off < bytes;) {
+    const size_t n = std::min(kStagePiece, bytes - off);
+    void* chunk = TakePinned(n, error);
+    if (!chunk) return nullptr;
+    memcpy(chunk, static_cast<const char*>(src) + off, n);
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipMemcpyAsync(static_cast<char*>(dst) + off, chunk, n, hipMemcpyHostToDevice, upload_);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ev, upload_);
+    if (e != hipSuccess) {
+      if (error) *error = HipMsg("host-to-device copy", e);
+      (void)hipStreamSynchronize(upload_);
+      if (ev) (void)hipEventDestroy(ev);
+      ReturnPinned(chunk, nullptr);
+      return nullptr;
+    }
+    ReturnPinned(chunk, ev);  // the staging pool owns `ev` from here
+    off += n;
+  }
+  hipEvent_t done = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(done, upload_);
+  if (e != hipSuccess) {
+    if (error) *error = HipMsg("hipEventRecord", e);
+    if (done) (void)hipEventDestroy(done);
+    return nullptr;
+  }
+  return done;
+}
+
+bool DeviceContext::UploadForCompute(void* dst, const void* src, size_t bytes, std::string* error) {
+  if (bytes == 0) return true;
+  hipEvent_t done = Upload(dst, src, bytes, error);
+  if (!done) return false;
+  hipError_t e = hipStreamWaitEvent(stream_, done, 0);
+  (void)hipEventDestroy(done);  // the wait keeps what it needs
+  if (e != hipSuccess) {
+    if (error) *error = HipMsg("hipStreamWaitEvent", e);
     return false;
   }
   return true;

@@ -1,21 +1,29 @@
-// HIP device context: one stream and one HBM caching allocator per GPU.
+// HIP device context: the streams, the HBM caching allocator and the pinned
+// staging memory of one GPU.
 //
 // Replaces src/execution/metal_buffer.{h,mm} (shared-storage MTLBuffer
 // allocation, metal_buffer.mm:13-29) and the size-exact BufferPool of
 // src/jam/jam_run.mm:74-112.  Differences by design:
 //  - memory is device HBM (hipMalloc), not CPU-visible unified memory;
-//  - every launch and copy of the plugin goes to the context's single
+//  - kernels, device-to-device and device-to-host copies go to the compute
 //    stream, so a block returned to the pool can be handed out again at once:
 //    any later use is ordered after the earlier use on that stream;
+//  - host-to-device uploads go to a second (transfer) stream, so they never
+//    wait for kernels already queued.  Data is first copied into pinned
+//    staging chunks on the calling thread, then DMA'd; the caller gets the
+//    hipEvent that marks the end of the DMA and makes whichever stream reads
+//    the data wait for it (hipStreamWaitEvent);
 //  - blocks are rounded to size classes (256 B granularity below 1 MiB,
 //    then 1/8-power-of-two steps) so near-equal sizes share free lists;
 //  - hipFree is only called on trim (allocation failure) or process exit.
+// Both streams have the default priority.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
 
 #include <cstddef>
 #include <cstdint>
+#include <deque>
 #include <map>
 #include <mutex>
 #include <string>
@@ -32,17 +40,31 @@ struct MemoryStats {
   int64_t bytes_limit = 0;     // total device memory
 };
 
+// What hipGetDeviceProperties reports about a GPU, kept for descriptions.
+struct GpuProps {
+  std::string arch;         // gcnArchName, e.g. "gfx950:sramecc+:xnack-"
+  std::string name;         // marketing name
+  std::string pci_bus_id;   // "0000:05:00.0"
+  int compute_units = 0;
+  int64_t hbm_bytes = 0;
+  int clock_khz = 0;
+};
+
 class DeviceContext {
  public:
   // Returns the context of HIP device `ordinal`, creating it on first use;
   // nullptr (and *error) when the device cannot be opened.
   static DeviceContext* Get(int ordinal, std::string* error);
   static int DeviceCount();
+  // Properties of device `ordinal` without opening a context (no streams).
+  static bool Probe(int ordinal, GpuProps* out, std::string* error);
 
   int ordinal() const { return ordinal_; }
-  hipStream_t stream() const { return stream_; }
-  const std::string& name() const { return name_; }
-  int compute_units() const { return cus_; }
+  hipStream_t stream() const { return stream_; }            // compute stream
+  hipStream_t transfer_stream() const { return upload_; }   // host-to-device stream
+  const GpuProps& props() const { return props_; }
+  const std::string& name() const { return props_.arch; }
+  int compute_units() const { return props_.compute_units; }
 
   // Stream-ordered allocation (see file comment).  Alloc(0) returns nullptr.
   void* Alloc(size_t bytes, std::string* error);
@@ -50,8 +72,19 @@ class DeviceContext {
   MemoryStats Stats();
   void Trim();  // release every cached block back to HIP
 
-  // Host <-> device copies on the context stream.
-  bool CopyToDevice(void* dst, const void* src, size_t bytes, std::string* error);  // blocks until done
+  // Host -> HBM without waiting for the compute stream (see file comment).
+  // Returns an event recorded on the transfer stream after the last byte
+  // landed (the caller destroys it), or nullptr and *error.  The host source
+  // may be reused as soon as this returns.
+  hipEvent_t Upload(void* dst, const void* src, size_t bytes, std::string* error);
+  // Upload, then order the compute stream after it (no host wait).
+  bool UploadForCompute(void* dst, const void* src, size_t bytes, std::string* error);
+
+  // Pinned host chunks for staging.  ReturnPinned(p, ev) puts p back once
+  // the GPU has passed `ev` (nullptr: at once).
+  void* TakePinned(size_t bytes, std::string* error);
+  void ReturnPinned(void* p, hipEvent_t busy_until);
+
   bool CopyToHostAsync(void* dst, const void* src, size_t bytes, std::string* error);
   bool CopyDeviceToDevice(void* dst, const void* src, size_t bytes, std::string* error);
   bool Synchronize(std::string* error);
@@ -60,15 +93,28 @@ class DeviceContext {
   explicit DeviceContext(int ordinal) : ordinal_(ordinal) {}
   bool Init(std::string* error);
   static size_t SizeClass(size_t bytes);
+  void ReapPinnedLocked();
 
   int ordinal_;
   hipStream_t stream_ = nullptr;
-  std::string name_;
-  int cus_ = 0;
+  hipStream_t upload_ = nullptr;
+  GpuProps props_;
   std::mutex mu_;
   std::multimap<size_t, void*> free_;   // size class -> cached block
   std::map<void*, size_t> live_;        // block -> size class
   MemoryStats stats_;
+
+  // pinned staging
+  std::mutex pin_mu_;
+  std::mutex upload_mu_;  // one upload at a time keeps chunk order simple
+  std::multimap<size_t, void*> pin_free_;
+  std::map<void*, size_t> pin_size_;
+  struct Busy {
+    void* p;
+    hipEvent_t until;
+  };
+  std::deque<Busy> pin_busy_;
+  size_t pin_cached_ = 0;
 };
 
 // Sets the calling thread's current HIP device.

@@ -17,7 +17,7 @@ std::vector<void*>* Program::DeviceConsts(int ordinal) {
   for (size_t i = v.size(); i < consts.size(); ++i) {
     void* p = dev->Alloc(consts[i].bytes.size(), &err);
     if (!p && !consts[i].bytes.empty()) return nullptr;
-    if (!dev->CopyToDevice(p, consts[i].bytes.data(), consts[i].bytes.size(), &err)) return nullptr;
+    if (!dev->UploadForCompute(p, consts[i].bytes.data(), consts[i].bytes.size(), &err)) return nullptr;
     v.push_back(p);
   }
   return &v;

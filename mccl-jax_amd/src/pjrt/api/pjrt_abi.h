@@ -338,16 +338,24 @@ MI_ARGS(PJRT_TopologyDescription_GetDeviceDescriptions_Args, PJRT_TopologyDescri
 MI_ARGS(PJRT_TopologyDescription_Attributes_Args, PJRT_TopologyDescription* topology;
         const PJRT_NamedValue* attributes; size_t num_attributes;)
 
+typedef struct PJRT_SerializedExecutable PJRT_SerializedExecutable;
+MI_ARGS(PJRT_Executable_Serialize_Args, const PJRT_Executable* executable;
+        const char* serialized_bytes; size_t serialized_bytes_size;
+        PJRT_SerializedExecutable* serialized_executable;
+        void (*serialized_executable_deleter)(PJRT_SerializedExecutable* exec);)
+MI_ARGS(PJRT_Executable_DeserializeAndLoad_Args, PJRT_Client* client; const char* serialized_executable;
+        size_t serialized_executable_size; PJRT_LoadedExecutable* loaded_executable;)
+MI_ARGS(PJRT_Compile_Args, const PJRT_TopologyDescription* topology; const PJRT_Program* program;
+        const char* compile_options; size_t compile_options_size; PJRT_Client* client;
+        PJRT_Executable* executable;)
+
 // ---- argument structs of functions answered with UNIMPLEMENTED (layout unused)
-typedef struct PJRT_Executable_Serialize_Args PJRT_Executable_Serialize_Args;
-typedef struct PJRT_Executable_DeserializeAndLoad_Args PJRT_Executable_DeserializeAndLoad_Args;
 typedef struct PJRT_CopyToDeviceStream_Destroy_Args PJRT_CopyToDeviceStream_Destroy_Args;
 typedef struct PJRT_CopyToDeviceStream_AddChunk_Args PJRT_CopyToDeviceStream_AddChunk_Args;
 typedef struct PJRT_CopyToDeviceStream_TotalBytes_Args PJRT_CopyToDeviceStream_TotalBytes_Args;
 typedef struct PJRT_CopyToDeviceStream_GranuleSize_Args PJRT_CopyToDeviceStream_GranuleSize_Args;
 typedef struct PJRT_CopyToDeviceStream_CurrentBytes_Args PJRT_CopyToDeviceStream_CurrentBytes_Args;
 typedef struct PJRT_TopologyDescription_Serialize_Args PJRT_TopologyDescription_Serialize_Args;
-typedef struct PJRT_Compile_Args PJRT_Compile_Args;
 
 // ---- the function table.  MI_PJRT_SLOTS lists the 100 slots in ABI order;
 // V marks the two slots whose functions return void.

@@ -297,3 +297,76 @@ def test_concurrent_execute_from_threads(client):
         for it in range(5):
             np.testing.assert_array_equal(got[t][it], want[t])
     e.destroy()
+
+
+def _queue_long_work(client, reps=24):
+    """Queue about reps x 1.1 ms of attention on the compute stream; returns
+    the executable, its input buffers, the outputs and the last event."""
+    d = inputs.c3_sdpa(8192)
+    e = client.compile(modules.sdpa(4, 16, 8192, 128, True))
+    bufs = [client.put(d[k], pjrt.BF16) for k in ("q", "k", "v")]
+    for b in bufs:
+        b.ready()
+    outs, ev = [], None
+    for _ in range(reps):
+        if ev is not None:
+            client.p.call("Event_Destroy", event=ev)
+        o, ev = e.execute(bufs, wait="event")
+        outs += o
+    return e, bufs, outs, ev
+
+
+def test_upload_does_not_wait_for_queued_kernels(client):
+    """BufferFromHostBuffer with tens of milliseconds of kernels queued: the
+    upload goes to the transfer stream, so its ready event completes while
+    the queued work is still running, and a program reading the uploaded
+    buffer (queued after it) sees its bytes."""
+    import time
+
+    print("case: pjrt async upload behind queued sdpa", flush=True)
+    e, bufs, outs, ev = _queue_long_work(client)
+    x = (np.arange(4 * 8, dtype=np.float32).reshape(4, 8) % 7).astype(np.float32)
+    t0 = time.perf_counter()
+    xb = client.put(bf16.to_bf16_bits(x), pjrt.BF16)  # small integers: exact in bf16
+    put_ms = (time.perf_counter() - t0) * 1e3
+    xb.ready()
+    assert not client.p.event_ready(ev), "the upload waited for the queued kernels"
+    red = client.compile(modules.reduce_sum(4, 8))
+    (y,) = red.execute([xb])
+    np.testing.assert_array_equal(y.to_numpy(), x.sum(-1))
+    client.p.await_event(ev)
+    assert put_ms < 20, put_ms
+    for b in bufs + outs + [xb, y]:
+        b.destroy()
+    e.destroy()
+    red.destroy()
+
+
+def test_download_is_asynchronous_and_callbacks_fire(client):
+    """ToHostBuffer queued behind running kernels returns at once; its event
+    completes later with the right bytes, and PJRT_Event_OnReady callbacks
+    (run by the plugin's watcher thread) fire for both events."""
+    import threading
+
+    print("case: pjrt async download + OnReady", flush=True)
+    e, bufs, outs, ev = _queue_long_work(client)
+    fired = []
+    done = threading.Event()
+
+    def note(err):
+        fired.append(err)
+        if len(fired) == 2:
+            done.set()
+
+    keep = [client.p.on_ready(ev, note)]
+    arr, dev = outs[-1].to_numpy_async()
+    assert not client.p.event_ready(dev), "ToHostBuffer blocked until the kernels finished"
+    keep.append(client.p.on_ready(dev, note))
+    assert done.wait(30), fired
+    assert fired == [None, None]
+    client.p.await_event(dev)
+    client.p.await_event(ev)
+    np.testing.assert_array_equal(arr, outs[0].to_numpy())  # every rep computes the same output
+    for b in bufs + outs:
+        b.destroy()
+    e.destroy()

@@ -143,21 +143,53 @@ def test_unimplemented_slots_and_multinode(plugin, client):
     assert ei.value.code == "UNIMPLEMENTED"
     # a stub slot answers UNIMPLEMENTED with its name
     import ctypes
-    fn = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p)(plugin.slot("Executable_Serialize"))
+    fn = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p)(plugin.slot("CopyToDeviceStream_TotalBytes"))
     err = fn(None)
     e = plugin._error(err)
-    assert e.code == "UNIMPLEMENTED" and "PJRT_Executable_Serialize" in e.message
+    assert e.code == "UNIMPLEMENTED" and "PJRT_CopyToDeviceStream_TotalBytes" in e.message
+    # exactly the copy-to-device-stream group and topology serialization are stubs
+    stubs = [s for s in pjrt.SLOTS
+             if s.startswith("CopyToDeviceStream_") or s == "TopologyDescription_Serialize"]
+    assert len(stubs) == 6
+
+
+def test_plugin_attributes_and_device_description(plugin, client):
+    """PJRT_Plugin_Attributes carries the StableHLO version window a client
+    serializes for; device descriptions carry what HIP reports."""
+    attrs = plugin.attributes()
+    assert attrs["xla_version"] == 2
+    assert attrs["stablehlo_current_version"] == [1, 0, 0]
+    assert attrs["stablehlo_minimum_version"] == [1, 0, 0]
+    dev = client.devices()[0]
+    d = client.device_attributes(dev)
+    assert set(d) == {"gfx_arch", "compute_units", "hbm_bytes", "pci_bus_id"}
+    assert client.device_string(dev).startswith("MI355X#0 (")
+
+
+def test_serialize_round_trip(client):
+    """Executable_Serialize then DeserializeAndLoad gives the same plan and
+    fingerprint; foreign bytes are refused with a named error."""
+    e = client.compile(modules.reduce_sum(4, 8))
+    blob = e.serialize()
+    assert blob.startswith(b"mi355x-jam/1\n") and modules.reduce_sum(4, 8).encode() in blob
+    e2 = client.deserialize(blob)
+    assert e2.plan() == e.plan() and e2.output_shapes() == [(4,)]
+    with pytest.raises(pjrt.PjrtError) as ei:
+        client.deserialize(b"not an executable")
+    assert ei.value.code == "INVALID_ARGUMENT" and "mi355x-pjrt" in ei.value.message
+    e.destroy()
+    e2.destroy()
 
 
 def test_execute_argument_count_checked(client):
     e = client.compile(modules.reduce_sum(4, 8))
     with pytest.raises(pjrt.PjrtError) as ei:
         e.execute([])
-    assert ei.value.code == "INVALID_ARGUMENT" and "expected 1 arguments" in ei.value.message
+    assert ei.value.code == "INVALID_ARGUMENT" and "takes 1 arguments, got 0" in ei.value.message
     e.delete()
     with pytest.raises(pjrt.PjrtError) as ei:
         e.execute([])
-    assert "deleted executable" in ei.value.message
+    assert "executable was deleted" in ei.value.message
     e.destroy()
 
 
