@@ -242,6 +242,23 @@ int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int64_t row_len
                         const void* updates, void* out, void* workspace);
 
 /* ------------------------------------------------------------------------
+ * a11  scatter-add that allocates nothing.  No counterpart in the reference:
+ * it exists for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same contract and same kernels as mk_scatter_add_rows, but the workspace
+ * is a fixed device array of the library, MK_SCATTER_ADD_SCRATCH_BYTES per
+ * GPU, held until the process ends.  Calls whose
+ * mk_scatter_add_workspace_bytes(n_rows, n_ids) exceeds it fail with
+ * MK_ERR_UNSUPPORTED (C4's 65536 ids into 50257 rows need about 1.5 MB).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller.
+ * ---------------------------------------------------------------------- */
+#define MK_SCATTER_ADD_SCRATCH_BYTES (8u << 20)
+int mk_scatter_add_rows_noalloc(void* stream, int dtype, int64_t n_rows, int64_t row_len,
+                                const void* table, int index_type, int64_t n_ids, const void* ids,
+                                const void* updates, void* out);
+
+/* ------------------------------------------------------------------------
  * a6  iota.  Replaces src/jam/ops/shape.mm:249-256 (coordinateAlongAxis +
  * castTensor).  out[idx] = idx[dim] for every index of the row-major shape.
  * out_type ∈ {MK_S32, MK_S64, MK_F32, MK_BF16, MK_U32}.

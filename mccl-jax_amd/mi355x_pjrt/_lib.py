@@ -53,6 +53,7 @@ SIGNATURES = {
     "mk_gather_rows": (_I, [_P, _I64, _I64, _P, _I, _I64, _P, _P]),
     "mk_scatter_add_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "mk_scatter_add_rows": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _P, _P, _P, _P]),
+    "mk_scatter_add_rows_noalloc": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _P, _P, _P]),
     "mk_iota": (_I, [_P, _I, _I, _P, _I, _P]),
     "mk_copy_strided": (_I, [_P, _I, _I, _P, _P, _P, _P]),
     "mk_softmax_rows": (_I, [_P, _I, _I64, _I64, _P, _P]),

@@ -268,6 +268,22 @@ def scatter_add_rows(table, ids, updates, out=None, workspace=None, stream=None)
     return out
 
 
+def scatter_add_rows_noalloc(table, ids, updates, out=None, stream=None):
+    """scatter_add_rows through mk_scatter_add_rows_noalloc: no workspace and
+    no device allocation inside the call (the library's fixed per-GPU
+    scratch array, MK_SCATTER_ADD_SCRATCH_BYTES, is used instead)."""
+    _require_cuda(table, ids, updates)
+    ids_c = ids.contiguous().reshape(-1)
+    n_rows, row_len = table.shape[0], table[0].numel()
+    if out is None:
+        out = torch.empty_like(table)
+    rc = lib().mk_scatter_add_rows_noalloc(_stream(stream), mk_dtype(table.dtype), n_rows, row_len,
+                                           _ptr(table), mk_dtype(ids.dtype), ids_c.numel(), _ptr(ids_c),
+                                           _ptr(updates.contiguous()), _ptr(out))
+    _check(rc, "mk_scatter_add_rows_noalloc")
+    return out
+
+
 # ------------------------------------------------------------------ C5 training step
 def _ws(nbytes, device, workspace):
     if workspace is None:

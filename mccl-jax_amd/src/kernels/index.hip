@@ -15,6 +15,8 @@
 #include "mk_common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 namespace mk {
@@ -440,21 +442,117 @@ extern "C" size_t mk_scatter_add_workspace_bytes(int64_t n_rows, int64_t n_ids) 
          align256(size_t(n_rows) * 8);
 }
 
+namespace mk {
+namespace {
+
+// Validates the arguments shared by both scatter-add entry points; MK_OK
+// means "go on", anything else is returned as is (with *done = true for a
+// valid call that has nothing to do).
+int scatter_check(const char* name, int dtype, int64_t n_rows, int64_t row_len, int index_type, int64_t n_ids,
+                  bool* done) {
+  *done = false;
+  const std::string n(name);
+  if (n_rows < 0 || row_len < 0 || n_ids < 0) return fail(MK_ERR_INVALID, n + ": negative size");
+  if (dtype != MK_F32 && dtype != MK_BF16) return fail(MK_ERR_UNSUPPORTED, n + ": dtype must be f32/bf16");
+  if (index_type != MK_S32 && index_type != MK_S64) return fail(MK_ERR_UNSUPPORTED, n + ": index_type must be s32/s64");
+  if (n_rows >= (int64_t(1) << 31) || n_ids >= (int64_t(1) << 31))
+    return fail(MK_ERR_UNSUPPORTED, n + ": n_rows and n_ids must be < 2^31");
+  *done = n_rows == 0 || row_len == 0;
+  return MK_OK;
+}
+
+// Scratch of the allocation-free scatter-add: one copy per GPU, for the
+// whole process.  Host code never uses this name as an address (on the host
+// it is a stand-in, not device memory): scratch_on() looks up each device's
+// own copy with hipGetSymbolAddress.
+__device__ __align__(256) unsigned char scratch[MK_SCATTER_ADD_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (looked up
+// once per device, with that device current).  nullptr and the error set on
+// failure.
+void* scratch_on(hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    fail(MK_ERR_INVALID, "mk_scatter_add_rows_noalloc: cannot tell the stream's device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  int cur = -1;
+  (void)hipGetDevice(&cur);
+  if (cur != dev) (void)hipSetDevice(dev);
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (cur != dev && cur >= 0) (void)hipSetDevice(cur);
+  if (e != hipSuccess || !p) {
+    (void)hipGetLastError();
+    fail(MK_ERR_LAUNCH, std::string("mk_scatter_add_rows_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  g_scratch_ptr[dev] = p;
+  return p;
+}
+
+int scatter_add_launch(hipStream_t s, int dtype, int64_t n_rows, int64_t row_len, const void* table,
+                       int index_type, int64_t n_ids, const void* ids, const void* updates, void* out,
+                       void* workspace, const char* name);
+
+}  // namespace
+}  // namespace mk
+
 extern "C" int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int64_t row_len,
                                    const void* table, int index_type, int64_t n_ids,
                                    const void* ids, const void* updates, void* out,
                                    void* workspace) {
   clear_error();
-  if (n_rows < 0 || row_len < 0 || n_ids < 0) return fail(MK_ERR_INVALID, "mk_scatter_add_rows: negative size");
-  if (dtype != MK_F32 && dtype != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: dtype must be f32/bf16");
-  if (index_type != MK_S32 && index_type != MK_S64)
-    return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: index_type must be s32/s64");
-  if (n_rows >= (int64_t(1) << 31) || n_ids >= (int64_t(1) << 31))
-    return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows: n_rows and n_ids must be < 2^31");
-  if (n_rows == 0 || row_len == 0) return MK_OK;
+  bool done = false;
+  if (int rc = scatter_check("mk_scatter_add_rows", dtype, n_rows, row_len, index_type, n_ids, &done)) return rc;
+  if (done) return MK_OK;
   if (!table || !out || (n_ids > 0 && (!ids || !updates || !workspace)))
     return fail(MK_ERR_INVALID, "mk_scatter_add_rows: null pointer");
+  return scatter_add_launch(as_stream(stream), dtype, n_rows, row_len, table, index_type, n_ids, ids, updates, out,
+                            workspace, "mk_scatter_add_rows");
+}
+
+extern "C" int mk_scatter_add_rows_noalloc(void* stream, int dtype, int64_t n_rows, int64_t row_len,
+                                           const void* table, int index_type, int64_t n_ids,
+                                           const void* ids, const void* updates, void* out) {
+  clear_error();
+  bool done = false;
+  if (int rc = scatter_check("mk_scatter_add_rows_noalloc", dtype, n_rows, row_len, index_type, n_ids, &done))
+    return rc;
+  if (done) return MK_OK;
+  const size_t need = mk_scatter_add_workspace_bytes(n_rows, n_ids);
+  if (need > size_t(MK_SCATTER_ADD_SCRATCH_BYTES))
+    return fail(MK_ERR_UNSUPPORTED, "mk_scatter_add_rows_noalloc: needs " + std::to_string(need) +
+                                        " bytes of scratch, more than the " +
+                                        std::to_string(size_t(MK_SCATTER_ADD_SCRATCH_BYTES)) +
+                                        " bytes it has; use mk_scatter_add_rows with a workspace");
+  if (!table || !out || (n_ids > 0 && (!ids || !updates)))
+    return fail(MK_ERR_INVALID, "mk_scatter_add_rows_noalloc: null pointer");
   hipStream_t s = as_stream(stream);
+  void* ws = scratch_on(s);
+  if (!ws) return MK_ERR_LAUNCH;
+  return scatter_add_launch(s, dtype, n_rows, row_len, table, index_type, n_ids, ids, updates, out, ws,
+                            "mk_scatter_add_rows_noalloc");
+}
+
+namespace mk {
+namespace {
+
+// Queues the whole scatter-add on `s`.  `workspace` holds at least
+// mk_scatter_add_workspace_bytes(n_rows, n_ids) bytes; every part of it that
+// is read is written first by the same call (the row bounds are cleared by
+// the prepare kernel), so leftovers of an earlier call do not matter.
+int scatter_add_launch(hipStream_t s, int dtype, int64_t n_rows, int64_t row_len, const void* table,
+                       int index_type, int64_t n_ids, const void* ids, const void* updates, void* out,
+                       void* workspace, const char* name) {
   ScatterWs w = carve(workspace, n_rows, n_ids);
   // bounds start at zero (rows without updates have an empty range); the
   // prepare kernel clears them
@@ -500,5 +598,8 @@ extern "C" int mk_scatter_add_rows(void* stream, int dtype, int64_t n_rows, int6
     hipLaunchKernelGGL(scatter_accumulate_kernel<false>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, vec_ok);
   else
     hipLaunchKernelGGL(scatter_accumulate_kernel<true>, g, dim3(kBlock), 0, s, table, out, n_rows, row_len, updates, w.vals0, w.bounds, in_place, false);
-  return check_launch("mk_scatter_add_rows");
+  return check_launch(name);
 }
+
+}  // namespace
+}  // namespace mk
