@@ -13,14 +13,18 @@ fusion GB/s % HBM peak".
              scatter-add, GB/s of algorithmic bytes and fraction of 8 TB/s
   roofline   the dominant kernel (SDPA at S=8192): achieved TFLOP/s from HIP
              events on the launch stream, against 2516.6 TFLOP/s bf16 dense
-  cpu_baseline  the float64 numpy oracle on a bounded sample of (b, h) pairs
-             of the same workload, extrapolated to all pairs
+  cpu_baseline  an fp32 torch-CPU restatement (not XLA:CPU; jax is absent)
+             on a bounded sample of (b, h) pairs of the same workload, scaled
+             to all pairs, with the thread count
+  pjrt_execute  the same attention through PJRT_LoadedExecutable_Execute
+             (the plugin path), and the per-Execute cost of a tiny module
   training_step  config C5: one GPT-2-small training step (forward, backward,
              Adam; 12 layers, d 768, 12 heads, seq 1024, batch 8, vocab
              50257, bf16 activations, fp32 Adam) replayed as one HIP graph;
              ms/step, tokens/s, model TFLOP/s (3x forward FLOPs) and MFU
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS] [--only sdpa|fusions|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS]
+       [--only sdpa|fusions|headline|calib|c5|gemm|pjrt]
 
 Before the first timed region the headline kernel runs untimed for --spinup
 seconds (default 1), so that no timed region includes the clocks' ramp from
@@ -55,7 +59,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--spinup", type=float, default=1.0,
                     help="seconds of untimed headline launches before anything is timed (clocks settle)")
-    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5"], default=None)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5", "gemm", "pjrt"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -118,42 +122,44 @@ def read_traffic(name):
     return None
 
 
-def cpu_baseline_sdpa(np, S, budget_s):
-    """The oracle (float64 numpy) on (b, h) pairs of the C3 workload until the
-    time budget is used, extrapolated to all B*H = 64 pairs."""
-    from oracle import bf16, inputs, ops
+def cpu_baseline_sdpa(torch, np, S, budget_s, gpu_out=None):
+    """CPU baseline: an fp32 torch-CPU restatement of the jitted computation
+    (einsum -> scale -> where(tril) -> softmax -> einsum, as BASELINE.md's
+    fallback plan specifies when jax is absent; it is NOT XLA:CPU) on (b, h)
+    pairs of the C3 workload until the time budget is used, then scaled to
+    all B*H = 64 pairs.  torch uses every core of this process's affinity
+    mask.  The first pair is compared with the GPU result (gpu_out)."""
+    from oracle import bf16, inputs
 
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-        cores = len(os.sched_getaffinity(0))
-        limiter = threadpool_limits(limits=cores)
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        limiter, threads = None, 1
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     d = inputs.c3_sdpa(S)
     B, H, D = 4, 16, 128
     scale = 1 / math.sqrt(D)
-    done = 0
+    mask = torch.ones(S, S, dtype=torch.bool).tril_()
+    done, err = 0, None
     t0 = time.perf_counter()
     for bh in range(B * H):
         b, h = divmod(bh, H)
-        q, k, v = (bf16.from_bf16_bits(d[n][b, h]) for n in ("q", "k", "v"))
-        ops.sdpa(q, k, v, scale, causal=True)
+        q, k, v = (torch.from_numpy(bf16.from_bf16_bits(d[n][b, h]).astype(np.float32)) for n in ("q", "k", "v"))
+        s_ = (q @ k.T) * scale
+        s_ = torch.where(mask, s_, torch.tensor(float("-inf")))
+        o = torch.softmax(s_, dim=-1) @ v
+        if bh == 0 and gpu_out is not None:
+            err = float((o - gpu_out[b, h].float().cpu()).abs().max())
         done += 1
         if time.perf_counter() - t0 > budget_s:
             break
     el = time.perf_counter() - t0
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
-    per_pair = el / done
-    total_s = per_pair * B * H
+    total_s = el / done * B * H
     return {
         "value": round(sdpa_flops(B, H, S, D) / total_s / 1e12, 5),
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": int(cores),
         "kind": "port",
-        "sample": f"float64 numpy oracle (ops.sdpa) on {done} of {B*H} (b,h) pairs at S={S}, "
-                  f"{el:.1f}s, extrapolated x{B*H/done:.1f}; BLAS threads={threads}",
+        "sample": f"CPU restatement, not XLA:CPU: fp32 torch-CPU einsum/where(tril)/softmax/einsum on {done} of "
+                  f"{B*H} (b,h) pairs at S={S}, {el:.1f}s, extrapolated x{B*H/done:.1f}; torch threads={cores}"
+                  + (f"; max |CPU - GPU| on pair (0,0) = {err:.2e}" if err is not None else ""),
     }
 
 
@@ -176,7 +182,7 @@ def run_sdpa(torch, np, K, args):
         sweep[str(S)] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
         log(f"sdpa S={S}: {ms:.3f} ms  {tf:.1f} TFLOP/s  ({100*tf/PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
         if S == args.seq:
-            head = (ms, tf, steps)
+            head = (ms, tf, steps, o[0:1].clone())
         del q, k, v, o
         torch.cuda.empty_cache()
     return sweep, head
@@ -218,6 +224,113 @@ def run_fusions(torch, np, K, args):
     rec("scatter_add_65536x768_into_50257x768_f32", 65536 * 768 * 4 + 65536 * 4 + 2 * 50257 * 768 * 4,
         lambda: K.scatter_add_rows(tf, idf, gr, out=out, workspace=ws))
     return res
+
+
+# The GEMMs of one C5 step: (tag, out dtype, M, N, K, A layout, B layout).
+# Layout "rm" = row-major [rows, cols] view, "t" = transposed view of the
+# row-major [cols, rows] tensor (a unit stride along the other dimension).
+C5_GEMMS = [
+    ("qkv", "bf16", 8192, 2304, 768, "rm", "rm"), ("o", "bf16", 8192, 768, 768, "rm", "rm"),
+    ("fc", "bf16", 8192, 3072, 768, "rm", "rm"), ("proj", "bf16", 8192, 768, 3072, "rm", "rm"),
+    ("logits", "bf16", 8192, 50257, 768, "rm", "t"), ("dhf", "bf16", 8192, 768, 50257, "rm", "rm"),
+    ("dwte", "f32", 50257, 768, 8192, "t", "rm"), ("dw_pr", "f32", 3072, 768, 8192, "t", "rm"),
+    ("dg", "bf16", 8192, 3072, 768, "rm", "t"), ("dw_fc", "f32", 768, 3072, 8192, "t", "rm"),
+    ("dh2", "bf16", 8192, 768, 3072, "rm", "t"), ("dw_o", "f32", 768, 768, 8192, "t", "rm"),
+    ("datt", "bf16", 8192, 768, 768, "rm", "t"), ("dw_qkv", "f32", 768, 2304, 8192, "t", "rm"),
+    ("dh", "bf16", 8192, 768, 2304, "rm", "t"),
+]
+
+
+def run_gemm(torch, np, K, args):
+    """mk_gemm (hand-written MFMA) and mk_gemm_blas (rocBLAS) on the C5 step's
+    15 GEMM shapes, and C1's two fp32 GEMMs (bias + ReLU, bias epilogues) on
+    mk_gemm; TFLOP/s against the bf16 (2516.6) or fp32 (157.3) peak."""
+    from oracle import inputs
+
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(0)
+
+    def mat(rows, cols, layout, dt):
+        if layout == "rm":
+            return torch.randn(rows, cols, device="cuda", generator=g).to(dt)
+        return torch.randn(cols, rows, device="cuda", generator=g).to(dt).t()
+
+    for tag, od, M, N, Kd, la, lb in C5_GEMMS:
+        a, b = mat(M, Kd, la, torch.bfloat16), mat(Kd, N, lb, torch.bfloat16)
+        odt = torch.float32 if od == "f32" else torch.bfloat16
+        c = torch.empty(M, N, dtype=odt, device="cuda")
+        fl = 2.0 * M * N * Kd
+        row = {"M": M, "N": N, "K": Kd}
+        for name, fn in (("mk_gemm", lambda: K.gemm(a, b, out_dtype=odt, out=c)),
+                         ("rocblas", lambda: K.gemm_blas(a, b, out=c))):
+            ms = time_launches(torch, fn, max(5, args.steps // 2), 3)
+            row[name + "_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+        row["mk_gemm_frac_peak"] = round(row["mk_gemm_tflops"] / PEAK_BF16_TFLOPS, 4)
+        res[tag] = row
+        log(f"gemm {tag} [{M}x{N}x{Kd}]: mk_gemm {row['mk_gemm_tflops']} TFLOP/s, rocBLAS {row['rocblas_tflops']}")
+        del a, b, c
+    d = inputs.c1_mlp()
+    x, w1, b1, w2, b2 = (torch.from_numpy(d[n]).cuda() for n in ("x", "w1", "b1", "w2", "b2"))
+    h = torch.empty(256, 4096, device="cuda")
+    y = torch.empty(256, 1024, device="cuda")
+
+    def mlp():
+        K.gemm(x, w1, bias=b1, relu=True, out=h)
+        K.gemm(h, w2, bias=b2, out=y)
+
+    ms = time_launches(torch, mlp, args.steps, 3)
+    fl = 2.0 * 256 * 1024 * 4096 * 2
+    res["c1_mlp_fp32"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                          "frac_peak_fp32": round(fl / (ms * 1e-3) / 1e12 / 157.3, 4)}
+    log(f"C1 MLP fp32 (two mk_gemm launches): {ms*1e3:.1f} us, {res['c1_mlp_fp32']['tflops']} TFLOP/s")
+    return res
+
+
+def run_pjrt(torch, np, args):
+    """The plugin path: the C3 module at S=8192 compiled by jam and run
+    through PJRT_LoadedExecutable_Execute with inputs resident in HBM (K
+    executes queued back to back, host wall clock until the last completion
+    event), and the per-Execute cost of a tiny module."""
+    from mi355x_pjrt import modules, pjrt
+    from oracle import bf16, inputs
+
+    p = pjrt.Plugin()
+    client = p.client()
+    d = inputs.c3_sdpa(args.seq)
+    e = client.compile(modules.sdpa(4, 16, args.seq, 128, True))
+    bufs = [client.put(d[k], pjrt.BF16) for k in ("q", "k", "v")]
+    for b in bufs:
+        b.ready()
+
+    def run(exe, inputs_, n):
+        outs, ev = [], None
+        t0 = time.perf_counter()
+        for _ in range(n):
+            if ev is not None:
+                p.call("Event_Destroy", event=ev)
+            o, ev = exe.execute(inputs_, wait="event")
+            outs += o
+        p.await_event(ev)
+        el = time.perf_counter() - t0
+        for o in outs:
+            o.destroy()
+        return el / n * 1e3
+
+    run(e, bufs, args.warmup)
+    ms = run(e, bufs, args.steps)
+    tf = sdpa_flops(4, 16, args.seq, 128) / (ms * 1e-3) / 1e12
+    small = client.compile(modules.reduce_sum(4, 8))
+    xb = client.put(bf16.to_bf16_bits(np.ones((4, 8), np.float32)), pjrt.BF16)
+    run(small, [xb], 20)
+    us = run(small, [xb], 200) * 1e3
+    log(f"PJRT Execute, C3 S={args.seq}: {ms:.3f} ms/execute, {tf:.1f} TFLOP/s; tiny module {us:.1f} us/execute")
+    for b in bufs + [xb]:
+        b.destroy()
+    e.destroy()
+    small.destroy()
+    client.close()
+    return {"sdpa_ms_per_execute": round(ms, 4), "sdpa_tflops": round(tf, 2),
+            "tiny_module_us_per_execute": round(us, 2)}
 
 
 def run_c5(torch, np, args):
@@ -288,6 +401,12 @@ def main():
     if args.only == "c5":
         print(json.dumps({"training_step": run_c5(torch, np, args)}))
         return
+    if args.only == "gemm":
+        print(json.dumps({"gemm": run_gemm(torch, np, K, args)}))
+        return
+    if args.only == "pjrt":
+        print(json.dumps({"pjrt": run_pjrt(torch, np, args)}))
+        return
     sweep, head, fusions = {}, None, {}
     spin_up(torch, np, K, args)
     if args.only in (None, "sdpa", "headline"):
@@ -298,9 +417,10 @@ def main():
         print(json.dumps({"fusions": fusions}))
         return
     c5 = run_c5(torch, np, args) if args.only is None else None
-    ms, tf, steps = head
+    plugin = run_pjrt(torch, np, args) if args.only is None else None
+    ms, tf, steps, o0 = head
     S = args.seq
-    cpu = None if args.no_cpu else cpu_baseline_sdpa(np, S, args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline_sdpa(torch, np, S, args.cpu_seconds, gpu_out=o0)
     traffic = read_traffic(f"sdpa_fwd_causal_b4h16d128_s{S}_traffic")
     line = {
         "metric": "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak; fusion GB/s % HBM peak",
@@ -325,6 +445,7 @@ def main():
         "sweep": sweep,
         "fusions": fusions,
         "training_step": c5,
+        "pjrt_execute": plugin,
     }
     print(json.dumps(line))
 
