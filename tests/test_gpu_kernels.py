@@ -269,6 +269,32 @@ def test_scatter_add_edge_cases(K):
     np.testing.assert_array_equal(got, native.scatter_add_bf16(tb, ids.astype(np.int32), ub))
 
 
+def test_scatter_add_wide_rows_edge_cases(K):
+    """Wide fp32 rows (256..1024 floats, the vector accumulate kernels with
+    one to four float4 per lane) bit-exact against the in-order oracle:
+    out-of-range ids, one hot row taking 20000 updates, Zipf-skewed ids,
+    int64 ids, fewer rows than ids, a single id, no ids, and in place."""
+    rng = np.random.default_rng(9)
+    for n_rows, row_len, ids, idx_dtype, in_place in [
+        (3001, 256, rng.integers(-100, 3100, size=9000), np.int32, False),
+        (3001, 256, np.full(20000, 1234), np.int32, False),
+        (3001, 512, (rng.zipf(1.3, size=30000) % 3001), np.int64, False),
+        (100, 800, rng.integers(0, 100, size=5000), np.int32, True),
+        (777, 1024, rng.integers(0, 777, size=1), np.int64, False),
+        (777, 1024, np.zeros(0), np.int32, False),
+    ]:
+        print(f"case: scatter-add wide rows rows={n_rows} len={row_len} ids={ids.size} in_place={in_place}",
+              flush=True)
+        ids = ids.astype(idx_dtype)
+        table = rng.standard_normal((n_rows, row_len)).astype(np.float32)
+        upd = (rng.standard_normal((ids.size, row_len)) * 10).astype(np.float32)
+        t = torch.from_numpy(table).cuda()
+        got = K.scatter_add_rows(t, torch.from_numpy(ids).cuda(), torch.from_numpy(upd).cuda(),
+                                 out=t if in_place else None).cpu().numpy()
+        np.testing.assert_array_equal(got, native.scatter_add_f32(table, ids.astype(np.int64).clip(-2**31, 2**31 - 1)
+                                                                  .astype(np.int32), upd))
+
+
 # ------------------------------------------------------------------ C3 attention
 def _sdpa_case(K, B, H, S, D, causal, seed, Sk=None, qk_std=1 / math.sqrt(128), k_ramp=0):
     rng = np.random.default_rng(seed)
