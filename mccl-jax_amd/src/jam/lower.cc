@@ -29,6 +29,7 @@
 #include <unordered_map>
 
 #include "jam/ir.h"
+#include "jam/bytecode.h"
 #include "jam/program.h"
 #include "mk_kernels.h"
 
@@ -2727,8 +2728,23 @@ class Lowerer {
 CompileResult Compile(const char* code, size_t size, const CompileOptions& opts) {
   CompileResult r;
   if (IsMlirBytecode(code, size)) {
-    r.error = "jam: MLIR bytecode (StableHLO portable artifact) input is not supported by this "
-              "build; pass the module as StableHLO text (PJRT_Program.format = \"mlir\")";
+    // A StableHLO portable artifact (what jaxlib serializes): the container
+    // is read and its operations named; lowering them needs VHLO's binary
+    // attribute and type encodings decoded, which this build does not do.
+    bytecode::Module bm;
+    std::string berr;
+    if (!bytecode::Read(reinterpret_cast<const uint8_t*>(code), size, &bm, &berr)) {
+      r.error = "jam: MLIR bytecode: " + berr;
+      return r;
+    }
+    std::string dialects;
+    for (size_t d = 0; d < bm.dialects.size(); ++d)
+      dialects += (d ? ", " : "") + bm.DialectVersionText(d);
+    r.error = "jam: MLIR bytecode v" + std::to_string(bm.version) + " from '" + bm.producer + "' (dialects " +
+              dialects + "; " + std::to_string(bm.attrs.size()) + " attributes, " + std::to_string(bm.types.size()) +
+              " types): ops " + bm.OpHistogram() +
+              ". Lowering needs the VHLO attribute and type encodings decoded, which is not implemented; "
+              "pass the module as StableHLO text (PJRT_Program.format = \"mlir\")";
     return r;
   }
   std::string err;
