@@ -68,6 +68,21 @@ int mk_gemm(void* stream, int ab_type, int c_type,
             void* C, int64_t c_bs, int64_t c_ms,
             const void* bias, int epilogue);
 
+/* Split-K form of mk_gemm for fp32 outputs with few output tiles and a long
+ * contraction (the weight gradients dW = Xᵀ dY of the training step: the
+ * dot_general of linalg.mm:47-105 with the token axis contracted).  The K
+ * axis is cut into `splits` equal slices; one batched mk_gemm writes the
+ * slices' products to the workspace (splits x M x N fp32) and a second pass
+ * adds them in slice order into C (deterministic: the result does not depend
+ * on scheduling).  K % splits == 0; N and c_ms multiples of 4; C and
+ * workspace 16-byte aligned; C is overwritten.  splits == 1 is a plain
+ * mk_gemm call (no workspace).  Operand convention as mk_gemm.
+ * Replaces, for these products: src/jam/ops/linalg.mm:98. */
+size_t mk_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits);
+int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A,
+                   int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C,
+                   int64_t c_ms, int64_t splits, void* workspace);
+
 /* Plain GEMM through rocBLAS (the linear layers of the training step and
  * their gradients: with no epilogue to fuse, a library GEMM does the work).  Same operand convention as
  * mk_gemm (row-major C with row stride c_ms, one unit stride per operand),

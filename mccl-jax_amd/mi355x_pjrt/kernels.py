@@ -319,6 +319,20 @@ def gemm_blas(a, b, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
     return out
 
 
+def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None):
+    """fp32 out = a @ b with the contraction cut into `splits` slices summed
+    in order (mk_gemm_splitk, hand-written kernels); a [M, K], b [K, N] 2-D views."""
+    _require_cuda(a, b)
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = torch.empty(M, N, dtype=torch.float32, device=a.device) if out is None else out
+    ws = _ws(lib().mk_gemm_splitk_workspace_bytes(M, N, splits), a.device, workspace)
+    rc = lib().mk_gemm_splitk(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
+                              _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), splits, _ptr(ws))
+    _check(rc, "mk_gemm_splitk")
+    return out
+
+
 def gemm_blas_splitk(a, b, splits, out=None, workspace=None, stream=None):
     """fp32 out = a @ b with the contraction cut into `splits` slices
     (mk_gemm_blas_splitk); a [M, K], b [K, N] 2-D views."""

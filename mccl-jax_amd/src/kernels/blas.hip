@@ -141,6 +141,17 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 }
 }  // namespace
 
+int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, float* C, int64_t c_ms,
+               const char* what) {
+  const int64_t nvec = M * N / 4;
+  const unsigned blocks = unsigned(std::min<int64_t>((nvec + 255) / 256, 4096));
+  if (splits == 2) hipLaunchKernelGGL(splitk_sum_kernel<2>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else if (splits == 4) hipLaunchKernelGGL(splitk_sum_kernel<4>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else if (splits == 8) hipLaunchKernelGGL(splitk_sum_kernel<8>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  else hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+  return check_launch(what);
+}
+
 }  // namespace mk
 
 extern "C" size_t mk_gemm_blas_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {
@@ -166,13 +177,7 @@ extern "C" int mk_gemm_blas_splitk(void* stream, int ab_type, int64_t M, int64_t
   if (int rc = mk::gemm_blas(s, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns,
                              W, M * N, N, 1.f, 0.f))
     return rc;
-  const int64_t nvec = M * N / 4;
-  const unsigned blocks = unsigned(std::min<int64_t>((nvec + 255) / 256, 4096));
-  if (splits == 2) hipLaunchKernelGGL(mk::splitk_sum_kernel<2>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else if (splits == 4) hipLaunchKernelGGL(mk::splitk_sum_kernel<4>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else if (splits == 8) hipLaunchKernelGGL(mk::splitk_sum_kernel<8>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else hipLaunchKernelGGL(mk::splitk_sum_kernel<0>, dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  return mk::check_launch("mk_gemm_blas_splitk");
+  return mk::splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_blas_splitk");
 }
 
 extern "C" int mk_gemm_blas(void* stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,

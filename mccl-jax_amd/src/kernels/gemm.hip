@@ -321,6 +321,37 @@ extern "C" int mk_gemm(void* stream, int ab_type, int c_type, int64_t batch, int
   a.vec_a = al16(A) && (a_bs % vec == 0) && ((a_kc ? a.a_ms : a.a_ks) % vec == 0);
   a.vec_b = al16(B) && (b_bs % vec == 0) && ((b_kc ? a.b_ns : a.b_ks) % vec == 0);
   hipStream_t s = as_stream(stream);
-  if (ab_type == MK_BF16) return launch_gemm<uint16_t>(s, a, batch, a_kc, b_kc);
+  if (ab_type == MK_BF16) {
+    const int r = gemm_tiled(s, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs,
+                             c_ms, bias, epilogue);
+    if (r >= 0) return r;
+    return launch_gemm<uint16_t>(s, a, batch, a_kc, b_kc);
+  }
   return launch_gemm<float>(s, a, batch, a_kc, b_kc);
+}
+
+extern "C" size_t mk_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t splits) {
+  if (M <= 0 || N <= 0 || splits <= 1) return 0;
+  return size_t(M * N * splits * 4);
+}
+
+extern "C" int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_ms,
+                              int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C, int64_t c_ms,
+                              int64_t splits, void* workspace) {
+  clear_error();
+  if (splits < 1 || K < 0 || M < 0 || N < 0) return fail(MK_ERR_INVALID, "mk_gemm_splitk: bad shape or splits");
+  if (splits == 1 || M == 0 || N == 0)
+    return mk_gemm(stream, ab_type, MK_F32, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
+  if (K % splits != 0) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K must be a multiple of splits");
+  if (!workspace || !C) return fail(MK_ERR_INVALID, "mk_gemm_splitk: null workspace or output");
+  if ((N % 4) != 0 || (c_ms % 4) != 0 || ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(workspace)) & 15))
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: N and c_ms multiples of 4, 16-byte aligned C and workspace");
+  const int64_t ks = K / splits;
+  // slice s reads A[:, s ks : (s+1) ks] and B[s ks : (s+1) ks, :] (element
+  // strides along k) and writes W[s]: one batched mk_gemm, then the ordered sum
+  float* W = static_cast<float*>(workspace);
+  if (int rc = mk_gemm(stream, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns,
+                       W, M * N, N, nullptr, 0))
+    return rc;
+  return splitk_sum(as_stream(stream), W, splits, M, N, C, c_ms, "mk_gemm_splitk");
 }

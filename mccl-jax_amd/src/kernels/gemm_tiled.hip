@@ -1,0 +1,471 @@
+// Large bf16 GEMM on MFMA for dot_general: mk_gemm's kernel for products
+// with enough output tiles to fill the chip (gemm.hip keeps the general
+// kernel for fp32, odd strides and small products).
+//   C[b] = A[b] · B[b] (+ bias)(ReLU), fp32 accumulate, bf16 / f16 / f32 out.
+//
+// Workgroup tile TM x TN, k in BK-deep tiles, WGM x WGN waves each owning a
+// (TM / WGM) x (TN / WGN) block of the tile as 32 x 32 v_mfma_f32_32x32x16_bf16
+// blocks.  The MFMA is issued with B's rows as its first operand, so a lane's
+// accumulator holds 4 consecutive C columns of one C row (lane (c, g), reg r:
+// row c, column 8 (r / 4) + 4 g + r % 4 of its 32 x 32 block).
+//
+// Operand tiles go from HBM/L2 straight into LDS with buffer_load_dwordx4 ...
+// lds (attn_common.h: lane l writes bytes 16 l .. 16 l + 15 of a 1 KB LDS
+// block, loaded from any offset of the operand), in S stages: the copies of
+// k tile t + S - 1 are issued before tile t is multiplied, one barrier per
+// tile.  Each operand keeps the orientation it has in memory:
+//   k-contiguous (A[m][k], or B stored as [n][k]): LDS rows of BK k, 16-byte
+//     chunk c of row r stored at chunk position c ^ (r & 7) (BK = 64) or
+//     c ^ ((r >> 1) & 3) (BK = 32), read with one ds_read_b128 per MFMA
+//     operand (8 consecutive k);
+//   m- / n-contiguous (A stored as [k][m], B[k][n]): one LDS row of R columns
+//     per k, chunk c of k-row r stored at position c ^ 2 (r & 3), read with
+//     two ds_read_b64_tr_b16 per operand, which hand each lane one column over
+//     4 consecutive k (k-rows 8g .. 8g + 3, then 8g + 4 .. 8g + 7).
+// Both forms give lane (c, g) of an MFMA operand column/row c and k = 8 g ..
+// 8 g + 7 in order, so any pairing of orientations multiplies correctly, and
+// the XOR placements spread each read over all LDS banks.  Chunks past M, N
+// or K are loaded from an out-of-range buffer offset, which reads zeros.
+//
+// Tile order: workgroups are dealt round-robin to the 8 XCDs, each with its
+// own L2, so workgroup i takes tile (i % 8) * (tiles / 8) + i / 8 of an
+// order that walks groups of 4 tile rows column by column: the tiles an XCD
+// runs at once form a compact 4 x 8 block, whose A rows and B columns are
+// fetched into that XCD's L2 once for 8 and 4 tiles respectively.
+// (The reference's dot_general materialises operand transposes first,
+// src/jam/ops/linalg.mm:34-45; no operand is copied in HBM here.)
+#include <atomic>
+
+#include "attn_common.h"
+
+namespace mk {
+namespace {
+
+using namespace attn;
+
+constexpr int kGroupM = 4;                  // tile rows per group of the tile order
+constexpr int kInvalid = int(0x80000000u);  // buffer offset past every accepted range
+
+struct TiledGemm {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;      // element stride of A's, B's, C's non-unit dimension
+  int64_t a_bs, b_bs, c_bs;   // batch strides (elements)
+  uint32_t a_bytes, b_bytes;  // bytes addressable from one batch's A / B base
+  int tiles_m, tiles_n;
+  int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU
+  int c_type;
+  int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
+                              // stored as 16-byte chunks / element by element
+};
+
+// The copies one wave makes of one operand's tile: copy c is j = wave + W c
+// (W waves), lane l of it writes LDS chunk position u = 64 j + l of the tile.
+//   KC:  LDS row u / (BK / 8), position u % (BK / 8), holding global chunk
+//        position ^ kc_swizzle(row)
+//   !KC: LDS k-row u / (R / 8), position u % (R / 8), holding global chunk
+//        position ^ 2 (k-row & 3)
+// Each copy keeps its byte offset for the first k tile and the first k it
+// reads (past every K when its row is outside the operand); tile t adds t
+// times the per-tile step, so the loop carries two registers per copy.
+// chunk placement of a k-contiguous LDS row: conflict-free ds_read_b128 of
+// 8 consecutive rows at one chunk
+template <int BK>
+__device__ inline int kc_swizzle(int row) {
+  return BK == 64 ? (row & 7) : ((row >> 1) & 3);
+}
+
+template <bool KC, int R, int BK, int kC, int W>
+struct Copies {
+  uint32_t off[kC];
+  int32_t k[kC];
+  __device__ inline Copies(int wave, int lane, int64_t r0, int64_t rows, int64_t ld) {
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      const int u = 64 * (wave + W * c) + lane;
+      int64_t gr, gk;
+      if constexpr (KC) {
+        constexpr int kCpr = BK / 8;
+        const int row = u / kCpr;
+        gr = r0 + row;
+        gk = 8 * ((u % kCpr) ^ kc_swizzle<BK>(row));
+        off[c] = uint32_t((gr * ld + gk) * 2);
+      } else {
+        constexpr int kCpr = R / 8;
+        const int kr = u / kCpr;
+        gr = r0 + 8 * ((u % kCpr) ^ (2 * (kr & 3)));
+        gk = kr;
+        off[c] = uint32_t((gk * ld + gr) * 2);
+      }
+      k[c] = gr < rows ? int32_t(gk) : 0x7fffffff - BK;
+    }
+  }
+  // offset for the k tile starting at k0 (step: its byte distance from the
+  // first), or an offset that reads zeros once the chunk lies past K
+  __device__ inline int at(int c, int k0, uint32_t step, int64_t K) const {
+    return int64_t(k[c]) + k0 < K ? int(off[c] + step) : kInvalid;
+  }
+};
+
+// MFMA operand (8 bf16) for rows rb .. rb + 31 of a tile of R rows and k-step
+// ks (k = 16 ks .. 16 ks + 15): lane (c, g) gets row rb + c, k 16 ks + 8 g ..+7.
+template <bool KC, int R, int BK>
+__device__ inline bf16x8_t read_operand(const uint16_t* t, int rb, int ks, int lane) {
+  if constexpr (KC) {
+    const int row = rb + (lane & 31), ch = (2 * ks + (lane >> 5)) ^ kc_swizzle<BK>(row);
+    return as_bf16x8(*reinterpret_cast<const u32x4_t*>(t + row * BK + 8 * ch));
+  } else {
+    // 16-lane group: lanes 4q .. 4q + 3 address k-row q of a 4 x 16 block,
+    // 8 bytes (4 columns) each; lane i of the group receives column i.
+    const int kr = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int col = rb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int at = 8 * ((col >> 3) ^ (2 * (kr & 3))) + (col & 7);
+    const uint2 lo = lds_read_tr(t + kr * R + at);
+    const uint2 hi = lds_read_tr(t + (kr + 4) * R + at);  // (kr + 4) & 3 == kr & 3
+    return as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
+  }
+}
+
+// 4 fp32 -> 4 packed 16-bit values (bf16 or f16, RNE) as two dwords
+template <int CT>
+__device__ inline uint2 pack4(const float (&v)[4]) {
+  if constexpr (CT == MK_BF16)
+    return uint2{f32_to_bf16(v[0]) | (uint32_t(f32_to_bf16(v[1])) << 16),
+                 f32_to_bf16(v[2]) | (uint32_t(f32_to_bf16(v[3])) << 16)};
+  return uint2{f32_to_f16(v[0]) | (uint32_t(f32_to_f16(v[1])) << 16),
+               f32_to_f16(v[2]) | (uint32_t(f32_to_f16(v[3])) << 16)};
+}
+
+// bias + ReLU on the 4 consecutive columns starting at n (bias read for
+// columns < N only)
+template <int CT>
+__device__ inline void finish4(const TiledGemm& p, int64_t n, float (&v)[4]) {
+  if (p.epilogue == 0) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] += n + q < p.N ? load_as_f32(p.bias, n + q, CT) : 0.f;
+    if (p.epilogue == 2) v[q] = fmaxf(v[q], 0.f);
+  }
+}
+
+// 16-bit C through LDS.  Lanes l and l + 32 trade halves (v_permlane32_swap)
+// so that each holds 8 consecutive columns: from the pair (rg 2h, rg 2h + 1)
+// lane g gets the chunk of columns 16 h + 8 g .. + 7 of its block.  Chunks go
+// to LDS rows of TN columns at chunk position ^ (row & 15, or & 7 when a row
+// has fewer than 16 chunks).  Then the workgroup stores runs of consecutive
+// C rows: whole 16-byte chunks when C rows are 16-byte aligned (ROWS16),
+// else one element per thread, consecutive threads on consecutive columns.
+template <int CT, bool ROWS16, int TM, int TN, int kW, int kWM, int kWN, int kI, int kJ>
+__device__ __attribute__((always_inline)) inline void store_staged(const TiledGemm& p,
+                                                                   const f32x16_t (&acc)[kI][kJ], uint16_t* st,
+                                                                   int64_t m0, int64_t n0, int wm, int wn,
+                                                                   int lane, int64_t bz) {
+  constexpr int kCpr = TN / 8;
+  constexpr int kSw = kCpr % 16 == 0 ? 15 : 7;
+  const int c = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int a = 0; a < kI; ++a) {
+    const int ml = wm * kWM + 32 * a + c;
+#pragma unroll
+    for (int b = 0; b < kJ; ++b) {
+      const int nb = wn * kWN + 32 * b;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint2 w[2];  // rg 2h, 2h + 1
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int rg = 2 * h + e;
+          float v[4] = {acc[a][b][4 * rg], acc[a][b][4 * rg + 1], acc[a][b][4 * rg + 2], acc[a][b][4 * rg + 3]};
+          finish4<CT>(p, n0 + nb + 8 * rg + 4 * g, v);
+          w[e] = pack4<CT>(v);
+        }
+        // lane g = 0 ends with (own rg 2h, partner's rg 2h): columns 16 h + 0..7;
+        // lane g = 1 with (partner's rg 2h + 1, own rg 2h + 1): 16 h + 8..15
+        const auto s0 = __builtin_amdgcn_permlane32_swap(w[0].x, w[1].x, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(w[0].y, w[1].y, false, false);
+        const u32x4_t chunk = {static_cast<uint32_t>(s0[0]), static_cast<uint32_t>(s1[0]),
+                               static_cast<uint32_t>(s0[1]), static_cast<uint32_t>(s1[1])};
+        const int cn = (nb + 16 * h + 8 * g) >> 3;
+        *reinterpret_cast<u32x4_t*>(st + ml * TN + 8 * (cn ^ (ml & kSw))) = chunk;
+      }
+    }
+  }
+  lds_barrier();
+  constexpr int kThreads = 64 * kW;
+  static_assert(TM * kCpr % kThreads == 0, "staged rows split evenly over the threads");
+  char* Cz = reinterpret_cast<char*>(p.C) + 2 * bz * p.c_bs;
+  if constexpr (!ROWS16) {
+    uint16_t* Ce = reinterpret_cast<uint16_t*>(Cz);
+    for (int it = 0; it < TM * TN / kThreads; ++it) {
+      const int e = it * kThreads + int(threadIdx.x);
+      const int row = e / TN, col = e % TN;
+      const uint16_t v = st[row * TN + 8 * ((col >> 3) ^ (row & kSw)) + (col & 7)];
+      const int64_t m = m0 + row, n = n0 + col;
+      if (m < p.M && n < p.N) Ce[m * p.ldc + n] = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int it = 0; it < TM * kCpr / kThreads; ++it) {
+    const int e = it * kThreads + int(threadIdx.x);
+    const int row = e / kCpr, cn = e % kCpr;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * (cn ^ (row & kSw)));
+    const int64_t m = m0 + row, n = n0 + 8 * cn;
+    if (m < p.M && n < p.N) *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
+  }
+}
+
+// Stores straight from the accumulators: 4 consecutive columns per lane and
+// register group, as one vector store (c_mode 1) or element by element.
+template <int CT, int kWM, int kWN, int kI, int kJ>
+__device__ __attribute__((always_inline)) inline void store_direct(const TiledGemm& p,
+                                                                   const f32x16_t (&acc)[kI][kJ], int64_t m0,
+                                                                   int64_t n0, int wm, int wn, int lane,
+                                                                   int64_t bz) {
+  constexpr int esz = CT == MK_F32 ? 4 : 2;
+  const int c = lane & 31, g = lane >> 5;
+  char* Cb = reinterpret_cast<char*>(p.C) + esz * bz * p.c_bs;
+#pragma unroll
+  for (int a = 0; a < kI; ++a) {
+    const int64_t m = m0 + wm * kWM + 32 * a + c;
+#pragma unroll
+    for (int b = 0; b < kJ; ++b)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int64_t n = n0 + wn * kWN + 32 * b + 8 * rg + 4 * g;
+        float v[4] = {acc[a][b][4 * rg], acc[a][b][4 * rg + 1], acc[a][b][4 * rg + 2], acc[a][b][4 * rg + 3]};
+        finish4<CT>(p, n, v);
+        if (m >= p.M || n >= p.N) continue;
+        char* dst = Cb + esz * (m * p.ldc + n);
+        if (p.c_mode == 1) {  // N, ldc, batch stride multiples of 4, C 16-byte aligned
+          if constexpr (CT == MK_F32) *reinterpret_cast<float4*>(dst) = float4{v[0], v[1], v[2], v[3]};
+          else *reinterpret_cast<uint2*>(dst) = pack4<CT>(v);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < p.N) store_from_f32(dst, q, CT, v[q]);
+        }
+      }
+  }
+}
+
+// Kernel shape: workgroup tile, wave grid, k-tile depth, LDS stages.
+template <int TM_, int TN_, int WGM_, int WGN_, int BK_, int S_>
+struct Shape {
+  static constexpr int TM = TM_, TN = TN_, WGM = WGM_, WGN = WGN_, BK = BK_, S = S_;
+};
+
+// s_waitcnt vmcnt(n) for a compile-time n, expcnt / lgkmcnt untouched
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <class Sh, bool AKC, bool BKC>
+__global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(const TiledGemm p) {
+  constexpr int TM = Sh::TM, TN = Sh::TN, WGN = Sh::WGN, BK = Sh::BK, S = Sh::S;
+  constexpr int kW = Sh::WGM * WGN;                      // waves
+  constexpr int kWM = TM / Sh::WGM, kWN = TN / WGN;      // wave block
+  constexpr int kI = kWM / 32, kJ = kWN / 32;            // MFMA blocks per wave (m, n)
+  constexpr int kCa = TM * BK / 512 / kW;                // 1 KB copies per wave per k tile, A
+  constexpr int kCb = TN * BK / 512 / kW;                // ... B
+  static_assert(BK == 32 || BK == 64, "k tile depth");
+  static_assert(kI * 32 * Sh::WGM == TM && kJ * 32 * WGN == TN, "wave blocks tile the workgroup tile");
+  static_assert(kCa * kW * 512 == TM * BK && kCb * kW * 512 == TN * BK, "copies split evenly over the waves");
+  static_assert(TM * TN <= S * BK * (TM + TN), "staging tile fits the operand buffers");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[S * BK * (TM + TN)];
+  uint16_t (*As)[TM * BK] = reinterpret_cast<uint16_t (*)[TM * BK]>(lds);
+  uint16_t (*Bs)[TN * BK] = reinterpret_cast<uint16_t (*)[TN * BK]>(lds + S * TM * BK);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+  // tile of this workgroup (see the header)
+  const uint32_t nt = gridDim.x, per = nt / 8, i = blockIdx.x;
+  const uint32_t t = i < 8 * per ? (i % 8) * per + i / 8 : i;
+  const uint32_t group = t / (kGroupM * uint32_t(p.tiles_n)), first_m = group * kGroupM;
+  const uint32_t gm = min(uint32_t(kGroupM), uint32_t(p.tiles_m) - first_m);
+  const uint32_t w_in = t - group * kGroupM * uint32_t(p.tiles_n);
+  const int64_t m0 = int64_t(first_m + w_in % gm) * TM;
+  const int64_t n0 = int64_t(w_in / gm) * TN;
+  const int64_t bz = blockIdx.y;
+  const i32x4_t ra = tile_desc(reinterpret_cast<const uint16_t*>(p.A) + bz * p.a_bs, p.a_bytes);
+  const i32x4_t rb = tile_desc(reinterpret_cast<const uint16_t*>(p.B) + bz * p.b_bs, p.b_bytes);
+
+  const Copies<AKC, TM, BK, kCa, kW> ca(wave, lane, m0, p.M, p.lda);
+  const Copies<BKC, TN, BK, kCb, kW> cb(wave, lane, n0, p.N, p.ldb);
+  // byte distance between consecutive k tiles
+  const uint32_t a_step = AKC ? 2 * BK : uint32_t(2 * BK * p.lda);
+  const uint32_t b_step = BKC ? 2 * BK : uint32_t(2 * BK * p.ldb);
+  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+    const int k0 = BK * kt;
+#pragma unroll
+    for (int c = 0; c < kCa; ++c)
+      copy_to_lds(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), ca.at(c, k0, uint32_t(kt) * a_step, p.K));
+#pragma unroll
+    for (int c = 0; c < kCb; ++c)
+      copy_to_lds(rb, lds_addr(&Bs[stage][(wave + kW * c) * 512]), cb.at(c, k0, uint32_t(kt) * b_step, p.K));
+  };
+
+  f32x16_t acc[kI][kJ];
+#pragma unroll
+  for (int a = 0; a < kI; ++a)
+#pragma unroll
+    for (int b = 0; b < kJ; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  // Tile kt lives in stage kt % S.  Before multiplying tile kt a wave waits
+  // for its own copies of it (the S - 2 tiles issued after it may still be in
+  // flight), then the barrier makes every wave's copies visible and also
+  // marks stage (kt - 1) % S, read in the previous iteration, free for the
+  // copies of tile kt + S - 1.
+  const int nk = int((p.K + BK - 1) / BK);
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + S - 2 < nk) wait_vm<(S - 2) * (kCa + kCb)>();
+    else wait_vm<0>();
+    lds_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const uint16_t* at = As[kt % S];
+    const uint16_t* bt = Bs[kt % S];
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8_t af[kI], bfr[kJ];
+#pragma unroll
+      for (int a = 0; a < kI; ++a) af[a] = read_operand<AKC, TM, BK>(at, wm * kWM + 32 * a, ks, lane);
+#pragma unroll
+      for (int b = 0; b < kJ; ++b) bfr[b] = read_operand<BKC, TN, BK>(bt, wn * kWN + 32 * b, ks, lane);
+#pragma unroll
+      for (int a = 0; a < kI; ++a)
+#pragma unroll
+        for (int b = 0; b < kJ; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[b], af[a], acc[a][b], 0, 0, 0);
+    }
+  }
+  lds_barrier();  // every wave is done with the operand stages before they hold C
+
+  if (p.c_mode == 2 && p.c_type == MK_BF16)
+    store_staged<MK_BF16, true, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
+  else if (p.c_mode == 2)
+    store_staged<MK_F16, true, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
+  else if (p.c_mode == 3 && p.c_type == MK_BF16)
+    store_staged<MK_BF16, false, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
+  else if (p.c_mode == 3)
+    store_staged<MK_F16, false, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
+  else if (p.c_type == MK_F32)
+    store_direct<MK_F32, kWM, kWN>(p, acc, m0, n0, wm, wn, lane, bz);
+  else if (p.c_type == MK_BF16)
+    store_direct<MK_BF16, kWM, kWN>(p, acc, m0, n0, wm, wn, lane, bz);
+  else
+    store_direct<MK_F16, kWM, kWN>(p, acc, m0, n0, wm, wn, lane, bz);
+}
+
+template <class Sh>
+int launch(hipStream_t s, TiledGemm& a, int64_t batch, bool a_kc, bool b_kc) {
+  a.tiles_m = int((a.M + Sh::TM - 1) / Sh::TM);
+  a.tiles_n = int((a.N + Sh::TN - 1) / Sh::TN);
+  const dim3 g{unsigned(int64_t(a.tiles_m) * a.tiles_n), unsigned(batch)}, b{unsigned(64 * Sh::WGM * Sh::WGN)};
+  if (a_kc && b_kc) hipLaunchKernelGGL((gemm_tiled_kernel<Sh, true, true>), g, b, 0, s, a);
+  else if (a_kc) hipLaunchKernelGGL((gemm_tiled_kernel<Sh, true, false>), g, b, 0, s, a);
+  else if (b_kc) hipLaunchKernelGGL((gemm_tiled_kernel<Sh, false, true>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((gemm_tiled_kernel<Sh, false, false>), g, b, 0, s, a);
+  return check_launch("mk_gemm");
+}
+
+// Bytes one batch's operand spans from its base: rows (m or n) x K with the
+// unit stride along k (kc) or along the rows.
+int64_t span_bytes(bool kc, int64_t rows, int64_t K, int64_t ld) {
+  return 2 * (kc ? (rows - 1) * ld + K : (K - 1) * ld + rows);
+}
+
+// Fills the kernel arguments; false when the shape, strides or alignment do
+// not fit the tiled kernel.
+bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
+                const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
+                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue) {
+  if (M < 128 || N < 128 || K < 64 || K % 8 != 0) return false;
+  a_kc = a_ks == 1;
+  b_kc = b_ks == 1;
+  if (!a_kc && a_ms != 1) return false;
+  if (!b_kc && b_ns != 1) return false;
+  const int64_t lda = a_kc ? a_ms : a_ks, ldb = b_kc ? b_ns : b_ks;
+  // every 16-byte chunk a copy loads is aligned and lies wholly inside or
+  // wholly outside the operand: 16-byte bases, strides multiples of 8
+  // elements, the contiguous extent (K, or M / N) a multiple of 8
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
+  if (!al16(A) || !al16(B) || lda % 8 != 0 || ldb % 8 != 0) return false;
+  if (batch > 1 && (a_bs % 8 != 0 || b_bs % 8 != 0)) return false;
+  if ((!a_kc && M % 8 != 0) || (!b_kc && N % 8 != 0)) return false;
+  if (lda < (a_kc ? K : M) || ldb < (b_kc ? K : N)) return false;  // overlapping rows
+  const int64_t ab = span_bytes(a_kc, M, K, lda), bb = span_bytes(b_kc, N, K, ldb);
+  if (ab >= (int64_t(1) << 31) || bb >= (int64_t(1) << 31)) return false;  // 32-bit buffer offsets
+  a.A = A; a.B = B; a.C = C; a.bias = bias;
+  a.M = M; a.N = N; a.K = K;
+  a.lda = lda; a.ldb = ldb; a.ldc = c_ms;
+  a.a_bs = a_bs; a.b_bs = b_bs; a.c_bs = c_bs;
+  a.a_bytes = uint32_t(ab); a.b_bytes = uint32_t(bb);
+  a.epilogue = epilogue;
+  a.c_type = c_type;
+  const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0 && N % 8 == 0;
+  const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0 && N % 4 == 0;
+  a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 1 : 0;
+  return true;
+}
+
+// compute units of the current device (cached per device)
+int64_t cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+}  // namespace
+
+int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
+               int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
+               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue) {
+  TiledGemm a;
+  bool a_kc, b_kc;
+  if (!tiled_args(a, a_kc, b_kc, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs, c_ms,
+                  bias, epilogue))
+    return -1;
+  // Kernel shape: the one with the least estimated time, counting whole
+  // rounds of workgroups over the CUs (one 256 x 256 workgroup per CU; the
+  // 4-wave shapes fit two per CU) and each shape's throughput per slot as
+  // measured on large products (8192 x 8192 x 4096: 1077, 1058 and 980
+  // TFLOP/s), so small tile counts weigh quantisation against tile size.
+  struct Option {
+    int tm, tn, per_cu;
+    double rate;
+  };
+  static const Option options[3] = {{256, 256, 1, 1077.0}, {128, 192, 2, 1058.0}, {128, 128, 2, 980.0}};
+  const int64_t slots_cu = cu_count();
+  int best = -1;
+  double best_t = 0;
+  for (int o = 0; o < 3; ++o) {
+    const Option& op = options[o];
+    if (M < op.tm || N < op.tn) continue;
+    const int64_t tiles = ((M + op.tm - 1) / op.tm) * ((N + op.tn - 1) / op.tn) * batch;
+    const int64_t slots = slots_cu * op.per_cu;
+    const double t = double((tiles + slots - 1) / slots) * op.tm * op.tn * op.per_cu / op.rate;
+    if (best < 0 || t < best_t) best = o, best_t = t;
+  }
+  if (best == 0) return launch<Shape<256, 256, 2, 4, 64, 2>>(s, a, batch, a_kc, b_kc);
+  if (best == 1) return launch<Shape<128, 192, 2, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
+  return launch<Shape<128, 128, 2, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
+}
+
+}  // namespace mk

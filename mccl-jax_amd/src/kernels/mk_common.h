@@ -25,6 +25,18 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
               const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
 
+// C = sum of the splits dense M x N fp32 slices of W, added in slice order
+// (blas.hip); N and c_ms multiples of 4, W and C 16-byte aligned.
+int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, float* C, int64_t c_ms,
+               const char* what);
+
+// Tiled bf16 GEMM for large products behind mk_gemm (gemm_tiled.hip), same
+// operand convention; returns -1 without launching when the shape, strides or
+// alignment do not fit it, else MK_OK or an MK_ERR_* code.
+int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
+               int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
+               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue);
+
 // Flash attention backward behind mk_sdpa_bwd for head_dim 64 / 128
 // (attention_bwd.hip); workspace: the per-row statistics.
 size_t sdpa_bwd_flash_workspace(int64_t B, int64_t H, int64_t Sq);

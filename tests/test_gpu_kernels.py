@@ -464,6 +464,85 @@ def test_gemm_batched_bf16_out(K):
     assert d.max() <= 1
 
 
+def _bf16_out_ok(got_bits, want, norm):
+    """bf16 GEMM output bar: within one ulp of the float64 value rounded once,
+    or, where the sum cancels to far below its terms, within the fp32
+    accumulation bound (1e-5 of sum |a||b|) of the float64 value."""
+    ulp = bf16.bf16_ulp_distance(got_bits, ops.round_to(want, "bf16"))
+    err = np.abs(bf16.from_bf16_bits(got_bits).astype(np.float64) - want)
+    return bool(np.all((ulp <= 1) | (err <= 1e-5 * norm)))
+
+
+def _bf16_operand(x, transposed):
+    """bf16 device view of x, stored transposed (unit stride along rows) when asked."""
+    if transposed:
+        return dev_bf16(bf16.to_bf16_bits(np.ascontiguousarray(x.T))).t()
+    return dev_bf16(bf16.to_bf16_bits(x))
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_tiled_bf16_shapes(K, ta, tb):
+    """bf16 products big enough for the 256-row tiled kernel: ragged M, N and
+    K (multiples of 8, partial 64-deep k tiles), both column tile widths, and
+    shapes whose strides send them to the general kernel (N = 777 with a
+    row-contiguous B).  fp32 out within 1e-5 norm-scaled; bf16 out within one
+    ulp of the float64 product rounded once."""
+    rng = np.random.default_rng(21)
+    for (M, N, Kd) in [(264, 264, 200), (520, 136, 72), (256, 1000, 64), (300, 777, 136), (769, 384, 1032)]:
+        print(f"case: tiled gemm ta={ta} tb={tb} M={M} N={N} K={Kd}", flush=True)
+        a = bf16.round_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+        b = bf16.round_bf16(rng.standard_normal((Kd, N)).astype(np.float32))
+        at, bt = _bf16_operand(a, ta), _bf16_operand(b, tb)
+        want = a.astype(np.float64) @ b
+        norm = np.abs(a).astype(np.float64) @ np.abs(b)
+        got = K.gemm(at, bt, out_dtype=torch.float32).cpu().numpy()
+        assert np.max(np.abs(got - want) / (norm + 1e-30)) < 1e-5, (M, N, Kd)
+        gb = host_bf16(K.gemm(at, bt, out_dtype=torch.bfloat16))
+        assert _bf16_out_ok(gb, want, norm), (M, N, Kd)
+
+
+def test_gemm_tiled_epilogues_and_layouts(K):
+    """Tiled kernel epilogues: bias, bias + ReLU, f16 out, C rows that are not
+    16-byte multiples (element stores), batched operands with padded leading
+    and batch strides, and a B shared by every batch (batch stride 0)."""
+    rng = np.random.default_rng(22)
+    M, N, Kd = 392, 520, 264
+    a = bf16.round_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+    b = bf16.round_bf16(rng.standard_normal((Kd, N)).astype(np.float32))
+    bias = bf16.round_bf16(rng.standard_normal(N).astype(np.float32))
+    prod = a.astype(np.float64) @ b
+    norm = np.abs(a).astype(np.float64) @ np.abs(b) + np.abs(bias)
+    at, bt = _bf16_operand(a, False), _bf16_operand(b, False)
+    bias_d = dev_bf16(bf16.to_bf16_bits(bias))
+    print("case: tiled gemm bias / relu epilogues, bf16 out", flush=True)
+    for relu in (False, True):
+        want = prod + bias
+        if relu:
+            want = np.maximum(want, 0)
+        got = host_bf16(K.gemm(at, bt, out_dtype=torch.bfloat16, bias=bias_d, relu=relu))
+        assert _bf16_out_ok(got, want, norm), relu
+    print("case: tiled gemm f16 out, bias", flush=True)
+    bias_h = torch.from_numpy(bias).cuda().half()
+    gh = K.gemm(at, bt, out_dtype=torch.float16, bias=bias_h).cpu().numpy().astype(np.float64)
+    want = prod + bias.astype(np.float16).astype(np.float64)
+    # f16 keeps 11 bits: half an ulp is 2^-11 relative, plus the fp32 bound
+    assert np.all(np.abs(gh - want) <= np.abs(want) * 2.0**-11 + 1e-5 * norm)
+    print("case: tiled gemm C rows 2 bytes off 16-byte alignment (element stores)", flush=True)
+    wide = torch.full((M, N + 3), -7.0, dtype=torch.bfloat16, device="cuda")
+    K.gemm(at, bt, out_dtype=torch.bfloat16, out=wide[:, :N])
+    wh = host_bf16(wide)
+    assert _bf16_out_ok(wh[:, :N], prod, norm)
+    assert np.all(bf16.from_bf16_bits(wh[:, N:]) == -7.0)  # padding untouched
+    print("case: tiled gemm batched, padded strides, shared B", flush=True)
+    a3 = bf16.round_bf16(rng.standard_normal((3, M, Kd)).astype(np.float32))
+    buf = torch.zeros((3, M + 8, Kd + 16), dtype=torch.bfloat16, device="cuda")
+    buf[:, :M, :Kd] = dev_bf16(bf16.to_bf16_bits(a3))
+    got3 = K.gemm(buf[:, :M, :Kd], bt, out_dtype=torch.float32).cpu().numpy()
+    want3 = np.matmul(a3.astype(np.float64), b)
+    norm3 = np.matmul(np.abs(a3).astype(np.float64), np.abs(b))
+    assert np.max(np.abs(got3 - want3) / (norm3 + 1e-30)) < 1e-5
+
+
 # ------------------------------------------------------------------ a6 iota, a12 layout, misc
 def test_iota_convert_fill_copy(K):
     it = K.iota((3, 5, 7), 1).cpu().numpy()

@@ -130,6 +130,24 @@ def test_gemm_blas_splitk(K, M, N, Kd, splits):
     assert torch.equal(got, K.gemm_blas_splitk(a, dy, splits))
 
 
+@pytest.mark.parametrize("M,N,Kd,splits", [(768, 3072, 8192, 4), (3072, 768, 8192, 2), (768, 768, 8192, 8),
+                                            (96, 64, 512, 8), (64, 32, 64, 1)])
+def test_gemm_splitk(K, M, N, Kd, splits):
+    """Hand-written split-K (mk_gemm_splitk) on the weight-gradient form
+    (A = Xᵀ stored [K, M], B = dY [K, N]): within fp32 accumulation of the
+    float64 product and bit-reproducible."""
+    print(f"case: mk_gemm_splitk M={M} N={N} K={Kd} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(M + N + splits)
+    x = (torch.randn(Kd, M, generator=g)).bfloat16().cuda()
+    dy = torch.randn(Kd, N, generator=g).bfloat16().cuda()
+    a = x.t()
+    got = K.gemm_splitk(a, dy, splits)
+    ref = _f64(a) @ _f64(dy)
+    scale = float((_f64(x).abs().t() @ _f64(dy).abs()).max())
+    assert float((_f64(got) - ref).abs().max()) < 2e-6 * scale
+    assert torch.equal(got, K.gemm_splitk(a, dy, splits))
+
+
 # ------------------------------------------------------------------ row adds
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (7, 13), (8192, 768), (33, 2304)])
