@@ -8,7 +8,7 @@ lines 71-75), for a pre-LayerNorm decoder with tied input/output embeddings,
 GELU(tanh) MLP and causal attention, without the pmean (one GPU).  Every
 operation is a call through the C-ABI of include/mk_kernels.h:
 
-  forward   gather + position add, per layer LN -> QKV GEMM, bias add -> causal
+  forward   gather + position add, per layer LN -> QKV GEMM (+ bias) -> causal
             attention -> output GEMM -> residual + bias add -> LN -> FC GEMM,
             bias add -> GELU -> projection GEMM -> residual + bias add; final
             LN, logits GEMM against the embedding table, fused softmax
@@ -23,9 +23,14 @@ operation is a call through the C-ABI of include/mk_kernels.h:
             working copy rewritten), lr and bias corrections read from a
             device buffer so the whole step can be replayed as a HIP graph
 
-The GEMMs have no epilogue here (the biases join the elementwise pass that
-follows), so they are plain library GEMMs (mk_gemm_blas, rocBLAS); every other
-operation is a hand-written kernel.  All parameters live in five flat buffers (fp32 master, bf16 working copy,
+The per-layer GEMMs run on the hand-written MFMA GEMM (mk_gemm; the QKV bias
+in its epilogue, the other biases in the elementwise pass that follows) and
+the weight gradients on its split-K form (mk_gemm_splitk).  The three GEMMs
+over the vocabulary (logits, and the two gradients through the tied
+embedding) stay on rocBLAS (mk_gemm_blas): their rows are 50257 elements, so
+operand rows are not 16-byte aligned and the tiled kernel's direct 16-byte
+HBM->LDS copies do not apply.  Every other operation is a hand-written
+kernel.  All parameters live in five flat buffers (fp32 master, bf16 working copy,
 fp32 gradient, fp32 m, fp32 v), each parameter a 64-element-aligned slice, so
 the optimizer is a single launch and every gradient is written in place.  The
 step is prepared once as a list of bound calls (device pointers and shapes
@@ -134,9 +139,11 @@ class GPT2TrainStep:
 
     # K-slices of the fp32 weight-gradient GEMMs (dW = Xᵀ dY, K = tokens):
     # their few output tiles leave most CUs idle unless K is split.  Counts
-    # measured at C5 on one MI355X (per GEMM: plain vs split, slices summed
-    # by mk_gemm_blas_splitk's second pass).
-    DW_SPLITS = {"dw_o": 8, "dw_qkv": 2, "dw_fc": 4, "dw_pr": 4}
+    # measured at C5 on one MI355X (mk_gemm_splitk with 1, 2, 4, 8 and 16
+    # slices; TFLOP/s dw_o 102/179/281/294/260, dw_qkv 304/493/596/462/315,
+    # dw_fc and dw_pr 415/593/621/514/367).
+    DW_SPLITS = {"dw_o": 8, "dw_qkv": 4, "dw_fc": 4, "dw_pr": 4}
+    VOCAB_GEMMS = ("logits", "dhf", "dwte")
 
     def __init__(self, cfg: GPT2Config, params: dict | None = None, seed: int = 0, lr: float = 3e-4,
                  b1: float = 0.9, b2: float = 0.999, adam_eps: float = 1e-8, device="cuda", stream=None):
@@ -218,9 +225,9 @@ class GPT2TrainStep:
         self.loss_rows = torch.empty(T, dtype=torch.float32, device=dev)
         self.loss_sum = torch.empty(1, dtype=torch.float32, device=dev)
         lib = self.lib
-        sk = [lib.mk_gemm_blas_splitk_workspace_bytes(d, n, self.DW_SPLITS.get(t, 1))
+        sk = [lib.mk_gemm_splitk_workspace_bytes(d, n, self.DW_SPLITS.get(t, 1))
               for t, n in (("dw_o", d), ("dw_qkv", 3 * d), ("dw_fc", c.d_ff))]
-        sk.append(lib.mk_gemm_blas_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS.get("dw_pr", 1)))
+        sk.append(lib.mk_gemm_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS.get("dw_pr", 1)))
         ws = max(*sk, lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
                  lib.mk_layernorm_bwd_workspace_bytes(T, d),
                  lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),
@@ -245,19 +252,26 @@ class GPT2TrainStep:
         def G(name):
             return P(self.view(self.grad, name))
 
-        def gemm(ab, ct, M, N, Kd, a, a_ms, a_ks, b, b_ks, b_ns, cptr, c_ms, tag="gemm"):
-            # plain GEMM (no epilogue) through rocBLAS; the fp32 weight
-            # gradients (few output tiles, K = tokens) split along K
+        def gemm(ab, ct, M, N, Kd, a, a_ms, a_ks, b, b_ks, b_ns, cptr, c_ms, tag="gemm", bias=None):
+            # hand-written GEMM (optionally + bias); the fp32 weight gradients
+            # (few output tiles, K = tokens) split along K; the vocabulary
+            # GEMMs (unaligned 50257-element rows) through rocBLAS
             sp = self.DW_SPLITS.get(tag, 1)
             if sp > 1 and ct == F32 and Kd % sp == 0:
-                calls.append(_Call(lib.mk_gemm_blas_splitk, [st, _I(ab), _I64(M), _I64(N), _I64(Kd), a, _I64(a_ms),
-                                                             _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr, _I64(c_ms),
-                                                             _I64(sp), ws], "mk_gemm_blas_splitk " + tag))
+                calls.append(_Call(lib.mk_gemm_splitk, [st, _I(ab), _I64(M), _I64(N), _I64(Kd), a, _I64(a_ms),
+                                                        _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr, _I64(c_ms),
+                                                        _I64(sp), ws], "mk_gemm_splitk " + tag))
                 return
-            calls.append(_Call(lib.mk_gemm_blas, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
-                                                  a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
-                                                  _I64(b_ns), cptr, _I64(0), _I64(c_ms), _F(1.0), _F(0.0)],
-                               "mk_gemm_blas " + tag))
+            if tag in self.VOCAB_GEMMS:
+                calls.append(_Call(lib.mk_gemm_blas, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
+                                                      a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
+                                                      _I64(b_ns), cptr, _I64(0), _I64(c_ms), _F(1.0), _F(0.0)],
+                                   "mk_gemm_blas " + tag))
+                return
+            calls.append(_Call(lib.mk_gemm, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
+                                             a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
+                                             _I64(b_ns), cptr, _I64(0), _I64(c_ms), bias or _P(0),
+                                             _I(0 if bias is None else 1)], "mk_gemm " + tag))
 
         def add_rows(out, rows, cols, a, b=None, bias=None, tag="add"):
             """out = a (+ b) (+ bias broadcast over rows), one mk_add_rows pass"""
@@ -296,8 +310,7 @@ class GPT2TrainStep:
         for l in range(L):
             p = f"h{l}."
             gemm(BF16, BF16, T, 3 * d, d, P(self.h1[l]), d, 1, W(p + "w_qkv"), 3 * d, 1, P(self.qkv[l]), 3 * d,
-                 tag="qkv")
-            add_rows(P(self.qkv[l]), T, 3 * d, P(self.qkv[l]), bias=W(p + "b_qkv"), tag="bias")
+                 tag="qkv", bias=W(p + "b_qkv"))
             q, k, v = (P(self.qkv[l], i * d) for i in range(3))
             strides_qkv = [_I64(S * 3 * d), _I64(hd), _I64(3 * d)]
             calls.append(_Call(lib.mk_sdpa_fwd, [st, _I64(B), _I64(H), _I64(S), _I64(S), _I64(hd),
