@@ -90,16 +90,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
 
-  __shared__ __attribute__((aligned(1024))) uint16_t K0[NK * 512];
-  __shared__ __attribute__((aligned(1024))) uint16_t K1[NK * 512];
-  __shared__ __attribute__((aligned(1024))) uint16_t V0[NV * 512];
-  __shared__ __attribute__((aligned(1024))) uint16_t V1[NV * 512];
-  auto kbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
-    if constexpr (decltype(i)::value == 0) return K0; else return K1;
+  // K0, K1, V0, V1 in one LDS array (element offsets below)
+  constexpr int kOffK1 = NK * 512, kOffV0 = 2 * NK * 512, kOffV1 = 2 * NK * 512 + NV * 512;
+  __shared__ __attribute__((aligned(1024))) uint16_t kv_lds[2 * (NK + NV) * 512];
+  auto buf_off = [](auto i, auto v) __attribute__((always_inline)) -> int {
+    if constexpr (decltype(v)::value) return decltype(i)::value == 0 ? kOffV0 : kOffV1;
+    else return decltype(i)::value == 0 ? 0 : kOffK1;
   };
-  auto vbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
-    if constexpr (decltype(i)::value == 0) return V0; else return V1;
-  };
+  auto kbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* { return kv_lds + buf_off(i, Flag<false>{}); };
+  auto vbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* { return kv_lds + buf_off(i, Flag<true>{}); };
 
   // heaviest (latest) query tiles first; consecutive ids walk over heads so
   // a head's tiles share an XCD when BH % 8 == 0
@@ -160,17 +159,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
 #pragma unroll
     for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, UV, p.v_ss);
   }
-  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int U, int n, int nw, uint16_t* dst, int tile) __attribute__((always_inline)) {
+  // LDS byte address of this wave's first copy block in the array; the
+  // empty asm at each use keeps the per-copy addresses (this + a constant)
+  // from being hoisted out of the key loop, where they would only occupy
+  // SGPRs (and spill): m0 costs one scalar add per copy instead.
+  const uint32_t lds_wave = lds_addr(kv_lds) + uint32_t(wave % GW) * 1024u;
+  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int U, int n, int nw, int dst_off, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
     const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
     const i32x4_t r = tile_desc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
+    uint32_t lw = lds_wave;
+    asm volatile("" : "+s"(lw));
 #pragma unroll
     for (int i = 0; i < nw; ++i)
       if (GW * i + (wave % GW) < n)  // wave-uniform
-        copy_to_lds(r, lds_addr(dst + (GW * i + (wave % GW)) * 512), kKeepOff ? off[i] : lane_off(i, U, ss));
+        copy_to_lds(r, lw + uint32_t(2 * dst_off + GW * i * 1024), kKeepOff ? off[i] : lane_off(i, U, ss));
   };
-  auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) { dma(kb, p.k_ss, koff, UK, NK, NKW, kbuf(buf), tile); };
-  auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) { dma(vb, p.v_ss, voff, UV, NV, NVW, vbuf(buf), tile); };
+  auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) {
+    dma(kb, p.k_ss, koff, UK, NK, NKW, buf_off(buf, Flag<false>{}), tile);
+  };
+  auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) {
+    dma(vb, p.v_ss, voff, UV, NV, NVW, buf_off(buf, Flag<true>{}), tile);
+  };
 
   // lane's element offset in a V tile for the transposed reads: key 4g + r/4,
   // d 16*hi + 4*(r%4) (r = lane % 16, hi = lane / 16 % 2)
@@ -314,6 +324,57 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     if (tt >= 0 && tt < n_rel) xphase(tt);
   };
 
+  // Phases M(t) X(t) M(t+1) X(t+1) for an even t.  STEADY: every wave has
+  // both products in both M phases and a softmax in both X phases, and no
+  // wave's sequence ends here, so the phases are fixed code (the running O
+  // stays in the same registers from pair to pair).  Returns true when this
+  // wave's last phase has run.
+  auto pair = [&](int t, auto steady) __attribute__((always_inline)) -> bool {
+    constexpr bool ST = decltype(steady)::value;
+    // ---- M(t) (A at t == 0: phase 0's barrier was the one before the loop)
+    if (grp == 0) {
+      if (t > 0) {
+        wait_copies();  // V[t-1] (started in X(t-1)) is read from this phase on
+        lds_barrier();
+      }
+    } else {
+      lds_barrier();
+    }
+    if constexpr (ST) mphase(Int<0>{}, Int<1>{}, Flag<true>{}, Flag<true>{});
+    else mstep(t, Int<0>{});
+    if (!ST && t == n_tiles && grp == 1) return true;  // B's last phase was M(n_tiles)
+    // ---- X(t)
+    if (grp == 0) {
+      lds_barrier();
+      if (ST || t < n_tiles) dma_v(t, Int<0>{});
+    } else {
+      wait_copies();  // K[t+1] (started in X(t-1)) is read from this phase on
+      lds_barrier();
+      if (t + 2 < n_tiles) dma_k(t + 2, Int<0>{});
+    }
+    if constexpr (ST) xphase(t);
+    else xstep(t);
+    if (!ST && t == n_tiles) return true;
+    // ---- M(t+1), t+1 odd
+    if (grp == 0) wait_copies();  // V[t]
+    lds_barrier();
+    if constexpr (ST) mphase(Int<1>{}, Int<0>{}, Flag<true>{}, Flag<true>{});
+    else mstep(t + 1, Int<1>{});
+    if (!ST && t + 1 == n_tiles && grp == 1) return true;
+    // ---- X(t+1)
+    if (grp == 0) {
+      lds_barrier();
+      if (ST || t + 1 < n_tiles) dma_v(t + 1, Int<1>{});
+    } else {
+      wait_copies();  // K[t+2]
+      lds_barrier();
+      if (t + 3 < n_tiles) dma_k(t + 3, Int<1>{});
+    }
+    if constexpr (ST) xphase(t + 1);
+    else xstep(t + 1);
+    return false;
+  };
+
   // Global phases: group A runs M(t) in phase 2t and X(t) in 2t+1, group B
   // one phase later.  Each wave runs its own M(0) X(0) M(1) X(1) ... with a
   // barrier before every phase; B waits out phase 0 first, so barriers pair
@@ -325,7 +386,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   //   B starts K[t+2] (into K<t%2>, last read in phase 2t+1) at the start of
   //     X(t), phase 2t+2, and waits for it before the barrier of phase 2t+4,
   //     where M(t+2) first reads it.
-  // Phases end at 2 n_tiles + 1 (B's M(n_tiles)).
+  // Phases end at 2 n_tiles + 1 (B's M(n_tiles)).  The pairs from t = 2 up
+  // to the last one in which wave 0 (the one with the fewest tiles under the
+  // causal mask) still has both products are steady for every wave; the
+  // first pair and the ragged tail run the general code.  The steady trip
+  // count is the same for all waves, so the barriers still pair up.
   if (n_tiles > 0) {
     if (grp == 1) {  // K[0] before phase 0, K[1] during it (B has no softmax yet)
       dma_k(0, Int<0>{});
@@ -335,44 +400,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     } else {
       lds_barrier();
     }
-    for (int t = 0; t <= n_tiles; t += 2) {
-      // ---- M(t), t even (A: phase 0's barrier was the one above)
-      if (grp == 0) {
-        if (t > 0) {
-          wait_copies();  // V[t-1] (started in X(t-1)) is read from this phase on
-          lds_barrier();
-        }
-      } else {
-        lds_barrier();
-      }
-      mstep(t, Int<0>{});
-      if (t == n_tiles && grp == 1) break;  // B's last phase was M(n_tiles)
-      // ---- X(t)
-      if (grp == 0) {
-        lds_barrier();
-        if (t < n_tiles) dma_v(t, Int<0>{});
-      } else {
-        wait_copies();  // K[t+1] (started in X(t-1)) is read from this phase on
-        lds_barrier();
-        if (t + 2 < n_tiles) dma_k(t + 2, Int<0>{});
-      }
-      xstep(t);
-      if (t == n_tiles) break;
-      // ---- M(t+1), t+1 odd
-      if (grp == 0) wait_copies();  // V[t]
-      lds_barrier();
-      mstep(t + 1, Int<1>{});
-      if (t + 1 == n_tiles && grp == 1) break;
-      // ---- X(t+1)
-      if (grp == 0) {
-        lds_barrier();
-        if (t + 1 < n_tiles) dma_v(t + 1, Int<1>{});
-      } else {
-        wait_copies();  // K[t+2]
-        lds_barrier();
-        if (t + 3 < n_tiles) dma_k(t + 3, Int<1>{});
-      }
-      xstep(t + 1);
+    const int n_rel_min = CAUSAL ? min(n_tiles, (qt * kBM + 31) / kBN + 1) : n_tiles;
+    if (!pair(0, Flag<false>{})) {
+      int t = 2;
+      for (; t + 2 <= n_rel_min; t += 2) pair(t, Flag<true>{});
+      for (; t <= n_tiles; t += 2)
+        if (pair(t, Flag<false>{})) break;
     }
   }
 
@@ -399,6 +432,309 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     if (p.lse && g == 0) {
       const float lse2 = (l_tot > 0.f) ? m_run + log2f(l_tot) : -INFINITY;
       p.lse[int64_t(bh) * p.Sq + qrow] = lse2 * 0.69314718055994531f;
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------- wide waves
+// One workgroup = 4 waves (one per SIMD) = 256 query rows of one (b, h); wave
+// w owns rows 64 w .. 64 w + 63 as two 32-row blocks.  Every K or Vᵀ operand
+// read from LDS feeds two MFMAs (one per row block), which halves the LDS
+// read traffic per MFMA of the 8-wave kernel above: there each wave owns 32
+// rows, and the waves of a phase read 1 KB of LDS per 32-cycle MFMA, the
+// CU's whole LDS read bandwidth (removing the reads there saves a third of
+// the time).
+// Keys are processed in halves of 32 (half h = keys 32 h .. 32 h + 31), and
+// with one wave per SIMD the matrix core is fed from within the wave.  Step h:
+//   rescale O if softmax(h) raised a row's max (rare; a wave-uniform branch),
+//   O += P(h) · V(h)  with  softmax(S(h+1)) -> P(h+1)   (MFMAs and VALU work
+//   on disjoint registers, one basic block: the compiler interleaves them),
+//   S(h+2) = K(h+2) · Qᵀ.
+// S and P each alternate between two register sets, so the live state is O
+// (128 registers at D = 128), Q (64), 2 x 32 scores, 2 x 16 P: the O
+// accumulators go to AGPRs, the rest fits the 256 VGPRs.
+// K/V tiles of 64 keys are staged as in the 8-wave kernel (same LDS layouts
+// and copies, split over the 4 waves), one barrier per tile: at the start of
+// step 2t, after which K(t+1) and V(t) are visible and K(t), V(t-1) free.
+// Online softmax in the log2 domain with lazy rescale as above, written
+// without branches (selects) so that it stays in the interleaved block.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p) {
+  constexpr int NW = 4, QB = 2;     // waves, 32-row blocks per wave
+  constexpr int kBM = 64 * NW;      // query rows per workgroup
+  constexpr int CH = D / 8;
+  constexpr int UK = CH + 1, UV = CH + 4;
+  constexpr int KS = UK * 8, VS = UV * 8;
+  constexpr int NK = UK, NV = UV;
+  constexpr int NKW = (NK + NW - 1) / NW, NVW = (NV + NW - 1) / NW;
+  constexpr int NDB = D / 32, NKS = D / 16;
+  constexpr int kOffK1 = NK * 512, kOffV0 = 2 * NK * 512, kOffV1 = 2 * NK * 512 + NV * 512;
+  __shared__ __attribute__((aligned(1024))) uint16_t kv_lds[2 * (NK + NV) * 512];
+
+  const int id = blockIdx.x;
+  const int qt = CAUSAL ? (p.n_qtiles - 1 - id / p.BH) : (id / p.BH);
+  const int bh = id % p.BH;
+  const int b = bh / p.H, h = bh % p.H;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 31, g = lane >> 5;
+  const int q0 = qt * kBM + wave * 64;  // first query row of this wave
+
+  const uint16_t* qb = p.q + b * p.q_bs + h * p.q_hs;
+  const uint16_t* kb = p.k + b * p.k_bs + h * p.k_hs;
+  const uint16_t* vb = p.v + b * p.v_bs + h * p.v_hs;
+
+  bf16x8_t qf[QB][NKS];
+#pragma unroll
+  for (int r = 0; r < QB; ++r) {
+    const int qrow = q0 + 32 * r + c;
+    const bool ok = qrow < p.Sq;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (ok) v = *reinterpret_cast<const u32x4_t*>(qb + int64_t(qrow) * p.q_ss + 16 * s + 8 * g);
+      qf[r][s] = as_bf16x8(v);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // Q has landed before any copy is in flight
+  int kv_end = p.Sk;
+  if (CAUSAL) kv_end = min(kv_end, min(qt * kBM + kBM, p.Sq));
+  const int n_tiles = (kv_end + kBN - 1) / kBN;
+  const int n_rel = CAUSAL ? min(n_tiles, (q0 + 63) / kBN + 1) : n_tiles;  // this wave's tiles
+  const int n_half = 2 * n_rel;
+
+  // copies: copy j of a tile by wave j % 4; lane offsets kept in registers
+  auto lane_off = [&](int i, int U, int64_t ss) __attribute__((always_inline)) {
+    const int u = 64 * (NW * i + wave) + lane, row = u / U, ch = u % U;
+    return (ch < CH && row < kBN) ? (row * int(ss) + ch * 8) * 2 : int(0x80000000u);
+  };
+  int koff[NKW], voff[NVW];
+#pragma unroll
+  for (int i = 0; i < NKW; ++i) koff[i] = lane_off(i, UK, p.k_ss);
+#pragma unroll
+  for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, UV, p.v_ss);
+  const uint32_t lds_wave = lds_addr(kv_lds) + uint32_t(wave) * 1024u;
+  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, int dst_off, int tile) __attribute__((always_inline)) {
+    const int kv0 = tile * kBN;
+    const int rows = min(kBN, p.Sk - kv0);
+    const i32x4_t r = tile_desc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
+    uint32_t lw = lds_wave;
+    asm volatile("" : "+s"(lw));
+#pragma unroll
+    for (int i = 0; i < nw; ++i)
+      if (NW * i + wave < n) copy_to_lds(r, lw + uint32_t(2 * dst_off + NW * i * 1024), off[i]);
+  };
+  auto dma_k = [&](int tile, int buf) __attribute__((always_inline)) {
+    dma(kb, p.k_ss, koff, NK, NKW, buf ? kOffK1 : 0, tile);
+  };
+  auto dma_v = [&](int tile, int buf) __attribute__((always_inline)) {
+    dma(vb, p.v_ss, voff, NV, NVW, buf ? kOffV1 : kOffV0, tile);
+  };
+
+  const int vlane = (4 * g + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int klane = c * KS + 8 * g;
+
+  f32x16_t o[QB][NDB];
+#pragma unroll
+  for (int r = 0; r < QB; ++r)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[r][db][e] = 0.f;
+  f32x16_t sc[2][QB];     // S(h) in set h % 2
+  bf16x8_t pf[2][QB][2];  // P(h) in set h % 2: [row block][16-key step]
+  float m_run[QB] = {-INFINITY, -INFINITY}, l_run[QB] = {0.f, 0.f};
+  float alpha[QB] = {1.f, 1.f};  // O rescale owed by the last softmax
+
+  // S(hh) = K(hh) · Qᵀ: key half hh % 2 of the tile in K<buffer>; each K
+  // operand (16-deep step) is read once and used for both row blocks
+  auto qk = [&](int set, int kbuf, int half) __attribute__((always_inline)) {
+    const uint16_t* ks = kv_lds + (kbuf ? kOffK1 : 0) + half * 32 * KS;
+#pragma unroll
+    for (int r = 0; r < QB; ++r)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[set][r][e] = 0.f;
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[klane + 16 * st]);
+#pragma unroll
+      for (int r = 0; r < QB; ++r)
+        sc[set][r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[r][st], sc[set][r], 0, 0, 0);
+    }
+  };
+  // O += P(hh) · V(hh): key half hh % 2 of the tile in V<buffer>; each Vᵀ
+  // operand (16-key step, d block; two transposed reads) used twice
+  auto pv = [&](int set, int vbuf, int half) __attribute__((always_inline)) {
+    const uint16_t* vs = kv_lds + (vbuf ? kOffV1 : kOffV0) + half * 32 * VS;
+#pragma unroll
+    for (int i = 0; i < 2 * NDB; ++i) {
+      const int kst = i / NDB, db = i % NDB;
+      const uint2 lo = lds_read_tr(&vs[vlane + 16 * kst * VS + db * 32]);
+      const uint2 hi = lds_read_tr(&vs[vlane + (16 * kst + 8) * VS + db * 32]);
+      const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+      for (int r = 0; r < QB; ++r)
+        o[r][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf[set][r][kst], o[r][db], 0, 0, 0);
+    }
+  };
+  // softmax of S(hh) into P(hh), in two parts.  softmax_max: mask (MASK),
+  // running max, alpha (the O rescale owed) and the exponent offset; it ends
+  // with the cross-lane exchange (v_permlane32_swap ends a scheduling region).
+  // softmax_exp: P = 2^(s scale - m) packed to bf16, row sum; pure VALU work
+  // that the compiler can interleave with the MFMAs around it.
+  float m_use[QB];
+  auto softmax_max = [&](int set, int hh, auto masked) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(masked)::value;
+    const int k0 = hh * 32;  // first key of the half
+    float mt[QB];
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      const int qrow = q0 + 32 * r + c;
+      if constexpr (MASK) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = k0 + 8 * (e / 4) + 4 * g + (e % 4);
+          if (key >= p.Sk || (CAUSAL && key > qrow)) sc[set][r][e] = -INFINITY;
+        }
+      }
+      mt[r] = sc[set][r][0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mt[r] = fmaxf(mt[r], sc[set][r][e]);
+    }
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      float lo, hi;
+      lane_halves_sched(mt[r], lo, hi);
+      const float m_old = m_run[r];
+      const float m_cand = fmaxf(m_old, fmaxf(lo, hi) * p.scale_log2);
+      // raise the max only when it grows by more than kRescaleLog2; a row
+      // with no unmasked key yet keeps -inf (alpha 1, p = 0)
+      const float m_new = (m_cand > m_old + kRescaleLog2) ? m_cand : m_old;
+      const bool none = m_new == -INFINITY;
+      m_use[r] = none ? 0.f : m_new;
+      // alpha = 2^(m_old - m_new): 1 when not raised, 0 from -inf (the
+      // exponent is clamped at -256, where exp2 is 0)
+      alpha[r] = __builtin_amdgcn_exp2f(none ? 0.f : fmaxf(m_old - m_new, -256.f));
+      m_run[r] = m_new;
+    }
+  };
+  auto softmax_exp = [&](int set) __attribute__((always_inline)) {
+    const bf16x2_t one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+#pragma unroll
+    for (int r = 0; r < QB; ++r) {
+      float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+      for (int j2 = 0; j2 < 2; ++j2) {
+        u32x4_t w;
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          const f32x2_t e = {__builtin_amdgcn_exp2f(fmaf(sc[set][r][8 * j2 + i], p.scale_log2, -m_use[r])),
+                             __builtin_amdgcn_exp2f(fmaf(sc[set][r][8 * j2 + i + 1], p.scale_log2, -m_use[r]))};
+          const bf16x2_t pr = __builtin_convertvector(e, bf16x2_t);
+          w[i / 2] = __builtin_bit_cast(uint32_t, pr);
+          if (i & 2) ls1 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls1, false);
+          else ls0 = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ls0, false);
+        }
+        pf[set][r][j2] = as_bf16x8(w);
+      }
+      l_run[r] = l_run[r] * alpha[r] + (ls0 + ls1);
+    }
+  };
+  auto rescale = [&]() __attribute__((always_inline)) {
+    if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f) != 0) {
+#pragma unroll
+      for (int r = 0; r < QB; ++r)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[r][db][e] *= alpha[r];
+    }
+  };
+
+  // Step hh (see the header).  HP = hh % 2 (the half within tile hh / 2,
+  // and the P / S register sets).  STEADY: every wave has all three parts
+  // and no mask.
+  auto step = [&](int hh, auto hp, auto steady) __attribute__((always_inline)) {
+    constexpr int HP = decltype(hp)::value;
+    constexpr bool ST = decltype(steady)::value;
+    const int t = hh >> 1;  // tile of half hh
+    if constexpr (HP == 0) {
+      wait_copies();
+      lds_barrier();
+      if (t + 2 < n_tiles) dma_k(t + 2, t & 1);
+      if (t + 1 < n_tiles) dma_v(t + 1, (t + 1) & 1);
+    }
+    if (ST || hh < n_half) rescale();
+    if constexpr (ST) {
+      // P·V of half hh, softmax of hh + 1, S of half hh + 2 (the same half
+      // of tile t + 1)
+      softmax_max(1 - HP, hh + 1, Flag<false>{});
+      pv(HP, t & 1, HP);
+      softmax_exp(1 - HP);
+      qk(HP, (t + 1) & 1, HP);
+    } else {
+      if (hh + 1 < n_half) softmax_max(1 - HP, hh + 1, Flag<true>{});
+      if (hh < n_half) pv(HP, t & 1, HP);
+      if (hh + 1 < n_half) softmax_exp(1 - HP);
+      if (hh + 2 < n_half) qk(HP, (t + 1) & 1, HP);
+    }
+  };
+
+  if (n_tiles > 0) {
+    dma_k(0, 0);
+    wait_copies();
+    lds_barrier();
+    if (1 < n_tiles) dma_k(1, 1);
+    dma_v(0, 0);
+    // S(0), S(1) (every wave has key tile 0), softmax(0)
+    qk(0, 0, 0);
+    qk(1, 0, 1);
+    softmax_max(0, 0, Flag<true>{});
+    softmax_exp(0);
+    // steady tiles: all waves active and tiles t, t + 1 unmasked for every
+    // wave (wave 0 has the fewest tiles under the causal mask; its last one
+    // is its diagonal tile)
+    const int n_rel_min = CAUSAL ? min(n_tiles, (qt * kBM + 63) / kBN + 1) : n_tiles;
+    const int n_steady = max(0, min(n_rel_min - 1, p.Sk / kBN));
+    int t = 0;
+    for (; t + 1 < n_steady; ++t) {
+      step(2 * t, Int<0>{}, Flag<true>{});
+      step(2 * t + 1, Int<1>{}, Flag<true>{});
+    }
+    for (; t < n_tiles; ++t) {
+      step(2 * t, Int<0>{}, Flag<false>{});
+      step(2 * t + 1, Int<1>{}, Flag<false>{});
+    }
+  }
+
+  // ---- epilogue (per row block, as in the 8-wave kernel)
+#pragma unroll
+  for (int r = 0; r < QB; ++r) {
+    const int qrow = q0 + 32 * r + c;
+    float l_lo, l_hi;
+    lane_halves(l_run[r], l_lo, l_hi);
+    const float l_tot = l_lo + l_hi;
+    if (qrow < p.Sq) {
+      const float inv = (l_tot > 0.f) ? 1.f / l_tot : __builtin_nanf("");
+      uint16_t* ob = p.o + b * p.o_bs + h * p.o_hs + int64_t(qrow) * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int d = db * 32 + 8 * r4 + 4 * g;
+          const f32x2_t lo = {o[r][db][4 * r4 + 0] * inv, o[r][db][4 * r4 + 1] * inv};
+          const f32x2_t hi = {o[r][db][4 * r4 + 2] * inv, o[r][db][4 * r4 + 3] * inv};
+          uint2 w;
+          w.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2_t));
+          w.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2_t));
+          *reinterpret_cast<uint2*>(ob + d) = w;
+        }
+      }
+      if (p.lse && g == 0) {
+        const float lse2 = (l_tot > 0.f) ? m_run[r] + log2f(l_tot) : -INFINITY;
+        p.lse[int64_t(bh) * p.Sq + qrow] = lse2 * 0.69314718055994531f;
+      }
     }
   }
 }
@@ -442,17 +778,22 @@ extern "C" int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
   a.H = int(H); a.Sq = int(Sq); a.Sk = int(Sk);
   a.BH = int(B * H);
   a.scale_log2 = scale * 1.4426950408889634f;
-  // 8 waves (256 query rows per workgroup) unless that grid would leave
-  // the GPU short of workgroups: then 4 waves (128 rows, two per CU)
-  const int64_t blocks8 = ((Sq + 255) / 256) * a.BH;
-  const int nw = blocks8 < 2 * 256 ? 4 : 8;  // 256 CUs
-  a.n_qtiles = int((Sq + 32 * nw - 1) / (32 * nw));
+  // 256 query rows per workgroup unless that grid would leave the GPU short
+  // of workgroups: then the 4-wave kernel (128 rows, two workgroups per CU).
+  // At 256 rows, head_dim 128 runs the 8-wave ping-pong kernel and head_dim
+  // 64 the wide-wave kernel (measured, warm clocks, causal B4 H16 S8192:
+  // D 128 8-wave 1029 / wide 901 TFLOP/s; D 64 8-wave 775 / wide 922)
+  const int64_t blocks256 = ((Sq + 255) / 256) * a.BH;
+  const bool rows256 = blocks256 >= 2 * 256;  // 256 CUs
+  const int rows = rows256 ? 256 : 128;
+  a.n_qtiles = int((Sq + rows - 1) / rows);
   const int64_t blocks = int64_t(a.n_qtiles) * a.BH;
   if (blocks >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_sdpa_fwd: grid too large");
   hipStream_t s = as_stream(stream);
-  const dim3 g{unsigned(blocks)}, bl{unsigned(64 * nw)};
+  const dim3 g{unsigned(blocks)};
   auto go = [&](auto nwt) {
     constexpr int NW = decltype(nwt)::value;
+    const dim3 bl{unsigned(64 * NW)};
     if (D == 128) {
       if (causal) hipLaunchKernelGGL((sdpa_fwd_kernel<128, true, NW>), g, bl, 0, s, a);
       else hipLaunchKernelGGL((sdpa_fwd_kernel<128, false, NW>), g, bl, 0, s, a);
@@ -461,7 +802,9 @@ extern "C" int mk_sdpa_fwd(void* stream, int64_t B, int64_t H, int64_t Sq, int64
       else hipLaunchKernelGGL((sdpa_fwd_kernel<64, false, NW>), g, bl, 0, s, a);
     }
   };
-  if (nw == 4) go(Int<4>{});
-  else go(Int<8>{});
+  if (!rows256) go(Int<4>{});
+  else if (D == 128) go(Int<8>{});
+  else if (causal) hipLaunchKernelGGL((sdpa_fwd_wide_kernel<64, true>), g, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((sdpa_fwd_wide_kernel<64, false>), g, dim3(256), 0, s, a);
   return check_launch("mk_sdpa_fwd");
 }

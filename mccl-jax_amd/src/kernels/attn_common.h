@@ -52,9 +52,12 @@ __device__ inline i32x4_t tile_desc(const void* base, uint32_t bytes) {
   return i32x4_t{int(uint32_t(a)), int(uint32_t(a >> 32) & 0xFFFFu), int(bytes), kBufferWord3};
 }
 
-// LDS byte address of a __shared__ location
+// LDS byte address of a __shared__ location: the low 32 bits of its generic
+// address (the shared aperture base has zero low bits).  Taking them directly
+// avoids the address-space cast's null check, which keeps 64-bit generic
+// addresses alive in SGPRs.
 __device__ inline uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+  return uint32_t(reinterpret_cast<uintptr_t>(p));
 }
 
 // One 1 KB copy HBM/L2 -> LDS: lane l loads 16 bytes at byte offset voff of
@@ -107,6 +110,17 @@ __device__ inline void lane_halves(float v, float& lo, float& hi) {
   uint32_t b = a;
   asm volatile("" : "+v"(b));
   const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  lo = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
+  hi = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
+// lane_halves without the asm: an inline asm statement ends the compiler's
+// scheduling region, which would keep independent MFMAs from being
+// interleaved across it.  The register allocator gives the two tied operands
+// of v_permlane32_swap separate registers (a copy) by itself.
+__device__ inline void lane_halves_sched(float v, float& lo, float& hi) {
+  const uint32_t a = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
   lo = __builtin_bit_cast(float, static_cast<uint32_t>(r[0]));
   hi = __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
 }

@@ -352,6 +352,39 @@ def test_sdpa_large_scores_rescale(K, causal):
         _sdpa_case(K, 1, 2, 700, D, causal, seed=23, qk_std=0.5, k_ramp=32)
 
 
+@pytest.mark.parametrize("S,Sk,causal,ramp", [(300, None, True, 0), (320, 1000, False, 0), (700, None, True, 8),
+                                               (700, None, False, 32), (64, None, True, 0)])
+def test_sdpa_wide_kernel_d64(K, S, Sk, causal, ramp):
+    """head_dim 64 with at least 512 workgroups of 256 query rows (B2 H128):
+    the wide-wave kernel (64 query rows per wave, 32-key half steps).
+    Ragged query and key lengths, cross lengths, the causal diagonal and
+    rising scores that raise the running max on many half steps."""
+    print(f"case: sdpa wide D=64 S={S} Sk={Sk} causal={causal} ramp={ramp}", flush=True)
+    _sdpa_case(K, 2, 128, S, 64, causal, seed=S + (Sk or 0) + ramp, Sk=Sk,
+               qk_std=0.5 if ramp else 1 / math.sqrt(128), k_ramp=ramp)
+
+
+def test_sdpa_wide_kernel_d64_long_sampled_rows(K):
+    """B4 H16 S8192 D64 causal (the wide kernel at a benchmark length): row 0
+    equals V[0] exactly; 4 (b,h) pairs x ~40 rows against the float64 oracle."""
+    B, H, S, D = 4, 16, 8192, 64
+    rng = np.random.default_rng(31)
+    x = [bf16.to_bf16_bits((rng.standard_normal((B, H, S, D)) / 8).astype(np.float32)) for _ in range(3)]
+    print("case: sdpa wide D=64 B4 H16 S8192 causal", flush=True)
+    o = host_bf16(K.sdpa_fwd(*(dev_bf16(a) for a in x), 0.125, True))
+    np.testing.assert_array_equal(o[:, :, 0, :], x[2][:, :, 0, :])
+    rows = np.array(sorted(set([1, 31, 32, 63, 64, 255, 256, 4095, 4096, S - 2, S - 1] +
+                               list(rng.integers(0, S, 30)))))
+    for b, h in [(0, 0), (1, 7), (2, 12), (3, 15)]:
+        qf, kf, vf = (bf16.from_bf16_bits(a[b, h]).astype(np.float64) for a in x)
+        sc = (qf[rows] @ kf.T) * 0.125
+        sc[np.arange(S)[None, :] > rows[:, None]] = -np.inf
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        want = (p @ vf) / p.sum(axis=1, keepdims=True)
+        got = bf16.from_bf16_bits(o[b, h, rows]).astype(np.float64)
+        assert np.abs(got - want).max() <= 2e-3, (b, h, np.abs(got - want).max())
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_sdpa_strided_views(K, D):
     """[B, S, H, D] storage (the layout a head split produces) passed as a
