@@ -83,6 +83,19 @@ __device__ inline void copy_to_lds(const i32x4_t& rsrc, uint32_t dst, int voff) 
                : "memory");
 }
 
+// copy_to_lds with an SGPR byte offset added to voff (the same wave-uniform
+// step for every lane), under the same rules: descriptor, offset and LDS
+// address read in SGPRs behind s_nop 4.
+__device__ inline void copy_to_lds_so(const i32x4_t& rsrc, uint32_t dst, int voff, uint32_t soff) {
+  const i32x4_t r = {__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
+                     __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)),
+                 "{m0}"(__builtin_amdgcn_readfirstlane(dst))
+               : "memory");
+}
+
 // wait until every copy this wave has issued has landed in LDS
 __device__ inline void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 

@@ -15,17 +15,23 @@
 // k tile t + S - 1 are issued before tile t is multiplied, one barrier per
 // tile.  Each operand keeps the orientation it has in memory:
 //   k-contiguous (A[m][k], or B stored as [n][k]): LDS rows of BK k, 16-byte
-//     chunk c of row r stored at chunk position c ^ (r & 7) (BK = 64) or
-//     c ^ ((r >> 1) & 3) (BK = 32), read with one ds_read_b128 per MFMA
+//     chunk c of row r stored at chunk position c ^ ((r >> 1) & 7) (BK = 64)
+//     or c ^ ((r >> 2) & 3) (BK = 32), read with one ds_read_b128 per MFMA
 //     operand (8 consecutive k);
 //   m- / n-contiguous (A stored as [k][m], B[k][n]): one LDS row of R columns
-//     per k, chunk c of k-row r stored at position c ^ 2 (r & 3), read with
-//     two ds_read_b64_tr_b16 per operand, which hand each lane one column over
-//     4 consecutive k (k-rows 8g .. 8g + 3, then 8g + 4 .. 8g + 7).
+//     per k, chunk c of k-row r stored at position c ^ 4 (r & 3) (R a
+//     multiple of 128) or c ^ 4 ((r >> 1) & 1) (R = 192), read with two
+//     ds_read_b64_tr_b16 per operand, which hand each lane one column over 4
+//     consecutive k (k-rows 8g .. 8g + 3, then 8g + 4 .. 8g + 7).
 // Both forms give lane (c, g) of an MFMA operand column/row c and k = 8 g ..
-// 8 g + 7 in order, so any pairing of orientations multiplies correctly, and
-// the XOR placements spread each read over all LDS banks.  Chunks past M, N
-// or K are loaded from an out-of-range buffer offset, which reads zeros.
+// 8 g + 7 in order, so any pairing of orientations multiplies correctly.
+// The XOR placements make every read conflict-free on gfx950's LDS (64 banks
+// of 4 bytes): a ds_read_b128 serves 16 lanes per cycle, which must cover
+// all 256 bank bytes, here 16 rows at one chunk; a ds_read_b64_tr_b16 serves
+// 32 lanes, here 4 k-rows x 4 chunks.  (An XOR with r & 7, or 2 (r & 3),
+// leaves two rows of each group on the same banks and halves the read rate.)
+// Chunks past M, N or K are loaded from an out-of-range buffer offset, which
+// reads zeros.
 //
 // Tile order: workgroups are dealt round-robin to the 8 XCDs, each with its
 // own L2, so workgroup i takes tile (i % 8) * (tiles / 8) + i / 8 of an
@@ -68,14 +74,27 @@ struct TiledGemm {
 //        position ^ kc_swizzle(row)
 //   !KC: LDS k-row u / (R / 8), position u % (R / 8), holding global chunk
 //        position ^ 2 (k-row & 3)
-// Each copy keeps its byte offset for the first k tile and the first k it
-// reads (past every K when its row is outside the operand); tile t adds t
-// times the per-tile step, so the loop carries two registers per copy.
-// chunk placement of a k-contiguous LDS row: conflict-free ds_read_b128 of
-// 8 consecutive rows at one chunk
+// Each copy keeps its byte offset for the first k tile (an out-of-range
+// offset when its row is outside the operand) and the first k it reads (past
+// every K for such a row).  A k tile wholly inside K passes t times the
+// per-tile step as the instruction's SGPR offset, so its copies need no
+// vector arithmetic; only the tile that crosses K compares each copy's k.
+// chunk placement of a k-contiguous LDS row (BK / 8 chunks): the 16 rows one
+// ds_read_b128 cycle reads at one chunk land on 16 different 16-byte bank
+// groups (rows 2 (64 B) or 4 (32 B) apart share the row's bank offset)
 template <int BK>
 __device__ inline int kc_swizzle(int row) {
-  return BK == 64 ? (row & 7) : ((row >> 1) & 3);
+  return BK == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+// chunk placement of an m- / n-contiguous LDS k-row (R / 8 chunks): the 4
+// k-rows x 4 chunks of one ds_read_b64_tr_b16 half-wave land on 16 different
+// bank groups; the XOR keeps each chunk inside its aligned group of 8 (R =
+// 192) or 16 chunks
+template <int R>
+__device__ inline int nc_swizzle(int kr) {
+  static_assert(R % 64 == 0, "k-row of whole 8-chunk groups");
+  return R % 128 == 0 ? 4 * (kr & 3) : 4 * ((kr >> 1) & 1);
 }
 
 template <bool KC, int R, int BK, int kC, int W>
@@ -96,11 +115,12 @@ struct Copies {
       } else {
         constexpr int kCpr = R / 8;
         const int kr = u / kCpr;
-        gr = r0 + 8 * ((u % kCpr) ^ (2 * (kr & 3)));
+        gr = r0 + 8 * ((u % kCpr) ^ nc_swizzle<R>(kr));
         gk = kr;
         off[c] = uint32_t((gk * ld + gr) * 2);
       }
       k[c] = gr < rows ? int32_t(gk) : 0x7fffffff - BK;
+      if (gr >= rows) off[c] = uint32_t(kInvalid);  // kInvalid + any step stays past every range
     }
   }
   // offset for the k tile starting at k0 (step: its byte distance from the
@@ -122,9 +142,9 @@ __device__ inline bf16x8_t read_operand(const uint16_t* t, int rb, int ks, int l
     // 8 bytes (4 columns) each; lane i of the group receives column i.
     const int kr = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
     const int col = rb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    const int at = 8 * ((col >> 3) ^ (2 * (kr & 3))) + (col & 7);
+    const int at = 8 * ((col >> 3) ^ nc_swizzle<R>(kr)) + (col & 7);
     const uint2 lo = lds_read_tr(t + kr * R + at);
-    const uint2 hi = lds_read_tr(t + (kr + 4) * R + at);  // (kr + 4) & 3 == kr & 3
+    const uint2 hi = lds_read_tr(t + (kr + 4) * R + at);  // k-row kr + 4 has kr's swizzle
     return as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
   }
 }
@@ -154,8 +174,9 @@ __device__ inline void finish4(const TiledGemm& p, int64_t n, float (&v)[4]) {
 // 16-bit C through LDS.  Lanes l and l + 32 trade halves (v_permlane32_swap)
 // so that each holds 8 consecutive columns: from the pair (rg 2h, rg 2h + 1)
 // lane g gets the chunk of columns 16 h + 8 g .. + 7 of its block.  Chunks go
-// to LDS rows of TN columns at chunk position ^ (row & 15, or & 7 when a row
-// has fewer than 16 chunks).  Then the workgroup stores runs of consecutive
+// to LDS rows of TN columns at chunk position ^ (row & 15) when a row holds a
+// multiple of 16 chunks, else ^ ((row >> 1) & 7) (rows of 8 mod 16 chunks:
+// rows 2 apart share the bank offset).  Then the workgroup stores runs of consecutive
 // C rows: whole 16-byte chunks when C rows are 16-byte aligned (ROWS16),
 // else one element per thread, consecutive threads on consecutive columns.
 template <int CT, bool ROWS16, int TM, int TN, int kW, int kWM, int kWN, int kI, int kJ>
@@ -164,7 +185,10 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
                                                                    int64_t m0, int64_t n0, int wm, int wn,
                                                                    int lane, int64_t bz) {
   constexpr int kCpr = TN / 8;
-  constexpr int kSw = kCpr % 16 == 0 ? 15 : 7;
+  static_assert(kCpr % 8 == 0, "staging rows of whole 8-chunk groups");
+  // chunk position of chunk cn in staging row r: the 16 rows one ds_write_b128
+  // cycle writes at one chunk land on 16 different bank groups
+  auto pos = [](int r, int cn) { return kCpr % 16 == 0 ? cn ^ (r & 15) : cn ^ ((r >> 1) & 7); };
   const int c = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int a = 0; a < kI; ++a) {
@@ -189,7 +213,7 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
         const u32x4_t chunk = {static_cast<uint32_t>(s0[0]), static_cast<uint32_t>(s1[0]),
                                static_cast<uint32_t>(s0[1]), static_cast<uint32_t>(s1[1])};
         const int cn = (nb + 16 * h + 8 * g) >> 3;
-        *reinterpret_cast<u32x4_t*>(st + ml * TN + 8 * (cn ^ (ml & kSw))) = chunk;
+        *reinterpret_cast<u32x4_t*>(st + ml * TN + 8 * pos(ml, cn)) = chunk;
       }
     }
   }
@@ -202,7 +226,7 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
     for (int it = 0; it < TM * TN / kThreads; ++it) {
       const int e = it * kThreads + int(threadIdx.x);
       const int row = e / TN, col = e % TN;
-      const uint16_t v = st[row * TN + 8 * ((col >> 3) ^ (row & kSw)) + (col & 7)];
+      const uint16_t v = st[row * TN + 8 * pos(row, col >> 3) + (col & 7)];
       const int64_t m = m0 + row, n = n0 + col;
       if (m < p.M && n < p.N) Ce[m * p.ldc + n] = v;
     }
@@ -212,7 +236,7 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
   for (int it = 0; it < TM * kCpr / kThreads; ++it) {
     const int e = it * kThreads + int(threadIdx.x);
     const int row = e / kCpr, cn = e % kCpr;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * (cn ^ (row & kSw)));
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * pos(row, cn));
     const int64_t m = m0 + row, n = n0 + 8 * cn;
     if (m < p.M && n < p.N) *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
   }
@@ -301,14 +325,29 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   // byte distance between consecutive k tiles
   const uint32_t a_step = AKC ? 2 * BK : uint32_t(2 * BK * p.lda);
   const uint32_t b_step = BKC ? 2 * BK : uint32_t(2 * BK * p.ldb);
-  auto issue = [&](int kt, int stage) __attribute__((always_inline)) {
+  // this wave's copies [lo, hi) of k tile kt into stage (A's kCa copies first,
+  // then B's kCb)
+  auto issue = [&](int kt, int stage, int lo, int hi) __attribute__((always_inline)) {
     const int k0 = BK * kt;
+    if (k0 + BK <= p.K) {
+      const uint32_t sa = uint32_t(kt) * a_step, sb = uint32_t(kt) * b_step;
 #pragma unroll
-    for (int c = 0; c < kCa; ++c)
-      copy_to_lds(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), ca.at(c, k0, uint32_t(kt) * a_step, p.K));
+      for (int c = 0; c < kCa + kCb; ++c) {
+        if (c < lo || c >= hi) continue;
+        if (c < kCa) copy_to_lds_so(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), int(ca.off[c]), sa);
+        else copy_to_lds_so(rb, lds_addr(&Bs[stage][(wave + kW * (c - kCa)) * 512]), int(cb.off[c - kCa]), sb);
+      }
+      return;
+    }
 #pragma unroll
-    for (int c = 0; c < kCb; ++c)
-      copy_to_lds(rb, lds_addr(&Bs[stage][(wave + kW * c) * 512]), cb.at(c, k0, uint32_t(kt) * b_step, p.K));
+    for (int c = 0; c < kCa + kCb; ++c) {
+      if (c < lo || c >= hi) continue;
+      if (c < kCa)
+        copy_to_lds(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), ca.at(c, k0, uint32_t(kt) * a_step, p.K));
+      else
+        copy_to_lds(rb, lds_addr(&Bs[stage][(wave + kW * (c - kCa)) * 512]),
+                    cb.at(c - kCa, k0, uint32_t(kt) * b_step, p.K));
+    }
   };
 
   f32x16_t acc[kI][kJ];
@@ -323,16 +362,20 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   // for its own copies of it (the S - 2 tiles issued after it may still be in
   // flight), then the barrier makes every wave's copies visible and also
   // marks stage (kt - 1) % S, read in the previous iteration, free for the
-  // copies of tile kt + S - 1.
+  // copies of tile kt + S - 1.  Those copies are issued in kParts groups,
+  // each after the operand reads of one k-step: a wave that issued all of
+  // them at once would stall on the full vector-memory queue (1 KB copies
+  // drain at about 60 bytes per clock per CU) with its MFMAs behind them.
   const int nk = int((p.K + BK - 1) / BK);
+  constexpr int kNC = kCa + kCb, kParts = BK / 16 < 2 ? BK / 16 : 2;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
-    if (st < nk) issue(st, st);
+    if (st < nk) issue(st, st, 0, kNC);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + S - 2 < nk) wait_vm<(S - 2) * (kCa + kCb)>();
+    if (kt + S - 2 < nk) wait_vm<(S - 2) * kNC>();
     else wait_vm<0>();
     lds_barrier();
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const bool more = kt + S - 1 < nk;
     const uint16_t* at = As[kt % S];
     const uint16_t* bt = Bs[kt % S];
 #pragma unroll
@@ -342,6 +385,7 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
       for (int a = 0; a < kI; ++a) af[a] = read_operand<AKC, TM, BK>(at, wm * kWM + 32 * a, ks, lane);
 #pragma unroll
       for (int b = 0; b < kJ; ++b) bfr[b] = read_operand<BKC, TN, BK>(bt, wn * kWN + 32 * b, ks, lane);
+      if (more && ks < kParts) issue(kt + S - 1, (kt + S - 1) % S, ks * kNC / kParts, (ks + 1) * kNC / kParts);
 #pragma unroll
       for (int a = 0; a < kI; ++a)
 #pragma unroll
