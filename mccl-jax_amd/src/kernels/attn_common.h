@@ -84,12 +84,16 @@ __device__ inline void copy_to_lds(const i32x4_t& rsrc, uint32_t dst, int voff) 
 }
 
 // copy_to_lds with an SGPR byte offset added to voff (the same wave-uniform
-// step for every lane), under the same rules: descriptor, offset and LDS
-// address read in SGPRs behind s_nop 4.
+// step for every lane), for callers whose descriptor and offset are
+// wave-uniform values the compiler keeps in SGPRs (computed by SALU, not
+// passed through a VALU readfirstlane right before the copy): it waits only
+// the one state the M0 write needs (s_nop 0).  tests/test_asm_hazards.py
+// checks every copy of the compiled kernels for a VALU write of one of its
+// SGPRs fewer than 5 wait states earlier.
 __device__ inline void copy_to_lds_so(const i32x4_t& rsrc, uint32_t dst, int voff, uint32_t soff) {
   const i32x4_t r = {__builtin_amdgcn_readfirstlane(rsrc.x), __builtin_amdgcn_readfirstlane(rsrc.y),
                      __builtin_amdgcn_readfirstlane(rsrc.z), __builtin_amdgcn_readfirstlane(rsrc.w)};
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
                : "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)),
                  "{m0}"(__builtin_amdgcn_readfirstlane(dst))

@@ -486,30 +486,35 @@ int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, i
   if (!tiled_args(a, a_kc, b_kc, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs, c_ms,
                   bias, epilogue))
     return -1;
-  // Kernel shape: the one with the least estimated time, counting whole
-  // rounds of workgroups over the CUs (one 256 x 256 workgroup per CU; the
-  // 4-wave shapes fit two per CU) and each shape's throughput per slot as
-  // measured on large products (8192 x 8192 x 4096: 1077, 1058 and 980
-  // TFLOP/s), so small tile counts weigh quantisation against tile size.
+  // Kernel shape: the one with the least estimated time.  Each shape has a
+  // throughput per CU measured on a large product (8192 x 8192 x 4096: 1240,
+  // 1083 and 1017 TFLOP/s) and a number of workgroups a CU holds at once (one
+  // 256 x 256 workgroup, two of the smaller ones).  Whole rounds of
+  // workgroups over the CUs run at that throughput; a last partial round
+  // that leaves every workgroup alone on its CU runs each at about 0.8 of it
+  // (a CU's throughput with one 8-wave workgroup instead of two, measured on
+  // the 8192 x 768 products with K = 768 .. 3072).
   struct Option {
     int tm, tn, per_cu;
     double rate;
   };
-  static const Option options[3] = {{256, 256, 1, 1077.0}, {128, 192, 2, 1058.0}, {128, 128, 2, 980.0}};
-  const int64_t slots_cu = cu_count();
+  static const Option options[3] = {{256, 256, 1, 1240.0}, {128, 192, 2, 1083.0}, {128, 128, 2, 1017.0}};
+  const int64_t cus = cu_count();
   int best = -1;
   double best_t = 0;
   for (int o = 0; o < 3; ++o) {
     const Option& op = options[o];
     if (M < op.tm || N < op.tn) continue;
     const int64_t tiles = ((M + op.tm - 1) / op.tm) * ((N + op.tn - 1) / op.tn) * batch;
-    const int64_t slots = slots_cu * op.per_cu;
-    const double t = double((tiles + slots - 1) / slots) * op.tm * op.tn * op.per_cu / op.rate;
+    const int64_t slots = cus * op.per_cu, rem = tiles % slots;
+    const double tile = double(op.tm) * op.tn / op.rate;
+    double t = double(tiles / slots) * op.per_cu * tile;
+    if (rem > 0) t += (op.per_cu > 1 && rem <= cus) ? tile / 0.8 : op.per_cu * tile;
     if (best < 0 || t < best_t) best = o, best_t = t;
   }
   if (best == 0) return launch<Shape<256, 256, 2, 4, 64, 2>>(s, a, batch, a_kc, b_kc);
-  if (best == 1) return launch<Shape<128, 192, 2, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
-  return launch<Shape<128, 128, 2, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
+  if (best == 1) return launch<Shape<128, 192, 4, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
+  return launch<Shape<128, 128, 4, 2, 64, 2>>(s, a, batch, a_kc, b_kc);
 }
 
 }  // namespace mk
