@@ -244,7 +244,10 @@ C5_GEMMS = [
 def run_gemm(torch, np, K, args):
     """mk_gemm (hand-written MFMA) and mk_gemm_blas (rocBLAS) on the C5 step's
     15 GEMM shapes, and C1's two fp32 GEMMs (bias + ReLU, bias epilogues) on
-    mk_gemm; TFLOP/s against the bf16 (2516.6) or fp32 (157.3) peak."""
+    mk_gemm; TFLOP/s against the bf16 (2516.6) or fp32 (157.3) peak.  The
+    fp32 weight-gradient shapes are also timed split along K as the C5 step
+    runs them (mk_gemm_splitk, and rocBLAS with the same slices)."""
+    from mi355x_pjrt.gpt2 import GPT2TrainStep
     from oracle import inputs
 
     res = {}
@@ -266,8 +269,17 @@ def run_gemm(torch, np, K, args):
             ms = time_launches(torch, fn, max(5, args.steps // 2), 3)
             row[name + "_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
         row["mk_gemm_frac_peak"] = round(row["mk_gemm_tflops"] / PEAK_BF16_TFLOPS, 4)
+        msg = f"gemm {tag} [{M}x{N}x{Kd}]: mk_gemm {row['mk_gemm_tflops']} TFLOP/s, rocBLAS {row['rocblas_tflops']}"
+        sp = GPT2TrainStep.DW_SPLITS.get(tag, 1)
+        if sp > 1:  # the C5 step runs these fp32 weight gradients split along K
+            for name, fn in (("mk_gemm_splitk", lambda: K.gemm_splitk(a, b, sp, out=c)),
+                             ("rocblas_splitk", lambda: K.gemm_blas_splitk(a, b, sp, out=c))):
+                ms = time_launches(torch, fn, max(5, args.steps // 2), 3)
+                row[name + "_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+            row["splits"] = sp
+            msg += f"; split {sp}: mk_gemm_splitk {row['mk_gemm_splitk_tflops']}, rocBLAS {row['rocblas_splitk_tflops']}"
         res[tag] = row
-        log(f"gemm {tag} [{M}x{N}x{Kd}]: mk_gemm {row['mk_gemm_tflops']} TFLOP/s, rocBLAS {row['rocblas_tflops']}")
+        log(msg)
         del a, b, c
     d = inputs.c1_mlp()
     x, w1, b1, w2, b2 = (torch.from_numpy(d[n]).cuda() for n in ("x", "w1", "b1", "w2", "b2"))
