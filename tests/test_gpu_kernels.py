@@ -261,6 +261,18 @@ def test_scatter_add_edge_cases(K):
         got = K.scatter_add_rows(torch.from_numpy(table).cuda(), torch.from_numpy(ids).cuda(),
                                  torch.from_numpy(upd).cuda()).cpu().numpy()
         np.testing.assert_array_equal(got, native.scatter_add_f32(table, ids, upd), err_msg=name)
+    # tables on both sides of the 16-bit key limit of the three-launch sort
+    # (n_rows < 65535; larger tables take the multi-pass radix sort), with
+    # out-of-range ids and a hot row
+    for n_rows in (65534, 65535, 70001):
+        print(f"case: scatter-add rows={n_rows}", flush=True)
+        tb = rng.standard_normal((n_rows, 4)).astype(np.float32)
+        ids = np.concatenate([rng.integers(-10, n_rows + 10, size=20000), np.full(3000, n_rows - 1)])
+        ids = rng.permutation(ids).astype(np.int32)
+        upd = rng.standard_normal((ids.size, 4)).astype(np.float32)
+        got = K.scatter_add_rows(torch.from_numpy(tb).cuda(), torch.from_numpy(ids).cuda(),
+                                 torch.from_numpy(upd).cuda()).cpu().numpy()
+        np.testing.assert_array_equal(got, native.scatter_add_f32(tb, ids, upd), err_msg=f"rows={n_rows}")
     # int64 ids, ragged row length (scalar path), bf16 rows rounded after every add
     ids = rng.integers(0, 40, size=700)
     tb = bf16.to_bf16_bits(rng.standard_normal((40, 9)).astype(np.float32))
