@@ -2586,7 +2586,40 @@ class Lowerer {
     const TensorType& t = m_.types[op.results[0]];
     int64_t outer = 1;
     for (int64_t k = 0; k < dim; ++k) outer *= t.dims[k];
-    if (outer != 1) throw std::string("jam: concatenate is supported along the outermost non-unit dim only");
+    if (outer != 1) {
+      // Along an inner dim the result is stored with `dim` outermost: each
+      // operand, viewed with `dim` moved first, is copied densely into its
+      // block, and consumers get the permuted (strided) view of the buffer.
+      std::vector<int> order{int(dim)};
+      for (int k = 0; k < t.rank(); ++k)
+        if (k != dim) order.push_back(k);
+      BufRef d = NewTemp(t.bytes());
+      int64_t off = 0;
+      for (int v : op.operands) {
+        const View& sv = NeedView(v);
+        View pv = sv;
+        for (size_t k = 0; k < order.size(); ++k) {
+          pv.dims[k] = sv.dims[order[k]];
+          pv.strides[k] = sv.strides[order[k]];
+        }
+        BufRef part = d;
+        part.offset += off;
+        EmitCopy(pv, part);
+        off += int64_t(m_.types[v].bytes());
+      }
+      std::vector<int64_t> pdims;
+      for (int k : order) pdims.push_back(t.dims[k]);
+      const std::vector<int64_t> ps = DenseStrides(pdims);
+      View rv;
+      rv.buf = d;
+      rv.offset = 0;
+      rv.dtype = t.dtype;
+      rv.dims = t.dims;
+      rv.strides.assign(t.rank(), 0);
+      for (size_t k = 0; k < order.size(); ++k) rv.strides[order[k]] = ps[k];
+      SetView(op.results[0], rv);
+      return;
+    }
     BufRef d = DestFor(op.results[0]);
     int64_t off = 0;
     for (int v : op.operands) {
