@@ -86,6 +86,8 @@ struct EwArgs {
   int out_reg;
   int out_type;
   int need_index;  // some input is strided: decompose the linear index
+  int in_vec[kEwMaxInputs];  // vector form: 4 consecutive elements in one 16-byte (f32) / 8-byte (bf16) load
+  int out_vec;               // vector form: 4 consecutive outputs in one store
   int32_t prog[kEwMaxInstr][4];
   float consts[kEwMaxConsts];
 };
@@ -124,32 +126,9 @@ __device__ inline float sign_f(float x) {
   return x > 0.f ? 1.f : (x < 0.f ? -1.f : x);  // keeps ±0 and NaN
 }
 
-// The whole program block travels as a by-value kernel argument (< 2 KiB),
-// so a launch needs no device-side staging buffer.
-__global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n, void* out) {
-  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (i >= n) return;
-  float r[kEwMaxRegs];
-#pragma unroll
-  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
-  const int rank = A.rank;
-  int64_t idx[kEwMaxRank];
-  if (A.need_index) {
-    int64_t rem = i;
-    for (int d = rank - 1; d >= 0; --d) {
-      idx[d] = rem % A.dims[d];
-      rem /= A.dims[d];
-    }
-  }
-  for (int t = 0; t < A.n_inputs; ++t) {
-    int64_t off = 0;
-    if (A.in_mode[t] == 1) {
-      off = i;
-    } else if (A.in_mode[t] == 2) {
-      for (int d = 0; d < rank; ++d) off += idx[d] * A.in_stride[t][d];
-    }
-    r[t] = ew_load(A.in[t], off, A.in_type[t]);
-  }
+// Runs the program on the register file r (inputs already in r[0 ..
+// n_inputs)).
+__device__ __attribute__((always_inline)) inline void ew_run(const EwArgs& A, float (&r)[kEwMaxRegs]) {
   for (int p = 0; p < A.n_instr; ++p) {
     const int op = A.prog[p][0], dst = A.prog[p][1], a = A.prog[p][2], b = A.prog[p][3];
     const float va = r[a];
@@ -218,7 +197,109 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
     }
     r[dst] = o;
   }
+}
+
+// The whole program block travels as a by-value kernel argument (< 2 KiB),
+// so a launch needs no device-side staging buffer.
+__global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n, void* out) {
+  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  float r[kEwMaxRegs];
+#pragma unroll
+  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
+  const int rank = A.rank;
+  int64_t idx[kEwMaxRank];
+  if (A.need_index) {
+    int64_t rem = i;
+    for (int d = rank - 1; d >= 0; --d) {
+      idx[d] = rem % A.dims[d];
+      rem /= A.dims[d];
+    }
+  }
+  for (int t = 0; t < A.n_inputs; ++t) {
+    int64_t off = 0;
+    if (A.in_mode[t] == 1) {
+      off = i;
+    } else if (A.in_mode[t] == 2) {
+      for (int d = 0; d < rank; ++d) off += idx[d] * A.in_stride[t][d];
+    }
+    r[t] = ew_load(A.in[t], off, A.in_type[t]);
+  }
+  ew_run(A, r);
   ew_store(out, i, A.out_type, r[A.out_reg]);
+}
+
+// The same program on kEwVec consecutive elements of the innermost dim per
+// thread (the host uses it when that dim is a multiple of kEwVec and every
+// index and input offset fits 32 bits): the multi-dim index is decomposed
+// once per thread in 32-bit arithmetic, and the inputs of all kEwVec
+// elements are loaded before the program runs on the first of them.
+constexpr int kEwVec = 4;
+__global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, uint32_t n, void* out) {
+  const uint32_t i0 = (blockIdx.x * uint32_t(kBlock) + threadIdx.x) * kEwVec;
+  if (i0 >= n) return;
+  uint32_t idx[kEwMaxRank];
+  if (A.need_index) {
+    uint32_t rem = i0;
+    for (int d = A.rank - 1; d >= 0; --d) {
+      const uint32_t n_d = uint32_t(A.dims[d]);
+      idx[d] = rem % n_d;
+      rem /= n_d;
+    }
+  }
+  float v[kEwVec][kEwMaxInputs];
+#pragma unroll
+  for (int t = 0; t < kEwMaxInputs; ++t) {
+    if (t >= A.n_inputs) break;
+    int32_t off = 0, step = 0;
+    if (A.in_mode[t] == 1) {
+      off = int32_t(i0);
+      step = 1;
+    } else if (A.in_mode[t] == 2) {
+      for (int d = 0; d < A.rank; ++d) off += int32_t(idx[d]) * int32_t(A.in_stride[t][d]);
+      step = int32_t(A.in_stride[t][A.rank - 1]);
+    }
+    if (A.in_vec[t] && A.in_type[t] == MK_F32) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(A.in[t]) + off);
+#pragma unroll
+      for (int e = 0; e < kEwVec; ++e) v[e][t] = w.v[e];
+    } else if (A.in_vec[t]) {  // bf16
+      const uint2 w = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(A.in[t]) + off);
+      v[0][t] = bf16_to_f32(uint16_t(w.x));
+      v[1][t] = bf16_to_f32(uint16_t(w.x >> 16));
+      v[2][t] = bf16_to_f32(uint16_t(w.y));
+      v[3][t] = bf16_to_f32(uint16_t(w.y >> 16));
+    } else {
+#pragma unroll
+      for (int e = 0; e < kEwVec; ++e) v[e][t] = ew_load(A.in[t], off + e * step, A.in_type[t]);
+    }
+  }
+  float r[kEwMaxRegs];
+#pragma unroll
+  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
+  // one copy of the interpreter: element e's inputs and result move by
+  // selects, so no register array is indexed by e
+  float o[kEwVec] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int e = 0; e < kEwVec; ++e) {
+#pragma unroll
+    for (int t = 0; t < kEwMaxInputs; ++t)
+      if (t < A.n_inputs) r[t] = e == 0 ? v[0][t] : e == 1 ? v[1][t] : e == 2 ? v[2][t] : v[3][t];
+    ew_run(A, r);
+    const float res = r[A.out_reg];
+#pragma unroll
+    for (int k = 0; k < kEwVec; ++k) o[k] = e == k ? res : o[k];
+  }
+  if (A.out_vec && A.out_type == MK_F32) {
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + i0) = f32x4{{o[0], o[1], o[2], o[3]}};
+  } else if (A.out_vec) {  // bf16
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i0) =
+        uint2{f32_to_bf16(o[0]) | (uint32_t(f32_to_bf16(o[1])) << 16),
+              f32_to_bf16(o[2]) | (uint32_t(f32_to_bf16(o[3])) << 16)};
+  } else {
+#pragma unroll
+    for (int e = 0; e < kEwVec; ++e) ew_store(out, int64_t(i0) + e, A.out_type, o[e]);
+  }
 }
 
 // ------------------------------------------------------------------ convert / fill / iota
@@ -410,8 +491,45 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
   }
   for (int c = 0; c < n_consts; ++c) a.consts[c] = consts[c];
   a.need_index = need_index;
-  hipLaunchKernelGGL(ew_program_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
-                     as_stream(stream), a, n, out);
+  // 32-bit form: the innermost dim a multiple of kEwVec, n and every input's
+  // largest offset below 2^31
+  bool narrow = rank >= 1 && dims[rank - 1] % kEwVec == 0 && n < (int64_t(1) << 31);
+  for (int t = 0; narrow && t < n_inputs; ++t) {
+    int64_t hi = 0;
+    for (int d = 0; d < rank; ++d) {
+      const int64_t st = a.in_stride[t][d];
+      if (st < 0) narrow = false;
+      hi += (dims[d] - 1) * st;
+    }
+    narrow = narrow && hi < (int64_t(1) << 31) - kEwVec;
+  }
+  if (narrow) {
+    // vector accesses: f32 / bf16 data whose 4 consecutive elements are
+    // adjacent (unit innermost stride) and aligned (base aligned, every other
+    // stride a multiple of 4 elements)
+    auto vec_ok = [&](const void* base, int type, const int64_t* st) {
+      const int w = type == MK_F32 ? 4 : type == MK_BF16 ? 2 : 0;
+      if (w == 0 || (reinterpret_cast<uintptr_t>(base) & uintptr_t(4 * w - 1)) != 0) return false;
+      if (st[rank - 1] != 1) return false;
+      for (int d = 0; d + 1 < rank; ++d)
+        if (st[d] % kEwVec != 0) return false;
+      return true;
+    };
+    for (int t = 0; t < n_inputs; ++t) a.in_vec[t] = a.in_mode[t] != 0 && vec_ok(a.in[t], a.in_type[t], a.in_stride[t]);
+    int64_t dense[kEwMaxRank];
+    int64_t acc = 1;
+    for (int d = rank - 1; d >= 0; --d) {
+      dense[d] = acc;
+      acc *= dims[d];
+    }
+    a.out_vec = vec_ok(out, out_type, dense);
+  }
+  if (narrow)
+    hipLaunchKernelGGL(ew_program_vec_kernel, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
+                       as_stream(stream), a, uint32_t(n), out);
+  else
+    hipLaunchKernelGGL(ew_program_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
+                       as_stream(stream), a, n, out);
   return check_launch("mk_ew_program");
 }
 
