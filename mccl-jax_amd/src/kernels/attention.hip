@@ -13,7 +13,7 @@
 // a VALU op: no LDS round trip on the softmax's critical path).  Those same
 // registers, converted to bf16, ARE the B operand of Oᵀ = Vᵀ · Pᵀ: the k-slot
 // (g, i) of P corresponds to key 16*j + 4*g + 8*(i/4) + i%4 of the 16-key
-// step j.  V stays row-major in LDS; the A operand (Vᵀ) is read with
+// step j.  V is not transposed in LDS; the A operand (Vᵀ) is read with
 // ds_read_b64_tr_b16, which hands each lane of a 16-lane group one column of
 // a 4-key x 16-d block: two such reads give the 8 k-slots of a lane.
 //
@@ -28,14 +28,14 @@
 //
 // K and V tiles go from HBM/L2 straight into LDS (buffer_load_dwordx4 ... lds:
 // lane l of a wave writes bytes [16 l, 16 l + 16) of a 1 KB LDS block, from
-// any global address), so no registers stage them.  Rows are padded in LDS
-// (K by 16 bytes, V by 64 bytes) so that the K reads (32 rows, one chunk
-// each) and the transposed V reads (4 rows x 2 chunks per 16 lanes) hit
-// distinct banks; the lanes whose 16 bytes fall on padding fetch from an
-// out-of-range offset, which the buffer unit answers with zeros.  The
-// descriptor of a tile ends at its last valid key, so rows past Sk are zeros
-// too.  The copies are issued from inline assembly, so the compiler neither
-// knows nor waits for them: the issuing wave waits for its own copies
+// any global address), so no registers stage them.  Since each lane chooses
+// its source, the tiles are stored dense with their 16-byte units permuted
+// (k_copy_off / v_copy_off below) so that the K reads (32 rows, one chunk
+// each) and the transposed V reads (4 rows x 64 bytes per 32 lanes) hit
+// distinct banks: D / 8 copies per tile, every lane useful.  The descriptor
+// of a tile ends at its last valid key, so rows past Sk are zeros.  The
+// copies are issued from inline assembly, so the compiler neither knows nor
+// waits for them: the issuing wave waits for its own copies
 // (s_waitcnt vmcnt(0)) right before the barrier that hands the data to the
 // other waves, and the barriers themselves order LDS only.  Q is waited for
 // before the key loop, so no wait the compiler places inside the loop can
@@ -56,8 +56,56 @@ namespace {
 
 using namespace attn;
 
+// one scheduling group of Size instructions of class Mask (0x008 MFMA,
+// 0x100 LDS read) at this point of the issue order
+template <int Mask, int Size>
+__device__ inline void sched_group() { __builtin_amdgcn_sched_group_barrier(Mask, Size, 0); }
+
 constexpr int kBN = 64;     // keys per tile
 constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
+
+// ---- K and V tiles in LDS: 64 rows x D bf16, dense (CH = D / 8 16-byte
+// chunks per row, 64 CH units per tile), with the units permuted so that the
+// operand reads are bank-conflict free AND addressed as a per-lane base plus
+// a constant of the k-step (an instruction immediate).  Unit u of a tile
+// holds row r, chunk j:
+//   K: u = 16 CH (r/16) + 8 CH (r/8 % 2) + 64 (j/8) + 16 (j/2 % 4)
+//          + r % 8 + 8 ((j + r/8) % 2)
+//      A K operand read (16 lanes per pass: one chunk of each of 16
+//      consecutive rows) then falls on 16 distinct units mod 16, i.e. each of
+//      the 64 banks once.
+//   V: u = 4 CH (r/4) + 16 (j/4) + 4 (r % 4) + j % 4
+//      each group of 4 rows is stored as 64-byte quads, quad-major with the 4
+//      rows side by side, so the transposed read (32 lanes per pass: 4 rows x
+//      one 64-byte quad) covers 256 distinct bytes.
+// Copy n of a tile fills units 64 n .. 64 n + 63 (lane l: unit 64 n + l,
+// fetched from the row and chunk below), so a tile is CH copies with no
+// padding lanes.
+template <int CH>
+__device__ inline int k_copy_off(int u, int64_t ss) {  // byte offset in the tile of K unit u
+  const int rb = u / (16 * CH), rh = (u / (8 * CH)) & 1, jb = (u % (8 * CH)) >> 6, t = u & 63;
+  const int row = 16 * rb + 8 * rh + (t & 7), ch = 8 * jb + 2 * (t >> 4) + (((t >> 3) & 1) ^ rh);
+  return (row * int(ss) + ch * 8) * 2;
+}
+template <int CH>
+__device__ inline int v_copy_off(int u, int64_t ss) {  // byte offset in the tile of V unit u
+  const int row = 4 * (u / (4 * CH)) + ((u >> 2) & 3), ch = 4 * ((u >> 4) % (CH / 4)) + (u & 3);
+  return (row * int(ss) + ch * 8) * 2;
+}
+// Element offset of this lane's K operand (row c, chunk g of the k-step) and
+// V operand (row 4 g + lane % 16 / 4, d 16 (lane / 16 % 2) + 4 (lane % 4)) in
+// the tile; the parts of the step, added as immediates:
+template <int CH>
+__device__ inline int k_lane(int c, int g) {
+  return 8 * (16 * CH * (c >> 4) + 8 * CH * ((c >> 3) & 1) + (c & 7) + 8 * ((g ^ (c >> 3)) & 1));
+}
+template <int D>
+__device__ inline int v_lane(int lane) {
+  return 32 * ((lane & 15) >> 2) + 4 * D * (lane >> 5) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+}
+// K: + k_step(s) for the 16-deep k-step s, + 32 D for rows 32..63.
+// V: + D kr + 128 db for rows kr.. (kr a multiple of 4), the 32-wide d block db.
+constexpr int k_step(int s) { return 512 * (s / 4) + 128 * (s % 4); }
 
 struct SdpaArgs {
   const uint16_t* q;
@@ -82,10 +130,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   constexpr int GW = NW / 2;       // waves per group
   constexpr int kBM = 32 * NW;     // query rows per workgroup
   constexpr int CH = D / 8;      // 16-byte chunks of a row
-  constexpr int UK = CH + 1;     // K row stride in LDS, 16-byte units
-  constexpr int UV = CH + 4;     // V row stride in LDS, 16-byte units
-  constexpr int KS = UK * 8, VS = UV * 8;  // the same in elements
-  constexpr int NK = UK, NV = UV;          // 1 KB copies per tile (64 rows x U units / 64 lanes)
+  constexpr int NK = CH, NV = CH;          // 1 KB copies per tile (64 rows x CH units / 64 lanes)
   constexpr int NKW = (NK + GW - 1) / GW, NVW = (NV + GW - 1) / GW;  // per wave: the GW waves of one group issue a tile
   constexpr int NDB = D / 32;  // 32-wide d blocks of O
   constexpr int NKS = D / 16;  // 16-deep k-steps of Q·Kᵀ
@@ -141,30 +186,30 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   const int n_rel = CAUSAL ? min(n_tiles, (q0 + 31) / kBN + 1) : n_tiles;
 
   // ---- staging: global -> LDS.  Copy j (1 KB) of a tile is issued by wave
-  // j % 4 of the issuing group and covers LDS units 64 j + lane; unit u
-  // holds row u / U, chunk u % U.
-  // the lane's byte offset within a tile for copy i (2^31: padding).  With
-  // 8 waves they are kept in registers; the 4-wave variant issues twice as
-  // many copies per wave and recomputes them at each copy instead (a few
-  // integer ops), which keeps it within 256 VGPRs.
-  auto lane_off = [&](int i, int U, int64_t ss) __attribute__((always_inline)) {
-    const int u = 64 * (GW * i + (wave % GW)) + lane, row = u / U, ch = u % U;
-    return (ch < CH && row < kBN) ? (row * int(ss) + ch * 8) * 2 : int(0x80000000u);
+  // j % GW of the issuing group and fills LDS units 64 j + lane.
+  // The lane's byte offset within a tile for copy i: with 8 waves they are
+  // kept in registers; the 4-wave variant issues twice as many copies per
+  // wave and recomputes them at each copy instead (a few integer ops), which
+  // keeps it within 256 VGPRs.
+  auto lane_off = [&](int i, auto is_v, int64_t ss) __attribute__((always_inline)) {
+    const int u = 64 * (GW * i + (wave % GW)) + lane;
+    if constexpr (decltype(is_v)::value) return v_copy_off<CH>(u, ss);
+    else return k_copy_off<CH>(u, ss);
   };
   constexpr bool kKeepOff = NW == 8;
   int koff[kKeepOff ? NKW : 1], voff[kKeepOff ? NVW : 1];
   if constexpr (kKeepOff) {
 #pragma unroll
-    for (int i = 0; i < NKW; ++i) koff[i] = lane_off(i, UK, p.k_ss);
+    for (int i = 0; i < NKW; ++i) koff[i] = lane_off(i, Flag<false>{}, p.k_ss);
 #pragma unroll
-    for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, UV, p.v_ss);
+    for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, Flag<true>{}, p.v_ss);
   }
   // LDS byte address of this wave's first copy block in the array; the
   // empty asm at each use keeps the per-copy addresses (this + a constant)
   // from being hoisted out of the key loop, where they would only occupy
   // SGPRs (and spill): m0 costs one scalar add per copy instead.
   const uint32_t lds_wave = lds_addr(kv_lds) + uint32_t(wave % GW) * 1024u;
-  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int U, int n, int nw, int dst_off, int tile) __attribute__((always_inline)) {
+  auto dma = [&](const uint16_t* base, int64_t ss, const int* off, auto is_v, int n, int nw, int dst_off, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
     const int rows = min(kBN, p.Sk - kv0);  // valid keys in the tile (>= 1); rows >= D elements apart
     const i32x4_t r = tile_desc(base + int64_t(kv0) * ss, uint32_t((rows - 1) * ss + D) * 2u);
@@ -173,19 +218,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
 #pragma unroll
     for (int i = 0; i < nw; ++i)
       if (GW * i + (wave % GW) < n)  // wave-uniform
-        copy_to_lds(r, lw + uint32_t(2 * dst_off + GW * i * 1024), kKeepOff ? off[i] : lane_off(i, U, ss));
+        copy_to_lds(r, lw + uint32_t(2 * dst_off + GW * i * 1024), kKeepOff ? off[i] : lane_off(i, is_v, ss));
   };
   auto dma_k = [&](int tile, auto buf) __attribute__((always_inline)) {
-    dma(kb, p.k_ss, koff, UK, NK, NKW, buf_off(buf, Flag<false>{}), tile);
+    dma(kb, p.k_ss, koff, Flag<false>{}, NK, NKW, buf_off(buf, Flag<false>{}), tile);
   };
   auto dma_v = [&](int tile, auto buf) __attribute__((always_inline)) {
-    dma(vb, p.v_ss, voff, UV, NV, NVW, buf_off(buf, Flag<true>{}), tile);
+    dma(vb, p.v_ss, voff, Flag<true>{}, NV, NVW, buf_off(buf, Flag<true>{}), tile);
   };
 
-  // lane's element offset in a V tile for the transposed reads: key 4g + r/4,
-  // d 16*hi + 4*(r%4) (r = lane % 16, hi = lane / 16 % 2)
-  const int vlane = (4 * g + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const int klane = c * KS + 8 * g;  // K row c, half g
+  const int vlane = v_lane<D>(lane);
+  const int klane = k_lane<CH>(c, g);  // K row c, chunk g of the k-step
 
   f32x16_t o[NDB];
 #pragma unroll
@@ -199,7 +242,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
 
   // ---- matrix phase M(t): S(t) = K[t]·Qᵀ (QK) and O += P(t-1)·V[t-1] (PV).
   // KB names K[t]'s buffer, VB V[t-1]'s.  The LDS reads are issued in the
-  // order their MFMAs use them and run ahead by LA MFMAs.
+  // order their MFMAs use them and run ahead by LA MFMAs; the issue order is
+  // fixed with scheduling groups (left to itself the scheduler bunched the
+  // reads and waited on a read issued just before its MFMA two or three
+  // times per eight MFMAs).
   auto mphase = [&](auto kbi, auto vbi, auto do_qk, auto do_pv) __attribute__((always_inline)) {
     constexpr bool QK = decltype(do_qk)::value, PV = decltype(do_pv)::value;
     const uint16_t* ks = kbuf(kbi);
@@ -218,10 +264,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     // A operand of MFMA n: K rows (QK) or Vᵀ from two transposed reads (PV)
     auto load_op = [&](int n) __attribute__((always_inline)) -> u32x4_t {
       const int i = index(n);
-      if (is_qk(n)) return *reinterpret_cast<const u32x4_t*>(&ks[klane + (i & 1) * 32 * KS + 16 * (i >> 1)]);
+      if (is_qk(n)) return *reinterpret_cast<const u32x4_t*>(&ks[klane + (i & 1) * 32 * D + k_step(i >> 1)]);
       const int kstep = 16 * (i / NDB), db = i % NDB;
-      const uint2 lo = lds_read_tr(&vs[vlane + kstep * VS + db * 32]);
-      const uint2 hi = lds_read_tr(&vs[vlane + (kstep + 8) * VS + db * 32]);
+      const uint2 lo = lds_read_tr(&vs[vlane + kstep * D + db * 128]);
+      const uint2 hi = lds_read_tr(&vs[vlane + (kstep + 8) * D + db * 128]);
       return u32x4_t{lo.x, lo.y, hi.x, hi.y};
     };
     if constexpr (QK) {
@@ -247,6 +293,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
           const int kb2 = i / (2 * NDB), j2 = (i / NDB) % 2, db = i % NDB;
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), pf[kb2][j2], o[db], 0, 0, 0);
         }
+      }
+    }
+    // issue order: the reads of the first LA operands, then MFMA n followed
+    // by the reads of operand n + LA (one ds_read_b128 for K, two transposed
+    // reads for V)
+#pragma unroll
+    for (int n = 0; n < LA && n < N; ++n) {
+      if (is_qk(n)) sched_group<0x100, 1>();
+      else sched_group<0x100, 2>();
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      sched_group<0x008, 1>();
+      if (n + LA < N) {
+        if (is_qk(n + LA)) sched_group<0x100, 1>();
+        else sched_group<0x100, 2>();
       }
     }
   };
@@ -309,6 +371,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
         pf[kb2][j2] = as_bf16x8(w);
       }
     l_run += ls0 + ls1;
+    // P and l are complete before the phase ends.  The barrier and its LDS
+    // fences order memory operations only, so without this the compiler
+    // sinks the exponentials (pure VALU work) past the next barrier into this
+    // wave's own matrix phase, where in-order issue stalls its MFMA stream
+    // while the other wave of the SIMD waits at the following barrier.
+    asm volatile("" ::"v"(pf[0][0]), "v"(pf[0][1]), "v"(pf[1][0]), "v"(pf[1][1]), "v"(l_run));
   };
 
   // M(t) for this wave: QK when t < n_rel, PV when 1 <= t <= n_rel.
@@ -464,9 +532,7 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
   constexpr int NW = 4, QB = 2;     // waves, 32-row blocks per wave
   constexpr int kBM = 64 * NW;      // query rows per workgroup
   constexpr int CH = D / 8;
-  constexpr int UK = CH + 1, UV = CH + 4;
-  constexpr int KS = UK * 8, VS = UV * 8;
-  constexpr int NK = UK, NV = UV;
+  constexpr int NK = CH, NV = CH;
   constexpr int NKW = (NK + NW - 1) / NW, NVW = (NV + NW - 1) / NW;
   constexpr int NDB = D / 32, NKS = D / 16;
   constexpr int kOffK1 = NK * 512, kOffV0 = 2 * NK * 512, kOffV1 = 2 * NK * 512 + NV * 512;
@@ -505,15 +571,11 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
   const int n_half = 2 * n_rel;
 
   // copies: copy j of a tile by wave j % 4; lane offsets kept in registers
-  auto lane_off = [&](int i, int U, int64_t ss) __attribute__((always_inline)) {
-    const int u = 64 * (NW * i + wave) + lane, row = u / U, ch = u % U;
-    return (ch < CH && row < kBN) ? (row * int(ss) + ch * 8) * 2 : int(0x80000000u);
-  };
   int koff[NKW], voff[NVW];
 #pragma unroll
-  for (int i = 0; i < NKW; ++i) koff[i] = lane_off(i, UK, p.k_ss);
+  for (int i = 0; i < NKW; ++i) koff[i] = k_copy_off<CH>(64 * (NW * i + wave) + lane, p.k_ss);
 #pragma unroll
-  for (int i = 0; i < NVW; ++i) voff[i] = lane_off(i, UV, p.v_ss);
+  for (int i = 0; i < NVW; ++i) voff[i] = v_copy_off<CH>(64 * (NW * i + wave) + lane, p.v_ss);
   const uint32_t lds_wave = lds_addr(kv_lds) + uint32_t(wave) * 1024u;
   auto dma = [&](const uint16_t* base, int64_t ss, const int* off, int n, int nw, int dst_off, int tile) __attribute__((always_inline)) {
     const int kv0 = tile * kBN;
@@ -532,8 +594,8 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
     dma(vb, p.v_ss, voff, NV, NVW, buf ? kOffV1 : kOffV0, tile);
   };
 
-  const int vlane = (4 * g + ((lane & 15) >> 2)) * VS + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const int klane = c * KS + 8 * g;
+  const int vlane = v_lane<D>(lane);
+  const int klane = k_lane<CH>(c, g);
 
   f32x16_t o[QB][NDB];
 #pragma unroll
@@ -550,14 +612,14 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
   // S(hh) = K(hh) · Qᵀ: key half hh % 2 of the tile in K<buffer>; each K
   // operand (16-deep step) is read once and used for both row blocks
   auto qk = [&](int set, int kbuf, int half) __attribute__((always_inline)) {
-    const uint16_t* ks = kv_lds + (kbuf ? kOffK1 : 0) + half * 32 * KS;
+    const uint16_t* ks = kv_lds + (kbuf ? kOffK1 : 0) + half * 32 * D;
 #pragma unroll
     for (int r = 0; r < QB; ++r)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[set][r][e] = 0.f;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[klane + 16 * st]);
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[klane + k_step(st)]);
 #pragma unroll
       for (int r = 0; r < QB; ++r)
         sc[set][r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[r][st], sc[set][r], 0, 0, 0);
@@ -566,12 +628,12 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
   // O += P(hh) · V(hh): key half hh % 2 of the tile in V<buffer>; each Vᵀ
   // operand (16-key step, d block; two transposed reads) used twice
   auto pv = [&](int set, int vbuf, int half) __attribute__((always_inline)) {
-    const uint16_t* vs = kv_lds + (vbuf ? kOffV1 : kOffV0) + half * 32 * VS;
+    const uint16_t* vs = kv_lds + (vbuf ? kOffV1 : kOffV0) + half * 32 * D;
 #pragma unroll
     for (int i = 0; i < 2 * NDB; ++i) {
       const int kst = i / NDB, db = i % NDB;
-      const uint2 lo = lds_read_tr(&vs[vlane + 16 * kst * VS + db * 32]);
-      const uint2 hi = lds_read_tr(&vs[vlane + (16 * kst + 8) * VS + db * 32]);
+      const uint2 lo = lds_read_tr(&vs[vlane + 16 * kst * D + db * 128]);
+      const uint2 hi = lds_read_tr(&vs[vlane + (16 * kst + 8) * D + db * 128]);
       const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
       for (int r = 0; r < QB; ++r)
