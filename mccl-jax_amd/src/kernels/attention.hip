@@ -69,11 +69,12 @@ constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
 // operand reads are bank-conflict free AND addressed as a per-lane base plus
 // a constant of the k-step (an instruction immediate).  Unit u of a tile
 // holds row r, chunk j:
-//   K: u = 16 CH (r/16) + 8 CH (r/8 % 2) + 64 (j/8) + 16 (j/2 % 4)
-//          + r % 8 + 8 ((j + r/8) % 2)
-//      A K operand read (16 lanes per pass: one chunk of each of 16
-//      consecutive rows) then falls on 16 distinct units mod 16, i.e. each of
-//      the 64 banks once.
+//   K: u = 64 ((r/16) (CH/4) + j/4) + 4 (r % 16) + (j + r/4) % 4
+//      one copy holds 16 rows x 4 chunks; its lanes 4 a .. 4 a + 3 fetch the
+//      64 contiguous bytes of one row (rotated by r/4, so a quad of lanes is
+//      one 64-byte request of the copy).  A K operand read (16 lanes per
+//      pass: one chunk of each of 16 consecutive rows) falls on 16 distinct
+//      units mod 16, i.e. each of the 64 banks once.
 //   V: u = 4 CH (r/4) + 16 (j/4) + 4 (r % 4) + j % 4
 //      each group of 4 rows is stored as 64-byte quads, quad-major with the 4
 //      rows side by side, so the transposed read (32 lanes per pass: 4 rows x
@@ -83,8 +84,8 @@ constexpr float kRescaleLog2 = 8.f;       // lazy-rescale threshold (log2 units)
 // padding lanes.
 template <int CH>
 __device__ inline int k_copy_off(int u, int64_t ss) {  // byte offset in the tile of K unit u
-  const int rb = u / (16 * CH), rh = (u / (8 * CH)) & 1, jb = (u % (8 * CH)) >> 6, t = u & 63;
-  const int row = 16 * rb + 8 * rh + (t & 7), ch = 8 * jb + 2 * (t >> 4) + (((t >> 3) & 1) ^ rh);
+  const int n = u >> 6, a = (u >> 2) & 15;
+  const int row = 16 * (n / (CH / 4)) + a, ch = 4 * (n % (CH / 4)) + (((u & 3) - (a >> 2)) & 3);
   return (row * int(ss) + ch * 8) * 2;
 }
 template <int CH>
@@ -92,20 +93,23 @@ __device__ inline int v_copy_off(int u, int64_t ss) {  // byte offset in the til
   const int row = 4 * (u / (4 * CH)) + ((u >> 2) & 3), ch = 4 * ((u >> 4) % (CH / 4)) + (u & 3);
   return (row * int(ss) + ch * 8) * 2;
 }
-// Element offset of this lane's K operand (row c, chunk g of the k-step) and
-// V operand (row 4 g + lane % 16 / 4, d 16 (lane / 16 % 2) + 4 (lane % 4)) in
-// the tile; the parts of the step, added as immediates:
+// Element offset of this lane's K operand (row c, chunk g of the k-step; one
+// base for even and one for odd k-steps, ODD) and V operand (row
+// 4 g + lane % 16 / 4, d 16 (lane / 16 % 2) + 4 (lane % 4)) in the tile; the
+// parts of the step, added as immediates:
 template <int CH>
-__device__ inline int k_lane(int c, int g) {
-  return 8 * (16 * CH * (c >> 4) + 8 * CH * ((c >> 3) & 1) + (c & 7) + 8 * ((g ^ (c >> 3)) & 1));
+__device__ inline int k_lane(int c, int g, int odd) {
+  const int x = (g + ((c & 15) >> 2)) & 3;
+  return 8 * (64 * (CH / 4) * (c >> 4) + 4 * (c & 15) + (x ^ (2 * odd)));
 }
 template <int D>
 __device__ inline int v_lane(int lane) {
   return 32 * ((lane & 15) >> 2) + 4 * D * (lane >> 5) + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 }
-// K: + k_step(s) for the 16-deep k-step s, + 32 D for rows 32..63.
+// K: base k_lane(.., s % 2) + k_step(s) for the 16-deep k-step s, + 32 D for
+// rows 32..63.
 // V: + D kr + 128 db for rows kr.. (kr a multiple of 4), the 32-wide d block db.
-constexpr int k_step(int s) { return 512 * (s / 4) + 128 * (s % 4); }
+constexpr int k_step(int s) { return 512 * (s / 2); }
 
 struct SdpaArgs {
   const uint16_t* q;
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
   };
 
   const int vlane = v_lane<D>(lane);
-  const int klane = k_lane<CH>(c, g);  // K row c, chunk g of the k-step
+  const int klane0 = k_lane<CH>(c, g, 0), klane1 = k_lane<CH>(c, g, 1);  // K row c, chunk g of the k-step
 
   f32x16_t o[NDB];
 #pragma unroll
@@ -264,7 +268,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void sdpa_fwd_kernel(const SdpaArg
     // A operand of MFMA n: K rows (QK) or Vᵀ from two transposed reads (PV)
     auto load_op = [&](int n) __attribute__((always_inline)) -> u32x4_t {
       const int i = index(n);
-      if (is_qk(n)) return *reinterpret_cast<const u32x4_t*>(&ks[klane + (i & 1) * 32 * D + k_step(i >> 1)]);
+      if (is_qk(n))
+        return *reinterpret_cast<const u32x4_t*>(&ks[((i >> 1) & 1 ? klane1 : klane0) + (i & 1) * 32 * D + k_step(i >> 1)]);
       const int kstep = 16 * (i / NDB), db = i % NDB;
       const uint2 lo = lds_read_tr(&vs[vlane + kstep * D + db * 128]);
       const uint2 hi = lds_read_tr(&vs[vlane + (kstep + 8) * D + db * 128]);
@@ -595,7 +600,7 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
   };
 
   const int vlane = v_lane<D>(lane);
-  const int klane = k_lane<CH>(c, g);
+  const int klane0 = k_lane<CH>(c, g, 0), klane1 = k_lane<CH>(c, g, 1);
 
   f32x16_t o[QB][NDB];
 #pragma unroll
@@ -619,7 +624,7 @@ __global__ __launch_bounds__(256, 1) void sdpa_fwd_wide_kernel(const SdpaArgs p)
       for (int e = 0; e < 16; ++e) sc[set][r][e] = 0.f;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[klane + k_step(st)]);
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(&ks[(st & 1 ? klane1 : klane0) + k_step(st)]);
 #pragma unroll
       for (int r = 0; r < QB; ++r)
         sc[set][r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), qf[r][st], sc[set][r], 0, 0, 0);
