@@ -28,7 +28,12 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup SECONDS]
 
 Before the first timed region the headline kernel runs untimed for --spinup
 seconds (default 1), so that no timed region includes the clocks' ramp from
-idle; then each workload runs W untimed and K timed launches.
+idle; then each workload runs W untimed and K timed launches.  Each SDPA
+sequence length first runs untimed on its own inputs (--spinup seconds at the
+headline length, up to 0.2 s at the others): the host-side input generation
+before it leaves the GPU idle long enough for the clocks to drop, and after
+that the first ~50 ms of launches run up to 10% slower than the sustained
+rate, which 10 warm-up launches do not cover.
 """
 
 from __future__ import annotations
@@ -101,6 +106,15 @@ def spin_up(torch, np, K, args):
         torch.cuda.synchronize()
     del q, o
     torch.cuda.empty_cache()
+
+
+def spin(torch, fn, seconds):
+    """Untimed calls of fn for `seconds`, synchronising every 10 calls."""
+    t0 = time.time()
+    while time.time() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
 
 
 def sdpa_flops(B, H, S, D):
@@ -177,7 +191,9 @@ def run_sdpa(torch, np, K, args):
         del d
         o = torch.empty_like(q)
         steps = args.steps if S == args.seq else max(5, min(args.steps, 20))
-        ms = time_launches(torch, lambda: K.sdpa_fwd(q, k, v, scale, True, out=o), steps, args.warmup)
+        call = lambda: K.sdpa_fwd(q, k, v, scale, True, out=o)  # noqa: E731
+        spin(torch, call, args.spinup if S == args.seq else min(args.spinup, 0.2))
+        ms = time_launches(torch, call, steps, args.warmup)
         tf = sdpa_flops(B, H, S, D) / (ms * 1e-3) / 1e12
         sweep[str(S)] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
         log(f"sdpa S={S}: {ms:.3f} ms  {tf:.1f} TFLOP/s  ({100*tf/PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
