@@ -279,6 +279,28 @@ class Builder:
         out, _ = self._reduce(self.stop(x), dims, "maximum", -math.inf)
         return out
 
+    def softmax_last(self, x: V) -> V:
+        """jax.nn.softmax over the last axis: the forward as it lowers
+        (max behind stop_gradient, exp, sum, divide) and its custom JVP rule
+        y * (x' - sum(y * x')) transposed, so the backward is
+        y g - y bcast(sum(y g)) with y g formed once (what jax.grad emits for
+        jax.nn.softmax after CSE)."""
+        r = len(x.shape) - 1
+        keep = tuple(range(r))
+        xs = self.stop(x)
+        m = self.reduce_max(xs, [r])
+        e = self.exp(self.sub(xs, self.bcast(m, x.shape, keep)))
+        z = self.reduce_sum(e, [r])
+        y = self.div(e, self.bcast(z, x.shape, keep))
+        y.needs_grad = x.needs_grad
+
+        def vjp(g):
+            ys = self.stop(y)
+            yg = self.mul(g, ys)
+            t = self.reduce_sum(yg, [r])
+            return [self.sub(yg, self.mul(ys, self.bcast(t, x.shape, keep)))]
+        return self._record(y, [x], vjp)
+
     # ------------------------------------------------------------------ products
     def dot(self, a: V, b: V, lc, rc, lb=(), rb=(), out_dt="f32") -> V:
         """dot_general; result dims: batch, a's free dims, b's free dims."""
@@ -459,10 +481,7 @@ def gpt2_train_step(cfg, b1=0.9, b2=0.999, eps=1e-8, return_grads=False) -> str:
         qkv = g.add(g.mm(h, p("w_qkv")), row_bcast(p("b_qkv"), T))
         q, k, v = (heads(t) for t in g.split(qkv, 1, (d, d, d)))
         s = g.select(causal, g.mul(g.bmm(q, k, 3, 3), scale), neg_inf)
-        m = g.reduce_max(s, [3])
-        e = g.exp(g.sub(s, g.bcast(m, (B, H, S, S), (0, 1, 2))))
-        z = g.reduce_sum(e, [3])
-        pr = g.div(e, g.bcast(z, (B, H, S, S), (0, 1, 2)))
+        pr = g.softmax_last(s)
         o = g.bmm(pr, v, 3, 2)  # [B, H, S, hd]
         a = g.reshape(g.transpose(o, (0, 2, 1, 3)), (T, d))
         x = g.add(x, g.add(g.mm(a, p("w_o")), row_bcast(p("b_o"), T)))

@@ -14,7 +14,9 @@
 //   * pattern matchers replace whole subgraphs by a fused kernel: causal /
 //     full scaled-dot-product attention (QKᵀ -> scale -> mask -> softmax ->
 //     PV, cf. TrySoftmax elementwise.mm:71-89), arg-max/min reduces
-//     (DetectArgReduce reduce.mm:29-43), dot_general + bias (+ ReLU);
+//     (DetectArgReduce reduce.mm:29-43), dot_general + bias (+ ReLU), and
+//     attention together with the backward jax.grad emits for it (the
+//     flash forward with lse, then the flash backward);
 //   * temporaries live in one arena per run, packed by liveness.
 #include <algorithm>
 #include <array>
@@ -52,6 +54,8 @@ const char* StepName(StepKind k) {
     case StepKind::kConvert: return "convert";
     case StepKind::kFill: return "fill";
     case StepKind::kCopy: return "copy";
+    case StepKind::kSdpaBwd: return "sdpa_bwd";
+    case StepKind::kGemmBlas: return "gemm_blas";
   }
   return "?";
 }
@@ -326,12 +330,15 @@ struct ValState {
 };
 
 struct Fused {
-  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu } kind;
+  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu, kSdpaBwd } kind;
   std::vector<int> deps;  // value ids the fused step reads
-  // sdpa
+  // sdpa (train: also lse and the bf16 O for the backward step)
   int q = -1, k = -1, v = -1;
   float scale = 1.f;
   bool causal = false;
+  bool train = false;
+  // sdpa_bwd: dO (bf16), the forward's anchor, the three gradients
+  int dout = -1, fwd = -1, dq = -1, dk = -1, dv = -1;
   // argmax
   int x = -1;
   bool is_min = false;
@@ -377,6 +384,7 @@ class Lowerer {
         s.view.strides = DenseStrides(s.view.dims);
       }
       Analyze();
+      Reachable();
       MatchPatterns();
       Liveness();
       Walk();
@@ -396,7 +404,9 @@ class Lowerer {
   static std::vector<size_t> WrittenBufs(const Step& s) {
     switch (s.kind) {
       case StepKind::kGemm: return {2};
-      case StepKind::kSdpa: return {3};
+      case StepKind::kSdpa: return s.bufs.size() > 4 ? std::vector<size_t>{3, 4} : std::vector<size_t>{3};
+      case StepKind::kSdpaBwd: return {6, 7, 8, 9};
+      case StepKind::kGemmBlas: return {2};
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
@@ -574,6 +584,36 @@ class Lowerer {
     for (int o : outputs_) ++uses_[o];
   }
   const Op* prod(int v) const { return v >= 0 && producer_[v] >= 0 ? &ops_[producer_[v]] : nullptr; }
+
+  // ops whose results reach a program output (before any fusion): the
+  // backward of a jitted step carries transposes nothing reads (the
+  // cotangent of a constant), which must not count as uses
+  void Reachable() {
+    reach_.assign(ops_.size(), false);
+    std::vector<int> stack(outputs_.begin(), outputs_.end());
+    std::vector<bool> seen(m_.types.size(), false);
+    while (!stack.empty()) {
+      const int v = stack.back();
+      stack.pop_back();
+      if (v < 0 || seen[v]) continue;
+      seen[v] = true;
+      const int pr = producer_[v];
+      if (pr < 0 || reach_[pr]) continue;
+      reach_[pr] = true;
+      for (int o : ops_[pr].operands) stack.push_back(o);
+      for (const auto& reg : ops_[pr].regions)
+        for (const auto& blk : reg->blocks)
+          for (const Op& inner : blk.ops)
+            for (int o : inner.operands) stack.push_back(o);
+    }
+  }
+  // reachable users of v
+  std::vector<int> live_users(int v) const {
+    std::vector<int> r;
+    for (int u : users_[v])
+      if (reach_[u]) r.push_back(u);
+    return r;
+  }
   bool is(int v, const char* name) const {
     const Op* p = prod(v);
     return p && p->name == name;
@@ -1308,30 +1348,41 @@ class Lowerer {
     return S;
   }
 
-  void TryMatchSdpa(int anchor) {
+  // The attention forward anchored at the P·V product: Q·Kᵀ (bf16
+  // operands), scale, optional mask select, softmax, P·V.
+  struct SdpaFwdMatch {
+    std::set<int> ops;  // matched ops, anchor included
+    int q = -1, k = -1, v = -1;
+    int pr = -1;        // the softmax output (the divide)
+    int mask = -1;
+    float scale = 1.f;
+    bool causal = false;
+  };
+  bool MatchSdpaFwd(int anchor, SdpaFwdMatch& r) {
     const Op& d2 = ops_[anchor];
     const int P = d2.operands[0], V = d2.operands[1];
     const TensorType& pt = m_.types[P];
     const TensorType& vt = m_.types[V];
-    if (pt.rank() != 4 || vt.rank() != 4) return;
+    if (pt.rank() != 4 || vt.rank() != 4) return false;
     DotDims dd = dot_dims(d2);
     if (dd.lb != std::vector<int64_t>{0, 1} || dd.rb != std::vector<int64_t>{0, 1} ||
         dd.lc != std::vector<int64_t>{3} || dd.rc != std::vector<int64_t>{2})
-      return;
-    std::set<int> ops;
+      return false;
+    std::set<int>& ops = r.ops;
     ops.insert(anchor);
     std::vector<int> path;
     const int Pin = through_converts(P, &path);
     for (int o : path) ops.insert(o);
     int S = MatchSoftmax(Pin, ops);
-    if (S < 0) return;
+    if (S < 0) return false;
+    r.pr = Pin;
     // mask: select(mask, scores, -inf)
     int mask = -1;
     int sc = S;
     if (is(sc, "stablehlo.select")) {
       const Op* sel = prod(sc);
       double c;
-      if (!scalar_of(sel->operands[2], &c) || !(c < -1e30)) return;
+      if (!scalar_of(sel->operands[2], &c) || !(c < -1e30)) return false;
       mask = sel->operands[0];
       ops.insert(producer_[sc]);
       sc = sel->operands[1];
@@ -1362,40 +1413,224 @@ class Lowerer {
     sc = through_converts(sc, &path);
     for (int o : path) ops.insert(o);
     const Op* d1 = prod(sc);
-    if (!d1 || d1->name != "stablehlo.dot_general") return;
+    if (!d1 || d1->name != "stablehlo.dot_general") return false;
     DotDims e = dot_dims(*d1);
     if (e.lb != std::vector<int64_t>{0, 1} || e.rb != std::vector<int64_t>{0, 1} ||
         e.lc != std::vector<int64_t>{3} || e.rc != std::vector<int64_t>{3})
-      return;
+      return false;
     ops.insert(producer_[sc]);
     const int Q = d1->operands[0], K = d1->operands[1];
     const TensorType& qt = m_.types[Q];
     const TensorType& kt = m_.types[K];
-    if (qt.dtype != DType::kBF16 || kt.dtype != DType::kBF16 || vt.dtype != DType::kBF16) return;
-    if (m_.types[d2.results[0]].dtype != DType::kBF16) return;
+    if (qt.dtype != DType::kBF16 || kt.dtype != DType::kBF16 || vt.dtype != DType::kBF16) return false;
     const int64_t D = qt.dims[3];
-    if ((D != 64 && D != 128) || vt.dims[3] != D) return;
+    if ((D != 64 && D != 128) || vt.dims[3] != D) return false;
     bool causal = false;
     if (mask >= 0) {
       const int cls = ClassifyMask(mask, qt.dims[0], qt.dims[1], qt.dims[2], kt.dims[2]);
-      if (cls < 0) return;
+      if (cls < 0) return false;
       causal = cls == 1;
     }
+    r.q = Q;
+    r.k = K;
+    r.v = V;
+    r.mask = mask;
+    r.scale = scale;
+    r.causal = causal;
+    return true;
+  }
+
+  void TryMatchSdpa(int anchor) {
+    SdpaFwdMatch r;
+    if (!MatchSdpaFwd(anchor, r)) return;
+    const Op& d2 = ops_[anchor];
+    bool inside = m_.types[d2.results[0]].dtype == DType::kBF16;
     // every intermediate result must stay inside the pattern
-    for (int o : ops)
-      for (int r : ops_[o].results)
-        if (o != anchor && !uses_within(r, ops)) return;
+    for (int o : r.ops)
+      for (int res : ops_[o].results)
+        if (o != anchor && !uses_within(res, r.ops)) inside = false;
+    if (!inside) {
+      TryMatchSdpaTrain(anchor, r);
+      return;
+    }
     Fused f;
     f.kind = Fused::kSdpa;
-    f.q = Q;
-    f.k = K;
-    f.v = V;
-    f.scale = scale;
-    f.causal = causal;
-    f.deps = {Q, K, V};
+    f.q = r.q;
+    f.k = r.k;
+    f.v = r.v;
+    f.scale = r.scale;
+    f.causal = r.causal;
+    f.deps = {r.q, r.k, r.v};
     fused_[anchor] = f;
-    prog_->patterns.push_back(std::string("sdpa(") + (causal ? "causal" : "full") + ", scale=" +
-                              std::to_string(scale) + ")");
+    prog_->patterns.push_back(std::string("sdpa(") + (r.causal ? "causal" : "full") + ", scale=" +
+                              std::to_string(r.scale) + ")");
+  }
+
+  // The attention forward together with the backward jax.grad emits for it
+  // (jax.nn.softmax's rule dS = P (dP - sum(P dP)) over the last axis):
+  //   dVᵀ = dot(dO, P) over the queries, dV = transpose(dVᵀ)
+  //   dP  = dot(dO, V) over D
+  //   G   = dP * P,  dS = G - P * bcast(sum(G))
+  //   [select(mask, dS, 0)] * scale -> bf16 -> dQ = dot(., K), dK = dot(., Q)
+  // The forward becomes mk_sdpa_fwd with lse (and its bf16 O kept), the
+  // backward one mk_sdpa_bwd step anchored at the first of its products;
+  // nothing S x S is formed.  Users that do not reach an output (transposes
+  // toward constants) are ignored.
+  void TryMatchSdpaTrain(int anchor, const SdpaFwdMatch& r) {
+    const Op& d2 = ops_[anchor];
+    const int Pbf = d2.operands[0], Vb = d2.operands[1];
+    const TensorType& qt = m_.types[r.q];
+    const TensorType& kt = m_.types[r.k];
+    const int64_t B = qt.dims[0], H = qt.dims[1], Sq = qt.dims[2], Sk = kt.dims[2], D = qt.dims[3];
+    auto dims_are = [&](int v, std::vector<int64_t> d) { return m_.types[v].dims == d; };
+    auto find_user = [&](int v, const char* name, auto pred) -> int {
+      for (int u : live_users(v))
+        if (ops_[u].name == name && pred(ops_[u])) return u;
+      return -1;
+    };
+    auto dot_is = [&](const Op& o, std::vector<int64_t> lc, std::vector<int64_t> rc) {
+      DotDims dd = dot_dims(o);
+      return dd.lb == std::vector<int64_t>{0, 1} && dd.rb == std::vector<int64_t>{0, 1} && dd.lc == lc && dd.rc == rc;
+    };
+    auto other = [](const Op& o, int v) { return o.operands[0] == v ? o.operands[1] : o.operands[0]; };
+    std::set<int> bw;
+    // dVᵀ = dot(dO, P) contracting the query dims, then the transpose to dV
+    int dvt = -1, dO = -1;
+    for (int u : live_users(Pbf)) {
+      const Op& o = ops_[u];
+      if (u != anchor && o.name == "stablehlo.dot_general" && o.operands.size() == 2 && o.operands[1] == Pbf &&
+          dot_is(o, {2}, {2})) {
+        dvt = u;
+        dO = o.operands[0];
+      }
+    }
+    if (dvt < 0 || m_.types[dO].dtype != DType::kBF16 || !dims_are(dO, {B, H, Sq, D})) return;
+    bw.insert(dvt);
+    const int dvt_v = ops_[dvt].results[0];
+    const auto dvt_users = live_users(dvt_v);
+    if (dvt_users.size() != 1 || ops_[dvt_users[0]].name != "stablehlo.transpose") return;
+    if (attr_ints(ops_[dvt_users[0]], {"permutation", "dims"}) != std::vector<int64_t>{0, 1, 3, 2}) return;
+    bw.insert(dvt_users[0]);
+    const int dv = ops_[dvt_users[0]].results[0];
+    // dP = dot(dO, V) over D
+    const int dpd = find_user(dO, "stablehlo.dot_general", [&](const Op& o) {
+      return o.operands.size() == 2 && o.operands[0] == dO && o.operands[1] == Vb && dot_is(o, {3}, {3});
+    });
+    if (dpd < 0) return;
+    bw.insert(dpd);
+    const int dP = ops_[dpd].results[0];
+    // G = dP * P
+    const int gm = find_user(dP, "stablehlo.multiply", [&](const Op& o) { return other(o, dP) == r.pr; });
+    if (gm < 0) return;
+    bw.insert(gm);
+    const int G = ops_[gm].results[0];
+    // t = sum(G) over the keys, P * bcast(t), dS = G - that
+    int tsum = -1;
+    for (int u : live_users(G))
+      if (ops_[u].name == "stablehlo.reduce" && is_reduce_over_last(ops_[u].results[0], "stablehlo.add", 4)) tsum = u;
+    if (tsum < 0) return;
+    bw.insert(tsum);
+    int tb = ops_[tsum].results[0];
+    while (true) {
+      const auto us = live_users(tb);
+      if (us.size() != 1) return;
+      const Op& o = ops_[us[0]];
+      if (o.name != "stablehlo.broadcast_in_dim" && o.name != "stablehlo.reshape") break;
+      bw.insert(us[0]);
+      tb = o.results[0];
+      if (dims_are(tb, {B, H, Sq, Sk})) break;
+    }
+    if (!dims_are(tb, {B, H, Sq, Sk})) return;
+    const int pm = find_user(tb, "stablehlo.multiply", [&](const Op& o) { return other(o, tb) == r.pr; });
+    if (pm < 0) return;
+    bw.insert(pm);
+    const int PT = ops_[pm].results[0];
+    const int dsub = find_user(G, "stablehlo.subtract", [&](const Op& o) {
+      return o.operands[0] == G && o.operands[1] == PT;
+    });
+    if (dsub < 0) return;
+    bw.insert(dsub);
+    int dS = ops_[dsub].results[0];
+    // select(mask, dS, 0) where the forward was masked
+    if (r.mask >= 0) {
+      const int sel = find_user(dS, "stablehlo.select", [&](const Op& o) {
+        double c;
+        return o.operands[1] == dS && scalar_of(o.operands[2], &c) && c == 0.0 &&
+               (o.operands[0] == r.mask ||
+                ClassifyMask(o.operands[0], B, H, Sq, Sk) == (r.causal ? 1 : 0));
+      });
+      if (sel < 0) return;
+      bw.insert(sel);
+      dS = ops_[sel].results[0];
+    }
+    // times the scale (splat constant, either side)
+    const int sm = find_user(dS, "stablehlo.multiply", [&](const Op& o) {
+      double c;
+      return scalar_of(other(o, dS), &c) && float(c) == r.scale;
+    });
+    if (sm < 0) return;
+    bw.insert(sm);
+    const int dSs = ops_[sm].results[0];
+    // bf16, then dQ = dot(dS, K) over the keys and dK = dot(dS, Q) over the queries
+    const auto cu = live_users(dSs);
+    if (cu.size() != 1 || ops_[cu[0]].name != "stablehlo.convert") return;
+    bw.insert(cu[0]);
+    const int dSb = ops_[cu[0]].results[0];
+    if (m_.types[dSb].dtype != DType::kBF16) return;
+    const int dqd = find_user(dSb, "stablehlo.dot_general", [&](const Op& o) {
+      return o.operands.size() == 2 && o.operands[0] == dSb && o.operands[1] == r.k && dot_is(o, {3}, {2});
+    });
+    const int dkd = find_user(dSb, "stablehlo.dot_general", [&](const Op& o) {
+      return o.operands.size() == 2 && o.operands[0] == dSb && o.operands[1] == r.q && dot_is(o, {2}, {2});
+    });
+    if (dqd < 0 || dkd < 0) return;
+    bw.insert(dqd);
+    bw.insert(dkd);
+    const int dq = ops_[dqd].results[0], dk = ops_[dkd].results[0];
+    if (!dims_are(dq, {B, H, Sq, D}) || !dims_are(dk, {B, H, Sk, D}) || !dims_are(dv, {B, H, Sk, D})) return;
+    // everything else stays inside forward + backward
+    std::set<int> all = r.ops;
+    all.insert(bw.begin(), bw.end());
+    const std::set<int> outs = {d2.results[0], dq, dk, dv};
+    for (int o : all)
+      for (int res : ops_[o].results) {
+        if (outs.count(res)) continue;
+        for (int oo : outputs_)
+          if (oo == res) return;
+        for (int u : live_users(res))
+          if (!all.count(u)) return;
+      }
+    // the backward runs at its first product, after the forward
+    const int banchor = std::min(dvt, dpd);
+    if (banchor <= anchor || fused_.count(banchor)) return;
+    Fused f;
+    f.kind = Fused::kSdpa;
+    f.train = true;
+    f.q = r.q;
+    f.k = r.k;
+    f.v = r.v;
+    f.scale = r.scale;
+    f.causal = r.causal;
+    f.deps = {r.q, r.k, r.v};
+    fused_[anchor] = f;
+    Fused b;
+    b.kind = Fused::kSdpaBwd;
+    b.q = r.q;
+    b.k = r.k;
+    b.v = r.v;
+    b.dout = dO;
+    b.fwd = anchor;
+    b.dq = dq;
+    b.dk = dk;
+    b.dv = dv;
+    b.scale = r.scale;
+    b.causal = r.causal;
+    b.deps = {r.q, r.k, r.v, dO, d2.results[0]};
+    fused_[banchor] = b;
+    for (int o : all)
+      if (o != anchor && o != banchor) absorbed_.insert(o);
+    prog_->patterns.push_back(std::string("sdpa_train(") + (r.causal ? "causal" : "full") + ", scale=" +
+                              std::to_string(r.scale) + ")");
   }
 
   void TryMatchArgmax(int anchor) {
@@ -2485,6 +2720,15 @@ class Lowerer {
     BufRef d = DestFor(res);
     Step st;
     st.kind = StepKind::kGemm;
+    // bf16 operands whose rows are not 16-byte aligned (a vocabulary of
+    // 50257) rule out the tiled kernel's 16-byte HBM->LDS copies; large such
+    // products go to the library GEMM, as the hand-scheduled step's
+    // vocabulary products do (the general kernel runs them at a tenth of
+    // its rate), the rest to mk_gemm's general kernel
+    const auto rows8 = [](int64_t bs, int64_t ms, int64_t ks) { return bs % 8 == 0 && (ms == 1 ? ks : ms) % 8 == 0; };
+    if (at == DType::kBF16 && !epi && (ct == DType::kF32 || ct == DType::kBF16) &&
+        !(rows8(a_bs, a_ms, a_ks) && rows8(b_bs, b_ns, b_ks)) && double(B) * M * N * K >= double(int64_t(1) << 30))
+      st.kind = StepKind::kGemmBlas;
     st.bufs = {lv.at(), rv.at(), d};
     int epilogue = 0;
     if (epi) {
@@ -2633,17 +2877,31 @@ class Lowerer {
   }
 
   // -------------------------------------------------------------- fused steps
+  // a bf16 -> f32 (or other) conversion step of a dense buffer
+  void EmitConvert(BufRef src, DType from, BufRef dst, DType to, int64_t n) {
+    Step st;
+    st.kind = StepKind::kConvert;
+    st.bufs = {src, dst};
+    st.i = {int64_t(from), int64_t(to), n};
+    Emit(st);
+  }
+
   void EmitFused(int anchor, const Fused& f) {
     const Op& op = ops_[anchor];
+    auto bf16_rows = [](const View& x) { return x.strides[3] == 1 && x.dtype == DType::kBF16; };
     if (f.kind == Fused::kSdpa) {
       const View& q = NeedView(f.q);
       const View& k = NeedView(f.k);
       const View& v = NeedView(f.v);
-      auto ok = [](const View& x) { return x.strides[3] == 1 && x.dtype == DType::kBF16; };
-      View qv = ok(q) ? q : Densify(q), kv = ok(k) ? k : Densify(k), vv = ok(v) ? v : Densify(v);
+      View qv = bf16_rows(q) ? q : Densify(q), kv = bf16_rows(k) ? k : Densify(k),
+           vv = bf16_rows(v) ? v : Densify(v);
       const int res = op.results[0];
-      BufRef d = DestFor(res);
       const auto& od = m_.types[res].dims;
+      // training: O in bf16 (kept for the backward) plus lse, then O in the
+      // module's dtype
+      const bool bf16_out = m_.types[res].dtype == DType::kBF16 && !f.train;
+      const int64_t n = od[0] * od[1] * od[2] * od[3];
+      BufRef d = bf16_out ? DestFor(res) : NewTemp(size_t(n) * 2);
       Step st;
       st.kind = StepKind::kSdpa;
       st.bufs = {qv.at(), kv.at(), vv.at(), d};
@@ -2654,8 +2912,58 @@ class Lowerer {
               od[1] * od[2] * od[3], od[2] * od[3], od[3], f.causal ? 1 : 0};
       st.f = {f.scale};
       st.note = f.causal ? "causal" : "full";
+      BufRef lse;
+      if (f.train) {
+        lse = NewTemp(size_t(od[0] * od[1] * od[2]) * 4);
+        st.bufs.push_back(lse);
+        st.note += " +lse";
+      }
       Emit(st);
-      SetDenseView(res, d);
+      if (f.train) sdpa_saved_[anchor] = {d, lse};
+      if (bf16_out) {
+        SetDenseView(res, d);
+      } else {
+        BufRef o = DestFor(res);
+        EmitConvert(d, DType::kBF16, o, m_.types[res].dtype, n);
+        SetDenseView(res, o);
+      }
+      return;
+    }
+    if (f.kind == Fused::kSdpaBwd) {
+      const View& q = NeedView(f.q);
+      const View& k = NeedView(f.k);
+      const View& v = NeedView(f.v);
+      const View& g = NeedView(f.dout);
+      View qv = bf16_rows(q) ? q : Densify(q), kv = bf16_rows(k) ? k : Densify(k),
+           vv = bf16_rows(v) ? v : Densify(v), gv = bf16_rows(g) ? g : Densify(g);
+      const auto it = sdpa_saved_.find(f.fwd);
+      if (it == sdpa_saved_.end()) throw std::string("jam: attention backward before its forward");
+      const int64_t B = qv.dims[0], H = qv.dims[1], Sq = qv.dims[2], Sk = kv.dims[2], D = qv.dims[3];
+      BufRef ws = NewTemp(mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk, D));
+      BufRef dqb = NewTemp(size_t(B * H * Sq * D) * 2), dkb = NewTemp(size_t(B * H * Sk * D) * 2),
+             dvb = NewTemp(size_t(B * H * Sk * D) * 2);
+      Step st;
+      st.kind = StepKind::kSdpaBwd;
+      st.bufs = {qv.at(), kv.at(), vv.at(), it->second.first, gv.at(), it->second.second, dqb, dkb, dvb, ws};
+      st.i = {B, H, Sq, Sk, D,
+              qv.strides[0], qv.strides[1], qv.strides[2],
+              kv.strides[0], kv.strides[1], kv.strides[2],
+              vv.strides[0], vv.strides[1], vv.strides[2],
+              H * Sq * D, Sq * D, D,
+              gv.strides[0], gv.strides[1], gv.strides[2],
+              H * Sq * D, Sq * D, D,
+              H * Sk * D, Sk * D, D,
+              H * Sk * D, Sk * D, D,
+              f.causal ? 1 : 0};
+      st.f = {f.scale};
+      st.note = f.causal ? "causal" : "full";
+      Emit(st);
+      const std::pair<int, BufRef> grads[3] = {{f.dq, dqb}, {f.dk, dkb}, {f.dv, dvb}};
+      for (const auto& gr : grads) {
+        BufRef o = DestFor(gr.first);
+        EmitConvert(gr.second, DType::kBF16, o, m_.types[gr.first].dtype, m_.types[gr.first].numel());
+        SetDenseView(gr.first, o);
+      }
       return;
     }
     if (f.kind == Fused::kArgmax) {
@@ -2751,6 +3059,8 @@ class Lowerer {
   std::vector<ValState> state_;
   std::map<int, Fused> fused_;
   std::set<int> absorbed_;
+  std::vector<bool> reach_;
+  std::map<int, std::pair<BufRef, BufRef>> sdpa_saved_;  // training forward anchor -> (bf16 O, lse)
   std::vector<bool> live_;
   std::vector<Temp> temps_;
   std::vector<bool> out_written_;

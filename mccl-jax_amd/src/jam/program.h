@@ -29,7 +29,7 @@ struct BufRef {
 
 enum class StepKind : uint8_t {
   kGemm, kSdpa, kRowReduce, kArgmax, kLayerNorm, kGelu, kEw, kGather, kScatterAdd,
-  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy,
+  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas,
 };
 
 const char* StepName(StepKind k);

@@ -54,7 +54,8 @@ void* Resolve(const BufRef& b, const Frame& f) {
 
 // Step encodings (written by lower.cc):
 //   gemm     bufs A,B,C[,bias]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
-//   sdpa     bufs Q,K,V,O       i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
+//   gemm_blas bufs A,B,C        i as gemm (no epilogue)
+//   sdpa     bufs Q,K,V,O[,lse] i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
 //   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
 //   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
 //   layernorm bufs x,g,b,y      i io_type,rows,cols  f eps
@@ -65,6 +66,8 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   iota     bufs out           i out_type,rank,dim,dims...
 //   copy_strided bufs in,out    i elem_bytes,rank,dims...  strides
 //   softmax  bufs x,y           i io_type,rows,cols
+//   sdpa_bwd bufs q,k,v,o,dout,lse,dq,dk,dv,workspace
+//            i B,H,Sq,Sk,D, (b,h,s strides) of q,k,v,o,dout,dq,dk,dv, causal  f scale
 //   convert  bufs in,out        i in_type,out_type,n
 //   fill     bufs out           i elem_bytes,n,pattern
 //   copy     bufs in,out        i bytes
@@ -78,7 +81,16 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
                      i[10], i[11], P(2), i[12], i[13], s.bufs.size() > 3 ? P(3) : nullptr, int(i[14]));
     case StepKind::kSdpa:
       return mk_sdpa_fwd(st, i[0], i[1], i[2], i[3], i[4], P(0), i[5], i[6], i[7], P(1), i[8], i[9], i[10],
-                         P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], s.f[0], int(i[17]), nullptr);
+                         P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], s.f[0], int(i[17]),
+                         s.bufs.size() > 4 ? static_cast<float*>(P(4)) : nullptr);
+    case StepKind::kGemmBlas:
+      return mk_gemm_blas(st, int(i[0]), int(i[1]), i[2], i[3], i[4], i[5], P(0), i[6], i[7], i[8], P(1), i[9],
+                          i[10], i[11], P(2), i[12], i[13], 1.f, 0.f);
+    case StepKind::kSdpaBwd:
+      return mk_sdpa_bwd(st, i[0], i[1], i[2], i[3], i[4], P(0), i[5], i[6], i[7], P(1), i[8], i[9], i[10],
+                         P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], P(4), i[17], i[18], i[19],
+                         static_cast<const float*>(P(5)), P(6), i[20], i[21], i[22], P(7), i[23], i[24], i[25],
+                         P(8), i[26], i[27], i[28], s.f[0], int(i[29]), P(9));
     case StepKind::kRowReduce:
       return mk_row_reduce(st, int(i[0]), int(i[1]), int(i[2]), i[3], i[4], P(0), s.f[0], P(1));
     case StepKind::kArgmax:

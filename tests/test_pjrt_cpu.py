@@ -98,8 +98,10 @@ def test_compile_indexing(client):
 def test_compile_jitted_training_step(client):
     """The C5 step as one module (train_hlo: forward, reverse-mode gradients,
     Adam) compiles: one output per loss / parameter / m / v (/ gradient), the
-    embedding gather and its gradient's scatter-add, the products on the GEMM
-    and the split of the fused QKV gradient as strided copies."""
+    embedding gather and its gradient's scatter-add, the weight products on
+    the GEMM, each layer's attention forward and backward as one flash
+    forward (with lse) and one flash backward step (nothing S x S), and the
+    split of the fused QKV gradient as strided copies."""
     from mi355x_pjrt import gpt2, train_hlo
 
     cfg = gpt2.GPT2Config(n_layer=2, d_model=128, n_head=2, seq=128, batch=2, vocab=257)
@@ -109,9 +111,11 @@ def test_compile_jitted_training_step(client):
         assert len(types) == 1 + (4 if grads else 3) * k and shapes[0] == () and set(types) == {pjrt.F32}
         assert shapes[1:1 + k] == [s for _, s in cfg.param_shapes()]
     assert plan.count("] gather") == 1 and plan.count("] scatter_add") == 1
-    # per layer 4 weight products and 2 attention products forward, twice as
-    # many backward; the tied logits 1 + 2
-    assert plan.count("] gemm") == 2 * (6 + 12) + 3
+    # per layer 4 weight products forward and 8 backward; the tied logits
+    # 1 + 2; the attention products are inside the two flash steps
+    assert plan.count("] gemm") == 2 * 12 + 3
+    assert plan.count("pattern sdpa_train(causal") == 2
+    assert plan.count("] sdpa (causal +lse)") == 2 and plan.count("] sdpa_bwd (causal)") == 2
     assert "copy_strided" in plan
 
 
