@@ -209,12 +209,16 @@ _EW_NAMES = ("CONST ADD SUB MUL DIV MAX MIN POW NEG EXP LOG TANH SQRT RSQRT ABS 
 EW = {n: i for i, n in enumerate(_EW_NAMES)}  # mirrors enum mk_ew_op in include/mk_kernels.h
 
 
-def ew_program(shape, inputs, program, consts, out_reg, out_dtype, stream=None):
+def ew_program(shape, inputs, program, consts, out_reg, out_dtype, stream=None, out=None):
     """Run a fused elementwise program.  `inputs` are tensors broadcast (via
-    torch.expand views) to `shape`; `program` is a list of (op, dst, a, b)."""
+    torch.expand views) to `shape`; `program` is a list of (op, dst, a, b);
+    `out` (optional) a dense tensor of `shape` and `out_dtype` to write."""
     rank = len(shape)
     dev = inputs[0].device if inputs else "cuda"
-    out = torch.empty(shape, dtype=out_dtype, device=dev)
+    if out is None:
+        out = torch.empty(shape, dtype=out_dtype, device=dev)
+    elif tuple(out.shape) != tuple(shape) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("ew_program: out must be a dense tensor of the given shape and dtype")
     ptrs = (ctypes.c_void_p * max(len(inputs), 1))(*[t.data_ptr() for t in inputs])
     types = (ctypes.c_int * max(len(inputs), 1))(*[mk_dtype(t.dtype) for t in inputs])
     strides = (ctypes.c_int64 * (6 * max(len(inputs), 1)))()

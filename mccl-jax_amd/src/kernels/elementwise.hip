@@ -201,32 +201,38 @@ __device__ __attribute__((always_inline)) inline void ew_run(const EwArgs& A, fl
 
 // The whole program block travels as a by-value kernel argument (< 2 KiB),
 // so a launch needs no device-side staging buffer.
+// One element per thread.  IdxT = int32_t when n and every input offset
+// fit 31 bits (the index decomposition is then 32-bit division), int64_t
+// otherwise.
+template <typename IdxT>
 __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n, void* out) {
-  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (i >= n) return;
+  const int64_t i64 = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (i64 >= n) return;
+  const IdxT i = IdxT(i64);
   float r[kEwMaxRegs];
 #pragma unroll
   for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
   const int rank = A.rank;
-  int64_t idx[kEwMaxRank];
+  IdxT idx[kEwMaxRank];
   if (A.need_index) {
-    int64_t rem = i;
+    IdxT rem = i;
     for (int d = rank - 1; d >= 0; --d) {
-      idx[d] = rem % A.dims[d];
-      rem /= A.dims[d];
+      const IdxT n_d = IdxT(A.dims[d]);
+      idx[d] = rem % n_d;
+      rem /= n_d;
     }
   }
   for (int t = 0; t < A.n_inputs; ++t) {
-    int64_t off = 0;
+    IdxT off = 0;
     if (A.in_mode[t] == 1) {
       off = i;
     } else if (A.in_mode[t] == 2) {
-      for (int d = 0; d < rank; ++d) off += idx[d] * A.in_stride[t][d];
+      for (int d = 0; d < rank; ++d) off += idx[d] * IdxT(A.in_stride[t][d]);
     }
-    r[t] = ew_load(A.in[t], off, A.in_type[t]);
+    r[t] = ew_load(A.in[t], int64_t(off), A.in_type[t]);
   }
   ew_run(A, r);
-  ew_store(out, i, A.out_type, r[A.out_reg]);
+  ew_store(out, i64, A.out_type, r[A.out_reg]);
 }
 
 // The same program on kEwVec consecutive elements of the innermost dim per
@@ -491,9 +497,9 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
   }
   for (int c = 0; c < n_consts; ++c) a.consts[c] = consts[c];
   a.need_index = need_index;
-  // 32-bit form: the innermost dim a multiple of kEwVec, n and every input's
-  // largest offset below 2^31
-  bool narrow = rank >= 1 && dims[rank - 1] % kEwVec == 0 && n < (int64_t(1) << 31);
+  // 32-bit forms: n and every input's largest offset below 2^31; the vector
+  // kernel also needs the innermost dim a multiple of kEwVec
+  bool narrow = rank >= 1 && n < (int64_t(1) << 31);
   for (int t = 0; narrow && t < n_inputs; ++t) {
     int64_t hi = 0;
     for (int d = 0; d < rank; ++d) {
@@ -524,11 +530,14 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
     }
     a.out_vec = vec_ok(out, out_type, dense);
   }
-  if (narrow)
+  if (narrow && dims[rank - 1] % kEwVec == 0)
     hipLaunchKernelGGL(ew_program_vec_kernel, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
                        as_stream(stream), a, uint32_t(n), out);
+  else if (narrow)
+    hipLaunchKernelGGL(ew_program_kernel<int32_t>, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
+                       as_stream(stream), a, n, out);
   else
-    hipLaunchKernelGGL(ew_program_kernel, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
+    hipLaunchKernelGGL(ew_program_kernel<int64_t>, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
                        as_stream(stream), a, n, out);
   return check_launch("mk_ew_program");
 }

@@ -609,6 +609,35 @@ def test_iota_convert_fill_copy(K):
                                   np.broadcast_to(np.arange(5, dtype=np.float32).reshape(5, 1), (5, 3)))
 
 
+def test_ew_program_ragged_rows(K):
+    """Rows whose length is not a multiple of 4 (a 50257-wide vocabulary):
+    groups of 4 along a row with a partial last group, no 4-wide access; a
+    transposed input, a broadcast column, bf16 output, and a rank-1 tensor
+    (which passes the alignment test with no outer stride to reject it)."""
+    E = K.EW
+    rng = np.random.default_rng(15)
+    for rows, cols in ((9, 257), (3, 50257), (1, 7), (5, 1)):
+        print(f"case: ew ragged {rows}x{cols}", flush=True)
+        x = rng.standard_normal((cols, rows)).astype(np.float32)  # read transposed
+        c = rng.standard_normal((rows, 1)).astype(np.float32)
+        xd = torch.from_numpy(x).cuda().t()
+        cd = torch.from_numpy(c).cuda()
+        prog = [(E["SUB"], 2, 0, 1), (E["MUL"], 3, 2, 2)]  # (x - c)^2: IEEE ops, one bf16 rounding
+        got = host_bf16(K.ew_program((rows, cols), [xd, cd], prog, [], 3, torch.bfloat16))
+        d = (x.T - c).astype(np.float32)
+        want = bf16.to_bf16_bits((d * d).astype(np.float32))
+        np.testing.assert_array_equal(got, want)
+    for n in (1001, 3, 4096 + 2):
+        print(f"case: ew ragged rank-1 n={n}", flush=True)
+        a = rng.standard_normal(n).astype(np.float32)
+        guard = torch.full((n + 64,), 7.0, device="cuda")
+        out = guard[:n]
+        got = K.ew_program((n,), [torch.from_numpy(a).cuda()], [(E["ADD"], 1, 0, 0)], [], 1, torch.float32,
+                           out=out)
+        np.testing.assert_array_equal(got.cpu().numpy(), a + a)
+        assert torch.all(guard[n:] == 7.0).item()
+
+
 def test_ew_program_fused_chain(K):
     """relu(x * w + b) with a broadcast row vector, plus a select/compare chain."""
     E = K.EW
