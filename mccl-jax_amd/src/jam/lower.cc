@@ -56,6 +56,7 @@ const char* StepName(StepKind k) {
     case StepKind::kCopy: return "copy";
     case StepKind::kSdpaBwd: return "sdpa_bwd";
     case StepKind::kGemmBlas: return "gemm_blas";
+    case StepKind::kSoftmaxXent: return "softmax_xent";
   }
   return "?";
 }
@@ -83,6 +84,7 @@ CompileOptions OptionsFromEnv() {
   o.fuse_layernorm = getenv("JAM_NO_LAYERNORM") == nullptr;
   o.fuse_gelu = getenv("JAM_NO_GELU") == nullptr;
   o.fuse_elementwise = getenv("JAM_NO_EW_FUSION") == nullptr;
+  o.fuse_xent = getenv("JAM_NO_XENT") == nullptr;
   return o;
 }
 
@@ -330,7 +332,7 @@ struct ValState {
 };
 
 struct Fused {
-  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu, kSdpaBwd } kind;
+  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu, kSdpaBwd, kXent } kind;
   std::vector<int> deps;  // value ids the fused step reads
   // sdpa (train: also lse and the bf16 O for the backward step)
   int q = -1, k = -1, v = -1;
@@ -339,6 +341,8 @@ struct Fused {
   bool train = false;
   // sdpa_bwd: dO (bf16), the forward's anchor, the three gradients
   int dout = -1, fwd = -1, dq = -1, dk = -1, dv = -1;
+  // softmax cross-entropy: logits (x), labels, per-row loss and dlogits values
+  int labels = -1, dlogits = -1;
   // argmax
   int x = -1;
   bool is_min = false;
@@ -407,6 +411,7 @@ class Lowerer {
       case StepKind::kSdpa: return s.bufs.size() > 4 ? std::vector<size_t>{3, 4} : std::vector<size_t>{3};
       case StepKind::kSdpaBwd: return {6, 7, 8, 9};
       case StepKind::kGemmBlas: return {2};
+      case StepKind::kSoftmaxXent: return {2, 3};
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
@@ -691,9 +696,13 @@ class Lowerer {
           opts_.fuse_argmax)
         TryMatchArgmax(int(i));
     }
+    if (opts_.fuse_xent)
+      for (size_t i = 0; i < ops_.size(); ++i)
+        if (ops_[i].name == "stablehlo.subtract" && !fused_.count(int(i))) TryMatchXent(int(i));
     if (opts_.fuse_gemm_epilogue)
       for (size_t i = 0; i < ops_.size(); ++i)
-        if (ops_[i].name == "stablehlo.add" && !fused_.count(int(i))) TryMatchGemmEpilogue(int(i));
+        if (ops_[i].name == "stablehlo.add" && !fused_.count(int(i)) && !absorbed_.count(int(i)))
+          TryMatchGemmEpilogue(int(i));
     if (opts_.fuse_gelu)
       for (size_t i = 0; i < ops_.size(); ++i)
         if (ops_[i].name == "stablehlo.multiply" && !fused_.count(int(i))) TryMatchGelu(int(i));
@@ -1631,6 +1640,173 @@ class Lowerer {
       if (o != anchor && o != banchor) absorbed_.insert(o);
     prog_->patterns.push_back(std::string("sdpa_train(") + (r.causal ? "causal" : "full") + ", scale=" +
                               std::to_string(r.scale) + ")");
+  }
+
+  // value of a scalar expression of splat constants (multiply, divide,
+  // negate, add, subtract; broadcasts and reshapes looked through)
+  bool const_eval(int v, double* out, int depth = 0) const {
+    if (scalar_of(v, out)) return true;
+    const Op* p = prod(v);
+    if (!p || depth > 8 || m_.types[v].numel() != 1) return false;
+    if (p->name == "stablehlo.broadcast_in_dim" || p->name == "stablehlo.reshape")
+      return const_eval(p->operands[0], out, depth + 1);
+    if (p->name == "stablehlo.negate") {
+      if (!const_eval(p->operands[0], out, depth + 1)) return false;
+      *out = -*out;
+      return true;
+    }
+    double a, b;
+    if (p->operands.size() != 2 || !const_eval(p->operands[0], &a, depth + 1) ||
+        !const_eval(p->operands[1], &b, depth + 1))
+      return false;
+    if (p->name == "stablehlo.multiply") *out = a * b;
+    else if (p->name == "stablehlo.divide") *out = a / b;
+    else if (p->name == "stablehlo.add") *out = a + b;
+    else if (p->name == "stablehlo.subtract") *out = a - b;
+    else return false;
+    if (m_.types[v].dtype == DType::kF32) *out = float(*out);
+    return true;
+  }
+
+  // Softmax cross-entropy with integer labels over the rows of fp32 / bf16
+  // logits X [T, V], with the gradient jax.grad emits for its mean:
+  //   M = max(X) (behind stop_gradient), E = exp(X - M), Z = sum(E)
+  //   loss_rows = (log Z + M) - sum(select(X's column == label, X, 0))
+  //   dX = select(onehot, bcast(-g), 0) + bcast(g / Z) * E
+  // with g = bcast(c) the per-row cotangent of a constant c (1/T for the
+  // mean).  Anchored at the loss_rows subtract: one mk_softmax_xent launch
+  // writes loss_rows and dX (which no other op computes then).  Labels
+  // outside [0, V) give NaN there (the module would drop the target term).
+  void TryMatchXent(int anchor) {
+    const Op& dsub = ops_[anchor];
+    const int LSE = dsub.operands[0], PK = dsub.operands[1];
+    if (m_.types[LSE].rank() != 1) return;
+    const int64_t T = m_.types[LSE].dims[0];
+    std::set<int> ops = {anchor};
+    auto row_bcast_of = [&](int v, int* src) {  // broadcast_in_dim [T] -> [T, V] along dim 0
+      const Op* b = prod(v);
+      if (!b || b->name != "stablehlo.broadcast_in_dim" || attr_ints(*b, {"dims", "broadcast_dimensions"}) != std::vector<int64_t>{0})
+        return false;
+      *src = b->operands[0];
+      return m_.types[*src].rank() == 1;
+    };
+    // lse = log(Z) + M
+    const Op* ad = prod(LSE);
+    if (!ad || ad->name != "stablehlo.add") return;
+    ops.insert(producer_[LSE]);
+    int LG = ad->operands[0], M = ad->operands[1];
+    if (!is(LG, "stablehlo.log")) std::swap(LG, M);
+    if (!is(LG, "stablehlo.log")) return;
+    ops.insert(producer_[LG]);
+    const int Z = prod(LG)->operands[0];
+    if (!is_reduce_over_last(Z, "stablehlo.add", 2)) return;
+    ops.insert(producer_[Z]);
+    const int E = prod(Z)->operands[0];
+    if (!is(E, "stablehlo.exponential")) return;
+    ops.insert(producer_[E]);
+    const int SH = prod(E)->operands[0];
+    if (!is(SH, "stablehlo.subtract")) return;
+    ops.insert(producer_[SH]);
+    const int X = prod(SH)->operands[0];
+    int Msrc = -1;
+    if (!row_bcast_of(prod(SH)->operands[1], &Msrc) || Msrc != M) return;
+    ops.insert(producer_[prod(SH)->operands[1]]);
+    if (!is_reduce_over_last(M, "stablehlo.maximum", 2) || prod(M)->operands[0] != X) return;
+    ops.insert(producer_[M]);
+    const TensorType& xt = m_.types[X];
+    if (xt.rank() != 2 || xt.dims[0] != T || (xt.dtype != DType::kF32 && xt.dtype != DType::kBF16)) return;
+    const int64_t V = xt.dims[1];
+    // picked = sum(select(onehot, X, 0)); onehot = compare EQ (iota over dim 1, bcast(labels))
+    if (!is_reduce_over_last(PK, "stablehlo.add", 2)) return;
+    ops.insert(producer_[PK]);
+    const int SEL = prod(PK)->operands[0];
+    if (!is(SEL, "stablehlo.select")) return;
+    const Op* sel = prod(SEL);
+    double z;
+    if (sel->operands[1] != X || !scalar_of(sel->operands[2], &z) || z != 0.0) return;
+    ops.insert(producer_[SEL]);
+    const int OH = sel->operands[0];
+    const Op* cmp = prod(OH);
+    if (!cmp || cmp->name != "stablehlo.compare") return;
+    {
+      std::string d;
+      if (const Attr* x = cmp->attr("comparison_direction")) d = x->s;
+      else if (const Attr* x = cmp->attr("enum0")) d = x->s;
+      if (d != "EQ") return;
+    }
+    int IO = cmp->operands[0], LB = cmp->operands[1];
+    if (!is(IO, "stablehlo.iota")) std::swap(IO, LB);
+    if (!is(IO, "stablehlo.iota") || attr_ints(*prod(IO), {"dim", "iota_dimension"}) != std::vector<int64_t>{1}) return;
+    int lab = -1;
+    if (!row_bcast_of(LB, &lab)) return;
+    while (is(lab, "stablehlo.convert")) lab = prod(lab)->operands[0];
+    const DType lt = m_.types[lab].dtype;
+    if (m_.types[lab].rank() != 1 || (lt != DType::kI32 && lt != DType::kI64)) return;
+    ops.insert(producer_[OH]);
+    ops.insert(producer_[LB]);
+    ops.insert(producer_[IO]);
+    // the gradient: add(select(onehot, bcast(-g), 0), mul(bcast(g / Z), E))
+    int dX = -1, gscale_v = -1;
+    for (int u : live_users(OH)) {
+      if (u == producer_[SEL] || ops_[u].name != "stablehlo.select") continue;
+      const Op& s2 = ops_[u];
+      double zz;
+      int negsrc = -1;
+      if (s2.operands[0] != OH || !scalar_of(s2.operands[2], &zz) || zz != 0.0 || !row_bcast_of(s2.operands[1], &negsrc) ||
+          !is(negsrc, "stablehlo.negate"))
+        continue;
+      const int g = prod(negsrc)->operands[0];
+      const auto us = live_users(s2.results[0]);
+      if (us.size() != 1 || ops_[us[0]].name != "stablehlo.add") continue;
+      const Op& a2 = ops_[us[0]];
+      const int other_t = a2.operands[0] == s2.results[0] ? a2.operands[1] : a2.operands[0];
+      const Op* m2 = prod(other_t);
+      if (!m2 || m2->name != "stablehlo.multiply") continue;
+      int bsrc = -1;
+      const int mb = m2->operands[0] == E ? m2->operands[1] : m2->operands[0];
+      if ((m2->operands[0] != E && m2->operands[1] != E) || !row_bcast_of(mb, &bsrc) || !is(bsrc, "stablehlo.divide"))
+        continue;
+      const Op* dv = prod(bsrc);
+      if (dv->operands[0] != g || dv->operands[1] != Z) continue;
+      ops.insert(u);
+      ops.insert(producer_[s2.operands[1]]);
+      ops.insert(producer_[negsrc]);
+      ops.insert(us[0]);
+      ops.insert(producer_[other_t]);
+      ops.insert(producer_[mb]);
+      ops.insert(producer_[bsrc]);
+      dX = a2.results[0];
+      gscale_v = g;
+    }
+    if (dX < 0) return;
+    // g: the row broadcast of a constant
+    const Op* gb = prod(gscale_v);
+    if (!gb || gb->name != "stablehlo.broadcast_in_dim") return;
+    double gscale;
+    if (!const_eval(gb->operands[0], &gscale)) return;
+    ops.insert(producer_[gscale_v]);
+    // every other result stays inside
+    for (int o : ops)
+      for (int res : ops_[o].results) {
+        if (res == dsub.results[0] || res == dX) continue;
+        for (int oo : outputs_)
+          if (oo == res) return;
+        for (int u : live_users(res))
+          if (!ops.count(u)) return;
+      }
+    if (m_.types[dX].dtype != xt.dtype || m_.types[dsub.results[0]].dtype != DType::kF32) return;
+    Fused f;
+    f.kind = Fused::kXent;
+    f.x = X;
+    f.labels = lab;
+    f.dlogits = dX;
+    f.scale = float(gscale);
+    f.deps = {X, lab};
+    fused_[anchor] = f;
+    for (int o : ops)
+      if (o != anchor) absorbed_.insert(o);
+    prog_->patterns.push_back("softmax_xent(" + std::to_string(T) + "x" + std::to_string(V) + ", grad_scale=" +
+                              std::to_string(gscale) + ")");
   }
 
   void TryMatchArgmax(int anchor) {
@@ -2927,6 +3103,24 @@ class Lowerer {
         EmitConvert(d, DType::kBF16, o, m_.types[res].dtype, n);
         SetDenseView(res, o);
       }
+      return;
+    }
+    if (f.kind == Fused::kXent) {
+      View x = NeedView(f.x);
+      if (!x.dense()) x = Densify(x);
+      View lab = NeedView(f.labels);
+      if (!lab.dense()) lab = Densify(lab);
+      const int res = op.results[0];
+      BufRef lr = DestFor(res);
+      BufRef dx = DestFor(f.dlogits);
+      Step st;
+      st.kind = StepKind::kSoftmaxXent;
+      st.bufs = {x.at(), lab.at(), lr, dx};
+      st.i = {int64_t(x.dtype), x.dims[0], x.dims[1], int64_t(lab.dtype)};
+      st.f = {f.scale};
+      Emit(st);
+      SetDenseView(res, lr);
+      SetDenseView(f.dlogits, dx);
       return;
     }
     if (f.kind == Fused::kSdpaBwd) {

@@ -29,7 +29,7 @@ struct BufRef {
 
 enum class StepKind : uint8_t {
   kGemm, kSdpa, kRowReduce, kArgmax, kLayerNorm, kGelu, kEw, kGather, kScatterAdd,
-  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas,
+  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas, kSoftmaxXent,
 };
 
 const char* StepName(StepKind k);
@@ -85,6 +85,7 @@ struct CompileOptions {
   bool fuse_layernorm = true;
   bool fuse_gelu = true;
   bool fuse_elementwise = true;
+  bool fuse_xent = true;        // env JAM_NO_XENT disables
 };
 
 struct CompileResult {

@@ -100,8 +100,9 @@ def test_compile_jitted_training_step(client):
     Adam) compiles: one output per loss / parameter / m / v (/ gradient), the
     embedding gather and its gradient's scatter-add, the weight products on
     the GEMM, each layer's attention forward and backward as one flash
-    forward (with lse) and one flash backward step (nothing S x S), and the
-    split of the fused QKV gradient as strided copies."""
+    forward (with lse) and one flash backward step (nothing S x S), the
+    cross-entropy with its gradient as one launch, and the split of the fused
+    QKV gradient as strided copies."""
     from mi355x_pjrt import gpt2, train_hlo
 
     cfg = gpt2.GPT2Config(n_layer=2, d_model=128, n_head=2, seq=128, batch=2, vocab=257)
@@ -116,6 +117,8 @@ def test_compile_jitted_training_step(client):
     assert plan.count("] gemm") == 2 * 12 + 3
     assert plan.count("pattern sdpa_train(causal") == 2
     assert plan.count("] sdpa (causal +lse)") == 2 and plan.count("] sdpa_bwd (causal)") == 2
+    # the mean softmax cross-entropy and its gradient: one fused launch
+    assert "pattern softmax_xent(256x257, grad_scale=0.003906)" in plan and plan.count("] softmax_xent") == 1
     assert "copy_strided" in plan
 
 
