@@ -127,75 +127,100 @@ __device__ inline float sign_f(float x) {
 }
 
 // Runs the program on the register file r (inputs already in r[0 ..
-// n_inputs)).
-__device__ __attribute__((always_inline)) inline void ew_run(const EwArgs& A, float (&r)[kEwMaxRegs]) {
+// n_inputs)).  Each register holds W lanes (W consecutive elements of one
+// thread; lane e of register k is r[e][k], each lane its own array so that
+// each is indexed by the wave-uniform register number alone); an instruction is decoded once and applied to every lane with the
+// same fp32 expression, so W = 4 gives the same bits per element as W = 1
+// while paying the decode (scalar loads and the opcode dispatch) once per W
+// elements.  NR (a power of two) registers per lane: the host checks that
+// every register operand, destination and input is below NR; the operand
+// fields are masked to NR - 1 because both are read for every opcode and a
+// CONST's first field is a constant index, not a register.
+template <int W, int NR>
+__device__ __attribute__((always_inline)) inline void ew_run(const EwArgs& A, float* const (&r)[W]) {
+  static_assert((NR & (NR - 1)) == 0 && NR <= kEwMaxRegs, "NR: a power of two, at most kEwMaxRegs");
   for (int p = 0; p < A.n_instr; ++p) {
-    const int op = A.prog[p][0], dst = A.prog[p][1], a = A.prog[p][2], b = A.prog[p][3];
-    const float va = r[a];
-    const float vb = r[b & 0xffff];
-    float o;
+    const int op = A.prog[p][0], dst = A.prog[p][1] & (NR - 1), a = A.prog[p][2] & (NR - 1), b = A.prog[p][3];
+    float va[W], vb[W], o[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) {
+      va[e] = r[e][a];
+      vb[e] = r[e][b & (NR - 1)];
+    }
+    // o[e] = f(va[e], vb[e]) on every lane
+    auto each = [&](auto f) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < W; ++e) o[e] = f(va[e], vb[e]);
+    };
     switch (op) {
-      case MK_EW_CONST: o = A.consts[a]; break;
-      case MK_EW_ADD: o = va + vb; break;
-      case MK_EW_SUB: o = va - vb; break;
-      case MK_EW_MUL: o = va * vb; break;
-      case MK_EW_DIV: o = va / vb; break;
-      case MK_EW_MAX: o = (va != va || vb != vb) ? __builtin_nanf("") : fmaxf(va, vb); break;
-      case MK_EW_MIN: o = (va != va || vb != vb) ? __builtin_nanf("") : fminf(va, vb); break;
-      case MK_EW_POW: o = powf(va, vb); break;
-      case MK_EW_NEG: o = -va; break;
-      case MK_EW_EXP: o = expf(va); break;
-      case MK_EW_LOG: o = logf(va); break;
-      case MK_EW_TANH: o = tanhf(va); break;
-      case MK_EW_SQRT: o = sqrtf(va); break;
-      case MK_EW_RSQRT: o = 1.f / sqrtf(va); break;
-      case MK_EW_ABS: o = fabsf(va); break;
-      case MK_EW_LOGISTIC: o = 1.f / (1.f + expf(-va)); break;
-      case MK_EW_CMP_EQ: o = va == vb ? 1.f : 0.f; break;
-      case MK_EW_CMP_NE: o = va != vb ? 1.f : 0.f; break;
-      case MK_EW_CMP_LT: o = va < vb ? 1.f : 0.f; break;
-      case MK_EW_CMP_LE: o = va <= vb ? 1.f : 0.f; break;
-      case MK_EW_CMP_GT: o = va > vb ? 1.f : 0.f; break;
-      case MK_EW_CMP_GE: o = va >= vb ? 1.f : 0.f; break;
-      case MK_EW_SELECT: o = va != 0.f ? r[b & 0xffff] : r[(b >> 16) & 0xffff]; break;
-      case MK_EW_CLAMP: {
-        const float lo = r[b & 0xffff], hi = r[(b >> 16) & 0xffff];
-        o = fminf(fmaxf(va, lo), hi);
+      case MK_EW_CONST: each([&](float, float) { return A.consts[A.prog[p][2]]; }); break;
+      case MK_EW_ADD: each([](float x, float y) { return x + y; }); break;
+      case MK_EW_SUB: each([](float x, float y) { return x - y; }); break;
+      case MK_EW_MUL: each([](float x, float y) { return x * y; }); break;
+      case MK_EW_DIV: each([](float x, float y) { return x / y; }); break;
+      case MK_EW_MAX: each([](float x, float y) { return (x != x || y != y) ? __builtin_nanf("") : fmaxf(x, y); }); break;
+      case MK_EW_MIN: each([](float x, float y) { return (x != x || y != y) ? __builtin_nanf("") : fminf(x, y); }); break;
+      case MK_EW_POW: each([](float x, float y) { return powf(x, y); }); break;
+      case MK_EW_NEG: each([](float x, float) { return -x; }); break;
+      case MK_EW_EXP: each([](float x, float) { return expf(x); }); break;
+      case MK_EW_LOG: each([](float x, float) { return logf(x); }); break;
+      case MK_EW_TANH: each([](float x, float) { return tanhf(x); }); break;
+      case MK_EW_SQRT: each([](float x, float) { return sqrtf(x); }); break;
+      case MK_EW_RSQRT: each([](float x, float) { return 1.f / sqrtf(x); }); break;
+      case MK_EW_ABS: each([](float x, float) { return fabsf(x); }); break;
+      case MK_EW_LOGISTIC: each([](float x, float) { return 1.f / (1.f + expf(-x)); }); break;
+      case MK_EW_CMP_EQ: each([](float x, float y) { return x == y ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_NE: each([](float x, float y) { return x != y ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_LT: each([](float x, float y) { return x < y ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_LE: each([](float x, float y) { return x <= y ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_GT: each([](float x, float y) { return x > y ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_GE: each([](float x, float y) { return x >= y ? 1.f : 0.f; }); break;
+      case MK_EW_SELECT: {
+        const int c = (b >> 16) & (NR - 1);
+#pragma unroll
+        for (int e = 0; e < W; ++e) o[e] = va[e] != 0.f ? vb[e] : r[e][c];
         break;
       }
-      case MK_EW_ROUND_BF16: o = bf16_to_f32(f32_to_bf16(va)); break;
-      case MK_EW_ROUND_F16: o = f16_to_f32(f32_to_f16(va)); break;
-      case MK_EW_FLOOR: o = floorf(va); break;
-      case MK_EW_CEIL: o = ceilf(va); break;
-      case MK_EW_SIGN: o = sign_f(va); break;
-      case MK_EW_AND: o = (va != 0.f && vb != 0.f) ? 1.f : 0.f; break;
-      case MK_EW_OR: o = (va != 0.f || vb != 0.f) ? 1.f : 0.f; break;
-      case MK_EW_NOT: o = va == 0.f ? 1.f : 0.f; break;
-      case MK_EW_MOV: o = va; break;
-      case MK_EW_CMP_LT_S32: o = as_i(va) < as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_CMP_GE_S32: o = as_i(va) >= as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_ADD_S32: o = as_f(as_i(va) + as_i(vb)); break;
-      case MK_EW_SUB_S32: o = as_f(as_i(va) - as_i(vb)); break;
-      case MK_EW_MUL_S32: o = as_f(as_i(va) * as_i(vb)); break;
-      case MK_EW_S32_TO_F32: o = float(as_i(va)); break;
-      case MK_EW_F32_TO_S32: o = as_f(int32_t(va)); break;
-      case MK_EW_ERF: o = erff(va); break;
-      case MK_EW_CMP_EQ_S32: o = as_i(va) == as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_CMP_NE_S32: o = as_i(va) != as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_CMP_LE_S32: o = as_i(va) <= as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_CMP_GT_S32: o = as_i(va) > as_i(vb) ? 1.f : 0.f; break;
-      case MK_EW_MAX_S32: o = as_f(max(as_i(va), as_i(vb))); break;
-      case MK_EW_MIN_S32: o = as_f(min(as_i(va), as_i(vb))); break;
-      case MK_EW_NEG_S32: o = as_f(-as_i(va)); break;
-      case MK_EW_AND_B32: o = as_f(as_i(va) & as_i(vb)); break;
-      case MK_EW_OR_B32: o = as_f(as_i(va) | as_i(vb)); break;
-      case MK_EW_XOR_B32: o = as_f(as_i(va) ^ as_i(vb)); break;
-      case MK_EW_PRED_TO_S32: o = as_f(va != 0.f ? 1 : 0); break;
-      case MK_EW_S32_TO_PRED: o = as_i(va) != 0 ? 1.f : 0.f; break;
-      case MK_EW_U32_TO_F32: o = float(uint32_t(as_i(va))); break;
-      default: o = 0.f; break;
+      case MK_EW_CLAMP: {
+        const int c = (b >> 16) & (NR - 1);
+#pragma unroll
+        for (int e = 0; e < W; ++e) o[e] = fminf(fmaxf(va[e], vb[e]), r[e][c]);
+        break;
+      }
+      case MK_EW_ROUND_BF16: each([](float x, float) { return bf16_to_f32(f32_to_bf16(x)); }); break;
+      case MK_EW_ROUND_F16: each([](float x, float) { return f16_to_f32(f32_to_f16(x)); }); break;
+      case MK_EW_FLOOR: each([](float x, float) { return floorf(x); }); break;
+      case MK_EW_CEIL: each([](float x, float) { return ceilf(x); }); break;
+      case MK_EW_SIGN: each([](float x, float) { return sign_f(x); }); break;
+      case MK_EW_AND: each([](float x, float y) { return (x != 0.f && y != 0.f) ? 1.f : 0.f; }); break;
+      case MK_EW_OR: each([](float x, float y) { return (x != 0.f || y != 0.f) ? 1.f : 0.f; }); break;
+      case MK_EW_NOT: each([](float x, float) { return x == 0.f ? 1.f : 0.f; }); break;
+      case MK_EW_MOV: each([](float x, float) { return x; }); break;
+      case MK_EW_CMP_LT_S32: each([](float x, float y) { return as_i(x) < as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_GE_S32: each([](float x, float y) { return as_i(x) >= as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_ADD_S32: each([](float x, float y) { return as_f(as_i(x) + as_i(y)); }); break;
+      case MK_EW_SUB_S32: each([](float x, float y) { return as_f(as_i(x) - as_i(y)); }); break;
+      case MK_EW_MUL_S32: each([](float x, float y) { return as_f(as_i(x) * as_i(y)); }); break;
+      case MK_EW_S32_TO_F32: each([](float x, float) { return float(as_i(x)); }); break;
+      case MK_EW_F32_TO_S32: each([](float x, float) { return as_f(int32_t(x)); }); break;
+      case MK_EW_ERF: each([](float x, float) { return erff(x); }); break;
+      case MK_EW_CMP_EQ_S32: each([](float x, float y) { return as_i(x) == as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_NE_S32: each([](float x, float y) { return as_i(x) != as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_LE_S32: each([](float x, float y) { return as_i(x) <= as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_CMP_GT_S32: each([](float x, float y) { return as_i(x) > as_i(y) ? 1.f : 0.f; }); break;
+      case MK_EW_MAX_S32: each([](float x, float y) { return as_f(max(as_i(x), as_i(y))); }); break;
+      case MK_EW_MIN_S32: each([](float x, float y) { return as_f(min(as_i(x), as_i(y))); }); break;
+      case MK_EW_NEG_S32: each([](float x, float) { return as_f(-as_i(x)); }); break;
+      case MK_EW_AND_B32: each([](float x, float y) { return as_f(as_i(x) & as_i(y)); }); break;
+      case MK_EW_OR_B32: each([](float x, float y) { return as_f(as_i(x) | as_i(y)); }); break;
+      case MK_EW_XOR_B32: each([](float x, float y) { return as_f(as_i(x) ^ as_i(y)); }); break;
+      case MK_EW_PRED_TO_S32: each([](float x, float) { return as_f(x != 0.f ? 1 : 0); }); break;
+      case MK_EW_S32_TO_PRED: each([](float x, float) { return as_i(x) != 0 ? 1.f : 0.f; }); break;
+      case MK_EW_U32_TO_F32: each([](float x, float) { return float(uint32_t(as_i(x))); }); break;
+      default: each([](float, float) { return 0.f; }); break;
     }
-    r[dst] = o;
+#pragma unroll
+    for (int e = 0; e < W; ++e) r[e][dst] = o[e];
   }
 }
 
@@ -209,9 +234,10 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
   const int64_t i64 = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (i64 >= n) return;
   const IdxT i = IdxT(i64);
-  float r[kEwMaxRegs];
+  float reg[kEwMaxRegs];
+  float* const r[1] = {reg};
 #pragma unroll
-  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
+  for (int k = 0; k < kEwMaxRegs; ++k) r[0][k] = 0.f;
   const int rank = A.rank;
   IdxT idx[kEwMaxRank];
   if (A.need_index) {
@@ -229,10 +255,10 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
     } else if (A.in_mode[t] == 2) {
       for (int d = 0; d < rank; ++d) off += idx[d] * IdxT(A.in_stride[t][d]);
     }
-    r[t] = ew_load(A.in[t], int64_t(off), A.in_type[t]);
+    r[0][t] = ew_load(A.in[t], int64_t(off), A.in_type[t]);
   }
-  ew_run(A, r);
-  ew_store(out, i64, A.out_type, r[A.out_reg]);
+  ew_run<1, kEwMaxRegs>(A, r);
+  ew_store(out, i64, A.out_type, r[0][A.out_reg]);
 }
 
 // The same program on kEwVec consecutive elements of the innermost dim per
@@ -241,19 +267,29 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
 // once per thread in 32-bit arithmetic, and the inputs of all kEwVec
 // elements are loaded before the program runs on the first of them.
 constexpr int kEwVec = 4;
+template <int NR>
 __global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, uint32_t n, void* out) {
   const uint32_t i0 = (blockIdx.x * uint32_t(kBlock) + threadIdx.x) * kEwVec;
   if (i0 >= n) return;
   uint32_t idx[kEwMaxRank];
   if (A.need_index) {
+    // loops over the maximum rank with static indices keep idx in registers
     uint32_t rem = i0;
-    for (int d = A.rank - 1; d >= 0; --d) {
-      const uint32_t n_d = uint32_t(A.dims[d]);
-      idx[d] = rem % n_d;
-      rem /= n_d;
+#pragma unroll
+    for (int d = kEwMaxRank - 1; d >= 0; --d) {
+      if (d < A.rank) {
+        const uint32_t n_d = uint32_t(A.dims[d]);
+        idx[d] = rem % n_d;
+        rem /= n_d;
+      }
     }
   }
-  float v[kEwVec][kEwMaxInputs];
+  float reg0[NR], reg1[NR], reg2[NR], reg3[NR];
+  float* const r[kEwVec] = {reg0, reg1, reg2, reg3};
+#pragma unroll
+  for (int e = 0; e < kEwVec; ++e)
+#pragma unroll
+    for (int k = 0; k < NR; ++k) r[e][k] = 0.f;
 #pragma unroll
   for (int t = 0; t < kEwMaxInputs; ++t) {
     if (t >= A.n_inputs) break;
@@ -262,40 +298,31 @@ __global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, 
       off = int32_t(i0);
       step = 1;
     } else if (A.in_mode[t] == 2) {
-      for (int d = 0; d < A.rank; ++d) off += int32_t(idx[d]) * int32_t(A.in_stride[t][d]);
+#pragma unroll
+      for (int d = 0; d < kEwMaxRank; ++d)
+        if (d < A.rank) off += int32_t(idx[d]) * int32_t(A.in_stride[t][d]);
       step = int32_t(A.in_stride[t][A.rank - 1]);
     }
     if (A.in_vec[t] && A.in_type[t] == MK_F32) {
       const f32x4 w = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(A.in[t]) + off);
 #pragma unroll
-      for (int e = 0; e < kEwVec; ++e) v[e][t] = w.v[e];
+      for (int e = 0; e < kEwVec; ++e) r[e][t] = w.v[e];
     } else if (A.in_vec[t]) {  // bf16
       const uint2 w = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(A.in[t]) + off);
-      v[0][t] = bf16_to_f32(uint16_t(w.x));
-      v[1][t] = bf16_to_f32(uint16_t(w.x >> 16));
-      v[2][t] = bf16_to_f32(uint16_t(w.y));
-      v[3][t] = bf16_to_f32(uint16_t(w.y >> 16));
+      r[0][t] = bf16_to_f32(uint16_t(w.x));
+      r[1][t] = bf16_to_f32(uint16_t(w.x >> 16));
+      r[2][t] = bf16_to_f32(uint16_t(w.y));
+      r[3][t] = bf16_to_f32(uint16_t(w.y >> 16));
     } else {
 #pragma unroll
-      for (int e = 0; e < kEwVec; ++e) v[e][t] = ew_load(A.in[t], off + e * step, A.in_type[t]);
+      for (int e = 0; e < kEwVec; ++e) r[e][t] = ew_load(A.in[t], off + e * step, A.in_type[t]);
     }
   }
-  float r[kEwMaxRegs];
+  // the program runs once on 4-lane registers
+  ew_run<kEwVec, NR>(A, r);
+  float o[kEwVec];
 #pragma unroll
-  for (int k = 0; k < kEwMaxRegs; ++k) r[k] = 0.f;
-  // one copy of the interpreter: element e's inputs and result move by
-  // selects, so no register array is indexed by e
-  float o[kEwVec] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int e = 0; e < kEwVec; ++e) {
-#pragma unroll
-    for (int t = 0; t < kEwMaxInputs; ++t)
-      if (t < A.n_inputs) r[t] = e == 0 ? v[0][t] : e == 1 ? v[1][t] : e == 2 ? v[2][t] : v[3][t];
-    ew_run(A, r);
-    const float res = r[A.out_reg];
-#pragma unroll
-    for (int k = 0; k < kEwVec; ++k) o[k] = e == k ? res : o[k];
-  }
+  for (int e = 0; e < kEwVec; ++e) o[e] = r[e][A.out_reg & (NR - 1)];
   if (A.out_vec && A.out_type == MK_F32) {
     *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + i0) = f32x4{{o[0], o[1], o[2], o[3]}};
   } else if (A.out_vec) {  // bf16
@@ -482,6 +509,8 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
     a.in_mode[t] = is_scalar ? 0 : (is_dense ? 1 : 2);
     need_index |= (a.in_mode[t] == 2);
   }
+  // highest register the program names (inputs occupy 0 .. n_inputs - 1)
+  int max_reg = max(out_reg, n_inputs - 1);
   for (int p = 0; p < n_instr; ++p) {
     const int32_t* ins = program + 4 * p;
     if (ins[0] < 0 || ins[0] >= MK_EW_NUM_OPS) return fail(MK_ERR_INVALID, "mk_ew_program: bad opcode");
@@ -492,7 +521,9 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
       if (ins[2] < 0 || ins[2] >= kEwMaxRegs || (ins[3] & 0xffff) >= kEwMaxRegs ||
           ((ins[3] >> 16) & 0xffff) >= kEwMaxRegs)
         return fail(MK_ERR_INVALID, "mk_ew_program: bad source register");
+      max_reg = max(max_reg, max(ins[2], max(ins[3] & 0xffff, (ins[3] >> 16) & 0xffff)));
     }
+    max_reg = max(max_reg, ins[1]);
     for (int k = 0; k < 4; ++k) a.prog[p][k] = ins[k];
   }
   for (int c = 0; c < n_consts; ++c) a.consts[c] = consts[c];
@@ -530,8 +561,13 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
     }
     a.out_vec = vec_ok(out, out_type, dense);
   }
-  if (narrow && dims[rank - 1] % kEwVec == 0)
-    hipLaunchKernelGGL(ew_program_vec_kernel, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
+  // the vector kernel with 16 registers per lane when the program fits (64
+  // VGPRs of registers instead of 128: more waves per SIMD)
+  if (narrow && dims[rank - 1] % kEwVec == 0 && max_reg < 16)
+    hipLaunchKernelGGL(ew_program_vec_kernel<16>, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
+                       as_stream(stream), a, uint32_t(n), out);
+  else if (narrow && dims[rank - 1] % kEwVec == 0)
+    hipLaunchKernelGGL(ew_program_vec_kernel<kEwMaxRegs>, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
                        as_stream(stream), a, uint32_t(n), out);
   else if (narrow)
     hipLaunchKernelGGL(ew_program_kernel<int32_t>, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,

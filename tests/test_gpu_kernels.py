@@ -638,6 +638,48 @@ def test_ew_program_ragged_rows(K):
         assert torch.all(guard[n:] == 7.0).item()
 
 
+def test_ew_program_vec_kernel_matches_one_element_kernel(K):
+    """The 4-lane interpreter (innermost dim a multiple of 4) and the
+    one-element interpreter (innermost dim 3) run the same program on the
+    same elements: the outputs must agree bit for bit.  The programs touch
+    the transcendental, division, compare/select/clamp, integer and rounding
+    opcodes, with values that include 0, negatives, NaN and infinities; the
+    first names registers up to 20 (the 32-register form of the 4-lane
+    kernel), the second stays below 16 (the 16-register form)."""
+    E = K.EW
+    rng = np.random.default_rng(16)
+    n = 4 * 3 * 1000
+    x = rng.standard_normal(n).astype(np.float32) * 3
+    y = rng.standard_normal(n).astype(np.float32)
+    x[:8] = [0.0, -0.0, np.nan, np.inf, -np.inf, 1e-40, -1e30, 88.5]
+    y[:8] = [0.0, 2.0, 1.0, -np.inf, np.nan, -1e-40, 0.5, -3.0]
+    i = rng.integers(-1000, 1000, n).astype(np.int32)
+    prog = [
+        (E["EXP"], 3, 0, 0), (E["LOG"], 4, 3, 0), (E["TANH"], 5, 1, 0), (E["DIV"], 6, 0, 1),
+        (E["POW"], 7, 3, 1), (E["ERF"], 8, 0, 0), (E["LOGISTIC"], 9, 1, 0), (E["RSQRT"], 10, 3, 0),
+        (E["CMP_GT"], 11, 0, 1), (E["SELECT"], 12, 11, 5 | (6 << 16)), (E["CLAMP"], 13, 8, 9 | (5 << 16)),
+        (E["ROUND_BF16"], 14, 7, 0), (E["ADD"], 15, 12, 13), (E["MUL"], 15, 15, 14), (E["SUB"], 15, 15, 10),
+        (E["MAX"], 15, 15, 4), (E["MUL_S32"], 16, 2, 2), (E["ADD_S32"], 16, 16, 2), (E["S32_TO_F32"], 17, 16, 0),
+        (E["FLOOR"], 18, 6, 0), (E["SIGN"], 19, 1, 0), (E["CONST"], 20, 0, 0), (E["MUL"], 18, 18, 20),
+        (E["ADD"], 15, 15, 17), (E["ADD"], 15, 15, 18), (E["ADD"], 15, 15, 19),
+    ]
+    prog16 = [
+        (E["EXP"], 3, 0, 0), (E["LOG"], 4, 3, 0), (E["TANH"], 5, 1, 0), (E["DIV"], 6, 0, 1),
+        (E["POW"], 7, 3, 1), (E["ERF"], 8, 0, 0), (E["CMP_GT"], 9, 0, 1), (E["SELECT"], 10, 9, 5 | (6 << 16)),
+        (E["CLAMP"], 11, 8, 7 | (5 << 16)), (E["ADD"], 12, 10, 11), (E["MUL_S32"], 13, 2, 2),
+        (E["S32_TO_F32"], 14, 13, 0), (E["ADD"], 15, 12, 14), (E["MAX"], 15, 15, 4),
+    ]
+    xs, ys, is_ = (torch.from_numpy(a).cuda() for a in (x, y, i))
+    for name, pr, cst in (("32-register", prog, [1e-3]), ("16-register", prog16, [])):
+        outs = []
+        for shape in ((n // 12, 12), (n // 3, 3)):
+            print(f"case: ew vec vs one-element, {name} program, shape {shape}", flush=True)
+            ins = [t.reshape(shape) for t in (xs, ys, is_)]
+            outs.append(K.ew_program(shape, ins, pr, cst, 15, torch.float32).reshape(-1).cpu().numpy())
+        np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+        assert np.isfinite(outs[0]).sum() > n // 2
+
+
 def test_ew_program_fused_chain(K):
     """relu(x * w + b) with a broadcast row vector, plus a select/compare chain."""
     E = K.EW
