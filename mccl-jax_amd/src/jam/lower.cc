@@ -2246,6 +2246,59 @@ class Lowerer {
     SetDenseView(v, dst);
     return state_[v].view;
   }
+  // Strides of a reshape of a strided view, when one exists: the dims of
+  // both shapes are cut into the shortest runs with equal products (unit
+  // dims aside); each input run must be one linear sequence of addresses
+  // (every stride the next one times its size), and the output run then
+  // walks the same sequence.  A run that is not linear (a transpose's
+  // dims merged) has no strided form: false.
+  static bool ReshapeStrides(const std::vector<int64_t>& id, const std::vector<int64_t>& is,
+                             const std::vector<int64_t>& od, std::vector<int64_t>& os) {
+    for (int64_t d : id)
+      if (d == 0) return false;
+    os.assign(od.size(), 0);
+    size_t i = 0, j = 0;
+    const size_t ni = id.size(), nj = od.size();
+    while (true) {
+      while (i < ni && id[i] == 1) ++i;
+      while (j < nj && od[j] == 1) ++j;
+      if (i >= ni || j >= nj) break;
+      int64_t pi = id[i], pj = od[j];
+      size_t i2 = i + 1, j2 = j + 1;
+      while (pi != pj) {
+        if (pi < pj) {
+          if (i2 >= ni) return false;
+          pi *= id[i2++];
+        } else {
+          if (j2 >= nj) return false;
+          pj *= od[j2++];
+        }
+      }
+      int64_t inner = 0, expect = -1;
+      for (size_t k = i2; k-- > i;) {
+        if (id[k] == 1) continue;
+        if (expect < 0) inner = is[k];
+        else if (is[k] != expect) return false;
+        expect = is[k] * id[k];
+      }
+      int64_t st = inner;
+      for (size_t k = j2; k-- > j;) {
+        os[k] = st;
+        st *= od[k];
+      }
+      i = i2;
+      j = j2;
+    }
+    for (; i < ni; ++i)
+      if (id[i] != 1) return false;
+    for (; j < nj; ++j)
+      if (od[j] != 1) return false;
+    // unit dims: the stride a row-major layout would give them (never used
+    // for addressing; keeps innermost-stride checks meaningful)
+    for (size_t k = nj; k-- > 0;)
+      if (od[k] == 1) os[k] = k + 1 < nj ? os[k + 1] * od[k + 1] : 1;
+    return true;
+  }
   // a dense copy of a view (for consumers that need row-major memory)
   View Densify(const View& src, int64_t elem_bytes_hint = 0) {
     if (src.dense()) return src;
@@ -2670,10 +2723,15 @@ class Lowerer {
         return;
       }
       View sv = NeedView(src);
-      if (!sv.dense()) sv = Densify(sv);
       View v = sv;
       v.dims = m_.types[res()].dims;
-      v.strides = DenseStrides(v.dims);
+      if (!ReshapeStrides(sv.dims, sv.strides, v.dims, v.strides)) {
+        // no strided form: copy to row-major first
+        if (!sv.dense()) sv = Densify(sv);
+        v = sv;
+        v.dims = m_.types[res()].dims;
+        v.strides = DenseStrides(v.dims);
+      }
       SetView(res(), v);
       return;
     }
