@@ -57,6 +57,7 @@ const char* StepName(StepKind k) {
     case StepKind::kSdpaBwd: return "sdpa_bwd";
     case StepKind::kGemmBlas: return "gemm_blas";
     case StepKind::kSoftmaxXent: return "softmax_xent";
+    case StepKind::kColSum: return "col_sum";
   }
   return "?";
 }
@@ -412,6 +413,7 @@ class Lowerer {
       case StepKind::kSdpaBwd: return {6, 7, 8, 9};
       case StepKind::kGemmBlas: return {2};
       case StepKind::kSoftmaxXent: return {2, 3};
+      case StepKind::kColSum: return {1, 2};
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
@@ -2861,6 +2863,24 @@ class Lowerer {
       pv.dims[k] = xv.dims[d];
       pv.strides[k++] = xv.strides[d];
       cols *= xv.dims[d];
+    }
+    // a sum over the leading dims of a row-major array into f32 (bias
+    // gradients): mk_col_sum reads the rows in place instead of a transposed
+    // copy plus a row reduce
+    bool lead = xv.dense() && rop == 0 && init == 0 && ot == DType::kF32 &&
+                (xt == DType::kF32 || xt == DType::kBF16) && rows > 0 && cols > 0 && !red.empty() && !keep.empty();
+    for (size_t r = 0; lead && r < red.size(); ++r) lead = red[r] == int(r);
+    if (lead) {
+      BufRef d = DestFor(op.results[0]);
+      BufRef ws = NewTemp(mk_col_sum_workspace_bytes(cols, rows));
+      Step st;
+      st.kind = StepKind::kColSum;
+      st.bufs = {xv.at(), d, ws};
+      st.i = {int64_t(xt), cols, rows};
+      st.note = body;
+      Emit(st);
+      SetDenseView(op.results[0], d);
+      return;
     }
     pv = Densify(pv);
     BufRef d = DestFor(op.results[0]);

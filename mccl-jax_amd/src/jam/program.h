@@ -29,7 +29,7 @@ struct BufRef {
 
 enum class StepKind : uint8_t {
   kGemm, kSdpa, kRowReduce, kArgmax, kLayerNorm, kGelu, kEw, kGather, kScatterAdd,
-  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas, kSoftmaxXent,
+  kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas, kSoftmaxXent, kColSum,
 };
 
 const char* StepName(StepKind k);

@@ -95,6 +95,8 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
                          P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], P(4), i[17], i[18], i[19],
                          static_cast<const float*>(P(5)), P(6), i[20], i[21], i[22], P(7), i[23], i[24], i[25],
                          P(8), i[26], i[27], i[28], s.f[0], int(i[29]), P(9));
+    case StepKind::kColSum:  // y[c] = sum_r x[r, c]: i = {dtype, rows, cols}
+      return mk_col_sum(st, int(i[0]), i[1], i[2], P(0), static_cast<float*>(P(1)), P(2));
     case StepKind::kRowReduce:
       return mk_row_reduce(st, int(i[0]), int(i[1]), int(i[2]), i[3], i[4], P(0), s.f[0], P(1));
     case StepKind::kArgmax:

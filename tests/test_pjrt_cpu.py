@@ -120,6 +120,8 @@ def test_compile_jitted_training_step(client):
     # the mean softmax cross-entropy and its gradient: one fused launch
     assert "pattern softmax_xent(256x257, grad_scale=0.003906)" in plan and plan.count("] softmax_xent") == 1
     assert "copy_strided" in plan
+    # bias gradients: sums over the leading (token) dims read in place
+    assert "] col_sum" in plan
 
 
 def test_compile_layernorm(client):
