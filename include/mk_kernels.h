@@ -387,8 +387,10 @@ int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, cons
  * (grad_scale = 1/rows gives the gradient of the mean loss, as
  * optax.softmax_cross_entropy_with_integer_labels(...).mean() under jax.grad).
  * io_type ∈ {MK_BF16, MK_F32} for logits / dlogits (dlogits may alias logits);
- * label_type ∈ {MK_S32, MK_S64}; a label outside [0, cols) gives loss NaN
- * and no target term.  loss_rows (fp32 [rows]) may be NULL. */
+ * label_type ∈ {MK_S32, MK_S64}.  A label outside [0, cols) has no target
+ * term: loss_rows[r] = lse_r and dlogits = softmax * grad_scale, which is what
+ * the one-hot form sum(select(iota == label, x, 0)) computes for it.
+ * loss_rows (fp32 [rows]) may be NULL. */
 int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,
                     int label_type, const void* labels, float grad_scale, float* loss_rows,
                     void* dlogits);

@@ -98,6 +98,30 @@ size_t DeviceContext::SizeClass(size_t bytes) {
   return (bytes + step - 1) / step * step;
 }
 
+hipEvent_t DeviceContext::TakeEventLocked() {
+  if (!idle_events_.empty()) {
+    hipEvent_t ev = idle_events_.back();
+    idle_events_.pop_back();
+    return ev;
+  }
+  hipEvent_t ev = nullptr;
+  if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return ev;
+}
+
+void DeviceContext::DropEventLocked(hipEvent_t ev) {
+  if (!ev) return;
+  // an event no stream can still be waiting on is recycled; a pending one is
+  // destroyed (HIP releases it once the recorded work has passed)
+  if (hipEventQuery(ev) == hipSuccess && idle_events_.size() < 256)
+    idle_events_.push_back(ev);
+  else
+    (void)hipEventDestroy(ev);
+}
+
 void* DeviceContext::Alloc(size_t bytes, std::string* error) {
   if (bytes == 0) return nullptr;
   const size_t cls = SizeClass(bytes);
@@ -105,13 +129,17 @@ void* DeviceContext::Alloc(size_t bytes, std::string* error) {
     std::lock_guard<std::mutex> lk(mu_);
     auto it = free_.find(cls);
     if (it != free_.end()) {
-      void* p = it->second;
+      Slot slot = it->second;
       free_.erase(it);
-      live_[p] = cls;
+      if (slot.reuse_after && hipEventQuery(slot.reuse_after) == hipSuccess) {
+        DropEventLocked(slot.reuse_after);
+        slot.reuse_after = nullptr;
+      }
+      live_[slot.p] = Live{cls, slot.reuse_after};
       stats_.bytes_in_use += int64_t(cls);
       stats_.peak_bytes_in_use = std::max(stats_.peak_bytes_in_use, stats_.bytes_in_use);
       ++stats_.num_allocs;
-      return p;
+      return slot.p;
     }
   }
   (void)UseDevice(ordinal_, nullptr);
@@ -128,7 +156,7 @@ void* DeviceContext::Alloc(size_t bytes, std::string* error) {
     }
   }
   std::lock_guard<std::mutex> lk(mu_);
-  live_[p] = cls;
+  live_[p] = Live{cls, nullptr};
   stats_.bytes_in_use += int64_t(cls);
   stats_.bytes_reserved += int64_t(cls);
   stats_.peak_bytes_in_use = std::max(stats_.peak_bytes_in_use, stats_.bytes_in_use);
@@ -139,20 +167,56 @@ void* DeviceContext::Alloc(size_t bytes, std::string* error) {
 
 void DeviceContext::Free(void* p) {
   if (!p) return;
+  (void)UseDevice(ordinal_, nullptr);
   std::lock_guard<std::mutex> lk(mu_);
   auto it = live_.find(p);
   if (it == live_.end()) return;  // not ours: ignore
-  stats_.bytes_in_use -= int64_t(it->second);
-  free_.emplace(it->second, p);
+  // every use of the block so far is queued on the compute stream (uploads
+  // into it were ordered before their readers): mark the point after them
+  hipEvent_t ev = TakeEventLocked();
+  if (ev && hipEventRecord(ev, stream_) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipEventDestroy(ev);
+    ev = nullptr;
+  }
+  if (!ev) {  // no event: wait here rather than risk a transfer-stream race
+    (void)hipStreamSynchronize(stream_);
+  }
+  DropEventLocked(it->second.reuse_after);
+  stats_.bytes_in_use -= int64_t(it->second.cls);
+  free_.emplace(it->second.cls, Slot{p, ev});
   live_.erase(it);
+}
+
+bool DeviceContext::OrderUploadInto(void* dst, std::string* error) {
+  std::lock_guard<std::mutex> lk(mu_);
+  auto it = live_.upper_bound(dst);
+  if (it == live_.begin()) return true;  // not a pool block: nothing to order
+  --it;
+  if (static_cast<char*>(dst) >= static_cast<char*>(it->first) + it->second.cls) return true;
+  hipEvent_t ev = it->second.reuse_after;
+  if (!ev) return true;
+  if (hipEventQuery(ev) == hipSuccess) {
+    DropEventLocked(ev);
+    it->second.reuse_after = nullptr;
+    return true;
+  }
+  hipError_t e = hipStreamWaitEvent(upload_, ev, 0);
+  if (e != hipSuccess) {
+    if (error) *error = HipMsg("hipStreamWaitEvent", e);
+    return false;
+  }
+  return true;
 }
 
 void DeviceContext::Trim() {
   std::vector<void*> release;
+  std::vector<hipEvent_t> events;
   {
     std::lock_guard<std::mutex> lk(mu_);
     for (auto& kv : free_) {
-      release.push_back(kv.second);
+      release.push_back(kv.second.p);
+      if (kv.second.reuse_after) events.push_back(kv.second.reuse_after);
       stats_.bytes_reserved -= int64_t(kv.first);
     }
     free_.clear();
@@ -161,6 +225,7 @@ void DeviceContext::Trim() {
   (void)UseDevice(ordinal_, nullptr);
   (void)hipStreamSynchronize(upload_);
   (void)hipStreamSynchronize(stream_);
+  for (hipEvent_t ev : events) (void)hipEventDestroy(ev);
   for (void* p : release) (void)hipFree(p);
 }
 
@@ -243,6 +308,7 @@ void DeviceContext::ReturnPinned(void* p, hipEvent_t busy_until) {
 hipEvent_t DeviceContext::Upload(void* dst, const void* src, size_t bytes, std::string* error) {
   if (!UseDevice(ordinal_, error)) return nullptr;
   std::lock_guard<std::mutex> lk(upload_mu_);
+  if (!OrderUploadInto(dst, error)) return nullptr;
   for (size_t off = 0; off < bytes;) {
     const size_t n = std::min(kStagePiece, bytes - off);
     void* chunk = TakePinned(n, error);

@@ -7,7 +7,10 @@
 //  - memory is device HBM (hipMalloc), not CPU-visible unified memory;
 //  - kernels, device-to-device and device-to-host copies go to the compute
 //    stream, so a block returned to the pool can be handed out again at once:
-//    any later use is ordered after the earlier use on that stream;
+//    any later compute-stream use is ordered after the earlier use.  Free
+//    records an event on the compute stream; a DMA on the transfer stream
+//    into a reused block first waits for that event (OrderUploadInto), so an
+//    upload never overwrites memory a queued kernel still reads;
 //  - host-to-device uploads go to a second (transfer) stream, so they never
 //    wait for kernels already queued.  Data is first copied into pinned
 //    staging chunks on the calling thread, then DMA'd; the caller gets the
@@ -72,6 +75,11 @@ class DeviceContext {
   MemoryStats Stats();
   void Trim();  // release every cached block back to HIP
 
+  // Makes the transfer stream wait until the compute-stream work queued
+  // before the last Free of the block holding `dst` has passed (no-op for a
+  // fresh block or one whose freeing work is already done).
+  bool OrderUploadInto(void* dst, std::string* error);
+
   // Host -> HBM without waiting for the compute stream (see file comment).
   // Returns an event recorded on the transfer stream after the last byte
   // landed (the caller destroys it), or nullptr and *error.  The host source
@@ -100,8 +108,21 @@ class DeviceContext {
   hipStream_t upload_ = nullptr;
   GpuProps props_;
   std::mutex mu_;
-  std::multimap<size_t, void*> free_;   // size class -> cached block
-  std::map<void*, size_t> live_;        // block -> size class
+  // A block's `reuse_after` is an event recorded on the compute stream when
+  // it was last freed (nullptr once that work is known done).
+  struct Slot {
+    void* p;
+    hipEvent_t reuse_after;
+  };
+  struct Live {
+    size_t cls;
+    hipEvent_t reuse_after;
+  };
+  hipEvent_t TakeEventLocked();
+  void DropEventLocked(hipEvent_t ev);  // ev may still be pending
+  std::multimap<size_t, Slot> free_;    // size class -> cached block
+  std::map<void*, Live> live_;          // block -> size class, reuse event
+  std::vector<hipEvent_t> idle_events_;
   MemoryStats stats_;
 
   // pinned staging

@@ -1541,17 +1541,40 @@ class Lowerer {
       if (ops_[u].name == "stablehlo.reduce" && is_reduce_over_last(ops_[u].results[0], "stablehlo.add", 4)) tsum = u;
     if (tsum < 0) return;
     bw.insert(tsum);
+    // the row sums [B,H,Sq] must come back along the keys: follow where each
+    // of their three axes lands through the broadcasts, and reshapes that
+    // only add or drop trailing unit dims, and require it to be {0,1,2}
     int tb = ops_[tsum].results[0];
+    std::vector<int64_t> at = {0, 1, 2};
     while (true) {
       const auto us = live_users(tb);
       if (us.size() != 1) return;
       const Op& o = ops_[us[0]];
-      if (o.name != "stablehlo.broadcast_in_dim" && o.name != "stablehlo.reshape") break;
+      if (o.name == "stablehlo.broadcast_in_dim") {
+        const auto bd = attr_ints(o, {"dims", "broadcast_dimensions"});
+        if (bd.size() != size_t(m_.types[tb].rank())) return;
+        for (auto& a : at) a = bd[size_t(a)];
+      } else if (o.name == "stablehlo.reshape") {
+        const auto& from = m_.types[tb].dims;
+        const auto& to = m_.types[o.results[0]].dims;
+        const size_t common = std::min(from.size(), to.size());
+        if (common < 3) return;
+        for (size_t i = 0; i < common; ++i)
+          if (from[i] != to[i]) return;
+        for (size_t i = common; i < from.size(); ++i)
+          if (from[i] != 1) return;
+        for (size_t i = common; i < to.size(); ++i)
+          if (to[i] != 1) return;
+        for (auto a : at)
+          if (size_t(a) >= common) return;
+      } else {
+        break;
+      }
       bw.insert(us[0]);
       tb = o.results[0];
       if (dims_are(tb, {B, H, Sq, Sk})) break;
     }
-    if (!dims_are(tb, {B, H, Sq, Sk})) return;
+    if (!dims_are(tb, {B, H, Sq, Sk}) || at != std::vector<int64_t>{0, 1, 2}) return;
     const int pm = find_user(tb, "stablehlo.multiply", [&](const Op& o) { return other(o, tb) == r.pr; });
     if (pm < 0) return;
     bw.insert(pm);
@@ -1677,8 +1700,8 @@ class Lowerer {
   //   dX = select(onehot, bcast(-g), 0) + bcast(g / Z) * E
   // with g = bcast(c) the per-row cotangent of a constant c (1/T for the
   // mean).  Anchored at the loss_rows subtract: one mk_softmax_xent launch
-  // writes loss_rows and dX (which no other op computes then).  Labels
-  // outside [0, V) give NaN there (the module would drop the target term).
+  // writes loss_rows and dX (which no other op computes then).  A label
+  // outside [0, V) drops the target term there, as the module's select does.
   void TryMatchXent(int anchor) {
     const Op& dsub = ops_[anchor];
     const int LSE = dsub.operands[0], PK = dsub.operands[1];
@@ -2866,9 +2889,13 @@ class Lowerer {
     }
     // a sum over the leading dims of a row-major array into f32 (bias
     // gradients): mk_col_sum reads the rows in place instead of a transposed
-    // copy plus a row reduce
+    // copy plus a row reduce.  Its grid has one y-block per 256 kept columns
+    // at the finest (f32 vectors), at most 65535 of them; wider sums take the
+    // row-reduce path.
+    constexpr int64_t kColSumMaxKept = int64_t(65535) * 256;
     bool lead = xv.dense() && rop == 0 && init == 0 && ot == DType::kF32 &&
-                (xt == DType::kF32 || xt == DType::kBF16) && rows > 0 && cols > 0 && !red.empty() && !keep.empty();
+                (xt == DType::kF32 || xt == DType::kBF16) && rows > 0 && rows <= kColSumMaxKept && cols > 0 &&
+                !red.empty() && !keep.empty();
     for (size_t r = 0; lead && r < red.size(); ++r) lead = red[r] == int(r);
     if (lead) {
       BufRef d = DestFor(op.results[0]);

@@ -600,7 +600,7 @@ __global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restric
   const float lse = M + __logf(S);
   const int64_t lab = int64_t(labels[row]);
   const bool lab_ok = lab >= 0 && lab < cols;
-  if (threadIdx.x == 0 && loss) loss[row] = lab_ok ? lse - ldf<T>(xr, lab) : __builtin_nanf("");
+  if (threadIdx.x == 0 && loss) loss[row] = lab_ok ? lse - ldf<T>(xr, lab) : lse;
   T* dr = dlogits + row * cols;
   for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
     const float p = __expf(ldf<T>(xr, j) - lse);
@@ -678,7 +678,7 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   const float S = block_reduce(sum, false);
   const float lse = M + __logf(S);
   const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
-  if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xlab_bits) : __builtin_nanf("");
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xlab_bits) : lse;
   // gradient, from the registers (every read of the row is done: in place is safe)
   u32x4_t* dv = reinterpret_cast<u32x4_t*>(dr + head);
 #pragma unroll

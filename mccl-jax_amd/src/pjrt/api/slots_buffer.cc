@@ -142,7 +142,7 @@ PJRT_Error* CopyInto(PJRT_Buffer* src, PJRT_Memory* mem, PJRT_Buffer** out, cons
     // source block is held until the DMA is done
     if (src->defined) err = src->defined->Wait();
     exec::DeviceContext* ctx = dst->ctx;
-    if (err.empty() && exec::UseDevice(ctx->ordinal(), &err)) {
+    if (err.empty() && exec::UseDevice(ctx->ordinal(), &err) && ctx->OrderUploadInto(dst->ptr, &err)) {
       hipError_t r = hipMemcpyAsync(dst->ptr, from->ptr, src->bytes, hipMemcpyHostToDevice, ctx->transfer_stream());
       if (r != hipSuccess) err = std::string("hipMemcpyAsync: ") + hipGetErrorString(r);
       else defined = RecordOn(ctx, ctx->transfer_stream(), Lane::kTransfer, [from] { return std::string(); }, &err);

@@ -194,8 +194,9 @@ def softmax_xent(logits, labels, grad_scale):
     loss rows and d(mean loss)/d logits of the jitted step's
     optax-style loss (temp/dp_train.py:67-70 value_and_grad of a mean loss),
     loss_r = logsumexp(x_r) - x_r[label_r], dlogits = (softmax(x_r) -
-    onehot(label_r)) * grad_scale.  An out-of-range label gives a NaN loss
-    and no one-hot term."""
+    onehot(label_r)) * grad_scale.  An out-of-range label has no target term
+    (loss = logsumexp, gradient = softmax * grad_scale), as the one-hot form
+    sum(select(iota == label, x, 0)) of the jitted module gives."""
     x = np.asarray(logits, dtype=np.float64)
     lab = np.asarray(labels).astype(np.int64).reshape(-1)
     m = np.max(x, axis=-1, keepdims=True)
@@ -203,7 +204,7 @@ def softmax_xent(logits, labels, grad_scale):
     s = e.sum(axis=-1, keepdims=True)
     lse = (m + np.log(s))[:, 0]
     ok = (lab >= 0) & (lab < x.shape[-1])
-    picked = np.where(ok, x[np.arange(x.shape[0]), np.clip(lab, 0, x.shape[-1] - 1)], np.nan)
+    picked = np.where(ok, x[np.arange(x.shape[0]), np.clip(lab, 0, x.shape[-1] - 1)], 0.0)
     grad = e / s
     grad[np.arange(x.shape[0])[ok], lab[ok]] -= 1.0
     return lse - picked, grad * grad_scale

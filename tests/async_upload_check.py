@@ -7,7 +7,10 @@ stream, and then a copy queued behind kernels waits for them).
 
 Queues about 26 ms of attention, uploads a small buffer, and checks that its
 ready event completes while the attention is still running and that a
-program queued after the upload reads its bytes.  Prints one line per trial;
+program queued after the upload reads its bytes.  Then the reuse case: with
+attention reading buffer A queued, A is destroyed and a buffer B of the same
+size is uploaded (the pool hands B A's block); every queued attention must
+still see A's bytes and B must hold its own.  Prints one line per trial;
 exits non-zero on failure."""
 
 import os
@@ -59,6 +62,38 @@ def main():
             return 1
         for b in outs + [xb, y]:
             b.destroy()
+    return check_reuse(p, client, e, bufs, d)
+
+
+def check_reuse(p, client, e, bufs, d):
+    (want,) = e.execute(bufs)
+    want_np = want.to_numpy()
+    want.destroy()
+    other = bf16.to_bf16_bits(-bf16.from_bf16_bits(d["q"]))  # same size, different bytes
+    for trial in range(2):
+        a = client.put(d["q"], pjrt.BF16)
+        a.ready()
+        outs, ev = [], None
+        for _ in range(24):
+            if ev is not None:
+                p.call("Event_Destroy", event=ev)
+            o, ev = e.execute([a, bufs[1], bufs[2]], wait="event")
+            outs += o
+        where = a.device_pointer()
+        a.destroy()
+        b = client.put(other, pjrt.BF16)
+        reused = b.device_pointer() == where
+        busy = not p.event_ready(ev)
+        p.await_event(ev)
+        bad = [i for i, o in enumerate(outs) if not np.array_equal(o.to_numpy(), want_np)]
+        b_ok = np.array_equal(b.to_numpy(), other)
+        print(f"reuse trial {trial}: block reused {reused}, attention still running at upload {busy}, "
+              f"outputs changed {len(bad)}/{len(outs)}, B intact {b_ok}", flush=True)
+        if bad or not b_ok:
+            print("FAIL: an upload into a reused block raced the kernels reading it", flush=True)
+            return 1
+        for x in outs + [b]:
+            x.destroy()
     return 0
 
 

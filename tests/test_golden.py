@@ -65,7 +65,8 @@ def test_golden_oracle_gpt2_step():
 
 def test_softmax_xent_oracle_pins():
     """ops.softmax_xent: uniform logits give ln(V) and 1/V - onehot; rows of
-    the gradient sum to 0 (in-range labels); torch float64 cross_entropy."""
+    the gradient sum to 0 (in-range labels); torch float64 cross_entropy;
+    out-of-range labels against logsumexp and softmax."""
     loss, dl = ops.softmax_xent(np.zeros((3, 7)), np.array([0, 3, 6]), 1.0)
     np.testing.assert_allclose(loss, np.log(7), rtol=0, atol=1e-15)
     want = np.full((3, 7), 1 / 7)
@@ -81,8 +82,13 @@ def test_softmax_xent_oracle_pins():
     ref.mean().backward()
     np.testing.assert_allclose(loss, ref.detach().numpy(), rtol=1e-13)
     np.testing.assert_allclose(dl, xt.grad.numpy(), rtol=1e-12, atol=1e-15)
-    loss, _ = ops.softmax_xent(x[:1], np.array([40]), 1.0)
-    assert math.isnan(loss[0])
+    # an out-of-range label (above or below) has no target term: loss is the
+    # row's logsumexp and the gradient is the softmax
+    for bad in (40, -1):
+        loss, dl = ops.softmax_xent(x[:1], np.array([bad]), 1.0)
+        m = x[0].max()
+        np.testing.assert_allclose(loss[0], m + np.log(np.exp(x[0] - m).sum()), rtol=1e-14)
+        np.testing.assert_allclose(dl[0], torch.softmax(torch.tensor(x[0]), -1).numpy(), rtol=1e-12, atol=1e-18)
 
 
 # ------------------------------------------------------------------ GPU: kernels against the fixtures
@@ -132,8 +138,7 @@ def test_golden_softmax_xent(K):
     g = load("softmax_xent")
     loss, dl = K.softmax_xent(dev_bf16(g["logits"]), torch.from_numpy(g["labels"]).cuda(), 1.0 / 8)
     loss = loss.cpu().numpy()
-    np.testing.assert_allclose(loss[:-1], g["loss"][:-1], rtol=1e-5, atol=1e-5)
-    assert math.isnan(loss[-1])
+    np.testing.assert_allclose(loss, g["loss"], rtol=1e-5, atol=1e-5)  # last row: label out of range
     np.testing.assert_allclose(dl.float().cpu().numpy(), g["dlogits"], rtol=2 ** -7, atol=1e-30)
 
 

@@ -170,6 +170,31 @@ def test_c4_gather_and_scatter_add(client):
     np.testing.assert_array_equal(t, native.scatter_add_f32(d["table_f32"], ids, d["grads"]))
 
 
+def test_reshape_of_strided_views(client):
+    """Reshapes of slices (kept as strided views), of transposes and of
+    broadcasts (copied), each feeding an add: x + x is exact, so the result
+    must equal numpy's bit for bit."""
+    from test_pjrt_cpu import RESHAPE_VIEWS
+
+    for case, (body, at, rt, _) in sorted(RESHAPE_VIEWS.items()):
+        print(f"case: reshape view {case}", flush=True)
+        text = f"func.func public @main(%arg0: {at}) -> {rt} {{\n{body}\n}}"
+        shape = tuple(int(d) for d in at[len("tensor<"):-len("xf32>")].split("x"))
+        x = np.arange(np.prod(shape), dtype=np.float32).reshape(shape) * 0.5 - 3
+        (got,) = run(client, text, (x, pjrt.F32))
+        if case == "slice_split":
+            want = x[:, 1:4].reshape(2, 2, 3)
+        elif case == "slice_unit_dim":
+            want = x[:, 0, 1:4]
+        elif case == "slice_merge":
+            want = x[:, 1:4].reshape(12)
+        elif case == "transpose_merge":
+            want = x.T.reshape(24)
+        else:
+            want = np.broadcast_to(x, (4, 6)).reshape(24)
+        np.testing.assert_array_equal(got, want + want)
+
+
 def test_constants_bf16_f16_rne(client):
     """Dense decimal constants are rounded once from the literal's double
     value to the element type, nearest-even, with subnormals and overflow to
@@ -320,8 +345,10 @@ def test_upload_does_not_wait_for_queued_kernels():
     """BufferFromHostBuffer with tens of milliseconds of kernels queued: the
     upload goes to the transfer stream, so its ready event completes while
     the queued work is still running, and a program reading the uploaded
-    buffer (queued after it) sees its bytes.  Run in a fresh process holding
-    only the plugin's streams (tests/async_upload_check.py says why)."""
+    buffer (queued after it) sees its bytes.  Then an upload into a block
+    freed while kernels still read it waits for them (the pool's reuse
+    event).  Run in a fresh process holding only the plugin's streams
+    (tests/async_upload_check.py says why)."""
     import subprocess
     import sys
 

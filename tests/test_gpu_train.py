@@ -353,25 +353,27 @@ def test_softmax_xent_bf16_in_place(K):
 def test_softmax_xent_bf16_shapes(K, rows, cols):
     """Register-resident rows (unaligned head / tail, every vector-count
     bucket) and the streaming kernel past 64K columns; -inf logits and an
-    out-of-range label (loss NaN, gradient without the one-hot term)."""
+    out-of-range label, above and below (loss = logsumexp, gradient without
+    the one-hot term)."""
     g = torch.Generator().manual_seed(rows + cols)
     x = (torch.randn(rows, cols, generator=g) * 3).bfloat16()
     if cols > 3:
         x[0, 1] = float("-inf")
         x[-1, -2] = float("-inf")
     lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int32)
-    lab[-1] = cols  # out of range
+    lab[-1] = cols  # out of range, above and below
+    if rows > 1:
+        lab[0] = -1
     loss, dl = K.softmax_xent(x.cuda(), lab.cuda(), 1.0 / rows)
     xr = x.double()
     lse = torch.logsumexp(xr, -1)
     p = torch.softmax(xr, -1)
     onehot = torch.zeros_like(p)
-    ok = lab < cols
+    ok = (lab >= 0) & (lab < cols)
     onehot[torch.arange(rows)[ok], lab[ok].long()] = 1.0
     want_grad = (p - onehot) / rows
-    want_loss = lse - xr[torch.arange(rows), lab.clamp(max=cols - 1).long()]
-    np.testing.assert_allclose(_f64(loss)[:-1], want_loss[:-1], rtol=1e-5, atol=1e-5)
-    assert math.isnan(float(loss[-1]))
+    want_loss = lse - torch.where(ok, xr[torch.arange(rows), lab.clamp(0, cols - 1).long()], 0.0)
+    np.testing.assert_allclose(_f64(loss), want_loss, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(_f64(dl), want_grad, rtol=2 ** -7, atol=1e-30)
 
 

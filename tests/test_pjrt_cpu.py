@@ -124,6 +124,83 @@ def test_compile_jitted_training_step(client):
     assert "] col_sum" in plan
 
 
+def test_sdpa_backward_needs_the_row_broadcast(client):
+    """The attention backward matcher follows the row sums sum(dP * P) back to
+    [B,H,Sq,Sk]: only a broadcast of the [B,H,Sq] axes onto dims {0,1,2}
+    (along the keys) is the softmax backward.  With Sq == Sk a broadcast onto
+    {0,1,3} type-checks but computes something else, so that layer must not
+    become the flash backward."""
+    from mi355x_pjrt import gpt2, train_hlo
+
+    cfg = gpt2.GPT2Config(n_layer=2, d_model=128, n_head=2, seq=128, batch=2, vocab=257)
+    text = train_hlo.gpt2_train_step(cfg)
+    sig = "dims = [0, 1, 2] : (tensor<2x2x128xf32>) -> tensor<2x2x128x128xf32>"
+    at = [i for i, ln in enumerate(text.split("\n")) if sig in ln]
+    assert len(at) == 6  # per layer: the forward's max and sum, the backward's row sum
+    lines = text.split("\n")
+    lines[at[-1]] = lines[at[-1]].replace("dims = [0, 1, 2]", "dims = [0, 1, 3]")
+    plan, _, _ = _plan(client, "\n".join(lines))
+    assert plan.count("] sdpa_bwd (causal)") == 1
+    plan, _, _ = _plan(client, text)
+    assert plan.count("] sdpa_bwd (causal)") == 2
+
+
+def _steps(client, body, arg_type, result_type):
+    text = (f"func.func public @main(%arg0: {arg_type}) -> {result_type} {{\n{body}\n}}")
+    plan, _, _ = _plan(client, text)
+    return [ln.split("] ", 1)[1].split(" ")[0] for ln in plan.splitlines() if "] " in ln]
+
+
+# reshape of a strided view: (module body, argument type, result type, steps)
+RESHAPE_VIEWS = {
+    # splitting the rows of a column slice keeps a view (no copy before the add)
+    "slice_split": ("""  %0 = stablehlo.slice %arg0 [0:4, 1:4] : (tensor<4x6xf32>) -> tensor<4x3xf32>
+  %1 = stablehlo.reshape %0 : (tensor<4x3xf32>) -> tensor<2x2x3xf32>
+  %2 = stablehlo.add %1, %1 : tensor<2x2x3xf32>
+  return %2 : tensor<2x2x3xf32>""", "tensor<4x6xf32>", "tensor<2x2x3xf32>", ["ew"]),
+    # a unit dim inside the merged run is linear too
+    "slice_unit_dim": ("""  %0 = stablehlo.slice %arg0 [0:4, 0:1, 1:4] : (tensor<4x1x6xf32>) -> tensor<4x1x3xf32>
+  %1 = stablehlo.reshape %0 : (tensor<4x1x3xf32>) -> tensor<4x3xf32>
+  %2 = stablehlo.add %1, %1 : tensor<4x3xf32>
+  return %2 : tensor<4x3xf32>""", "tensor<4x1x6xf32>", "tensor<4x3xf32>", ["ew"]),
+    # merging rows of a column slice is not linear in memory: copy
+    "slice_merge": ("""  %0 = stablehlo.slice %arg0 [0:4, 1:4] : (tensor<4x6xf32>) -> tensor<4x3xf32>
+  %1 = stablehlo.reshape %0 : (tensor<4x3xf32>) -> tensor<12xf32>
+  %2 = stablehlo.add %1, %1 : tensor<12xf32>
+  return %2 : tensor<12xf32>""", "tensor<4x6xf32>", "tensor<12xf32>", ["copy_strided", "ew"]),
+    "transpose_merge": ("""  %0 = stablehlo.transpose %arg0, dims = [1, 0] : (tensor<4x6xf32>) -> tensor<6x4xf32>
+  %1 = stablehlo.reshape %0 : (tensor<6x4xf32>) -> tensor<24xf32>
+  %2 = stablehlo.add %1, %1 : tensor<24xf32>
+  return %2 : tensor<24xf32>""", "tensor<4x6xf32>", "tensor<24xf32>", ["copy_strided", "ew"]),
+    "broadcast_merge": ("""  %0 = stablehlo.broadcast_in_dim %arg0, dims = [1] : (tensor<6xf32>) -> tensor<4x6xf32>
+  %1 = stablehlo.reshape %0 : (tensor<4x6xf32>) -> tensor<24xf32>
+  %2 = stablehlo.add %1, %1 : tensor<24xf32>
+  return %2 : tensor<24xf32>""", "tensor<6xf32>", "tensor<24xf32>", ["copy_strided", "ew"]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(RESHAPE_VIEWS))
+def test_reshape_of_strided_views(client, case):
+    body, at, rt, want = RESHAPE_VIEWS[case]
+    assert _steps(client, body, at, rt) == want
+
+
+def test_col_sum_respects_its_grid_limit(client):
+    """Sums over the leading dim lower to col_sum while the kept extent fits
+    its grid (65535 blocks of 256 columns); wider ones take the row-reduce
+    path (compile only: nothing is allocated)."""
+    def body(n):
+        return (f"  %c = stablehlo.constant dense<0.0> : tensor<f32>\n"
+                f"  %0 = stablehlo.reduce(%arg0 init: %c) applies stablehlo.add across dimensions = [0] : "
+                f"(tensor<2x{n}xf32>, tensor<f32>) -> tensor<{n}xf32>\n"
+                f"  return %0 : tensor<{n}xf32>")
+    ok = 65535 * 256
+    assert "col_sum" in _steps(client, body(ok), f"tensor<2x{ok}xf32>", f"tensor<{ok}xf32>")
+    wide = ok + 256
+    steps = _steps(client, body(wide), f"tensor<2x{wide}xf32>", f"tensor<{wide}xf32>")
+    assert "col_sum" not in steps and "row_reduce" in steps
+
+
 def test_compile_layernorm(client):
     plan, types, shapes = _plan(client, modules.layernorm(64, 256))
     assert types == [pjrt.BF16] and shapes == [(64, 256)]
