@@ -79,10 +79,10 @@ def check_reuse(p, client, e, bufs, d):
                 p.call("Event_Destroy", event=ev)
             o, ev = e.execute([a, bufs[1], bufs[2]], wait="event")
             outs += o
-        where = a.device_pointer()
+        where = a.device_pointer
         a.destroy()
         b = client.put(other, pjrt.BF16)
-        reused = b.device_pointer() == where
+        reused = b.device_pointer == where
         busy = not p.event_ready(ev)
         p.await_event(ev)
         bad = [i for i, o in enumerate(outs) if not np.array_equal(o.to_numpy(), want_np)]
