@@ -474,6 +474,78 @@ std::string Module::DialectVersionText(size_t d) const {
   return s + " " + nums;
 }
 
+bool Payload::Byte(uint8_t* v) {
+  if (p_ == end_) return false;
+  *v = *p_++;
+  return true;
+}
+
+bool Payload::VarInt(uint64_t* v) {
+  uint8_t first = 0;
+  if (!Byte(&first)) return false;
+  if (first & 1) {
+    *v = first >> 1;
+    return true;
+  }
+  if (first == 0) {
+    if (left() < 8) return false;
+    uint64_t x = 0;
+    for (int i = 7; i >= 0; --i) x = (x << 8) | p_[i];
+    p_ += 8;
+    *v = x;
+    return true;
+  }
+  const int n = __builtin_ctz(first) + 1;
+  if (left() < size_t(n - 1)) return false;
+  uint64_t x = first;
+  for (int i = 0; i < n - 1; ++i) x |= uint64_t(p_[i]) << (8 * (i + 1));
+  p_ += n - 1;
+  *v = x >> n;
+  return true;
+}
+
+bool Payload::SignedVarInt(int64_t* v) {
+  uint64_t u;
+  if (!VarInt(&u)) return false;
+  *v = int64_t((u >> 1) ^ (~(u & 1) + 1));
+  return true;
+}
+
+bool Payload::Blob(const uint8_t** data, size_t* size) {
+  uint64_t n;
+  if (!VarInt(&n) || n > left()) return false;
+  *data = p_;
+  *size = size_t(n);
+  p_ += n;
+  return true;
+}
+
+bool Payload::APInt(unsigned width, uint64_t* bits, bool* wide) {
+  if (wide) *wide = false;
+  if (width <= 8) {
+    uint8_t b;
+    if (!Byte(&b)) return false;
+    *bits = b;
+    return true;
+  }
+  if (width <= 64) {
+    int64_t x;
+    if (!SignedVarInt(&x)) return false;
+    *bits = uint64_t(x);
+    return true;
+  }
+  uint64_t words;
+  if (!VarInt(&words) || words > left()) return false;
+  *bits = 0;
+  for (uint64_t w = 0; w < words; ++w) {
+    int64_t x;
+    if (!SignedVarInt(&x)) return false;
+    if (w == 0) *bits = uint64_t(x);
+    else if (x != 0 && wide) *wide = true;
+  }
+  return true;
+}
+
 bool Read(const uint8_t* data, size_t size, Module* out, std::string* error) {
   error->clear();
   *out = Module();

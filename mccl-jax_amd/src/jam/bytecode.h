@@ -21,9 +21,8 @@
 // attribute-dictionary / type / value references and the regions, blocks and
 // block arguments, plus each attribute's and type's entry (dialect, bytes,
 // whether it is a dialect-specific binary encoding or the textual form).
-// Turning VHLO's binary attribute and type encodings into jam IR is the part
-// that is not implemented: there is no artifact in this environment to check
-// a decoder against.
+// Turning VHLO's binary attribute and type encodings into jam IR is done by
+// vhlo.cc on top of this tree.
 #pragma once
 
 #include <cstddef>
@@ -99,5 +98,28 @@ struct Module {
 // Parses a whole bytecode buffer.  On failure returns false and sets *error to
 // a message naming the offset and what was malformed.
 bool Read(const uint8_t* data, size_t size, Module* out, std::string* error);
+
+// Reader of one attribute or type payload in a dialect's binary encoding:
+// the primitives MLIR's DialectBytecodeReader offers (varints, zigzag signed
+// varints, blobs, APInts of a known width).  Every method returns false at
+// the end of the payload.
+class Payload {
+ public:
+  Payload(const uint8_t* p, size_t n) : p_(p), end_(p + n) {}
+  bool at_end() const { return p_ == end_; }
+  size_t left() const { return size_t(end_ - p_); }
+  bool Byte(uint8_t* v);
+  bool VarInt(uint64_t* v);
+  bool SignedVarInt(int64_t* v);  // zigzag: (u >> 1) ^ -(u & 1)
+  bool Blob(const uint8_t** data, size_t* size);  // varint length, then the bytes
+  // An APInt of `width` bits: one raw byte up to 8 bits, a signed varint up
+  // to 64 bits, else a word count and that many signed-varint words (only
+  // the low word is kept; *wide is set when higher words are non-zero).
+  bool APInt(unsigned width, uint64_t* bits, bool* wide = nullptr);
+
+ private:
+  const uint8_t* p_;
+  const uint8_t* end_;
+};
 
 }  // namespace mi::jam::bytecode

@@ -32,6 +32,7 @@
 
 #include "jam/ir.h"
 #include "jam/bytecode.h"
+#include "jam/vhlo.h"
 #include "jam/program.h"
 #include "mk_kernels.h"
 
@@ -3369,31 +3370,34 @@ class Lowerer {
 
 CompileResult Compile(const char* code, size_t size, const CompileOptions& opts) {
   CompileResult r;
+  std::unique_ptr<Module> m;
+  std::string err;
   if (IsMlirBytecode(code, size)) {
     // A StableHLO portable artifact (what jaxlib serializes): the container
-    // is read and its operations named; lowering them needs VHLO's binary
-    // attribute and type encodings decoded, which this build does not do.
+    // is read (bytecode.cc), its VHLO operations, types and attributes are
+    // decoded into jam IR (vhlo.cc), and the module is lowered like text.
     bytecode::Module bm;
     std::string berr;
     if (!bytecode::Read(reinterpret_cast<const uint8_t*>(code), size, &bm, &berr)) {
       r.error = "jam: MLIR bytecode: " + berr;
       return r;
     }
-    std::string dialects;
-    for (size_t d = 0; d < bm.dialects.size(); ++d)
-      dialects += (d ? ", " : "") + bm.DialectVersionText(d);
-    r.error = "jam: MLIR bytecode v" + std::to_string(bm.version) + " from '" + bm.producer + "' (dialects " +
-              dialects + "; " + std::to_string(bm.attrs.size()) + " attributes, " + std::to_string(bm.types.size()) +
-              " types): ops " + bm.OpHistogram() +
-              ". Lowering needs the VHLO attribute and type encodings decoded, which is not implemented; "
-              "pass the module as StableHLO text (PJRT_Program.format = \"mlir\")";
-    return r;
-  }
-  std::string err;
-  auto m = ParseText(code, size, err);
-  if (!m) {
-    r.error = err;
-    return r;
+    m = FromVhlo(bm, err);
+    if (!m) {
+      std::string dialects;
+      for (size_t d = 0; d < bm.dialects.size(); ++d)
+        dialects += (d ? ", " : "") + bm.DialectVersionText(d);
+      r.error = err + " (artifact: MLIR bytecode v" + std::to_string(bm.version) + " from '" + bm.producer +
+                "', dialects " + dialects + ", " + std::to_string(bm.attrs.size()) + " attributes, " +
+                std::to_string(bm.types.size()) + " types; ops " + bm.OpHistogram() + ")";
+      return r;
+    }
+  } else {
+    m = ParseText(code, size, err);
+    if (!m) {
+      r.error = err;
+      return r;
+    }
   }
   Lowerer L(*m, opts);
   r.program = L.Run(err);

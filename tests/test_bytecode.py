@@ -10,8 +10,10 @@ attribute-type-offset / IR / properties sections, isolated regions in nested
 IR sections from version 2, use-list orders from version 3, elided unknown
 block-argument locations and an op-name count from version 4, registered
 flags on op names and op properties from version 5).  The reader's output
-reaches the test through the named compile error, which lists the dialects
-(with versions), the producer and every operation of the tree.  CPU only."""
+reaches the test through the compiled plan (a hand-assembled VHLO artifact
+compiles to the plan of the same module as text) or through the named
+compile error, which lists the dialects (with versions), the producer and
+every operation of the tree.  CPU only."""
 
 import struct
 
@@ -186,24 +188,56 @@ class Stream:
         return out
 
 
-def artifact_v1():
-    """The shape of a StableHLO portable artifact of `lambda a, b: a + b`:
-    builtin.module { vhlo.func_v1 (isolated) { ^bb(%a, %b): vhlo.add_v1;
-    vhlo.return_v1 } }, VHLO's attributes and types in binary form."""
+def svarint(v):
+    """Signed varint: zigzag ((v << 1) ^ (v >> 63)), then a prefix varint."""
+    z = ((v << 1) ^ (v >> 63)) & ((1 << 64) - 1)
+    return varint(z, wide=z >= (1 << 56))
+
+
+# VHLO type codes (f32, tensor, function) and the builtin attribute codes the
+# artifacts below use (DictionaryAttr, StringAttr, UnknownLoc)
+TY_F32, TY_TENSOR, TY_FUNCTION = 4, 20, 8
+BI_DICT, BI_STRING, BI_UNKNOWN_LOC = 1, 2, 15
+AT_STRING, AT_TYPE, AT_CMP_DIR, AT_CMP_TYPE = 13, 17, 2, 3   # decoded by name, not by code
+
+
+def artifact_v1(f32_code=TY_F32, dim=4, module_level_extra=False):
+    """A StableHLO portable artifact of `lambda a, b: a + b` over f32[4],
+    assembled byte for byte: builtin.module { vhlo.func_v1 @main (isolated)
+    { ^bb(%a, %b): vhlo.add_v1; vhlo.return_v1 } }, with VHLO's binary types
+    (f32; tensor = {rank, zigzag dims, element}; function = {inputs,
+    results}) and attributes (a builtin DictionaryAttr of builtin StringAttr
+    names holding a string and a type attribute)."""
     st = Stream(1, "StableHLO_v1.0.0")
     builtin = st.dialect("builtin")
     vhlo = st.dialect("vhlo", [1, 0, 0])
     module = st.op_name(builtin, "module")
     func, add, ret = (st.op_name(vhlo, n) for n in ("func_v1", "add_v1", "return_v1"))
-    loc = st.attr(builtin, "loc(unknown)", False)
-    fattrs = st.attr(vhlo, b"\x05\x07\x09", True)
-    tensor = st.type(vhlo, b"\x03\x11\x21", True)
+    loc = st.attr(builtin, varint(BI_UNKNOWN_LOC), True)
+    k_ft = st.attr(builtin, varint(BI_STRING) + varint(st.s("function_type")), True)
+    k_name = st.attr(builtin, varint(BI_STRING) + varint(st.s("sym_name")), True)
+    f32 = st.type(vhlo, varint(f32_code), True)
+    tensor = st.type(vhlo, varint(TY_TENSOR) + varint(1) + svarint(dim) + varint(f32), True)
+    fty = st.type(vhlo, varint(TY_FUNCTION) + varint(2) + varint(tensor) * 2 + varint(1) + varint(tensor), True)
+    v_name = st.attr(vhlo, varint(AT_STRING) + varint(st.s("main")), True)
+    v_ft = st.attr(vhlo, varint(AT_TYPE) + varint(fty), True)
+    fattrs = st.attr(builtin, varint(BI_DICT) + varint(2) + varint(k_ft) + varint(v_ft) + varint(k_name) +
+                     varint(v_name), True)
     body = {"blocks": [{"args": [(tensor, loc), (tensor, loc)],
                         "ops": [{"name": add, "loc": loc, "results": [tensor], "operands": [0, 1]},
                                 {"name": ret, "loc": loc, "operands": [2]}]}], "num_values": 3}
     fn = {"name": func, "loc": loc, "attrs": fattrs, "regions": [body], "isolated": True}
-    top = {"name": module, "loc": loc, "regions": [{"blocks": [{"ops": [fn]}], "num_values": 0}], "isolated": True}
+    ops = [fn]
+    if module_level_extra:
+        ops.append({"name": ret, "loc": loc})
+    top = {"name": module, "loc": loc, "regions": [{"blocks": [{"ops": ops}], "num_values": 0}], "isolated": True}
     return st, top
+
+
+ADD_TEXT = """func.func public @main(%a: tensor<4xf32>, %b: tensor<4xf32>) -> tensor<4xf32> {
+  %0 = stablehlo.add %a, %b : tensor<4xf32>
+  return %0 : tensor<4xf32>
+}"""
 
 
 @pytest.fixture(scope="module")
@@ -218,8 +252,16 @@ def compile_error(client, blob):
     with pytest.raises(pjrt.PjrtError) as ei:
         client.compile(blob)
     assert ei.value.code == "INVALID_ARGUMENT"
-    assert ei.value.message.startswith("jam compile: jam: MLIR bytecode")
+    assert ei.value.message.startswith(("jam compile: jam: MLIR bytecode", "jam compile: jam: VHLO"))
     return ei.value.message
+
+
+def plan_of(client, program):
+    e = client.compile(program)
+    try:
+        return e.plan(), e.output_types(), e.output_shapes()
+    finally:
+        e.destroy()
 
 
 def test_varint_encodings_fixed_by_the_format():
@@ -230,13 +272,69 @@ def test_varint_encodings_fixed_by_the_format():
     assert varint(5, wide=True) == b"\x00\x05" + b"\x00" * 7
 
 
-def test_portable_artifact_v1_is_read(client):
+def test_portable_artifact_v1_compiles(client):
+    """The hand-assembled artifact of a + b compiles to the plan of the same
+    module as text: one elementwise launch, f32[4] out."""
     st, top = artifact_v1()
-    msg = compile_error(client, st.build([top]))
-    assert "MLIR bytecode v1 from 'StableHLO_v1.0.0'" in msg
-    assert "dialects builtin, vhlo 1.0.0" in msg and "2 attributes, 1 types" in msg
-    assert "ops builtin.module x1, vhlo.func_v1 x1, vhlo.add_v1 x1, vhlo.return_v1 x1" in msg
-    assert "VHLO attribute and type encodings" in msg and "not implemented" in msg
+    assert plan_of(client, st.build([top])) == plan_of(client, ADD_TEXT)
+    assert "] ew" in plan_of(client, ADD_TEXT)[0]
+
+
+def test_vhlo_decoding_errors_are_named(client):
+    """What the decoder refuses names itself, with the container summary
+    (producer, dialect versions, op histogram) after it."""
+    cases = {
+        "dynamic dim": (artifact_v1(dim=-(1 << 63)), "has a dynamic dimension"),
+        "unknown type code": (artifact_v1(f32_code=200), "type code 200, which is not decoded"),
+        "complex element": (artifact_v1(f32_code=1), "element type complex is not supported"),
+        "module-level op": (artifact_v1(module_level_extra=True), "module-level operation vhlo.return_v1"),
+    }
+    for name, ((st, top), needle) in cases.items():
+        msg = compile_error(client, st.build([top]))
+        assert needle in msg, (name, msg)
+        assert "artifact: MLIR bytecode v1 from 'StableHLO_v1.0.0', dialects builtin, vhlo 1.0.0" in msg, msg
+        assert "vhlo.func_v1 x1" in msg
+
+
+def test_compare_type_checks_the_element_codes(client):
+    """compare_type must fit the operands' element type: SIGNED on f32
+    operands means the element type codes were not read as written."""
+    def artifact(cmp_type):
+        st = Stream(1, "StableHLO_v1.0.0")
+        builtin = st.dialect("builtin")
+        vhlo = st.dialect("vhlo", [1, 0, 0])
+        module = st.op_name(builtin, "module")
+        func, cmp, ret = (st.op_name(vhlo, n) for n in ("func_v1", "compare_v1", "return_v1"))
+        loc = st.attr(builtin, varint(BI_UNKNOWN_LOC), True)
+        keys = {k: st.attr(builtin, varint(BI_STRING) + varint(st.s(k)), True)
+                for k in ("compare_type", "comparison_direction", "function_type", "sym_name")}
+        f32 = st.type(vhlo, varint(TY_F32), True)
+        i1 = st.type(vhlo, varint(0), True)
+        t = st.type(vhlo, varint(TY_TENSOR) + varint(1) + svarint(4) + varint(f32), True)
+        tb = st.type(vhlo, varint(TY_TENSOR) + varint(1) + svarint(4) + varint(i1), True)
+        fty = st.type(vhlo, varint(TY_FUNCTION) + varint(2) + varint(t) * 2 + varint(1) + varint(tb), True)
+        v_name = st.attr(vhlo, varint(AT_STRING) + varint(st.s("main")), True)
+        v_ft = st.attr(vhlo, varint(AT_TYPE) + varint(fty), True)
+        v_dir = st.attr(vhlo, varint(AT_CMP_DIR) + varint(3), True)        # GT
+        v_ct = st.attr(vhlo, varint(AT_CMP_TYPE) + varint(cmp_type), True)
+        fattrs = st.attr(builtin, varint(BI_DICT) + varint(2) + varint(keys["function_type"]) + varint(v_ft) +
+                         varint(keys["sym_name"]) + varint(v_name), True)
+        cattrs = st.attr(builtin, varint(BI_DICT) + varint(2) + varint(keys["compare_type"]) + varint(v_ct) +
+                         varint(keys["comparison_direction"]) + varint(v_dir), True)
+        body = {"blocks": [{"args": [(t, loc), (t, loc)],
+                            "ops": [{"name": cmp, "loc": loc, "attrs": cattrs, "results": [tb], "operands": [0, 1]},
+                                    {"name": ret, "loc": loc, "operands": [2]}]}], "num_values": 3}
+        fn = {"name": func, "loc": loc, "attrs": fattrs, "regions": [body], "isolated": True}
+        top = {"name": module, "loc": loc, "regions": [{"blocks": [{"ops": [fn]}], "num_values": 0}],
+               "isolated": True}
+        return st.build([top])
+
+    text = """func.func public @main(%a: tensor<4xf32>, %b: tensor<4xf32>) -> tensor<4xi1> {
+  %0 = stablehlo.compare GT, %a, %b, FLOAT : (tensor<4xf32>, tensor<4xf32>) -> tensor<4xi1>
+  return %0 : tensor<4xi1>
+}"""
+    assert plan_of(client, artifact(1)) == plan_of(client, text)  # FLOAT
+    assert "compare_type SIGNED on f32 operands" in compile_error(client, artifact(3))
 
 
 def test_newest_layout_features(client):
@@ -261,6 +359,7 @@ def test_newest_layout_features(client):
     top = {"name": module, "loc": loc, "regions": [{"blocks": [blk], "num_values": 4}], "isolated": True}
     blob = st.build([top], align_ir=8)
     msg = compile_error(client, blob)
+    assert "holds no vhlo dialect" in msg  # read in full, then refused: not an artifact
     assert "MLIR bytecode v6 from 'MLIR21'" in msg and "test 7" in msg
     assert "ops builtin.module x1, test.two_results x1, test.use x2" in msg
 
