@@ -18,8 +18,9 @@
 namespace mi::pjrt {
 namespace {
 
-// Serialized executables: this magic, then the StableHLO text they were
-// compiled from (recompiled on load; compilation is deterministic).
+// Serialized executables: this magic, then the program bytes they were
+// compiled from, StableHLO text or a portable artifact (recompiled on load;
+// compilation is deterministic).
 constexpr char kSerialMagic[] = "mi355x-jam/1\n";
 
 struct Compiled {
