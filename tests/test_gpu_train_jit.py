@@ -99,3 +99,74 @@ def test_gpt2_jitted_steps_descend(client):
         loss, params, m, v, _ = _step(client, cfg, params, m, v, ids, np.roll(ids, -1, axis=1), 3e-3, t)
         losses.append(loss)
     assert np.isfinite(losses).all() and losses[2] < losses[0], losses
+
+
+def test_gpt2_jitted_step_c5_full_size(client):
+    """The benchmark configuration (12 layers, d 768, B 8, S 1024, V 50257)
+    as one jitted module through Execute, against the hand-scheduled step
+    (GPT2TrainStep: the same kernels launched from Python) on the same fp32
+    parameters and batch:
+      - loss within 0.5 of ln V at random init, and within 2e-3 relative of
+        the hand-scheduled step's;
+      - every output finite;
+      - each gradient within 3e-2 relative L2 of the hand-scheduled step's
+        (both round the products' operands to bf16);
+      - gradient signs agree on at least 99% of the elements whose |g| is
+        above 5% of the tensor's rms (clear of bf16 rounding noise);
+      - the updated parameters: at t = 1 Adam moves each by
+        lr * g / (|g| + eps), so where both gradients have one sign and
+        |g| > 1e-5 (1000 eps) the new parameters agree to 1e-3 lr plus fp32
+        rounding."""
+    import torch
+
+    cfg = gpt2.GPT2Config()
+    print("case: jitted gpt2 step C5 full size through PJRT Execute vs GPT2TrainStep", flush=True)
+    params = gpt2.init_params(cfg, 0)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, cfg.vocab, (cfg.batch, cfg.seq))
+    labels = np.roll(ids, -1, axis=1)
+    zeros = {n: np.zeros_like(a) for n, a in params.items()}
+    lr = 3e-4
+    loss, new_p, new_m, new_v, grads = _step(client, cfg, params, zeros, zeros, ids, labels, lr, 1)
+    assert abs(loss - np.log(cfg.vocab)) < 0.5, loss
+    for out in (new_p, new_m, new_v, grads):
+        bad = [n for n, a in out.items() if not np.isfinite(a).all()]
+        assert not bad, bad
+
+    step = gpt2.GPT2TrainStep(cfg, params=params, lr=lr)
+    step.set_batch(ids, labels)
+    step.step()
+    torch.cuda.synchronize()
+    h_loss = step.loss_value()
+    h_grad = step.params_numpy(step.grad)
+    h_p = step.params_numpy(step.master)
+    print(f"loss jitted {loss:.6f}  hand-scheduled {h_loss:.6f}", flush=True)
+    assert abs(loss - h_loss) <= 2e-3 * abs(h_loss)
+    worst_g, worst_p, worst_agree = 0.0, 0.0, 1.0
+    for n in params:
+        g, hg = grads[n].astype(np.float64), h_grad[n].astype(np.float64)
+        rel = float(np.linalg.norm(g - hg) / max(np.linalg.norm(hg), 1e-30))
+        worst_g = max(worst_g, rel)
+        assert rel < 3e-2, (n, rel)
+        # signs are compared where |g| is well above both steps' rounding
+        # noise (bf16 operands: about 1% of the tensor's rms)
+        big = np.abs(hg) > 0.05 * np.sqrt(np.mean(hg ** 2))
+        same = np.sign(g) == np.sign(hg)
+        agree = float(np.mean(same[big])) if big.any() else 1.0
+        worst_agree = min(worst_agree, agree)
+        assert agree >= 0.99, (n, agree)
+        # where both |g| exceed 1e-5 = 1000 eps with one sign, each update is
+        # sign(g) lr (1 - eps / |g|): the two agree to 1e-3 lr
+        sel = (np.abs(g) > 1e-5) & (np.abs(hg) > 1e-5) & same
+        d = np.abs(new_p[n].astype(np.float64) - h_p[n].astype(np.float64))[sel]
+        tol = 1e-3 * lr + 2.0 ** -22 * np.abs(params[n].astype(np.float64))[sel]
+        if d.size:
+            worst_p = max(worst_p, float((d / tol).max()))
+        if not np.all(d <= tol):
+            k = np.flatnonzero(sel)[np.argmax(d - tol)]
+            print(f"{n}: {int((d > tol).sum())} of {d.size} elements out of bound; worst at {k}: g {g.flat[k]:.6e} "
+                  f"hand g {hg.flat[k]:.6e} p0 {params[n].flat[k]:.8e} jitted p {new_p[n].flat[k]:.8e} "
+                  f"hand p {h_p[n].flat[k]:.8e}", flush=True)
+        assert np.all(d <= tol), (n, float(d.max()))
+    print(f"worst gradient rel L2 {worst_g:.3e}, worst sign agreement {worst_agree:.5f}, "
+          f"worst parameter diff / bound {worst_p:.3f}", flush=True)
