@@ -230,6 +230,19 @@ int mk_ew_program(void* stream, int rank, const int64_t* dims,
                   int n_instr, const int32_t* program, const float* consts, int n_consts,
                   int out_reg, int out_type, void* out);
 
+/* mk_ew_program with 1 to 4 outputs of the same shape, each dense row-major:
+ * register out_regs[k] is stored to outs[k] as out_types[k].  Every input
+ * element is loaded before any output element is stored, so an output may
+ * be the memory of an input read at the same index (in place).  The sibling
+ * outputs of one fused chain (an optimizer's new parameter and moments, or
+ * values a backward pass keeps) take one launch that reads the shared
+ * inputs once, instead of one launch per output. */
+int mk_ew_program_multi(void* stream, int rank, const int64_t* dims,
+                        int n_inputs, const void* const* inputs, const int* in_types,
+                        const int64_t* in_strides,
+                        int n_instr, const int32_t* program, const float* consts, int n_consts,
+                        int n_outputs, const int* out_regs, const int* out_types, void* const* outs);
+
 /* ------------------------------------------------------------------------
  * a10  row gather (embedding lookup), bit-exact copy.
  * Replaces: src/jam/ops/gather_scatter.mm:185-196 (gatherWithUpdatesTensor

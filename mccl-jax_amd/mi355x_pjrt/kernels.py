@@ -239,6 +239,35 @@ def ew_program(shape, inputs, program, consts, out_reg, out_dtype, stream=None, 
     return out
 
 
+def ew_program_multi(shape, inputs, program, consts, out_regs, outs, stream=None):
+    """mk_ew_program_multi: one program, 1 to 4 outputs (dense tensors of
+    `shape`, each written from its register in out_regs)."""
+    rank = len(shape)
+    for o in outs:
+        if tuple(o.shape) != tuple(shape) or not o.is_contiguous():
+            raise ValueError("ew_program_multi: outputs must be dense tensors of the given shape")
+    ptrs = (ctypes.c_void_p * max(len(inputs), 1))(*[t.data_ptr() for t in inputs])
+    types = (ctypes.c_int * max(len(inputs), 1))(*[mk_dtype(t.dtype) for t in inputs])
+    strides = (ctypes.c_int64 * (6 * max(len(inputs), 1)))()
+    for i, t in enumerate(inputs):
+        tt = t.expand(shape)
+        for d in range(rank):
+            strides[6 * i + d] = tt.stride(d)
+    prog = (ctypes.c_int32 * (4 * max(len(program), 1)))()
+    for p, ins in enumerate(program):
+        for j in range(4):
+            prog[4 * p + j] = int(ins[j])
+    cst = (ctypes.c_float * max(len(consts), 1))(*consts)
+    dims = (ctypes.c_int64 * max(rank, 1))(*shape)
+    regs = (ctypes.c_int * len(outs))(*out_regs)
+    otypes = (ctypes.c_int * len(outs))(*[mk_dtype(o.dtype) for o in outs])
+    optrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    rc = lib().mk_ew_program_multi(_stream(stream), rank, dims, len(inputs), ptrs, types, strides, len(program),
+                                   prog, cst, len(consts), len(outs), regs, otypes, optrs)
+    _check(rc, "mk_ew_program_multi")
+    return outs
+
+
 # ------------------------------------------------------------------ a10/a11 indexing
 def gather_rows(table, ids, stream=None):
     _require_cuda(table, ids)

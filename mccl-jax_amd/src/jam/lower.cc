@@ -59,6 +59,7 @@ const char* StepName(StepKind k) {
     case StepKind::kGemmBlas: return "gemm_blas";
     case StepKind::kSoftmaxXent: return "softmax_xent";
     case StepKind::kColSum: return "col_sum";
+    case StepKind::kGemmSplitK: return "gemm_splitk";
   }
   return "?";
 }
@@ -415,11 +416,16 @@ class Lowerer {
       case StepKind::kGemmBlas: return {2};
       case StepKind::kSoftmaxXent: return {2, 3};
       case StepKind::kColSum: return {1, 2};
+      case StepKind::kGemmSplitK: return {2, 3};
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
       case StepKind::kGelu: return {1};
-      case StepKind::kEw: return {size_t(s.i[7])};
+      case StepKind::kEw: {
+        std::vector<size_t> w;
+        for (size_t k = size_t(s.i[7]); k < s.bufs.size(); ++k) w.push_back(k);
+        return w;
+      }
       case StepKind::kGather: return {2};
       case StepKind::kScatterAdd: return {3, 4};
       case StepKind::kIota: return {0};
@@ -458,7 +464,10 @@ class Lowerer {
       if (is_in(s.bufs[j]) && std::find(wr.begin(), wr.end(), j) == wr.end()) reads.push_back(j);
     if (reads.empty()) return true;
     // the writer reads the input too: only element-for-element in place
-    const BufRef& out = s.bufs[wr.front()];
+    size_t wo = wr.front();
+    for (size_t w : wr)
+      if (is_out(s.bufs[w])) wo = w;
+    const BufRef& out = s.bufs[wo];
     for (size_t j : reads)
       if (s.bufs[j].offset != 0 || out.offset != 0) {
         why = "writer reads the input at an offset";
@@ -475,7 +484,9 @@ class Lowerer {
         const int rank = int(s.i[0]);
         std::vector<int64_t> dims(s.i.begin() + 1, s.i.begin() + 1 + rank);
         const std::vector<int64_t> dense = DenseStrides(dims);
-        const int out_type = int(s.i[9]);
+        // output k of the step: its type is i[9] for k = 0, else i[11 + 2 (k - 1)]
+        const size_t k_out = wo - size_t(s.i[7]);
+        const int out_type = int(k_out == 0 ? s.i[9] : s.i[11 + 2 * (k_out - 1)]);
         for (size_t j : reads) {
           if (DTypeBytes(DType(s.types[j])) != DTypeBytes(DType(out_type))) {
             why = "elementwise input and output widths differ";
@@ -2560,28 +2571,41 @@ class Lowerer {
     return dst;
   }
 
-  void EmitEw(int v, BufRef dst) {
+  void EmitEw(int v, BufRef dst) { EmitEwGroup({v}, {dst}); }
+
+  // One program computing every root (same shape) into its destination:
+  // the roots' shared subexpressions and inputs are evaluated and loaded
+  // once.  Returns false (emitting nothing) when a group of more than one
+  // root does not fit the interpreter's limits; a single root is split
+  // until it fits.
+  bool EmitEwGroup(const std::vector<int>& roots, const std::vector<BufRef>& dsts) {
+    const TensorType& t = m_.types[roots[0]];
     for (int attempt = 0; attempt < 64; ++attempt) {
       std::vector<int> leaves;
       std::unordered_map<int, int> refs;
       std::set<int> seen;
-      CollectLeaves(v, leaves, refs, seen);
+      for (int v : roots) CollectLeaves(v, leaves, refs, seen);
+      for (int v : roots) ++refs[v];  // a root's register is held until its store
       if (leaves.size() > 8) {
-        SplitLargestChild(v);
+        if (roots.size() > 1) return false;
+        SplitLargestChild(roots[0]);
         continue;
       }
       EwBuild b;
       b.leaves = leaves;
       b.refs = refs;
       b.next_reg = int(leaves.size());
-      int out_reg;
+      std::vector<int> out_regs;
       try {
-        out_reg = Gen(b, v, true);
+        // a root that other roots also read is generated as an interior
+        // value (with its per-op rounding); storing it rounds it again to
+        // the same bits
+        for (int v : roots) out_regs.push_back(Gen(b, v, refs[v] == 1));
       } catch (int) {
-        SplitLargestChild(v);
+        if (roots.size() > 1) return false;
+        SplitLargestChild(roots[0]);
         continue;
       }
-      const TensorType& t = m_.types[v];
       if (t.rank() > 6) throw std::string("jam: rank > 6 elementwise is not supported");
       Step st;
       st.kind = StepKind::kEw;
@@ -2592,12 +2616,14 @@ class Lowerer {
         st.types.push_back(int32_t(lv.dtype));
         for (int d = 0; d < 6; ++d) st.strides.push_back(d < lv.rank() ? lv.strides[d] : 0);
       }
-      st.bufs.push_back(dst);
+      for (const BufRef& d : dsts) st.bufs.push_back(d);
       st.i = {t.rank()};
       for (int d = 0; d < 6; ++d) st.i.push_back(d < t.rank() ? t.dims[d] : 1);
       st.i.push_back(int64_t(leaves.size()));
-      st.i.push_back(out_reg);
-      st.i.push_back(int64_t(t.dtype));
+      for (size_t k = 0; k < roots.size(); ++k) {
+        st.i.push_back(out_regs[k]);
+        st.i.push_back(int64_t(m_.types[roots[k]].dtype));
+      }
       for (auto& ins : b.prog)
         for (int k = 0; k < 4; ++k) st.prog.push_back(ins[k]);
       for (uint32_t c : b.consts) {
@@ -2605,12 +2631,58 @@ class Lowerer {
         memcpy(&f, &c, 4);
         st.f.push_back(f);
       }
-      st.note = ops_[state_[v].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
-                std::to_string(leaves.size()) + " inputs)";
+      st.note = ops_[state_[roots[0]].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
+                std::to_string(leaves.size()) + " inputs" +
+                (roots.size() > 1 ? ", " + std::to_string(roots.size()) + " outputs" : "") + ")";
       Emit(st);
-      return;
+      return true;
     }
     throw std::string("jam: could not split an elementwise expression");
+  }
+
+  // Output k (an elementwise value) together with the later outputs of the
+  // same shape whose chains read at least one of its inputs, up to four
+  // outputs and eight inputs in all: one launch writes them all (the Adam
+  // update's new parameter, m and v read p, g, m and v once).
+  void EmitOutputGroup(size_t k, BufRef dst) {
+    const int v = outputs_[k];
+    auto leaf_set = [&](int r) {
+      std::vector<int> leaves;
+      std::unordered_map<int, int> refs;
+      std::set<int> seen;
+      CollectLeaves(r, leaves, refs, seen);
+      return std::set<int>(leaves.begin(), leaves.end());
+    };
+    std::vector<int> roots = {v};
+    std::vector<BufRef> dsts = {dst};
+    std::vector<size_t> ks = {k};
+    if (opts_.fuse_elementwise) {
+      std::set<int> all = leaf_set(v);
+      for (size_t j = k + 1; j < outputs_.size() && roots.size() < 4; ++j) {
+        const int w = outputs_[j];
+        if (out_written_[j] || state_[w].kind != ValState::kEw || m_.types[w].dims != m_.types[v].dims ||
+            std::count(roots.begin(), roots.end(), w))
+          continue;
+        const std::set<int> lw = leaf_set(w);
+        std::set<int> u = all;
+        u.insert(lw.begin(), lw.end());
+        bool shares = false;
+        for (int l : lw) shares = shares || all.count(l);
+        if (!shares || u.size() > 8) continue;
+        roots.push_back(w);
+        dsts.push_back(BufRef{Space::kOutput, int(j), 0});
+        ks.push_back(j);
+        all = u;
+      }
+    }
+    if (roots.size() > 1 && EmitEwGroup(roots, dsts)) {
+      for (size_t i = 1; i < roots.size(); ++i) {
+        out_written_[ks[i]] = true;
+        SetDenseView(roots[i], dsts[i]);
+      }
+      return;
+    }
+    EmitEw(v, dst);
   }
 
   // materialize the biggest in-expression child of v so the expression shrinks
@@ -2659,7 +2731,7 @@ class Lowerer {
         BufRef dst{Space::kOutput, int(k), 0};
         out_written_[k] = true;
         if (state_[v].kind == ValState::kEw) {
-          EmitEw(v, dst);
+          EmitOutputGroup(k, dst);
         } else {
           const TensorType& t = m_.types[v];
           Step st;
@@ -3011,6 +3083,26 @@ class Lowerer {
     if (at == DType::kBF16 && !epi && (ct == DType::kF32 || ct == DType::kBF16) &&
         !(rows8(a_bs, a_ms, a_ks) && rows8(b_bs, b_ns, b_ks)) && double(B) * M * N * K >= double(int64_t(1) << 30))
       st.kind = StepKind::kGemmBlas;
+    // one fp32 product with few output tiles and a long contraction (the
+    // weight gradients Xᵀ·dY, contracted over the tokens): the K axis is cut
+    // into slices summed in order (mk_gemm_splitk), enough of them that the
+    // grid covers the CUs (about 400 workgroups of 128x128), each slice at
+    // least 256 deep
+    if (st.kind == StepKind::kGemm && !epi && B == 1 && ct == DType::kF32 && N % 4 == 0 && K >= 2 * std::max(M, N)) {
+      const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+      int64_t splits = 1;
+      while (splits < 8 && tiles * splits < 400 && K % (2 * splits) == 0 && K / (2 * splits) >= 256) splits *= 2;
+      if (splits > 1) {
+        st.kind = StepKind::kGemmSplitK;
+        st.bufs = {lv.at(), rv.at(), d, NewTemp(mk_gemm_splitk_workspace_bytes(M, N, splits))};
+        st.i = {int64_t(at), M, N, K, a_ms, a_ks, b_ks, b_ns, N, splits};
+        st.note = std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " in " +
+                  std::to_string(splits) + " slices";
+        Emit(st);
+        SetDenseView(res, d);
+        return;
+      }
+    }
     st.bufs = {lv.at(), rv.at(), d};
     int epilogue = 0;
     if (epi) {

@@ -55,12 +55,14 @@ void* Resolve(const BufRef& b, const Frame& f) {
 // Step encodings (written by lower.cc):
 //   gemm     bufs A,B,C[,bias]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
 //   gemm_blas bufs A,B,C        i as gemm (no epilogue)
+//   gemm_splitk bufs A,B,C,workspace  i ab_type,M,N,K,a_ms,a_ks,b_ks,b_ns,c_ms,splits
 //   sdpa     bufs Q,K,V,O[,lse] i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
 //   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
 //   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
 //   layernorm bufs x,g,b,y      i io_type,rows,cols  f eps
 //   gelu     bufs x,y           i io_type,n
-//   ew       bufs in...,out     i rank,dims[6],n_inputs,out_reg,out_type  prog  strides[6n]  types[n]  f consts
+//   ew       bufs in...,out...  i rank,dims[6],n_inputs,(out_reg,out_type) per output  prog  strides[6n]
+//                               types[n]  f consts
 //   gather   bufs table,ids,out i n_rows,row_bytes,index_type,n_ids
 //   scatter_add bufs table,ids,updates,out,workspace  i dtype,n_rows,row_len,index_type,n_ids
 //   iota     bufs out           i out_type,rank,dim,dims...
@@ -95,6 +97,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
                          P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], P(4), i[17], i[18], i[19],
                          static_cast<const float*>(P(5)), P(6), i[20], i[21], i[22], P(7), i[23], i[24], i[25],
                          P(8), i[26], i[27], i[28], s.f[0], int(i[29]), P(9));
+    case StepKind::kGemmSplitK:
+      return mk_gemm_splitk(st, int(i[0]), i[1], i[2], i[3], P(0), i[4], i[5], P(1), i[6], i[7],
+                            static_cast<float*>(P(2)), i[8], i[9], P(3));
     case StepKind::kColSum:  // y[c] = sum_r x[r, c]: i = {dtype, rows, cols}
       return mk_col_sum(st, int(i[0]), i[1], i[2], P(0), static_cast<float*>(P(1)), P(2));
     case StepKind::kRowReduce:
@@ -107,14 +112,23 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
       return mk_gelu_tanh(st, int(i[0]), i[1], P(0), P(1));
     case StepKind::kEw: {
       const int n_in = int(i[7]);
+      const int n_out = int(s.bufs.size()) - n_in;
+      if (n_in > 8 || n_out < 1 || n_out > 4) return MK_ERR_INVALID;
       const void* ins[8];
       int types[8];
       for (int k = 0; k < n_in; ++k) {
         ins[k] = P(size_t(k));
         types[k] = s.types[size_t(k)];
       }
-      return mk_ew_program(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
-                           s.prog.data(), s.f.data(), int(s.f.size()), int(i[8]), int(i[9]), P(size_t(n_in)));
+      int regs[4], otypes[4];
+      void* outs[4];
+      for (int k = 0; k < n_out; ++k) {
+        regs[k] = int(i[8 + 2 * size_t(k)]);
+        otypes[k] = int(i[9 + 2 * size_t(k)]);
+        outs[k] = P(size_t(n_in + k));
+      }
+      return mk_ew_program_multi(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
+                                 s.prog.data(), s.f.data(), int(s.f.size()), n_out, regs, otypes, outs);
     }
     case StepKind::kGather:
       return mk_gather_rows(st, i[0], i[1], P(0), int(i[2]), i[3], P(1), P(2));

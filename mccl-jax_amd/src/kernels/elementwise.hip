@@ -73,6 +73,7 @@ constexpr int kEwMaxInputs = 8;
 constexpr int kEwMaxRegs = 32;
 constexpr int kEwMaxInstr = 64;
 constexpr int kEwMaxConsts = 64;
+constexpr int kEwMaxOutputs = 4;
 
 struct EwArgs {
   const void* in[kEwMaxInputs];
@@ -83,11 +84,13 @@ struct EwArgs {
   int rank;
   int n_inputs;
   int n_instr;
-  int out_reg;
-  int out_type;
+  int n_out;                 // 1 .. kEwMaxOutputs dense outputs of the shape
+  int out_reg[kEwMaxOutputs];
+  int out_type[kEwMaxOutputs];
+  void* out[kEwMaxOutputs];
   int need_index;  // some input is strided: decompose the linear index
   int in_vec[kEwMaxInputs];  // vector form: 4 consecutive elements in one 16-byte (f32) / 8-byte (bf16) load
-  int out_vec;               // vector form: 4 consecutive outputs in one store
+  int out_vec[kEwMaxOutputs];  // vector form: 4 consecutive outputs in one store
   int32_t prog[kEwMaxInstr][4];
   float consts[kEwMaxConsts];
 };
@@ -230,7 +233,7 @@ __device__ __attribute__((always_inline)) inline void ew_run(const EwArgs& A, fl
 // fit 31 bits (the index decomposition is then 32-bit division), int64_t
 // otherwise.
 template <typename IdxT>
-__global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n, void* out) {
+__global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int64_t n) {
   const int64_t i64 = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (i64 >= n) return;
   const IdxT i = IdxT(i64);
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
     r[0][t] = ew_load(A.in[t], int64_t(off), A.in_type[t]);
   }
   ew_run<1, kEwMaxRegs>(A, r);
-  ew_store(out, i64, A.out_type, r[0][A.out_reg]);
+  for (int k = 0; k < A.n_out; ++k) ew_store(A.out[k], i64, A.out_type[k], r[0][A.out_reg[k]]);
 }
 
 // The same program on kEwVec consecutive elements of the innermost dim per
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(kBlock) void ew_program_kernel(const EwArgs A, int6
 // elements are loaded before the program runs on the first of them.
 constexpr int kEwVec = 4;
 template <int NR>
-__global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, uint32_t n, void* out) {
+__global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, uint32_t n) {
   const uint32_t i0 = (blockIdx.x * uint32_t(kBlock) + threadIdx.x) * kEwVec;
   if (i0 >= n) return;
   uint32_t idx[kEwMaxRank];
@@ -320,18 +323,21 @@ __global__ __launch_bounds__(kBlock) void ew_program_vec_kernel(const EwArgs A, 
   }
   // the program runs once on 4-lane registers
   ew_run<kEwVec, NR>(A, r);
-  float o[kEwVec];
+  for (int k = 0; k < A.n_out; ++k) {
+    float o[kEwVec];
 #pragma unroll
-  for (int e = 0; e < kEwVec; ++e) o[e] = r[e][A.out_reg & (NR - 1)];
-  if (A.out_vec && A.out_type == MK_F32) {
-    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + i0) = f32x4{{o[0], o[1], o[2], o[3]}};
-  } else if (A.out_vec) {  // bf16
-    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i0) =
-        uint2{f32_to_bf16(o[0]) | (uint32_t(f32_to_bf16(o[1])) << 16),
-              f32_to_bf16(o[2]) | (uint32_t(f32_to_bf16(o[3])) << 16)};
-  } else {
+    for (int e = 0; e < kEwVec; ++e) o[e] = r[e][A.out_reg[k] & (NR - 1)];
+    void* out = A.out[k];
+    if (A.out_vec[k] && A.out_type[k] == MK_F32) {
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + i0) = f32x4{{o[0], o[1], o[2], o[3]}};
+    } else if (A.out_vec[k]) {  // bf16
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i0) =
+          uint2{f32_to_bf16(o[0]) | (uint32_t(f32_to_bf16(o[1])) << 16),
+                f32_to_bf16(o[2]) | (uint32_t(f32_to_bf16(o[3])) << 16)};
+    } else {
 #pragma unroll
-    for (int e = 0; e < kEwVec; ++e) ew_store(out, int64_t(i0) + e, A.out_type, o[e]);
+      for (int e = 0; e < kEwVec; ++e) ew_store(out, int64_t(i0) + e, A.out_type[k], o[e]);
+    }
   }
 }
 
@@ -466,30 +472,38 @@ extern "C" int mk_gelu_tanh(void* stream, int io_type, int64_t n, const void* x,
   return fail(MK_ERR_UNSUPPORTED, "mk_gelu_tanh: io_type must be bf16/f32");
 }
 
-extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_inputs,
-                             const void* const* inputs, const int* in_types,
-                             const int64_t* in_strides, int n_instr, const int32_t* program,
-                             const float* consts, int n_consts, int out_reg, int out_type,
-                             void* out) {
+extern "C" int mk_ew_program_multi(void* stream, int rank, const int64_t* dims, int n_inputs,
+                                   const void* const* inputs, const int* in_types,
+                                   const int64_t* in_strides, int n_instr, const int32_t* program,
+                                   const float* consts, int n_consts, int n_outputs, const int* out_regs,
+                                   const int* out_types, void* const* outs) {
   clear_error();
   if (rank < 0 || rank > kEwMaxRank) return fail(MK_ERR_INVALID, "mk_ew_program: rank > 6");
+  if (n_outputs < 1 || n_outputs > kEwMaxOutputs) return fail(MK_ERR_INVALID, "mk_ew_program: 1 to 4 outputs");
   if (n_inputs < 0 || n_inputs > kEwMaxInputs) return fail(MK_ERR_INVALID, "mk_ew_program: > 8 inputs");
   if (n_instr < 0 || n_instr > kEwMaxInstr) return fail(MK_ERR_INVALID, "mk_ew_program: > 64 instructions");
   if (n_consts < 0 || n_consts > kEwMaxConsts) return fail(MK_ERR_INVALID, "mk_ew_program: > 64 constants");
-  if (out_reg < 0 || out_reg >= kEwMaxRegs) return fail(MK_ERR_INVALID, "mk_ew_program: bad out_reg");
+  for (int k = 0; k < n_outputs; ++k) {
+    if (out_regs[k] < 0 || out_regs[k] >= kEwMaxRegs) return fail(MK_ERR_INVALID, "mk_ew_program: bad out_reg");
+    if (dtype_bytes(out_types[k]) == 0) return fail(MK_ERR_UNSUPPORTED, "mk_ew_program: bad output dtype");
+  }
   int64_t n = 1;
   for (int d = 0; d < rank; ++d) {
     if (dims[d] < 0) return fail(MK_ERR_INVALID, "mk_ew_program: negative dim");
     n *= dims[d];
   }
   if (n == 0) return MK_OK;
-  if (!out) return fail(MK_ERR_INVALID, "mk_ew_program: null output");
   EwArgs a{};
   a.rank = rank;
   a.n_inputs = n_inputs;
   a.n_instr = n_instr;
-  a.out_reg = out_reg;
-  a.out_type = out_type;
+  a.n_out = n_outputs;
+  for (int k = 0; k < n_outputs; ++k) {
+    if (!outs[k]) return fail(MK_ERR_INVALID, "mk_ew_program: null output");
+    a.out[k] = outs[k];
+    a.out_reg[k] = out_regs[k];
+    a.out_type[k] = out_types[k];
+  }
   for (int d = 0; d < rank; ++d) a.dims[d] = dims[d];
   int need_index = 0;
   for (int t = 0; t < n_inputs; ++t) {
@@ -510,7 +524,8 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
     need_index |= (a.in_mode[t] == 2);
   }
   // highest register the program names (inputs occupy 0 .. n_inputs - 1)
-  int max_reg = max(out_reg, n_inputs - 1);
+  int max_reg = n_inputs - 1;
+  for (int k = 0; k < n_outputs; ++k) max_reg = max(max_reg, out_regs[k]);
   for (int p = 0; p < n_instr; ++p) {
     const int32_t* ins = program + 4 * p;
     if (ins[0] < 0 || ins[0] >= MK_EW_NUM_OPS) return fail(MK_ERR_INVALID, "mk_ew_program: bad opcode");
@@ -559,23 +574,32 @@ extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_
       dense[d] = acc;
       acc *= dims[d];
     }
-    a.out_vec = vec_ok(out, out_type, dense);
+    for (int k = 0; k < n_outputs; ++k) a.out_vec[k] = vec_ok(outs[k], out_types[k], dense);
   }
   // the vector kernel with 16 registers per lane when the program fits (64
   // VGPRs of registers instead of 128: more waves per SIMD)
   if (narrow && dims[rank - 1] % kEwVec == 0 && max_reg < 16)
     hipLaunchKernelGGL(ew_program_vec_kernel<16>, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
-                       as_stream(stream), a, uint32_t(n), out);
+                       as_stream(stream), a, uint32_t(n));
   else if (narrow && dims[rank - 1] % kEwVec == 0)
     hipLaunchKernelGGL(ew_program_vec_kernel<kEwMaxRegs>, dim3(blocks_for(n / kEwVec, kBlock)), dim3(kBlock), 0,
-                       as_stream(stream), a, uint32_t(n), out);
+                       as_stream(stream), a, uint32_t(n));
   else if (narrow)
     hipLaunchKernelGGL(ew_program_kernel<int32_t>, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
-                       as_stream(stream), a, n, out);
+                       as_stream(stream), a, n);
   else
     hipLaunchKernelGGL(ew_program_kernel<int64_t>, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0,
-                       as_stream(stream), a, n, out);
+                       as_stream(stream), a, n);
   return check_launch("mk_ew_program");
+}
+
+extern "C" int mk_ew_program(void* stream, int rank, const int64_t* dims, int n_inputs,
+                             const void* const* inputs, const int* in_types,
+                             const int64_t* in_strides, int n_instr, const int32_t* program,
+                             const float* consts, int n_consts, int out_reg, int out_type,
+                             void* out) {
+  return mk_ew_program_multi(stream, rank, dims, n_inputs, inputs, in_types, in_strides, n_instr, program, consts,
+                             n_consts, 1, &out_reg, &out_type, &out);
 }
 
 extern "C" int mk_convert(void* stream, int in_type, int out_type, int64_t n, const void* in,

@@ -680,6 +680,46 @@ def test_ew_program_vec_kernel_matches_one_element_kernel(K):
         assert np.isfinite(outs[0]).sum() > n // 2
 
 
+@pytest.mark.parametrize("shape", [(512, 768), (37, 3)])
+def test_ew_program_multi_outputs(K, shape):
+    """Three outputs of one program (an Adam-shaped update: m' = b1 m +
+    (1-b1) g, v' = b2 v + (1-b2) g g, p' = p - lr m' / (sqrt(v') + eps),
+    lr a broadcast scalar) equal the three single-output programs bit for
+    bit, also written in place over p, m and v (f32) and with p' in bf16;
+    shapes for the 4-lane and one-element kernels."""
+    E = K.EW
+    rng = np.random.default_rng(21)
+    p, g, m, v = (rng.standard_normal(shape).astype(np.float32) for _ in range(4))
+    v = np.abs(v)
+    lr = np.array([1e-3], np.float32)
+    cst = [0.9, 0.1, 0.999, 0.001, 1e-8]
+    # registers: 0 p, 1 g, 2 m, 3 v, 4 lr
+    prog = [(E["CONST"], 5, 0, 0), (E["MUL"], 5, 5, 2), (E["CONST"], 6, 1, 0), (E["MUL"], 6, 6, 1),
+            (E["ADD"], 7, 5, 6),                                   # m'
+            (E["CONST"], 5, 2, 0), (E["MUL"], 5, 5, 3), (E["MUL"], 6, 1, 1), (E["CONST"], 8, 3, 0),
+            (E["MUL"], 6, 6, 8), (E["ADD"], 9, 5, 6),              # v'
+            (E["SQRT"], 10, 9, 0), (E["CONST"], 11, 4, 0), (E["ADD"], 10, 10, 11), (E["MUL"], 12, 4, 7),
+            (E["DIV"], 12, 12, 10), (E["SUB"], 13, 0, 12)]         # p'
+    ins = [torch.from_numpy(a).cuda() for a in (p, g, m, v)] + [torch.from_numpy(lr).cuda().reshape((1,) * len(shape))]
+    print(f"case: ew multi-output {shape}", flush=True)
+    singles = [K.ew_program(shape, ins, prog, cst, r, torch.float32).cpu().numpy() for r in (13, 7, 9)]
+    outs = [torch.empty(shape, device="cuda") for _ in range(3)]
+    K.ew_program_multi(shape, ins, prog, cst, [13, 7, 9], outs)
+    for a, b in zip(outs, singles):
+        np.testing.assert_array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32))
+    # in place: p', m', v' over p, m, v
+    pd, md, vd = ins[0].clone(), ins[2].clone(), ins[3].clone()
+    K.ew_program_multi(shape, [pd, ins[1], md, vd, ins[4]], prog, cst, [13, 7, 9], [pd, md, vd])
+    for a, b in zip((pd, md, vd), singles):
+        np.testing.assert_array_equal(a.cpu().numpy().view(np.uint32), b.view(np.uint32))
+    # mixed output types
+    pb = torch.empty(shape, dtype=torch.bfloat16, device="cuda")
+    mo = torch.empty(shape, device="cuda")
+    K.ew_program_multi(shape, ins, prog, cst, [13, 7], [pb, mo])
+    np.testing.assert_array_equal(host_bf16(pb), bf16.to_bf16_bits(singles[0]))
+    np.testing.assert_array_equal(mo.cpu().numpy().view(np.uint32), singles[1].view(np.uint32))
+
+
 def test_ew_program_fused_chain(K):
     """relu(x * w + b) with a broadcast row vector, plus a select/compare chain."""
     E = K.EW
