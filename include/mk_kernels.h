@@ -408,6 +408,15 @@ int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const
                     int label_type, const void* labels, float grad_scale, float* loss_rows,
                     void* dlogits);
 
+/* mk_softmax_xent with fp32 logits and bf16 dlogits (logits_type MK_F32,
+ * dlogits_type MK_BF16; equal types are mk_softmax_xent):
+ * the gradient of a jitted step whose only readers are bf16 products, so
+ * the fp32 gradient and its conversion are never written.  Same loss and
+ * label rules; dlogits is rounded to bf16 once. */
+int mk_softmax_xent_typed(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
+                          const void* logits, int label_type, const void* labels, float grad_scale,
+                          float* loss_rows, void* dlogits);
+
 /* One Adam step, the update of temp/dp_train.py:71-75:
  *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
  *   p = p - lr (m / bc1) / (sqrt(v / bc2) + eps)       (bc1 = 1-b1^t, bc2 = 1-b2^t)

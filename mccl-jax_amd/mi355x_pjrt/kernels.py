@@ -478,16 +478,17 @@ def gelu_tanh_bwd_colsum(x, dy, out=None, workspace=None, stream=None):
 
 def softmax_xent(logits, labels, grad_scale, loss_rows=None, dlogits=None, stream=None):
     """Per-row softmax cross-entropy loss (fp32) and the logit gradient
-    (dlogits may be logits itself)."""
+    (dlogits may be logits itself; a bf16 dlogits for fp32 logits takes the
+    mixed-type kernel)."""
     _require_cuda(logits, labels)
     cols = logits.shape[-1]
     rows = logits.numel() // cols
     loss_rows = torch.empty(rows, dtype=torch.float32, device=logits.device) if loss_rows is None else loss_rows
     dlogits = torch.empty_like(logits) if dlogits is None else dlogits
-    rc = lib().mk_softmax_xent(_stream(stream), mk_dtype(logits.dtype), rows, cols, _ptr(logits),
-                               mk_dtype(labels.dtype), _ptr(labels), float(grad_scale), _ptr(loss_rows),
-                               _ptr(dlogits))
-    _check(rc, "mk_softmax_xent")
+    rc = lib().mk_softmax_xent_typed(_stream(stream), mk_dtype(logits.dtype), mk_dtype(dlogits.dtype), rows, cols,
+                                     _ptr(logits), mk_dtype(labels.dtype), _ptr(labels), float(grad_scale),
+                                     _ptr(loss_rows), _ptr(dlogits))
+    _check(rc, "mk_softmax_xent_typed")
     return loss_rows, dlogits
 
 

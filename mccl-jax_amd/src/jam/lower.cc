@@ -344,8 +344,11 @@ struct Fused {
   bool train = false;
   // sdpa_bwd: dO (bf16), the forward's anchor, the three gradients
   int dout = -1, fwd = -1, dq = -1, dk = -1, dv = -1;
-  // softmax cross-entropy: logits (x), labels, per-row loss and dlogits values
+  // softmax cross-entropy: logits (x), labels, per-row loss and dlogits values;
+  // when every reader of an f32 dlogits converts it to bf16, those converts'
+  // results (written by the fused step instead)
   int labels = -1, dlogits = -1;
+  std::vector<int> dlogits_bf16;
   // argmax
   int x = -1;
   bool is_min = false;
@@ -1839,6 +1842,22 @@ class Lowerer {
     f.dlogits = dX;
     f.scale = float(gscale);
     f.deps = {X, lab};
+    // f32 logits whose gradient is only read through converts to bf16 (the
+    // operands of the two products of the vocabulary projection's backward):
+    // the kernel writes the bf16 gradient, and neither the f32 gradient nor
+    // the conversion pass exists
+    if (xt.dtype == DType::kF32 && std::count(outputs_.begin(), outputs_.end(), dX) == 0) {
+      const auto us = live_users(dX);
+      bool all_bf16 = !us.empty();
+      for (int u : us)
+        all_bf16 = all_bf16 && ops_[u].name == "stablehlo.convert" &&
+                   m_.types[ops_[u].results[0]].dtype == DType::kBF16;
+      if (all_bf16)
+        for (int u : us) {
+          f.dlogits_bf16.push_back(ops_[u].results[0]);
+          ops.insert(u);
+        }
+    }
     fused_[anchor] = f;
     for (int o : ops)
       if (o != anchor) absorbed_.insert(o);
@@ -2257,12 +2276,136 @@ class Lowerer {
     s.view.offset = 0;
   }
 
+  // ---- narrow copies
+  // narrow_[v] is a view of bf16 data that holds exactly the values of the
+  // f32 value v (v = widen(narrow_[v])): an attention result rounded to bf16
+  // by its kernel, or a product written in bf16 because every reader rounds
+  // it to bf16.  While nothing needs v's f32 form it is never written:
+  // layout ops carry the narrow view along, a convert back to bf16 is that
+  // view, and a sum reads it (widening on load is exact).
+  bool NarrowOnly(int v) {
+    auto memo = narrow_only_.find(v);
+    if (memo != narrow_only_.end()) return memo->second;
+    bool ok = m_.types[v].dtype == DType::kF32 && std::count(outputs_.begin(), outputs_.end(), v) == 0;
+    bool any = false;
+    for (int u : users_[v]) {
+      if (!ok) break;
+      if (!live_[u]) continue;  // inside a fused step, which reads its own inputs
+      any = true;
+      const Op& o = ops_[u];
+      if (fused_.count(u)) {
+        ok = false;
+      } else if (o.name == "stablehlo.convert") {
+        ok = m_.types[o.results[0]].dtype == DType::kBF16;
+      } else if (o.name == "stablehlo.transpose" || o.name == "stablehlo.reshape" ||
+                 o.name == "stablehlo.broadcast_in_dim" || o.name == "stablehlo.slice" ||
+                 o.name == "stablehlo.concatenate") {
+        ok = o.operands[0] == v || o.name == "stablehlo.concatenate";
+        ok = ok && NarrowOnly(o.results[0]);
+      } else if (o.name == "stablehlo.reduce") {
+        ok = o.operands.size() == 2 && o.operands[0] == v && reduce_body_op(o) == "stablehlo.add" &&
+             m_.types[o.results[0]].dtype == DType::kF32;
+      } else {
+        ok = false;
+      }
+    }
+    ok = ok && any;
+    narrow_only_[v] = ok;
+    return ok;
+  }
+
+  // The view a layout op (broadcast_in_dim, reshape, transpose, slice) makes
+  // of `sv`, its operand's view; a reshape with no strided form copies first.
+  View ApplyLayout(const Op& op, View sv) {
+    const std::string& n = op.name;
+    const TensorType& t = m_.types[op.results[0]];
+    View v = sv;
+    if (n == "stablehlo.broadcast_in_dim") {
+      const auto dims = attr_ints(op, {"dims", "broadcast_dimensions"});
+      v.dims = t.dims;
+      v.strides.assign(t.rank(), 0);
+      for (size_t k = 0; k < dims.size(); ++k) v.strides[dims[k]] = sv.dims[k] == 1 ? 0 : sv.strides[k];
+    } else if (n == "stablehlo.reshape") {
+      v.dims = t.dims;
+      if (!ReshapeStrides(sv.dims, sv.strides, v.dims, v.strides)) {
+        if (!sv.dense()) sv = Densify(sv);
+        v = sv;
+        v.dims = t.dims;
+        v.strides = DenseStrides(v.dims);
+      }
+    } else if (n == "stablehlo.transpose") {
+      const auto perm = attr_ints(op, {"dims", "permutation"});
+      for (size_t k = 0; k < perm.size(); ++k) {
+        v.dims[k] = sv.dims[perm[k]];
+        v.strides[k] = sv.strides[perm[k]];
+      }
+    } else if (n == "stablehlo.slice") {
+      const auto st = attr_ints(op, {"start_indices"});
+      const auto sd = attr_ints(op, {"strides"});
+      v.dims = t.dims;
+      for (int k = 0; k < sv.rank(); ++k) {
+        v.offset += st.at(k) * sv.strides[k];
+        v.strides[k] = sv.strides[k] * (sd.empty() ? 1 : sd[k]);
+      }
+    } else {
+      throw std::string("jam: internal: not a layout op: " + n);
+    }
+    return v;
+  }
+
+  // The concatenate that merges the three attention gradients when each is
+  // transpose(0,2,1,3) -> reshape [B·S, H·D] (nothing else reading them)
+  // and the three are its operands in order along dim 1; -1 otherwise.
+  int MergedQkvConcat(const int g[3], int64_t B, int64_t H, int64_t S, int64_t D) {
+    int concat = -1;
+    for (int k = 0; k < 3; ++k) {
+      if (m_.types[g[k]].dtype != DType::kF32 || !NarrowOnly(g[k])) return -1;
+      const auto u1 = live_users(g[k]);
+      if (u1.size() != 1 || ops_[u1[0]].name != "stablehlo.transpose" ||
+          attr_ints(ops_[u1[0]], {"dims", "permutation"}) != std::vector<int64_t>{0, 2, 1, 3})
+        return -1;
+      const int t = ops_[u1[0]].results[0];
+      const auto u2 = live_users(t);
+      if (u2.size() != 1 || ops_[u2[0]].name != "stablehlo.reshape" ||
+          m_.types[ops_[u2[0]].results[0]].dims != std::vector<int64_t>{B * S, H * D})
+        return -1;
+      const int r = ops_[u2[0]].results[0];
+      const auto u3 = live_users(r);
+      if (u3.size() != 1 || ops_[u3[0]].name != "stablehlo.concatenate") return -1;
+      const Op& c = ops_[u3[0]];
+      const auto dd = attr_ints(c, {"dim", "dimension"});
+      if (c.operands.size() != 3 || c.operands[size_t(k)] != r || dd.empty() || dd[0] != 1) return -1;
+      if (concat >= 0 && concat != u3[0]) return -1;
+      concat = u3[0];
+    }
+    return concat;
+  }
+
+  // A layout op over a value with a narrow copy, whose result is only read
+  // narrow: the result gets the narrow copy's view and no wide form.
+  bool PropagateNarrow(const Op& op) {
+    if (op.name == "stablehlo.broadcast") return false;
+    auto nw = narrow_.find(op.operands[0]);
+    if (nw == narrow_.end() || !NarrowOnly(op.results[0])) return false;
+    narrow_[op.results[0]] = ApplyLayout(op, nw->second);
+    return true;
+  }
+
   // Guarantee that `v` is available as a view; emits steps as needed.
   const View& NeedView(int v) {
     ValState& s = state_[v];
     if (s.kind == ValState::kView) return s.view;
-    if (s.kind == ValState::kUnset)
-      throw std::string("jam: value %" + std::to_string(v) + " used before it was lowered");
+    if (s.kind == ValState::kUnset) {
+      auto nw = narrow_.find(v);
+      if (nw == narrow_.end())
+        throw std::string("jam: value %" + std::to_string(v) + " used before it was lowered");
+      // its wide form after all: widen the narrow copy
+      const View src = nw->second.dense() ? nw->second : Densify(nw->second);
+      BufRef d = DestFor(v);
+      EmitConvert(src.at(), src.dtype, d, m_.types[v].dtype, m_.types[v].numel());
+      SetDenseView(v, d);
+      return state_[v].view;
+    }
     const TensorType& t = m_.types[v];
     BufRef dst = DestFor(v);
     if (s.kind == ValState::kScalar) {
@@ -2610,7 +2753,8 @@ class Lowerer {
       Step st;
       st.kind = StepKind::kEw;
       for (int l : leaves) {
-        const View& lv = NeedView(l);
+        auto nw = narrow_.find(l);
+        const View lv = state_[l].kind == ValState::kUnset && nw != narrow_.end() ? nw->second : NeedView(l);
         if (lv.rank() != t.rank()) throw std::string("jam: elementwise operand rank mismatch");
         st.bufs.push_back(lv.at());
         st.types.push_back(int32_t(lv.dtype));
@@ -2789,6 +2933,7 @@ class Lowerer {
       return;
     }
     if (n == "stablehlo.broadcast_in_dim" || n == "stablehlo.broadcast") {
+      if (PropagateNarrow(op)) return;
       const int src = op.operands[0];
       const TensorType& t = m_.types[res()];
       if (state_[src].kind == ValState::kScalar) {
@@ -2815,6 +2960,7 @@ class Lowerer {
       return;
     }
     if (n == "stablehlo.reshape") {
+      if (PropagateNarrow(op)) return;
       const int src = op.operands[0];
       if (state_[src].kind == ValState::kScalar) {
         state_[res()] = state_[src];
@@ -2834,6 +2980,7 @@ class Lowerer {
       return;
     }
     if (n == "stablehlo.transpose") {
+      if (PropagateNarrow(op)) return;
       const int src = op.operands[0];
       if (state_[src].kind == ValState::kScalar) {
         state_[res()] = state_[src];
@@ -2850,6 +2997,7 @@ class Lowerer {
       return;
     }
     if (n == "stablehlo.slice") {
+      if (PropagateNarrow(op)) return;
       const View& sv = NeedView(op.operands[0]);
       const auto st = attr_ints(op, {"start_indices"});
       const auto sd = attr_ints(op, {"strides"});
@@ -2861,6 +3009,13 @@ class Lowerer {
       }
       SetView(res(), v);
       return;
+    }
+    if (n == "stablehlo.convert") {
+      auto nw = narrow_.find(op.operands[0]);
+      if (nw != narrow_.end() && nw->second.dtype == m_.types[res()].dtype) {
+        SetView(res(), nw->second);  // bf16 -> f32 -> bf16: the narrow copy itself
+        return;
+      }
     }
     if (IsElementwise(n)) {
       ValState& s = state_[res()];
@@ -2937,11 +3092,15 @@ class Lowerer {
       const DType st_ = m_.types[src].dtype;
       if (st_ == DType::kBF16 || st_ == DType::kF16) x = src;
     }
-    const DType xt = m_.types[x].dtype;
+    // a sum over an f32 value with a narrow copy reads the copy (the same
+    // values; the kernel widens on load)
+    auto nw = narrow_.find(x);
+    const bool use_narrow = nw != narrow_.end() && m_.types[x].dtype == DType::kF32;
+    const DType xt = use_narrow ? nw->second.dtype : m_.types[x].dtype;
     const DType ot = m_.types[op.results[0]].dtype;
     if (!(xt == DType::kF32 || xt == DType::kBF16 || xt == DType::kF16))
       throw std::string("jam: reduce over ") + DTypeName(xt) + " is not supported";
-    View xv = NeedView(x);
+    View xv = use_narrow ? nw->second : NeedView(x);
     const auto dims = reduce_dims(op);
     // move reduced dims last (a transposed view), then make it dense
     std::vector<int> keep, red;
@@ -3103,6 +3262,13 @@ class Lowerer {
         return;
       }
     }
+    // an f32 product every reader rounds to bf16 is written in bf16 (one
+    // rounding of the fp32 accumulator, as the module's convert does)
+    bool narrow_out = false;
+    if (!epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res)) {
+      narrow_out = true;
+      d = NewTemp(size_t(m_.types[res].numel()) * 2);
+    }
     st.bufs = {lv.at(), rv.at(), d};
     int epilogue = 0;
     if (epi) {
@@ -3110,9 +3276,20 @@ class Lowerer {
       st.bufs.push_back(Densify(bv).at());
       epilogue = epi->relu ? 2 : 1;
     }
-    st.i = {int64_t(at), int64_t(ct), B, M, N, K, a_bs, a_ms, a_ks, b_bs, b_ks, b_ns, M * N, N, epilogue};
+    st.i = {int64_t(at), int64_t(narrow_out ? DType::kBF16 : ct), B, M, N, K, a_bs, a_ms, a_ks, b_bs, b_ks, b_ns,
+            M * N, N, epilogue};
     st.note = std::to_string(B) + "x" + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
+    if (narrow_out) st.note += " -> bf16";
     Emit(st);
+    if (narrow_out) {
+      View nv;
+      nv.buf = d;
+      nv.dtype = DType::kBF16;
+      nv.dims = m_.types[res].dims;
+      nv.strides = DenseStrides(nv.dims);
+      narrow_[res] = nv;
+      return;
+    }
     SetDenseView(res, d);
   }
 
@@ -3202,6 +3379,63 @@ class Lowerer {
     const auto dd = attr_ints(op, {"dim", "dimension"});
     const int64_t dim = dd.empty() ? 0 : dd[0];
     const TensorType& t = m_.types[op.results[0]];
+    // operands with narrow copies, read only narrow: when the copies already
+    // lie side by side along `dim` (gradients written into place by their
+    // kernel), the result is a view of them; else the concatenation is made
+    // of the narrow copies (half the bytes of the wide form)
+    bool narrow = NarrowOnly(op.results[0]);
+    for (int v : op.operands) narrow = narrow && narrow_.count(v);
+    if (narrow) {
+      const View& v0 = narrow_[op.operands[0]];
+      bool tiled = true;
+      int64_t at = 0;
+      for (int v : op.operands) {
+        const View& w = narrow_[v];
+        tiled = tiled && w.buf.space == v0.buf.space && w.buf.index == v0.buf.index &&
+                w.buf.offset == v0.buf.offset && w.dtype == v0.dtype && w.strides == v0.strides &&
+                w.offset == v0.offset + at * v0.strides[size_t(dim)];
+        for (int k = 0; tiled && k < t.rank(); ++k)
+          if (k != dim) tiled = w.dims[size_t(k)] == t.dims[size_t(k)];
+        at += m_.types[v].dims[size_t(dim)];
+      }
+      View rv = v0;
+      rv.dims = t.dims;
+      if (tiled) {
+        narrow_[op.results[0]] = rv;
+        return;
+      }
+      View out;
+      out.dtype = v0.dtype;
+      out.dims = t.dims;
+      out.strides = DenseStrides(t.dims);
+      out.buf = NewTemp(size_t(t.numel()) * DTypeBytes(v0.dtype));
+      // copy each operand into its block: a dense destination needs the
+      // blocks contiguous, so along an inner dim the narrow result is kept
+      // dim-major and handed out as a strided view (as below)
+      std::vector<int> order{int(dim)};
+      for (int k = 0; k < t.rank(); ++k)
+        if (k != dim) order.push_back(k);
+      int64_t off = 0;
+      for (int v : op.operands) {
+        const View& sv = narrow_[v];
+        View pv = sv;
+        for (size_t k = 0; k < order.size(); ++k) {
+          pv.dims[k] = sv.dims[size_t(order[k])];
+          pv.strides[k] = sv.strides[size_t(order[k])];
+        }
+        BufRef part = out.buf;
+        part.offset += off;
+        EmitCopy(pv, part);
+        off += m_.types[v].numel() * DTypeBytes(v0.dtype);
+      }
+      std::vector<int64_t> pdims;
+      for (int k : order) pdims.push_back(t.dims[size_t(k)]);
+      const std::vector<int64_t> ps = DenseStrides(pdims);
+      out.strides.assign(t.rank(), 0);
+      for (size_t k = 0; k < order.size(); ++k) out.strides[size_t(order[k])] = ps[k];
+      narrow_[op.results[0]] = out;
+      return;
+    }
     int64_t outer = 1;
     for (int64_t k = 0; k < dim; ++k) outer *= t.dims[k];
     if (outer != 1) {
@@ -3276,6 +3510,16 @@ class Lowerer {
       const bool bf16_out = m_.types[res].dtype == DType::kBF16 && !f.train;
       const int64_t n = od[0] * od[1] * od[2] * od[3];
       BufRef d = bf16_out ? DestFor(res) : NewTemp(size_t(n) * 2);
+      // in a training step whose f32 O is only read back in bf16 (the head
+      // merge [B,H,S,D] -> [B,S,H·D] ahead of the output projection), O is
+      // written in [B,S,H,D] order: the merge is then a dense view of it
+      const bool narrow = f.train && NarrowOnly(res);
+      View ov;
+      ov.buf = d;
+      ov.dtype = DType::kBF16;
+      ov.dims = od;
+      ov.strides = narrow ? std::vector<int64_t>{od[2] * od[1] * od[3], od[3], od[1] * od[3], 1}
+                          : DenseStrides(od);
       Step st;
       st.kind = StepKind::kSdpa;
       st.bufs = {qv.at(), kv.at(), vv.at(), d};
@@ -3283,7 +3527,7 @@ class Lowerer {
               qv.strides[0], qv.strides[1], qv.strides[2],
               kv.strides[0], kv.strides[1], kv.strides[2],
               vv.strides[0], vv.strides[1], vv.strides[2],
-              od[1] * od[2] * od[3], od[2] * od[3], od[3], f.causal ? 1 : 0};
+              ov.strides[0], ov.strides[1], ov.strides[2], f.causal ? 1 : 0};
       st.f = {f.scale};
       st.note = f.causal ? "causal" : "full";
       BufRef lse;
@@ -3293,9 +3537,11 @@ class Lowerer {
         st.note += " +lse";
       }
       Emit(st);
-      if (f.train) sdpa_saved_[anchor] = {d, lse};
+      if (f.train) sdpa_saved_[anchor] = {ov, lse};
       if (bf16_out) {
         SetDenseView(res, d);
+      } else if (narrow) {
+        narrow_[res] = ov;
       } else {
         BufRef o = DestFor(res);
         EmitConvert(d, DType::kBF16, o, m_.types[res].dtype, n);
@@ -3310,15 +3556,21 @@ class Lowerer {
       if (!lab.dense()) lab = Densify(lab);
       const int res = op.results[0];
       BufRef lr = DestFor(res);
-      BufRef dx = DestFor(f.dlogits);
+      const bool to_bf16 = !f.dlogits_bf16.empty();
+      BufRef dx = DestFor(to_bf16 ? f.dlogits_bf16[0] : f.dlogits);
       Step st;
       st.kind = StepKind::kSoftmaxXent;
       st.bufs = {x.at(), lab.at(), lr, dx};
-      st.i = {int64_t(x.dtype), x.dims[0], x.dims[1], int64_t(lab.dtype)};
+      st.i = {int64_t(x.dtype), x.dims[0], x.dims[1], int64_t(lab.dtype),
+              int64_t(to_bf16 ? DType::kBF16 : x.dtype)};
       st.f = {f.scale};
       Emit(st);
       SetDenseView(res, lr);
-      SetDenseView(f.dlogits, dx);
+      if (to_bf16) {
+        for (int c : f.dlogits_bf16) SetDenseView(c, dx);
+      } else {
+        SetDenseView(f.dlogits, dx);
+      }
       return;
     }
     if (f.kind == Fused::kSdpaBwd) {
@@ -3332,29 +3584,59 @@ class Lowerer {
       if (it == sdpa_saved_.end()) throw std::string("jam: attention backward before its forward");
       const int64_t B = qv.dims[0], H = qv.dims[1], Sq = qv.dims[2], Sk = kv.dims[2], D = qv.dims[3];
       BufRef ws = NewTemp(mk_sdpa_bwd_workspace_bytes(B, H, Sq, Sk, D));
-      BufRef dqb = NewTemp(size_t(B * H * Sq * D) * 2), dkb = NewTemp(size_t(B * H * Sk * D) * 2),
-             dvb = NewTemp(size_t(B * H * Sk * D) * 2);
+      const View& ov = it->second.first;
+      // the gradients (bf16 from the kernel, f32 in the module): when each is
+      // only read back in bf16 and the three are merged to [B,S,H·D] and
+      // concatenated along the features (the fused QKV projection's
+      // gradient), they are written straight into that [B·S, 3·H·D] layout
+      const int grads_v[3] = {f.dq, f.dk, f.dv};
+      const int merged = MergedQkvConcat(grads_v, B, H, Sq, D);
+      View gview[3];
+      if (merged >= 0 && Sq == Sk) {
+        BufRef buf = NewTemp(size_t(B * Sq * 3 * H * D) * 2);
+        for (int k = 0; k < 3; ++k) {
+          gview[k].buf = buf;
+          gview[k].dtype = DType::kBF16;
+          gview[k].dims = {B, H, Sq, D};
+          gview[k].strides = {Sq * 3 * H * D, D, 3 * H * D, 1};
+          gview[k].offset = int64_t(k) * H * D;
+        }
+      } else {
+        for (int k = 0; k < 3; ++k) {
+          const int64_t S_k = k == 0 ? Sq : Sk;
+          gview[k].buf = NewTemp(size_t(B * H * S_k * D) * 2);
+          gview[k].dtype = DType::kBF16;
+          gview[k].dims = {B, H, S_k, D};
+          gview[k].strides = DenseStrides(gview[k].dims);
+        }
+      }
       Step st;
       st.kind = StepKind::kSdpaBwd;
-      st.bufs = {qv.at(), kv.at(), vv.at(), it->second.first, gv.at(), it->second.second, dqb, dkb, dvb, ws};
+      st.bufs = {qv.at(), kv.at(), vv.at(), ov.at(), gv.at(), it->second.second,
+                 gview[0].at(), gview[1].at(), gview[2].at(), ws};
       st.i = {B, H, Sq, Sk, D,
               qv.strides[0], qv.strides[1], qv.strides[2],
               kv.strides[0], kv.strides[1], kv.strides[2],
               vv.strides[0], vv.strides[1], vv.strides[2],
-              H * Sq * D, Sq * D, D,
+              ov.strides[0], ov.strides[1], ov.strides[2],
               gv.strides[0], gv.strides[1], gv.strides[2],
-              H * Sq * D, Sq * D, D,
-              H * Sk * D, Sk * D, D,
-              H * Sk * D, Sk * D, D,
+              gview[0].strides[0], gview[0].strides[1], gview[0].strides[2],
+              gview[1].strides[0], gview[1].strides[1], gview[1].strides[2],
+              gview[2].strides[0], gview[2].strides[1], gview[2].strides[2],
               f.causal ? 1 : 0};
       st.f = {f.scale};
-      st.note = f.causal ? "causal" : "full";
+      st.note = std::string(f.causal ? "causal" : "full") + (merged >= 0 ? ", into the merged QKV gradient" : "");
       Emit(st);
-      const std::pair<int, BufRef> grads[3] = {{f.dq, dqb}, {f.dk, dkb}, {f.dv, dvb}};
-      for (const auto& gr : grads) {
-        BufRef o = DestFor(gr.first);
-        EmitConvert(gr.second, DType::kBF16, o, m_.types[gr.first].dtype, m_.types[gr.first].numel());
-        SetDenseView(gr.first, o);
+      for (int k = 0; k < 3; ++k) {
+        const int g = grads_v[k];
+        if (m_.types[g].dtype == DType::kF32 && NarrowOnly(g)) {
+          narrow_[g] = gview[k];
+          continue;
+        }
+        const View src = gview[k].dense() ? gview[k] : Densify(gview[k]);
+        BufRef o = DestFor(g);
+        EmitConvert(src.at(), DType::kBF16, o, m_.types[g].dtype, m_.types[g].numel());
+        SetDenseView(g, o);
       }
       return;
     }
@@ -3452,7 +3734,9 @@ class Lowerer {
   std::map<int, Fused> fused_;
   std::set<int> absorbed_;
   std::vector<bool> reach_;
-  std::map<int, std::pair<BufRef, BufRef>> sdpa_saved_;  // training forward anchor -> (bf16 O, lse)
+  std::map<int, std::pair<View, BufRef>> sdpa_saved_;  // training forward anchor -> (bf16 O view, lse)
+  std::unordered_map<int, View> narrow_;   // f32 value -> bf16 view of the same values
+  std::unordered_map<int, bool> narrow_only_;
   std::vector<bool> live_;
   std::vector<Temp> temps_;
   std::vector<bool> out_written_;

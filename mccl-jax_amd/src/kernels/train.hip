@@ -711,6 +711,134 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   }
 }
 
+// fp32 logits, bf16 dlogits (the gradient only feeds bf16 products): one
+// workgroup of kXentF32Threads per row, the row held in registers (NPT
+// elements per thread, element j on thread j % kXentF32Threads), read once
+// with coalesced loads; exact row max, then the sum of exp(x - max), then
+// dlogits = (exp(x - lse) - [j == label]) * grad_scale stored as bf16.
+constexpr int kXentF32Threads = 1024;
+
+template <int NPT, typename L>
+__global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_kernel(
+    const float* __restrict__ logits, int64_t cols, const L* __restrict__ labels, float grad_scale,
+    float* __restrict__ loss, uint16_t* __restrict__ dlogits) {
+  constexpr int NW = kXentF32Threads / 64;
+  constexpr float kL2e = 1.4426950408889634f;
+  __shared__ float red[NW];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const float* xr = logits + row * cols;
+  uint16_t* dr = dlogits + row * cols;
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  const float xlab = xr[lab_ok ? lab : 0];
+  float x[NPT];
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int64_t j = t + int64_t(k) * kXentF32Threads;
+    x[k] = j < cols ? xr[j] : -INFINITY;
+  }
+  auto block_reduce = [&](float v, bool is_max) __attribute__((always_inline)) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    if (lane == 0) red[wv] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    __syncthreads();
+    return r;
+  };
+  float m = x[0];
+#pragma unroll
+  for (int k = 1; k < NPT; ++k) m = fmaxf(m, x[k]);
+  const float M = block_reduce(m, true);
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) sum += __builtin_amdgcn_exp2f((x[k] - M) * kL2e);
+  const float S = block_reduce(sum, false);
+  const float lse = M + __logf(S);
+  const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - xlab : lse;
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int64_t j = t + int64_t(k) * kXentF32Threads;
+    if (j < cols) {
+      const float pr = __builtin_amdgcn_exp2f(fmaf(x[k] - M, kL2e, -ls2));
+      dr[j] = f32_to_bf16((j == lab ? pr - 1.f : pr) * grad_scale);
+    }
+  }
+}
+
+// The same for rows longer than the registers hold (more than 32
+// elements per thread): the row is streamed twice in chunks of C elements
+// per thread.  Pass 1 keeps a running (max, sum of exp) per thread, raised
+// once per chunk; pass 2 re-reads the row (from the L2 / MALL, where one
+// row per CU stays resident between the passes) and writes dlogits.
+template <int C, typename L>
+__global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_stream_kernel(
+    const float* __restrict__ logits, int64_t cols, const L* __restrict__ labels, float grad_scale,
+    float* __restrict__ loss, uint16_t* __restrict__ dlogits) {
+  constexpr int NW = kXentF32Threads / 64;
+  constexpr float kL2e = 1.4426950408889634f;
+  constexpr int64_t kChunk = int64_t(C) * kXentF32Threads;
+  __shared__ float red[NW];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const float* xr = logits + row * cols;
+  uint16_t* dr = dlogits + row * cols;
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  const float xlab = xr[lab_ok ? lab : 0];
+  float m = -INFINITY, sum = 0.f;  // running max and sum of exp2((x - m) log2 e)
+  for (int64_t c0 = 0; c0 < cols; c0 += kChunk) {
+    float x[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      const int64_t j = c0 + t + int64_t(k) * kXentF32Threads;
+      x[k] = j < cols ? xr[j] : -INFINITY;
+    }
+    float cm = x[0];
+#pragma unroll
+    for (int k = 1; k < C; ++k) cm = fmaxf(cm, x[k]);
+    const float mn = fmaxf(m, cm);
+    if (mn != -INFINITY) {
+      float cs = 0.f;
+#pragma unroll
+      for (int k = 0; k < C; ++k) cs += __builtin_amdgcn_exp2f((x[k] - mn) * kL2e);
+      sum = (m == -INFINITY ? 0.f : sum * __builtin_amdgcn_exp2f((m - mn) * kL2e)) + cs;
+      m = mn;
+    }
+  }
+  // combine (m, sum) over the workgroup
+  const float wm = wave_max(m);
+  const float ws = wave_sum(m == -INFINITY ? 0.f : sum * __builtin_amdgcn_exp2f((m - wm) * kL2e));
+  __shared__ float red_s[NW];
+  if (lane == 0) {
+    red[wv] = wm;
+    red_s[wv] = ws;
+  }
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, red[w]);
+  float S = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) S += red[w] == -INFINITY ? 0.f : red_s[w] * __builtin_amdgcn_exp2f((red[w] - M) * kL2e);
+  const float lse = M + __logf(S);
+  const float ls2 = __builtin_amdgcn_logf(S);
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - xlab : lse;
+  for (int64_t c0 = 0; c0 < cols; c0 += kChunk) {
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      const int64_t j = c0 + t + int64_t(k) * kXentF32Threads;
+      if (j < cols) {
+        const float pr = __builtin_amdgcn_exp2f(fmaf(xr[j] - M, kL2e, -ls2));
+        dr[j] = f32_to_bf16((j == lab ? pr - 1.f : pr) * grad_scale);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- Adam
 // fp32 gradient, four parameters per thread per trip (16-byte loads and
 // stores; the bf16 copy as one 8-byte store); same arithmetic as adam_kernel.
@@ -1154,6 +1282,53 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     parts[n] = a.part_s; outs[n++] = dx_colsum;
   }
   return n ? col_final(s, n, parts, outs, nb, cols) : MK_OK;
+}
+
+extern "C" int mk_softmax_xent_typed(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
+                                     const void* logits, int label_type, const void* labels, float grad_scale,
+                                     float* loss_rows, void* dlogits) {
+  if (logits_type == dlogits_type)
+    return mk_softmax_xent(stream, logits_type, rows, cols, logits, label_type, labels, grad_scale, loss_rows,
+                           dlogits);
+  clear_error();
+  if (logits_type != MK_F32 || dlogits_type != MK_BF16)
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: mixed types need f32 logits and bf16 dlogits");
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_softmax_xent_typed: bad shape");
+  if (rows == 0) return MK_OK;
+  if (rows >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: too many rows");
+  if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent_typed: null pointer");
+  if (label_type != MK_S32 && label_type != MK_S64)
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: labels must be s32/s64");
+  hipStream_t s = as_stream(stream);
+  const int64_t npt = (cols + kXentF32Threads - 1) / kXentF32Threads;
+  auto launch = [&](auto nt) {
+    constexpr int NPT = decltype(nt)::value;
+    if (label_type == MK_S32)
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int32_t>), dim3(unsigned(rows)), dim3(kXentF32Threads), 0,
+                         s, (const float*)logits, cols, (const int32_t*)labels, grad_scale, loss_rows,
+                         (uint16_t*)dlogits);
+    else
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int64_t>), dim3(unsigned(rows)), dim3(kXentF32Threads), 0,
+                         s, (const float*)logits, cols, (const int64_t*)labels, grad_scale, loss_rows,
+                         (uint16_t*)dlogits);
+  };
+  if (npt <= 8) {
+    launch(IntC<8>{});
+  } else if (npt <= 16) {
+    launch(IntC<16>{});
+  } else if (npt <= 24) {
+    launch(IntC<24>{});
+  } else {
+    if (label_type == MK_S32)
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int32_t>), dim3(unsigned(rows)),
+                         dim3(kXentF32Threads), 0, s, (const float*)logits, cols, (const int32_t*)labels, grad_scale,
+                         loss_rows, (uint16_t*)dlogits);
+    else
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int64_t>), dim3(unsigned(rows)),
+                         dim3(kXentF32Threads), 0, s, (const float*)logits, cols, (const int64_t*)labels, grad_scale,
+                         loss_rows, (uint16_t*)dlogits);
+  }
+  return check_launch("mk_softmax_xent_typed");
 }
 
 extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,

@@ -12,6 +12,8 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import bf16
+
 pytestmark = pytest.mark.gpu
 
 
@@ -375,6 +377,34 @@ def test_softmax_xent_bf16_shapes(K, rows, cols):
     want_loss = lse - torch.where(ok, xr[torch.arange(rows), lab.clamp(0, cols - 1).long()], 0.0)
     np.testing.assert_allclose(_f64(loss), want_loss, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(_f64(dl), want_grad, rtol=2 ** -7, atol=1e-30)
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 1000), (5, 20011), (4, 50257), (2, 70001)])
+def test_softmax_xent_f32_logits_bf16_dlogits(K, rows, cols):
+    """fp32 logits with a bf16 gradient (mk_softmax_xent_typed): registers
+    for up to 24 elements per thread, the two-pass streaming kernel above;
+    the loss as the fp32 kernel's to 1e-5 relative, the gradient within
+    one bf16 ulp of the float64 value; out-of-range labels (-1 and cols)."""
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = torch.randn(rows, cols, generator=g) * 3
+    x[0, 1] = float("-inf")
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int32)
+    lab[-1] = cols
+    lab[0] = -1
+    dl = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")
+    loss, dl = K.softmax_xent(x.cuda(), lab.cuda(), 1.0 / rows, dlogits=dl)
+    xr = x.double()
+    lse = torch.logsumexp(xr, -1)
+    ok = (lab >= 0) & (lab < cols)
+    want_loss = lse - torch.where(ok, xr[torch.arange(rows), lab.clamp(0, cols - 1).long()], 0.0)
+    np.testing.assert_allclose(_f64(loss), want_loss, rtol=1e-5, atol=1e-5)
+    p = torch.softmax(xr, -1)
+    onehot = torch.zeros_like(p)
+    onehot[torch.arange(rows)[ok], lab[ok].long()] = 1.0
+    want = ((p - onehot) / rows).numpy()
+    got = bf16.from_bf16_bits(dl.cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-7 * np.abs(want).max())
 
 
 def test_softmax_xent_bf16_dlogits_offset_view(K):
