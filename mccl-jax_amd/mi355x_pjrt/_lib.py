@@ -50,6 +50,7 @@ SIGNATURES = {
     "mk_layernorm": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _F, _P]),
     "mk_gelu_tanh": (_I, [_P, _I, _I64, _P, _P]),
     "mk_ew_program": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P]),
+    "mk_ew_program_multi": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "mk_gather_rows": (_I, [_P, _I64, _I64, _P, _I, _I64, _P, _P]),
     "mk_scatter_add_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "mk_scatter_add_rows": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _P, _P, _P, _P]),
@@ -75,6 +76,7 @@ SIGNATURES = {
     "mk_adam_update_dev": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P, _P, ctypes.c_double, ctypes.c_double,
                                 ctypes.c_double]),
     "mk_softmax_xent": (_I, [_P, _I, _I64, _I64, _P, _I, _P, _F, _P, _P]),
+    "mk_softmax_xent_typed": (_I, [_P, _I, _I, _I64, _I64, _P, _I, _P, _F, _P, _P]),
     "mk_adam_update": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P] + [ctypes.c_double] * 6),
     "mk_sdpa_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "mk_sdpa_bwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64]
