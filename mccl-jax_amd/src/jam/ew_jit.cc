@@ -1,0 +1,599 @@
+#include "jam/ew_jit.h"
+
+#include <hip/hip_runtime_api.h>
+#include <dlfcn.h>
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <array>
+#include <chrono>
+#include <cinttypes>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+#include <type_traits>
+#include <unordered_map>
+
+#include "jam/program.h"
+#include "mk_kernels.h"
+
+namespace mi::jam {
+namespace {
+
+constexpr int kMaxRank = 6;
+constexpr int kMaxRegs = 32;  // the interpreter's register file; programs are checked against it
+constexpr int kMaxInputs = 8;
+constexpr int kMaxOutputs = 4;
+constexpr int kLanes = 4;     // consecutive elements per thread when the innermost dim allows
+
+// Helpers every generated kernel uses.  The conversions are the kernel
+// library's (mk_common.h): bf16 widening by shift, narrowing by the hardware
+// RNE conversion of __bf16, f16 through _Float16; max / min propagate NaN.
+// The f16 conversions pass their fp32 side through an empty asm so that the
+// compiler cannot fold them with a neighbouring multiply into a mixed-
+// precision FMA with a +0 addend (v_fma_mix), which turns a -0 product into
+// +0; the interpreter converts separately, and so must these kernels.
+const char kPreamble[] = R"(typedef float mkj_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mkj_u2 __attribute__((ext_vector_type(2)));
+static __device__ __forceinline__ float mkj_f(int i) { return __builtin_bit_cast(float, i); }
+static __device__ __forceinline__ float mkj_fu(unsigned u) { return __builtin_bit_cast(float, u); }
+static __device__ __forceinline__ int mkj_i(float f) { return __builtin_bit_cast(int, f); }
+static __device__ __forceinline__ float mkj_bf2f(unsigned short h) { return mkj_fu(unsigned(h) << 16); }
+static __device__ __forceinline__ unsigned short mkj_f2bf(float f) { return __builtin_bit_cast(unsigned short, static_cast<__bf16>(f)); }
+static __device__ __forceinline__ float mkj_h2f(unsigned short h) { float f = float(__builtin_bit_cast(_Float16, h)); asm("" : "+v"(f)); return f; }
+static __device__ __forceinline__ unsigned short mkj_f2h(float f) { asm("" : "+v"(f)); return __builtin_bit_cast(unsigned short, static_cast<_Float16>(f)); }
+static __device__ __forceinline__ float mkj_sign(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : x); }
+static __device__ __forceinline__ float mkj_max(float x, float y) { return (x != x || y != y) ? __builtin_nanf("") : fmaxf(x, y); }
+static __device__ __forceinline__ float mkj_min(float x, float y) { return (x != x || y != y) ? __builtin_nanf("") : fminf(x, y); }
+static __device__ __forceinline__ int mkj_smax(int x, int y) { return x > y ? x : y; }
+static __device__ __forceinline__ int mkj_smin(int x, int y) { return x < y ? x : y; }
+)";
+
+// Scalar load of element `o` of `p` into the register convention of the
+// interpreter: float types widen to fp32, integer types hold their int32 bit
+// pattern (64-bit truncated), predicates 0 / 1.
+bool LoadExpr(int t, const std::string& p, const std::string& o, std::string* e) {
+  auto at = [&](const char* ty) { return "((const " + std::string(ty) + "*)" + p + ")[" + o + "]"; };
+  switch (t) {
+    case MK_F32: *e = at("float"); return true;
+    case MK_BF16: *e = "mkj_bf2f(" + at("unsigned short") + ")"; return true;
+    case MK_F16: *e = "mkj_h2f(" + at("unsigned short") + ")"; return true;
+    case MK_F64: *e = "float(" + at("double") + ")"; return true;
+    case MK_PRED: *e = "(" + at("unsigned char") + " ? 1.f : 0.f)"; return true;
+    case MK_S8: *e = "mkj_f(int(" + at("signed char") + "))"; return true;
+    case MK_U8: *e = "mkj_f(int(" + at("unsigned char") + "))"; return true;
+    case MK_S16: *e = "mkj_f(int(" + at("short") + "))"; return true;
+    case MK_U16: *e = "mkj_f(int(" + at("unsigned short") + "))"; return true;
+    case MK_S32: case MK_U32: *e = "mkj_f(" + at("int") + ")"; return true;
+    case MK_S64: case MK_U64: *e = "mkj_f(int(" + at("long long") + "))"; return true;
+    default: return false;
+  }
+}
+
+// Store of fp32 register value `v` as element `o` of `q` (the interpreter's
+// ew_store).
+bool StoreStmt(int t, const std::string& q, const std::string& o, const std::string& v, std::string* s) {
+  auto at = [&](const char* ty) { return "((" + std::string(ty) + "*)" + q + ")[" + o + "] = "; };
+  switch (t) {
+    case MK_F32: *s = at("float") + v + ";"; return true;
+    case MK_BF16: *s = at("unsigned short") + "mkj_f2bf(" + v + ");"; return true;
+    case MK_F16: *s = at("unsigned short") + "mkj_f2h(" + v + ");"; return true;
+    case MK_F64: *s = at("double") + "double(" + v + ");"; return true;
+    case MK_PRED: *s = at("unsigned char") + "(" + v + " != 0.f);"; return true;
+    case MK_S8: case MK_U8: *s = at("unsigned char") + "(unsigned char)mkj_i(" + v + ");"; return true;
+    case MK_S16: case MK_U16: *s = at("unsigned short") + "(unsigned short)mkj_i(" + v + ");"; return true;
+    case MK_S32: case MK_U32: *s = at("int") + "mkj_i(" + v + ");"; return true;
+    case MK_S64: *s = at("long long") + "(long long)mkj_i(" + v + ");"; return true;
+    case MK_U64: *s = at("unsigned long long") + "(unsigned long long)(unsigned)mkj_i(" + v + ");"; return true;
+    default: return false;
+  }
+}
+
+std::string FloatLit(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  char b[32];
+  snprintf(b, sizeof b, "mkj_fu(0x%08xu)", u);
+  return b;
+}
+
+// The fp32 expression of one instruction (the interpreter's ew_run case for
+// its opcode) over operand names a, b, c.  Integer arithmetic wraps through
+// unsigned, which is what the interpreter's int32 operations compile to.
+bool InstrExpr(int op, const std::string& a, const std::string& b, const std::string& c, std::string* e) {
+  auto cmp = [&](const char* rel) { return "(" + a + " " + rel + " " + b + " ? 1.f : 0.f)"; };
+  auto icmp = [&](const char* rel) { return "(mkj_i(" + a + ") " + rel + " mkj_i(" + b + ") ? 1.f : 0.f)"; };
+  auto iop = [&](const char* o) {
+    return "mkj_f(int(unsigned(mkj_i(" + a + ")) " + o + " unsigned(mkj_i(" + b + "))))";
+  };
+  switch (op) {
+    case MK_EW_ADD: *e = "(" + a + " + " + b + ")"; return true;
+    case MK_EW_SUB: *e = "(" + a + " - " + b + ")"; return true;
+    case MK_EW_MUL: *e = "(" + a + " * " + b + ")"; return true;
+    case MK_EW_DIV: *e = "(" + a + " / " + b + ")"; return true;
+    case MK_EW_MAX: *e = "mkj_max(" + a + ", " + b + ")"; return true;
+    case MK_EW_MIN: *e = "mkj_min(" + a + ", " + b + ")"; return true;
+    case MK_EW_POW: *e = "powf(" + a + ", " + b + ")"; return true;
+    case MK_EW_NEG: *e = "(-" + a + ")"; return true;
+    case MK_EW_EXP: *e = "expf(" + a + ")"; return true;
+    case MK_EW_LOG: *e = "logf(" + a + ")"; return true;
+    case MK_EW_TANH: *e = "tanhf(" + a + ")"; return true;
+    case MK_EW_SQRT: *e = "sqrtf(" + a + ")"; return true;
+    case MK_EW_RSQRT: *e = "(1.f / sqrtf(" + a + "))"; return true;
+    case MK_EW_ABS: *e = "fabsf(" + a + ")"; return true;
+    case MK_EW_LOGISTIC: *e = "(1.f / (1.f + expf(-" + a + ")))"; return true;
+    case MK_EW_CMP_EQ: *e = cmp("=="); return true;
+    case MK_EW_CMP_NE: *e = cmp("!="); return true;
+    case MK_EW_CMP_LT: *e = cmp("<"); return true;
+    case MK_EW_CMP_LE: *e = cmp("<="); return true;
+    case MK_EW_CMP_GT: *e = cmp(">"); return true;
+    case MK_EW_CMP_GE: *e = cmp(">="); return true;
+    case MK_EW_SELECT: *e = "(" + a + " != 0.f ? " + b + " : " + c + ")"; return true;
+    case MK_EW_CLAMP: *e = "fminf(fmaxf(" + a + ", " + b + "), " + c + ")"; return true;
+    case MK_EW_ROUND_BF16: *e = "mkj_bf2f(mkj_f2bf(" + a + "))"; return true;
+    case MK_EW_ROUND_F16: *e = "mkj_h2f(mkj_f2h(" + a + "))"; return true;
+    case MK_EW_FLOOR: *e = "floorf(" + a + ")"; return true;
+    case MK_EW_CEIL: *e = "ceilf(" + a + ")"; return true;
+    case MK_EW_SIGN: *e = "mkj_sign(" + a + ")"; return true;
+    case MK_EW_AND: *e = "((" + a + " != 0.f && " + b + " != 0.f) ? 1.f : 0.f)"; return true;
+    case MK_EW_OR: *e = "((" + a + " != 0.f || " + b + " != 0.f) ? 1.f : 0.f)"; return true;
+    case MK_EW_NOT: *e = "(" + a + " == 0.f ? 1.f : 0.f)"; return true;
+    case MK_EW_MOV: *e = a; return true;
+    case MK_EW_CMP_LT_S32: *e = icmp("<"); return true;
+    case MK_EW_CMP_GE_S32: *e = icmp(">="); return true;
+    case MK_EW_ADD_S32: *e = iop("+"); return true;
+    case MK_EW_SUB_S32: *e = iop("-"); return true;
+    case MK_EW_MUL_S32: *e = iop("*"); return true;
+    case MK_EW_S32_TO_F32: *e = "float(mkj_i(" + a + "))"; return true;
+    case MK_EW_F32_TO_S32: *e = "mkj_f(int(" + a + "))"; return true;
+    case MK_EW_ERF: *e = "erff(" + a + ")"; return true;
+    case MK_EW_CMP_EQ_S32: *e = icmp("=="); return true;
+    case MK_EW_CMP_NE_S32: *e = icmp("!="); return true;
+    case MK_EW_CMP_LE_S32: *e = icmp("<="); return true;
+    case MK_EW_CMP_GT_S32: *e = icmp(">"); return true;
+    case MK_EW_MAX_S32: *e = "mkj_f(mkj_smax(mkj_i(" + a + "), mkj_i(" + b + ")))"; return true;
+    case MK_EW_MIN_S32: *e = "mkj_f(mkj_smin(mkj_i(" + a + "), mkj_i(" + b + ")))"; return true;
+    case MK_EW_NEG_S32: *e = "mkj_f(int(0u - unsigned(mkj_i(" + a + "))))"; return true;
+    case MK_EW_AND_B32: *e = "mkj_f(mkj_i(" + a + ") & mkj_i(" + b + "))"; return true;
+    case MK_EW_OR_B32: *e = "mkj_f(mkj_i(" + a + ") | mkj_i(" + b + "))"; return true;
+    case MK_EW_XOR_B32: *e = "mkj_f(mkj_i(" + a + ") ^ mkj_i(" + b + "))"; return true;
+    case MK_EW_PRED_TO_S32: *e = "mkj_f(" + a + " != 0.f ? 1 : 0)"; return true;
+    case MK_EW_S32_TO_PRED: *e = "(mkj_i(" + a + ") != 0 ? 1.f : 0.f)"; return true;
+    case MK_EW_U32_TO_F32: *e = "float(unsigned(mkj_i(" + a + ")))"; return true;
+    default: return false;
+  }
+}
+
+uint64_t Fnv1a(const std::string& s) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+void ReplaceAll(std::string& s, const std::string& from, const std::string& to) {
+  for (size_t p = s.find(from); p != std::string::npos; p = s.find(from, p + to.size())) s.replace(p, from.size(), to);
+}
+
+}  // namespace
+
+// Step encoding (lower.cc EmitEwGroup): bufs = inputs then outputs; i = rank,
+// dims[6], n_inputs, (out_reg, out_type) per output; prog 4 ints per
+// instruction; strides 6 per input; types per input; f = constants.
+bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
+  auto no = [&](const std::string& w) {
+    *why = w;
+    return false;
+  };
+  if (s.kind != StepKind::kEw || s.i.size() < 8) return no("not an ew step");
+  const int rank = int(s.i[0]);
+  const int n_in = int(s.i[7]);
+  const int n_out = int(s.bufs.size()) - n_in;
+  if (rank < 0 || rank > kMaxRank) return no("rank");
+  if (n_in < 0 || n_in > kMaxInputs || n_out < 1 || n_out > kMaxOutputs) return no("operand count");
+  if (s.i.size() != size_t(8 + 2 * n_out) || s.strides.size() != size_t(kMaxRank * n_in) ||
+      s.types.size() != size_t(n_in) || s.prog.size() % 4 != 0)
+    return no("malformed step");
+  int64_t dims[kMaxRank];
+  int64_t n = 1;
+  for (int d = 0; d < rank; ++d) {
+    dims[d] = s.i[1 + size_t(d)];
+    if (dims[d] < 0) return no("negative dim");
+    n *= dims[d];
+  }
+  k->align.assign(s.bufs.size(), 1);
+  if (n == 0) {
+    k->blocks = 0;
+    k->name.clear();
+    k->source.clear();
+    return true;
+  }
+  // inputs: the interpreter's modes (size-1 dims never contribute)
+  enum Mode { kScalar, kDense, kStrided };
+  std::vector<Mode> mode(static_cast<size_t>(n_in));
+  std::vector<std::array<int64_t, kMaxRank>> st(static_cast<size_t>(n_in));
+  bool narrow = rank >= 1 && n < (int64_t(1) << 31);
+  for (int t = 0; t < n_in; ++t) {
+    int64_t expect = 1, hi = 0;
+    bool dense = true, scalar = true;
+    for (int d = rank - 1; d >= 0; --d) {
+      const int64_t v = dims[d] == 1 ? 0 : s.strides[size_t(t * kMaxRank + d)];
+      st[size_t(t)][size_t(d)] = v;
+      if (dims[d] != 1 && v != expect) dense = false;
+      if (dims[d] != 1 && v != 0) scalar = false;
+      if (v < 0) narrow = false;
+      hi += (dims[d] - 1) * v;
+      expect *= dims[d];
+    }
+    if (hi >= (int64_t(1) << 31) - kLanes) narrow = false;
+    mode[size_t(t)] = scalar ? kScalar : (dense ? kDense : kStrided);
+    std::string probe;
+    if (!LoadExpr(s.types[size_t(t)], "p", "0", &probe)) return no("input dtype");
+  }
+  std::vector<int> out_reg(static_cast<size_t>(n_out)), out_type(static_cast<size_t>(n_out));
+  for (int o = 0; o < n_out; ++o) {
+    out_reg[size_t(o)] = int(s.i[8 + 2 * size_t(o)]);
+    out_type[size_t(o)] = int(s.i[9 + 2 * size_t(o)]);
+    std::string probe;
+    if (out_reg[size_t(o)] < 0 || out_reg[size_t(o)] >= kMaxRegs) return no("output register");
+    if (!StoreStmt(out_type[size_t(o)], "q", "0", "v", &probe)) return no("output dtype");
+  }
+  const int lanes = rank >= 1 && dims[rank - 1] % kLanes == 0 ? kLanes : 1;
+  const int64_t threads = n / lanes;
+  const int64_t blocks = (threads + kEwJitBlock - 1) / kEwJitBlock;
+  if (blocks >= (int64_t(1) << 31)) return no("grid too large");
+  const std::string IT = narrow ? "unsigned" : "long long";
+  const std::string U = narrow ? "u" : "ll";
+
+  std::ostringstream src;
+  // ---- the program as a straight-line function of one element's inputs
+  {
+    std::string reg[kMaxRegs];
+    for (int r = 0; r < kMaxRegs; ++r) reg[r] = r < n_in ? "x" + std::to_string(r) : "0.f";
+    src << "static __device__ __forceinline__ void @K@_body(";
+    for (int t = 0; t < n_in; ++t) src << "float x" << t << ", ";
+    src << "float* y) {\n#pragma clang fp contract(off)\n";
+    const size_t n_instr = s.prog.size() / 4;
+    for (size_t p = 0; p < n_instr; ++p) {
+      const int op = s.prog[4 * p], dst = s.prog[4 * p + 1], a = s.prog[4 * p + 2], b = s.prog[4 * p + 3];
+      if (dst < 0 || dst >= kMaxRegs) return no("destination register");
+      std::string e;
+      if (op == MK_EW_CONST) {
+        if (a < 0 || size_t(a) >= s.f.size()) return no("constant index");
+        e = FloatLit(s.f[size_t(a)]);
+      } else {
+        const int rb = b & 0xffff, rc = (b >> 16) & 0xffff;
+        if (a < 0 || a >= kMaxRegs || rb >= kMaxRegs || rc >= kMaxRegs) return no("source register");
+        if (!InstrExpr(op, reg[a], reg[rb], reg[rc], &e)) return no("opcode " + std::to_string(op));
+      }
+      src << "  const float v" << p << " = " << e << ";\n";
+      reg[dst] = "v" + std::to_string(p);
+    }
+    for (int o = 0; o < n_out; ++o) src << "  y[" << o << "] = " << reg[out_reg[size_t(o)]] << ";\n";
+    src << "}\n";
+  }
+  // ---- the entry: index, loads, lanes, stores
+  src << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(";
+  for (int t = 0; t < n_in; ++t) src << "const void* p" << t << ", ";
+  for (int o = 0; o < n_out; ++o) src << "void* q" << o << (o + 1 < n_out ? ", " : ") {\n");
+  if (narrow)
+    src << "  const unsigned i0 = (blockIdx.x * " << kEwJitBlock << "u + threadIdx.x) * " << lanes << "u;\n";
+  else
+    src << "  const long long i0 = ((long long)blockIdx.x * " << kEwJitBlock << " + threadIdx.x) * " << lanes << ";\n";
+  src << "  if (i0 >= " << n << U << ") return;\n";
+  // multi-dim index: only as far out as some strided input needs
+  int lo = rank;
+  for (int t = 0; t < n_in; ++t)
+    if (mode[size_t(t)] == kStrided)
+      for (int d = 0; d < rank; ++d)
+        if (st[size_t(t)][size_t(d)] != 0) lo = std::min(lo, d);
+  if (lo < rank) {
+    src << "  " << IT << " r_ = i0;\n";
+    for (int d = rank - 1; d >= lo; --d) {
+      if (d == 0) {
+        src << "  const " << IT << " d0 = r_;\n";
+      } else {
+        src << "  const " << IT << " d" << d << " = r_ % " << dims[d] << U << ";\n";
+        if (d > lo) src << "  r_ /= " << dims[d] << U << ";\n";
+      }
+    }
+  }
+  // per input and lane: the fp32 value name
+  std::vector<std::array<std::string, kLanes>> x(static_cast<size_t>(n_in));
+  for (int t = 0; t < n_in; ++t) {
+    const int ty = s.types[size_t(t)];
+    const std::string p = "p" + std::to_string(t);
+    const std::string tn = std::to_string(t);
+    std::string off, e;
+    int64_t step = 0;
+    if (mode[size_t(t)] == kScalar) {
+      LoadExpr(ty, p, "0", &e);
+      src << "  const float x" << tn << " = " << e << ";\n";
+      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "x" + tn;
+      continue;
+    }
+    if (mode[size_t(t)] == kDense) {
+      off = "i0";
+      step = 1;
+    } else {
+      std::string sum;
+      for (int d = lo; d < rank; ++d) {
+        const int64_t v = st[size_t(t)][size_t(d)];
+        if (v == 0) continue;
+        sum += (sum.empty() ? "" : " + ") + std::string("d") + std::to_string(d) +
+               (v == 1 ? "" : " * " + std::to_string(v) + U);
+      }
+      src << "  const " << IT << " o" << tn << " = " << sum << ";\n";
+      off = "o" + tn;
+      step = st[size_t(t)][size_t(rank - 1)];
+    }
+    // vector form: 4 consecutive f32 / bf16 elements adjacent and aligned
+    // (unit inner stride, every other stride a multiple of 4 elements; the
+    // base pointer's alignment is checked at launch)
+    bool vec = lanes == kLanes && step == 1 && (ty == MK_F32 || ty == MK_BF16);
+    for (int d = 0; vec && d + 1 < rank; ++d)
+      if (st[size_t(t)][size_t(d)] % kLanes != 0) vec = false;
+    if (vec && ty == MK_F32) {
+      src << "  const mkj_f4 w" << tn << " = *(const mkj_f4*)((const float*)" << p << " + " << off << ");\n";
+      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "w" + tn + "[" + std::to_string(l) + "]";
+      k->align[size_t(t)] = 16;
+    } else if (vec) {
+      src << "  const mkj_u2 w" << tn << " = *(const mkj_u2*)((const unsigned short*)" << p << " + " << off
+          << ");\n";
+      for (int l = 0; l < lanes; ++l) {
+        src << "  const float x" << tn << "_" << l << " = mkj_bf2f((unsigned short)(w" << tn << "[" << l / 2 << "]"
+            << (l % 2 ? " >> 16" : "") << "));\n";
+        x[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
+      }
+      k->align[size_t(t)] = 8;
+    } else if (step == 0 || lanes == 1) {
+      LoadExpr(ty, p, off, &e);
+      src << "  const float x" << tn << " = " << e << ";\n";
+      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "x" + tn;
+    } else {
+      for (int l = 0; l < lanes; ++l) {
+        const std::string ol = l == 0 ? off : "(" + off + " + " + std::to_string(int64_t(l) * step) + U + ")";
+        LoadExpr(ty, p, ol, &e);
+        src << "  const float x" << tn << "_" << l << " = " << e << ";\n";
+        x[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
+      }
+    }
+  }
+  for (int l = 0; l < lanes; ++l) {
+    src << "  float y" << l << "[" << n_out << "];\n  @K@_body(";
+    for (int t = 0; t < n_in; ++t) src << x[size_t(t)][size_t(l)] << ", ";
+    src << "y" << l << ");\n";
+  }
+  for (int o = 0; o < n_out; ++o) {
+    const int ty = out_type[size_t(o)];
+    const std::string q = "q" + std::to_string(o);
+    auto y = [&](int l) { return "y" + std::to_string(l) + "[" + std::to_string(o) + "]"; };
+    if (lanes == kLanes && ty == MK_F32) {
+      src << "  *(mkj_f4*)((float*)" << q << " + i0) = mkj_f4{" << y(0) << ", " << y(1) << ", " << y(2) << ", "
+          << y(3) << "};\n";
+      k->align[size_t(n_in + o)] = 16;
+    } else if (lanes == kLanes && ty == MK_BF16) {
+      src << "  *(mkj_u2*)((unsigned short*)" << q << " + i0) = mkj_u2{unsigned(mkj_f2bf(" << y(0)
+          << ")) | (unsigned(mkj_f2bf(" << y(1) << ")) << 16), unsigned(mkj_f2bf(" << y(2)
+          << ")) | (unsigned(mkj_f2bf(" << y(3) << ")) << 16)};\n";
+      k->align[size_t(n_in + o)] = 8;
+    } else {
+      for (int l = 0; l < lanes; ++l) {
+        std::string stmt;
+        StoreStmt(ty, q, l == 0 ? "i0" : "i0 + " + std::to_string(l), y(l), &stmt);
+        src << "  " << stmt << "\n";
+      }
+    }
+  }
+  src << "}\n";
+  std::string text = src.str();
+  char name[32];
+  snprintf(name, sizeof name, "ew_%016" PRIx64, Fnv1a(text));
+  ReplaceAll(text, "@K@", name);
+  k->name = name;
+  k->source = std::move(text);
+  k->blocks = uint32_t(blocks);
+  return true;
+}
+
+// ------------------------------------------------------------------ compile / load
+struct EwJit::Code {
+  std::vector<char> bin;
+  std::string error;
+  double seconds = 0;
+  std::mutex mu;
+  std::vector<hipModule_t> modules;  // per device ordinal (null: not loaded)
+};
+
+namespace {
+
+// The runtime compiler, loaded from the ROCm installation ($ROCM_PATH, else
+// /opt/rocm) into a link namespace of its own: a process may already hold
+// another ROCm's hiprtc / comgr under the same sonames (PyTorch wheels bundle
+// theirs), and the generated kernels must come from the compiler that built
+// the kernel library, whose math routines they share bit for bit.  When that
+// fails, the hiprtc the process resolves by name is used.
+struct Rtc {
+  decltype(&hiprtcCreateProgram) create = nullptr;
+  decltype(&hiprtcCompileProgram) compile = nullptr;
+  decltype(&hiprtcGetProgramLogSize) log_size = nullptr;
+  decltype(&hiprtcGetProgramLog) log = nullptr;
+  decltype(&hiprtcGetCodeSize) code_size = nullptr;
+  decltype(&hiprtcGetCode) code = nullptr;
+  decltype(&hiprtcDestroyProgram) destroy = nullptr;
+  decltype(&hiprtcGetErrorString) error_string = nullptr;
+  std::string where, error;
+};
+
+const Rtc& LoadRtc() {
+  static const Rtc rtc = [] {
+    Rtc r;
+    const char* root = getenv("ROCM_PATH");
+    const std::string path = std::string(root && *root ? root : "/opt/rocm") + "/lib/libhiprtc.so";
+    void* h = dlmopen(LM_ID_NEWLM, path.c_str(), RTLD_NOW | RTLD_LOCAL);
+    r.where = path + " (own namespace)";
+    if (!h) {
+      r.error = dlerror();
+      h = dlopen("libhiprtc.so", RTLD_NOW | RTLD_LOCAL);
+      r.where = "libhiprtc.so";
+    }
+    if (!h) {
+      r.error = "cannot load hiprtc (" + r.error + "; " + dlerror() + ")";
+      return r;
+    }
+    bool ok = true;
+    auto sym = [&](auto& fn, const char* name) {
+      fn = reinterpret_cast<std::remove_reference_t<decltype(fn)>>(dlsym(h, name));
+      ok = ok && fn != nullptr;
+    };
+    sym(r.create, "hiprtcCreateProgram");
+    sym(r.compile, "hiprtcCompileProgram");
+    sym(r.log_size, "hiprtcGetProgramLogSize");
+    sym(r.log, "hiprtcGetProgramLog");
+    sym(r.code_size, "hiprtcGetCodeSize");
+    sym(r.code, "hiprtcGetCode");
+    sym(r.destroy, "hiprtcDestroyProgram");
+    sym(r.error_string, "hiprtcGetErrorString");
+    if (!ok) r.error = r.where + ": missing hiprtc symbols";
+    else r.error.clear();
+    return r;
+  }();
+  return rtc;
+}
+
+// code objects by full source, for the life of the process
+std::mutex g_codes_mu;
+std::unordered_map<std::string, std::shared_ptr<EwJit::Code>>& Codes() {
+  static auto* m = new std::unordered_map<std::string, std::shared_ptr<EwJit::Code>>();
+  return *m;
+}
+
+}  // namespace
+
+int EwJit::Add(EwKernel k) {
+  auto it = by_name_.find(k.name);
+  if (it != by_name_.end()) return it->second;
+  const int idx = int(kernels_.size());
+  by_name_[k.name] = idx;
+  kernels_.push_back(std::move(k));
+  return idx;
+}
+
+std::string EwJit::error() const {
+  std::lock_guard<std::mutex> lk(mu_);
+  return error_;
+}
+
+bool EwJit::Build() {
+  std::lock_guard<std::mutex> lk(mu_);
+  if (built_) return error_.empty();
+  built_ = true;
+  std::string source = kPreamble;
+  for (const EwKernel& k : kernels_) source += k.source;
+  if (const char* path = getenv("JAM_EW_JIT_SOURCE")) {  // debugging: the generated source
+    if (FILE* fp = fopen(path, "w")) {
+      fwrite(source.data(), 1, source.size(), fp);
+      fclose(fp);
+    }
+  }
+  std::shared_ptr<Code> code;
+  {
+    std::lock_guard<std::mutex> g(g_codes_mu);
+    auto& m = Codes();
+    auto it = m.find(source);
+    if (it != m.end()) code = it->second;
+    else {
+      code = std::make_shared<Code>();
+      m[source] = code;
+    }
+  }
+  // one compile per distinct source; a concurrent Build of the same source
+  // waits on the code's mutex
+  std::lock_guard<std::mutex> cl(code->mu);
+  if (code->bin.empty() && code->error.empty()) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const Rtc& rtc = LoadRtc();
+    hiprtcProgram p = nullptr;
+    hiprtcResult r = HIPRTC_SUCCESS;
+    if (!rtc.error.empty()) {
+      code->error = rtc.error;
+    } else if ((r = rtc.create(&p, source.c_str(), "jam_ew.hip", 0, nullptr, nullptr)) != HIPRTC_SUCCESS) {
+      code->error = std::string("hiprtcCreateProgram: ") + rtc.error_string(r);
+    } else {
+      // the kernel library's code generation: gfx950, -O3, no packed fp32
+      // ops, hipcc's default contraction mode (the math library's inlined
+      // code then compiles as in the interpreter; the generated program's
+      // own operations are kept apart by the pragma in each body)
+      const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=fast-honor-pragmas",
+                            "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
+                            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+      r = rtc.compile(p, int(sizeof opts / sizeof opts[0]), opts);
+      if (r != HIPRTC_SUCCESS) {
+        size_t ls = 0;
+        rtc.log_size(p, &ls);
+        std::string log(ls, '\0');
+        if (ls) rtc.log(p, &log[0]);
+        if (log.size() > 2000) log.resize(2000);
+        code->error = std::string("hiprtcCompileProgram (") + rtc.where + "): " + rtc.error_string(r) + ": " + log;
+      } else {
+        size_t cs = 0;
+        rtc.code_size(p, &cs);
+        code->bin.resize(cs);
+        if (cs) rtc.code(p, code->bin.data());
+        if (code->bin.empty()) code->error = "hiprtc: empty code object";
+      }
+      rtc.destroy(&p);
+    }
+    code->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  }
+  if (const char* path = getenv("JAM_EW_JIT_CODE")) {  // debugging: the code object
+    if (FILE* fp = fopen(path, "wb")) {
+      fwrite(code->bin.data(), 1, code->bin.size(), fp);
+      fclose(fp);
+    }
+  }
+  code_ = code;
+  compile_seconds_ = code->seconds;
+  error_ = code->error;
+  return error_.empty();
+}
+
+void* const* EwJit::Functions(int ordinal) {
+  if (ordinal < 0 || !Build()) return nullptr;
+  std::lock_guard<std::mutex> lk(mu_);
+  if (!error_.empty()) return nullptr;  // a failed load is not retried
+  if (fns_.size() <= size_t(ordinal)) fns_.resize(size_t(ordinal) + 1);
+  std::vector<void*>& f = fns_[size_t(ordinal)];
+  if (f.size() == kernels_.size()) return f.data();
+  hipModule_t mod = nullptr;
+  {
+    std::lock_guard<std::mutex> cl(code_->mu);
+    if (code_->modules.size() <= size_t(ordinal)) code_->modules.resize(size_t(ordinal) + 1, nullptr);
+    if (!code_->modules[size_t(ordinal)]) {
+      hipError_t e = hipModuleLoadData(&code_->modules[size_t(ordinal)], code_->bin.data());
+      if (e != hipSuccess) {
+        code_->modules[size_t(ordinal)] = nullptr;
+        error_ = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
+        return nullptr;
+      }
+    }
+    mod = code_->modules[size_t(ordinal)];
+  }
+  std::vector<void*> out;
+  for (const EwKernel& k : kernels_) {
+    hipFunction_t fn = nullptr;
+    hipError_t e = hipModuleGetFunction(&fn, mod, k.name.c_str());
+    if (e != hipSuccess) {
+      error_ = "hipModuleGetFunction(" + k.name + "): " + hipGetErrorString(e);
+      return nullptr;
+    }
+    out.push_back(reinterpret_cast<void*>(fn));
+  }
+  f = std::move(out);
+  return f.data();
+}
+
+}  // namespace mi::jam

@@ -71,6 +71,11 @@ std::string Program::Dump() const {
      << " consts\n";
   for (const auto& p : patterns) os << "  pattern " << p << "\n";
   for (const auto& a : alias_notes) os << "  alias " << a << "\n";
+  if (ew_jit) {
+    int n = 0;
+    for (const Step& st : steps) n += st.jit >= 0;
+    os << "  ew_jit " << ew_jit->size() << " kernels for " << n << " steps\n";
+  }
   for (size_t i = 0; i < steps.size(); ++i) {
     os << "  [" << i << "] " << StepName(steps[i].kind);
     if (!steps[i].note.empty()) os << " (" << steps[i].note << ")";
@@ -88,6 +93,9 @@ CompileOptions OptionsFromEnv() {
   o.fuse_gelu = getenv("JAM_NO_GELU") == nullptr;
   o.fuse_elementwise = getenv("JAM_NO_EW_FUSION") == nullptr;
   o.fuse_xent = getenv("JAM_NO_XENT") == nullptr;
+  o.ew_jit = getenv("JAM_NO_EW_JIT") == nullptr;
+  o.ew_jit_eager = getenv("JAM_EW_JIT_EAGER") != nullptr;
+  o.ew_jit_strict = getenv("JAM_EW_JIT_STRICT") != nullptr;
   return o;
 }
 
@@ -3777,7 +3785,31 @@ CompileResult Compile(const char* code, size_t size, const CompileOptions& opts)
   }
   Lowerer L(*m, opts);
   r.program = L.Run(err);
-  if (!r.program) r.error = err.empty() ? "jam: lowering failed" : err;
+  if (!r.program) {
+    r.error = err.empty() ? "jam: lowering failed" : err;
+    return r;
+  }
+  if (opts.ew_jit) {
+    // every ew step also as a generated kernel (ew_jit.h); one that cannot
+    // be generated keeps the interpreter
+    auto jit = std::make_shared<EwJit>();
+    jit->strict = opts.ew_jit_strict;
+    for (Step& st : r.program->steps) {
+      if (st.kind != StepKind::kEw) continue;
+      EwKernel k;
+      std::string why;
+      if (GenerateEwKernel(st, &k, &why) && k.blocks > 0) st.jit = jit->Add(std::move(k));
+      else if (opts.ew_jit_strict && !why.empty()) {
+        r.program = nullptr;
+        r.error = "jam: no generated kernel for ew step (" + st.note + "): " + why;
+        return r;
+      }
+    }
+    if (jit->size()) {
+      r.program->ew_jit = jit;
+      if (opts.ew_jit_eager && !jit->Build()) r.program->patterns.push_back("ew_jit failed: " + jit->error());
+    }
+  }
   return r;
 }
 

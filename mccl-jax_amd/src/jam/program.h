@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "jam/ew_jit.h"
 #include "jam/ir.h"
 
 namespace mi::jam {
@@ -44,6 +45,7 @@ struct Step {
   std::vector<int64_t> strides;  // ew per-input strides (6 per input) / copy strides
   std::vector<int32_t> types;  // ew per-input dtypes
   std::string note;            // provenance for dumps / errors
+  int jit = -1;                // ew: index of its generated kernel in Program::ew_jit (-1: interpreter)
 };
 
 struct ConstBlob {
@@ -67,6 +69,8 @@ class Program {
   std::vector<std::string> alias_notes;  // why a requested alias was or was not taken (dumps)
   std::vector<std::string> patterns;   // fused patterns recognised (for tests / dumps)
   std::string name = "jam.main";
+  // generated kernels of the ew steps (null when disabled)
+  std::shared_ptr<EwJit> ew_jit;
 
   std::string Dump() const;
 
@@ -87,6 +91,9 @@ struct CompileOptions {
   bool fuse_gelu = true;
   bool fuse_elementwise = true;
   bool fuse_xent = true;        // env JAM_NO_XENT disables
+  bool ew_jit = true;           // env JAM_NO_EW_JIT disables (ew steps run the interpreter)
+  bool ew_jit_eager = false;    // env JAM_EW_JIT_EAGER: compile the generated kernels in Compile
+  bool ew_jit_strict = false;   // env JAM_EW_JIT_STRICT: no interpreter fallback (EwJit::strict)
 };
 
 struct CompileResult {

@@ -1,6 +1,8 @@
 #include "jam/run.h"
 
+#include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "mk_kernels.h"
 
@@ -39,6 +41,9 @@ struct Frame {
   std::vector<RunOutput>* outputs;
   std::vector<void*>* consts;
   char* arena;
+  const EwJit* jit;          // generated ew kernels of the plan (null: none)
+  void* const* jit_fns;      // their hipFunction_t handles on this device (null: interpreter)
+  std::string* error;        // message of a failure not reported through mk_last_error
 };
 
 void* Resolve(const BufRef& b, const Frame& f) {
@@ -112,6 +117,30 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     case StepKind::kGelu:
       return mk_gelu_tanh(st, int(i[0]), i[1], P(0), P(1));
     case StepKind::kEw: {
+      if (s.jit >= 0 && f.jit_fns) {
+        // the step's generated kernel, when every pointer has the alignment
+        // its vector accesses assume (otherwise the interpreter below)
+        const EwKernel& k = f.jit->kernel(s.jit);
+        void* ptrs[16];
+        bool aligned = s.bufs.size() <= 16;
+        for (size_t b = 0; aligned && b < s.bufs.size(); ++b) {
+          ptrs[b] = P(b);
+          aligned = reinterpret_cast<uintptr_t>(ptrs[b]) % k.align[b] == 0;
+        }
+        if (aligned) {
+          void* args[16];
+          for (size_t b = 0; b < s.bufs.size(); ++b) args[b] = &ptrs[b];
+          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[s.jit]), k.blocks, 1, 1,
+                                               kEwJitBlock, 1, 1, 0, stream, args, nullptr);
+          if (e == hipSuccess) return MK_OK;
+          *f.error = "hipModuleLaunchKernel(" + k.name + "): " + hipGetErrorString(e);
+          return MK_ERR_LAUNCH;
+        }
+        if (f.jit->strict) {
+          *f.error = "generated kernel " + k.name + ": a buffer misses its alignment (strict mode)";
+          return MK_ERR_INVALID;
+        }
+      }
       const int n_in = int(i[7]);
       const int n_out = int(s.bufs.size()) - n_in;
       if (n_in > 8 || n_out < 1 || n_out > 4) return MK_ERR_INVALID;
@@ -148,7 +177,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     case StepKind::kCopy: {
       if (i[0] == 0 || P(0) == P(1)) return MK_OK;  // same memory: an output written over its donated input
       hipError_t e = hipMemcpyAsync(P(1), P(0), size_t(i[0]), hipMemcpyDeviceToDevice, stream);
-      return e == hipSuccess ? MK_OK : MK_ERR_LAUNCH;
+      if (e == hipSuccess) return MK_OK;
+      *f.error = std::string("hipMemcpyAsync: ") + hipGetErrorString(e);
+      return MK_ERR_LAUNCH;
     }
   }
   return MK_ERR_UNSUPPORTED;
@@ -201,13 +232,31 @@ std::string Run(Program& prog, exec::DeviceContext& dev, const std::vector<RunIn
     dev.Free(arena);
     return "jam run: " + err;
   }
-  Frame f{&inputs, &outs, consts, arena};
+  // generated ew kernels: compiled on the plan's first run, loaded once per
+  // device; when that fails the interpreter runs them (reported once)
+  void* const* jit_fns = nullptr;
+  if (prog.ew_jit) {
+    jit_fns = prog.ew_jit->Functions(dev.ordinal());
+    if (!jit_fns && prog.ew_jit->strict) {
+      release();
+      dev.Free(arena);
+      return "jam run: generated elementwise kernels unavailable: " + prog.ew_jit->error();
+    }
+    if (!jit_fns) {
+      static std::once_flag warned;
+      std::call_once(warned, [&] {
+        fprintf(stderr, "jam: generated elementwise kernels unavailable (%s); running the interpreter\n",
+                prog.ew_jit->error().c_str());
+      });
+    }
+  }
+  std::string step_error;
+  Frame f{&inputs, &outs, consts, arena, prog.ew_jit.get(), jit_fns, &step_error};
   for (size_t k = 0; k < prog.steps.size(); ++k) {
     const int rc = RunStep(prog.steps[k], f, dev.stream());
     if (rc != MK_OK) {
       std::string msg = "jam run: step " + std::to_string(k) + " (" + StepName(prog.steps[k].kind) + "): " +
-                        (rc == MK_ERR_LAUNCH && prog.steps[k].kind == StepKind::kCopy ? "hipMemcpyAsync failed"
-                                                                                       : mk_last_error());
+                        (!step_error.empty() ? step_error : std::string(mk_last_error()));
       (void)dev.Synchronize(nullptr);
       release();
       dev.Free(arena);

@@ -44,7 +44,7 @@ def build_writer(outdir):
         objs = list(ex.map(cc, sources))
     exe = os.path.join(outdir, "vhlo_writer")
     lib = os.path.join(PKG, "lib")
-    subprocess.run(["g++", "-o", exe, *objs, "-L" + lib, "-lmk_kernels", "-L/opt/rocm/lib", "-lamdhip64",
+    subprocess.run(["g++", "-o", exe, *objs, "-L" + lib, "-lmk_kernels", "-L/opt/rocm/lib", "-lamdhip64", "-ldl",
                     "-Wl,-rpath," + lib, "-Wl,-rpath,/opt/rocm/lib"], check=True)
     return exe
 
