@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--spinup", type=float, default=1.0,
                     help="seconds of untimed headline launches before anything is timed (clocks settle)")
-    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5", "gemm", "pjrt"], default=None)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5", "gemm", "pjrt", "c5jit"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -314,21 +314,9 @@ def run_gemm(torch, np, K, args):
     return res
 
 
-def run_pjrt(torch, np, args):
-    """The plugin path: the C3 module at S=8192 compiled by jam and run
-    through PJRT_LoadedExecutable_Execute with inputs resident in HBM (K
-    executes queued back to back, host wall clock until the last completion
-    event), and the per-Execute cost of a tiny module."""
-    from mi355x_pjrt import modules, pjrt
-    from oracle import bf16, inputs
-
-    p = pjrt.Plugin()
-    client = p.client()
-    d = inputs.c3_sdpa(args.seq)
-    e = client.compile(modules.sdpa(4, 16, args.seq, 128, True))
-    bufs = [client.put(d[k], pjrt.BF16) for k in ("q", "k", "v")]
-    for b in bufs:
-        b.ready()
+def pjrt_runner(p):
+    """run(exe, inputs, n): n executes queued back to back; host wall clock
+    per execute (ms) until the last completion event."""
 
     def run(exe, inputs_, n):
         # each execution's outputs are dropped once the next one is queued,
@@ -349,6 +337,37 @@ def run_pjrt(torch, np, args):
             b.destroy()
         return el / n * 1e3
 
+    return run
+
+
+def run_pjrt_c5(np, args):
+    """Only the jitted C5 step through the plugin (for profiling)."""
+    from mi355x_pjrt import pjrt
+
+    p = pjrt.Plugin()
+    client = p.client()
+    res = run_c5_jitted(np, p, client, pjrt_runner(p), args)
+    client.close()
+    return res
+
+
+def run_pjrt(torch, np, args):
+    """The plugin path: the C3 module at S=8192 compiled by jam and run
+    through PJRT_LoadedExecutable_Execute with inputs resident in HBM (K
+    executes queued back to back, host wall clock until the last completion
+    event), and the per-Execute cost of a tiny module."""
+    from mi355x_pjrt import modules, pjrt
+    from oracle import bf16, inputs
+
+    p = pjrt.Plugin()
+    client = p.client()
+    d = inputs.c3_sdpa(args.seq)
+    e = client.compile(modules.sdpa(4, 16, args.seq, 128, True))
+    bufs = [client.put(d[k], pjrt.BF16) for k in ("q", "k", "v")]
+    for b in bufs:
+        b.ready()
+
+    run = pjrt_runner(p)
     run(e, bufs, args.warmup)
     ms = run(e, bufs, args.steps)
     tf = sdpa_flops(4, 16, args.seq, 128) / (ms * 1e-3) / 1e12
@@ -476,6 +495,9 @@ def main():
         return
     if args.only == "pjrt":
         print(json.dumps({"pjrt": run_pjrt(torch, np, args)}))
+        return
+    if args.only == "c5jit":
+        print(json.dumps({"c5_jitted_step": run_pjrt_c5(np, args)}))
         return
     sweep, head, fusions = {}, None, {}
     spin_up(torch, np, K, args)

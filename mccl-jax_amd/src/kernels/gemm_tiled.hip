@@ -65,7 +65,7 @@ struct TiledGemm {
   int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU
   int c_type;
   int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
-                              // stored as 16-byte chunks / element by element
+                              // stored as 16-byte chunks / element by element, 4 staged fp32 rows
 };
 
 // The copies one wave makes of one operand's tile: copy c is j = wave + W c
@@ -242,6 +242,63 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
   }
 }
 
+// fp32 C through LDS, for C rows that are not 16-byte aligned (an odd N such
+// as a vocabulary, where direct stores would go out one dword at a time, 32
+// rows per instruction).  The tile is staged in passes of RP rows (whole
+// wave rows; RP x TN floats fit the operand buffers): the waves owning those
+// rows write their accumulators as 16-byte chunks, chunk c of staging row r
+// at position c ^ (r & 15), then every thread stores consecutive columns of
+// consecutive rows, so each wave writes 256 contiguous bytes of a C row.
+template <int TM, int TN, int kW, int kWM, int kWN, int kI, int kJ, int kLdsFloats>
+__device__ __attribute__((always_inline)) inline void store_staged_f32(const TiledGemm& p,
+                                                                       const f32x16_t (&acc)[kI][kJ], float* st,
+                                                                       int64_t m0, int64_t n0, int wm, int wn,
+                                                                       int lane, int64_t bz) {
+  constexpr int kCpr = TN / 4;
+  static_assert(kCpr % 16 == 0, "staging rows of whole 16-chunk groups");
+  // rows per pass: the largest multiple of kWM dividing TM whose staging fits
+  constexpr int kRP = [] {
+    int rp = kWM;
+    for (int r = kWM; r <= TM; r += kWM)
+      if (TM % r == 0 && r * TN <= kLdsFloats) rp = r;
+    return rp;
+  }();
+  static_assert(kRP * TN <= kLdsFloats, "one wave row of staging fits");
+  static_assert(kRP >= kWM && TM % kRP == 0, "passes of whole wave rows");
+  constexpr int kThreads = 64 * kW;
+  static_assert(kRP * TN % kThreads == 0, "staged rows split evenly over the threads");
+  const int c = lane & 31, g = lane >> 5;
+  float* Cz = reinterpret_cast<float*>(p.C) + bz * p.c_bs;
+#pragma unroll
+  for (int pass = 0; pass < TM / kRP; ++pass) {
+    if (wm * kWM >= pass * kRP && wm * kWM < (pass + 1) * kRP) {
+#pragma unroll
+      for (int a = 0; a < kI; ++a) {
+        const int ml = wm * kWM + 32 * a + c - pass * kRP;
+#pragma unroll
+        for (int b = 0; b < kJ; ++b)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const int nl = wn * kWN + 32 * b + 8 * rg + 4 * g;
+            float v[4] = {acc[a][b][4 * rg], acc[a][b][4 * rg + 1], acc[a][b][4 * rg + 2], acc[a][b][4 * rg + 3]};
+            finish4<MK_F32>(p, n0 + nl, v);
+            *reinterpret_cast<f32x4*>(st + ml * TN + 4 * ((nl >> 2) ^ (ml & 15))) = f32x4{{v[0], v[1], v[2], v[3]}};
+          }
+      }
+    }
+    lds_barrier();
+#pragma unroll 4
+    for (int it = 0; it < kRP * TN / kThreads; ++it) {
+      const int e = it * kThreads + int(threadIdx.x);
+      const int row = e / TN, col = e % TN;
+      const float v = st[row * TN + 4 * ((col >> 2) ^ (row & 15)) + (col & 3)];
+      const int64_t m = m0 + pass * kRP + row, n = n0 + col;
+      if (m < p.M && n < p.N) Cz[m * p.ldc + n] = v;
+    }
+    lds_barrier();
+  }
+}
+
 // Stores straight from the accumulators: 4 consecutive columns per lane and
 // register group, as one vector store (c_mode 1) or element by element.
 template <int CT, int kWM, int kWN, int kI, int kJ>
@@ -403,6 +460,9 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
     store_staged<MK_BF16, false, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
   else if (p.c_mode == 3)
     store_staged<MK_F16, false, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
+  else if (p.c_mode == 4)
+    store_staged_f32<TM, TN, kW, kWM, kWN, kI, kJ, S * BK * (TM + TN) / 2>(p, acc, reinterpret_cast<float*>(lds), m0,
+                                                                           n0, wm, wn, lane, bz);
   else if (p.c_type == MK_F32)
     store_direct<MK_F32, kWM, kWN>(p, acc, m0, n0, wm, wn, lane, bz);
   else if (p.c_type == MK_BF16)
@@ -459,7 +519,7 @@ bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch,
   a.c_type = c_type;
   const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0 && N % 8 == 0;
   const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0 && N % 4 == 0;
-  a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 1 : 0;
+  a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 1 : 4;
   return true;
 }
 

@@ -588,6 +588,29 @@ def test_gemm_tiled_epilogues_and_layouts(K):
     assert np.max(np.abs(got3 - want3) / (norm3 + 1e-30)) < 1e-5
 
 
+def test_gemm_tiled_f32_out_unaligned_rows(K):
+    """fp32 C whose rows are not 16-byte aligned (odd N, as a vocabulary
+    projection has): the tile goes out through LDS, a pass of rows at a time,
+    one C row segment per wave.  Shapes that select each tile size (256 x 256,
+    128 x 192, 128 x 128 on 256 CUs), with an fp32 bias, written into a wider
+    buffer whose padding columns must stay untouched; within 1e-5 of the
+    float64 product, scaled by the product of magnitudes."""
+    rng = np.random.default_rng(23)
+    for (M, N, Kd) in [(3072, 4099, 64), (2048, 2051, 136), (520, 517, 72)]:
+        print(f"case: tiled gemm fp32 out M={M} N={N} K={Kd}", flush=True)
+        a = bf16.round_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+        b = bf16.round_bf16(rng.standard_normal((Kd, N)).astype(np.float32))
+        bias = bf16.round_bf16(rng.standard_normal(N).astype(np.float32))
+        at, bt = _bf16_operand(a, False), _bf16_operand(b, True)
+        want = a.astype(np.float64) @ b + bias
+        norm = np.abs(a).astype(np.float64) @ np.abs(b) + np.abs(bias)
+        wide = torch.full((M, N + 3), -7.0, dtype=torch.float32, device="cuda")
+        K.gemm(at, bt, out_dtype=torch.float32, bias=torch.from_numpy(bias).cuda(), out=wide[:, :N])
+        got = wide.cpu().numpy()
+        assert np.max(np.abs(got[:, :N] - want) / (norm + 1e-30)) < 1e-5, (M, N, Kd)
+        assert np.all(got[:, N:] == -7.0)
+
+
 # ------------------------------------------------------------------ a6 iota, a12 layout, misc
 def test_iota_convert_fill_copy(K):
     it = K.iota((3, 5, 7), 1).cpu().numpy()
