@@ -249,6 +249,7 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
   const std::string U = narrow ? "u" : "ll";
 
   std::ostringstream src;
+  src << "#ifndef @K@_DEF\n#define @K@_DEF\n";
   // ---- the program as a straight-line function of one element's inputs
   {
     std::string reg[kMaxRegs];
@@ -275,14 +276,16 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
     for (int o = 0; o < n_out; ++o) src << "  y[" << o << "] = " << reg[out_reg[size_t(o)]] << ";\n";
     src << "}\n";
   }
-  // ---- the entry: index, loads, lanes, stores
-  src << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(";
-  for (int t = 0; t < n_in; ++t) src << "const void* p" << t << ", ";
-  for (int o = 0; o < n_out; ++o) src << "void* q" << o << (o + 1 < n_out ? ", " : ") {\n");
+  // ---- one block's work (block blk of the step's grid): index, loads,
+  // lanes, stores
+  std::string params;
+  for (int t = 0; t < n_in; ++t) params += "const void* p" + std::to_string(t) + ", ";
+  for (int o = 0; o < n_out; ++o) params += "void* q" + std::to_string(o) + (o + 1 < n_out ? ", " : "");
+  src << "static __device__ __forceinline__ void @K@_run(unsigned blk, " << params << ") {\n";
   if (narrow)
-    src << "  const unsigned i0 = (blockIdx.x * " << kEwJitBlock << "u + threadIdx.x) * " << lanes << "u;\n";
+    src << "  const unsigned i0 = (blk * " << kEwJitBlock << "u + threadIdx.x) * " << lanes << "u;\n";
   else
-    src << "  const long long i0 = ((long long)blockIdx.x * " << kEwJitBlock << " + threadIdx.x) * " << lanes << ";\n";
+    src << "  const long long i0 = ((long long)blk * " << kEwJitBlock << " + threadIdx.x) * " << lanes << ";\n";
   src << "  if (i0 >= " << n << U << ") return;\n";
   // multi-dim index: only as far out as some strided input needs
   int lo = rank;
@@ -388,14 +391,46 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
       }
     }
   }
-  src << "}\n";
-  std::string text = src.str();
+  src << "}\n#endif\n";
+  std::string helpers = src.str();
+  std::string args;
+  for (int t = 0; t < n_in; ++t) args += ", p" + std::to_string(t);
+  for (int o = 0; o < n_out; ++o) args += ", q" + std::to_string(o);
+  std::string entry = "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kEwJitBlock) + ") @K@(" +
+                      params + ") { @K@_run(blockIdx.x" + args + "); }\n";
   char name[32];
-  snprintf(name, sizeof name, "ew_%016" PRIx64, Fnv1a(text));
-  ReplaceAll(text, "@K@", name);
+  snprintf(name, sizeof name, "ew_%016" PRIx64, Fnv1a(helpers + entry));
+  ReplaceAll(helpers, "@K@", name);
+  ReplaceAll(entry, "@K@", name);
   k->name = name;
-  k->source = std::move(text);
+  k->base = name;
+  k->helpers = std::move(helpers);
+  k->source = k->helpers + entry;
   k->blocks = uint32_t(blocks);
+  k->n_in = n_in;
+  k->n_out = n_out;
+  k->batch = 0;
+  return true;
+}
+
+bool BatchEwKernel(const EwKernel& single, int batch, EwKernel* k) {
+  if (single.batch != 0 || batch < 2 || batch > kEwJitMaxBatch) return false;
+  if (int64_t(single.blocks) * batch >= (int64_t(1) << 31)) return false;
+  *k = single;
+  k->batch = batch;
+  k->name = single.base + "_x" + std::to_string(batch);
+  const int pi = std::max(single.n_in, 1);
+  std::ostringstream e;
+  // the instances' pointers by value: p[k][t] inputs, q[k][o] outputs
+  e << "struct " << k->name << "_args { const void* p[" << batch << "][" << pi << "]; void* q[" << batch << "]["
+    << single.n_out << "]; };\n";
+  e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") " << k->name << "(const " << k->name
+    << "_args a) {\n  const unsigned k = blockIdx.x / " << single.blocks << "u, blk = blockIdx.x - k * "
+    << single.blocks << "u;\n  " << single.base << "_run(blk";
+  for (int t = 0; t < single.n_in; ++t) e << ", a.p[k][" << t << "]";
+  for (int o = 0; o < single.n_out; ++o) e << ", a.q[k][" << o << "]";
+  e << ");\n}\n";
+  k->source = single.helpers + e.str();
   return true;
 }
 

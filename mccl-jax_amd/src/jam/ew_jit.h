@@ -27,13 +27,22 @@ namespace mi::jam {
 
 struct Step;
 
-constexpr int kEwJitBlock = 256;  // threads per block of every generated kernel
+constexpr int kEwJitBlock = 256;    // threads per block of every generated kernel
+constexpr int kEwJitMaxBatch = 32;  // instances of one batched launch
 
 // One generated kernel.
 struct EwKernel {
-  std::string name;       // "ew_" + 16 hex digits of the body's hash
-  std::string source;     // its __device__ body and extern "C" __global__ entry
-  uint32_t blocks = 0;    // grid size (kEwJitBlock threads each); 0: nothing to do
+  std::string name;       // entry: "ew_" + 16 hex digits of the code's hash [+ "_x<batch>"]
+  std::string base;       // name of the single-instance entry
+  std::string helpers;    // the program and one block's work as __device__ functions
+  std::string source;     // helpers and the extern "C" __global__ entry
+  uint32_t blocks = 0;    // grid of one instance (kEwJitBlock threads per block); 0: nothing to do
+  int n_in = 0, n_out = 0;
+  // 0: the entry takes the step's pointers; k >= 2: it takes a struct of k
+  // instances' pointers (inputs p[k][t], outputs q[k][o]) and a grid of
+  // instances x blocks, block b running block b % blocks of instance
+  // b / blocks — independent steps of one shape in one launch
+  int batch = 0;
   // per step buffer (inputs then outputs): byte alignment its resolved
   // pointer must have for the vector accesses the kernel makes (1: any)
   std::vector<uint8_t> align;
@@ -42,6 +51,8 @@ struct EwKernel {
 // Writes the kernel of ew step `s`; false with `why` when the step's encoding
 // is outside what the generator handles (the step keeps the interpreter).
 bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why);
+// The batched entry (`batch` instances) of a single-instance kernel.
+bool BatchEwKernel(const EwKernel& single, int batch, EwKernel* k);
 
 // The generated kernels of one launch plan.  Identical kernels (same name)
 // are kept once.  Compiled on first use; the code object is shared by every

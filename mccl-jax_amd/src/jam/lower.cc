@@ -96,6 +96,7 @@ CompileOptions OptionsFromEnv() {
   o.ew_jit = getenv("JAM_NO_EW_JIT") == nullptr;
   o.ew_jit_eager = getenv("JAM_EW_JIT_EAGER") != nullptr;
   o.ew_jit_strict = getenv("JAM_EW_JIT_STRICT") != nullptr;
+  o.ew_batch = getenv("JAM_NO_EW_BATCH") == nullptr;
   return o;
 }
 
@@ -3752,6 +3753,143 @@ class Lowerer {
 
 }  // namespace
 
+namespace {
+
+// Memory an ew step reads or writes: a byte range of one buffer.  A program
+// output that a donated input may carry is the same buffer as that input.
+struct Extent {
+  int space, index;
+  int64_t lo, hi;
+};
+
+bool Overlap(const std::vector<Extent>& a, const std::vector<Extent>& b) {
+  for (const Extent& x : a)
+    for (const Extent& y : b)
+      if (x.space == y.space && x.index == y.index && x.lo < y.hi && y.lo < x.hi) return true;
+  return false;
+}
+
+// Independent ew steps with the same generated kernel in one launch: each
+// maximal run of consecutive jitted ew steps that pairwise touch no common
+// memory (no step writes what another reads or writes) may run in any order,
+// so the run's steps of one kernel become one batched step (placed at its
+// first member), up to kEwJitMaxBatch instances each.  The Adam updates of
+// a training step's parameters of one shape are such a run.
+void BatchIndependentEwSteps(Program& prog) {
+  EwJit& jit = *prog.ew_jit;
+  std::vector<int> alias_of_output(prog.outputs.size(), -1);
+  for (size_t in = 0; in < prog.input_alias.size(); ++in)
+    if (prog.input_alias[in] >= 0 && size_t(prog.input_alias[in]) < alias_of_output.size())
+      alias_of_output[size_t(prog.input_alias[in])] = int(in);
+  auto ext = [&](const BufRef& b, int64_t lo, int64_t hi) {
+    Extent e{int(b.space), b.index, b.offset + lo, b.offset + hi};
+    if (b.space == Space::kOutput && alias_of_output[size_t(b.index)] >= 0) {
+      e.space = int(Space::kInput);
+      e.index = alias_of_output[size_t(b.index)];
+    }
+    if (b.space == Space::kArena) e.index = 0;
+    return e;
+  };
+  struct Acc {
+    std::vector<Extent> reads, writes;
+  };
+  auto access = [&](const Step& st) {
+    Acc a;
+    const int rank = int(st.i[0]), n_in = int(st.i[7]);
+    int64_t n = 1;
+    for (int d = 0; d < rank; ++d) n *= st.i[1 + size_t(d)];
+    for (int t = 0; t < n_in; ++t) {
+      const int64_t elt = DTypeBytes(DType(st.types[size_t(t)]));
+      int64_t last = 0;
+      bool neg = false;
+      for (int d = 0; d < rank; ++d) {
+        const int64_t str = st.i[1 + size_t(d)] == 1 ? 0 : st.strides[size_t(t * 6 + d)];
+        neg |= str < 0;
+        last += (st.i[1 + size_t(d)] - 1) * str;
+      }
+      a.reads.push_back(neg ? ext(st.bufs[size_t(t)], INT64_MIN / 4, INT64_MAX / 4)
+                            : ext(st.bufs[size_t(t)], 0, (last + 1) * elt));
+    }
+    for (size_t o = size_t(n_in); o < st.bufs.size(); ++o) {
+      const int64_t elt = DTypeBytes(DType(st.i[9 + 2 * (o - size_t(n_in))]));
+      a.writes.push_back(ext(st.bufs[o], 0, n * elt));
+    }
+    return a;
+  };
+  auto batchable = [&](const Step& st) { return st.kind == StepKind::kEw && st.jit >= 0 && st.batch == 1; };
+  std::vector<Step> out;
+  out.reserve(prog.steps.size());
+  std::map<std::pair<int, int>, int> batched_kernel;  // (single kernel, count) -> batched kernel
+  auto flush = [&](std::vector<size_t>& run) {
+    // groups by kernel, in order of first appearance
+    std::vector<std::vector<size_t>> groups;
+    std::map<int, size_t> group_of;
+    for (size_t j : run) {
+      auto it = group_of.find(prog.steps[j].jit);
+      if (it == group_of.end()) {
+        group_of[prog.steps[j].jit] = groups.size();
+        groups.push_back({j});
+      } else {
+        groups[it->second].push_back(j);
+      }
+    }
+    for (const auto& g : groups) {
+      for (size_t c0 = 0; c0 < g.size(); c0 += kEwJitMaxBatch) {
+        const size_t cnt = std::min(g.size() - c0, size_t(kEwJitMaxBatch));
+        Step st = prog.steps[g[c0]];
+        if (cnt > 1) {
+          const int single = st.jit;
+          auto key = std::make_pair(single, int(cnt));
+          auto it = batched_kernel.find(key);
+          if (it == batched_kernel.end()) {
+            EwKernel bk;
+            if (!BatchEwKernel(jit.kernel(single), int(cnt), &bk)) {
+              for (size_t m = 0; m < cnt; ++m) out.push_back(prog.steps[g[c0 + m]]);
+              continue;
+            }
+            it = batched_kernel.emplace(key, jit.Add(std::move(bk))).first;
+          }
+          st.jit = it->second;
+          st.batch = int(cnt);
+          for (size_t m = 1; m < cnt; ++m)
+            st.bufs.insert(st.bufs.end(), prog.steps[g[c0 + m]].bufs.begin(), prog.steps[g[c0 + m]].bufs.end());
+          st.note += ", " + std::to_string(cnt) + " independent instances";
+        }
+        out.push_back(std::move(st));
+      }
+    }
+    run.clear();
+  };
+  std::vector<size_t> run;
+  std::vector<Acc> run_acc;
+  for (size_t j = 0; j < prog.steps.size(); ++j) {
+    const Step& st = prog.steps[j];
+    if (!batchable(st)) {
+      flush(run);
+      run_acc.clear();
+      out.push_back(st);
+      continue;
+    }
+    Acc a = access(st);
+    bool indep = true;
+    for (const Acc& b : run_acc)
+      if (Overlap(a.writes, b.reads) || Overlap(a.writes, b.writes) || Overlap(b.writes, a.reads)) {
+        indep = false;
+        break;
+      }
+    if (!indep) {
+      flush(run);
+      run_acc.clear();
+    }
+    run.push_back(j);
+    run_acc.push_back(std::move(a));
+  }
+  flush(run);
+  prog.steps = std::move(out);
+}
+
+}  // namespace
+
 CompileResult Compile(const char* code, size_t size, const CompileOptions& opts) {
   CompileResult r;
   std::unique_ptr<Module> m;
@@ -3807,6 +3945,7 @@ CompileResult Compile(const char* code, size_t size, const CompileOptions& opts)
     }
     if (jit->size()) {
       r.program->ew_jit = jit;
+      if (opts.ew_batch) BatchIndependentEwSteps(*r.program);
       if (opts.ew_jit_eager && !jit->Build()) r.program->patterns.push_back("ew_jit failed: " + jit->error());
     }
   }

@@ -46,6 +46,7 @@ struct Step {
   std::vector<int32_t> types;  // ew per-input dtypes
   std::string note;            // provenance for dumps / errors
   int jit = -1;                // ew: index of its generated kernel in Program::ew_jit (-1: interpreter)
+  int batch = 1;               // ew: independent instances of one program; bufs holds each one's in turn
 };
 
 struct ConstBlob {
@@ -94,6 +95,7 @@ struct CompileOptions {
   bool ew_jit = true;           // env JAM_NO_EW_JIT disables (ew steps run the interpreter)
   bool ew_jit_eager = false;    // env JAM_EW_JIT_EAGER: compile the generated kernels in Compile
   bool ew_jit_strict = false;   // env JAM_EW_JIT_STRICT: no interpreter fallback (EwJit::strict)
+  bool ew_batch = true;         // env JAM_NO_EW_BATCH disables batching independent ew steps
 };
 
 struct CompileResult {

@@ -67,7 +67,7 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   layernorm bufs x,g,b,y      i io_type,rows,cols  f eps
 //   gelu     bufs x,y           i io_type,n
 //   ew       bufs in...,out...  i rank,dims[6],n_inputs,(out_reg,out_type) per output  prog  strides[6n]
-//                               types[n]  f consts
+//                               types[n]  f consts  (batch > 1: bufs of each instance in turn)
 //   gather   bufs table,ids,out i n_rows,row_bytes,index_type,n_ids
 //   scatter_add bufs table,ids,updates,out,workspace  i dtype,n_rows,row_len,index_type,n_ids
 //   iota     bufs out           i out_type,rank,dim,dims...
@@ -117,21 +117,34 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     case StepKind::kGelu:
       return mk_gelu_tanh(st, int(i[0]), i[1], P(0), P(1));
     case StepKind::kEw: {
+      const int n_in = int(i[7]);
+      const int per = s.batch > 0 ? int(s.bufs.size()) / s.batch : 0;
+      const int n_out = per - n_in;
+      if (n_in > 8 || n_out < 1 || n_out > 4 || per * s.batch != int(s.bufs.size())) return MK_ERR_INVALID;
       if (s.jit >= 0 && f.jit_fns) {
         // the step's generated kernel, when every pointer has the alignment
-        // its vector accesses assume (otherwise the interpreter below)
+        // its vector accesses assume (otherwise the interpreter below); a
+        // batched kernel takes every instance's pointers in one struct
         const EwKernel& k = f.jit->kernel(s.jit);
-        void* ptrs[16];
-        bool aligned = s.bufs.size() <= 16;
-        for (size_t b = 0; aligned && b < s.bufs.size(); ++b) {
-          ptrs[b] = P(b);
-          aligned = reinterpret_cast<uintptr_t>(ptrs[b]) % k.align[b] == 0;
-        }
+        const int pi = n_in > 0 ? n_in : 1;
+        void* ptrs[kEwJitMaxBatch * 13];
+        bool aligned = (k.batch == 0 ? s.batch == 1 : k.batch == s.batch) && k.n_in == n_in && k.n_out == n_out;
+        for (int inst = 0; aligned && inst < s.batch; ++inst)
+          for (int b = 0; aligned && b < per; ++b) {
+            void* ptr = P(size_t(inst * per + b));
+            aligned = reinterpret_cast<uintptr_t>(ptr) % k.align[size_t(b)] == 0;
+            if (k.batch == 0) ptrs[b] = ptr;
+            else if (b < n_in) ptrs[inst * pi + b] = ptr;
+            else ptrs[s.batch * pi + inst * n_out + (b - n_in)] = ptr;
+          }
         if (aligned) {
           void* args[16];
-          for (size_t b = 0; b < s.bufs.size(); ++b) args[b] = &ptrs[b];
-          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[s.jit]), k.blocks, 1, 1,
-                                               kEwJitBlock, 1, 1, 0, stream, args, nullptr);
+          if (k.batch == 0)
+            for (int b = 0; b < per; ++b) args[b] = &ptrs[b];
+          else
+            args[0] = ptrs;
+          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[s.jit]), k.blocks * uint32_t(s.batch),
+                                               1, 1, kEwJitBlock, 1, 1, 0, stream, args, nullptr);
           if (e == hipSuccess) return MK_OK;
           *f.error = "hipModuleLaunchKernel(" + k.name + "): " + hipGetErrorString(e);
           return MK_ERR_LAUNCH;
@@ -141,24 +154,26 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
           return MK_ERR_INVALID;
         }
       }
-      const int n_in = int(i[7]);
-      const int n_out = int(s.bufs.size()) - n_in;
-      if (n_in > 8 || n_out < 1 || n_out > 4) return MK_ERR_INVALID;
-      const void* ins[8];
-      int types[8];
-      for (int k = 0; k < n_in; ++k) {
-        ins[k] = P(size_t(k));
-        types[k] = s.types[size_t(k)];
+      for (int inst = 0; inst < s.batch; ++inst) {
+        const void* ins[8];
+        int types[8];
+        for (int k = 0; k < n_in; ++k) {
+          ins[k] = P(size_t(inst * per + k));
+          types[k] = s.types[size_t(k)];
+        }
+        int regs[4], otypes[4];
+        void* outs[4];
+        for (int k = 0; k < n_out; ++k) {
+          regs[k] = int(i[8 + 2 * size_t(k)]);
+          otypes[k] = int(i[9 + 2 * size_t(k)]);
+          outs[k] = P(size_t(inst * per + n_in + k));
+        }
+        const int rc = mk_ew_program_multi(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(),
+                                           int(s.prog.size() / 4), s.prog.data(), s.f.data(), int(s.f.size()), n_out,
+                                           regs, otypes, outs);
+        if (rc != MK_OK) return rc;
       }
-      int regs[4], otypes[4];
-      void* outs[4];
-      for (int k = 0; k < n_out; ++k) {
-        regs[k] = int(i[8 + 2 * size_t(k)]);
-        otypes[k] = int(i[9 + 2 * size_t(k)]);
-        outs[k] = P(size_t(n_in + k));
-      }
-      return mk_ew_program_multi(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
-                                 s.prog.data(), s.f.data(), int(s.f.size()), n_out, regs, otypes, outs);
+      return MK_OK;
     }
     case StepKind::kGather:
       return mk_gather_rows(st, i[0], i[1], P(0), int(i[2]), i[3], P(1), P(2));
