@@ -180,191 +180,264 @@ void ReplaceAll(std::string& s, const std::string& from, const std::string& to) 
 
 }  // namespace
 
-// Step encoding (lower.cc EmitEwGroup): bufs = inputs then outputs; i = rank,
-// dims[6], n_inputs, (out_reg, out_type) per output; prog 4 ints per
-// instruction; strides 6 per input; types per input; f = constants.
-bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
-  auto no = [&](const std::string& w) {
-    *why = w;
-    return false;
-  };
-  if (s.kind != StepKind::kEw || s.i.size() < 8) return no("not an ew step");
-  const int rank = int(s.i[0]);
-  const int n_in = int(s.i[7]);
-  const int n_out = int(s.bufs.size()) - n_in;
-  if (rank < 0 || rank > kMaxRank) return no("rank");
-  if (n_in < 0 || n_in > kMaxInputs || n_out < 1 || n_out > kMaxOutputs) return no("operand count");
-  if (s.i.size() != size_t(8 + 2 * n_out) || s.strides.size() != size_t(kMaxRank * n_in) ||
-      s.types.size() != size_t(n_in) || s.prog.size() % 4 != 0)
-    return no("malformed step");
-  int64_t dims[kMaxRank];
+namespace {
+
+// The iteration space of a program and how each input is read in it (the
+// interpreter's modes; size-1 dims never contribute).
+enum Mode { kScalarIn, kDenseIn, kStridedIn };
+struct IterSpace {
+  int rank = 0;
+  int64_t dims[kMaxRank] = {};
   int64_t n = 1;
+  int n_in = 0;
+  std::vector<Mode> mode;
+  std::vector<std::array<int64_t, kMaxRank>> st;
+  std::vector<int> types;
+  bool narrow = true;  // every index and offset fits 32 bits
+};
+
+bool Analyze(int rank, const int64_t* dims, int n_in, const std::vector<int64_t>& strides,
+             const std::vector<int32_t>& types, IterSpace* sp, std::string* why) {
+  if (rank < 0 || rank > kMaxRank) return (*why = "rank", false);
+  if (n_in < 0 || n_in > kMaxInputs) return (*why = "operand count", false);
+  if (strides.size() != size_t(kMaxRank * n_in) || types.size() != size_t(n_in))
+    return (*why = "malformed step", false);
+  sp->rank = rank;
+  sp->n = 1;
   for (int d = 0; d < rank; ++d) {
-    dims[d] = s.i[1 + size_t(d)];
-    if (dims[d] < 0) return no("negative dim");
-    n *= dims[d];
+    if (dims[d] < 0) return (*why = "negative dim", false);
+    sp->dims[d] = dims[d];
+    sp->n *= dims[d];
   }
-  k->align.assign(s.bufs.size(), 1);
-  if (n == 0) {
-    k->blocks = 0;
-    k->name.clear();
-    k->source.clear();
-    return true;
-  }
-  // inputs: the interpreter's modes (size-1 dims never contribute)
-  enum Mode { kScalar, kDense, kStrided };
-  std::vector<Mode> mode(static_cast<size_t>(n_in));
-  std::vector<std::array<int64_t, kMaxRank>> st(static_cast<size_t>(n_in));
-  bool narrow = rank >= 1 && n < (int64_t(1) << 31);
+  sp->n_in = n_in;
+  sp->narrow = rank >= 1 && sp->n < (int64_t(1) << 31);
+  sp->mode.assign(size_t(n_in), kScalarIn);
+  sp->st.assign(size_t(n_in), {});
+  sp->types.assign(types.begin(), types.end());
   for (int t = 0; t < n_in; ++t) {
     int64_t expect = 1, hi = 0;
     bool dense = true, scalar = true;
     for (int d = rank - 1; d >= 0; --d) {
-      const int64_t v = dims[d] == 1 ? 0 : s.strides[size_t(t * kMaxRank + d)];
-      st[size_t(t)][size_t(d)] = v;
+      const int64_t v = dims[d] == 1 ? 0 : strides[size_t(t * kMaxRank + d)];
+      sp->st[size_t(t)][size_t(d)] = v;
       if (dims[d] != 1 && v != expect) dense = false;
       if (dims[d] != 1 && v != 0) scalar = false;
-      if (v < 0) narrow = false;
+      if (v < 0) sp->narrow = false;
       hi += (dims[d] - 1) * v;
       expect *= dims[d];
     }
-    if (hi >= (int64_t(1) << 31) - kLanes) narrow = false;
-    mode[size_t(t)] = scalar ? kScalar : (dense ? kDense : kStrided);
+    if (hi >= (int64_t(1) << 31) - kLanes) sp->narrow = false;
+    sp->mode[size_t(t)] = scalar ? kScalarIn : (dense ? kDenseIn : kStridedIn);
     std::string probe;
-    if (!LoadExpr(s.types[size_t(t)], "p", "0", &probe)) return no("input dtype");
+    if (!LoadExpr(types[size_t(t)], "p", "0", &probe)) return (*why = "input dtype", false);
+  }
+  return true;
+}
+
+// The program as a straight-line __device__ function of one element's
+// inputs x0.. writing the registers `out_regs` to y[0..].
+bool BodyFn(const std::vector<int32_t>& prog, const std::vector<float>& consts, int n_in,
+            const std::vector<int>& out_regs, std::ostringstream& src, std::string* why) {
+  if (prog.size() % 4 != 0) return (*why = "malformed program", false);
+  std::string reg[kMaxRegs];
+  for (int r = 0; r < kMaxRegs; ++r) reg[r] = r < n_in ? "x" + std::to_string(r) : "0.f";
+  src << "static __device__ __forceinline__ void @K@_body(";
+  for (int t = 0; t < n_in; ++t) src << "float x" << t << ", ";
+  src << "float* y) {\n#pragma clang fp contract(off)\n";
+  for (size_t p = 0; p < prog.size() / 4; ++p) {
+    const int op = prog[4 * p], dst = prog[4 * p + 1], a = prog[4 * p + 2], b = prog[4 * p + 3];
+    if (dst < 0 || dst >= kMaxRegs) return (*why = "destination register", false);
+    std::string e;
+    if (op == MK_EW_CONST) {
+      if (a < 0 || size_t(a) >= consts.size()) return (*why = "constant index", false);
+      e = FloatLit(consts[size_t(a)]);
+    } else {
+      const int rb = b & 0xffff, rc = (b >> 16) & 0xffff;
+      if (a < 0 || a >= kMaxRegs || rb >= kMaxRegs || rc >= kMaxRegs) return (*why = "source register", false);
+      if (!InstrExpr(op, reg[a], reg[rb], reg[rc], &e)) return (*why = "opcode " + std::to_string(op), false);
+    }
+    src << "  const float v" << p << " = " << e << ";\n";
+    reg[dst] = "v" + std::to_string(p);
+  }
+  for (size_t o = 0; o < out_regs.size(); ++o) {
+    if (out_regs[o] < 0 || out_regs[o] >= kMaxRegs) return (*why = "output register", false);
+    src << "  y[" << o << "] = " << reg[out_regs[o]] << ";\n";
+  }
+  src << "}\n";
+  return true;
+}
+
+// Index decomposition of the linear element index `i0` (lanes consecutive
+// elements per thread: the innermost dim is a multiple of lanes) and the
+// loads of every input; x[t][l] names input t's fp32 value in lane l.  Vector
+// loads (4 consecutive f32 / bf16 elements, unit inner stride, the other
+// strides multiples of 4) record the byte alignment the input's pointer
+// needs in align[t].
+void EmitLoads(const IterSpace& sp, int lanes, const std::string& i0, const std::string& ind,
+               std::ostringstream& src, std::vector<std::array<std::string, kLanes>>* x,
+               std::vector<uint8_t>* align) {
+  const std::string IT = sp.narrow ? "unsigned" : "long long";
+  const std::string U = sp.narrow ? "u" : "ll";
+  const int rank = sp.rank;
+  // multi-dim index: only as far out as some strided input needs
+  int lo = rank;
+  for (int t = 0; t < sp.n_in; ++t)
+    if (sp.mode[size_t(t)] == kStridedIn)
+      for (int d = 0; d < rank; ++d)
+        if (sp.st[size_t(t)][size_t(d)] != 0) lo = std::min(lo, d);
+  if (lo < rank) {
+    src << ind << IT << " r_ = " << i0 << ";\n";
+    for (int d = rank - 1; d >= lo; --d) {
+      if (d == 0) {
+        src << ind << "const " << IT << " d0 = r_;\n";
+      } else {
+        src << ind << "const " << IT << " d" << d << " = r_ % " << sp.dims[d] << U << ";\n";
+        if (d > lo) src << ind << "r_ /= " << sp.dims[d] << U << ";\n";
+      }
+    }
+  }
+  x->assign(size_t(sp.n_in), {});
+  for (int t = 0; t < sp.n_in; ++t) {
+    const int ty = sp.types[size_t(t)];
+    const std::string p = "p" + std::to_string(t), tn = std::to_string(t);
+    std::string off, e;
+    int64_t step = 0;
+    if (sp.mode[size_t(t)] == kScalarIn) {
+      LoadExpr(ty, p, "0", &e);
+      src << ind << "const float x" << tn << " = " << e << ";\n";
+      for (int l = 0; l < lanes; ++l) (*x)[size_t(t)][size_t(l)] = "x" + tn;
+      continue;
+    }
+    if (sp.mode[size_t(t)] == kDenseIn) {
+      off = i0;
+      step = 1;
+    } else {
+      std::string sum;
+      for (int d = lo; d < rank; ++d) {
+        const int64_t v = sp.st[size_t(t)][size_t(d)];
+        if (v == 0) continue;
+        sum += (sum.empty() ? "" : " + ") + std::string("d") + std::to_string(d) +
+               (v == 1 ? "" : " * " + std::to_string(v) + U);
+      }
+      src << ind << "const " << IT << " o" << tn << " = " << sum << ";\n";
+      off = "o" + tn;
+      step = sp.st[size_t(t)][size_t(rank - 1)];
+    }
+    bool vec = lanes == kLanes && step == 1 && (ty == MK_F32 || ty == MK_BF16);
+    for (int d = 0; vec && d + 1 < rank; ++d)
+      if (sp.st[size_t(t)][size_t(d)] % kLanes != 0) vec = false;
+    if (vec && ty == MK_F32) {
+      src << ind << "const mkj_f4 w" << tn << " = *(const mkj_f4*)((const float*)" << p << " + " << off << ");\n";
+      for (int l = 0; l < lanes; ++l) (*x)[size_t(t)][size_t(l)] = "w" + tn + "[" + std::to_string(l) + "]";
+      (*align)[size_t(t)] = 16;
+    } else if (vec) {
+      src << ind << "const mkj_u2 w" << tn << " = *(const mkj_u2*)((const unsigned short*)" << p << " + " << off
+          << ");\n";
+      for (int l = 0; l < lanes; ++l) {
+        src << ind << "const float x" << tn << "_" << l << " = mkj_bf2f((unsigned short)(w" << tn << "[" << l / 2
+            << "]" << (l % 2 ? " >> 16" : "") << "));\n";
+        (*x)[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
+      }
+      (*align)[size_t(t)] = 8;
+    } else if (step == 0 || lanes == 1) {
+      LoadExpr(ty, p, off, &e);
+      src << ind << "const float x" << tn << " = " << e << ";\n";
+      for (int l = 0; l < lanes; ++l) (*x)[size_t(t)][size_t(l)] = "x" + tn;
+    } else {
+      for (int l = 0; l < lanes; ++l) {
+        const std::string ol = l == 0 ? off : "(" + off + " + " + std::to_string(int64_t(l) * step) + U + ")";
+        LoadExpr(ty, p, ol, &e);
+        src << ind << "const float x" << tn << "_" << l << " = " << e << ";\n";
+        (*x)[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
+      }
+    }
+  }
+}
+
+// Names the kernel by its text's hash and fills the entry fields.
+void Finish(std::string helpers, std::string entry, EwKernel* k) {
+  char name[32];
+  snprintf(name, sizeof name, "ew_%016" PRIx64, Fnv1a(helpers + entry));
+  ReplaceAll(helpers, "@K@", name);
+  ReplaceAll(entry, "@K@", name);
+  k->name = name;
+  k->base = name;
+  k->helpers = std::move(helpers);
+  k->source = k->helpers + entry;
+}
+
+// fp32 value rounded to the type a materialized value would have
+std::string RoundTo(int type, const std::string& v) {
+  if (type == MK_BF16) return "mkj_bf2f(mkj_f2bf(" + v + "))";
+  if (type == MK_F16) return "mkj_h2f(mkj_f2h(" + v + "))";
+  return v;
+}
+
+// Row chunks of a sum over leading dims: enough blocks (tiles x chunks)
+// to fill the chip, at most 512 chunks, every chunk non-empty.
+int64_t ReduceChunks(int64_t rows, int64_t tiles) {
+  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>({rows, (1024 + tiles - 1) / tiles, int64_t(512)}));
+  const int64_t rpc = (rows + chunks - 1) / chunks;
+  return (rows + rpc - 1) / rpc;
+}
+
+std::string Combine(int rop, const std::string& a, const std::string& b) {
+  switch (rop) {
+    case 0: return "(" + a + " + " + b + ")";
+    case 1: return "fmaxf(" + a + ", " + b + ")";
+    case 2: return "fminf(" + a + ", " + b + ")";
+    default: return "(" + a + " * " + b + ")";
+  }
+}
+
+}  // namespace
+
+// Step encoding (lower.cc EmitEwGroup): bufs = inputs then outputs; i = rank,
+// dims[6], n_inputs, (out_reg, out_type) per output; prog 4 ints per
+// instruction; strides 6 per input; types per input; f = constants.
+bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
+  if (s.kind == StepKind::kEwReduce) return GenerateEwReduceKernel(s, k, why);
+  if (s.kind != StepKind::kEw || s.i.size() < 8) return (*why = "not an ew step", false);
+  const int rank = int(s.i[0]);
+  const int n_in = int(s.i[7]);
+  const int n_out = int(s.bufs.size()) - n_in;
+  if (n_out < 1 || n_out > kMaxOutputs || s.i.size() != size_t(8 + 2 * n_out)) return (*why = "operand count", false);
+  IterSpace sp;
+  if (rank < 0 || rank > kMaxRank || !Analyze(rank, &s.i[1], n_in, s.strides, s.types, &sp, why)) return false;
+  k->align.assign(s.bufs.size(), 1);
+  if (sp.n == 0) {
+    k->blocks = 0;
+    k->name.clear();
+    k->source.clear();
+    return true;
   }
   std::vector<int> out_reg(static_cast<size_t>(n_out)), out_type(static_cast<size_t>(n_out));
   for (int o = 0; o < n_out; ++o) {
     out_reg[size_t(o)] = int(s.i[8 + 2 * size_t(o)]);
     out_type[size_t(o)] = int(s.i[9 + 2 * size_t(o)]);
     std::string probe;
-    if (out_reg[size_t(o)] < 0 || out_reg[size_t(o)] >= kMaxRegs) return no("output register");
-    if (!StoreStmt(out_type[size_t(o)], "q", "0", "v", &probe)) return no("output dtype");
+    if (!StoreStmt(out_type[size_t(o)], "q", "0", "v", &probe)) return (*why = "output dtype", false);
   }
-  const int lanes = rank >= 1 && dims[rank - 1] % kLanes == 0 ? kLanes : 1;
-  const int64_t threads = n / lanes;
-  const int64_t blocks = (threads + kEwJitBlock - 1) / kEwJitBlock;
-  if (blocks >= (int64_t(1) << 31)) return no("grid too large");
-  const std::string IT = narrow ? "unsigned" : "long long";
-  const std::string U = narrow ? "u" : "ll";
+  const int lanes = rank >= 1 && sp.dims[rank - 1] % kLanes == 0 ? kLanes : 1;
+  const int64_t blocks = (sp.n / lanes + kEwJitBlock - 1) / kEwJitBlock;
+  if (blocks >= (int64_t(1) << 31)) return (*why = "grid too large", false);
+  const std::string U = sp.narrow ? "u" : "ll";
 
   std::ostringstream src;
   src << "#ifndef @K@_DEF\n#define @K@_DEF\n";
-  // ---- the program as a straight-line function of one element's inputs
-  {
-    std::string reg[kMaxRegs];
-    for (int r = 0; r < kMaxRegs; ++r) reg[r] = r < n_in ? "x" + std::to_string(r) : "0.f";
-    src << "static __device__ __forceinline__ void @K@_body(";
-    for (int t = 0; t < n_in; ++t) src << "float x" << t << ", ";
-    src << "float* y) {\n#pragma clang fp contract(off)\n";
-    const size_t n_instr = s.prog.size() / 4;
-    for (size_t p = 0; p < n_instr; ++p) {
-      const int op = s.prog[4 * p], dst = s.prog[4 * p + 1], a = s.prog[4 * p + 2], b = s.prog[4 * p + 3];
-      if (dst < 0 || dst >= kMaxRegs) return no("destination register");
-      std::string e;
-      if (op == MK_EW_CONST) {
-        if (a < 0 || size_t(a) >= s.f.size()) return no("constant index");
-        e = FloatLit(s.f[size_t(a)]);
-      } else {
-        const int rb = b & 0xffff, rc = (b >> 16) & 0xffff;
-        if (a < 0 || a >= kMaxRegs || rb >= kMaxRegs || rc >= kMaxRegs) return no("source register");
-        if (!InstrExpr(op, reg[a], reg[rb], reg[rc], &e)) return no("opcode " + std::to_string(op));
-      }
-      src << "  const float v" << p << " = " << e << ";\n";
-      reg[dst] = "v" + std::to_string(p);
-    }
-    for (int o = 0; o < n_out; ++o) src << "  y[" << o << "] = " << reg[out_reg[size_t(o)]] << ";\n";
-    src << "}\n";
-  }
-  // ---- one block's work (block blk of the step's grid): index, loads,
-  // lanes, stores
+  if (!BodyFn(s.prog, s.f, n_in, out_reg, src, why)) return false;
+  // one block's work (block blk of the step's grid)
   std::string params;
   for (int t = 0; t < n_in; ++t) params += "const void* p" + std::to_string(t) + ", ";
   for (int o = 0; o < n_out; ++o) params += "void* q" + std::to_string(o) + (o + 1 < n_out ? ", " : "");
   src << "static __device__ __forceinline__ void @K@_run(unsigned blk, " << params << ") {\n";
-  if (narrow)
+  if (sp.narrow)
     src << "  const unsigned i0 = (blk * " << kEwJitBlock << "u + threadIdx.x) * " << lanes << "u;\n";
   else
     src << "  const long long i0 = ((long long)blk * " << kEwJitBlock << " + threadIdx.x) * " << lanes << ";\n";
-  src << "  if (i0 >= " << n << U << ") return;\n";
-  // multi-dim index: only as far out as some strided input needs
-  int lo = rank;
-  for (int t = 0; t < n_in; ++t)
-    if (mode[size_t(t)] == kStrided)
-      for (int d = 0; d < rank; ++d)
-        if (st[size_t(t)][size_t(d)] != 0) lo = std::min(lo, d);
-  if (lo < rank) {
-    src << "  " << IT << " r_ = i0;\n";
-    for (int d = rank - 1; d >= lo; --d) {
-      if (d == 0) {
-        src << "  const " << IT << " d0 = r_;\n";
-      } else {
-        src << "  const " << IT << " d" << d << " = r_ % " << dims[d] << U << ";\n";
-        if (d > lo) src << "  r_ /= " << dims[d] << U << ";\n";
-      }
-    }
-  }
-  // per input and lane: the fp32 value name
-  std::vector<std::array<std::string, kLanes>> x(static_cast<size_t>(n_in));
-  for (int t = 0; t < n_in; ++t) {
-    const int ty = s.types[size_t(t)];
-    const std::string p = "p" + std::to_string(t);
-    const std::string tn = std::to_string(t);
-    std::string off, e;
-    int64_t step = 0;
-    if (mode[size_t(t)] == kScalar) {
-      LoadExpr(ty, p, "0", &e);
-      src << "  const float x" << tn << " = " << e << ";\n";
-      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "x" + tn;
-      continue;
-    }
-    if (mode[size_t(t)] == kDense) {
-      off = "i0";
-      step = 1;
-    } else {
-      std::string sum;
-      for (int d = lo; d < rank; ++d) {
-        const int64_t v = st[size_t(t)][size_t(d)];
-        if (v == 0) continue;
-        sum += (sum.empty() ? "" : " + ") + std::string("d") + std::to_string(d) +
-               (v == 1 ? "" : " * " + std::to_string(v) + U);
-      }
-      src << "  const " << IT << " o" << tn << " = " << sum << ";\n";
-      off = "o" + tn;
-      step = st[size_t(t)][size_t(rank - 1)];
-    }
-    // vector form: 4 consecutive f32 / bf16 elements adjacent and aligned
-    // (unit inner stride, every other stride a multiple of 4 elements; the
-    // base pointer's alignment is checked at launch)
-    bool vec = lanes == kLanes && step == 1 && (ty == MK_F32 || ty == MK_BF16);
-    for (int d = 0; vec && d + 1 < rank; ++d)
-      if (st[size_t(t)][size_t(d)] % kLanes != 0) vec = false;
-    if (vec && ty == MK_F32) {
-      src << "  const mkj_f4 w" << tn << " = *(const mkj_f4*)((const float*)" << p << " + " << off << ");\n";
-      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "w" + tn + "[" + std::to_string(l) + "]";
-      k->align[size_t(t)] = 16;
-    } else if (vec) {
-      src << "  const mkj_u2 w" << tn << " = *(const mkj_u2*)((const unsigned short*)" << p << " + " << off
-          << ");\n";
-      for (int l = 0; l < lanes; ++l) {
-        src << "  const float x" << tn << "_" << l << " = mkj_bf2f((unsigned short)(w" << tn << "[" << l / 2 << "]"
-            << (l % 2 ? " >> 16" : "") << "));\n";
-        x[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
-      }
-      k->align[size_t(t)] = 8;
-    } else if (step == 0 || lanes == 1) {
-      LoadExpr(ty, p, off, &e);
-      src << "  const float x" << tn << " = " << e << ";\n";
-      for (int l = 0; l < lanes; ++l) x[size_t(t)][size_t(l)] = "x" + tn;
-    } else {
-      for (int l = 0; l < lanes; ++l) {
-        const std::string ol = l == 0 ? off : "(" + off + " + " + std::to_string(int64_t(l) * step) + U + ")";
-        LoadExpr(ty, p, ol, &e);
-        src << "  const float x" << tn << "_" << l << " = " << e << ";\n";
-        x[size_t(t)][size_t(l)] = "x" + tn + "_" + std::to_string(l);
-      }
-    }
-  }
+  src << "  if (i0 >= " << sp.n << U << ") return;\n";
+  std::vector<std::array<std::string, kLanes>> x;
+  EmitLoads(sp, lanes, "i0", "  ", src, &x, &k->align);
   for (int l = 0; l < lanes; ++l) {
     src << "  float y" << l << "[" << n_out << "];\n  @K@_body(";
     for (int t = 0; t < n_in; ++t) src << x[size_t(t)][size_t(l)] << ", ";
@@ -392,20 +465,13 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
     }
   }
   src << "}\n#endif\n";
-  std::string helpers = src.str();
   std::string args;
   for (int t = 0; t < n_in; ++t) args += ", p" + std::to_string(t);
   for (int o = 0; o < n_out; ++o) args += ", q" + std::to_string(o);
-  std::string entry = "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kEwJitBlock) + ") @K@(" +
-                      params + ") { @K@_run(blockIdx.x" + args + "); }\n";
-  char name[32];
-  snprintf(name, sizeof name, "ew_%016" PRIx64, Fnv1a(helpers + entry));
-  ReplaceAll(helpers, "@K@", name);
-  ReplaceAll(entry, "@K@", name);
-  k->name = name;
-  k->base = name;
-  k->helpers = std::move(helpers);
-  k->source = k->helpers + entry;
+  const std::string entry = "extern \"C\" __global__ void __launch_bounds__(" + std::to_string(kEwJitBlock) +
+                            ") @K@(" + params + ") { @K@_run(blockIdx.x" + args + "); }\n";
+  Finish(src.str(), entry, k);
+  k->kind = 0;
   k->blocks = uint32_t(blocks);
   k->n_in = n_in;
   k->n_out = n_out;
@@ -413,8 +479,148 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
   return true;
 }
 
+// Reduction of an ew program's value (lower.cc LowerReduce): bufs = inputs,
+// out, tmp, ws; i = rank, dims[6] (the iteration space), n_inputs, out_reg,
+// val_type, out_type, rop, rows, cols, mode, init bits.  Mode 0 reduces the
+// trailing dims (rows = kept elements, cols = reduced per row), one wave per
+// row; mode 1 sums the leading dims (rows = reduced, cols = kept), partial
+// sums of row chunks into ws, then a second kernel adds the chunks.  The
+// value is rounded to val_type before it is combined, as the materialized
+// value would be.
+bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
+  if (s.kind != StepKind::kEwReduce || s.i.size() != 16) return (*why = "not an ew reduce step", false);
+  const int rank = int(s.i[0]), n_in = int(s.i[7]), out_reg = int(s.i[8]), val_type = int(s.i[9]),
+            out_type = int(s.i[10]), rop = int(s.i[11]), mode = int(s.i[14]);
+  const int64_t rows = s.i[12], cols = s.i[13];
+  uint32_t init_bits = uint32_t(s.i[15]);
+  float init;
+  memcpy(&init, &init_bits, 4);
+  if (s.bufs.size() != size_t(n_in + 3)) return (*why = "malformed ew reduce step", false);
+  IterSpace sp;
+  if (rank < 1 || rank > kMaxRank || !Analyze(rank, &s.i[1], n_in, s.strides, s.types, &sp, why)) return false;
+  if (rows * cols != sp.n || rows <= 0 || cols <= 0) return (*why = "empty or inconsistent reduction", false);
+  if (rop < 0 || rop > 3 || (mode == 1 && (rop != 0 || out_type != MK_F32))) return (*why = "reduction kind", false);
+  if (val_type != MK_F32 && val_type != MK_BF16 && val_type != MK_F16) return (*why = "value type", false);
+  std::string probe;
+  if (!StoreStmt(out_type, "q", "0", "v", &probe)) return (*why = "output dtype", false);
+  k->align.assign(s.bufs.size(), 1);
+  const int lanes = sp.dims[rank - 1] % kLanes == 0 && cols % kLanes == 0 ? kLanes : 1;
+  const std::string IT = sp.narrow ? "unsigned" : "long long";
+  const std::string U = sp.narrow ? "u" : "ll";
+  static const char* kIdentity[] = {"0.f", "-__builtin_inff()", "__builtin_inff()", "1.f"};
+
+  std::ostringstream src;
+  src << "#ifndef @K@_DEF\n#define @K@_DEF\n";
+  if (!BodyFn(s.prog, s.f, n_in, {out_reg}, src, why)) return false;
+  src << "#endif\n";
+  std::string params;
+  for (int t = 0; t < n_in; ++t) params += "const void* p" + std::to_string(t) + ", ";
+  std::ostringstream e;
+  // per element: loads, the program, rounding, combine into the lane's acc
+  auto element = [&](const std::string& i0, const std::string& ind, const std::string& acc, bool per_lane) {
+    std::vector<std::array<std::string, kLanes>> x;
+    e << ind << "{\n";
+    EmitLoads(sp, lanes, i0, ind + "  ", e, &x, &k->align);
+    for (int l = 0; l < lanes; ++l) {
+      e << ind << "  float y" << l << "[1];\n" << ind << "  @K@_body(";
+      for (int t = 0; t < n_in; ++t) e << x[size_t(t)][size_t(l)] << ", ";
+      e << "y" << l << ");\n";
+      const std::string v = RoundTo(val_type, "y" + std::to_string(l) + "[0]");
+      const std::string a = per_lane ? acc + "[" + std::to_string(l) + "]" : acc;
+      e << ind << "  { const float v = " << v << ";";
+      if (rop == 1 || rop == 2) e << " nan_ |= v != v;";
+      e << " " << a << " = " << Combine(rop, a, "v") << "; }\n";
+    }
+    e << ind << "}\n";
+  };
+  if (mode == 0) {
+    // one wave per row, lanes x 64 columns per iteration
+    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "void* q0) {\n";
+    e << "#pragma clang fp contract(off)\n  const unsigned lane = threadIdx.x & 63u;\n";
+    e << "  const " << IT << " row = (" << IT << ")blockIdx.x * " << kEwJitBlock / 64 << " + (threadIdx.x >> 6);\n";
+    e << "  if (row >= " << rows << U << ") return;\n";
+    e << "  float acc = " << kIdentity[rop] << ";\n  bool nan_ = false;\n";
+    e << "  for (" << IT << " c = lane * " << lanes << U << "; c < " << cols << U << "; c += " << 64 * lanes << U
+      << ") {\n";
+    e << "    const " << IT << " i0 = row * " << cols << U << " + c;\n";
+    element("i0", "    ", "acc", false);
+    e << "  }\n";
+    for (int m = 32; m >= 1; m /= 2) e << "  acc = " << Combine(rop, "acc", "__shfl_xor(acc, " + std::to_string(m) + ")") << ";\n";
+    e << "  const bool any_nan = __any(nan_);\n  (void)any_nan;\n";
+    e << "  if (lane == 0) {\n    float r = " << Combine(rop, "acc", FloatLit(init)) << ";\n";
+    if (rop == 1 || rop == 2) e << "    if (any_nan || " << (init != init ? "true" : "false") << ") r = __builtin_nanf(\"\");\n";
+    std::string stmt;
+    StoreStmt(out_type, "q0", "row", "r", &stmt);
+    e << "    " << stmt << "\n  }\n}\n";
+    k->blocks = uint32_t((rows + kEwJitBlock / 64 - 1) / (kEwJitBlock / 64));
+    k->kind = 1;
+    k->chunks = 0;
+  } else {
+    // column tiles of 64 x lanes columns; row chunks; 4 waves per block
+    // take every 4th row of the chunk; partial sums to ws[chunk][col]
+    const int64_t tile_cols = 64 * lanes;
+    const int64_t tiles = (cols + tile_cols - 1) / tile_cols;
+    const int64_t chunks = ReduceChunks(rows, tiles);
+    const int64_t rpc = (rows + chunks - 1) / chunks;
+    if (tiles * chunks >= (int64_t(1) << 31)) return (*why = "grid too large", false);
+    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "float* ws) {\n";
+    e << "#pragma clang fp contract(off)\n  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n";
+    e << "  const unsigned tile = blockIdx.x % " << tiles << "u, chunk = blockIdx.x / " << tiles << "u;\n";
+    e << "  const " << IT << " c = (" << IT << ")tile * " << tile_cols << U << " + lane * " << lanes << U << ";\n";
+    e << "  float acc[" << lanes << "] = {};\n  bool nan_ = false;\n  (void)nan_;\n";
+    e << "  if (c < " << cols << U << ") {\n";
+    e << "    const " << IT << " r1 = (" << IT << ")(chunk + 1) * " << rpc << U << " < " << rows << U << " ? (" << IT
+      << ")(chunk + 1) * " << rpc << U << " : " << rows << U << ";\n";
+    e << "    for (" << IT << " r = (" << IT << ")chunk * " << rpc << U << " + wave; r < r1; r += 4) {\n";
+    e << "      const " << IT << " i0 = r * " << cols << U << " + c;\n";
+    element("i0", "      ", "acc", true);
+    e << "    }\n  }\n";
+    e << "  __shared__ float red_[4][" << tile_cols << "];\n";
+    for (int l = 0; l < lanes; ++l) e << "  red_[wave][lane * " << lanes << " + " << l << "] = acc[" << l << "];\n";
+    e << "  __syncthreads();\n";
+    e << "  if (wave == 0 && c < " << cols << U << ") {\n";
+    for (int l = 0; l < lanes; ++l)
+      e << "    ws[(" << IT << ")chunk * " << cols << U << " + c + " << l << "] = ((red_[0][lane * " << lanes << " + "
+        << l << "] + red_[1][lane * " << lanes << " + " << l << "]) + red_[2][lane * " << lanes << " + " << l
+        << "]) + red_[3][lane * " << lanes << " + " << l << "];\n";
+    e << "  }\n}\n";
+    // the chunks' partial sums: 64 columns per block, wave w adding chunks
+    // w, w + 4, ..., then the four waves' totals in order
+    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@_final(const float* ws, void* q0) {\n";
+    e << "#pragma clang fp contract(off)\n";
+    e << "  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n";
+    e << "  const " << IT << " c = (" << IT << ")blockIdx.x * 64" << U << " + lane;\n";
+    e << "  float s = 0.f;\n";
+    e << "  if (c < " << cols << U << ")\n";
+    e << "    for (" << IT << " j = wave; j < " << chunks << U << "; j += 4) s += ws[j * " << cols << U << " + c];\n";
+    e << "  __shared__ float part_[4][64];\n  part_[wave][lane] = s;\n  __syncthreads();\n";
+    e << "  if (wave != 0 || c >= " << cols << U << ") return;\n";
+    e << "  s = ((part_[0][lane] + part_[1][lane]) + part_[2][lane]) + part_[3][lane];\n";
+    e << "  s = s + " << FloatLit(init) << ";\n";
+    std::string stmt;
+    StoreStmt(out_type, "q0", "c", "s", &stmt);
+    e << "  " << stmt << "\n}\n";
+    k->blocks = uint32_t(tiles * chunks);
+    k->final_blocks = uint32_t((cols + 63) / 64);
+    k->kind = 2;
+    k->chunks = chunks;
+  }
+  Finish(src.str(), e.str(), k);
+  if (k->kind == 2) k->final_name = k->name + "_final";
+  k->n_in = n_in;
+  k->n_out = 1;
+  k->batch = 0;
+  return true;
+}
+
+int64_t EwReduceWorkspaceBytes(int64_t rows, int64_t cols, int64_t inner) {
+  const int lanes = inner % kLanes == 0 && cols % kLanes == 0 ? kLanes : 1;
+  const int64_t tile_cols = 64 * lanes;
+  return ReduceChunks(rows, (cols + tile_cols - 1) / tile_cols) * cols * 4;
+}
+
 bool BatchEwKernel(const EwKernel& single, int batch, EwKernel* k) {
-  if (single.batch != 0 || batch < 2 || batch > kEwJitMaxBatch) return false;
+  if (single.kind != 0 || single.batch != 0 || batch < 2 || batch > kEwJitMaxBatch) return false;
   if (int64_t(single.blocks) * batch >= (int64_t(1) << 31)) return false;
   *k = single;
   k->batch = batch;
@@ -602,7 +808,7 @@ void* const* EwJit::Functions(int ordinal) {
   if (!error_.empty()) return nullptr;  // a failed load is not retried
   if (fns_.size() <= size_t(ordinal)) fns_.resize(size_t(ordinal) + 1);
   std::vector<void*>& f = fns_[size_t(ordinal)];
-  if (f.size() == kernels_.size()) return f.data();
+  if (f.size() == 2 * kernels_.size()) return f.data();
   hipModule_t mod = nullptr;
   {
     std::lock_guard<std::mutex> cl(code_->mu);
@@ -619,13 +825,17 @@ void* const* EwJit::Functions(int ordinal) {
   }
   std::vector<void*> out;
   for (const EwKernel& k : kernels_) {
-    hipFunction_t fn = nullptr;
-    hipError_t e = hipModuleGetFunction(&fn, mod, k.name.c_str());
-    if (e != hipSuccess) {
-      error_ = "hipModuleGetFunction(" + k.name + "): " + hipGetErrorString(e);
-      return nullptr;
+    for (const std::string* name : {&k.name, &k.final_name}) {
+      hipFunction_t fn = nullptr;
+      if (!name->empty()) {
+        hipError_t e = hipModuleGetFunction(&fn, mod, name->c_str());
+        if (e != hipSuccess) {
+          error_ = "hipModuleGetFunction(" + *name + "): " + hipGetErrorString(e);
+          return nullptr;
+        }
+      }
+      out.push_back(reinterpret_cast<void*>(fn));
     }
-    out.push_back(reinterpret_cast<void*>(fn));
   }
   f = std::move(out);
   return f.data();

@@ -38,6 +38,13 @@ struct EwKernel {
   std::string source;     // helpers and the extern "C" __global__ entry
   uint32_t blocks = 0;    // grid of one instance (kEwJitBlock threads per block); 0: nothing to do
   int n_in = 0, n_out = 0;
+  // 0: elementwise; 1: reduction of the program's value over trailing dims
+  // (one launch); 2: sum over leading dims (this entry writes partial sums
+  // of `chunks` row chunks, then `final_name` on `final_blocks` blocks adds them)
+  int kind = 0;
+  std::string final_name;
+  uint32_t final_blocks = 0;
+  int64_t chunks = 0;
   // 0: the entry takes the step's pointers; k >= 2: it takes a struct of k
   // instances' pointers (inputs p[k][t], outputs q[k][o]) and a grid of
   // instances x blocks, block b running block b % blocks of instance
@@ -51,6 +58,12 @@ struct EwKernel {
 // Writes the kernel of ew step `s`; false with `why` when the step's encoding
 // is outside what the generator handles (the step keeps the interpreter).
 bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why);
+// The kernel(s) of an ew reduce step (an ew program's value reduced without
+// being stored).
+bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why);
+// Workspace bytes of a sum over leading dims (rows summed, cols kept, inner
+// the iteration space's innermost dim).
+int64_t EwReduceWorkspaceBytes(int64_t rows, int64_t cols, int64_t inner);
 // The batched entry (`batch` instances) of a single-instance kernel.
 bool BatchEwKernel(const EwKernel& single, int batch, EwKernel* k);
 
@@ -67,8 +80,9 @@ class EwJit {
   // Compiles (once) without touching a device.  False when hiprtc failed;
   // error() says why.
   bool Build();
-  // hipFunction_t handles, one per kernel, on the device `ordinal` (which
-  // must be current); compiles and loads on first call.  Null on failure.
+  // hipFunction_t handles, two per kernel (entry, final entry or null), on
+  // the device `ordinal` (which must be current); compiles and loads on
+  // first call.  Null on failure.
   void* const* Functions(int ordinal);
   std::string error() const;
   double compile_seconds() const { return compile_seconds_; }

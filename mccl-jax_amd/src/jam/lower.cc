@@ -60,6 +60,7 @@ const char* StepName(StepKind k) {
     case StepKind::kSoftmaxXent: return "softmax_xent";
     case StepKind::kColSum: return "col_sum";
     case StepKind::kGemmSplitK: return "gemm_splitk";
+    case StepKind::kEwReduce: return "ew_reduce";
   }
   return "?";
 }
@@ -79,6 +80,10 @@ std::string Program::Dump() const {
   for (size_t i = 0; i < steps.size(); ++i) {
     os << "  [" << i << "] " << StepName(steps[i].kind);
     if (!steps[i].note.empty()) os << " (" << steps[i].note << ")";
+    if (getenv("JAM_DUMP_BUFFERS")) {  // debugging: where each step's buffers live
+      static const char* kSpace[] = {"in", "out", "arena", "const", "none"};
+      for (const BufRef& b : steps[i].bufs) os << " " << kSpace[int(b.space)] << b.index << "@" << b.offset;
+    }
     os << "\n";
   }
   return os.str();
@@ -437,6 +442,10 @@ class Lowerer {
         std::vector<size_t> w;
         for (size_t k = size_t(s.i[7]); k < s.bufs.size(); ++k) w.push_back(k);
         return w;
+      }
+      case StepKind::kEwReduce: {
+        const size_t L = size_t(s.i[7]);
+        return {L, L + 1, L + 2};
       }
       case StepKind::kGather: return {2};
       case StepKind::kScatterAdd: return {3, 4};
@@ -3101,6 +3110,10 @@ class Lowerer {
       const DType st_ = m_.types[src].dtype;
       if (st_ == DType::kBF16 || st_ == DType::kF16) x = src;
     }
+    // a reduction of an elementwise value read by nothing else: the value is
+    // computed inside the reduction's generated kernel, never stored
+    if (opts_.ew_jit && opts_.fuse_elementwise && InExpr(x) && uses_[x] == 1 && EmitEwReduce(op, x, rop, init, body))
+      return;
     // a sum over an f32 value with a narrow copy reads the copy (the same
     // values; the kernel widens on load)
     auto nw = narrow_.find(x);
@@ -3160,6 +3173,99 @@ class Lowerer {
     st.note = body;
     Emit(st);
     SetDenseView(op.results[0], d);
+  }
+
+  // The ew program of value v over its leaves; false when it does not fit
+  // the interpreter's limits (eight inputs, its register file).
+  bool BuildEwProgram(int v, EwBuild* out, int* reg) {
+    std::vector<int> leaves;
+    std::unordered_map<int, int> refs;
+    std::set<int> seen;
+    CollectLeaves(v, leaves, refs, seen);
+    ++refs[v];
+    if (leaves.size() > 8) return false;
+    EwBuild b;
+    b.leaves = leaves;
+    b.refs = refs;
+    b.next_reg = int(leaves.size());
+    try {
+      *reg = Gen(b, v, true);
+    } catch (int) {
+      return false;
+    }
+    *out = std::move(b);
+    return true;
+  }
+
+  // reduce(x) with x an elementwise expression: one kEwReduce step whose
+  // generated kernel evaluates x where the reduction reads it.  Trailing
+  // reduced dims (after moving them last): one wave per kept element; a sum
+  // over the leading dims into f32 (bias, gamma and beta gradients): column
+  // partial sums over row chunks, then their total.  The step keeps a
+  // buffer for x for the interpreter fallback (x stored, then the library's
+  // reduction).
+  bool EmitEwReduce(const Op& op, int x, int rop, double init, const std::string& body) {
+    const TensorType& xt = m_.types[x];
+    const DType vt = xt.dtype, ot = m_.types[op.results[0]].dtype;
+    auto fl = [](DType d) { return d == DType::kF32 || d == DType::kBF16 || d == DType::kF16; };
+    if (!fl(vt) || !fl(ot) || xt.rank() < 1 || xt.rank() > 6) return false;
+    const auto rd = reduce_dims(op);
+    std::vector<int> keep, red;
+    for (int d = 0; d < xt.rank(); ++d)
+      (std::find(rd.begin(), rd.end(), d) != rd.end() ? red : keep).push_back(d);
+    int64_t nk = 1, nr = 1;
+    for (int d : keep) nk *= xt.dims[size_t(d)];
+    for (int d : red) nr *= xt.dims[size_t(d)];
+    if (red.empty() || nk <= 0 || nr <= 0) return false;
+    bool lead = !keep.empty() && rop == 0 && init == 0 && ot == DType::kF32 && (vt == DType::kF32 || vt == DType::kBF16);
+    for (size_t r = 0; lead && r < red.size(); ++r) lead = red[r] == int(r);
+    std::vector<int> order;
+    if (lead) {
+      for (int d = 0; d < xt.rank(); ++d) order.push_back(d);
+    } else {
+      order = keep;
+      order.insert(order.end(), red.begin(), red.end());
+    }
+    EwBuild b;
+    int reg = 0;
+    if (!BuildEwProgram(x, &b, &reg)) return false;
+    Step st;
+    st.kind = StepKind::kEwReduce;
+    for (int l : b.leaves) {
+      auto nw = narrow_.find(l);
+      const View lv = state_[l].kind == ValState::kUnset && nw != narrow_.end() ? nw->second : NeedView(l);
+      if (lv.rank() != xt.rank()) throw std::string("jam: elementwise operand rank mismatch");
+      st.bufs.push_back(lv.at());
+      st.types.push_back(int32_t(lv.dtype));
+      for (int k = 0; k < 6; ++k) st.strides.push_back(k < xt.rank() ? lv.strides[size_t(order[size_t(k)])] : 0);
+    }
+    const BufRef d = DestFor(op.results[0]);
+    st.bufs.push_back(d);
+    st.bufs.push_back(NewTemp(xt.bytes()));
+    const int64_t rows = lead ? nr : nk, cols = lead ? nk : nr;
+    const int64_t inner = xt.dims[size_t(order.back())];
+    st.bufs.push_back(lead ? NewTemp(size_t(std::max<int64_t>(int64_t(mk_col_sum_workspace_bytes(rows, cols)),
+                                                                 EwReduceWorkspaceBytes(rows, cols, inner))))
+                           : BufRef{});
+    const float fi = float(init);
+    uint32_t ib;
+    memcpy(&ib, &fi, 4);
+    st.i = {xt.rank()};
+    for (int k = 0; k < 6; ++k) st.i.push_back(k < xt.rank() ? xt.dims[size_t(order[size_t(k)])] : 1);
+    st.i.push_back(int64_t(b.leaves.size()));
+    st.i.insert(st.i.end(), {reg, int64_t(vt), int64_t(ot), rop, rows, cols, lead ? 1 : 0, int64_t(ib)});
+    for (auto& ins : b.prog)
+      for (int k = 0; k < 4; ++k) st.prog.push_back(ins[k]);
+    for (uint32_t c : b.consts) {
+      float f;
+      memcpy(&f, &c, 4);
+      st.f.push_back(f);
+    }
+    st.note = body + " of " + ops_[state_[x].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
+              std::to_string(b.leaves.size()) + " inputs, " + (lead ? "leading dims" : "trailing dims") + ")";
+    Emit(st);
+    SetDenseView(op.results[0], d);
+    return true;
   }
 
   // Map a dot_general to mk_gemm; `epi` optionally carries bias / relu.
@@ -3933,7 +4039,7 @@ CompileResult Compile(const char* code, size_t size, const CompileOptions& opts)
     auto jit = std::make_shared<EwJit>();
     jit->strict = opts.ew_jit_strict;
     for (Step& st : r.program->steps) {
-      if (st.kind != StepKind::kEw) continue;
+      if (st.kind != StepKind::kEw && st.kind != StepKind::kEwReduce) continue;
       EwKernel k;
       std::string why;
       if (GenerateEwKernel(st, &k, &why) && k.blocks > 0) st.jit = jit->Add(std::move(k));

@@ -77,6 +77,9 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //                               f grad_scale
 //   sdpa_bwd bufs q,k,v,o,dout,lse,dq,dk,dv,workspace
 //            i B,H,Sq,Sk,D, (b,h,s strides) of q,k,v,o,dout,dq,dk,dv, causal  f scale
+//   ew_reduce bufs in...,out,tmp,ws  i rank,dims[6],n_inputs,out_reg,val_type,out_type,rop,rows,cols,
+//                               mode,init bits  prog strides types f as ew (mode 0: reduce trailing dims,
+//                               mode 1: sum leading dims)
 //   convert  bufs in,out        i in_type,out_type,n
 //   fill     bufs out           i elem_bytes,n,pattern
 //   copy     bufs in,out        i bytes
@@ -143,7 +146,7 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
             for (int b = 0; b < per; ++b) args[b] = &ptrs[b];
           else
             args[0] = ptrs;
-          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[s.jit]), k.blocks * uint32_t(s.batch),
+          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[2 * s.jit]), k.blocks * uint32_t(s.batch),
                                                1, 1, kEwJitBlock, 1, 1, 0, stream, args, nullptr);
           if (e == hipSuccess) return MK_OK;
           *f.error = "hipModuleLaunchKernel(" + k.name + "): " + hipGetErrorString(e);
@@ -174,6 +177,59 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
         if (rc != MK_OK) return rc;
       }
       return MK_OK;
+    }
+    case StepKind::kEwReduce: {
+      const int n_in = int(i[7]);
+      if (n_in > 8 || s.bufs.size() != size_t(n_in + 3) || i.size() != 16) return MK_ERR_INVALID;
+      const int mode = int(i[14]);
+      if (s.jit >= 0 && f.jit_fns) {
+        // generated: the reduction reads the program's inputs (mode 1: then
+        // adds the row chunks' partial sums from the workspace)
+        const EwKernel& k = f.jit->kernel(s.jit);
+        void* ptrs[9];
+        bool aligned = k.n_in == n_in;
+        for (int b = 0; aligned && b < n_in; ++b) {
+          ptrs[b] = P(size_t(b));
+          aligned = reinterpret_cast<uintptr_t>(ptrs[b]) % k.align[size_t(b)] == 0;
+        }
+        if (aligned) {
+          ptrs[n_in] = k.kind == 1 ? P(size_t(n_in)) : P(size_t(n_in + 2));
+          void* args[9];
+          for (int b = 0; b <= n_in; ++b) args[b] = &ptrs[b];
+          hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[2 * s.jit]), k.blocks, 1, 1,
+                                               kEwJitBlock, 1, 1, 0, stream, args, nullptr);
+          if (e == hipSuccess && k.kind == 2) {
+            void* fp[2] = {P(size_t(n_in + 2)), P(size_t(n_in))};
+            void* fa[2] = {&fp[0], &fp[1]};
+            e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[2 * s.jit + 1]), k.final_blocks, 1, 1,
+                                      kEwJitBlock, 1, 1, 0, stream, fa, nullptr);
+          }
+          if (e == hipSuccess) return MK_OK;
+          *f.error = "hipModuleLaunchKernel(" + k.name + "): " + hipGetErrorString(e);
+          return MK_ERR_LAUNCH;
+        }
+        if (f.jit->strict) {
+          *f.error = "generated kernel " + k.name + ": a buffer misses its alignment (strict mode)";
+          return MK_ERR_INVALID;
+        }
+      }
+      // interpreter: the value into tmp, then the library's reduction
+      const void* ins[8];
+      int types[8];
+      for (int k = 0; k < n_in; ++k) {
+        ins[k] = P(size_t(k));
+        types[k] = s.types[size_t(k)];
+      }
+      int reg = int(i[8]), vt = int(i[9]);
+      void* tmp = P(size_t(n_in + 1));
+      int rc = mk_ew_program_multi(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
+                                   s.prog.data(), s.f.data(), int(s.f.size()), 1, &reg, &vt, &tmp);
+      if (rc != MK_OK) return rc;
+      if (mode == 1) return mk_col_sum(st, vt, i[12], i[13], tmp, static_cast<float*>(P(size_t(n_in))), P(size_t(n_in + 2)));
+      uint32_t ib = uint32_t(i[15]);
+      float init;
+      memcpy(&init, &ib, 4);
+      return mk_row_reduce(st, vt, int(i[10]), int(i[11]), i[12], i[13], tmp, init, P(size_t(n_in)));
     }
     case StepKind::kGather:
       return mk_gather_rows(st, i[0], i[1], P(0), int(i[2]), i[3], P(1), P(2));
