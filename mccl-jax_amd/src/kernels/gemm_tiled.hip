@@ -65,7 +65,8 @@ struct TiledGemm {
   int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU
   int c_type;
   int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
-                              // stored as 16-byte chunks / element by element, 4 staged fp32 rows
+                              // stored as 16-byte chunks / element by element, 4 / 5 staged fp32 rows
+                              // stored element by element / as 16-byte chunks
 };
 
 // The copies one wave makes of one operand's tile: copy c is j = wave + W c
@@ -249,7 +250,7 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
 // rows write their accumulators as 16-byte chunks, chunk c of staging row r
 // at position c ^ (r & 15), then every thread stores consecutive columns of
 // consecutive rows, so each wave writes 256 contiguous bytes of a C row.
-template <int TM, int TN, int kW, int kWM, int kWN, int kI, int kJ, int kLdsFloats>
+template <bool ROWS16, int TM, int TN, int kW, int kWM, int kWN, int kI, int kJ, int kLdsFloats>
 __device__ __attribute__((always_inline)) inline void store_staged_f32(const TiledGemm& p,
                                                                        const f32x16_t (&acc)[kI][kJ], float* st,
                                                                        int64_t m0, int64_t n0, int wm, int wn,
@@ -287,13 +288,27 @@ __device__ __attribute__((always_inline)) inline void store_staged_f32(const Til
       }
     }
     lds_barrier();
+    if constexpr (ROWS16) {
+      // 16-byte aligned rows, N a multiple of 4: whole chunks, each wave
+      // writing 1 KB of one C row per instruction
+      static_assert(kRP * kCpr % kThreads == 0, "staged chunks split evenly over the threads");
 #pragma unroll 4
-    for (int it = 0; it < kRP * TN / kThreads; ++it) {
-      const int e = it * kThreads + int(threadIdx.x);
-      const int row = e / TN, col = e % TN;
-      const float v = st[row * TN + 4 * ((col >> 2) ^ (row & 15)) + (col & 3)];
-      const int64_t m = m0 + pass * kRP + row, n = n0 + col;
-      if (m < p.M && n < p.N) Cz[m * p.ldc + n] = v;
+      for (int it = 0; it < kRP * kCpr / kThreads; ++it) {
+        const int e = it * kThreads + int(threadIdx.x);
+        const int row = e / kCpr, cn = e % kCpr;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(st + row * TN + 4 * (cn ^ (row & 15)));
+        const int64_t m = m0 + pass * kRP + row, n = n0 + 4 * cn;
+        if (m < p.M && n < p.N) *reinterpret_cast<f32x4*>(Cz + m * p.ldc + n) = v;
+      }
+    } else {
+#pragma unroll 4
+      for (int it = 0; it < kRP * TN / kThreads; ++it) {
+        const int e = it * kThreads + int(threadIdx.x);
+        const int row = e / TN, col = e % TN;
+        const float v = st[row * TN + 4 * ((col >> 2) ^ (row & 15)) + (col & 3)];
+        const int64_t m = m0 + pass * kRP + row, n = n0 + col;
+        if (m < p.M && n < p.N) Cz[m * p.ldc + n] = v;
+      }
     }
     lds_barrier();
   }
@@ -461,8 +476,11 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   else if (p.c_mode == 3)
     store_staged<MK_F16, false, TM, TN, kW, kWM, kWN>(p, acc, lds, m0, n0, wm, wn, lane, bz);
   else if (p.c_mode == 4)
-    store_staged_f32<TM, TN, kW, kWM, kWN, kI, kJ, S * BK * (TM + TN) / 2>(p, acc, reinterpret_cast<float*>(lds), m0,
-                                                                           n0, wm, wn, lane, bz);
+    store_staged_f32<false, TM, TN, kW, kWM, kWN, kI, kJ, S * BK * (TM + TN) / 2>(
+        p, acc, reinterpret_cast<float*>(lds), m0, n0, wm, wn, lane, bz);
+  else if (p.c_mode == 5)
+    store_staged_f32<true, TM, TN, kW, kWM, kWN, kI, kJ, S * BK * (TM + TN) / 2>(
+        p, acc, reinterpret_cast<float*>(lds), m0, n0, wm, wn, lane, bz);
   else if (p.c_type == MK_F32)
     store_direct<MK_F32, kWM, kWN>(p, acc, m0, n0, wm, wn, lane, bz);
   else if (p.c_type == MK_BF16)
@@ -519,7 +537,7 @@ bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch,
   a.c_type = c_type;
   const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0 && N % 8 == 0;
   const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0 && N % 4 == 0;
-  a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 1 : 4;
+  a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 5 : 4;
   return true;
 }
 
