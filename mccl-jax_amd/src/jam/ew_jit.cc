@@ -486,9 +486,12 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
 // row; mode 1 sums the leading dims (rows = reduced, cols = kept), partial
 // sums of row chunks into ws, then a second kernel adds the chunks.  The
 // value is rounded to val_type before it is combined, as the materialized
-// value would be.
+// value would be.  i[16] set: the value is also stored, densely in the
+// iteration order, into tmp (the value's own buffer; the lowering only asks
+// for it when that order is the value's layout).
 bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
-  if (s.kind != StepKind::kEwReduce || s.i.size() != 16) return (*why = "not an ew reduce step", false);
+  if (s.kind != StepKind::kEwReduce || s.i.size() != 17) return (*why = "not an ew reduce step", false);
+  const bool store = s.i[16] != 0;  // the value is also stored (into tmp, in iteration order)
   const int rank = int(s.i[0]), n_in = int(s.i[7]), out_reg = int(s.i[8]), val_type = int(s.i[9]),
             out_type = int(s.i[10]), rop = int(s.i[11]), mode = int(s.i[14]);
   const int64_t rows = s.i[12], cols = s.i[13];
@@ -515,8 +518,10 @@ bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
   src << "#endif\n";
   std::string params;
   for (int t = 0; t < n_in; ++t) params += "const void* p" + std::to_string(t) + ", ";
+  const std::string sparam = store ? ", void* qs" : "";
   std::ostringstream e;
   // per element: loads, the program, rounding, combine into the lane's acc
+  // (and the stored copy of the value)
   auto element = [&](const std::string& i0, const std::string& ind, const std::string& acc, bool per_lane) {
     std::vector<std::array<std::string, kLanes>> x;
     e << ind << "{\n";
@@ -531,11 +536,31 @@ bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
       if (rop == 1 || rop == 2) e << " nan_ |= v != v;";
       e << " " << a << " = " << Combine(rop, a, "v") << "; }\n";
     }
+    if (store) {
+      auto y = [&](int l) { return "y" + std::to_string(l) + "[0]"; };
+      if (lanes == kLanes && val_type == MK_F32) {
+        e << ind << "  *(mkj_f4*)((float*)qs + " << i0 << ") = mkj_f4{" << y(0) << ", " << y(1) << ", " << y(2)
+          << ", " << y(3) << "};\n";
+        k->align[size_t(n_in + 1)] = 16;
+      } else if (lanes == kLanes && val_type == MK_BF16) {
+        e << ind << "  *(mkj_u2*)((unsigned short*)qs + " << i0 << ") = mkj_u2{unsigned(mkj_f2bf(" << y(0)
+          << ")) | (unsigned(mkj_f2bf(" << y(1) << ")) << 16), unsigned(mkj_f2bf(" << y(2)
+          << ")) | (unsigned(mkj_f2bf(" << y(3) << ")) << 16)};\n";
+        k->align[size_t(n_in + 1)] = 8;
+      } else {
+        for (int l = 0; l < lanes; ++l) {
+          std::string stmt;
+          StoreStmt(val_type, "qs", l == 0 ? i0 : i0 + " + " + std::to_string(l), y(l), &stmt);
+          e << ind << "  " << stmt << "\n";
+        }
+      }
+    }
     e << ind << "}\n";
   };
   if (mode == 0) {
     // one wave per row, lanes x 64 columns per iteration
-    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "void* q0) {\n";
+    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "void* q0" << sparam
+      << ") {\n";
     e << "#pragma clang fp contract(off)\n  const unsigned lane = threadIdx.x & 63u;\n";
     e << "  const " << IT << " row = (" << IT << ")blockIdx.x * " << kEwJitBlock / 64 << " + (threadIdx.x >> 6);\n";
     e << "  if (row >= " << rows << U << ") return;\n";
@@ -563,7 +588,8 @@ bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
     const int64_t chunks = ReduceChunks(rows, tiles);
     const int64_t rpc = (rows + chunks - 1) / chunks;
     if (tiles * chunks >= (int64_t(1) << 31)) return (*why = "grid too large", false);
-    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "float* ws) {\n";
+    e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@(" << params << "float* ws" << sparam
+      << ") {\n";
     e << "#pragma clang fp contract(off)\n  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n";
     e << "  const unsigned tile = blockIdx.x % " << tiles << "u, chunk = blockIdx.x / " << tiles << "u;\n";
     e << "  const " << IT << " c = (" << IT << ")tile * " << tile_cols << U << " + lane * " << lanes << U << ";\n";
@@ -584,24 +610,24 @@ bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
         << l << "] + red_[1][lane * " << lanes << " + " << l << "]) + red_[2][lane * " << lanes << " + " << l
         << "]) + red_[3][lane * " << lanes << " + " << l << "];\n";
     e << "  }\n}\n";
-    // the chunks' partial sums: 64 columns per block, wave w adding chunks
-    // w, w + 4, ..., then the four waves' totals in order
+    // the chunks' partial sums: 16 columns per block, 16 threads per
+    // column adding chunks g, g + 16, ..., then their 16 totals in order
     e << "extern \"C\" __global__ void __launch_bounds__(" << kEwJitBlock << ") @K@_final(const float* ws, void* q0) {\n";
     e << "#pragma clang fp contract(off)\n";
-    e << "  const unsigned lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n";
-    e << "  const " << IT << " c = (" << IT << ")blockIdx.x * 64" << U << " + lane;\n";
+    e << "  const unsigned t = threadIdx.x & 15u, g = threadIdx.x >> 4;\n";
+    e << "  const " << IT << " c = (" << IT << ")blockIdx.x * 16" << U << " + t;\n";
     e << "  float s = 0.f;\n";
-    e << "  if (c < " << cols << U << ")\n";
-    e << "    for (" << IT << " j = wave; j < " << chunks << U << "; j += 4) s += ws[j * " << cols << U << " + c];\n";
-    e << "  __shared__ float part_[4][64];\n  part_[wave][lane] = s;\n  __syncthreads();\n";
-    e << "  if (wave != 0 || c >= " << cols << U << ") return;\n";
-    e << "  s = ((part_[0][lane] + part_[1][lane]) + part_[2][lane]) + part_[3][lane];\n";
+    e << "  if (c < " << cols << U << ") {\n#pragma unroll 4\n";
+    e << "    for (" << IT << " j = g; j < " << chunks << U << "; j += 16) s += ws[j * " << cols << U << " + c];\n  }\n";
+    e << "  __shared__ float part_[16][16];\n  part_[g][t] = s;\n  __syncthreads();\n";
+    e << "  if (g != 0 || c >= " << cols << U << ") return;\n";
+    e << "  s = part_[0][t];\n  for (int k = 1; k < 16; ++k) s += part_[k][t];\n";
     e << "  s = s + " << FloatLit(init) << ";\n";
     std::string stmt;
     StoreStmt(out_type, "q0", "c", "s", &stmt);
     e << "  " << stmt << "\n}\n";
     k->blocks = uint32_t(tiles * chunks);
-    k->final_blocks = uint32_t((cols + 63) / 64);
+    k->final_blocks = uint32_t((cols + 15) / 16);
     k->kind = 2;
     k->chunks = chunks;
   }

@@ -3112,7 +3112,7 @@ class Lowerer {
     }
     // a reduction of an elementwise value read by nothing else: the value is
     // computed inside the reduction's generated kernel, never stored
-    if (opts_.ew_jit && opts_.fuse_elementwise && InExpr(x) && uses_[x] == 1 && EmitEwReduce(op, x, rop, init, body))
+    if (opts_.ew_jit && opts_.fuse_elementwise && InExpr(x) && EmitEwReduce(op, x, rop, init, body, uses_[x] > 1))
       return;
     // a sum over an f32 value with a narrow copy reads the copy (the same
     // values; the kernel widens on load)
@@ -3204,7 +3204,7 @@ class Lowerer {
   // partial sums over row chunks, then their total.  The step keeps a
   // buffer for x for the interpreter fallback (x stored, then the library's
   // reduction).
-  bool EmitEwReduce(const Op& op, int x, int rop, double init, const std::string& body) {
+  bool EmitEwReduce(const Op& op, int x, int rop, double init, const std::string& body, bool store) {
     const TensorType& xt = m_.types[x];
     const DType vt = xt.dtype, ot = m_.types[op.results[0]].dtype;
     auto fl = [](DType d) { return d == DType::kF32 || d == DType::kBF16 || d == DType::kF16; };
@@ -3226,6 +3226,10 @@ class Lowerer {
       order = keep;
       order.insert(order.end(), red.begin(), red.end());
     }
+    // a value that other ops read is stored by the same kernel, which
+    // writes it in iteration order: only when that is its own layout
+    for (size_t k = 0; store && k < order.size(); ++k)
+      if (order[k] != int(k)) return false;
     EwBuild b;
     int reg = 0;
     if (!BuildEwProgram(x, &b, &reg)) return false;
@@ -3241,7 +3245,8 @@ class Lowerer {
     }
     const BufRef d = DestFor(op.results[0]);
     st.bufs.push_back(d);
-    st.bufs.push_back(NewTemp(xt.bytes()));
+    const BufRef xs = store ? DestFor(x) : NewTemp(xt.bytes());
+    st.bufs.push_back(xs);
     const int64_t rows = lead ? nr : nk, cols = lead ? nk : nr;
     const int64_t inner = xt.dims[size_t(order.back())];
     st.bufs.push_back(lead ? NewTemp(size_t(std::max<int64_t>(int64_t(mk_col_sum_workspace_bytes(rows, cols)),
@@ -3253,7 +3258,7 @@ class Lowerer {
     st.i = {xt.rank()};
     for (int k = 0; k < 6; ++k) st.i.push_back(k < xt.rank() ? xt.dims[size_t(order[size_t(k)])] : 1);
     st.i.push_back(int64_t(b.leaves.size()));
-    st.i.insert(st.i.end(), {reg, int64_t(vt), int64_t(ot), rop, rows, cols, lead ? 1 : 0, int64_t(ib)});
+    st.i.insert(st.i.end(), {reg, int64_t(vt), int64_t(ot), rop, rows, cols, lead ? 1 : 0, int64_t(ib), store ? 1 : 0});
     for (auto& ins : b.prog)
       for (int k = 0; k < 4; ++k) st.prog.push_back(ins[k]);
     for (uint32_t c : b.consts) {
@@ -3262,9 +3267,11 @@ class Lowerer {
       st.f.push_back(f);
     }
     st.note = body + " of " + ops_[state_[x].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
-              std::to_string(b.leaves.size()) + " inputs, " + (lead ? "leading dims" : "trailing dims") + ")";
+              std::to_string(b.leaves.size()) + " inputs, " + (lead ? "leading dims" : "trailing dims") +
+              (store ? ", value stored" : "") + ")";
     Emit(st);
     SetDenseView(op.results[0], d);
+    if (store) SetDenseView(x, xs);
     return true;
   }
 

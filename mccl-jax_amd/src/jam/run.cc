@@ -78,8 +78,8 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   sdpa_bwd bufs q,k,v,o,dout,lse,dq,dk,dv,workspace
 //            i B,H,Sq,Sk,D, (b,h,s strides) of q,k,v,o,dout,dq,dk,dv, causal  f scale
 //   ew_reduce bufs in...,out,tmp,ws  i rank,dims[6],n_inputs,out_reg,val_type,out_type,rop,rows,cols,
-//                               mode,init bits  prog strides types f as ew (mode 0: reduce trailing dims,
-//                               mode 1: sum leading dims)
+//                               mode,init bits,store  prog strides types f as ew (mode 0: reduce
+//                               trailing dims, mode 1: sum leading dims; store: the value into tmp too)
 //   convert  bufs in,out        i in_type,out_type,n
 //   fill     bufs out           i elem_bytes,n,pattern
 //   copy     bufs in,out        i bytes
@@ -180,22 +180,25 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     }
     case StepKind::kEwReduce: {
       const int n_in = int(i[7]);
-      if (n_in > 8 || s.bufs.size() != size_t(n_in + 3) || i.size() != 16) return MK_ERR_INVALID;
+      if (n_in > 8 || s.bufs.size() != size_t(n_in + 3) || i.size() != 17) return MK_ERR_INVALID;
       const int mode = int(i[14]);
+      const bool store = i[16] != 0;
       if (s.jit >= 0 && f.jit_fns) {
         // generated: the reduction reads the program's inputs (mode 1: then
         // adds the row chunks' partial sums from the workspace)
         const EwKernel& k = f.jit->kernel(s.jit);
-        void* ptrs[9];
+        void* ptrs[10];
         bool aligned = k.n_in == n_in;
         for (int b = 0; aligned && b < n_in; ++b) {
           ptrs[b] = P(size_t(b));
           aligned = reinterpret_cast<uintptr_t>(ptrs[b]) % k.align[size_t(b)] == 0;
         }
+        if (store) aligned = aligned && reinterpret_cast<uintptr_t>(P(size_t(n_in + 1))) % k.align[size_t(n_in + 1)] == 0;
         if (aligned) {
           ptrs[n_in] = k.kind == 1 ? P(size_t(n_in)) : P(size_t(n_in + 2));
-          void* args[9];
-          for (int b = 0; b <= n_in; ++b) args[b] = &ptrs[b];
+          ptrs[n_in + 1] = P(size_t(n_in + 1));
+          void* args[10];
+          for (int b = 0; b <= n_in + (store ? 1 : 0); ++b) args[b] = &ptrs[b];
           hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[2 * s.jit]), k.blocks, 1, 1,
                                                kEwJitBlock, 1, 1, 0, stream, args, nullptr);
           if (e == hipSuccess && k.kind == 2) {

@@ -394,3 +394,44 @@ def test_fused_reduction_of_elementwise_value(client, case):
         out_round = 2.0 ** -8 * np.abs(want) if vtype == "bf16" else 0
         bad = np.abs(got - want) > 1e-6 * mag + out_round + 1e-30
         assert not bad.any(), (case, got[bad][:4], want[bad][:4], mag[bad][:4])
+
+
+@pytest.mark.parametrize("shape,rdims", [((64, 768), [1]), ((33, 101), [1]), ((6, 512, 768), [0, 1]),
+                                         ((300, 37), [0])])
+def test_fused_reduction_stores_a_shared_value(client, shape, rdims):
+    """A reduced elementwise value that other ops also read is stored by the
+    reduction's kernel in the same pass (ew_reduce, value stored): the
+    stored value exactly the f32 product, the sum within 1e-6 of the sum of
+    magnitudes, and its other reader (here a second output) sees it."""
+    st = "x".join(str(d) for d in shape)
+    keep = [d for d in range(len(shape)) if d not in rdims]
+    ot = "x".join(str(shape[d]) for d in keep)
+    text = f"""func.func public @main(%x: tensor<{st}xf32>, %y: tensor<{st}xf32>) -> (tensor<{ot}xf32>, tensor<{st}xf32>) {{
+  %e = stablehlo.multiply %x, %y : tensor<{st}xf32>
+  %z = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+  %r = stablehlo.reduce(%e init: %z) applies stablehlo.add across dimensions = {rdims} : (tensor<{st}xf32>, tensor<f32>) -> tensor<{ot}xf32>
+  %two = stablehlo.constant dense<2.000000e+00> : tensor<{st}xf32>
+  %d = stablehlo.multiply %e, %two : tensor<{st}xf32>
+  return %r, %d : tensor<{ot}xf32>, tensor<{st}xf32>
+}}"""
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal(shape).astype(np.float32)
+    y = rng.standard_normal(shape).astype(np.float32)
+    print(f"case: ew_reduce stored value {shape} over {rdims}", flush=True)
+    os.environ["JAM_EW_JIT_STRICT"] = "1"
+    try:
+        e = client.compile(text)
+    finally:
+        del os.environ["JAM_EW_JIT_STRICT"]
+    assert "value stored" in e.plan()
+    bufs = [client.put(x), client.put(y)]
+    outs = e.execute(bufs)
+    r, d = (o.to_numpy() for o in outs)
+    for b in bufs + outs:
+        b.destroy()
+    e.destroy()
+    v = x * y
+    np.testing.assert_array_equal(d, v * np.float32(2))
+    want = np.sum(v.astype(np.float64), axis=tuple(rdims))
+    mag = np.sum(np.abs(v).astype(np.float64), axis=tuple(rdims))
+    assert np.all(np.abs(r - want) <= 1e-6 * mag + 1e-30)
