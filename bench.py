@@ -16,6 +16,11 @@ fusion GB/s % HBM peak".
   cpu_baseline  an fp32 torch-CPU restatement (not XLA:CPU; jax is absent)
              on a bounded sample of (b, h) pairs of the same workload, scaled
              to all pairs, with the thread count
+  cpu_baselines_other_configs  the same kind of restatement for C1, the C2 and
+             C4 fusions and the C5 training step (bounded samples, in each
+             GPU figure's unit)
+  gemm       the C5 step's 15 GEMM shapes on mk_gemm and rocBLAS, and C1
+             through PJRT Execute (TFLOP/s, fraction of the fp32 peak)
   pjrt_execute  the same attention through PJRT_LoadedExecutable_Execute
              (the plugin path), and the per-Execute cost of a tiny module
   training_step  config C5: one GPT-2-small training step (forward, backward,
@@ -64,7 +69,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--spinup", type=float, default=1.0,
                     help="seconds of untimed headline launches before anything is timed (clocks settle)")
-    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5", "gemm", "pjrt", "c5jit"], default=None)
+    ap.add_argument("--only", choices=["sdpa", "fusions", "headline", "calib", "c5", "gemm", "pjrt", "c5jit", "c1"], default=None)
     ap.add_argument("--seq", type=int, default=8192, help="headline sequence length")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -175,6 +180,108 @@ def cpu_baseline_sdpa(torch, np, S, budget_s, gpu_out=None):
                   f"{B*H} (b,h) pairs at S={S}, {el:.1f}s, extrapolated x{B*H/done:.1f}; torch threads={cores}"
                   + (f"; max |CPU - GPU| on pair (0,0) = {err:.2e}" if err is not None else ""),
     }
+
+
+CPU_LABEL = "CPU restatement, not XLA:CPU"
+
+
+def _cpu_time(fn, budget_s, min_reps=1):
+    """Seconds per call of fn on the CPU (at least min_reps calls, until the
+    budget is used)."""
+    fn()  # first call outside the timing (allocation, thread start)
+    n, t0 = 0, time.perf_counter()
+    while n < min_reps or time.perf_counter() - t0 < budget_s:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_baselines(torch, np, budget_s):
+    """fp32 torch-CPU restatements of the other configs, each timed on a
+    bounded sample for about budget_s seconds and reported in the GPU
+    figure's unit (scaled to the full workload where a sample is used).
+    Not XLA:CPU (jax is absent); torch runs on every core of this process's
+    affinity mask."""
+    from oracle import bf16, gpt2_ref, inputs
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {}
+
+    def rec(name, value, unit, sample):
+        out[name] = {"value": round(value, 4), "unit": unit, "cores": int(cores), "kind": "port",
+                     "sample": f"{CPU_LABEL}: {sample}; torch threads={cores}"}
+        log(f"cpu {name}: {value:.3f} {unit}")
+
+    # C1: the MLP forward, full size
+    d = inputs.c1_mlp()
+    x, w1, b1, w2, b2 = (torch.from_numpy(d[n]) for n in ("x", "w1", "b1", "w2", "b2"))
+    sec, n = _cpu_time(lambda: torch.relu(x @ w1 + b1) @ w2 + b2, budget_s, 3)
+    rec("c1_mlp_fp32", 2.0 * 256 * 1024 * 4096 * 2 / sec / 1e12, "TFLOP/s",
+        f"fp32 x@W1+b1, ReLU, @W2+b2 at full size, {n} calls")
+    # C2: bf16 in, fp32 compute, on the first rows; GB/s of the same
+    # algorithmic bytes per element as the GPU figures
+    rows = 1024
+    ln = inputs.c2_layernorm(rows=rows)  # the first rows of the C2 array (same generator stream)
+    xl = torch.from_numpy(bf16.from_bf16_bits(ln["x"]))
+    gl, bl = (torch.from_numpy(bf16.from_bf16_bits(ln[k])) for k in ("gamma", "beta"))
+    sec, n = _cpu_time(lambda: torch.nn.functional.layer_norm(xl, (4096,), gl, bl, 1e-5).to(torch.bfloat16),
+                       budget_s / 4)
+    rec("layernorm_8192x4096_bf16", rows * 4096 * 4 / sec / 1e9, "GB/s",
+        f"torch layer_norm on rows 0..{rows} of [8192,4096] widened to fp32, result to bf16, {n} calls")
+    del ln, xl
+    xg = torch.from_numpy(bf16.from_bf16_bits(inputs.c2_gelu(rows=256)["x"]))
+    sec, n = _cpu_time(lambda: torch.nn.functional.gelu(xg, approximate="tanh").to(torch.bfloat16), budget_s / 4)
+    rec("gelu_tanh_8192x16384_bf16", xg.numel() * 4 / sec / 1e9, "GB/s",
+        f"torch gelu(tanh) on rows 0..256 of [8192,16384] in fp32, result to bf16, {n} calls")
+    del xg
+    rows = 8192
+    xr = torch.from_numpy(bf16.from_bf16_bits(inputs.c2_reduce(rows=rows)["x"]))
+    sec, n = _cpu_time(lambda: xr.sum(dim=1), budget_s / 4)
+    rec("reduce_sum_65536x1024_bf16", rows * (1024 * 2 + 4) / sec / 1e9, "GB/s",
+        f"fp32 row sums of rows 0..{rows} of [65536,1024], {n} calls")
+    sec, n = _cpu_time(lambda: xr.argmax(dim=1), budget_s / 4)
+    rec("argmax_65536x1024_bf16", rows * (1024 * 2 + 4) / sec / 1e9, "GB/s",
+        f"row argmax of rows 0..{rows} of [65536,1024], {n} calls")
+    del xr
+    # C4: full size
+    c4 = inputs.c4_indexing()
+    table = torch.from_numpy(bf16.from_bf16_bits(c4["table_bf16"])).to(torch.bfloat16)
+    ids = torch.from_numpy(c4["ids"]).reshape(-1).long()
+    sec, n = _cpu_time(lambda: table.index_select(0, ids), budget_s / 2)
+    rec("gather_32x2048_from_50257x768_bf16", (65536 * 4 + 2 * 65536 * 768 * 2) / sec / 1e9, "GB/s",
+        f"index_select of 65536 rows of [50257,768] bf16, {n} calls")
+    tf, gr = torch.from_numpy(c4["table_f32"]), torch.from_numpy(c4["grads"])
+    sec, n = _cpu_time(lambda: tf.clone().index_add_(0, ids, gr), budget_s / 2)
+    rec("scatter_add_65536x768_into_50257x768_f32", (65536 * 768 * 4 + 65536 * 4 + 2 * 50257 * 768 * 4) / sec / 1e9,
+        "GB/s", f"index_add_ of 65536 rows into a copy of [50257,768] fp32, {n} calls")
+    del c4, table, tf, gr
+    # C5: the GPT-2 step (forward, backward, Adam) for one of the 8 sequences
+    from mi355x_pjrt import gpt2
+
+    cfg = gpt2.GPT2Config()
+    params = {k: torch.tensor(v, requires_grad=True) for k, v in gpt2.init_params(cfg, 0).items()}
+    st = {k: (torch.zeros_like(v), torch.zeros_like(v)) for k, v in params.items()}
+    rng = np.random.default_rng(5000)
+    ids5 = rng.integers(0, cfg.vocab, (1, cfg.seq)).astype(np.int64)
+    labels = np.roll(ids5, -1, axis=1)
+
+    def step():
+        loss = gpt2_ref.forward_loss(params, ids5, labels, cfg.n_layer, cfg.n_head)
+        loss.backward()
+        with torch.no_grad():
+            for k, p_ in params.items():
+                m, v = st[k]
+                m.mul_(0.9).add_(p_.grad, alpha=0.1)
+                v.mul_(0.999).addcmul_(p_.grad, p_.grad, value=0.001)
+                p_.sub_(3e-4 * (m / 0.1) / ((v / 0.001).sqrt() + 1e-8))
+                p_.grad = None
+
+    sec, n = _cpu_time(step, budget_s, 1)
+    rec("c5_gpt2_train_step", cfg.seq / sec, "tokens/s",
+        f"fp32 torch autograd of the GPT-2-small step (12 layers, d 768, vocab 50257) on 1 of the 8 sequences "
+        f"(1024 tokens) plus Adam over all parameters, {n} steps; tokens/s of that sample")
+    return out
 
 
 def run_sdpa(torch, np, K, args):
@@ -297,21 +404,37 @@ def run_gemm(torch, np, K, args):
         res[tag] = row
         log(msg)
         del a, b, c
-    d = inputs.c1_mlp()
-    x, w1, b1, w2, b2 = (torch.from_numpy(d[n]).cuda() for n in ("x", "w1", "b1", "w2", "b2"))
-    h = torch.empty(256, 4096, device="cuda")
-    y = torch.empty(256, 1024, device="cuda")
-
-    def mlp():
-        K.gemm(x, w1, bias=b1, relu=True, out=h)
-        K.gemm(h, w2, bias=b2, out=y)
-
-    ms = time_launches(torch, mlp, args.steps, 3)
-    fl = 2.0 * 256 * 1024 * 4096 * 2
-    res["c1_mlp_fp32"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
-                          "frac_peak_fp32": round(fl / (ms * 1e-3) / 1e12 / 157.3, 4)}
-    log(f"C1 MLP fp32 (two mk_gemm launches): {ms*1e3:.1f} us, {res['c1_mlp_fp32']['tflops']} TFLOP/s")
+    res["c1_mlp_fp32"] = run_c1_pjrt(np, args)
     return res
+
+
+def run_c1_pjrt(np, args):
+    """Config C1 (fp32 MLP forward) as jaxlib runs it: the module compiled by
+    jam (each product split along K into about 256 workgroups, bias / ReLU as
+    one elementwise pass each) and run through PJRT Execute on resident
+    inputs; TFLOP/s against the fp32 MFMA peak (157.3)."""
+    from mi355x_pjrt import modules, pjrt
+    from oracle import inputs
+
+    p = pjrt.Plugin()
+    client = p.client()
+    e = client.compile(modules.mlp())
+    d = inputs.c1_mlp()
+    bufs = [client.put(d[k]) for k in ("x", "w1", "b1", "w2", "b2")]
+    for b in bufs:
+        b.ready()
+    run = pjrt_runner(p)
+    run(e, bufs, 5)
+    ms = run(e, bufs, max(20, args.steps))
+    for b in bufs:
+        b.destroy()
+    e.destroy()
+    client.close()
+    fl = 2.0 * 256 * 1024 * 4096 * 2
+    tf = fl / (ms * 1e-3) / 1e12
+    log(f"C1 MLP fp32 through PJRT Execute: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s ({100*tf/157.3:.1f}% of fp32 peak)")
+    return {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_peak_fp32": round(tf / 157.3, 4),
+            "path": "PJRT Execute of the C1 module (jam: gemm_splitk + ew epilogue per layer)"}
 
 
 def pjrt_runner(p):
@@ -496,6 +619,9 @@ def main():
     if args.only == "pjrt":
         print(json.dumps({"pjrt": run_pjrt(torch, np, args)}))
         return
+    if args.only == "c1":
+        print(json.dumps({"c1_mlp_fp32": run_c1_pjrt(np, args)}))
+        return
     if args.only == "c5jit":
         print(json.dumps({"c5_jitted_step": run_pjrt_c5(np, args)}))
         return
@@ -510,9 +636,11 @@ def main():
         return
     c5 = run_c5(torch, np, args) if args.only is None else None
     plugin = run_pjrt(torch, np, args) if args.only is None else None
+    gemm = run_gemm(torch, np, K, args) if args.only is None else None
     ms, tf, steps, o0 = head
     S = args.seq
     cpu = None if args.no_cpu else cpu_baseline_sdpa(torch, np, S, args.cpu_seconds, gpu_out=o0)
+    cpu_other = None if args.no_cpu or args.only is not None else cpu_baselines(torch, np, args.cpu_seconds / 3)
     traffic = read_traffic(f"sdpa_fwd_causal_b4h16d128_s{S}_traffic")
     line = {
         "metric": "SDPA TFLOP/s vs seq len (512-16384) & % MFMA peak; fusion GB/s % HBM peak",
@@ -534,10 +662,12 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
+        "cpu_baselines_other_configs": cpu_other,
         "sweep": sweep,
         "fusions": fusions,
         "training_step": c5,
         "pjrt_execute": plugin,
+        "gemm": gemm,
     }
     print(json.dumps(line))
 

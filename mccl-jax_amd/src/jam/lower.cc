@@ -3275,6 +3275,27 @@ class Lowerer {
     return true;
   }
 
+  // C[M,N] (f32, dense) = C + bias[N], then max(C, 0) when the epilogue has
+  // the ReLU: one elementwise step in place (the epilogue of mk_gemm, for a
+  // product computed without it).
+  void EmitBiasEpilogue(BufRef c, int64_t M, int64_t N, const Fused& epi) {
+    const View bv = Densify(NeedView(epi.bias));
+    if (bv.dtype != DType::kF32) throw std::string("jam: split product with a non-f32 bias");
+    Step st;
+    st.kind = StepKind::kEw;
+    st.bufs = {c, bv.at(), c};
+    st.types = {int32_t(DType::kF32), int32_t(DType::kF32)};
+    st.strides = {N, 1, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0};
+    st.i = {2, M, N, 1, 1, 1, 1, 2, 2, int64_t(DType::kF32)};
+    st.prog = {MK_EW_ADD, 2, 0, 1};
+    if (epi.relu) {
+      st.prog.insert(st.prog.end(), {MK_EW_CONST, 3, 0, 0, MK_EW_MAX, 2, 2, 3});
+      st.f = {0.f};
+    }
+    st.note = epi.relu ? "bias + relu epilogue" : "bias epilogue";
+    Emit(st);
+  }
+
   // Map a dot_general to mk_gemm; `epi` optionally carries bias / relu.
   void LowerDot(int idx, const Fused* epi, int result_override = -1) {
     const Op& op = ops_[idx];
@@ -3369,10 +3390,22 @@ class Lowerer {
     // into slices summed in order (mk_gemm_splitk), enough of them that the
     // grid covers the CUs (about 400 workgroups of 128x128), each slice at
     // least 256 deep
-    if (st.kind == StepKind::kGemm && !epi && B == 1 && ct == DType::kF32 && N % 4 == 0 && K >= 2 * std::max(M, N)) {
-      const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    // fp32 operands (mk_gemm's general kernel, 128x128 tiles) with fewer
+    // output tiles than CUs (config C1's [256,1024]x[1024,4096] has 64, its
+    // [256,4096]x[4096,1024] 16) are cut the same way into about 256
+    // workgroups, slices at least 128 deep (512 workgroups measured no
+    // faster); a fused bias / ReLU then runs as an elementwise pass over the
+    // summed product.
+    const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128);
+    const bool f32_underfill = at == DType::kF32 && tiles128 < 256 && K >= 256;
+    if (st.kind == StepKind::kGemm && (!epi || f32_underfill) && B == 1 && ct == DType::kF32 && N % 4 == 0 &&
+        (K >= 2 * std::max(M, N) || f32_underfill)) {
+      const int64_t tiles = tiles128;
       int64_t splits = 1;
-      while (splits < 8 && tiles * splits < 400 && K % (2 * splits) == 0 && K / (2 * splits) >= 256) splits *= 2;
+      if (f32_underfill)
+        while (splits < 16 && tiles * splits < 256 && K % (2 * splits) == 0 && K / (2 * splits) >= 128) splits *= 2;
+      else
+        while (splits < 8 && tiles * splits < 400 && K % (2 * splits) == 0 && K / (2 * splits) >= 256) splits *= 2;
       if (splits > 1) {
         st.kind = StepKind::kGemmSplitK;
         st.bufs = {lv.at(), rv.at(), d, NewTemp(mk_gemm_splitk_workspace_bytes(M, N, splits))};
@@ -3380,6 +3413,7 @@ class Lowerer {
         st.note = std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " in " +
                   std::to_string(splits) + " slices";
         Emit(st);
+        if (epi) EmitBiasEpilogue(d, M, N, *epi);
         SetDenseView(res, d);
         return;
       }
