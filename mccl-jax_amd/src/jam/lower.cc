@@ -2300,9 +2300,14 @@ class Lowerer {
   // by its kernel, or a product written in bf16 because every reader rounds
   // it to bf16.  While nothing needs v's f32 form it is never written:
   // layout ops carry the narrow view along, a convert back to bf16 is that
-  // view, and a sum reads it (widening on load is exact).
-  bool NarrowOnly(int v) {
-    auto memo = narrow_only_.find(v);
+  // view, and a sum reads it (widening on load is exact).  A sum is only an
+  // allowed reader (allow_sum) where v's f32 values are the kernel's bf16
+  // results anyway (the fused attention's outputs and gradients, within
+  // that fusion's tolerance); a product whose f32 values a sum reads is
+  // written in f32, since the sum of the rounded values would differ.
+  bool NarrowOnly(int v, bool allow_sum = true) {
+    const int key = 2 * v + (allow_sum ? 1 : 0);
+    auto memo = narrow_only_.find(key);
     if (memo != narrow_only_.end()) return memo->second;
     bool ok = m_.types[v].dtype == DType::kF32 && std::count(outputs_.begin(), outputs_.end(), v) == 0;
     bool any = false;
@@ -2319,16 +2324,16 @@ class Lowerer {
                  o.name == "stablehlo.broadcast_in_dim" || o.name == "stablehlo.slice" ||
                  o.name == "stablehlo.concatenate") {
         ok = o.operands[0] == v || o.name == "stablehlo.concatenate";
-        ok = ok && NarrowOnly(o.results[0]);
+        ok = ok && NarrowOnly(o.results[0], allow_sum);
       } else if (o.name == "stablehlo.reduce") {
-        ok = o.operands.size() == 2 && o.operands[0] == v && reduce_body_op(o) == "stablehlo.add" &&
+        ok = allow_sum && o.operands.size() == 2 && o.operands[0] == v && reduce_body_op(o) == "stablehlo.add" &&
              m_.types[o.results[0]].dtype == DType::kF32;
       } else {
         ok = false;
       }
     }
     ok = ok && any;
-    narrow_only_[v] = ok;
+    narrow_only_[key] = ok;
     return ok;
   }
 
@@ -3421,7 +3426,7 @@ class Lowerer {
     // an f32 product every reader rounds to bf16 is written in bf16 (one
     // rounding of the fp32 accumulator, as the module's convert does)
     bool narrow_out = false;
-    if (!epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res)) {
+    if (!epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res, false)) {
       narrow_out = true;
       d = NewTemp(size_t(m_.types[res].numel()) * 2);
     }

@@ -435,3 +435,29 @@ def test_fused_reduction_stores_a_shared_value(client, shape, rdims):
     want = np.sum(v.astype(np.float64), axis=tuple(rdims))
     mag = np.sum(np.abs(v).astype(np.float64), axis=tuple(rdims))
     assert np.all(np.abs(r - want) <= 1e-6 * mag + 1e-30)
+
+
+def test_sum_of_a_product_also_rounded_to_bf16(client):
+    """A bf16 product with an f32 result that is both rounded to bf16 and
+    summed: the sum is of the f32 values (within 1e-5 of the float64 sum of
+    the products, scaled by magnitudes), the rounded copy RNE of them."""
+    from oracle import bf16
+    from test_pjrt_cpu import SUM_AND_ROUND
+
+    rng = np.random.default_rng(33)
+    a = bf16.round_bf16(rng.standard_normal((256, 128)).astype(np.float32))
+    b = bf16.round_bf16(rng.standard_normal((128, 256)).astype(np.float32))
+    print("case: product summed and rounded", flush=True)
+    e = client.compile(SUM_AND_ROUND)
+    bufs = [client.put(bf16.to_bf16_bits(a), pjrt.BF16), client.put(bf16.to_bf16_bits(b), pjrt.BF16)]
+    outs = e.execute(bufs)
+    z, s = (o.to_numpy() for o in outs)
+    for x in bufs + outs:
+        x.destroy()
+    e.destroy()
+    y = a.astype(np.float64) @ b
+    mag = np.abs(a).astype(np.float64) @ np.abs(b)
+    want = y.sum(axis=0)
+    assert np.all(np.abs(s - want) <= 1e-5 * mag.sum(axis=0))
+    zf = bf16.from_bf16_bits(z).astype(np.float64)
+    assert np.all(np.abs(zf - y) <= 2.0 ** -8 * np.abs(y) + 1e-5 * mag)

@@ -335,3 +335,24 @@ def test_donation_aliases_in_plan(client):
     assert "alias input 0 -> output 0 not in place" in plan and "layout" in plan
     plan, _, _ = _plan(client, modules.donated("donor_add"))
     assert "alias input 0 -> output 0 in place (jax.buffer_donor)" in plan
+
+
+SUM_AND_ROUND = """func.func public @main(%a: tensor<256x128xbf16>, %b: tensor<128x256xbf16>) -> (tensor<256x256xbf16>, tensor<256xf32>) {
+  %y = stablehlo.dot_general %a, %b, contracting_dims = [1] x [0] : (tensor<256x128xbf16>, tensor<128x256xbf16>) -> tensor<256x256xf32>
+  %z = stablehlo.convert %y : (tensor<256x256xf32>) -> tensor<256x256xbf16>
+  %c = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+  %s = stablehlo.reduce(%y init: %c) applies stablehlo.add across dimensions = [0] : (tensor<256x256xf32>, tensor<f32>) -> tensor<256xf32>
+  return %z, %s : tensor<256x256xbf16>, tensor<256xf32>
+}"""
+
+
+def test_product_read_by_a_sum_stays_f32(client):
+    """An f32 product that a sum reads is written in f32 (the sum of its
+    bf16 roundings would differ); a product only ever rounded to bf16 is
+    written in bf16."""
+    plan, _, _ = _plan(client, SUM_AND_ROUND)
+    assert "] gemm (1x256x256x128)\n" in plan and "-> bf16" not in plan
+    plan, _, _ = _plan(client, SUM_AND_ROUND.replace(", %s : tensor<256x256xbf16>, tensor<256xf32>",
+                                                         " : tensor<256x256xbf16>")
+                       .replace("-> (tensor<256x256xbf16>, tensor<256xf32>)", "-> tensor<256x256xbf16>"))
+    assert "-> bf16" in plan
