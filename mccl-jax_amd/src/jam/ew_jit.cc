@@ -487,18 +487,22 @@ bool GenerateEwKernel(const Step& s, EwKernel* k, std::string* why) {
 // sums of row chunks into ws, then a second kernel adds the chunks.  The
 // value is rounded to val_type before it is combined, as the materialized
 // value would be.  i[16] set: the value is also stored, densely in the
-// iteration order, into tmp (the value's own buffer; the lowering only asks
-// for it when that order is the value's layout).
+// iteration order, into a fourth buffer (the value's own, or its bf16 copy;
+// the lowering only asks for it when that order is the value's layout).
 bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
   if (s.kind != StepKind::kEwReduce || s.i.size() != 17) return (*why = "not an ew reduce step", false);
-  const bool store = s.i[16] != 0;  // the value is also stored (into tmp, in iteration order)
+  // i[16]: the value is also stored, densely in iteration order, into the
+  // step's fourth buffer: 1 in val_type, 2 rounded to bf16 (its readers'
+  // narrow copy)
+  const bool store = s.i[16] != 0;
   const int rank = int(s.i[0]), n_in = int(s.i[7]), out_reg = int(s.i[8]), val_type = int(s.i[9]),
             out_type = int(s.i[10]), rop = int(s.i[11]), mode = int(s.i[14]);
   const int64_t rows = s.i[12], cols = s.i[13];
+  const int store_type = s.i[16] == 2 ? MK_BF16 : val_type;
   uint32_t init_bits = uint32_t(s.i[15]);
   float init;
   memcpy(&init, &init_bits, 4);
-  if (s.bufs.size() != size_t(n_in + 3)) return (*why = "malformed ew reduce step", false);
+  if (s.bufs.size() != size_t(n_in + (store ? 4 : 3))) return (*why = "malformed ew reduce step", false);
   IterSpace sp;
   if (rank < 1 || rank > kMaxRank || !Analyze(rank, &s.i[1], n_in, s.strides, s.types, &sp, why)) return false;
   if (rows * cols != sp.n || rows <= 0 || cols <= 0) return (*why = "empty or inconsistent reduction", false);
@@ -538,19 +542,19 @@ bool GenerateEwReduceKernel(const Step& s, EwKernel* k, std::string* why) {
     }
     if (store) {
       auto y = [&](int l) { return "y" + std::to_string(l) + "[0]"; };
-      if (lanes == kLanes && val_type == MK_F32) {
+      if (lanes == kLanes && store_type == MK_F32) {
         e << ind << "  *(mkj_f4*)((float*)qs + " << i0 << ") = mkj_f4{" << y(0) << ", " << y(1) << ", " << y(2)
           << ", " << y(3) << "};\n";
-        k->align[size_t(n_in + 1)] = 16;
-      } else if (lanes == kLanes && val_type == MK_BF16) {
+        k->align[size_t(n_in + 3)] = 16;
+      } else if (lanes == kLanes && store_type == MK_BF16) {
         e << ind << "  *(mkj_u2*)((unsigned short*)qs + " << i0 << ") = mkj_u2{unsigned(mkj_f2bf(" << y(0)
           << ")) | (unsigned(mkj_f2bf(" << y(1) << ")) << 16), unsigned(mkj_f2bf(" << y(2)
           << ")) | (unsigned(mkj_f2bf(" << y(3) << ")) << 16)};\n";
-        k->align[size_t(n_in + 1)] = 8;
+        k->align[size_t(n_in + 3)] = 8;
       } else {
         for (int l = 0; l < lanes; ++l) {
           std::string stmt;
-          StoreStmt(val_type, "qs", l == 0 ? i0 : i0 + " + " + std::to_string(l), y(l), &stmt);
+          StoreStmt(store_type, "qs", l == 0 ? i0 : i0 + " + " + std::to_string(l), y(l), &stmt);
           e << ind << "  " << stmt << "\n";
         }
       }

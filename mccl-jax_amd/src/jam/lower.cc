@@ -445,6 +445,7 @@ class Lowerer {
       }
       case StepKind::kEwReduce: {
         const size_t L = size_t(s.i[7]);
+        if (s.bufs.size() > L + 3) return {L, L + 1, L + 2, L + 3};
         return {L, L + 1, L + 2};
       }
       case StepKind::kGather: return {2};
@@ -3180,6 +3181,26 @@ class Lowerer {
     SetDenseView(op.results[0], d);
   }
 
+  // Every reader of v other than `except` converts it to bf16 (directly or
+  // through layout ops), and v is no program output.
+  bool OnlyBf16Converts(int v, const Op& except) {
+    if (std::count(outputs_.begin(), outputs_.end(), v) != 0) return false;
+    for (int u : users_[v]) {
+      if (&ops_[u] == &except || !live_[u]) continue;
+      const Op& o = ops_[u];
+      if (fused_.count(u)) return false;
+      if (o.name == "stablehlo.convert") {
+        if (m_.types[o.results[0]].dtype != DType::kBF16) return false;
+      } else if (o.name == "stablehlo.transpose" || o.name == "stablehlo.reshape" ||
+                 o.name == "stablehlo.broadcast_in_dim" || o.name == "stablehlo.slice") {
+        if (!NarrowOnly(o.results[0], false)) return false;
+      } else {
+        return false;
+      }
+    }
+    return true;
+  }
+
   // The ew program of value v over its leaves; false when it does not fit
   // the interpreter's limits (eight inputs, its register file).
   bool BuildEwProgram(int v, EwBuild* out, int* reg) {
@@ -3248,22 +3269,33 @@ class Lowerer {
       st.types.push_back(int32_t(lv.dtype));
       for (int k = 0; k < 6; ++k) st.strides.push_back(k < xt.rank() ? lv.strides[size_t(order[size_t(k)])] : 0);
     }
+    // stored: in f32, or only its bf16 rounding when every other reader
+    // converts it to bf16 (the sum reads the exact values inside the kernel)
+    const bool narrow_store = store && vt == DType::kF32 && OnlyBf16Converts(x, op);
     const BufRef d = DestFor(op.results[0]);
     st.bufs.push_back(d);
-    const BufRef xs = store ? DestFor(x) : NewTemp(xt.bytes());
+    const BufRef xs = store && !narrow_store ? DestFor(x) : NewTemp(xt.bytes());
     st.bufs.push_back(xs);
     const int64_t rows = lead ? nr : nk, cols = lead ? nk : nr;
     const int64_t inner = xt.dims[size_t(order.back())];
     st.bufs.push_back(lead ? NewTemp(size_t(std::max<int64_t>(int64_t(mk_col_sum_workspace_bytes(rows, cols)),
                                                                  EwReduceWorkspaceBytes(rows, cols, inner))))
                            : BufRef{});
+    BufRef xn;
+    if (narrow_store) {
+      xn = NewTemp(size_t(xt.numel()) * 2);
+      st.bufs.push_back(xn);
+    } else if (store) {
+      st.bufs.push_back(xs);
+    }
     const float fi = float(init);
     uint32_t ib;
     memcpy(&ib, &fi, 4);
     st.i = {xt.rank()};
     for (int k = 0; k < 6; ++k) st.i.push_back(k < xt.rank() ? xt.dims[size_t(order[size_t(k)])] : 1);
     st.i.push_back(int64_t(b.leaves.size()));
-    st.i.insert(st.i.end(), {reg, int64_t(vt), int64_t(ot), rop, rows, cols, lead ? 1 : 0, int64_t(ib), store ? 1 : 0});
+    st.i.insert(st.i.end(), {reg, int64_t(vt), int64_t(ot), rop, rows, cols, lead ? 1 : 0, int64_t(ib),
+                             narrow_store ? 2 : store ? 1 : 0});
     for (auto& ins : b.prog)
       for (int k = 0; k < 4; ++k) st.prog.push_back(ins[k]);
     for (uint32_t c : b.consts) {
@@ -3273,10 +3305,20 @@ class Lowerer {
     }
     st.note = body + " of " + ops_[state_[x].op].name + " chain (" + std::to_string(b.prog.size()) + " instr, " +
               std::to_string(b.leaves.size()) + " inputs, " + (lead ? "leading dims" : "trailing dims") +
-              (store ? ", value stored" : "") + ")";
+              (narrow_store ? ", bf16 copy stored" : store ? ", value stored" : "") + ")";
     Emit(st);
     SetDenseView(op.results[0], d);
-    if (store) SetDenseView(x, xs);
+    if (narrow_store) {
+      View nv;
+      nv.buf = xn;
+      nv.dtype = DType::kBF16;
+      nv.dims = xt.dims;
+      nv.strides = DenseStrides(nv.dims);
+      narrow_[x] = nv;
+      state_[x].kind = ValState::kUnset;  // its f32 form is never written
+    } else if (store) {
+      SetDenseView(x, xs);
+    }
     return true;
   }
 

@@ -77,9 +77,10 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //                               f grad_scale
 //   sdpa_bwd bufs q,k,v,o,dout,lse,dq,dk,dv,workspace
 //            i B,H,Sq,Sk,D, (b,h,s strides) of q,k,v,o,dout,dq,dk,dv, causal  f scale
-//   ew_reduce bufs in...,out,tmp,ws  i rank,dims[6],n_inputs,out_reg,val_type,out_type,rop,rows,cols,
-//                               mode,init bits,store  prog strides types f as ew (mode 0: reduce
-//                               trailing dims, mode 1: sum leading dims; store: the value into tmp too)
+//   ew_reduce bufs in...,out,tmp,ws[,stored]  i rank,dims[6],n_inputs,out_reg,val_type,out_type,rop,
+//                               rows,cols,mode,init bits,store  prog strides types f as ew (mode 0: reduce
+//                               trailing dims, mode 1: sum leading dims; store 1 / 2: the value also
+//                               into `stored`, as val_type / bf16)
 //   convert  bufs in,out        i in_type,out_type,n
 //   fill     bufs out           i elem_bytes,n,pattern
 //   copy     bufs in,out        i bytes
@@ -180,9 +181,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     }
     case StepKind::kEwReduce: {
       const int n_in = int(i[7]);
-      if (n_in > 8 || s.bufs.size() != size_t(n_in + 3) || i.size() != 17) return MK_ERR_INVALID;
+      const bool store = i.size() == 17 && i[16] != 0;
+      if (n_in > 8 || s.bufs.size() != size_t(n_in + (store ? 4 : 3)) || i.size() != 17) return MK_ERR_INVALID;
       const int mode = int(i[14]);
-      const bool store = i[16] != 0;
       if (s.jit >= 0 && f.jit_fns) {
         // generated: the reduction reads the program's inputs (mode 1: then
         // adds the row chunks' partial sums from the workspace)
@@ -193,10 +194,10 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
           ptrs[b] = P(size_t(b));
           aligned = reinterpret_cast<uintptr_t>(ptrs[b]) % k.align[size_t(b)] == 0;
         }
-        if (store) aligned = aligned && reinterpret_cast<uintptr_t>(P(size_t(n_in + 1))) % k.align[size_t(n_in + 1)] == 0;
+        if (store) aligned = aligned && reinterpret_cast<uintptr_t>(P(size_t(n_in + 3))) % k.align[size_t(n_in + 3)] == 0;
         if (aligned) {
           ptrs[n_in] = k.kind == 1 ? P(size_t(n_in)) : P(size_t(n_in + 2));
-          ptrs[n_in + 1] = P(size_t(n_in + 1));
+          if (store) ptrs[n_in + 1] = P(size_t(n_in + 3));
           void* args[10];
           for (int b = 0; b <= n_in + (store ? 1 : 0); ++b) args[b] = &ptrs[b];
           hipError_t e = hipModuleLaunchKernel(static_cast<hipFunction_t>(f.jit_fns[2 * s.jit]), k.blocks, 1, 1,
@@ -228,11 +229,17 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
       int rc = mk_ew_program_multi(st, int(i[0]), &i[1], n_in, ins, types, s.strides.data(), int(s.prog.size() / 4),
                                    s.prog.data(), s.f.data(), int(s.f.size()), 1, &reg, &vt, &tmp);
       if (rc != MK_OK) return rc;
-      if (mode == 1) return mk_col_sum(st, vt, i[12], i[13], tmp, static_cast<float*>(P(size_t(n_in))), P(size_t(n_in + 2)));
-      uint32_t ib = uint32_t(i[15]);
-      float init;
-      memcpy(&init, &ib, 4);
-      return mk_row_reduce(st, vt, int(i[10]), int(i[11]), i[12], i[13], tmp, init, P(size_t(n_in)));
+      if (mode == 1) {
+        rc = mk_col_sum(st, vt, i[12], i[13], tmp, static_cast<float*>(P(size_t(n_in))), P(size_t(n_in + 2)));
+      } else {
+        uint32_t ib = uint32_t(i[15]);
+        float init;
+        memcpy(&init, &ib, 4);
+        rc = mk_row_reduce(st, vt, int(i[10]), int(i[11]), i[12], i[13], tmp, init, P(size_t(n_in)));
+      }
+      // the stored copy: the value itself (tmp is that buffer) or its bf16 rounding
+      if (rc == MK_OK && store && i[16] == 2) rc = mk_convert(st, vt, MK_BF16, i[12] * i[13], tmp, P(size_t(n_in + 3)));
+      return rc;
     }
     case StepKind::kGather:
       return mk_gather_rows(st, i[0], i[1], P(0), int(i[2]), i[3], P(1), P(2));

@@ -461,3 +461,43 @@ def test_sum_of_a_product_also_rounded_to_bf16(client):
     assert np.all(np.abs(s - want) <= 1e-5 * mag.sum(axis=0))
     zf = bf16.from_bf16_bits(z).astype(np.float64)
     assert np.all(np.abs(zf - y) <= 2.0 ** -8 * np.abs(y) + 1e-5 * mag)
+
+
+@pytest.mark.parametrize("shape,rdims", [((64, 768), [1]), ((6, 512, 768), [0, 1])])
+def test_fused_reduction_stores_a_bf16_copy(client, shape, rdims):
+    """The value's other readers only convert it to bf16: the reduction's
+    kernel stores just that bf16 copy (its f32 form is never written) and
+    sums the exact f32 values."""
+    from oracle import bf16
+
+    st = "x".join(str(d) for d in shape)
+    keep = [d for d in range(len(shape)) if d not in rdims]
+    ot = "x".join(str(shape[d]) for d in keep)
+    text = f"""func.func public @main(%x: tensor<{st}xf32>, %y: tensor<{st}xf32>) -> (tensor<{ot}xf32>, tensor<{st}xbf16>) {{
+  %e = stablehlo.multiply %x, %y : tensor<{st}xf32>
+  %z = stablehlo.constant dense<0.000000e+00> : tensor<f32>
+  %r = stablehlo.reduce(%e init: %z) applies stablehlo.add across dimensions = {rdims} : (tensor<{st}xf32>, tensor<f32>) -> tensor<{ot}xf32>
+  %d = stablehlo.convert %e : (tensor<{st}xf32>) -> tensor<{st}xbf16>
+  return %r, %d : tensor<{ot}xf32>, tensor<{st}xbf16>
+}}"""
+    rng = np.random.default_rng(34)
+    x = rng.standard_normal(shape).astype(np.float32)
+    y = rng.standard_normal(shape).astype(np.float32)
+    print(f"case: ew_reduce bf16 copy {shape} over {rdims}", flush=True)
+    os.environ["JAM_EW_JIT_STRICT"] = "1"
+    try:
+        e = client.compile(text)
+    finally:
+        del os.environ["JAM_EW_JIT_STRICT"]
+    assert "bf16 copy stored" in e.plan()
+    bufs = [client.put(x), client.put(y)]
+    outs = e.execute(bufs)
+    r, d = (o.to_numpy() for o in outs)
+    for b in bufs + outs:
+        b.destroy()
+    e.destroy()
+    v = x * y
+    np.testing.assert_array_equal(d, bf16.to_bf16_bits(v))
+    want = np.sum(v.astype(np.float64), axis=tuple(rdims))
+    mag = np.sum(np.abs(v).astype(np.float64), axis=tuple(rdims))
+    assert np.all(np.abs(r - want) <= 1e-6 * mag + 1e-30)
