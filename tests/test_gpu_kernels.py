@@ -421,7 +421,11 @@ def test_sdpa_c3_full_size_sampled_rows(K, S):
     print(f"case: sdpa C3 full S={S}", flush=True)
     qd, kd, vd = dev_bf16(d["q"]), dev_bf16(d["k"]), dev_bf16(d["v"])
     scale = 1 / math.sqrt(128)
-    o = host_bf16(K.sdpa_fwd(qd, kd, vd, scale, True))
+    # NaN-filled output: every query tile of every (b, h) must be written
+    # (S >= 8192 runs the XCD-grouped tile order)
+    out = torch.full_like(qd, float("nan"))
+    o = host_bf16(K.sdpa_fwd(qd, kd, vd, scale, True, out=out))
+    assert bool(torch.isfinite(out).all())
     np.testing.assert_array_equal(o[:, :, 0, :], d["v"][:, :, 0, :])
     if S <= 2048:
         pairs = [(b, h) for b in range(4) for h in range(16)]
@@ -454,6 +458,30 @@ def test_sdpa_c3_full_size_sampled_rows(K, S):
             bad = e > 2.0 ** -8 * wabs + 2.0 ** -9 * np.abs(want) + 1e-6
             assert not bad.any(), (b, h, rr[np.nonzero(bad)[0][:5]], e[bad][:5])
     print(f"case: sdpa C3 full S={S} max abs err {worst:.2e} over {len(pairs)} (b,h) x {len(rows)} rows", flush=True)
+
+
+def test_sdpa_noncausal_long_grouped_order(K):
+    """Non-causal B1 H16 S8192 D128: 512 workgroups of 256 rows, so the
+    8-wave kernel runs its XCD-grouped tile order with ascending query
+    tiles.  Every row is written (NaN-filled output) and sampled rows of
+    four heads, spread over query tiles, match the float64 oracle."""
+    B, H, S, D = 1, 16, 8192, 128
+    rng = np.random.default_rng(77)
+    x = [bf16.to_bf16_bits((rng.standard_normal((B, H, S, D)) / math.sqrt(D)).astype(np.float32)) for _ in range(3)]
+    print("case: sdpa non-causal B1 H16 S8192 D128", flush=True)
+    qd, kd, vd = (dev_bf16(a) for a in x)
+    out = torch.full_like(qd, float("nan"))
+    K.sdpa_fwd(qd, kd, vd, 1 / math.sqrt(D), False, out=out)
+    assert bool(torch.isfinite(out).all())
+    o = host_bf16(out)
+    rows = np.array([0, 255, 256, 4095, 4096, 8191] + list(rng.integers(0, S, 26)))
+    for h in (0, 5, 10, 15):
+        qf, kf, vf = (bf16.from_bf16_bits(a[0, h]).astype(np.float64) for a in x)
+        sc = (qf[rows] @ kf.T) / math.sqrt(D)
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        want = (p @ vf) / p.sum(axis=1, keepdims=True)
+        got = bf16.from_bf16_bits(o[0, h, rows]).astype(np.float64)
+        assert np.abs(got - want).max() <= 2e-2, (h, np.abs(got - want).max())
 
 
 def test_sdpa_prefix_mean_closed_form(K):
