@@ -83,6 +83,18 @@ int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, c
                    int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C,
                    int64_t c_ms, int64_t splits, void* workspace);
 
+/* mk_gemm_splitk with the output type chosen (c_type MK_F32, or MK_BF16:
+ * the ordered fp32 slice sum rounded once to bf16) and, for bf16 operands
+ * the tiled kernel takes (16-byte aligned rows), any K: when K % splits != 0
+ * the slices are ceil(K / splits) rounded up to a multiple of 8 apart and the
+ * last one is shorter (the vocabulary products of the training step, which
+ * contract over 50257 tokens' classes).  Same workspace size and rules as
+ * mk_gemm_splitk otherwise (bf16 C: 8-byte aligned).
+ * Replaces, for these products: src/jam/ops/linalg.mm:98. */
+int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K, const void* A,
+                         int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* C,
+                         int64_t c_ms, int64_t splits, void* workspace);
+
 /* Plain GEMM through rocBLAS (the linear layers of the training step and
  * their gradients: with no epilogue to fuse, a library GEMM does the work).  Same operand convention as
  * mk_gemm (row-major C with row stride c_ms, one unit stride per operand),
@@ -416,6 +428,18 @@ int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const
 int mk_softmax_xent_typed(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
                           const void* logits, int label_type, const void* labels, float grad_scale,
                           float* loss_rows, void* dlogits);
+
+/* mk_softmax_xent_typed over rows `ld_logits` / `ld_dlogits` elements apart
+ * (each >= cols; only the first cols elements of a row are read or written):
+ * a vocabulary of 50257 classes kept in rows padded to 16-byte multiples, so
+ * that the products reading the gradient take aligned operand rows.  Type
+ * pairs bf16/bf16, f32/f32 (dlogits may alias logits when the pitches are
+ * equal) and f32/bf16; same loss, gradient and label rules.
+ * Replaces, for the fused loss of a jitted step: src/jam/ops/elementwise.mm:71-89
+ * (the softmax of the logits and its gradient through the one-hot select). */
+int mk_softmax_xent_strided(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
+                            const void* logits, int64_t ld_logits, int label_type, const void* labels,
+                            float grad_scale, float* loss_rows, void* dlogits, int64_t ld_dlogits);
 
 /* One Adam step, the update of temp/dp_train.py:71-75:
  *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2

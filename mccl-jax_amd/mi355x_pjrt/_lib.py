@@ -71,12 +71,15 @@ SIGNATURES = {
     "mk_gelu_tanh_bwd_colsum": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P, _P]),
     "mk_gemm_splitk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "mk_gemm_splitk": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
+    "mk_gemm_splitk_typed": (_I, [_P, _I, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                  _P]),
     "mk_gemm_blas_splitk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "mk_gemm_blas_splitk": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
     "mk_adam_update_dev": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P, _P, ctypes.c_double, ctypes.c_double,
                                 ctypes.c_double]),
     "mk_softmax_xent": (_I, [_P, _I, _I64, _I64, _P, _I, _P, _F, _P, _P]),
     "mk_softmax_xent_typed": (_I, [_P, _I, _I, _I64, _I64, _P, _I, _P, _F, _P, _P]),
+    "mk_softmax_xent_strided": (_I, [_P, _I, _I, _I64, _I64, _P, _I64, _I, _P, _F, _P, _P, _I64]),
     "mk_adam_update": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P] + [ctypes.c_double] * 6),
     "mk_sdpa_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
     "mk_sdpa_bwd": (_I, [_P, _I64, _I64, _I64, _I64, _I64]

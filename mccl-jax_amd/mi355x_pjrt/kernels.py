@@ -352,17 +352,24 @@ def gemm_blas(a, b, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
     return out
 
 
-def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None):
-    """fp32 out = a @ b with the contraction cut into `splits` slices summed
-    in order (mk_gemm_splitk, hand-written kernels); a [M, K], b [K, N] 2-D views."""
+def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=torch.float32):
+    """out = a @ b with the contraction cut into `splits` slices summed in
+    order in fp32 (mk_gemm_splitk; mk_gemm_splitk_typed for a bf16 `out_dtype`
+    or a K that `splits` does not divide); a [M, K], b [K, N] 2-D views."""
     _require_cuda(a, b)
     M, Kd = a.shape
     N = b.shape[1]
-    out = torch.empty(M, N, dtype=torch.float32, device=a.device) if out is None else out
+    out = torch.empty(M, N, dtype=out_dtype, device=a.device) if out is None else out
     ws = _ws(lib().mk_gemm_splitk_workspace_bytes(M, N, splits), a.device, workspace)
-    rc = lib().mk_gemm_splitk(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
-                              _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), splits, _ptr(ws))
-    _check(rc, "mk_gemm_splitk")
+    if out.dtype == torch.float32 and Kd % splits == 0:
+        rc = lib().mk_gemm_splitk(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
+                                  _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), splits, _ptr(ws))
+        _check(rc, "mk_gemm_splitk")
+        return out
+    rc = lib().mk_gemm_splitk_typed(_stream(stream), mk_dtype(a.dtype), mk_dtype(out.dtype), M, N, Kd, _ptr(a),
+                                    a.stride(0), a.stride(1), _ptr(b), b.stride(0), b.stride(1), _ptr(out),
+                                    out.stride(0), splits, _ptr(ws))
+    _check(rc, "mk_gemm_splitk_typed")
     return out
 
 
@@ -485,6 +492,16 @@ def softmax_xent(logits, labels, grad_scale, loss_rows=None, dlogits=None, strea
     rows = logits.numel() // cols
     loss_rows = torch.empty(rows, dtype=torch.float32, device=logits.device) if loss_rows is None else loss_rows
     dlogits = torch.empty_like(logits) if dlogits is None else dlogits
+    if logits.dim() == 2 and (logits.stride(0) != cols or dlogits.stride(0) != cols):
+        # row pitches of 2-D views (padded rows): mk_softmax_xent_strided
+        if logits.stride(1) != 1 or dlogits.stride(1) != 1 or dlogits.shape != logits.shape:
+            raise ValueError("softmax_xent: rows must be contiguous")
+        rc = lib().mk_softmax_xent_strided(_stream(stream), mk_dtype(logits.dtype), mk_dtype(dlogits.dtype), rows,
+                                           cols, _ptr(logits), logits.stride(0), mk_dtype(labels.dtype),
+                                           _ptr(labels), float(grad_scale), _ptr(loss_rows), _ptr(dlogits),
+                                           dlogits.stride(0))
+        _check(rc, "mk_softmax_xent_strided")
+        return loss_rows, dlogits
     rc = lib().mk_softmax_xent_typed(_stream(stream), mk_dtype(logits.dtype), mk_dtype(dlogits.dtype), rows, cols,
                                      _ptr(logits), mk_dtype(labels.dtype), _ptr(labels), float(grad_scale),
                                      _ptr(loss_rows), _ptr(dlogits))

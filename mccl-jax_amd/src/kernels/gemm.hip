@@ -335,23 +335,47 @@ extern "C" size_t mk_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t s
   return size_t(M * N * splits * 4);
 }
 
+extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K,
+                                    const void* A, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks,
+                                    int64_t b_ns, void* C, int64_t c_ms, int64_t splits, void* workspace) {
+  clear_error();
+  if (splits < 1 || K < 0 || M < 0 || N < 0) return fail(MK_ERR_INVALID, "mk_gemm_splitk: bad shape or splits");
+  if (c_type != MK_F32 && c_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: c_type must be f32 or bf16");
+  if (splits == 1 || M == 0 || N == 0)
+    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
+  if (!workspace || !C) return fail(MK_ERR_INVALID, "mk_gemm_splitk: null workspace or output");
+  const uintptr_t cal = c_type == MK_F32 ? 15u : 7u;
+  if ((N % 4) != 0 || (c_ms % 4) != 0 || (reinterpret_cast<uintptr_t>(C) & cal) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: N and c_ms multiples of 4, aligned C and workspace");
+  float* W = static_cast<float*>(workspace);
+  hipStream_t s = as_stream(stream);
+  if (K % splits == 0) {
+    // slice s reads A[:, s ks : (s+1) ks] and B[s ks : (s+1) ks, :] (element
+    // strides along k) and writes W[s]: one batched mk_gemm, then the ordered sum
+    const int64_t ks = K / splits;
+    if (int rc = mk_gemm(stream, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks,
+                         b_ns, W, M * N, N, nullptr, 0))
+      return rc;
+    return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type);
+  }
+  // uneven slices: ks apart (a multiple of 8, so every slice starts on a
+  // 16-byte boundary of a k-contiguous operand), the last one K - (splits-1) ks
+  // long; only the tiled kernel takes a per-batch contraction length
+  const int64_t ks = ((K + splits - 1) / splits + 7) / 8 * 8;
+  const int64_t rem = K - (splits - 1) * ks;
+  if (ab_type != MK_BF16 || rem <= 0)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K % splits != 0 needs bf16 operands and a non-empty last slice");
+  const int r = gemm_tiled(s, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns, W, M * N,
+                           N, nullptr, 0, rem);
+  if (r < 0) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K % splits != 0 needs operands the tiled GEMM takes");
+  if (r != MK_OK) return r;
+  return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type);
+}
+
 extern "C" int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_ms,
                               int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C, int64_t c_ms,
                               int64_t splits, void* workspace) {
-  clear_error();
-  if (splits < 1 || K < 0 || M < 0 || N < 0) return fail(MK_ERR_INVALID, "mk_gemm_splitk: bad shape or splits");
-  if (splits == 1 || M == 0 || N == 0)
-    return mk_gemm(stream, ab_type, MK_F32, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
-  if (K % splits != 0) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K must be a multiple of splits");
-  if (!workspace || !C) return fail(MK_ERR_INVALID, "mk_gemm_splitk: null workspace or output");
-  if ((N % 4) != 0 || (c_ms % 4) != 0 || ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(workspace)) & 15))
-    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: N and c_ms multiples of 4, 16-byte aligned C and workspace");
-  const int64_t ks = K / splits;
-  // slice s reads A[:, s ks : (s+1) ks] and B[s ks : (s+1) ks, :] (element
-  // strides along k) and writes W[s]: one batched mk_gemm, then the ordered sum
-  float* W = static_cast<float*>(workspace);
-  if (int rc = mk_gemm(stream, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns,
-                       W, M * N, N, nullptr, 0))
-    return rc;
-  return splitk_sum(as_stream(stream), W, splits, M, N, C, c_ms, "mk_gemm_splitk");
+  return mk_gemm_splitk_typed(stream, ab_type, MK_F32, M, N, K, A, a_ms, a_ks, B, b_ks, b_ns, C, c_ms, splits,
+                              workspace);
 }

@@ -31,7 +31,16 @@
 // 32 lanes, here 4 k-rows x 4 chunks.  (An XOR with r & 7, or 2 (r & 3),
 // leaves two rows of each group on the same banks and halves the read rate.)
 // Chunks past M, N or K are loaded from an out-of-range buffer offset, which
-// reads zeros.
+// reads zeros.  A chunk that straddles M or N (an m- / n-contiguous operand
+// whose extent is not a multiple of 8) is loaded whole: its extra elements
+// lie inside the row pitch (or past the buffer's range, reading zeros) and
+// only reach C rows / columns that are never stored.  A chunk that straddles
+// K (a k-contiguous operand, K not a multiple of 8) is loaded whole too.  In
+// the last k tile the wave that copied a straddling chunk rewrites it in LDS
+// (between two barriers) from the operand, element by element, with zeros
+// past the end: K-straddling chunks then add exact zeros whatever the row
+// pitch held, and the operand's last row, whose straddling chunk ran past
+// the buffer range (read as zeros), gets its valid elements back.
 //
 // Tile order: workgroups are dealt round-robin to the 8 XCDs, each with its
 // own L2, so workgroup i takes tile (i % 8) * (tiles / 8) + i / 8 of an
@@ -58,6 +67,7 @@ struct TiledGemm {
   void* C;
   const void* bias;
   int64_t M, N, K;
+  int64_t k_rem;              // > 0: K of the last batch (a split-K's last, shorter slice)
   int64_t lda, ldb, ldc;      // element stride of A's, B's, C's non-unit dimension
   int64_t a_bs, b_bs, c_bs;   // batch strides (elements)
   uint32_t a_bytes, b_bytes;  // bytes addressable from one batch's A / B base
@@ -128,6 +138,52 @@ struct Copies {
   // first), or an offset that reads zeros once the chunk lies past K
   __device__ inline int at(int c, int k0, uint32_t step, int64_t K) const {
     return int64_t(k[c]) + k0 < K ? int(off[c] + step) : kInvalid;
+  }
+  // Chunks of the last k tile (k0) that straddle the operand's end: along
+  // K for a k-contiguous operand (K % 8 != 0), along the rows for an m- /
+  // n-contiguous one (rows % 8 != 0).  The copy loaded such a chunk whole,
+  // so its elements past the end hold whatever the row pitch held, and in the
+  // operand's last row (k-row) the part past the buffer range read as zeros.
+  // Called between two barriers once the tile is in LDS: the lane rewrites
+  // its chunk from the operand itself, element by element, with zeros past
+  // the end (base: the batch's operand base; step: the copy's byte step per
+  // k tile).
+  __device__ inline void refill_ragged(uint16_t* tile, const char* base, uint32_t step, int kt, int wave, int lane,
+                                       int64_t r0, int64_t rows, int64_t K) const {
+    const int k0 = BK * kt;
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      const int u = 64 * (wave + W * c) + lane;
+      int64_t gr, kk;
+      int n;
+      bool straddle;
+      if constexpr (KC) {
+        constexpr int kCpr = BK / 8;
+        const int row = u / kCpr;
+        gr = r0 + row;
+        kk = int64_t(8 * ((u % kCpr) ^ kc_swizzle<BK>(row))) + k0;
+        straddle = gr < rows && kk < K && kk + 8 > K;
+        n = int(K - kk);
+      } else {
+        constexpr int kCpr = R / 8;
+        const int kr = u / kCpr;
+        gr = r0 + 8 * ((u % kCpr) ^ nc_swizzle<R>(kr));
+        kk = int64_t(kr) + k0;
+        straddle = kk < K && gr < rows && gr + 8 > rows;
+        n = int(rows - gr);
+      }
+      if (straddle) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(base + (off[c] + uint32_t(kt) * step));
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = 2 * e < n ? uint32_t(src[2 * e]) : 0u;
+          const uint32_t hi = 2 * e + 1 < n ? uint32_t(src[2 * e + 1]) : 0u;
+          w[e] = lo | (hi << 16);
+        }
+        *reinterpret_cast<u32x4_t*>(tile + (wave + W * c) * 512 + 8 * lane) = u32x4_t{w[0], w[1], w[2], w[3]};
+      }
+    }
   }
 };
 
@@ -389,6 +445,8 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   const int64_t m0 = int64_t(first_m + w_in % gm) * TM;
   const int64_t n0 = int64_t(w_in / gm) * TN;
   const int64_t bz = blockIdx.y;
+  // contraction length of this batch
+  const int64_t Kb = (p.k_rem > 0 && bz == int64_t(gridDim.y) - 1) ? p.k_rem : p.K;
   const i32x4_t ra = tile_desc(reinterpret_cast<const uint16_t*>(p.A) + bz * p.a_bs, p.a_bytes);
   const i32x4_t rb = tile_desc(reinterpret_cast<const uint16_t*>(p.B) + bz * p.b_bs, p.b_bytes);
 
@@ -401,7 +459,7 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   // then B's kCb)
   auto issue = [&](int kt, int stage, int lo, int hi) __attribute__((always_inline)) {
     const int k0 = BK * kt;
-    if (k0 + BK <= p.K) {
+    if (k0 + BK <= Kb) {
       const uint32_t sa = uint32_t(kt) * a_step, sb = uint32_t(kt) * b_step;
 #pragma unroll
       for (int c = 0; c < kCa + kCb; ++c) {
@@ -415,10 +473,10 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
     for (int c = 0; c < kCa + kCb; ++c) {
       if (c < lo || c >= hi) continue;
       if (c < kCa)
-        copy_to_lds(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), ca.at(c, k0, uint32_t(kt) * a_step, p.K));
+        copy_to_lds(ra, lds_addr(&As[stage][(wave + kW * c) * 512]), ca.at(c, k0, uint32_t(kt) * a_step, Kb));
       else
         copy_to_lds(rb, lds_addr(&Bs[stage][(wave + kW * (c - kCa)) * 512]),
-                    cb.at(c - kCa, k0, uint32_t(kt) * b_step, p.K));
+                    cb.at(c - kCa, k0, uint32_t(kt) * b_step, Kb));
     }
   };
 
@@ -438,15 +496,15 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
   // each after the operand reads of one k-step: a wave that issued all of
   // them at once would stall on the full vector-memory queue (1 KB copies
   // drain at about 60 bytes per clock per CU) with its MFMAs behind them.
-  const int nk = int((p.K + BK - 1) / BK);
+  const int nk = int((Kb + BK - 1) / BK);
+  // an operand chunk straddles K, M or N (wave-uniform)
+  const bool ragged = (((AKC || BKC) ? Kb : 0) & 7) != 0 || (!AKC && (p.M & 7) != 0) || (!BKC && (p.N & 7) != 0);
   constexpr int kNC = kCa + kCb, kParts = BK / 16 < 2 ? BK / 16 : 2;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < nk) issue(st, st, 0, kNC);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + S - 2 < nk) wait_vm<(S - 2) * kNC>();
-    else wait_vm<0>();
-    lds_barrier();
+  // multiply k tile kt (in stage kt % S), issuing the copies of tile kt + S - 1
+  auto multiply = [&](int kt) __attribute__((always_inline)) {
     const bool more = kt + S - 1 < nk;
     const uint16_t* at = As[kt % S];
     const uint16_t* bt = Bs[kt % S];
@@ -464,6 +522,31 @@ __global__ __launch_bounds__(64 * Sh::WGM * Sh::WGN, 1) void gemm_tiled_kernel(c
         for (int b = 0; b < kJ; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[b], af[a], acc[a][b], 0, 0, 0);
     }
+  };
+  // with an operand chunk straddling K, M or N the last k tile runs after
+  // the loop, with the refill
+  const int nk_loop = ragged ? nk - 1 : nk;
+  for (int kt = 0; kt < nk_loop; ++kt) {
+    if (kt + S - 2 < nk) wait_vm<(S - 2) * kNC>();
+    else wait_vm<0>();
+    lds_barrier();
+    multiply(kt);
+  }
+  if (ragged) {
+    // the last k tile is in LDS: each wave rewrites the chunks it copied
+    // that straddle K, M or N from the operands (zeros past the end), then
+    // a second barrier publishes them.  The batch's operand bases are taken
+    // from the copy descriptors (held through the loop anyway).
+    wait_vm<0>();
+    lds_barrier();
+    auto desc_base = [](const i32x4_t& r) __attribute__((always_inline)) {
+      return reinterpret_cast<const char*>((uint64_t(uint32_t(r.y) & 0xFFFFu) << 32) | uint32_t(r.x));
+    };
+    const int kt = nk - 1;
+    ca.refill_ragged(As[kt % S], desc_base(ra), a_step, kt, wave, lane, m0, p.M, Kb);
+    cb.refill_ragged(Bs[kt % S], desc_base(rb), b_step, kt, wave, lane, n0, p.N, Kb);
+    lds_barrier();
+    multiply(kt);
   }
   lds_barrier();  // every wave is done with the operand stages before they hold C
 
@@ -511,25 +594,27 @@ int64_t span_bytes(bool kc, int64_t rows, int64_t K, int64_t ld) {
 // not fit the tiled kernel.
 bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
                 const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
-                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue) {
-  if (M < 128 || N < 128 || K < 64 || K % 8 != 0) return false;
+                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem) {
+  if (M < 128 || N < 128 || K < 64) return false;
+  if (k_rem < 0 || k_rem > K || (k_rem > 0 && (batch < 2 || K % 8 != 0))) return false;
   a_kc = a_ks == 1;
   b_kc = b_ks == 1;
   if (!a_kc && a_ms != 1) return false;
   if (!b_kc && b_ns != 1) return false;
   const int64_t lda = a_kc ? a_ms : a_ks, ldb = b_kc ? b_ns : b_ks;
-  // every 16-byte chunk a copy loads is aligned and lies wholly inside or
-  // wholly outside the operand: 16-byte bases, strides multiples of 8
-  // elements, the contiguous extent (K, or M / N) a multiple of 8
+  // every 16-byte chunk a copy loads is aligned: 16-byte bases, strides
+  // multiples of 8 elements.  The pitch is then at least the contiguous
+  // extent rounded up to 8, so a chunk straddling K, M or N stays inside its
+  // row's pitch (or runs past the buffer range, which reads zeros).
   auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
   if (!al16(A) || !al16(B) || lda % 8 != 0 || ldb % 8 != 0) return false;
   if (batch > 1 && (a_bs % 8 != 0 || b_bs % 8 != 0)) return false;
-  if ((!a_kc && M % 8 != 0) || (!b_kc && N % 8 != 0)) return false;
   if (lda < (a_kc ? K : M) || ldb < (b_kc ? K : N)) return false;  // overlapping rows
   const int64_t ab = span_bytes(a_kc, M, K, lda), bb = span_bytes(b_kc, N, K, ldb);
   if (ab >= (int64_t(1) << 31) || bb >= (int64_t(1) << 31)) return false;  // 32-bit buffer offsets
   a.A = A; a.B = B; a.C = C; a.bias = bias;
   a.M = M; a.N = N; a.K = K;
+  a.k_rem = k_rem;
   a.lda = lda; a.ldb = ldb; a.ldc = c_ms;
   a.a_bs = a_bs; a.b_bs = b_bs; a.c_bs = c_bs;
   a.a_bytes = uint32_t(ab); a.b_bytes = uint32_t(bb);
@@ -558,11 +643,11 @@ int64_t cu_count() {
 
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
-               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue) {
+               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem) {
   TiledGemm a;
   bool a_kc, b_kc;
   if (!tiled_args(a, a_kc, b_kc, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs, c_ms,
-                  bias, epilogue))
+                  bias, epilogue, k_rem))
     return -1;
   // Kernel shape: the one with the least estimated time.  Each shape has a
   // throughput per CU measured on a large product (8192 x 8192 x 4096: 1240,

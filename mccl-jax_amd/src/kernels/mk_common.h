@@ -26,16 +26,21 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
 
 // C = sum of the splits dense M x N fp32 slices of W, added in slice order
-// (blas.hip); N and c_ms multiples of 4, W and C 16-byte aligned.
-int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, float* C, int64_t c_ms,
-               const char* what);
+// (blas.hip), stored as c_type (MK_F32, or MK_BF16 rounded once from the
+// fp32 sum); N and c_ms multiples of 4, W 16-byte and C 16- (fp32) or
+// 8-byte (bf16) aligned.
+int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, void* C, int64_t c_ms,
+               const char* what, int c_type = 0);
 
 // Tiled bf16 GEMM for large products behind mk_gemm (gemm_tiled.hip), same
 // operand convention; returns -1 without launching when the shape, strides or
-// alignment do not fit it, else MK_OK or an MK_ERR_* code.
+// alignment do not fit it, else MK_OK or an MK_ERR_* code.  k_rem > 0: the
+// last batch contracts over its first k_rem k only (the last, shorter slice
+// of a split along K whose slices are K apart).
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
-               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue);
+               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue,
+               int64_t k_rem = 0);
 
 // Flash attention backward behind mk_sdpa_bwd for head_dim 64 / 128
 // (attention_bwd.hip); workspace: the per-row statistics.

@@ -561,12 +561,13 @@ struct IntC {
 // combined across the workgroup; lse = max + log(sum).  loss = lse - x[label].
 // Pass 2: dlogits = (exp(x - lse) - [j == label]) * grad_scale.
 template <typename T, typename L>
-__global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restrict__ logits, int64_t cols,
+__global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restrict__ logits, int64_t cols, int64_t ld_in,
                                                             const L* __restrict__ labels, float grad_scale,
-                                                            float* __restrict__ loss, T* __restrict__ dlogits) {
+                                                            float* __restrict__ loss, T* __restrict__ dlogits,
+                                                            int64_t ld_out) {
   __shared__ float sm[kBlock / 64], ss[kBlock / 64];
   const int64_t row = blockIdx.x;
-  const T* xr = logits + row * cols;
+  const T* xr = logits + row * ld_in;
   float m = -INFINITY, s = 0.f;
   for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
     const float v = ldf<T>(xr, j);
@@ -601,7 +602,7 @@ __global__ __launch_bounds__(kBlock) void softmax_xent_kernel(const T* __restric
   const int64_t lab = int64_t(labels[row]);
   const bool lab_ok = lab >= 0 && lab < cols;
   if (threadIdx.x == 0 && loss) loss[row] = lab_ok ? lse - ldf<T>(xr, lab) : lse;
-  T* dr = dlogits + row * cols;
+  T* dr = dlogits + row * ld_out;
   for (int64_t j = threadIdx.x; j < cols; j += kBlock) {
     const float p = __expf(ldf<T>(xr, j) - lse);
     stf<T>(dr, j, (p - (j == lab ? 1.f : 0.f)) * grad_scale);
@@ -620,16 +621,16 @@ constexpr uint32_t kBf16NegInfPair = 0xFF80FF80u;
 
 template <int NVT, typename L>
 __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const uint16_t* logits, int64_t cols,
-                                                                       const L* __restrict__ labels,
+                                                                       int64_t ld_in, const L* __restrict__ labels,
                                                                        float grad_scale, float* __restrict__ loss,
-                                                                       uint16_t* dlogits) {
+                                                                       uint16_t* dlogits, int64_t ld_out) {
   constexpr int NW = kXentThreads / 64;
   constexpr float kL2e = 1.4426950408889634f;
   __shared__ float red[NW];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const uint16_t* xr = logits + row * cols;
-  uint16_t* dr = dlogits + row * cols;
+  const uint16_t* xr = logits + row * ld_in;
+  uint16_t* dr = dlogits + row * ld_out;
   const int64_t head = min<int64_t>(cols, int64_t(((16u - (reinterpret_cast<uintptr_t>(xr) & 15u)) & 15u) / 2u));
   const int64_t nv = (cols - head) / 8, tail = cols - head - nv * 8;
   const u32x4_t* xv = reinterpret_cast<const u32x4_t*>(xr + head);
@@ -720,15 +721,15 @@ constexpr int kXentF32Threads = 1024;
 
 template <int NPT, typename L>
 __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_kernel(
-    const float* __restrict__ logits, int64_t cols, const L* __restrict__ labels, float grad_scale,
-    float* __restrict__ loss, uint16_t* __restrict__ dlogits) {
+    const float* __restrict__ logits, int64_t cols, int64_t ld_in, const L* __restrict__ labels, float grad_scale,
+    float* __restrict__ loss, uint16_t* __restrict__ dlogits, int64_t ld_out) {
   constexpr int NW = kXentF32Threads / 64;
   constexpr float kL2e = 1.4426950408889634f;
   __shared__ float red[NW];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const float* xr = logits + row * cols;
-  uint16_t* dr = dlogits + row * cols;
+  const float* xr = logits + row * ld_in;
+  uint16_t* dr = dlogits + row * ld_out;
   const int64_t lab = int64_t(labels[row]);
   const bool lab_ok = lab >= 0 && lab < cols;
   const float xlab = xr[lab_ok ? lab : 0];
@@ -776,16 +777,16 @@ __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_kernel(
 // row per CU stays resident between the passes) and writes dlogits.
 template <int C, typename L>
 __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_stream_kernel(
-    const float* __restrict__ logits, int64_t cols, const L* __restrict__ labels, float grad_scale,
-    float* __restrict__ loss, uint16_t* __restrict__ dlogits) {
+    const float* __restrict__ logits, int64_t cols, int64_t ld_in, const L* __restrict__ labels, float grad_scale,
+    float* __restrict__ loss, uint16_t* __restrict__ dlogits, int64_t ld_out) {
   constexpr int NW = kXentF32Threads / 64;
   constexpr float kL2e = 1.4426950408889634f;
   constexpr int64_t kChunk = int64_t(C) * kXentF32Threads;
   __shared__ float red[NW];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const float* xr = logits + row * cols;
-  uint16_t* dr = dlogits + row * cols;
+  const float* xr = logits + row * ld_in;
+  uint16_t* dr = dlogits + row * ld_out;
   const int64_t lab = int64_t(labels[row]);
   const bool lab_ok = lab >= 0 && lab < cols;
   const float xlab = xr[lab_ok ? lab : 0];
@@ -835,6 +836,84 @@ __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_stream_
         const float pr = __builtin_amdgcn_exp2f(fmaf(xr[j] - M, kL2e, -ls2));
         dr[j] = f32_to_bf16((j == lab ? pr - 1.f : pr) * grad_scale);
       }
+    }
+  }
+}
+
+// fp32 logits, bf16 dlogits, rows 16-byte aligned (a padded row pitch): the
+// row held in registers as NV 16-byte vectors per thread (vector v on thread
+// v % kXentF32Threads), read once; dlogits stored as 8-byte groups of four.
+// A last, partial vector is read and written element by element, so nothing
+// past `cols` is touched.  Same arithmetic as softmax_xent_f32_bf16_kernel.
+template <int NV, typename L>
+__global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_vec_kernel(
+    const float* __restrict__ logits, int64_t cols, int64_t ld_in, const L* __restrict__ labels, float grad_scale,
+    float* __restrict__ loss, uint16_t* __restrict__ dlogits, int64_t ld_out) {
+  constexpr int NW = kXentF32Threads / 64;
+  constexpr float kL2e = 1.4426950408889634f;
+  __shared__ float red[NW];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const float* xr = logits + row * ld_in;
+  uint16_t* dr = dlogits + row * ld_out;
+  const int64_t lab = int64_t(labels[row]);
+  const bool lab_ok = lab >= 0 && lab < cols;
+  const float xlab = xr[lab_ok ? lab : 0];
+  const int64_t nfull = cols / 4;  // whole vectors; a partial one follows when cols % 4 != 0
+  const f32x4* xv = reinterpret_cast<const f32x4*>(xr);
+  f32x4 x[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t v = t + int64_t(i) * kXentF32Threads;
+    if (v < nfull) {
+      x[i] = ld_stream(&xv[v]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[i].v[j] = 4 * v + j < cols ? xr[4 * v + j] : -INFINITY;
+    }
+  }
+  auto block_reduce = [&](float val, bool is_max) __attribute__((always_inline)) {
+    val = is_max ? wave_max(val) : wave_sum(val);
+    if (lane == 0) red[wv] = val;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
+    __syncthreads();
+    return r;
+  };
+  float m = x[0].v[0];
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, x[i].v[j]);
+  const float M = block_reduce(m, true);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sum += __builtin_amdgcn_exp2f((x[i].v[j] - M) * kL2e);
+  const float S = block_reduce(sum, false);
+  const float lse = M + __logf(S);
+  const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
+  if (t == 0 && loss) loss[row] = lab_ok ? lse - xlab : lse;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t v = t + int64_t(i) * kXentF32Threads;
+    if (4 * v >= cols) continue;
+    float g[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float pr = __builtin_amdgcn_exp2f(fmaf(x[i].v[j] - M, kL2e, -ls2));
+      g[j] = (4 * v + j == lab ? pr - 1.f : pr) * grad_scale;
+    }
+    if (v < nfull) {
+      *reinterpret_cast<uint2*>(dr + 4 * v) = uint2{f32_to_bf16(g[0]) | (uint32_t(f32_to_bf16(g[1])) << 16),
+                                                    f32_to_bf16(g[2]) | (uint32_t(f32_to_bf16(g[3])) << 16)};
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * v + j < cols) dr[4 * v + j] = f32_to_bf16(g[j]);
     }
   }
 }
@@ -1284,103 +1363,135 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
   return n ? col_final(s, n, parts, outs, nb, cols) : MK_OK;
 }
 
-extern "C" int mk_softmax_xent_typed(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
-                                     const void* logits, int label_type, const void* labels, float grad_scale,
-                                     float* loss_rows, void* dlogits) {
-  if (logits_type == dlogits_type)
-    return mk_softmax_xent(stream, logits_type, rows, cols, logits, label_type, labels, grad_scale, loss_rows,
-                           dlogits);
+namespace {
+// The cross-entropy kernels for rows `ld_in` / `ld_out` elements apart.
+int xent_launch(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols, const void* logits,
+                int64_t ld_in, int label_type, const void* labels, float grad_scale, float* loss_rows, void* dlogits,
+                int64_t ld_out, const char* what) {
   clear_error();
-  if (logits_type != MK_F32 || dlogits_type != MK_BF16)
-    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: mixed types need f32 logits and bf16 dlogits");
-  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_softmax_xent_typed: bad shape");
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, std::string(what) + ": bad shape");
   if (rows == 0) return MK_OK;
-  if (rows >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: too many rows");
-  if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent_typed: null pointer");
+  if (rows >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, std::string(what) + ": too many rows");
+  if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, std::string(what) + ": null pointer");
+  if (ld_in < cols || ld_out < cols) return fail(MK_ERR_INVALID, std::string(what) + ": row pitch below cols");
   if (label_type != MK_S32 && label_type != MK_S64)
-    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: labels must be s32/s64");
+    return fail(MK_ERR_UNSUPPORTED, std::string(what) + ": labels must be s32/s64");
+  const bool s32 = label_type == MK_S32;
   hipStream_t s = as_stream(stream);
-  const int64_t npt = (cols + kXentF32Threads - 1) / kXentF32Threads;
-  auto launch = [&](auto nt) {
-    constexpr int NPT = decltype(nt)::value;
-    if (label_type == MK_S32)
-      hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int32_t>), dim3(unsigned(rows)), dim3(kXentF32Threads), 0,
-                         s, (const float*)logits, cols, (const int32_t*)labels, grad_scale, loss_rows,
-                         (uint16_t*)dlogits);
+  const dim3 g{unsigned(rows)};
+  if (logits_type == MK_F32 && dlogits_type == MK_BF16) {
+    // rows 16-byte aligned: the vector kernel; otherwise one element per load
+    const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && ld_in % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(dlogits) & 7u) == 0 && ld_out % 4 == 0;
+    const int64_t nvt = ((cols + 3) / 4 + kXentF32Threads - 1) / kXentF32Threads;  // vectors per thread
+    auto vlaunch = [&](auto nt) {
+      constexpr int NV = decltype(nt)::value;
+      if (s32)
+        hipLaunchKernelGGL((softmax_xent_f32_bf16_vec_kernel<NV, int32_t>), g, dim3(kXentF32Threads), 0, s,
+                           (const float*)logits, cols, ld_in, (const int32_t*)labels, grad_scale, loss_rows,
+                           (uint16_t*)dlogits, ld_out);
+      else
+        hipLaunchKernelGGL((softmax_xent_f32_bf16_vec_kernel<NV, int64_t>), g, dim3(kXentF32Threads), 0, s,
+                           (const float*)logits, cols, ld_in, (const int64_t*)labels, grad_scale, loss_rows,
+                           (uint16_t*)dlogits, ld_out);
+    };
+    const int64_t npt = (cols + kXentF32Threads - 1) / kXentF32Threads;
+    auto launch = [&](auto nt) {
+      constexpr int NPT = decltype(nt)::value;
+      if (s32)
+        hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int32_t>), g, dim3(kXentF32Threads), 0, s,
+                           (const float*)logits, cols, ld_in, (const int32_t*)labels, grad_scale, loss_rows,
+                           (uint16_t*)dlogits, ld_out);
+      else
+        hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int64_t>), g, dim3(kXentF32Threads), 0, s,
+                           (const float*)logits, cols, ld_in, (const int64_t*)labels, grad_scale, loss_rows,
+                           (uint16_t*)dlogits, ld_out);
+    };
+    if (vec && nvt <= 4) vlaunch(IntC<4>{});
+    else if (vec && nvt <= 8) vlaunch(IntC<8>{});
+    else if (vec && nvt <= 12) vlaunch(IntC<12>{});
+    else if (vec && nvt <= 16) vlaunch(IntC<16>{});
+    else if (npt <= 8) launch(IntC<8>{});
+    else if (npt <= 16) launch(IntC<16>{});
+    else if (npt <= 24) launch(IntC<24>{});
+    else if (s32)
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int32_t>), g, dim3(kXentF32Threads), 0, s,
+                         (const float*)logits, cols, ld_in, (const int32_t*)labels, grad_scale, loss_rows,
+                         (uint16_t*)dlogits, ld_out);
     else
-      hipLaunchKernelGGL((softmax_xent_f32_bf16_kernel<NPT, int64_t>), dim3(unsigned(rows)), dim3(kXentF32Threads), 0,
-                         s, (const float*)logits, cols, (const int64_t*)labels, grad_scale, loss_rows,
-                         (uint16_t*)dlogits);
-  };
-  if (npt <= 8) {
-    launch(IntC<8>{});
-  } else if (npt <= 16) {
-    launch(IntC<16>{});
-  } else if (npt <= 24) {
-    launch(IntC<24>{});
-  } else {
-    if (label_type == MK_S32)
-      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int32_t>), dim3(unsigned(rows)),
-                         dim3(kXentF32Threads), 0, s, (const float*)logits, cols, (const int32_t*)labels, grad_scale,
-                         loss_rows, (uint16_t*)dlogits);
-    else
-      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int64_t>), dim3(unsigned(rows)),
-                         dim3(kXentF32Threads), 0, s, (const float*)logits, cols, (const int64_t*)labels, grad_scale,
-                         loss_rows, (uint16_t*)dlogits);
+      hipLaunchKernelGGL((softmax_xent_f32_bf16_stream_kernel<16, int64_t>), g, dim3(kXentF32Threads), 0, s,
+                         (const float*)logits, cols, ld_in, (const int64_t*)labels, grad_scale, loss_rows,
+                         (uint16_t*)dlogits, ld_out);
+    return check_launch(what);
   }
-  return check_launch("mk_softmax_xent_typed");
-}
-
-extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,
-                               int label_type, const void* labels, float grad_scale, float* loss_rows,
-                               void* dlogits) {
-  clear_error();
-  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_softmax_xent: bad shape");
-  if (rows == 0) return MK_OK;
-  if (rows >= (int64_t(1) << 31)) return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: too many rows");
-  if (!logits || !labels || !dlogits) return fail(MK_ERR_INVALID, "mk_softmax_xent: null pointer");
-  hipStream_t s = as_stream(stream);
-  const dim3 g{unsigned(rows)}, b{unsigned(kBlock)};
+  if (logits_type != dlogits_type || (logits_type != MK_BF16 && logits_type != MK_F32))
+    return fail(MK_ERR_UNSUPPORTED, std::string(what) + ": logits / dlogits types must be bf16/bf16, f32/f32 or f32/bf16");
   // bf16 rows of up to 64K columns: the register-resident kernel.  It takes
   // the unaligned head of a row from the logits' 16-byte phase and stores
-  // dlogits with 16-byte vectors at the same offsets, so both must share
-  // that phase; otherwise the element-wise kernel below runs.
+  // dlogits with 16-byte vectors at the same offsets, so every row of both
+  // must share that phase; otherwise the element-wise kernel below runs.
   const bool same_phase =
-      ((reinterpret_cast<uintptr_t>(logits) ^ reinterpret_cast<uintptr_t>(dlogits)) & 15u) == 0;
-  if (io_type == MK_BF16 && same_phase && cols <= int64_t(kXentThreads) * 8 * 16) {
+      ((reinterpret_cast<uintptr_t>(logits) ^ reinterpret_cast<uintptr_t>(dlogits)) & 15u) == 0 &&
+      (ld_in - ld_out) % 8 == 0;
+  if (logits_type == MK_BF16 && same_phase && cols <= int64_t(kXentThreads) * 8 * 16) {
     const int64_t nvt = (cols / 8 + kXentThreads - 1) / kXentThreads;  // vectors per thread (bound)
     auto launch = [&](auto nt, auto ltag) {
       constexpr int NVT = decltype(nt)::value;
       using L = decltype(ltag);
       hipLaunchKernelGGL((softmax_xent_bf16_kernel<NVT, L>), g, dim3(kXentThreads), 0, s, (const uint16_t*)logits,
-                         cols, (const L*)labels, grad_scale, loss_rows, (uint16_t*)dlogits);
+                         cols, ld_in, (const L*)labels, grad_scale, loss_rows, (uint16_t*)dlogits, ld_out);
     };
     auto with_labels = [&](auto nt) {
-      if (label_type == MK_S32) launch(nt, int32_t{});
-      else if (label_type == MK_S64) launch(nt, int64_t{});
+      if (s32) launch(nt, int32_t{});
+      else launch(nt, int64_t{});
     };
-    if (label_type != MK_S32 && label_type != MK_S64)
-      return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: labels must be s32/s64");
     if (nvt <= 4) with_labels(IntC<4>{});
     else if (nvt <= 8) with_labels(IntC<8>{});
     else with_labels(IntC<16>{});
-    return check_launch("mk_softmax_xent");
+    return check_launch(what);
   }
   auto go = [&](auto tag) {
     using T = decltype(tag);
-    if (label_type == MK_S32)
-      hipLaunchKernelGGL((softmax_xent_kernel<T, int32_t>), g, b, 0, s, (const T*)logits, cols,
-                         (const int32_t*)labels, grad_scale, loss_rows, (T*)dlogits);
+    if (s32)
+      hipLaunchKernelGGL((softmax_xent_kernel<T, int32_t>), g, dim3(kBlock), 0, s, (const T*)logits, cols, ld_in,
+                         (const int32_t*)labels, grad_scale, loss_rows, (T*)dlogits, ld_out);
     else
-      hipLaunchKernelGGL((softmax_xent_kernel<T, int64_t>), g, b, 0, s, (const T*)logits, cols,
-                         (const int64_t*)labels, grad_scale, loss_rows, (T*)dlogits);
+      hipLaunchKernelGGL((softmax_xent_kernel<T, int64_t>), g, dim3(kBlock), 0, s, (const T*)logits, cols, ld_in,
+                         (const int64_t*)labels, grad_scale, loss_rows, (T*)dlogits, ld_out);
   };
-  if (label_type != MK_S32 && label_type != MK_S64)
-    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: labels must be s32/s64");
-  if (io_type == MK_BF16) go(uint16_t{});
-  else if (io_type == MK_F32) go(float{});
-  else return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: io_type must be bf16/f32");
-  return check_launch("mk_softmax_xent");
+  if (logits_type == MK_BF16) go(uint16_t{});
+  else go(float{});
+  return check_launch(what);
+}
+}  // namespace
+
+extern "C" int mk_softmax_xent_strided(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
+                                       const void* logits, int64_t ld_logits, int label_type, const void* labels,
+                                       float grad_scale, float* loss_rows, void* dlogits, int64_t ld_dlogits) {
+  return xent_launch(stream, logits_type, dlogits_type, rows, cols, logits, ld_logits, label_type, labels, grad_scale,
+                     loss_rows, dlogits, ld_dlogits, "mk_softmax_xent_strided");
+}
+
+extern "C" int mk_softmax_xent_typed(void* stream, int logits_type, int dlogits_type, int64_t rows, int64_t cols,
+                                     const void* logits, int label_type, const void* labels, float grad_scale,
+                                     float* loss_rows, void* dlogits) {
+  if (logits_type != dlogits_type && (logits_type != MK_F32 || dlogits_type != MK_BF16)) {
+    clear_error();
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent_typed: mixed types need f32 logits and bf16 dlogits");
+  }
+  return xent_launch(stream, logits_type, dlogits_type, rows, cols, logits, cols, label_type, labels, grad_scale,
+                     loss_rows, dlogits, cols, "mk_softmax_xent_typed");
+}
+
+extern "C" int mk_softmax_xent(void* stream, int io_type, int64_t rows, int64_t cols, const void* logits,
+                               int label_type, const void* labels, float grad_scale, float* loss_rows,
+                               void* dlogits) {
+  if (io_type != MK_BF16 && io_type != MK_F32) {
+    clear_error();
+    return fail(MK_ERR_UNSUPPORTED, "mk_softmax_xent: io_type must be bf16/f32");
+  }
+  return xent_launch(stream, io_type, io_type, rows, cols, logits, cols, label_type, labels, grad_scale, loss_rows,
+                     dlogits, cols, "mk_softmax_xent");
 }
 
 namespace {

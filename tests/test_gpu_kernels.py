@@ -639,6 +639,86 @@ def test_gemm_tiled_f32_out_unaligned_rows(K):
         assert np.all(got[:, N:] == -7.0)
 
 
+def _nan_padded(x, pad_cols, transposed):
+    """bf16 device view of x ([rows, cols]) whose storage rows are padded with
+    NaN to a multiple of 8 columns (+ pad_cols); transposed: the storage holds
+    x.T padded the same way and the view is its transpose."""
+    src = np.ascontiguousarray(x.T) if transposed else x
+    r, c = src.shape
+    cp = (c + 7) // 8 * 8 + pad_cols
+    buf = torch.full((r, cp), float("nan"), dtype=torch.bfloat16, device="cuda")
+    buf[:, :c] = dev_bf16(bf16.to_bf16_bits(src))
+    v = buf[:, :c]
+    return v.t() if transposed else v
+
+
+def test_gemm_tiled_ragged_k_and_rows(K):
+    """The tiled kernel on extents that are not multiples of 8, with NaN in
+    every storage element past them: a k-contiguous operand whose K % 8 != 0
+    (the chunk straddling K is cleared past K in LDS), an m- or n-contiguous
+    operand whose M or N % 8 != 0 (the straddling chunk only reaches C rows or
+    columns that are never stored), and both at once.  No NaN may leak; fp32
+    out within 1e-5 of the float64 product scaled by the product of
+    magnitudes, bf16 out within one ulp of it rounded once; repeat calls are
+    bit-identical."""
+    rng = np.random.default_rng(31)
+    # (M, N, K, A stored transposed (m-contiguous), B stored transposed (k-contiguous))
+    cases = [(264, 392, 203, False, True), (261, 384, 136, True, True), (264, 389, 200, False, False),
+             (517, 389, 197, True, False), (300, 260, 1001, False, True), (256, 256, 67, False, True)]
+    for (M, N, Kd, ta, tb) in cases:
+        print(f"case: tiled gemm ragged M={M} N={N} K={Kd} ta={ta} tb={tb}", flush=True)
+        a = bf16.round_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+        b = bf16.round_bf16(rng.standard_normal((Kd, N)).astype(np.float32))
+        at = _nan_padded(a, 8, ta)
+        bt = _nan_padded(b, 8, tb)
+        want = a.astype(np.float64) @ b
+        norm = np.abs(a).astype(np.float64) @ np.abs(b)
+        got_t = K.gemm(at, bt, out_dtype=torch.float32)
+        got = got_t.cpu().numpy()
+        assert np.isfinite(got).all(), (M, N, Kd)
+        assert np.max(np.abs(got - want) / (norm + 1e-30)) < 1e-5, (M, N, Kd)
+        assert torch.equal(got_t, K.gemm(at, bt, out_dtype=torch.float32))
+        gb = host_bf16(K.gemm(at, bt, out_dtype=torch.bfloat16))
+        assert _bf16_out_ok(gb, want, norm), (M, N, Kd)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_splitk_uneven_slices(K, out_dtype):
+    """Split-K whose K the slice count does not divide (mk_gemm_splitk_typed:
+    slices a multiple of 8 apart, a shorter last one, K % 8 != 0 cleared in
+    the last slice), in the two vocabulary-product forms: a k-contiguous A
+    with NaN past K against a row-major B (dX = dlogits W), and an
+    m-contiguous A (dW = dlogitsᵀ X).  fp32 / bf16 out against the float64
+    product; bit-identical on repeat and to the same call with the slices'
+    results summed in order on the host."""
+    rng = np.random.default_rng(32)
+    for (M, N, Kd, ta, splits) in [(256, 768, 4099, False, 4), (264, 384, 1003, True, 3), (384, 256, 2050, False, 8)]:
+        print(f"case: splitk uneven M={M} N={N} K={Kd} ta={ta} splits={splits} out={out_dtype}", flush=True)
+        a = bf16.round_bf16(rng.standard_normal((M, Kd)).astype(np.float32))
+        b = bf16.round_bf16(rng.standard_normal((Kd, N)).astype(np.float32))
+        at = _nan_padded(a, 8, ta)
+        bt = dev_bf16(bf16.to_bf16_bits(b))
+        want = a.astype(np.float64) @ b
+        norm = np.abs(a).astype(np.float64) @ np.abs(b)
+        got_t = K.gemm_splitk(at, bt, splits, out_dtype=out_dtype)
+        assert torch.equal(got_t, K.gemm_splitk(at, bt, splits, out_dtype=out_dtype))
+        if out_dtype == torch.float32:
+            got = got_t.cpu().numpy()
+            assert np.isfinite(got).all()
+            assert np.max(np.abs(got - want) / (norm + 1e-30)) < 2e-5, (M, N, Kd)
+            # the slices' own products (fp32, tiled kernel) summed in slice order
+            ks = ((Kd + splits - 1) // splits + 7) // 8 * 8
+            acc = None
+            for si in range(splits):
+                k0, k1 = si * ks, min(Kd, (si + 1) * ks)
+                part = K.gemm(at[:, k0:k1], bt[k0:k1, :], out_dtype=torch.float32)
+                acc = part if acc is None else acc + part
+            assert torch.equal(got_t, acc)
+        else:
+            gb = host_bf16(got_t)
+            assert _bf16_out_ok(gb, want, norm), (M, N, Kd)
+
+
 # ------------------------------------------------------------------ a6 iota, a12 layout, misc
 def test_iota_convert_fill_copy(K):
     it = K.iota((3, 5, 7), 1).cpu().numpy()

@@ -407,6 +407,71 @@ def test_softmax_xent_f32_logits_bf16_dlogits(K, rows, cols):
     assert np.all(np.abs(got - want) <= ulp + 1e-7 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("cols,ld_in,ld_out", [(50257, 50260, 50264), (50257, 50264, 50264), (4096, 4100, 4104),
+                                              (4099, 4104, 4104), (70001, 70004, 70008)])
+def test_softmax_xent_strided_f32_logits_bf16_dlogits(K, cols, ld_in, ld_out):
+    """Padded row pitches (mk_softmax_xent_strided): fp32 logits rows ld_in
+    apart with NaN in the padding (never read), bf16 dlogits rows ld_out
+    apart whose padding must stay untouched; 16-byte aligned rows take the
+    vector kernel (a partial last vector when cols % 4 != 0), 70001 columns
+    the streaming kernel.  Loss to 1e-5 of float64, gradient within one bf16
+    ulp, out-of-range labels -1 and cols."""
+    rows = 6
+    print(f"case: xent strided cols={cols} ld_in={ld_in} ld_out={ld_out}", flush=True)
+    g = torch.Generator().manual_seed(cols + ld_in)
+    x = torch.randn(rows, cols, generator=g) * 3
+    x[1, 2] = float("-inf")
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int32)
+    lab[-1] = cols
+    lab[0] = -1
+    lab[2] = cols - 1
+    xbuf = torch.full((rows, ld_in), float("nan"), dtype=torch.float32, device="cuda")
+    xbuf[:, :cols] = x.cuda()
+    dbuf = torch.full((rows, ld_out), -7.0, dtype=torch.bfloat16, device="cuda")
+    loss, dl = K.softmax_xent(xbuf[:, :cols], lab.cuda(), 1.0 / rows, dlogits=dbuf[:, :cols])
+    xr = x.double()
+    lse = torch.logsumexp(xr, -1)
+    ok = (lab >= 0) & (lab < cols)
+    want_loss = lse - torch.where(ok, xr[torch.arange(rows), lab.clamp(0, cols - 1).long()], 0.0)
+    np.testing.assert_allclose(_f64(loss), want_loss, rtol=1e-5, atol=1e-5)
+    p = torch.softmax(xr, -1)
+    onehot = torch.zeros_like(p)
+    onehot[torch.arange(rows)[ok], lab[ok].long()] = 1.0
+    want = ((p - onehot) / rows).numpy()
+    got = bf16.from_bf16_bits(dbuf[:, :cols].cpu().view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+    assert np.all(np.abs(got - want) <= ulp + 1e-7 * np.abs(want).max())
+    assert bool((dbuf[:, cols:].float() == -7.0).all())
+    if cols % 4 == 0:
+        # packed rows of a multiple of 4 columns take the same vector kernel:
+        # the same bits (other widths run the element-wise kernels, whose
+        # sums of exponentials are ordered differently)
+        dl2 = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")
+        loss2, dl2 = K.softmax_xent(x.cuda(), lab.cuda(), 1.0 / rows, dlogits=dl2)
+        assert torch.equal(loss2, loss)
+        assert torch.equal(dl2, dbuf[:, :cols])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_softmax_xent_strided_same_type_in_place(K, dtype):
+    """bf16 (register-resident kernel) and fp32 logits with a padded row pitch,
+    the gradient written in place over them: same bits as the packed rows,
+    padding untouched."""
+    rows, cols, ld = 5, 50257, 50264
+    g = torch.Generator().manual_seed(17)
+    x = (torch.randn(rows, cols, generator=g) * 3).to(dtype)
+    lab = torch.randint(0, cols, (rows,), generator=g, dtype=torch.int64)
+    buf = torch.full((rows, ld), -7.0, dtype=dtype, device="cuda")
+    buf[:, :cols] = x.cuda()
+    v = buf[:, :cols]
+    loss, dl = K.softmax_xent(v, lab.cuda(), 1.0 / rows, dlogits=v)
+    xd = x.cuda()
+    loss2, dl2 = K.softmax_xent(xd, lab.cuda(), 1.0 / rows, dlogits=xd)
+    assert torch.equal(loss, loss2)
+    assert torch.equal(buf[:, :cols], dl2)
+    assert bool((buf[:, cols:].float() == -7.0).all())
+
+
 def test_softmax_xent_bf16_dlogits_offset_view(K):
     """dlogits in a different 16-byte phase from logits (an offset view):
     the launcher must not use the register-resident kernel's vector stores,
