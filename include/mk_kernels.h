@@ -88,8 +88,9 @@ int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, c
  * the tiled kernel takes (16-byte aligned rows), any K: when K % splits != 0
  * the slices are ceil(K / splits) rounded up to a multiple of 8 apart and the
  * last one is shorter (the vocabulary products of the training step, which
- * contract over 50257 tokens' classes).  Same workspace size and rules as
- * mk_gemm_splitk otherwise (bf16 C: 8-byte aligned).
+ * contract over 50257 classes).  A product with K % splits != 0 that the
+ * tiled kernel does not take runs unsplit (mk_gemm).  Same workspace size
+ * and rules as mk_gemm_splitk otherwise (bf16 C: 8-byte aligned).
  * Replaces, for these products: src/jam/ops/linalg.mm:98. */
 int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K, const void* A,
                          int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* C,

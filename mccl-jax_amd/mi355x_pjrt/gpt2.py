@@ -25,12 +25,15 @@ operation is a call through the C-ABI of include/mk_kernels.h:
 
 The per-layer GEMMs run on the hand-written MFMA GEMM (mk_gemm; the QKV bias
 in its epilogue, the other biases in the elementwise pass that follows) and
-the weight gradients on its split-K form (mk_gemm_splitk).  The three GEMMs
-over the vocabulary (logits, and the two gradients through the tied
-embedding) stay on rocBLAS (mk_gemm_blas): their rows are 50257 elements, so
-operand rows are not 16-byte aligned and the tiled kernel's direct 16-byte
-HBM->LDS copies do not apply.  Every other operation is a hand-written
-kernel.  All parameters live in five flat buffers (fp32 master, bf16 working copy,
+the weight gradients on its split-K form (mk_gemm_splitk).  The logits and
+their gradient live in one bf16 buffer whose rows are padded from 50257 to
+50264 elements (16-byte multiples), so the two gradient products through the
+tied embedding take aligned operand rows on the hand-written kernels: the
+embedding gradient on mk_gemm, the hidden-state gradient (a contraction over
+the 50257 classes into a 8192 x 768 result) on mk_gemm_splitk_typed, 8
+slices.  The logits product itself (K = 768 into 8192 x 50257) stays on
+rocBLAS (mk_gemm_blas), which runs it 10-25% faster than the tiled kernel.
+Every other operation is a hand-written kernel.  All parameters live in five flat buffers (fp32 master, bf16 working copy,
 fp32 gradient, fp32 m, fp32 v), each parameter a 64-element-aligned slice, so
 the optimizer is a single launch and every gradient is written in place.  The
 step is prepared once as a list of bound calls (device pointers and shapes
@@ -143,7 +146,12 @@ class GPT2TrainStep:
     # slices; TFLOP/s dw_o 102/179/281/294/260, dw_qkv 304/493/596/462/315,
     # dw_fc and dw_pr 415/593/621/514/367).
     DW_SPLITS = {"dw_o": 8, "dw_qkv": 4, "dw_fc": 4, "dw_pr": 4}
-    VOCAB_GEMMS = ("logits", "dhf", "dwte")
+    # the hidden-state gradient through the embedding (K = vocabulary): bf16
+    # out, split along K in uneven slices (measured: 8 slices 664 us, 2 693,
+    # unsplit 910; rocBLAS 682-687)
+    DHF_SPLITS = 8
+    # products on the library GEMM (measured faster there; see the module doc)
+    BLAS_GEMMS = ("logits",)
 
     def __init__(self, cfg: GPT2Config, params: dict | None = None, seed: int = 0, lr: float = 3e-4,
                  b1: float = 0.9, b2: float = 0.999, adam_eps: float = 1e-8, device="cuda", stream=None):
@@ -215,7 +223,10 @@ class GPT2TrainStep:
         self.f = [torch.empty(T, c.d_ff, **bf) for _ in range(L)]
         self.g = [torch.empty(T, c.d_ff, **bf) for _ in range(L)]
         self.hf = torch.empty(T, d, **bf)
-        self.logits = torch.empty(T, c.vocab, **bf)
+        # logits, then their gradient in place, rows padded to a 16-byte
+        # multiple (the padding is never written)
+        self.vocab_pitch = (c.vocab + 7) // 8 * 8
+        self.logits = torch.zeros(T, self.vocab_pitch, **bf)
         self.tmp = torch.empty(T, d, **bf)
         self.dx = torch.empty(T, d, **bf)
         self.dh = torch.empty(T, d, **bf)
@@ -228,6 +239,7 @@ class GPT2TrainStep:
         sk = [lib.mk_gemm_splitk_workspace_bytes(d, n, self.DW_SPLITS.get(t, 1))
               for t, n in (("dw_o", d), ("dw_qkv", 3 * d), ("dw_fc", c.d_ff))]
         sk.append(lib.mk_gemm_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS.get("dw_pr", 1)))
+        sk.append(lib.mk_gemm_splitk_workspace_bytes(T, d, self.DHF_SPLITS))
         ws = max(*sk, lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
                  lib.mk_layernorm_bwd_workspace_bytes(T, d),
                  lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),
@@ -262,11 +274,17 @@ class GPT2TrainStep:
                                                         _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr, _I64(c_ms),
                                                         _I64(sp), ws], "mk_gemm_splitk " + tag))
                 return
-            if tag in self.VOCAB_GEMMS:
+            if tag in self.BLAS_GEMMS:
                 calls.append(_Call(lib.mk_gemm_blas, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
                                                       a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
                                                       _I64(b_ns), cptr, _I64(0), _I64(c_ms), _F(1.0), _F(0.0)],
                                    "mk_gemm_blas " + tag))
+                return
+            if tag == "dhf":
+                calls.append(_Call(lib.mk_gemm_splitk_typed, [st, _I(ab), _I(ct), _I64(M), _I64(N), _I64(Kd), a,
+                                                              _I64(a_ms), _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr,
+                                                              _I64(c_ms), _I64(self.DHF_SPLITS), ws],
+                                   "mk_gemm_splitk_typed " + tag))
                 return
             calls.append(_Call(lib.mk_gemm, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),
                                              a, _I64(0), _I64(a_ms), _I64(a_ks), b, _I64(0), _I64(b_ks),
@@ -326,16 +344,18 @@ class GPT2TrainStep:
             nxt, y = (f"h{l + 1}.ln1", P(self.h1[l + 1])) if l + 1 < L else ("lnf", P(self.hf))
             add_layernorm(P(self.xm[l]), P(self.tmp), W(p + "b_pr"), nxt, P(self.x[l + 1]), y)
         # logits = hf @ wteᵀ, then loss rows and dlogits (over the logits)
-        gemm(BF16, BF16, T, V, d, P(self.hf), d, 1, W("wte"), 1, d, P(self.logits), V, tag="logits")
-        calls.append(_Call(lib.mk_softmax_xent, [st, _I(BF16), _I64(T), _I64(V), P(self.logits), _I(S32),
-                                                 P(self.labels), _F(1.0 / T), P(self.loss_rows), P(self.logits)],
-                           "mk_softmax_xent"))
+        Vp = self.vocab_pitch
+        gemm(BF16, BF16, T, V, d, P(self.hf), d, 1, W("wte"), 1, d, P(self.logits), Vp, tag="logits")
+        calls.append(_Call(lib.mk_softmax_xent_strided, [st, _I(BF16), _I(BF16), _I64(T), _I64(V), P(self.logits),
+                                                         _I64(Vp), _I(S32), P(self.labels), _F(1.0 / T),
+                                                         P(self.loss_rows), P(self.logits), _I64(Vp)],
+                           "mk_softmax_xent_strided"))
         calls.append(_Call(lib.mk_row_reduce, [st, _I(F32), _I(F32), _I(0), _I64(1), _I64(T), P(self.loss_rows),
                                                _F(0.0), P(self.loss_sum)], "mk_row_reduce"))
         # ---- backward
         dlog = P(self.logits)
-        gemm(BF16, BF16, T, d, V, dlog, V, 1, W("wte"), d, 1, P(self.dh), d, tag="dhf")
-        gemm(BF16, F32, V, d, T, dlog, 1, V, P(self.hf), d, 1, G("wte"), d, tag="dwte")
+        gemm(BF16, BF16, T, d, V, dlog, Vp, 1, W("wte"), d, 1, P(self.dh), d, tag="dhf")
+        gemm(BF16, F32, V, d, T, dlog, 1, Vp, P(self.hf), d, 1, G("wte"), d, tag="dwte")
         # the bias gradient of each residual projection is the column sum of
         # the residual-stream gradient, produced by the LayerNorm backward
         # that writes it

@@ -1880,6 +1880,27 @@ class Lowerer {
     fused_[anchor] = f;
     for (int o : ops)
       if (o != anchor) absorbed_.insert(o);
+    // rows padded to 8 elements (16 bytes of bf16, 32 of f32): the logits
+    // when a product writes them (through reshapes: its result's last dim is
+    // the vocabulary), and the gradient the kernel writes
+    if (V % 8 != 0) {
+      const int64_t pitch = (V + 7) / 8 * 8;
+      auto not_output = [&](int v) { return std::count(outputs_.begin(), outputs_.end(), v) == 0; };
+      int src = X;
+      while (is(src, "stablehlo.reshape") && m_.types[prod(src)->operands[0]].dims.back() == V)
+        src = prod(src)->operands[0];
+      if ((is(src, "stablehlo.dot_general") || is(src, "stablehlo.dot")) && not_output(src) &&
+          m_.types[src].dims.back() == V)
+        pad_rows_[src] = pitch;
+      if (f.dlogits_bf16.empty()) {
+        if (not_output(dX)) pad_rows_[dX] = pitch;
+      } else {
+        bool ok = true;
+        for (int c : f.dlogits_bf16) ok = ok && not_output(c);
+        if (ok)
+          for (int c : f.dlogits_bf16) pad_rows_[c] = pitch;
+      }
+    }
     prog_->patterns.push_back("softmax_xent(" + std::to_string(T) + "x" + std::to_string(V) + ", grad_scale=" +
                               std::to_string(gscale) + ")");
   }
@@ -2284,6 +2305,26 @@ class Lowerer {
         return BufRef{Space::kOutput, int(k), 0};
       }
     return NewTemp(m_.types[v].bytes());
+  }
+  // rows of value v (its last dim) `pitch` elements apart in `where`
+  void SetPaddedView(int v, BufRef where, int64_t pitch) {
+    SetDenseView(v, where);
+    ValState& s = state_[v];
+    const int r = s.view.rank();
+    int64_t e = 1;
+    for (int d = r - 1; d >= 0; --d) {
+      s.view.strides[d] = e;
+      e *= d == r - 1 ? pitch : s.view.dims[d];
+    }
+  }
+  // a temp for value v with its rows padded to pad_rows_[v] (0: not padded)
+  int64_t PaddedPitch(int v) const {
+    const auto it = pad_rows_.find(v);
+    return it == pad_rows_.end() ? 0 : it->second;
+  }
+  BufRef NewPaddedTemp(int v, int64_t pitch) {
+    const TensorType& t = m_.types[v];
+    return NewTemp(size_t(t.numel() / t.dims.back() * pitch) * DTypeBytes(t.dtype));
   }
   void SetDenseView(int v, BufRef where) {
     ValState& s = state_[v];
@@ -3420,7 +3461,14 @@ class Lowerer {
     if (N == 1) b_ns = b_ks == 1 ? K : 1;
     if (B == 1) a_bs = b_bs = 0;
     const DType ct = m_.types[res].dtype;
-    BufRef d = DestFor(res);
+    // a padded destination (rows c_pitch apart) when the result's last dim is N
+    const int64_t pad = (B == 1 && !epi && m_.types[res].dims.back() == N) ? PaddedPitch(res) : 0;
+    const int64_t c_pitch = pad > 0 ? pad : N;
+    BufRef d = pad > 0 ? NewPaddedTemp(res, pad) : DestFor(res);
+    auto set_result = [&](BufRef where) {
+      if (pad > 0) SetPaddedView(res, where, pad);
+      else SetDenseView(res, where);
+    };
     Step st;
     st.kind = StepKind::kGemm;
     // bf16 operands whose rows are not 16-byte aligned (a vocabulary of
@@ -3449,26 +3497,30 @@ class Lowerer {
         (K >= 2 * std::max(M, N) || f32_underfill)) {
       const int64_t tiles = tiles128;
       int64_t splits = 1;
+      // bf16 operands: K need not divide evenly (mk_gemm_splitk's uneven
+      // slices, a contraction over a vocabulary of 50257)
+      const bool any_k = at == DType::kBF16;
       if (f32_underfill)
         while (splits < 16 && tiles * splits < 256 && K % (2 * splits) == 0 && K / (2 * splits) >= 128) splits *= 2;
       else
-        while (splits < 8 && tiles * splits < 400 && K % (2 * splits) == 0 && K / (2 * splits) >= 256) splits *= 2;
+        while (splits < 8 && tiles * splits < 400 && (any_k || K % (2 * splits) == 0) && K / (2 * splits) >= 256)
+          splits *= 2;
       if (splits > 1) {
         st.kind = StepKind::kGemmSplitK;
         st.bufs = {lv.at(), rv.at(), d, NewTemp(mk_gemm_splitk_workspace_bytes(M, N, splits))};
-        st.i = {int64_t(at), M, N, K, a_ms, a_ks, b_ks, b_ns, N, splits};
+        st.i = {int64_t(at), M, N, K, a_ms, a_ks, b_ks, b_ns, c_pitch, splits};
         st.note = std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " in " +
                   std::to_string(splits) + " slices";
         Emit(st);
         if (epi) EmitBiasEpilogue(d, M, N, *epi);
-        SetDenseView(res, d);
+        set_result(d);
         return;
       }
     }
     // an f32 product every reader rounds to bf16 is written in bf16 (one
     // rounding of the fp32 accumulator, as the module's convert does)
     bool narrow_out = false;
-    if (!epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res, false)) {
+    if (pad == 0 && !epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res, false)) {
       narrow_out = true;
       d = NewTemp(size_t(m_.types[res].numel()) * 2);
     }
@@ -3480,7 +3532,7 @@ class Lowerer {
       epilogue = epi->relu ? 2 : 1;
     }
     st.i = {int64_t(at), int64_t(narrow_out ? DType::kBF16 : ct), B, M, N, K, a_bs, a_ms, a_ks, b_bs, b_ks, b_ns,
-            M * N, N, epilogue};
+            M * N, c_pitch, epilogue};
     st.note = std::to_string(B) + "x" + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
     if (narrow_out) st.note += " -> bf16";
     Emit(st);
@@ -3493,7 +3545,7 @@ class Lowerer {
       narrow_[res] = nv;
       return;
     }
-    SetDenseView(res, d);
+    set_result(d);
   }
 
   void LowerGather(int idx) {
@@ -3753,26 +3805,34 @@ class Lowerer {
       return;
     }
     if (f.kind == Fused::kXent) {
+      // logits rows may be padded (row stride >= cols, unit stride along them)
       View x = NeedView(f.x);
-      if (!x.dense()) x = Densify(x);
+      if (!(x.rank() == 2 && x.strides[1] == 1 && x.strides[0] >= x.dims[1])) x = Densify(x);
       View lab = NeedView(f.labels);
       if (!lab.dense()) lab = Densify(lab);
       const int res = op.results[0];
       BufRef lr = DestFor(res);
       const bool to_bf16 = !f.dlogits_bf16.empty();
-      BufRef dx = DestFor(to_bf16 ? f.dlogits_bf16[0] : f.dlogits);
+      const int dv = to_bf16 ? f.dlogits_bf16[0] : f.dlogits;
+      const int64_t dpad = PaddedPitch(dv);
+      BufRef dx = dpad > 0 ? NewPaddedTemp(dv, dpad) : DestFor(dv);
       Step st;
       st.kind = StepKind::kSoftmaxXent;
       st.bufs = {x.at(), lab.at(), lr, dx};
       st.i = {int64_t(x.dtype), x.dims[0], x.dims[1], int64_t(lab.dtype),
-              int64_t(to_bf16 ? DType::kBF16 : x.dtype)};
+              int64_t(to_bf16 ? DType::kBF16 : x.dtype), x.strides[0], dpad > 0 ? dpad : x.dims[1]};
       st.f = {f.scale};
+      if (x.strides[0] != x.dims[1] || dpad > 0) st.note = "rows padded";
       Emit(st);
       SetDenseView(res, lr);
+      auto set_dx = [&](int v) {
+        if (dpad > 0) SetPaddedView(v, dx, dpad);
+        else SetDenseView(v, dx);
+      };
       if (to_bf16) {
-        for (int c : f.dlogits_bf16) SetDenseView(c, dx);
+        for (int c : f.dlogits_bf16) set_dx(c);
       } else {
-        SetDenseView(f.dlogits, dx);
+        set_dx(f.dlogits);
       }
       return;
     }
@@ -3936,6 +3996,11 @@ class Lowerer {
   std::vector<ValState> state_;
   std::map<int, Fused> fused_;
   std::set<int> absorbed_;
+  // values stored with their rows (last dim) padded to this pitch (elements):
+  // the logits and the gradient of a fused cross-entropy over a vocabulary
+  // whose rows are not 16-byte multiples, so that the products that write
+  // and read them take aligned rows
+  std::map<int, int64_t> pad_rows_;
   std::vector<bool> reach_;
   std::map<int, std::pair<View, BufRef>> sdpa_saved_;  // training forward anchor -> (bf16 O view, lse)
   std::unordered_map<int, View> narrow_;   // f32 value -> bf16 view of the same values

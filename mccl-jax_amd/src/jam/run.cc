@@ -73,8 +73,8 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   iota     bufs out           i out_type,rank,dim,dims...
 //   copy_strided bufs in,out    i elem_bytes,rank,dims...  strides
 //   softmax  bufs x,y           i io_type,rows,cols
-//   softmax_xent bufs logits,labels,loss_rows,dlogits  i logits_type,rows,cols,label_type,dlogits_type
-//                               f grad_scale
+//   softmax_xent bufs logits,labels,loss_rows,dlogits  i logits_type,rows,cols,label_type,dlogits_type,
+//                               ld_logits,ld_dlogits  f grad_scale
 //   sdpa_bwd bufs q,k,v,o,dout,lse,dq,dk,dv,workspace
 //            i B,H,Sq,Sk,D, (b,h,s strides) of q,k,v,o,dout,dq,dk,dv, causal  f scale
 //   ew_reduce bufs in...,out,tmp,ws[,stored]  i rank,dims[6],n_inputs,out_reg,val_type,out_type,rop,
@@ -97,8 +97,8 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
                          P(2), i[11], i[12], i[13], P(3), i[14], i[15], i[16], s.f[0], int(i[17]),
                          s.bufs.size() > 4 ? static_cast<float*>(P(4)) : nullptr);
     case StepKind::kSoftmaxXent:
-      return mk_softmax_xent_typed(st, int(i[0]), int(i[4]), i[1], i[2], P(0), int(i[3]), P(1), s.f[0],
-                                   static_cast<float*>(P(2)), P(3));
+      return mk_softmax_xent_strided(st, int(i[0]), int(i[4]), i[1], i[2], P(0), i[5], int(i[3]), P(1), s.f[0],
+                                     static_cast<float*>(P(2)), P(3), i[6]);
     case StepKind::kGemmBlas:
       return mk_gemm_blas(st, int(i[0]), int(i[1]), i[2], i[3], i[4], i[5], P(0), i[6], i[7], i[8], P(1), i[9],
                           i[10], i[11], P(2), i[12], i[13], 1.f, 0.f);

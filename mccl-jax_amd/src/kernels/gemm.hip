@@ -361,14 +361,17 @@ extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64
   }
   // uneven slices: ks apart (a multiple of 8, so every slice starts on a
   // 16-byte boundary of a k-contiguous operand), the last one K - (splits-1) ks
-  // long; only the tiled kernel takes a per-batch contraction length
+  // long.  Only the tiled kernel takes a per-batch contraction length; a
+  // product it does not take runs unsplit (deterministic too, with the fp32
+  // additions in another order).
   const int64_t ks = ((K + splits - 1) / splits + 7) / 8 * 8;
   const int64_t rem = K - (splits - 1) * ks;
-  if (ab_type != MK_BF16 || rem <= 0)
-    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K % splits != 0 needs bf16 operands and a non-empty last slice");
-  const int r = gemm_tiled(s, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns, W, M * N,
-                           N, nullptr, 0, rem);
-  if (r < 0) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: K % splits != 0 needs operands the tiled GEMM takes");
+  const int r = ab_type == MK_BF16 && rem > 0
+                    ? gemm_tiled(s, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks, b_ns, W,
+                                 M * N, N, nullptr, 0, rem)
+                    : -1;
+  if (r < 0)
+    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
   if (r != MK_OK) return r;
   return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type);
 }

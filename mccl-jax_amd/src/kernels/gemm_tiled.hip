@@ -295,7 +295,14 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
     const int row = e / kCpr, cn = e % kCpr;
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * pos(row, cn));
     const int64_t m = m0 + row, n = n0 + 8 * cn;
-    if (m < p.M && n < p.N) *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
+    if (m < p.M && n + 8 <= p.N) {
+      *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
+    } else if (m < p.M && n < p.N) {  // the chunk that straddles N: its columns below N only
+      uint16_t* Ce = reinterpret_cast<uint16_t*>(Cz) + m * p.ldc + n;
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (n + q < p.N) Ce[q] = uint16_t(v[q / 2] >> (16 * (q & 1)));
+    }
   }
 }
 
@@ -354,7 +361,13 @@ __device__ __attribute__((always_inline)) inline void store_staged_f32(const Til
         const int row = e / kCpr, cn = e % kCpr;
         const f32x4 v = *reinterpret_cast<const f32x4*>(st + row * TN + 4 * (cn ^ (row & 15)));
         const int64_t m = m0 + pass * kRP + row, n = n0 + 4 * cn;
-        if (m < p.M && n < p.N) *reinterpret_cast<f32x4*>(Cz + m * p.ldc + n) = v;
+        if (m < p.M && n + 4 <= p.N) {
+          *reinterpret_cast<f32x4*>(Cz + m * p.ldc + n) = v;
+        } else if (m < p.M && n < p.N) {  // the chunk that straddles N
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < p.N) Cz[m * p.ldc + n + q] = v.v[q];
+        }
       }
     } else {
 #pragma unroll 4
@@ -620,8 +633,10 @@ bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch,
   a.a_bytes = uint32_t(ab); a.b_bytes = uint32_t(bb);
   a.epilogue = epilogue;
   a.c_type = c_type;
-  const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0 && N % 8 == 0;
-  const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0 && N % 4 == 0;
+  // C rows 16-byte aligned: whole 16-byte chunks (the one straddling N, when
+  // N is not a multiple of the chunk, column by column)
+  const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0;
+  const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0;
   a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 5 : 4;
   return true;
 }

@@ -678,8 +678,18 @@ def test_gemm_tiled_ragged_k_and_rows(K):
         assert np.isfinite(got).all(), (M, N, Kd)
         assert np.max(np.abs(got - want) / (norm + 1e-30)) < 1e-5, (M, N, Kd)
         assert torch.equal(got_t, K.gemm(at, bt, out_dtype=torch.float32))
-        gb = host_bf16(K.gemm(at, bt, out_dtype=torch.bfloat16))
+        gb_t = K.gemm(at, bt, out_dtype=torch.bfloat16)
+        gb = host_bf16(gb_t)
         assert _bf16_out_ok(gb, want, norm), (M, N, Kd)
+        # C rows 16-byte aligned with N not a multiple of the store chunk:
+        # the straddling chunk is stored column by column, the pitch's
+        # padding stays untouched, the values are the dense call's
+        pitch = (N + 7) // 8 * 8 + 8
+        for dt, dense in ((torch.float32, got_t), (torch.bfloat16, gb_t)):
+            wide = torch.full((M, pitch), -7.0, dtype=dt, device="cuda")
+            K.gemm(at, bt, out_dtype=dt, out=wide[:, :N])
+            assert torch.equal(wide[:, :N], dense), (M, N, Kd, dt)
+            assert bool((wide[:, N:].float() == -7.0).all()), (M, N, Kd, dt)
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])

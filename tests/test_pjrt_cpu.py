@@ -126,8 +126,12 @@ def test_compile_jitted_training_step(client):
     assert plan.count("] sdpa (causal +lse)") == 2 and plan.count("] sdpa_bwd (causal") == 2
     # the attention gradients are written into the fused QKV gradient's layout
     assert plan.count("into the merged QKV gradient") == 2
-    # the mean softmax cross-entropy and its gradient: one fused launch
+    # the mean softmax cross-entropy and its gradient: one fused launch, over
+    # logits and a gradient whose 257-element rows are padded to 264 so that
+    # the three vocabulary products take aligned rows on the hand-written
+    # GEMM (none on the library GEMM)
     assert "pattern softmax_xent(256x257, grad_scale=0.003906)" in plan and plan.count("] softmax_xent") == 1
+    assert "] softmax_xent (rows padded)" in plan and "gemm_blas" not in plan
     # no layout copies around the attention: O is written in [B,S,H,D] order
     # and read back narrow; only the position-embedding broadcast is copied
     assert plan.count("] copy_strided") <= 1
