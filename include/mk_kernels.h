@@ -84,7 +84,10 @@ int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, c
                    int64_t c_ms, int64_t splits, void* workspace);
 
 /* mk_gemm_splitk with the output type chosen (c_type MK_F32, or MK_BF16:
- * the ordered fp32 slice sum rounded once to bf16) and, for bf16 operands
+ * the ordered fp32 slice sum rounded once to bf16), mk_gemm's epilogue
+ * applied to the sum (0 none, 1 + bias, 2 + bias then max(., 0); bias has
+ * c_type; config C1's fp32 layers, whose 64 and 16 output tiles are cut
+ * along K) and, for bf16 operands
  * the tiled kernel takes (16-byte aligned rows), any K: when K % splits != 0
  * the slices are ceil(K / splits) rounded up to a multiple of 8 apart and the
  * last one is shorter (the vocabulary products of the training step, which
@@ -94,7 +97,7 @@ int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, c
  * Replaces, for these products: src/jam/ops/linalg.mm:98. */
 int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K, const void* A,
                          int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* C,
-                         int64_t c_ms, int64_t splits, void* workspace);
+                         int64_t c_ms, int64_t splits, void* workspace, const void* bias, int epilogue);
 
 /* Plain GEMM through rocBLAS (the linear layers of the training step and
  * their gradients: with no epilogue to fuse, a library GEMM does the work).  Same operand convention as

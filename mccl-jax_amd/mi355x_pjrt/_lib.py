@@ -72,7 +72,7 @@ SIGNATURES = {
     "mk_gemm_splitk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "mk_gemm_splitk": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
     "mk_gemm_splitk_typed": (_I, [_P, _I, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
-                                  _P]),
+                                  _P, _P, _I]),
     "mk_gemm_blas_splitk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "mk_gemm_blas_splitk": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
     "mk_adam_update_dev": (_I, [_P, _I64, _I, _P, _P, _I, _P, _P, _P, _P, ctypes.c_double, ctypes.c_double,

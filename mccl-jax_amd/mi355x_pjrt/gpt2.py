@@ -283,7 +283,7 @@ class GPT2TrainStep:
             if tag == "dhf":
                 calls.append(_Call(lib.mk_gemm_splitk_typed, [st, _I(ab), _I(ct), _I64(M), _I64(N), _I64(Kd), a,
                                                               _I64(a_ms), _I64(a_ks), b, _I64(b_ks), _I64(b_ns), cptr,
-                                                              _I64(c_ms), _I64(self.DHF_SPLITS), ws],
+                                                              _I64(c_ms), _I64(self.DHF_SPLITS), ws, _P(0), _I(0)],
                                    "mk_gemm_splitk_typed " + tag))
                 return
             calls.append(_Call(lib.mk_gemm, [st, _I(ab), _I(ct), _I64(1), _I64(M), _I64(N), _I64(Kd),

@@ -352,23 +352,26 @@ def gemm_blas(a, b, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
     return out
 
 
-def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=torch.float32):
-    """out = a @ b with the contraction cut into `splits` slices summed in
-    order in fp32 (mk_gemm_splitk; mk_gemm_splitk_typed for a bf16 `out_dtype`
-    or a K that `splits` does not divide); a [M, K], b [K, N] 2-D views."""
+def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=torch.float32, bias=None,
+                relu=False):
+    """out = a @ b (+ bias)(ReLU) with the contraction cut into `splits`
+    slices summed in order in fp32 (mk_gemm_splitk; mk_gemm_splitk_typed for
+    a bf16 `out_dtype`, a bias or a K that `splits` does not divide);
+    a [M, K], b [K, N] 2-D views."""
     _require_cuda(a, b)
     M, Kd = a.shape
     N = b.shape[1]
     out = torch.empty(M, N, dtype=out_dtype, device=a.device) if out is None else out
     ws = _ws(lib().mk_gemm_splitk_workspace_bytes(M, N, splits), a.device, workspace)
-    if out.dtype == torch.float32 and Kd % splits == 0:
+    if out.dtype == torch.float32 and Kd % splits == 0 and bias is None:
         rc = lib().mk_gemm_splitk(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
                                   _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), splits, _ptr(ws))
         _check(rc, "mk_gemm_splitk")
         return out
     rc = lib().mk_gemm_splitk_typed(_stream(stream), mk_dtype(a.dtype), mk_dtype(out.dtype), M, N, Kd, _ptr(a),
                                     a.stride(0), a.stride(1), _ptr(b), b.stride(0), b.stride(1), _ptr(out),
-                                    out.stride(0), splits, _ptr(ws))
+                                    out.stride(0), splits, _ptr(ws), _ptr(bias),
+                                    0 if bias is None else (2 if relu else 1))
     _check(rc, "mk_gemm_splitk_typed")
     return out
 

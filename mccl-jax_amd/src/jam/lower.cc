@@ -3366,24 +3366,6 @@ class Lowerer {
   // C[M,N] (f32, dense) = C + bias[N], then max(C, 0) when the epilogue has
   // the ReLU: one elementwise step in place (the epilogue of mk_gemm, for a
   // product computed without it).
-  void EmitBiasEpilogue(BufRef c, int64_t M, int64_t N, const Fused& epi) {
-    const View bv = Densify(NeedView(epi.bias));
-    if (bv.dtype != DType::kF32) throw std::string("jam: split product with a non-f32 bias");
-    Step st;
-    st.kind = StepKind::kEw;
-    st.bufs = {c, bv.at(), c};
-    st.types = {int32_t(DType::kF32), int32_t(DType::kF32)};
-    st.strides = {N, 1, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0};
-    st.i = {2, M, N, 1, 1, 1, 1, 2, 2, int64_t(DType::kF32)};
-    st.prog = {MK_EW_ADD, 2, 0, 1};
-    if (epi.relu) {
-      st.prog.insert(st.prog.end(), {MK_EW_CONST, 3, 0, 0, MK_EW_MAX, 2, 2, 3});
-      st.f = {0.f};
-    }
-    st.note = epi.relu ? "bias + relu epilogue" : "bias epilogue";
-    Emit(st);
-  }
-
   // Map a dot_general to mk_gemm; `epi` optionally carries bias / relu.
   void LowerDot(int idx, const Fused* epi, int result_override = -1) {
     const Op& op = ops_[idx];
@@ -3508,11 +3490,18 @@ class Lowerer {
       if (splits > 1) {
         st.kind = StepKind::kGemmSplitK;
         st.bufs = {lv.at(), rv.at(), d, NewTemp(mk_gemm_splitk_workspace_bytes(M, N, splits))};
-        st.i = {int64_t(at), M, N, K, a_ms, a_ks, b_ks, b_ns, c_pitch, splits};
+        st.i = {int64_t(at), M, N, K, a_ms, a_ks, b_ks, b_ns, c_pitch, splits, 0};
         st.note = std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K) + " in " +
                   std::to_string(splits) + " slices";
+        if (epi) {
+          // the bias (+ ReLU) applied by the pass that sums the slices
+          const View bv = Densify(NeedView(epi->bias));
+          if (bv.dtype != DType::kF32) throw std::string("jam: split product with a non-f32 bias");
+          st.bufs.push_back(bv.at());
+          st.i[10] = epi->relu ? 2 : 1;
+          st.note += epi->relu ? ", + bias + relu" : ", + bias";
+        }
         Emit(st);
-        if (epi) EmitBiasEpilogue(d, M, N, *epi);
         set_result(d);
         return;
       }

@@ -60,7 +60,7 @@ void* Resolve(const BufRef& b, const Frame& f) {
 // Step encodings (written by lower.cc):
 //   gemm     bufs A,B,C[,bias]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
 //   gemm_blas bufs A,B,C        i as gemm (no epilogue)
-//   gemm_splitk bufs A,B,C,workspace  i ab_type,M,N,K,a_ms,a_ks,b_ks,b_ns,c_ms,splits
+//   gemm_splitk bufs A,B,C,workspace[,bias]  i ab_type,M,N,K,a_ms,a_ks,b_ks,b_ns,c_ms,splits,epilogue
 //   sdpa     bufs Q,K,V,O[,lse] i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
 //   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
 //   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
@@ -108,8 +108,8 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
                          static_cast<const float*>(P(5)), P(6), i[20], i[21], i[22], P(7), i[23], i[24], i[25],
                          P(8), i[26], i[27], i[28], s.f[0], int(i[29]), P(9));
     case StepKind::kGemmSplitK:
-      return mk_gemm_splitk(st, int(i[0]), i[1], i[2], i[3], P(0), i[4], i[5], P(1), i[6], i[7],
-                            static_cast<float*>(P(2)), i[8], i[9], P(3));
+      return mk_gemm_splitk_typed(st, int(i[0]), MK_F32, i[1], i[2], i[3], P(0), i[4], i[5], P(1), i[6], i[7], P(2),
+                                  i[8], i[9], P(3), s.bufs.size() > 4 ? P(4) : nullptr, int(i[10]));
     case StepKind::kColSum:  // y[c] = sum_r x[r, c]: i = {dtype, rows, cols}
       return mk_col_sum(st, int(i[0]), i[1], i[2], P(0), static_cast<float*>(P(1)), P(2));
     case StepKind::kRowReduce:

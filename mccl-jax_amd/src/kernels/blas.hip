@@ -112,7 +112,8 @@ namespace {
 // the next); S == 0: any count.  Same order of adds either way.
 template <int S, bool BF16>
 __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ w, int64_t splits, int64_t M,
-                                                        int64_t N, void* __restrict__ c, int64_t c_ms) {
+                                                        int64_t N, void* __restrict__ c, int64_t c_ms,
+                                                        const void* __restrict__ bias, int epilogue) {
   const int64_t nvec = M * N / 4, slab = M * N / 4;
   const int64_t stride = int64_t(gridDim.x) * 256;
   const f32x4* wv = reinterpret_cast<const f32x4*>(w);
@@ -136,6 +137,13 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
       }
     }
     const int64_t e = i * 4, m = e / N, n = e % N;
+    if (epilogue != 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a.v[j] += BF16 ? bf16_to_f32(static_cast<const uint16_t*>(bias)[n + j]) : static_cast<const float*>(bias)[n + j];
+        if (epilogue == 2) a.v[j] = fmaxf(a.v[j], 0.f);
+      }
+    }
     if constexpr (BF16)
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(c) + m * c_ms + n) =
           uint2{f32_to_bf16(a.v[0]) | (uint32_t(f32_to_bf16(a.v[1])) << 16),
@@ -147,20 +155,21 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 
 template <bool BF16>
 void splitk_sum_launch(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, void* C, int64_t c_ms,
-                       unsigned blocks) {
-  if (splits == 2) hipLaunchKernelGGL((splitk_sum_kernel<2, BF16>), dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else if (splits == 4) hipLaunchKernelGGL((splitk_sum_kernel<4, BF16>), dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else if (splits == 8) hipLaunchKernelGGL((splitk_sum_kernel<8, BF16>), dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
-  else hipLaunchKernelGGL((splitk_sum_kernel<0, BF16>), dim3(blocks), dim3(256), 0, s, W, splits, M, N, C, c_ms);
+                       unsigned blocks, const void* bias, int epi) {
+  const dim3 g(blocks), b(256);
+  if (splits == 2) hipLaunchKernelGGL((splitk_sum_kernel<2, BF16>), g, b, 0, s, W, splits, M, N, C, c_ms, bias, epi);
+  else if (splits == 4) hipLaunchKernelGGL((splitk_sum_kernel<4, BF16>), g, b, 0, s, W, splits, M, N, C, c_ms, bias, epi);
+  else if (splits == 8) hipLaunchKernelGGL((splitk_sum_kernel<8, BF16>), g, b, 0, s, W, splits, M, N, C, c_ms, bias, epi);
+  else hipLaunchKernelGGL((splitk_sum_kernel<0, BF16>), g, b, 0, s, W, splits, M, N, C, c_ms, bias, epi);
 }
 }  // namespace
 
 int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, void* C, int64_t c_ms,
-               const char* what, int c_type) {
+               const char* what, int c_type, const void* bias, int epilogue) {
   const int64_t nvec = M * N / 4;
   const unsigned blocks = unsigned(std::min<int64_t>((nvec + 255) / 256, 4096));
-  if (c_type == MK_BF16) splitk_sum_launch<true>(s, W, splits, M, N, C, c_ms, blocks);
-  else splitk_sum_launch<false>(s, W, splits, M, N, C, c_ms, blocks);
+  if (c_type == MK_BF16) splitk_sum_launch<true>(s, W, splits, M, N, C, c_ms, blocks, bias, epilogue);
+  else splitk_sum_launch<false>(s, W, splits, M, N, C, c_ms, blocks, bias, epilogue);
   return check_launch(what);
 }
 

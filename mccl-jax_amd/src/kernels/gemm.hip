@@ -337,12 +337,16 @@ extern "C" size_t mk_gemm_splitk_workspace_bytes(int64_t M, int64_t N, int64_t s
 
 extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K,
                                     const void* A, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks,
-                                    int64_t b_ns, void* C, int64_t c_ms, int64_t splits, void* workspace) {
+                                    int64_t b_ns, void* C, int64_t c_ms, int64_t splits, void* workspace,
+                                    const void* bias, int epilogue) {
   clear_error();
   if (splits < 1 || K < 0 || M < 0 || N < 0) return fail(MK_ERR_INVALID, "mk_gemm_splitk: bad shape or splits");
   if (c_type != MK_F32 && c_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: c_type must be f32 or bf16");
+  if (epilogue < 0 || epilogue > 2) return fail(MK_ERR_INVALID, "mk_gemm_splitk: epilogue must be 0, 1 or 2");
+  if (epilogue != 0 && !bias) return fail(MK_ERR_INVALID, "mk_gemm_splitk: epilogue needs bias");
   if (splits == 1 || M == 0 || N == 0)
-    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
+    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, bias,
+                   epilogue);
   if (!workspace || !C) return fail(MK_ERR_INVALID, "mk_gemm_splitk: null workspace or output");
   const uintptr_t cal = c_type == MK_F32 ? 15u : 7u;
   if ((N % 4) != 0 || (c_ms % 4) != 0 || (reinterpret_cast<uintptr_t>(C) & cal) ||
@@ -357,7 +361,7 @@ extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64
     if (int rc = mk_gemm(stream, ab_type, MK_F32, splits, M, N, ks, A, ks * a_ks, a_ms, a_ks, B, ks * b_ks, b_ks,
                          b_ns, W, M * N, N, nullptr, 0))
       return rc;
-    return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type);
+    return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type, bias, epilogue);
   }
   // uneven slices: ks apart (a multiple of 8, so every slice starts on a
   // 16-byte boundary of a k-contiguous operand), the last one K - (splits-1) ks
@@ -371,14 +375,15 @@ extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64
                                  M * N, N, nullptr, 0, rem)
                     : -1;
   if (r < 0)
-    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, nullptr, 0);
+    return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, bias,
+                   epilogue);
   if (r != MK_OK) return r;
-  return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type);
+  return splitk_sum(s, W, splits, M, N, C, c_ms, "mk_gemm_splitk", c_type, bias, epilogue);
 }
 
 extern "C" int mk_gemm_splitk(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_ms,
                               int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, float* C, int64_t c_ms,
                               int64_t splits, void* workspace) {
   return mk_gemm_splitk_typed(stream, ab_type, MK_F32, M, N, K, A, a_ms, a_ks, B, b_ks, b_ns, C, c_ms, splits,
-                              workspace);
+                              workspace, nullptr, 0);
 }

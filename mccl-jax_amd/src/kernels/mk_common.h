@@ -26,11 +26,12 @@ int gemm_blas(hipStream_t stream, int ab_type, int c_type, int64_t batch, int64_
               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, float alpha, float beta);
 
 // C = sum of the splits dense M x N fp32 slices of W, added in slice order
-// (blas.hip), stored as c_type (MK_F32, or MK_BF16 rounded once from the
-// fp32 sum); N and c_ms multiples of 4, W 16-byte and C 16- (fp32) or
+// (blas.hip), then + bias (c_type, per column; epilogue 1) and max(., 0)
+// (epilogue 2), stored as c_type (MK_F32, or MK_BF16 rounded once from the
+// fp32 result); N and c_ms multiples of 4, W 16-byte and C 16- (fp32) or
 // 8-byte (bf16) aligned.
 int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t N, void* C, int64_t c_ms,
-               const char* what, int c_type = 0);
+               const char* what, int c_type = 0, const void* bias = nullptr, int epilogue = 0);
 
 // Tiled bf16 GEMM for large products behind mk_gemm (gemm_tiled.hip), same
 // operand convention; returns -1 without launching when the shape, strides or

@@ -50,14 +50,14 @@ def _plan(client, text):
 def test_compile_mlp_fuses_bias_relu(client):
     """C1's fp32 products have 64 and 16 output tiles of 128x128: each is cut
     along K into about 256 workgroups (gemm_splitk), and the matched bias /
-    bias + ReLU epilogue runs as one elementwise pass over the sum."""
+    bias + ReLU epilogue is applied by the pass that sums the slices: two
+    steps in all."""
     plan, types, shapes = _plan(client, modules.mlp())
     assert types == [pjrt.F32] and shapes == [(256, 1024)]
     assert "pattern gemm+bias+relu" in plan and "pattern gemm+bias\n" in plan
-    assert "] gemm_splitk (256x4096x1024 in 4 slices)" in plan
-    assert "] gemm_splitk (256x1024x4096 in 16 slices)" in plan
-    assert "] ew (bias + relu epilogue)" in plan and "] ew (bias epilogue)" in plan
-    assert plan.count("] gemm") == 2 and plan.count("] ew") == 2
+    assert "] gemm_splitk (256x4096x1024 in 4 slices, + bias + relu)" in plan
+    assert "] gemm_splitk (256x1024x4096 in 16 slices, + bias)" in plan
+    assert plan.count("] gemm") == 2 and plan.count("] ew") == 0
 
 
 def test_compile_sdpa_is_one_flash_launch(client):
