@@ -376,15 +376,21 @@ def run_gemm(torch, np, K, args):
     res = {}
     g = torch.Generator(device="cuda").manual_seed(0)
 
+    V = 50257
+    Vp = (V + 7) // 8 * 8
+
     def mat(rows, cols, layout, dt):
-        if layout == "rm":
-            return torch.randn(rows, cols, device="cuda", generator=g).to(dt)
-        return torch.randn(cols, rows, device="cuda", generator=g).to(dt).t()
+        # the vocabulary dimension is stored with the padded row pitch the
+        # C5 step uses (50264), so the vocabulary products see its layout
+        r2, c2 = (rows, cols) if layout == "rm" else (cols, rows)
+        pc = Vp if c2 == V else c2
+        t = torch.randn(r2, pc, device="cuda", generator=g).to(dt)[:, :c2]
+        return t if layout == "rm" else t.t()
 
     for tag, od, M, N, Kd, la, lb in C5_GEMMS:
         a, b = mat(M, Kd, la, torch.bfloat16), mat(Kd, N, lb, torch.bfloat16)
         odt = torch.float32 if od == "f32" else torch.bfloat16
-        c = torch.empty(M, N, dtype=odt, device="cuda")
+        c = torch.empty(M, Vp if N == V else N, dtype=odt, device="cuda")[:, :N]
         fl = 2.0 * M * N * Kd
         row = {"M": M, "N": N, "K": Kd}
         for name, fn in (("mk_gemm", lambda: K.gemm(a, b, out_dtype=odt, out=c)),
@@ -393,6 +399,15 @@ def run_gemm(torch, np, K, args):
             row[name + "_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
         row["mk_gemm_frac_peak"] = round(row["mk_gemm_tflops"] / PEAK_BF16_TFLOPS, 4)
         msg = f"gemm {tag} [{M}x{N}x{Kd}]: mk_gemm {row['mk_gemm_tflops']} TFLOP/s, rocBLAS {row['rocblas_tflops']}"
+        if tag == "dhf":  # the C5 step splits it along the vocabulary (uneven slices, bf16 out)
+            sp = GPT2TrainStep.DHF_SPLITS
+            ms = time_launches(torch, lambda: K.gemm_splitk(a, b, sp, out=c, out_dtype=odt), max(5, args.steps // 2), 3)
+            row["mk_gemm_splitk_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+            row["splits"] = sp
+            msg += f"; split {sp}: mk_gemm_splitk_typed {row['mk_gemm_splitk_tflops']}"
+        row["c5_step_path"] = ("rocBLAS" if tag in GPT2TrainStep.BLAS_GEMMS else
+                               "mk_gemm_splitk_typed" if tag == "dhf" else
+                               "mk_gemm_splitk" if tag in GPT2TrainStep.DW_SPLITS else "mk_gemm")
         sp = GPT2TrainStep.DW_SPLITS.get(tag, 1)
         if sp > 1:  # the C5 step runs these fp32 weight gradients split along K
             for name, fn in (("mk_gemm_splitk", lambda: K.gemm_splitk(a, b, sp, out=c)),
