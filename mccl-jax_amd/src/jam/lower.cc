@@ -80,6 +80,8 @@ std::string Program::Dump() const {
   for (size_t i = 0; i < steps.size(); ++i) {
     os << "  [" << i << "] " << StepName(steps[i].kind);
     if (!steps[i].note.empty()) os << " (" << steps[i].note << ")";
+    // the generated kernel that runs the step (its name in profiles)
+    if (ew_jit && steps[i].jit >= 0) os << " -> " << ew_jit->kernel(steps[i].jit).name;
     if (getenv("JAM_DUMP_BUFFERS")) {  // debugging: where each step's buffers live
       static const char* kSpace[] = {"in", "out", "arena", "const", "none"};
       for (const BufRef& b : steps[i].bufs) os << " " << kSpace[int(b.space)] << b.index << "@" << b.offset;
@@ -2917,11 +2919,41 @@ class Lowerer {
     SetDenseView(best, d);
   }
 
+  // Conversions of module inputs to a narrower float type whose results
+  // only non-elementwise ops read (the bf16 copies of a training step's fp32
+  // weights for its products) are emitted first, one after another: they
+  // depend on nothing else, and as a run of independent steps each group of
+  // one shape becomes one batched launch (BatchIndependentEwSteps) instead
+  // of a launch in front of every product.
+  std::set<int> hoisted_;
+  void HoistInputConverts() {
+    if (!opts_.fuse_elementwise) return;
+    for (size_t i = 0; i < ops_.size(); ++i) {
+      const Op& op = ops_[i];
+      if (!live_[i] || fused_.count(int(i)) || op.name != "stablehlo.convert" || op.operands.size() != 1) continue;
+      const int src = op.operands[0], res = op.results[0];
+      if (state_[src].kind != ValState::kView || state_[src].view.buf.space != Space::kInput) continue;
+      const DType it = m_.types[src].dtype, ot = m_.types[res].dtype;
+      if (!(it == DType::kF32 && (ot == DType::kBF16 || ot == DType::kF16))) continue;
+      if (std::count(outputs_.begin(), outputs_.end(), res)) continue;
+      const auto us = live_users(res);
+      bool ok = !us.empty();
+      // readers that take it from memory: products and layout ops, also
+      // inside a matched pattern (a product with its bias epilogue)
+      for (int u : us) ok = ok && !IsElementwise(ops_[u].name);
+      if (!ok) continue;
+      LowerOp(int(i));   // the lazy conversion
+      NeedView(res);     // written now
+      hoisted_.insert(int(i));
+    }
+  }
+
   // -------------------------------------------------------------- the walk
   void Walk() {
     out_written_.assign(outputs_.size(), false);
+    HoistInputConverts();
     for (size_t i = 0; i < ops_.size(); ++i) {
-      if (!live_[i]) continue;
+      if (!live_[i] || hoisted_.count(int(i))) continue;
       auto f = fused_.find(int(i));
       if (f != fused_.end()) {
         EmitFused(int(i), f->second);
