@@ -506,8 +506,25 @@ def run_pjrt(torch, np, args):
         b.ready()
 
     run = pjrt_runner(p)
-    run(e, bufs, args.warmup)
-    ms = run(e, bufs, args.steps)
+    # Executes first run for --spinup seconds on the same inputs (the clocks
+    # leave whatever state the previous section left them in), then the
+    # Execute path and the bare kernel (mk_sdpa_fwd on copies of the same
+    # inputs, HIP events) are timed alternately, three rounds each, so the
+    # per-Execute overhead is the difference of the two in one warm state
+    from mi355x_pjrt import kernels as K
+    t0 = time.time()
+    while time.time() - t0 < max(args.spinup, 0.3):
+        run(e, bufs, 10)
+    qd, kd, vd = (torch.from_numpy(d[k].view(np.int16)).view(torch.bfloat16).cuda() for k in ("q", "k", "v"))
+    od = torch.empty_like(qd)
+    ex, bare = [], []
+    for _ in range(3):
+        run(e, bufs, args.warmup)
+        ex.append(run(e, bufs, args.steps))
+        bare.append(time_launches(torch, lambda: K.sdpa_fwd(qd, kd, vd, 1 / math.sqrt(128), True, out=od),
+                                  args.steps, args.warmup))
+    ms, ms_bare = sorted(ex)[1], sorted(bare)[1]
+    del qd, kd, vd, od
     tf = sdpa_flops(4, 16, args.seq, 128) / (ms * 1e-3) / 1e12
     small = client.compile(modules.reduce_sum(4, 8))
     xb = client.put(bf16.to_bf16_bits(np.ones((4, 8), np.float32)), pjrt.BF16)
@@ -519,6 +536,8 @@ def run_pjrt(torch, np, args):
     e.destroy()
     small.destroy()
     res = {"sdpa_ms_per_execute": round(ms, 4), "sdpa_tflops": round(tf, 2),
+           "sdpa_bare_kernel_ms_same_state": round(ms_bare, 4),
+           "execute_overhead_frac": round(ms / ms_bare - 1, 4),
            "tiny_module_us_per_execute": round(us, 2)}
     res["c5_jitted_step"] = run_c5_jitted(np, p, client, run, args)
     client.close()
