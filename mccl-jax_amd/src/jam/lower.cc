@@ -3395,9 +3395,6 @@ class Lowerer {
     return true;
   }
 
-  // C[M,N] (f32, dense) = C + bias[N], then max(C, 0) when the epilogue has
-  // the ReLU: one elementwise step in place (the epilogue of mk_gemm, for a
-  // product computed without it).
   // Map a dot_general to mk_gemm; `epi` optionally carries bias / relu.
   void LowerDot(int idx, const Fused* epi, int result_override = -1) {
     const Op& op = ops_[idx];
