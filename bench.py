@@ -425,9 +425,9 @@ def run_gemm(torch, np, K, args):
 
 def run_c1_pjrt(np, args):
     """Config C1 (fp32 MLP forward) as jaxlib runs it: the module compiled by
-    jam (each product split along K into about 256 workgroups, bias / ReLU as
-    one elementwise pass each) and run through PJRT Execute on resident
-    inputs; TFLOP/s against the fp32 MFMA peak (157.3)."""
+    jam (each product split along K into about 256 workgroups, bias / ReLU
+    applied by the pass that sums the slices) and run through PJRT Execute on
+    resident inputs; TFLOP/s against the fp32 MFMA peak (157.3)."""
     from mi355x_pjrt import modules, pjrt
     from oracle import inputs
 
@@ -449,7 +449,7 @@ def run_c1_pjrt(np, args):
     tf = fl / (ms * 1e-3) / 1e12
     log(f"C1 MLP fp32 through PJRT Execute: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s ({100*tf/157.3:.1f}% of fp32 peak)")
     return {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_peak_fp32": round(tf / 157.3, 4),
-            "path": "PJRT Execute of the C1 module (jam: gemm_splitk + ew epilogue per layer)"}
+            "path": "PJRT Execute of the C1 module (jam: one gemm_splitk per layer, bias / ReLU in the slice sum)"}
 
 
 def pjrt_runner(p):
