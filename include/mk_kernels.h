@@ -187,6 +187,15 @@ int mk_row_argmax(void* stream, int in_type, int is_min, int64_t rows, int64_t c
 int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t cols,
                  const void* x, const void* gamma, const void* beta, float eps, void* y);
 
+/* mk_layernorm with the stored type separate from the input's: x, gamma,
+ * beta of in_type, y of out_type, (in, out) ∈ {(bf16, bf16), (f32, f32),
+ * (f32, bf16)}.  (f32, bf16) is the LayerNorm of an fp32 residual stream
+ * whose result only feeds a bf16 matrix product (the convert that
+ * reduce.mm / elementwise.mm would run as its own node folded into the
+ * store: one rounding of the fp32 result). */
+int mk_layernorm_typed(void* stream, int in_type, int out_type, int64_t rows, int64_t cols, const void* x,
+                       const void* gamma, const void* beta, float eps, void* y);
+
 /* ------------------------------------------------------------------------
  * a7  fused GELU (tanh approximation), fp32 math, one rounding on store.
  * Replaces the multiply/add/tanh chain of elementwise.mm:91-171 for the

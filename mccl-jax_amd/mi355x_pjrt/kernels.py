@@ -135,14 +135,17 @@ def row_argmax(x, is_min=False, index_dtype=torch.int32, with_values=True, strea
     return idx, vals
 
 
-def layernorm(x, gamma=None, beta=None, eps=1e-5, stream=None):
+def layernorm(x, gamma=None, beta=None, eps=1e-5, out_dtype=None, stream=None):
+    """LayerNorm over the last axis; out_dtype (default x's) may be bf16 for
+    fp32 x (mk_layernorm_typed)."""
     _require_cuda(x)
     x = x.contiguous()
-    y = torch.empty_like(x)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
     rows = x.numel() // x.shape[-1]
-    rc = lib().mk_layernorm(_stream(stream), mk_dtype(x.dtype), rows, x.shape[-1], _ptr(x),
-                            _ptr(gamma), _ptr(beta), float(eps), _ptr(y))
-    _check(rc, "mk_layernorm")
+    rc = lib().mk_layernorm_typed(_stream(stream), mk_dtype(x.dtype), mk_dtype(out_dtype), rows, x.shape[-1],
+                                  _ptr(x), _ptr(gamma), _ptr(beta), float(eps), _ptr(y))
+    _check(rc, "mk_layernorm_typed")
     return y
 
 

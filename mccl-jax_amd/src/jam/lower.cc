@@ -59,6 +59,7 @@ const char* StepName(StepKind k) {
     case StepKind::kGemmBlas: return "gemm_blas";
     case StepKind::kSoftmaxXent: return "softmax_xent";
     case StepKind::kColSum: return "col_sum";
+    case StepKind::kLayerNormBwd: return "layernorm_bwd";
     case StepKind::kGemmSplitK: return "gemm_splitk";
     case StepKind::kEwReduce: return "ew_reduce";
   }
@@ -351,7 +352,7 @@ struct ValState {
 };
 
 struct Fused {
-  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu, kSdpaBwd, kXent } kind;
+  enum Kind { kSdpa, kArgmax, kGemmEpi, kLayerNorm, kGelu, kSdpaBwd, kXent, kLayerNormBwd } kind;
   std::vector<int> deps;  // value ids the fused step reads
   // sdpa (train: also lse and the bf16 O for the backward step)
   int q = -1, k = -1, v = -1;
@@ -372,10 +373,14 @@ struct Fused {
   // gemm epilogue
   int dot = -1, bias = -1;
   bool relu = false;
-  // layernorm
+  // layernorm (in_dtype: x, gamma and beta; out_dtype: the result)
   int gamma = -1, beta = -1;
   float eps = 0;
   DType out_dtype = DType::kInvalid;
+  DType in_dtype = DType::kInvalid;
+  // layernorm backward (x, gamma, dout = dy): the residual cotangent added to
+  // dx, and the dgamma / dbeta / bias-gradient values it also writes (-1: none)
+  int dres = -1, dgamma = -1, dbeta = -1, colsum = -1;
 };
 
 class Lowerer {
@@ -439,6 +444,7 @@ class Lowerer {
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
+      case StepKind::kLayerNormBwd: return {4, 5, 6, 7, 8};
       case StepKind::kGelu: return {1};
       case StepKind::kEw: {
         std::vector<size_t> w;
@@ -744,11 +750,17 @@ class Lowerer {
     if (opts_.fuse_gelu)
       for (size_t i = 0; i < ops_.size(); ++i)
         if (ops_[i].name == "stablehlo.multiply" && !fused_.count(int(i))) TryMatchGelu(int(i));
-    if (opts_.fuse_layernorm)
+    if (opts_.fuse_layernorm) {
+      auto candidate = [&](size_t i) {
+        return !fused_.count(int(i)) && !absorbed_.count(int(i)) &&
+               (ops_[i].name == "stablehlo.add" || ops_[i].name == "stablehlo.multiply" ||
+                ops_[i].name == "stablehlo.convert");
+      };
       for (size_t i = ops_.size(); i-- > 0;)
-        if (!fused_.count(int(i)) && (ops_[i].name == "stablehlo.add" || ops_[i].name == "stablehlo.multiply" ||
-                                      ops_[i].name == "stablehlo.convert"))
-          TryMatchLayerNorm(int(i));
+        if (candidate(i)) TryMatchLayerNormTrain(int(i));
+      for (size_t i = ops_.size(); i-- > 0;)
+        if (candidate(i)) TryMatchLayerNorm(int(i));
+    }
   }
 
   // ---- small structural-matching helpers
@@ -2091,22 +2103,33 @@ class Lowerer {
   //   XF = convert?(x); MEAN = sum(XF)/n; XC = XF - bcast(MEAN);
   //   VAR = sum(XC*XC)/n; N = XC * bcast(rsqrt(VAR + eps));
   //   Y = N [* bcast(gamma)] [+ bcast(beta)]  [-> convert to the storage type]
-  void TryMatchLayerNorm(int idx) {
+  // The values a differentiated step reads again are recorded: the gamma
+  // and beta broadcasts GB / BB, N (Y0), XC, the rsqrt R and its broadcast RB.
+  struct LnMatch {
+    int anchor = -1, out_v = -1, Y = -1;
+    int gamma = -1, beta = -1, GB = -1, BB = -1;
+    int Y0 = -1, XC = -1, XF = -1, R = -1, RB = -1;
+    float eps = 0;
+    std::set<int> ops;  // the forward's ops, anchor included
+  };
+  bool MatchLnForward(int idx, LnMatch& m) const {
     int Y = ops_[idx].results[0];
-    int anchor = idx;
-    int out_v = Y;
+    m.anchor = idx;
+    m.out_v = Y;
     if (ops_[idx].name == "stablehlo.convert") {  // output rounding folded in
       Y = ops_[idx].operands[0];
-      if (users_[Y].size() != 1 || uses_[Y] != 1) return;
+      if (users_[Y].size() != 1 || uses_[Y] != 1) return false;
     }
+    m.Y = Y;
     const TensorType& yt = m_.types[Y];
-    if (yt.dtype != DType::kF32 || yt.rank() < 1) return;
+    if (yt.dtype != DType::kF32 || yt.rank() < 1) return false;
     const int64_t n = yt.dims.back();
-    std::set<int> ops{idx};
-    int gamma = -1, beta = -1, N = Y;
+    std::set<int>& ops = m.ops;
+    ops = {idx};
+    int N = Y;
     // optional + beta
     {
-      int rest = -1, bvec = -1;
+      int rest = -1, bvec = -1, bb = -1;
       std::set<int> bops;
       if (Comm(Y, "stablehlo.add", [&](int a, int b) {
             bops.clear();
@@ -2114,9 +2137,11 @@ class Lowerer {
             if (vec < 0) return false;
             rest = a;
             bvec = vec;
+            bb = b;
             return true;
           })) {
-        beta = bvec;
+        m.beta = bvec;
+        m.BB = bb;
         N = rest;
         ops.insert(producer_[Y]);
         ops.insert(bops.begin(), bops.end());
@@ -2124,7 +2149,7 @@ class Lowerer {
     }
     // optional * gamma
     {
-      int rest = -1, gvec = -1;
+      int rest = -1, gvec = -1, gb = -1;
       std::set<int> gops;
       int N2 = N;
       if (Comm(N2, "stablehlo.multiply", [&](int a, int b) {
@@ -2135,17 +2160,17 @@ class Lowerer {
             if (!is(a, "stablehlo.multiply")) return false;
             rest = a;
             gvec = vec;
+            gb = b;
             return true;
           })) {
-        gamma = gvec;
+        m.gamma = gvec;
+        m.GB = gb;
         ops.insert(producer_[N2]);
         ops.insert(gops.begin(), gops.end());
         N = rest;
       }
     }
     // N = XC * bcast(rsqrt(VAR + eps))
-    int XC = -1, XF = -1;
-    float eps = 0;
     const bool core = Comm(N, "stablehlo.multiply", [&](int xc, int r) {
       std::set<int> cops;
       int rs = r;
@@ -2166,9 +2191,9 @@ class Lowerer {
       cops.insert(producer_[prod(rs)->operands[0]]);
       // XC = XF - bcast(MEAN(XF))
       int xf = -1;
-      if (!NonComm(xc, "stablehlo.subtract", [&](int a, int m) {
+      if (!NonComm(xc, "stablehlo.subtract", [&](int a, int mv) {
             std::set<int> mops;
-            int in = RowMeanOf(m, n, mops);
+            int in = RowMeanOf(mv, n, mops);
             if (in < 0 || in != a) return false;
             xf = a;
             cops.insert(mops.begin(), mops.end());
@@ -2186,36 +2211,303 @@ class Lowerer {
       cops.insert(vops.begin(), vops.end());
       ops.insert(producer_[N]);
       ops.insert(cops.begin(), cops.end());
-      XC = xc;
-      XF = xf;
-      eps = float(e);
+      m.XC = xc;
+      m.XF = xf;
+      m.R = rs;
+      m.RB = r;
+      m.eps = float(e);
       return true;
     });
-    if (!core) return;
+    if (!core) return false;
+    m.Y0 = N;
+    return true;
+  }
+
+  void TryMatchLayerNorm(int idx) {
+    LnMatch m;
+    if (!MatchLnForward(idx, m)) return;
     // every value computed inside the pattern stays inside it
-    for (int o : ops)
+    for (int o : m.ops)
       for (int r : ops_[o].results)
-        if (o != anchor && !uses_within(r, ops)) return;
-    int src = XF;
-    if (is(XF, "stablehlo.convert")) src = prod(XF)->operands[0];
-    const DType io = m_.types[out_v].dtype;
+        if (o != idx && !uses_within(r, m.ops)) return;
+    int src = m.XF;
+    if (is(m.XF, "stablehlo.convert")) src = prod(m.XF)->operands[0];
+    const DType io = m_.types[m.out_v].dtype;
     if (m_.types[src].dtype != io || (io != DType::kBF16 && io != DType::kF32)) return;
-    if ((gamma >= 0 && m_.types[gamma].dtype != io) || (beta >= 0 && m_.types[beta].dtype != io)) return;
-    (void)XC;
+    if ((m.gamma >= 0 && m_.types[m.gamma].dtype != io) || (m.beta >= 0 && m_.types[m.beta].dtype != io)) return;
     Fused f;
     f.kind = Fused::kLayerNorm;
     f.x = src;
-    f.gamma = gamma;
-    f.beta = beta;
-    f.eps = eps;
+    f.gamma = m.gamma;
+    f.beta = m.beta;
+    f.eps = m.eps;
     f.out_dtype = io;
+    f.in_dtype = io;
     f.deps = {src};
-    if (gamma >= 0) f.deps.push_back(gamma);
-    if (beta >= 0) f.deps.push_back(beta);
-    fused_[anchor] = f;
-    for (int o : ops)
-      if (o != anchor) absorbed_.insert(o);
-    prog_->patterns.push_back(std::string("layernorm(") + DTypeName(io) + ", eps=" + std::to_string(eps) + ")");
+    if (m.gamma >= 0) f.deps.push_back(m.gamma);
+    if (m.beta >= 0) f.deps.push_back(m.beta);
+    fused_[idx] = f;
+    for (int o : m.ops)
+      if (o != idx) absorbed_.insert(o);
+    prog_->patterns.push_back(std::string("layernorm(") + DTypeName(io) + ", eps=" + std::to_string(m.eps) + ")");
+  }
+
+  // A LayerNorm of fp32 rows [rows, n] (gamma required, beta optional) with
+  // the backward that reverse-mode differentiation emits for it, rule by
+  // rule (the transposes of the forward's ops, as jax.grad produces them):
+  //   dY0 = dy GB;  dgamma = sum_0(dy Y0);  [dbeta = sum_0(dy)]
+  //   dR = sum_1(dY0 XC);  dVE = dR (-0.5) (R (R R));  dS2 = dVE (1/n)
+  //   dXC = dY0 RB + bcast(dS2) XC + bcast(dS2) XC      (the square's two operands)
+  //   dx = [prev +] dXC;  dx += bcast(sum_1(-dXC) (1/n))
+  //   [the bias gradient sum_0(dx) of the projection that wrote x]
+  // The forward becomes one LayerNorm launch (the output convert folded into
+  // its store) and the backward one mk_layernorm_bwd launch, which
+  // recomputes the row statistics from x and writes dx (prev as the residual
+  // branch), dgamma, dbeta and the bias gradient.  Every value in between
+  // must be read by these ops only.
+  void TryMatchLayerNormTrain(int idx) {
+    LnMatch m;
+    if (!MatchLnForward(idx, m) || m.gamma < 0) return;
+    const int X = m.XF;
+    const TensorType& xt = m_.types[X];
+    if (is(X, "stablehlo.convert") || xt.dtype != DType::kF32 || xt.rank() != 2) return;
+    if (m_.types[m.gamma].dtype != DType::kF32 || (m.beta >= 0 && m_.types[m.beta].dtype != DType::kF32)) return;
+    const DType out_t = m_.types[m.out_v].dtype;
+    if (out_t != DType::kF32 && out_t != DType::kBF16) return;
+    const int64_t n = xt.dims[1];
+    if (n > 2048) return;  // mk_layernorm_bwd's row limit
+    auto uniq_users = [&](int v) {
+      std::vector<int> r;
+      for (int u : live_users(v))
+        if (std::find(r.begin(), r.end(), u) == r.end()) r.push_back(u);
+      return r;
+    };
+    auto outside = [&](int v) {
+      std::vector<int> r;
+      for (int u : uniq_users(v))
+        if (!m.ops.count(u)) r.push_back(u);
+      return r;
+    };
+    auto single = [&](int v) {
+      const auto u = uniq_users(v);
+      return u.size() == 1 ? u[0] : -1;
+    };
+    auto res = [&](int op) { return ops_[op].results[0]; };
+    // op = multiply(a, other) in either order
+    auto mul_with = [&](int op, int a, int* other) {
+      if (op < 0) return false;
+      const Op& o = ops_[op];
+      if (o.name != "stablehlo.multiply" || o.operands.size() != 2) return false;
+      if (o.operands[0] == a) *other = o.operands[1];
+      else if (o.operands[1] == a) *other = o.operands[0];
+      else return false;
+      return true;
+    };
+    auto add_of = [&](int op, int a, int b) {
+      if (op < 0) return false;
+      const Op& o = ops_[op];
+      return o.name == "stablehlo.add" && o.operands.size() == 2 &&
+             ((o.operands[0] == a && o.operands[1] == b) || (o.operands[0] == b && o.operands[1] == a));
+    };
+    auto sum_over = [&](int op, int64_t dim) {
+      if (op < 0) return false;
+      const Op& o = ops_[op];
+      double init;
+      return o.name == "stablehlo.reduce" && o.operands.size() == 2 && o.results.size() == 1 &&
+             reduce_body_op(o) == "stablehlo.add" && scalar_of(o.operands[1], &init) && init == 0.0 &&
+             reduce_dims(o) == std::vector<int64_t>{dim} && m_.types[o.operands[0]].dims == xt.dims &&
+             m_.types[o.results[0]].dtype == DType::kF32;
+    };
+    auto rows_bcast = [&](int op) {  // [rows] -> [rows, n] along dim 0
+      if (op < 0) return false;
+      const Op& o = ops_[op];
+      return o.name == "stablehlo.broadcast_in_dim" &&
+             attr_ints(o, {"dims", "broadcast_dimensions"}) == std::vector<int64_t>{0} &&
+             m_.types[o.results[0]].dims == xt.dims;
+    };
+    const double inv_n = 1.0 / double(n);
+    std::set<int> b;  // the backward's ops
+    // dY0 = dy * GB, the broadcast gamma's one reader outside the forward
+    const auto gu = outside(m.GB);
+    int DY = -1;
+    if (gu.size() != 1 || !mul_with(gu[0], m.GB, &DY)) return;
+    if (m_.types[DY].dtype != DType::kF32 || m_.types[DY].dims != xt.dims) return;
+    const int CTY0 = res(gu[0]);
+    b.insert(gu[0]);
+    // dgamma = sum_0(dy * Y0)
+    const auto yu = outside(m.Y0);
+    int o = -1;
+    if (yu.size() != 1 || !mul_with(yu[0], m.Y0, &o) || o != DY) return;
+    b.insert(yu[0]);
+    const int dg_op = single(res(yu[0]));
+    if (!sum_over(dg_op, 0)) return;
+    b.insert(dg_op);
+    const int DG = res(dg_op);
+    // dY0's readers: * RB (into dXC) and * XC (into dR)
+    const auto cu = uniq_users(CTY0);
+    if (cu.size() != 2) return;
+    int CTXC1 = -1, CTRB = -1;
+    for (int u : cu) {
+      if (!mul_with(u, CTY0, &o)) return;
+      if (o == m.RB) CTXC1 = res(u);
+      else if (o == m.XC) CTRB = res(u);
+      b.insert(u);
+    }
+    if (CTXC1 < 0 || CTRB < 0) return;
+    const int dr_op = single(CTRB);
+    if (!sum_over(dr_op, 1)) return;
+    b.insert(dr_op);
+    // dVE = (dR * -0.5) * (R * (R * R))
+    const int a1_op = single(res(dr_op));
+    if (!mul_with(a1_op, res(dr_op), &o) || !IsConstNear(o, -0.5)) return;
+    b.insert(a1_op);
+    const auto ru = outside(m.R);
+    int R2 = -1, R3 = -1;
+    for (int u : ru) {
+      const Op& p = ops_[u];
+      if (p.name == "stablehlo.multiply" && p.operands[0] == m.R && p.operands[1] == m.R) R2 = res(u);
+    }
+    if (R2 < 0 || ru.size() != 2) return;
+    for (int u : ru)
+      if (res(u) != R2 && mul_with(u, m.R, &o) && o == R2) R3 = res(u);
+    if (R3 < 0 || single(R2) != producer_[R3]) return;
+    b.insert(producer_[R2]);
+    b.insert(producer_[R3]);
+    const int ve_op = single(res(a1_op));
+    if (!mul_with(ve_op, res(a1_op), &o) || o != R3 || single(R3) != ve_op) return;
+    b.insert(ve_op);
+    // dS2 = dVE * (1/n), broadcast over the row
+    const int s2_op = single(res(ve_op));
+    if (!mul_with(s2_op, res(ve_op), &o) || !IsConstNear(o, inv_n)) return;
+    b.insert(s2_op);
+    const int b2_op = single(res(s2_op));
+    if (!rows_bcast(b2_op)) return;
+    b.insert(b2_op);
+    // the square's two cotangents: bcast(dS2) * XC, twice
+    const auto b2u = uniq_users(res(b2_op));
+    if (b2u.size() != 2) return;
+    for (int u : b2u) {
+      if (!mul_with(u, res(b2_op), &o) || o != m.XC) return;
+      b.insert(u);
+    }
+    const int M1 = res(b2u[0]), M2 = res(b2u[1]);
+    // dXC = (dY0 RB + M) + M'
+    const int a2_op = single(CTXC1);
+    int Mlast = -1;
+    if (add_of(a2_op, CTXC1, M1)) Mlast = M2;
+    else if (add_of(a2_op, CTXC1, M2)) Mlast = M1;
+    else return;
+    if (single(M1) < 0 || single(M2) < 0) return;
+    b.insert(a2_op);
+    const int xc_op = single(res(a2_op));
+    if (!add_of(xc_op, res(a2_op), Mlast)) return;
+    b.insert(xc_op);
+    const int DXC = res(xc_op);
+    // dXC's readers: its negation (into the mean's cotangent) and the
+    // accumulation into x's cotangent
+    const auto xu = uniq_users(DXC);
+    if (xu.size() != 2) return;
+    int ng_op = -1, acc_op = -1;
+    for (int u : xu) {
+      if (ops_[u].name == "stablehlo.negate") ng_op = u;
+      else if (ops_[u].name == "stablehlo.add") acc_op = u;
+    }
+    if (ng_op < 0 || acc_op < 0) return;
+    b.insert(ng_op);
+    const int dm_op = single(res(ng_op));
+    if (!sum_over(dm_op, 1)) return;
+    b.insert(dm_op);
+    const int s1_op = single(res(dm_op));
+    if (!mul_with(s1_op, res(dm_op), &o) || !IsConstNear(o, inv_n)) return;
+    b.insert(s1_op);
+    const int b3_op = single(res(s1_op));
+    if (!rows_bcast(b3_op)) return;
+    b.insert(b3_op);
+    const int B3 = res(b3_op);
+    const int fin = single(B3);
+    int PREV = -1;
+    if (fin == acc_op) {
+      // no other cotangent of x: dx = dXC + bcast(...)
+      if (!add_of(fin, DXC, B3)) return;
+    } else {
+      const Op& q = ops_[acc_op];
+      PREV = q.operands[0] == DXC ? q.operands[1] : q.operands[0];
+      if (PREV == DXC || m_.types[PREV].dtype != DType::kF32 || m_.types[PREV].dims != xt.dims) return;
+      if (single(res(acc_op)) != fin || !add_of(fin, res(acc_op), B3)) return;
+      b.insert(acc_op);
+    }
+    const int DXT = res(fin);
+    // optional: dbeta = sum_0(dy), the bias gradient sum_0(dx)
+    int DB = -1, CS = -1;
+    if (m.beta >= 0)
+      for (int u : uniq_users(DY))
+        if (sum_over(u, 0) && !b.count(u)) {
+          DB = res(u);
+          b.insert(u);
+          break;
+        }
+    for (int u : uniq_users(DXT))
+      if (sum_over(u, 0)) {
+        CS = res(u);
+        b.insert(u);
+        break;
+      }
+    // every value in between is read by these ops only; the results the
+    // fused backward writes are read after it
+    // (live readers: the cotangents of the constant 1/n factors are formed
+    // and never read)
+    std::set<int> all = m.ops;
+    all.insert(b.begin(), b.end());
+    all.insert(fin);
+    auto read_within = [&](int v) {
+      if (std::count(outputs_.begin(), outputs_.end(), v)) return false;
+      for (int u : live_users(v))
+        if (!all.count(u)) return false;
+      return true;
+    };
+    for (int op : m.ops)
+      for (int r : ops_[op].results)
+        if (op != idx && !read_within(r)) return;
+    for (int op : b) {
+      const int r = res(op);
+      if (r == DG || r == DB || r == CS) {
+        for (int u : live_users(r))
+          if (u <= fin) return;
+        continue;
+      }
+      if (!read_within(r)) return;
+    }
+    if (idx >= fin) return;
+    Fused ff;
+    ff.kind = Fused::kLayerNorm;
+    ff.x = X;
+    ff.gamma = m.gamma;
+    ff.beta = m.beta;
+    ff.eps = m.eps;
+    ff.out_dtype = out_t;
+    ff.in_dtype = DType::kF32;
+    ff.deps = {X, m.gamma};
+    if (m.beta >= 0) ff.deps.push_back(m.beta);
+    fused_[idx] = ff;
+    Fused fb;
+    fb.kind = Fused::kLayerNormBwd;
+    fb.x = X;
+    fb.gamma = m.gamma;
+    fb.dout = DY;
+    fb.dres = PREV;
+    fb.dgamma = DG;
+    fb.dbeta = DB;
+    fb.colsum = CS;
+    fb.eps = m.eps;
+    fb.deps = {X, m.gamma, DY};
+    if (PREV >= 0) fb.deps.push_back(PREV);
+    fused_[fin] = fb;
+    for (int op : m.ops)
+      if (op != idx) absorbed_.insert(op);
+    for (int op : b) absorbed_.insert(op);
+    prog_->patterns.push_back(std::string("layernorm_train(f32 -> ") + DTypeName(out_t) + ", eps=" +
+                              std::to_string(m.eps) + (PREV >= 0 ? ", residual" : "") +
+                              (DB >= 0 ? ", dbeta" : "") + (CS >= 0 ? ", bias gradient" : "") + ")");
   }
 
   // -------------------------------------------------------------- liveness / DCE
@@ -3979,9 +4271,41 @@ class Lowerer {
       st.kind = StepKind::kLayerNorm;
       st.bufs = {x.at(), g, b, d};
       st.i = {int64_t(f.out_dtype), x.numel() / std::max<int64_t>(cols, 1), cols};
+      if (f.in_dtype != f.out_dtype) {
+        st.i.push_back(int64_t(f.in_dtype));
+        st.note = std::string(DTypeName(f.in_dtype)) + " -> " + DTypeName(f.out_dtype);
+      }
       st.f = {f.eps};
       Emit(st);
       SetDenseView(res, d);
+      return;
+    }
+    if (f.kind == Fused::kLayerNormBwd) {
+      const View x = Densify(NeedView(f.x));
+      const View g = Densify(NeedView(f.gamma));
+      const View dy = Densify(NeedView(f.dout));
+      const int64_t cols = x.dims.back(), rows = x.numel() / std::max<int64_t>(cols, 1);
+      BufRef dres{};
+      if (f.dres >= 0) dres = Densify(NeedView(f.dres)).at();
+      const int res = op.results[0];
+      BufRef dx = DestFor(res);
+      // dgamma and dbeta are written together (dbeta to scratch when the
+      // module does not read it)
+      BufRef dg = DestFor(f.dgamma);
+      BufRef db = f.dbeta >= 0 ? DestFor(f.dbeta) : NewTemp(size_t(cols) * 4);
+      BufRef cs = f.colsum >= 0 ? DestFor(f.colsum) : BufRef{};
+      BufRef ws = NewTemp(mk_layernorm_bwd_workspace_bytes(rows, cols));
+      Step st;
+      st.kind = StepKind::kLayerNormBwd;
+      st.bufs = {x.at(), g.at(), dy.at(), dres, dx, dg, db, cs, ws};
+      st.i = {int64_t(DType::kF32), rows, cols};
+      st.f = {f.eps};
+      st.note = std::string(f.dres >= 0 ? "residual" : "no residual") + (f.colsum >= 0 ? ", bias gradient" : "");
+      Emit(st);
+      SetDenseView(res, dx);
+      SetDenseView(f.dgamma, dg);
+      if (f.dbeta >= 0) SetDenseView(f.dbeta, db);
+      if (f.colsum >= 0) SetDenseView(f.colsum, cs);
       return;
     }
     throw std::string("jam: internal: unknown fused pattern");

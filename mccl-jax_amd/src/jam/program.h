@@ -31,7 +31,7 @@ struct BufRef {
 enum class StepKind : uint8_t {
   kGemm, kSdpa, kRowReduce, kArgmax, kLayerNorm, kGelu, kEw, kGather, kScatterAdd,
   kIota, kCopyStrided, kSoftmax, kConvert, kFill, kCopy, kSdpaBwd, kGemmBlas, kSoftmaxXent, kColSum,
-  kGemmSplitK, kEwReduce,
+  kGemmSplitK, kEwReduce, kLayerNormBwd,
 };
 
 const char* StepName(StepKind k);

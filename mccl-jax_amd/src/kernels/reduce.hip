@@ -10,6 +10,7 @@
 #include "mk_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 namespace mk {
@@ -269,12 +270,14 @@ __global__ __launch_bounds__(kBlock) void row_argmax16_kernel(const uint16_t* __
 // kLnMaxPerLane fp32 per lane), two-pass mean/variance, single store.
 constexpr int kLnMaxVecs = 8;  // 8 × 8 bf16 = 64 elements per lane → cols ≤ 4096 in registers
 
-template <typename T>
+// TO: the stored type (T, or bf16 for fp32 rows: four values as one 8-byte
+// store, y rows 8-byte aligned).
+template <typename T, typename TO = T>
 __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restrict__ x,
                                                                const T* __restrict__ gamma,
                                                                const T* __restrict__ beta,
                                                                int64_t rows, int cols, float eps,
-                                                               T* __restrict__ y) {
+                                                               TO* __restrict__ y) {
   using V = typename Vec<T>::V;
   constexpr int N = Vec<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
@@ -313,23 +316,36 @@ __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restri
   const float rstd = 1.f / sqrtf(var + eps);
   const V* gv = reinterpret_cast<const V*>(gamma);
   const V* bv = reinterpret_cast<const V*>(beta);
-  V* yv = reinterpret_cast<V*>(y + row * int64_t(cols));
+  constexpr bool kNarrow = sizeof(TO) < sizeof(T);
+  static_assert(!kNarrow || N == 4, "narrowing store: fp32 rows to bf16");
+  using VO = std::conditional_t<kNarrow, uint2, V>;
+  VO* yv = reinterpret_cast<VO*>(y + row * int64_t(cols));
 #pragma unroll
   for (int k = 0; k < kLnMaxVecs; ++k) {
     int i = lane + k * kWave;
     if (i < nv) {
-      V g{}, b{}, o;
+      V g{}, b{};
+      float o[N];
       if (gamma) g = gv[i];
       if (beta) b = bv[i];
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         float gj = gamma ? to_f32<T>(g.v[j]) : 1.f;
         float bj = beta ? to_f32<T>(b.v[j]) : 0.f;
-        float v = (r[k][j] - mean) * rstd * gj + bj;
-        if constexpr (sizeof(T) == 2) o.v[j] = f32_to_bf16(v);
-        else o.v[j] = v;
+        o[j] = (r[k][j] - mean) * rstd * gj + bj;
       }
-      yv[i] = o;
+      if constexpr (kNarrow) {
+        yv[i] = uint2{uint32_t(f32_to_bf16(o[0])) | (uint32_t(f32_to_bf16(o[1])) << 16),
+                      uint32_t(f32_to_bf16(o[2])) | (uint32_t(f32_to_bf16(o[3])) << 16)};
+      } else {
+        V ov;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+          if constexpr (sizeof(T) == 2) ov.v[j] = f32_to_bf16(o[j]);
+          else ov.v[j] = o[j];
+        }
+        yv[i] = ov;
+      }
     }
   }
 }
@@ -428,12 +444,12 @@ __global__ __launch_bounds__(kBlock) void layernorm_bf16_split_kernel(
 }
 
 // Fallback LayerNorm for any width: three streaming passes over the row.
-template <typename T>
+template <typename T, typename TO = T>
 __global__ __launch_bounds__(kBlock) void layernorm_loop_kernel(const T* __restrict__ x,
                                                                 const T* __restrict__ gamma,
                                                                 const T* __restrict__ beta,
                                                                 int64_t rows, int64_t cols,
-                                                                float eps, T* __restrict__ y) {
+                                                                float eps, TO* __restrict__ y) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -447,12 +463,12 @@ __global__ __launch_bounds__(kBlock) void layernorm_loop_kernel(const T* __restr
     q += d * d;
   }
   const float rstd = 1.f / sqrtf(wave_sum(q) / float(cols) + eps);
-  T* yr = y + row * cols;
+  TO* yr = y + row * cols;
   for (int64_t c = lane; c < cols; c += kWave) {
     float gj = gamma ? to_f32<T>(gamma[c]) : 1.f;
     float bj = beta ? to_f32<T>(beta[c]) : 0.f;
     float v = (to_f32<T>(xr[c]) - mean) * rstd * gj + bj;
-    if constexpr (sizeof(T) == 2) yr[c] = f32_to_bf16(v);
+    if constexpr (sizeof(TO) == 2) yr[c] = f32_to_bf16(v);
     else yr[c] = v;
   }
 }
@@ -614,6 +630,30 @@ extern "C" int mk_layernorm(void* stream, int io_type, int64_t rows, int64_t col
     return fail(MK_ERR_UNSUPPORTED, "mk_layernorm: io_type must be bf16/f32");
   }
   return check_launch("mk_layernorm");
+}
+
+extern "C" int mk_layernorm_typed(void* stream, int in_type, int out_type, int64_t rows, int64_t cols,
+                                  const void* x, const void* gamma, const void* beta, float eps, void* y) {
+  if (in_type == out_type) return mk_layernorm(stream, in_type, rows, cols, x, gamma, beta, eps, y);
+  clear_error();
+  if (in_type != MK_F32 || out_type != MK_BF16)
+    return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_typed: (in, out) must be (bf16, bf16), (f32, f32) or (f32, bf16)");
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_layernorm_typed: bad shape");
+  if (rows == 0) return MK_OK;
+  if (!x || !y) return fail(MK_ERR_INVALID, "mk_layernorm_typed: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(grid_for_rows(rows)), b(kBlock);
+  const float *xp = (const float*)x, *gp = (const float*)gamma, *bp = (const float*)beta;
+  const bool vec = cols % 4 == 0 && cols / 4 <= int64_t(kLnMaxVecs) * kWave && aligned16(x) &&
+                   (reinterpret_cast<uintptr_t>(y) & 7u) == 0 && (!gamma || aligned16(gamma)) &&
+                   (!beta || aligned16(beta));
+  if (vec)
+    hipLaunchKernelGGL((layernorm_reg_kernel<float, uint16_t>), g, b, 0, s, xp, gp, bp, rows, int(cols), eps,
+                       (uint16_t*)y);
+  else
+    hipLaunchKernelGGL((layernorm_loop_kernel<float, uint16_t>), g, b, 0, s, xp, gp, bp, rows, cols, eps,
+                       (uint16_t*)y);
+  return check_launch("mk_layernorm_typed");
 }
 
 extern "C" int mk_softmax_rows(void* stream, int io_type, int64_t rows, int64_t cols,

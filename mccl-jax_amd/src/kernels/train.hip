@@ -1340,6 +1340,7 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
     auto with_kv = [&](auto vect) {
       if (kv == 1) launch(tag, IntC<1>{}, vect);
       else if (kv == 2) launch(tag, IntC<2>{}, vect);
+      else if (kv == 3 && NV == 4 && decltype(vect)::value) launch(tag, IntC<3>{}, vect);  // fp32 rows of 768
       else if (kv <= 4) launch(tag, IntC<4>{}, vect);
       else if constexpr (NV == 4) launch(tag, IntC<8>{}, vect);  // fp32 only: bf16 rows fit KV 4
     };

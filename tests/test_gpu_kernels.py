@@ -186,6 +186,44 @@ def test_layernorm_widths_f32_bf16(K, cols):
     _bf16_close(got, ops.layernorm(xf, gf, bf_), _ln_scale(xf, gf, bf_), exact_frac=0.98)
 
 
+@pytest.mark.parametrize("cols,off", [(1, 0), (100, 0), (768, 0), (1000, 0), (2048, 0), (4096, 0), (768, 3)])
+def test_layernorm_f32_rows_bf16_out(K, cols, off):
+    """fp32 rows, bf16 result (mk_layernorm_typed): the same arithmetic as the
+    fp32 kernel, so each element is the round-to-nearest-even bf16 of the fp32
+    kernel's result (bit for bit), and within bf16 rounding of the oracle.
+    off > 0 starts x and y off their 16-byte alignment (the streaming kernel)."""
+    rng = np.random.default_rng(cols + 7 * off)
+    rows = 8192 if cols == 768 and off == 0 else 23
+    x = (rng.standard_normal((rows, cols)) * 3 + 1).astype(np.float32)
+    g = rng.standard_normal(cols).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32)
+    print(f"case: layernorm f32 -> bf16 [{rows},{cols}] off={off}", flush=True)
+    xd = torch.from_numpy(np.concatenate([np.zeros(off, np.float32), x.ravel()])).cuda()[off:].view(rows, cols)
+    gd, bd = torch.from_numpy(g).cuda(), torch.from_numpy(b).cuda()
+    y16 = K.layernorm(xd, gd, bd, out_dtype=torch.bfloat16)
+    assert y16.dtype == torch.bfloat16 and y16.shape == (rows, cols)
+    y32 = K.layernorm(xd, gd, bd).cpu().numpy()
+    got = host_bf16(y16)
+    if off == 0 and cols % 4 == 0 and cols <= 2048:
+        np.testing.assert_array_equal(got, bf16.to_bf16_bits(y32))
+    want = ops.layernorm(x, g, b)
+    _bf16_close(got, want, np.abs(g)[None, :] * 8 + np.abs(b)[None, :], exact_frac=0.98)
+    # the unaligned output rows take the streaming kernel
+    if off:
+        yb = torch.empty(rows * cols + 1, dtype=torch.bfloat16, device="cuda")[1:].view(rows, cols)
+        rc = K.lib().mk_layernorm_typed(None, 11, 13, rows, cols, K._ptr(xd), K._ptr(gd), K._ptr(bd), 1e-5,
+                                        K._ptr(yb))
+        assert rc == 0
+        np.testing.assert_array_equal(host_bf16(yb), got)
+
+
+def test_layernorm_typed_rejects_bf16_to_f32(K):
+    x = torch.zeros(4, 8, dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros(4, 8, dtype=torch.float32, device="cuda")
+    rc = K.lib().mk_layernorm_typed(None, 13, 11, 4, 8, K._ptr(x), None, None, 1e-5, K._ptr(y))
+    assert rc != 0
+
+
 def test_gelu_c2_full(K):
     x = inputs.c2_gelu()["x"]
     print("case: gelu_tanh [8192,16384] bf16", flush=True)

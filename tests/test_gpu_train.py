@@ -270,7 +270,8 @@ def test_layernorm_bwd_bf16_c5_rows(K):
 
 
 @pytest.mark.parametrize("dtype,rows,cols", [(torch.bfloat16, 8192, 768), (torch.bfloat16, 50, 1000),
-                                             (torch.float32, 37, 1000), (torch.float32, 9, 2048),
+                                             (torch.float32, 8192, 768), (torch.float32, 37, 1000),
+                                             (torch.float32, 9, 2048),
                                              (torch.bfloat16, 5, 100)])
 def test_layernorm_bwd_residual_and_colsum(K, dtype, rows, cols):
     """dx = dres + LN'(dy) in place over dres, with dgamma, dbeta and the

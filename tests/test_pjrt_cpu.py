@@ -137,6 +137,37 @@ def test_compile_jitted_training_step(client):
     assert plan.count("] copy_strided") <= 1
     # bias gradients: sums over the leading (token) dims read in place
     assert "] col_sum" in plan
+    # each LayerNorm (2 per layer and the final one) with its backward: one
+    # forward launch on the fp32 residual stream writing the bf16 operand of
+    # the next product, and one backward launch writing dx (the residual
+    # branch's cotangent added), dgamma, dbeta and, where a projection wrote
+    # x, that projection's bias gradient
+    assert plan.count("pattern layernorm_train(f32 -> bf16, eps=0.000010") == 5
+    assert plan.count("] layernorm (f32 -> bf16)") == 5 and plan.count("] layernorm_bwd (") == 5
+    assert plan.count("] layernorm_bwd (residual, bias gradient)") == 3
+    assert plan.count("] layernorm_bwd (no residual, bias gradient)") == 1  # the final LayerNorm
+    assert plan.count("] layernorm_bwd (residual)") == 1  # the first, over the embeddings
+
+
+def test_layernorm_train_needs_its_whole_backward(client):
+    """The training LayerNorm pattern takes the forward and the backward
+    together: when one rule of the backward differs (here the rsqrt
+    derivative's -0.5 factor of one LayerNorm made -0.25), that LayerNorm
+    keeps the generic path (forward and backward), and the others still
+    match."""
+    from mi355x_pjrt import gpt2, train_hlo
+
+    cfg = gpt2.GPT2Config(n_layer=1, d_model=128, n_head=2, seq=128, batch=2, vocab=257)
+    text = train_hlo.gpt2_train_step(cfg)
+    plan, _, _ = _plan(client, text)
+    assert plan.count("] layernorm_bwd (") == 3
+    cst = "stablehlo.constant dense<-5.000000000e-01> : tensor<f32>"
+    assert text.count(cst) == 3
+    i = text.index(cst)
+    bad = text[:i] + cst.replace("-5.0", "-2.5") + text[i + len(cst):]
+    plan, _, _ = _plan(client, bad)
+    assert plan.count("] layernorm_bwd (") == 2 and plan.count("pattern layernorm_train") == 2
+    assert plan.count("] layernorm (f32 -> bf16)") == 2
 
 
 def test_sdpa_backward_needs_the_row_broadcast(client):
