@@ -59,7 +59,10 @@ int mk_device_count(void);
  * (MK_F16 returns MK_ERR_UNSUPPORTED); c_type ∈ {MK_F32, MK_BF16, MK_F16};
  * accumulation is always fp32 (true fp32 MFMA for MK_F32 operands).
  * epilogue: 0 none, 1 +bias, 2 +bias then max(.,0).  bias has c_type, may be
- * NULL when epilogue == 0.
+ * NULL when epilogue == 0.  5 / 6: as 1 / 2 with an fp32 bias whatever c_type
+ * (an fp32 product plus fp32 bias that the module only reads rounded to
+ * bf16, written as bf16: the bias added to the fp32 accumulator, one
+ * rounding).
  * ---------------------------------------------------------------------- */
 int mk_gemm(void* stream, int ab_type, int c_type,
             int64_t batch, int64_t M, int64_t N, int64_t K,
@@ -418,6 +421,14 @@ size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
                      const void* gamma, const void* dy, const void* dres, float eps, void* dx,
                      float* dgamma, float* dbeta, float* dx_colsum, void* workspace);
+
+/* mk_layernorm_bwd that also stores dx_bf16 (may be NULL; fp32 rows only):
+ * the bf16 rounding (RNE) of each dx element, the operand of the bf16
+ * products that read this gradient next (the convert node of the
+ * reference's graph folded into the same pass). */
+int mk_layernorm_bwd_typed(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                           const void* gamma, const void* dy, const void* dres, float eps, void* dx,
+                           void* dx_bf16, float* dgamma, float* dbeta, float* dx_colsum, void* workspace);
 
 /* Softmax cross-entropy over rows of logits, loss and gradient together:
  *   lse_r = log sum_j exp(x[r, j]);  loss_rows[r] = lse_r - x[r, labels[r]]

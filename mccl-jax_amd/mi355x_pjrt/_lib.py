@@ -69,6 +69,7 @@ SIGNATURES = {
     "mk_col_sum": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
     "mk_layernorm_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "mk_layernorm_bwd": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P]),
+    "mk_layernorm_bwd_typed": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P]),
     "mk_gelu_tanh_bwd_colsum": (_I, [_P, _I, _I64, _I64, _P, _P, _P, _P, _P]),
     "mk_gemm_splitk_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "mk_gemm_splitk": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),

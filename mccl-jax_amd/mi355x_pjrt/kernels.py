@@ -100,6 +100,8 @@ def gemm(a, b, out_dtype=None, bias=None, relu=False, out=None, stream=None):
     o3 = out.unsqueeze(0) if out.dim() == 2 else out
     b_bs = b3.stride(0) if b3.shape[0] == batch and b.dim() == 3 else 0
     epi = 0 if bias is None else (2 if relu else 1)
+    if bias is not None and bias.dtype == torch.float32 and out_dtype != torch.float32:
+        epi |= 4  # an fp32 bias added before the narrowing store
     rc = lib().mk_gemm(
         _stream(stream), mk_dtype(a.dtype), mk_dtype(out_dtype), batch, M, N, K,
         _ptr(a3), a3.stride(0), a3.stride(1), a3.stride(2),
@@ -374,7 +376,8 @@ def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=t
     rc = lib().mk_gemm_splitk_typed(_stream(stream), mk_dtype(a.dtype), mk_dtype(out.dtype), M, N, Kd, _ptr(a),
                                     a.stride(0), a.stride(1), _ptr(b), b.stride(0), b.stride(1), _ptr(out),
                                     out.stride(0), splits, _ptr(ws), _ptr(bias),
-                                    0 if bias is None else (2 if relu else 1))
+                                    0 if bias is None else ((2 if relu else 1) |
+                                                            (4 if bias.dtype != out.dtype else 0)))
     _check(rc, "mk_gemm_splitk_typed")
     return out
 
@@ -457,9 +460,10 @@ def col_sum(x, out=None, workspace=None, stream=None):
 
 
 def layernorm_bwd(x, gamma, dy, eps=1e-5, dx=None, dgamma=None, dbeta=None, workspace=None, want_params=True,
-                  dres=None, want_colsum=False, stream=None):
+                  dres=None, want_colsum=False, dx_bf16=None, stream=None):
     """(dx, dgamma, dbeta[, dx_colsum]) of LayerNorm over the last axis (fp32
-    dgamma/dbeta/colsum); dx = LN'(dy) + dres when dres is given."""
+    dgamma/dbeta/colsum); dx = LN'(dy) + dres when dres is given; dx_bf16
+    (fp32 rows) also receives dx rounded to bf16."""
     _require_cuda(x, dy)
     cols = x.shape[-1]
     rows = x.numel() // cols
@@ -469,10 +473,11 @@ def layernorm_bwd(x, gamma, dy, eps=1e-5, dx=None, dgamma=None, dbeta=None, work
         dbeta = torch.empty(cols, dtype=torch.float32, device=x.device) if dbeta is None else dbeta
     colsum = torch.empty(cols, dtype=torch.float32, device=x.device) if want_colsum else None
     ws = _ws(lib().mk_layernorm_bwd_workspace_bytes(rows, cols), x.device, workspace)
-    rc = lib().mk_layernorm_bwd(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(gamma), _ptr(dy),
-                                _ptr(dres), float(eps), _ptr(dx), _ptr(dgamma if want_params else None),
-                                _ptr(dbeta if want_params else None), _ptr(colsum), _ptr(ws))
-    _check(rc, "mk_layernorm_bwd")
+    rc = lib().mk_layernorm_bwd_typed(_stream(stream), mk_dtype(x.dtype), rows, cols, _ptr(x), _ptr(gamma),
+                                      _ptr(dy), _ptr(dres), float(eps), _ptr(dx), _ptr(dx_bf16),
+                                      _ptr(dgamma if want_params else None), _ptr(dbeta if want_params else None),
+                                      _ptr(colsum), _ptr(ws))
+    _check(rc, "mk_layernorm_bwd_typed")
     return (dx, dgamma, dbeta, colsum) if want_colsum else (dx, dgamma, dbeta)
 
 

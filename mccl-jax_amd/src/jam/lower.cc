@@ -381,6 +381,7 @@ struct Fused {
   // layernorm backward (x, gamma, dout = dy): the residual cotangent added to
   // dx, and the dgamma / dbeta / bias-gradient values it also writes (-1: none)
   int dres = -1, dgamma = -1, dbeta = -1, colsum = -1;
+  std::vector<int> dx_bf16;  // converts of dx to bf16 whose results it writes too
 };
 
 class Lowerer {
@@ -444,7 +445,8 @@ class Lowerer {
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
       case StepKind::kLayerNorm: return {3};
-      case StepKind::kLayerNormBwd: return {4, 5, 6, 7, 8};
+      case StepKind::kLayerNormBwd: return s.bufs.size() > 9 ? std::vector<size_t>{4, 5, 6, 7, 8, 9}
+                                                             : std::vector<size_t>{4, 5, 6, 7, 8};
       case StepKind::kGelu: return {1};
       case StepKind::kEw: {
         std::vector<size_t> w;
@@ -2446,12 +2448,16 @@ class Lowerer {
           b.insert(u);
           break;
         }
-    for (int u : uniq_users(DXT))
-      if (sum_over(u, 0)) {
+    std::vector<int> dx16;  // dx rounded to bf16 for the products that read it next
+    for (int u : uniq_users(DXT)) {
+      if (CS < 0 && sum_over(u, 0)) {
         CS = res(u);
         b.insert(u);
-        break;
+      } else if (ops_[u].name == "stablehlo.convert" && m_.types[res(u)].dtype == DType::kBF16 &&
+                 !std::count(outputs_.begin(), outputs_.end(), res(u))) {
+        dx16.push_back(res(u));
       }
+    }
     // every value in between is read by these ops only; the results the
     // fused backward writes are read after it
     // (live readers: the cotangents of the constant 1/n factors are formed
@@ -2498,6 +2504,7 @@ class Lowerer {
     fb.dgamma = DG;
     fb.dbeta = DB;
     fb.colsum = CS;
+    fb.dx_bf16 = dx16;
     fb.eps = m.eps;
     fb.deps = {X, m.gamma, DY};
     if (PREV >= 0) fb.deps.push_back(PREV);
@@ -2505,6 +2512,7 @@ class Lowerer {
     for (int op : m.ops)
       if (op != idx) absorbed_.insert(op);
     for (int op : b) absorbed_.insert(op);
+    for (int c : dx16) absorbed_.insert(producer_[c]);
     prog_->patterns.push_back(std::string("layernorm_train(f32 -> ") + DTypeName(out_t) + ", eps=" +
                               std::to_string(m.eps) + (PREV >= 0 ? ", residual" : "") +
                               (DB >= 0 ? ", dbeta" : "") + (CS >= 0 ? ", bias gradient" : "") + ")");
@@ -3828,9 +3836,13 @@ class Lowerer {
       }
     }
     // an f32 product every reader rounds to bf16 is written in bf16 (one
-    // rounding of the fp32 accumulator, as the module's convert does)
+    // rounding of the fp32 accumulator, as the module's convert does); with
+    // a matched fp32 bias (+ ReLU) the epilogue adds it to the fp32
+    // accumulator before that rounding (mk_gemm epilogue 5 / 6), which is
+    // the module's f32 add followed by its convert
     bool narrow_out = false;
-    if (pad == 0 && !epi && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res, false)) {
+    if (pad == 0 && ct == DType::kF32 && at == DType::kBF16 && NarrowOnly(res, false) &&
+        (!epi || m_.types[epi->bias].dtype == DType::kF32)) {
       narrow_out = true;
       d = NewTemp(size_t(m_.types[res].numel()) * 2);
     }
@@ -3839,7 +3851,7 @@ class Lowerer {
     if (epi) {
       const View& bv = NeedView(epi->bias);
       st.bufs.push_back(Densify(bv).at());
-      epilogue = epi->relu ? 2 : 1;
+      epilogue = (epi->relu ? 2 : 1) | (narrow_out ? 4 : 0);
     }
     st.i = {int64_t(at), int64_t(narrow_out ? DType::kBF16 : ct), B, M, N, K, a_bs, a_ms, a_ks, b_bs, b_ks, b_ns,
             M * N, c_pitch, epilogue};
@@ -4301,8 +4313,15 @@ class Lowerer {
       st.i = {int64_t(DType::kF32), rows, cols};
       st.f = {f.eps};
       st.note = std::string(f.dres >= 0 ? "residual" : "no residual") + (f.colsum >= 0 ? ", bias gradient" : "");
+      BufRef d16{};
+      if (!f.dx_bf16.empty()) {
+        d16 = DestFor(f.dx_bf16[0]);
+        st.bufs.push_back(d16);
+        st.note += ", bf16 copy";
+      }
       Emit(st);
       SetDenseView(res, dx);
+      for (int c : f.dx_bf16) SetDenseView(c, d16);
       SetDenseView(f.dgamma, dg);
       if (f.dbeta >= 0) SetDenseView(f.dbeta, db);
       if (f.colsum >= 0) SetDenseView(f.colsum, cs);

@@ -65,7 +65,7 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
 //   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
 //   layernorm bufs x,g,b,y      i out_type,rows,cols[,in_type]  f eps
-//   layernorm_bwd bufs x,g,dy,dres,dx,dgamma,dbeta,dx_colsum,workspace  i io_type,rows,cols  f eps
+//   layernorm_bwd bufs x,g,dy,dres,dx,dgamma,dbeta,dx_colsum,workspace[,dx_bf16]  i io_type,rows,cols  f eps
 //   gelu     bufs x,y           i io_type,n
 //   ew       bufs in...,out...  i rank,dims[6],n_inputs,(out_reg,out_type) per output  prog  strides[6n]
 //                               types[n]  f consts  (batch > 1: bufs of each instance in turn)
@@ -121,8 +121,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
       if (i.size() > 3) return mk_layernorm_typed(st, int(i[3]), int(i[0]), i[1], i[2], P(0), P(1), P(2), s.f[0], P(3));
       return mk_layernorm(st, int(i[0]), i[1], i[2], P(0), P(1), P(2), s.f[0], P(3));
     case StepKind::kLayerNormBwd:
-      return mk_layernorm_bwd(st, int(i[0]), i[1], i[2], P(0), P(1), P(2), P(3), s.f[0], P(4),
-                              static_cast<float*>(P(5)), static_cast<float*>(P(6)), static_cast<float*>(P(7)), P(8));
+      return mk_layernorm_bwd_typed(st, int(i[0]), i[1], i[2], P(0), P(1), P(2), P(3), s.f[0], P(4),
+                                    s.bufs.size() > 9 ? P(9) : nullptr, static_cast<float*>(P(5)),
+                                    static_cast<float*>(P(6)), static_cast<float*>(P(7)), P(8));
     case StepKind::kGelu:
       return mk_gelu_tanh(st, int(i[0]), i[1], P(0), P(1));
     case StepKind::kEw: {

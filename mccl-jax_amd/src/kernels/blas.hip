@@ -138,10 +138,11 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
     }
     const int64_t e = i * 4, m = e / N, n = e % N;
     if (epilogue != 0) {
+      const bool bias16 = BF16 && (epilogue & 4) == 0;  // | 4: an fp32 bias with bf16 C
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        a.v[j] += BF16 ? bf16_to_f32(static_cast<const uint16_t*>(bias)[n + j]) : static_cast<const float*>(bias)[n + j];
-        if (epilogue == 2) a.v[j] = fmaxf(a.v[j], 0.f);
+        a.v[j] += bias16 ? bf16_to_f32(static_cast<const uint16_t*>(bias)[n + j]) : static_cast<const float*>(bias)[n + j];
+        if ((epilogue & 3) == 2) a.v[j] = fmaxf(a.v[j], 0.f);
       }
     }
     if constexpr (BF16)

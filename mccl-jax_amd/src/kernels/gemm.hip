@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
     const int64_t n = n0 + wn * 64 + j * 32 + c;
     if (n >= p.N) continue;
     float bias = 0.f;
-    if (p.epilogue != 0) bias = load_as_f32(p.bias, n, p.c_type);
+    if (p.epilogue != 0) bias = load_as_f32(p.bias, n, (p.epilogue & 4) ? MK_F32 : p.c_type);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
         if (m >= p.M) continue;
         float v = acc[i][j][r];
         if (p.epilogue != 0) v += bias;
-        if (p.epilogue == 2) v = fmaxf(v, 0.f);
+        if ((p.epilogue & 3) == 2) v = fmaxf(v, 0.f);
         const int64_t off = bz * p.c_bs + m * p.c_ms + n;
         if (cbytes == 4) reinterpret_cast<float*>(Cb)[off] = v;
         else store_from_f32(Cb, off, p.c_type, v);
@@ -264,6 +264,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
     }
   }
 }
+
+// 0 none, 1 + bias, 2 + bias then ReLU; 5 / 6: 1 / 2 with an fp32 bias
+// whatever C's type
+inline bool epilogue_ok(int e) { return e == 0 || e == 1 || e == 2 || e == 5 || e == 6; }
 
 template <typename T>
 int launch_gemm(hipStream_t s, const GemmArgs& a, int64_t batch, bool a_kc, bool b_kc) {
@@ -291,7 +295,7 @@ extern "C" int mk_gemm(void* stream, int ab_type, int c_type, int64_t batch, int
     return fail(MK_ERR_UNSUPPORTED, "mk_gemm: ab_type must be bf16 or f32");
   if (c_type != MK_F32 && c_type != MK_BF16 && c_type != MK_F16)
     return fail(MK_ERR_UNSUPPORTED, "mk_gemm: c_type must be f32, bf16 or f16");
-  if (epilogue < 0 || epilogue > 2) return fail(MK_ERR_INVALID, "mk_gemm: epilogue must be 0, 1 or 2");
+  if (!epilogue_ok(epilogue)) return fail(MK_ERR_INVALID, "mk_gemm: epilogue must be 0, 1, 2, 5 or 6");
   if (epilogue != 0 && !bias) return fail(MK_ERR_INVALID, "mk_gemm: epilogue needs bias");
   if (batch == 0 || M == 0 || N == 0) return MK_OK;
   if (!A || !B || !C) return fail(MK_ERR_INVALID, "mk_gemm: null pointer");
@@ -342,7 +346,7 @@ extern "C" int mk_gemm_splitk_typed(void* stream, int ab_type, int c_type, int64
   clear_error();
   if (splits < 1 || K < 0 || M < 0 || N < 0) return fail(MK_ERR_INVALID, "mk_gemm_splitk: bad shape or splits");
   if (c_type != MK_F32 && c_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_splitk: c_type must be f32 or bf16");
-  if (epilogue < 0 || epilogue > 2) return fail(MK_ERR_INVALID, "mk_gemm_splitk: epilogue must be 0, 1 or 2");
+  if (!epilogue_ok(epilogue)) return fail(MK_ERR_INVALID, "mk_gemm_splitk: epilogue must be 0, 1, 2, 5 or 6");
   if (epilogue != 0 && !bias) return fail(MK_ERR_INVALID, "mk_gemm_splitk: epilogue needs bias");
   if (splits == 1 || M == 0 || N == 0)
     return mk_gemm(stream, ab_type, c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms, bias,

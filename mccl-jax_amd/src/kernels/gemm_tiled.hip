@@ -72,7 +72,7 @@ struct TiledGemm {
   int64_t a_bs, b_bs, c_bs;   // batch strides (elements)
   uint32_t a_bytes, b_bytes;  // bytes addressable from one batch's A / B base
   int tiles_m, tiles_n;
-  int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU
+  int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU; | 4: the bias is fp32
   int c_type;
   int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
                               // stored as 16-byte chunks / element by element, 4 / 5 staged fp32 rows
@@ -220,11 +220,12 @@ __device__ inline uint2 pack4(const float (&v)[4]) {
 // columns < N only)
 template <int CT>
 __device__ inline void finish4(const TiledGemm& p, int64_t n, float (&v)[4]) {
-  if (p.epilogue == 0) return;
+  if ((p.epilogue & 3) == 0) return;
+  const bool bias32 = (p.epilogue & 4) != 0;  // an fp32 bias whatever C's type
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    v[q] += n + q < p.N ? load_as_f32(p.bias, n + q, CT) : 0.f;
-    if (p.epilogue == 2) v[q] = fmaxf(v[q], 0.f);
+    v[q] += n + q < p.N ? (bias32 ? static_cast<const float*>(p.bias)[n + q] : load_as_f32(p.bias, n + q, CT)) : 0.f;
+    if ((p.epilogue & 3) == 2) v[q] = fmaxf(v[q], 0.f);
   }
 }
 

@@ -300,6 +300,7 @@ struct LnBwdArgs {
   const void* dy;
   const void* dres;
   void* dx;
+  uint16_t* dx16;  // fp32 rows: the bf16 rounding of dx as well (may be null)
   int64_t rows, rpb;
   int cols;
   float eps;
@@ -422,11 +423,20 @@ __global__ __launch_bounds__(64 * W) void layernorm_bwd_kernel(const LnBwdArgs a
       }
       const int c0 = (k * 64 + lane) * NV;
       if constexpr (VEC) {
-        if (c0 < cols) *reinterpret_cast<Raw*>(dx + r * cols + c0) = RV::pack(o);
+        if (c0 < cols) {
+          *reinterpret_cast<Raw*>(dx + r * cols + c0) = RV::pack(o);
+          if constexpr (sizeof(T) == 4 && NV == 4) {
+            if (a.dx16)
+              *reinterpret_cast<uint2*>(a.dx16 + r * cols + c0) = uint2{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+          }
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j)
-          if (c0 + j < cols) stf<T>(dx, r * cols + c0 + j, o[j]);
+          if (c0 + j < cols) {
+            stf<T>(dx, r * cols + c0 + j, o[j]);
+            if (sizeof(T) == 4 && a.dx16) a.dx16[r * cols + c0 + j] = f32_to_bf16(o[j]);
+          }
       }
     }
   };
@@ -1280,9 +1290,35 @@ extern "C" size_t mk_layernorm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
   return size_t(3 * align256(kLnBwdBlocks * cols * 4));
 }
 
+namespace {
+int layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x, const void* gamma,
+                  const void* dy, const void* dres, float eps, void* dx, void* dx_bf16, float* dgamma, float* dbeta,
+                  float* dx_colsum, void* workspace);
+}
+
 extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
                                 const void* gamma, const void* dy, const void* dres, float eps, void* dx,
                                 float* dgamma, float* dbeta, float* dx_colsum, void* workspace) {
+  return layernorm_bwd(stream, io_type, rows, cols, x, gamma, dy, dres, eps, dx, nullptr, dgamma, dbeta, dx_colsum,
+                       workspace);
+}
+
+extern "C" int mk_layernorm_bwd_typed(void* stream, int io_type, int64_t rows, int64_t cols, const void* x,
+                                      const void* gamma, const void* dy, const void* dres, float eps, void* dx,
+                                      void* dx_bf16, float* dgamma, float* dbeta, float* dx_colsum,
+                                      void* workspace) {
+  if (dx_bf16 && io_type != MK_F32) {
+    clear_error();
+    return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd_typed: a bf16 copy of dx is for fp32 rows");
+  }
+  return layernorm_bwd(stream, io_type, rows, cols, x, gamma, dy, dres, eps, dx, dx_bf16, dgamma, dbeta, dx_colsum,
+                       workspace);
+}
+
+namespace {
+int layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t cols, const void* x, const void* gamma,
+                  const void* dy, const void* dres, float eps, void* dx, void* dx_bf16, float* dgamma, float* dbeta,
+                  float* dx_colsum, void* workspace) {
   clear_error();
   if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_layernorm_bwd: bad shape");
   if (cols > kLnBwdMaxCols) return fail(MK_ERR_UNSUPPORTED, "mk_layernorm_bwd: rows of at most 2048 columns");
@@ -1307,6 +1343,7 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
   char* ws = static_cast<char*>(workspace);
   LnBwdArgs a;
   a.x = x; a.gamma = gamma; a.dy = dy; a.dres = dres; a.dx = dx;
+  a.dx16 = static_cast<uint16_t*>(dx_bf16);
   a.rows = rows; a.rpb = rpb; a.cols = int(cols); a.eps = eps;
   a.part_g = dgamma ? reinterpret_cast<float*>(ws) : nullptr;
   a.part_b = dgamma ? reinterpret_cast<float*>(ws + slab) : nullptr;
@@ -1344,7 +1381,8 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
       else if (kv <= 4) launch(tag, IntC<4>{}, vect);
       else if constexpr (NV == 4) launch(tag, IntC<8>{}, vect);  // fp32 only: bf16 rows fit KV 4
     };
-    if (rows_are_vectors<T>(cols, {x, dy, dres, dx})) with_kv(std::true_type{});
+    if (rows_are_vectors<T>(cols, {x, dy, dres, dx}) && (reinterpret_cast<uintptr_t>(dx_bf16) & 7u) == 0)
+      with_kv(std::true_type{});
     else with_kv(std::false_type{});
     };
     if (io_type == MK_BF16) dispatch(uint16_t{});
@@ -1363,6 +1401,7 @@ extern "C" int mk_layernorm_bwd(void* stream, int io_type, int64_t rows, int64_t
   }
   return n ? col_final(s, n, parts, outs, nb, cols) : MK_OK;
 }
+}  // namespace
 
 namespace {
 // The cross-entropy kernels for rows `ld_in` / `ld_out` elements apart.

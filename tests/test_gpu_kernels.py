@@ -767,6 +767,28 @@ def test_gemm_splitk_uneven_slices(K, out_dtype):
             assert _bf16_out_ok(gb, want, norm), (M, N, Kd)
 
 
+@pytest.mark.parametrize("relu", [False, True])
+def test_gemm_fp32_bias_bf16_out(K, relu):
+    """Epilogue 5 / 6: an fp32 bias (+ ReLU) added to the fp32 accumulator and
+    rounded once to bf16 -- bit for bit the fp32-output product with the same
+    bias, rounded to bf16 afterwards (the module's f32 add then convert), on
+    the tiled kernel, the general kernel and the split-K sum."""
+    rng = np.random.default_rng(55 + relu)
+    for (M, N, Kd, splits) in [(512, 2304, 768, 1), (40, 72, 96, 1), (256, 768, 2048, 4)]:
+        print(f"case: fp32 bias bf16 out M={M} N={N} K={Kd} splits={splits} relu={relu}", flush=True)
+        a = dev_bf16(bf16.to_bf16_bits(rng.standard_normal((M, Kd)).astype(np.float32)))
+        b = dev_bf16(bf16.to_bf16_bits(rng.standard_normal((Kd, N)).astype(np.float32)))
+        bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32) * 3).cuda()
+        if splits == 1:
+            ref = K.gemm(a, b, out_dtype=torch.float32, bias=bias, relu=relu)
+            got = K.gemm(a, b, out_dtype=torch.bfloat16, bias=bias, relu=relu)
+        else:
+            ref = K.gemm_splitk(a, b, splits, out_dtype=torch.float32, bias=bias, relu=relu)
+            got = K.gemm_splitk(a, b, splits, out_dtype=torch.bfloat16, bias=bias, relu=relu)
+        assert got.dtype == torch.bfloat16
+        assert torch.equal(got, ref.bfloat16()), (M, N, Kd, splits)
+
+
 # ------------------------------------------------------------------ a6 iota, a12 layout, misc
 def test_iota_convert_fill_copy(K):
     it = K.iota((3, 5, 7), 1).cpu().numpy()

@@ -282,9 +282,12 @@ def test_layernorm_bwd_residual_and_colsum(K, dtype, rows, cols):
     dy = torch.randn(rows, cols, generator=g).to(dtype)
     dres = torch.randn(rows, cols, generator=g).to(dtype)
     buf = dres.cuda()
+    d16 = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda") if dtype == torch.float32 else None
     dx, dgam, dbet, csum = K.layernorm_bwd(x.cuda(), gamma.cuda(), dy.cuda(), 1e-5, dx=buf, dres=buf,
-                                           want_colsum=True)
+                                           want_colsum=True, dx_bf16=d16)
     assert dx.data_ptr() == buf.data_ptr()
+    if d16 is not None:  # the bf16 copy is the RNE rounding of the stored fp32 dx
+        assert torch.equal(d16.cpu(), dx.cpu().bfloat16())
     xr = x.double().requires_grad_(True)
     gr = gamma.double().requires_grad_(True)
     br = torch.zeros(cols, dtype=torch.float64, requires_grad=True)

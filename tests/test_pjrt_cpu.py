@@ -141,12 +141,17 @@ def test_compile_jitted_training_step(client):
     # forward launch on the fp32 residual stream writing the bf16 operand of
     # the next product, and one backward launch writing dx (the residual
     # branch's cotangent added), dgamma, dbeta and, where a projection wrote
-    # x, that projection's bias gradient
+    # x, that projection's bias gradient, and dx rounded to bf16 where the
+    # products that read it next take it so
     assert plan.count("pattern layernorm_train(f32 -> bf16, eps=0.000010") == 5
     assert plan.count("] layernorm (f32 -> bf16)") == 5 and plan.count("] layernorm_bwd (") == 5
-    assert plan.count("] layernorm_bwd (residual, bias gradient)") == 3
-    assert plan.count("] layernorm_bwd (no residual, bias gradient)") == 1  # the final LayerNorm
+    assert plan.count("] layernorm_bwd (residual, bias gradient, bf16 copy)") == 3
+    assert plan.count("] layernorm_bwd (no residual, bias gradient, bf16 copy)") == 1  # the final LayerNorm
     assert plan.count("] layernorm_bwd (residual)") == 1  # the first, over the embeddings
+    # the QKV projection (+ fp32 bias) is only read in bf16 (the attention's
+    # operands): written in bf16 by its epilogue, no conversion pass
+    assert plan.count("] gemm (1x256x384x128 -> bf16)") == 2
+    assert "convert chain (1 instr, 1 inputs), 3 independent instances" not in plan
 
 
 def test_layernorm_train_needs_its_whole_backward(client):
