@@ -382,6 +382,16 @@ int mk_add_layernorm(void* stream, int64_t rows, int64_t cols, const void* a, co
                      const void* bias, const void* gamma, const void* beta, float eps, void* sum_out,
                      void* y);
 
+/* mk_add_layernorm with input and output types: (bf16, bf16) is
+ * mk_add_layernorm; for fp32 rows (a, b, gamma, beta, sum_out fp32, y fp32
+ * or bf16) sum = a + b (one fp32 add, no bias: b already holds it) is stored
+ * and normalised as mk_layernorm_typed normalises a row -- the residual
+ * update of a pre-LN block in an fp32 module, then the next LayerNorm whose
+ * result feeds a bf16 product. */
+int mk_add_layernorm_typed(void* stream, int in_type, int out_type, int64_t rows, int64_t cols, const void* a,
+                           const void* b, const void* bias, const void* gamma, const void* beta, float eps,
+                           void* sum_out, void* y);
+
 /* pre = x + bias[c] (bf16, one rounding) and y = gelu_tanh(pre) (as
  * mk_gelu_tanh on the stored pre) in one pass: the MLP's bias add and
  * activation (elementwise.mm add + the GELU chain).  pre may alias x. */

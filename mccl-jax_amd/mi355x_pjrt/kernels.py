@@ -416,15 +416,18 @@ def add_rows(a, b=None, bias=None, out=None, stream=None):
     return out
 
 
-def add_layernorm(a, b, bias, gamma, beta, eps=1e-5, sum_out=None, y=None, stream=None):
-    """(a + b + bias, LayerNorm of that sum) for bf16 [rows, cols] a, b."""
+def add_layernorm(a, b, bias, gamma, beta, eps=1e-5, sum_out=None, y=None, out_dtype=None, stream=None):
+    """(a + b + bias, LayerNorm of that sum) for [rows, cols] a, b: bf16 rows
+    (mk_add_layernorm), or fp32 rows without a bias and an fp32 or bf16
+    LayerNorm (mk_add_layernorm_typed)."""
     _require_cuda(a)
     rows, cols = a.shape
+    out_dtype = a.dtype if out_dtype is None else out_dtype
     sum_out = torch.empty_like(a) if sum_out is None else sum_out
-    y = torch.empty_like(a) if y is None else y
-    rc = lib().mk_add_layernorm(_stream(stream), rows, cols, _ptr(a), _ptr(b), _ptr(bias), _ptr(gamma), _ptr(beta),
-                                float(eps), _ptr(sum_out), _ptr(y))
-    _check(rc, "mk_add_layernorm")
+    y = torch.empty(a.shape, dtype=out_dtype, device=a.device) if y is None else y
+    rc = lib().mk_add_layernorm_typed(_stream(stream), mk_dtype(a.dtype), mk_dtype(y.dtype), rows, cols, _ptr(a),
+                                      _ptr(b), _ptr(bias), _ptr(gamma), _ptr(beta), float(eps), _ptr(sum_out), _ptr(y))
+    _check(rc, "mk_add_layernorm_typed")
     return sum_out, y
 
 

@@ -114,6 +114,10 @@ hipEvent_t DeviceContext::TakeEventLocked() {
 
 void DeviceContext::DropEventLocked(hipEvent_t ev) {
   if (!ev) return;
+  // one event marks every block of a flush: the last holder releases it
+  auto r = event_refs_.find(ev);
+  if (r != event_refs_.end() && --r->second > 0) return;
+  if (r != event_refs_.end()) event_refs_.erase(r);
   // an event no stream can still be waiting on is recycled; a pending one is
   // destroyed (HIP releases it once the recorded work has passed)
   if (hipEventQuery(ev) == hipSuccess && idle_events_.size() < 256)
@@ -122,11 +126,34 @@ void DeviceContext::DropEventLocked(hipEvent_t ev) {
     (void)hipEventDestroy(ev);
 }
 
+void DeviceContext::FlushFreedLocked() {
+  if (freed_.empty()) return;
+  // every use of these blocks is queued on the compute stream (uploads into
+  // them were ordered before their readers): one event after all of it,
+  // recorded now, serves every block freed since the last flush (one
+  // marker in the stream instead of one per block; later than each Free,
+  // so never too early)
+  hipEvent_t ev = TakeEventLocked();
+  if (ev && hipEventRecord(ev, stream_) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipEventDestroy(ev);
+    ev = nullptr;
+  }
+  if (!ev) {  // no event: wait here rather than risk a transfer-stream race
+    (void)hipStreamSynchronize(stream_);
+  } else {
+    event_refs_[ev] = int(freed_.size());
+  }
+  for (const Freed& f : freed_) free_.emplace(f.cls, Slot{f.p, ev});
+  freed_.clear();
+}
+
 void* DeviceContext::Alloc(size_t bytes, std::string* error) {
   if (bytes == 0) return nullptr;
   const size_t cls = SizeClass(bytes);
   {
     std::lock_guard<std::mutex> lk(mu_);
+    FlushFreedLocked();
     auto it = free_.find(cls);
     if (it != free_.end()) {
       Slot slot = it->second;
@@ -171,20 +198,11 @@ void DeviceContext::Free(void* p) {
   std::lock_guard<std::mutex> lk(mu_);
   auto it = live_.find(p);
   if (it == live_.end()) return;  // not ours: ignore
-  // every use of the block so far is queued on the compute stream (uploads
-  // into it were ordered before their readers): mark the point after them
-  hipEvent_t ev = TakeEventLocked();
-  if (ev && hipEventRecord(ev, stream_) != hipSuccess) {
-    (void)hipGetLastError();
-    (void)hipEventDestroy(ev);
-    ev = nullptr;
-  }
-  if (!ev) {  // no event: wait here rather than risk a transfer-stream race
-    (void)hipStreamSynchronize(stream_);
-  }
+  // cached once the next Alloc (or Trim) records the event that marks the
+  // end of its queued uses (FlushFreedLocked)
   DropEventLocked(it->second.reuse_after);
   stats_.bytes_in_use -= int64_t(it->second.cls);
-  free_.emplace(it->second.cls, Slot{p, ev});
+  freed_.push_back(Freed{p, it->second.cls});
   live_.erase(it);
 }
 
@@ -214,11 +232,18 @@ void DeviceContext::Trim() {
   std::vector<hipEvent_t> events;
   {
     std::lock_guard<std::mutex> lk(mu_);
+    FlushFreedLocked();
     for (auto& kv : free_) {
       release.push_back(kv.second.p);
-      if (kv.second.reuse_after) events.push_back(kv.second.reuse_after);
-      stats_.bytes_reserved -= int64_t(kv.first);
+      // a shared event is destroyed once, by its last holder
+      if (kv.second.reuse_after) {
+        auto r = event_refs_.find(kv.second.reuse_after);
+        if (r != event_refs_.end() && --r->second > 0) continue;
+        if (r != event_refs_.end()) event_refs_.erase(r);
+        events.push_back(kv.second.reuse_after);
+      }
     }
+    for (auto& kv : free_) stats_.bytes_reserved -= int64_t(kv.first);
     free_.clear();
   }
   if (release.empty()) return;

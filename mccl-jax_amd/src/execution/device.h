@@ -7,9 +7,11 @@
 //  - memory is device HBM (hipMalloc), not CPU-visible unified memory;
 //  - kernels, device-to-device and device-to-host copies go to the compute
 //    stream, so a block returned to the pool can be handed out again at once:
-//    any later compute-stream use is ordered after the earlier use.  Free
-//    records an event on the compute stream; a DMA on the transfer stream
-//    into a reused block first waits for that event (OrderUploadInto), so an
+//    any later compute-stream use is ordered after the earlier use.  The
+//    next Alloc after a run of Frees records one event on the compute stream
+//    for all of those blocks (a step dropping hundreds of outputs adds one
+//    marker to the stream, not hundreds); a DMA on the transfer stream into
+//    a reused block first waits for that event (OrderUploadInto), so an
 //    upload never overwrites memory a queued kernel still reads;
 //  - host-to-device uploads go to a second (transfer) stream, so they never
 //    wait for kernels already queued.  Data is first copied into pinned
@@ -118,10 +120,17 @@ class DeviceContext {
     size_t cls;
     hipEvent_t reuse_after;
   };
+  struct Freed {
+    void* p;
+    size_t cls;
+  };
   hipEvent_t TakeEventLocked();
-  void DropEventLocked(hipEvent_t ev);  // ev may still be pending
+  void DropEventLocked(hipEvent_t ev);  // ev may still be pending; one holder's release
+  void FlushFreedLocked();              // freed_ -> free_ behind one new event
   std::multimap<size_t, Slot> free_;    // size class -> cached block
   std::map<void*, Live> live_;          // block -> size class, reuse event
+  std::vector<Freed> freed_;            // freed since the last flush (not yet reusable)
+  std::map<hipEvent_t, int> event_refs_;  // blocks holding each shared event
   std::vector<hipEvent_t> idle_events_;
   MemoryStats stats_;
 

@@ -378,6 +378,7 @@ struct Fused {
   float eps = 0;
   DType out_dtype = DType::kInvalid;
   DType in_dtype = DType::kInvalid;
+  int add_a = -1, add_b = -1;  // x = add_a + add_b computed and stored by the LayerNorm step
   // layernorm backward (x, gamma, dout = dy): the residual cotangent added to
   // dx, and the dgamma / dbeta / bias-gradient values it also writes (-1: none)
   int dres = -1, dgamma = -1, dbeta = -1, colsum = -1;
@@ -444,7 +445,7 @@ class Lowerer {
       case StepKind::kGemmSplitK: return {2, 3};
       case StepKind::kRowReduce: return {1};
       case StepKind::kArgmax: return {1, 2};
-      case StepKind::kLayerNorm: return {3};
+      case StepKind::kLayerNorm: return s.bufs.size() > 4 ? std::vector<size_t>{3, 5} : std::vector<size_t>{3};
       case StepKind::kLayerNormBwd: return s.bufs.size() > 9 ? std::vector<size_t>{4, 5, 6, 7, 8, 9}
                                                              : std::vector<size_t>{4, 5, 6, 7, 8};
       case StepKind::kGelu: return {1};
@@ -2484,6 +2485,31 @@ class Lowerer {
       if (!read_within(r)) return;
     }
     if (idx >= fin) return;
+    // x = a + b, the residual update (fp32 operands read in place, not
+    // layout views): added and stored by the forward launch itself, which
+    // writes x for the backward and the next update; every reader of x
+    // outside the forward comes after it
+    int add_op = -1;
+    {
+      const int p = producer_[X];
+      auto in_place = [&](int v) {
+        if (m_.types[v].dtype != DType::kF32 || m_.types[v].dims != xt.dims) return false;
+        const Op* q = prod(v);
+        if (!q) return true;  // a module argument
+        static const char* views[] = {"stablehlo.broadcast_in_dim", "stablehlo.reshape", "stablehlo.transpose",
+                                      "stablehlo.slice", "stablehlo.concatenate", "stablehlo.convert"};
+        for (const char* n : views)
+          if (q->name == n) return false;
+        return true;
+      };
+      if (p >= 0 && ops_[p].name == "stablehlo.add" && ops_[p].operands.size() == 2 && !fused_.count(p) &&
+          !absorbed_.count(p) && in_place(ops_[p].operands[0]) && in_place(ops_[p].operands[1])) {
+        bool later = true;
+        for (int u : live_users(X))
+          if (!m.ops.count(u) && u < idx) later = false;
+        if (later) add_op = p;
+      }
+    }
     Fused ff;
     ff.kind = Fused::kLayerNorm;
     ff.x = X;
@@ -2493,6 +2519,12 @@ class Lowerer {
     ff.out_dtype = out_t;
     ff.in_dtype = DType::kF32;
     ff.deps = {X, m.gamma};
+    if (add_op >= 0) {
+      ff.add_a = ops_[add_op].operands[0];
+      ff.add_b = ops_[add_op].operands[1];
+      ff.deps = {ff.add_a, ff.add_b, m.gamma};
+      absorbed_.insert(add_op);
+    }
     if (m.beta >= 0) ff.deps.push_back(m.beta);
     fused_[idx] = ff;
     Fused fb;
@@ -2514,7 +2546,8 @@ class Lowerer {
     for (int op : b) absorbed_.insert(op);
     for (int c : dx16) absorbed_.insert(producer_[c]);
     prog_->patterns.push_back(std::string("layernorm_train(f32 -> ") + DTypeName(out_t) + ", eps=" +
-                              std::to_string(m.eps) + (PREV >= 0 ? ", residual" : "") +
+                              std::to_string(m.eps) + (add_op >= 0 ? ", input added" : "") +
+                              (PREV >= 0 ? ", residual" : "") +
                               (DB >= 0 ? ", dbeta" : "") + (CS >= 0 ? ", bias gradient" : "") + ")");
   }
 
@@ -4272,7 +4305,8 @@ class Lowerer {
       return;
     }
     if (f.kind == Fused::kLayerNorm) {
-      const View x = Densify(NeedView(f.x));
+      const bool add = f.add_a >= 0;
+      const View x = Densify(NeedView(add ? f.add_a : f.x));
       BufRef g{}, b{};
       if (f.gamma >= 0) g = Densify(NeedView(f.gamma)).at();
       if (f.beta >= 0) b = Densify(NeedView(f.beta)).at();
@@ -4283,12 +4317,22 @@ class Lowerer {
       st.kind = StepKind::kLayerNorm;
       st.bufs = {x.at(), g, b, d};
       st.i = {int64_t(f.out_dtype), x.numel() / std::max<int64_t>(cols, 1), cols};
-      if (f.in_dtype != f.out_dtype) {
+      if (f.in_dtype != f.out_dtype || add) {
         st.i.push_back(int64_t(f.in_dtype));
         st.note = std::string(DTypeName(f.in_dtype)) + " -> " + DTypeName(f.out_dtype);
       }
+      BufRef xs{};
+      if (add) {
+        // x = a + b written by the step (bufs 4, 5: b and x)
+        const View b2 = Densify(NeedView(f.add_b));
+        xs = DestFor(f.x);
+        st.bufs.push_back(b2.at());
+        st.bufs.push_back(xs);
+        st.note += ", input added";
+      }
       st.f = {f.eps};
       Emit(st);
+      if (add) SetDenseView(f.x, xs);
       SetDenseView(res, d);
       return;
     }

@@ -64,7 +64,7 @@ void* Resolve(const BufRef& b, const Frame& f) {
 //   sdpa     bufs Q,K,V,O[,lse] i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
 //   row_reduce bufs x,y         i in_type,out_type,op,rows,cols  f init
 //   argmax   bufs x,values,idx  i in_type,is_min,rows,cols,index_type,has_values
-//   layernorm bufs x,g,b,y      i out_type,rows,cols[,in_type]  f eps
+//   layernorm bufs x,g,b,y[,x2,xsum]  i out_type,rows,cols[,in_type]  f eps (x2: x + x2 normalised, stored to xsum)
 //   layernorm_bwd bufs x,g,dy,dres,dx,dgamma,dbeta,dx_colsum,workspace[,dx_bf16]  i io_type,rows,cols  f eps
 //   gelu     bufs x,y           i io_type,n
 //   ew       bufs in...,out...  i rank,dims[6],n_inputs,(out_reg,out_type) per output  prog  strides[6n]
@@ -118,6 +118,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
     case StepKind::kArgmax:
       return mk_row_argmax(st, int(i[0]), int(i[1]), i[2], i[3], P(0), i[5] ? P(1) : nullptr, int(i[4]), P(2));
     case StepKind::kLayerNorm:
+      if (s.bufs.size() > 4)  // x = bufs 0 + bufs 4, stored to bufs 5
+        return mk_add_layernorm_typed(st, int(i[3]), int(i[0]), i[1], i[2], P(0), P(4), nullptr, P(1), P(2), s.f[0],
+                                      P(5), P(3));
       if (i.size() > 3) return mk_layernorm_typed(st, int(i[3]), int(i[0]), i[1], i[2], P(0), P(1), P(2), s.f[0], P(3));
       return mk_layernorm(st, int(i[0]), i[1], i[2], P(0), P(1), P(2), s.f[0], P(3));
     case StepKind::kLayerNormBwd:

@@ -271,15 +271,19 @@ __global__ __launch_bounds__(kBlock) void row_argmax16_kernel(const uint16_t* __
 constexpr int kLnMaxVecs = 8;  // 8 × 8 bf16 = 64 elements per lane → cols ≤ 4096 in registers
 
 // TO: the stored type (T, or bf16 for fp32 rows: four values as one 8-byte
-// store, y rows 8-byte aligned).
-template <typename T, typename TO = T>
+// store, y rows 8-byte aligned).  ADD (fp32 rows): the row is x + x2 (one
+// fp32 add per element, the residual stream's update), stored to xsum and
+// normalised.
+template <typename T, typename TO = T, bool ADD = false>
 __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restrict__ x,
                                                                const T* __restrict__ gamma,
                                                                const T* __restrict__ beta,
                                                                int64_t rows, int cols, float eps,
-                                                               TO* __restrict__ y) {
+                                                               TO* __restrict__ y, const T* __restrict__ x2 = nullptr,
+                                                               T* __restrict__ xsum = nullptr) {
   using V = typename Vec<T>::V;
   constexpr int N = Vec<T>::N;
+  static_assert(!ADD || sizeof(T) == 4, "the fused residual add is for fp32 rows");
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -292,6 +296,12 @@ __global__ __launch_bounds__(kBlock) void layernorm_reg_kernel(const T* __restri
     int i = lane + k * kWave;
     if (i < nv) {
       V a = xv[i];
+      if constexpr (ADD) {
+        const V b = reinterpret_cast<const V*>(x2 + row * int64_t(cols))[i];
+#pragma unroll
+        for (int j = 0; j < N; ++j) a.v[j] = a.v[j] + b.v[j];
+        reinterpret_cast<V*>(xsum + row * int64_t(cols))[i] = a;
+      }
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         r[k][j] = to_f32<T>(a.v[j]);
@@ -444,16 +454,25 @@ __global__ __launch_bounds__(kBlock) void layernorm_bf16_split_kernel(
 }
 
 // Fallback LayerNorm for any width: three streaming passes over the row.
+// With x2 (fp32 rows): the row is x + x2, written to xsum first (the passes
+// then read that row back; each lane reads only what it wrote).
 template <typename T, typename TO = T>
 __global__ __launch_bounds__(kBlock) void layernorm_loop_kernel(const T* __restrict__ x,
                                                                 const T* __restrict__ gamma,
                                                                 const T* __restrict__ beta,
                                                                 int64_t rows, int64_t cols,
-                                                                float eps, TO* __restrict__ y) {
+                                                                float eps, TO* __restrict__ y,
+                                                                const T* x2 = nullptr, T* xsum = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * cols;
+  if constexpr (sizeof(T) == 4) {
+    if (x2) {
+      for (int64_t c = lane; c < cols; c += kWave) xsum[row * cols + c] = xr[c] + x2[row * cols + c];
+      xr = xsum + row * cols;
+    }
+  }
   float s = 0.f;
   for (int64_t c = lane; c < cols; c += kWave) s += to_f32<T>(xr[c]);
   const float mean = wave_sum(s) / float(cols);
@@ -654,6 +673,44 @@ extern "C" int mk_layernorm_typed(void* stream, int in_type, int out_type, int64
     hipLaunchKernelGGL((layernorm_loop_kernel<float, uint16_t>), g, b, 0, s, xp, gp, bp, rows, cols, eps,
                        (uint16_t*)y);
   return check_launch("mk_layernorm_typed");
+}
+
+extern "C" int mk_add_layernorm_typed(void* stream, int in_type, int out_type, int64_t rows, int64_t cols,
+                                      const void* a, const void* b, const void* bias, const void* gamma,
+                                      const void* beta, float eps, void* sum_out, void* y) {
+  if (in_type == MK_BF16 && out_type == MK_BF16)
+    return mk_add_layernorm(stream, rows, cols, a, b, bias, gamma, beta, eps, sum_out, y);
+  clear_error();
+  if (in_type != MK_F32 || (out_type != MK_F32 && out_type != MK_BF16))
+    return fail(MK_ERR_UNSUPPORTED, "mk_add_layernorm_typed: (in, out) must be (bf16, bf16), (f32, f32) or (f32, bf16)");
+  if (bias) return fail(MK_ERR_UNSUPPORTED, "mk_add_layernorm_typed: no bias for fp32 rows (add it to b)");
+  if (rows < 0 || cols <= 0) return fail(MK_ERR_INVALID, "mk_add_layernorm_typed: bad shape");
+  if (rows == 0) return MK_OK;
+  if (!a || !b || !sum_out || !y) return fail(MK_ERR_INVALID, "mk_add_layernorm_typed: null pointer");
+  hipStream_t s = as_stream(stream);
+  dim3 g(grid_for_rows(rows)), blk(kBlock);
+  const float *ap = (const float*)a, *bp = (const float*)b, *gp = (const float*)gamma, *tp = (const float*)beta;
+  float* sp = (float*)sum_out;
+  const uintptr_t ymask = out_type == MK_BF16 ? 7u : 15u;
+  const bool vec = cols % 4 == 0 && cols / 4 <= int64_t(kLnMaxVecs) * kWave && aligned16(a) && aligned16(b) &&
+                   aligned16(sum_out) && (reinterpret_cast<uintptr_t>(y) & ymask) == 0 && (!gamma || aligned16(gamma)) &&
+                   (!beta || aligned16(beta));
+  if (out_type == MK_BF16) {
+    if (vec)
+      hipLaunchKernelGGL((layernorm_reg_kernel<float, uint16_t, true>), g, blk, 0, s, ap, gp, tp, rows, int(cols), eps,
+                         (uint16_t*)y, bp, sp);
+    else
+      hipLaunchKernelGGL((layernorm_loop_kernel<float, uint16_t>), g, blk, 0, s, ap, gp, tp, rows, cols, eps,
+                         (uint16_t*)y, bp, sp);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((layernorm_reg_kernel<float, float, true>), g, blk, 0, s, ap, gp, tp, rows, int(cols), eps,
+                         (float*)y, bp, sp);
+    else
+      hipLaunchKernelGGL((layernorm_loop_kernel<float, float>), g, blk, 0, s, ap, gp, tp, rows, cols, eps, (float*)y,
+                         bp, sp);
+  }
+  return check_launch("mk_add_layernorm_typed");
 }
 
 extern "C" int mk_softmax_rows(void* stream, int io_type, int64_t rows, int64_t cols,

@@ -194,6 +194,32 @@ def test_add_layernorm(K, rows, cols):
     assert torch.equal(s1, a)
 
 
+@pytest.mark.parametrize("rows,cols,off", [(8192, 768, 0), (37, 100, 0), (5, 4096, 0), (3, 768, 1)])
+def test_add_layernorm_f32_rows(K, rows, cols, off):
+    """fp32 rows (mk_add_layernorm_typed): the stored sum is the fp32 a + b
+    bit for bit, and the LayerNorm (fp32 or bf16) is mk_layernorm_typed of
+    that sum bit for bit (same kernel arithmetic; off = 1 starts the operands
+    off their 16-byte alignment, the streaming kernel)."""
+    g = torch.Generator().manual_seed(rows * 5 + cols + off)
+
+    def dev(t):
+        flat = torch.zeros(t.numel() + off, dtype=t.dtype)
+        flat[off:] = t.reshape(-1)
+        return flat.cuda()[off:].view(t.shape)
+    a, b = (dev(torch.randn(rows, cols, generator=g) * 2) for _ in range(2))
+    gamma = dev(1 + 0.1 * torch.randn(cols, generator=g))
+    beta = dev(0.1 * torch.randn(cols, generator=g))
+    for od in (torch.float32, torch.bfloat16):
+        s, y = K.add_layernorm(a, b, None, gamma, beta, 1e-5, out_dtype=od)
+        assert s.dtype == torch.float32 and y.dtype == od
+        assert torch.equal(s, a + b)
+        if off == 0:  # (the plain LayerNorm of the aligned sum takes the other kernel when off > 0)
+            assert torch.equal(y, K.layernorm(s, gamma, beta, 1e-5, out_dtype=od))
+        want = torch.nn.functional.layer_norm(_f64(s), (cols,), _f64(gamma), _f64(beta), 1e-5)
+        tol = 2 ** -7 if od == torch.bfloat16 else 1e-5
+        assert float((_f64(y) - want).abs().max()) <= tol * (float(want.abs().max()) + 1)
+
+
 @pytest.mark.parametrize("rows,cols", [(8192, 3072), (33, 100)])
 def test_bias_gelu(K, rows, cols):
     """pre equals mk_add_rows and y equals mk_gelu_tanh of pre, bit for bit

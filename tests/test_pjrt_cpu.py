@@ -144,7 +144,10 @@ def test_compile_jitted_training_step(client):
     # x, that projection's bias gradient, and dx rounded to bf16 where the
     # products that read it next take it so
     assert plan.count("pattern layernorm_train(f32 -> bf16, eps=0.000010") == 5
-    assert plan.count("] layernorm (f32 -> bf16)") == 5 and plan.count("] layernorm_bwd (") == 5
+    assert plan.count("] layernorm (f32 -> bf16") == 5 and plan.count("] layernorm_bwd (") == 5
+    # the residual updates x + proj(...) are added by the LayerNorm that
+    # reads them (the embedding sum, a broadcast view, is not)
+    assert plan.count("] layernorm (f32 -> bf16, input added)") == 4
     assert plan.count("] layernorm_bwd (residual, bias gradient, bf16 copy)") == 3
     assert plan.count("] layernorm_bwd (no residual, bias gradient, bf16 copy)") == 1  # the final LayerNorm
     assert plan.count("] layernorm_bwd (residual)") == 1  # the first, over the embeddings
@@ -172,7 +175,7 @@ def test_layernorm_train_needs_its_whole_backward(client):
     bad = text[:i] + cst.replace("-5.0", "-2.5") + text[i + len(cst):]
     plan, _, _ = _plan(client, bad)
     assert plan.count("] layernorm_bwd (") == 2 and plan.count("pattern layernorm_train") == 2
-    assert plan.count("] layernorm (f32 -> bf16)") == 2
+    assert plan.count("] layernorm (f32 -> bf16") == 2
 
 
 def test_sdpa_backward_needs_the_row_broadcast(client):
