@@ -71,6 +71,18 @@ int mk_gemm(void* stream, int ab_type, int c_type,
             void* C, int64_t c_bs, int64_t c_ms,
             const void* bias, int epilogue);
 
+/* mk_gemm (batch 1, epilogue 0, 1 or 5) whose epilogue also writes
+ * Y[m][n] = bf16(gelu_tanh(C[m][n] as stored)) -- mk_gelu_tanh's function of
+ * the stored (for bf16 C: rounded) value -- rows y_ms apart: the MLP's
+ * up-projection, its bias and its activation in one pass (the reference's
+ * dot_general, add and GELU chain, linalg.mm:47-105 and elementwise.mm).
+ * Runs only on the tiled kernel: bf16 operands with 16-byte aligned rows,
+ * M, N >= 128, K >= 64, c_type bf16 (C and Y rows 16-byte aligned) or f32
+ * (C rows 16-byte, Y rows 8-byte aligned); MK_ERR_UNSUPPORTED otherwise. */
+int mk_gemm_bias_gelu(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K, const void* A,
+                      int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* C,
+                      int64_t c_ms, const void* bias, int epilogue, void* Y, int64_t y_ms);
+
 /* Split-K form of mk_gemm for fp32 outputs with few output tiles and a long
  * contraction (the weight gradients dW = Xᵀ dY of the training step: the
  * dot_general of linalg.mm:47-105 with the token axis contracted).  The K

@@ -357,6 +357,22 @@ def gemm_blas(a, b, out=None, out_dtype=None, alpha=1.0, beta=0.0, stream=None):
     return out
 
 
+def gemm_bias_gelu(a, b, bias=None, out_dtype=torch.bfloat16, out=None, y=None, stream=None):
+    """(C, Y): C = a @ b (+ bias) in out_dtype and Y = bf16 gelu_tanh(C as
+    stored), one launch (mk_gemm_bias_gelu); a [M, K], b [K, N] 2-D views."""
+    _require_cuda(a, b)
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = torch.empty(M, N, dtype=out_dtype, device=a.device) if out is None else out
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=a.device) if y is None else y
+    epi = 0 if bias is None else (5 if bias.dtype == torch.float32 and out.dtype != torch.float32 else 1)
+    rc = lib().mk_gemm_bias_gelu(_stream(stream), mk_dtype(a.dtype), mk_dtype(out.dtype), M, N, Kd, _ptr(a),
+                                 a.stride(0), a.stride(1), _ptr(b), b.stride(0), b.stride(1), _ptr(out),
+                                 out.stride(0), _ptr(bias), epi, _ptr(y), y.stride(0))
+    _check(rc, "mk_gemm_bias_gelu")
+    return out, y
+
+
 def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=torch.float32, bias=None,
                 relu=False):
     """out = a @ b (+ bias)(ReLU) with the contraction cut into `splits`

@@ -370,9 +370,10 @@ struct Fused {
   int x = -1;
   bool is_min = false;
   int red_op = -1;
-  // gemm epilogue
+  // gemm epilogue (gelu_out: a bf16 GELU of the result the epilogue also writes)
   int dot = -1, bias = -1;
   bool relu = false;
+  int gelu_out = -1;
   // layernorm (in_dtype: x, gamma and beta; out_dtype: the result)
   int gamma = -1, beta = -1;
   float eps = 0;
@@ -436,7 +437,7 @@ class Lowerer {
   // run.cc.
   static std::vector<size_t> WrittenBufs(const Step& s) {
     switch (s.kind) {
-      case StepKind::kGemm: return {2};
+      case StepKind::kGemm: return s.bufs.size() > 4 ? std::vector<size_t>{2, 4} : std::vector<size_t>{2};
       case StepKind::kSdpa: return s.bufs.size() > 4 ? std::vector<size_t>{3, 4} : std::vector<size_t>{3};
       case StepKind::kSdpaBwd: return {6, 7, 8, 9};
       case StepKind::kGemmBlas: return {2};
@@ -750,6 +751,10 @@ class Lowerer {
       for (size_t i = 0; i < ops_.size(); ++i)
         if (ops_[i].name == "stablehlo.add" && !fused_.count(int(i)) && !absorbed_.count(int(i)))
           TryMatchGemmEpilogue(int(i));
+    if (opts_.fuse_gemm_epilogue && opts_.fuse_gelu)
+      for (size_t i = 0; i < ops_.size(); ++i)
+        if (ops_[i].name == "stablehlo.convert" && !fused_.count(int(i)) && !absorbed_.count(int(i)))
+          TryMatchGemmGelu(int(i));
     if (opts_.fuse_gelu)
       for (size_t i = 0; i < ops_.size(); ++i)
         if (ops_[i].name == "stablehlo.multiply" && !fused_.count(int(i))) TryMatchGelu(int(i));
@@ -2036,6 +2041,84 @@ class Lowerer {
   // jax.nn.gelu(approximate=True) lowers it (X^3 = X * (X * X)); either order
   // of every commutative op.  X is f32 (optionally convert(bf16)); a
   // convert-to-bf16 consumer is folded in so the kernel rounds once.
+  // x when v = gelu_tanh(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+  // in either association of the 0.5 factor, x * (0.5 (1 + t)) (jax.nn.gelu)
+  // or (0.5 x) (1 + t), with x^3 = x (x x); else -1
+  int GeluInput(int v) const {
+    auto tanh_input = [&](int t) {
+      int xr = -1;
+      if (!is(t, "stablehlo.tanh")) return -1;
+      Comm(prod(t)->operands[0], "stablehlo.multiply", [&](int cc, int u) {
+        if (!IsConstNear(cc, 0.7978845608028654, 1e-6)) return false;
+        return Comm(u, "stablehlo.add", [&](int x, int w) {
+          return Comm(w, "stablehlo.multiply", [&](int c2, int c3) {
+            if (!IsConstNear(c2, 0.044715, 1e-6)) return false;
+            return Comm(c3, "stablehlo.multiply", [&](int a, int b) {
+              if (a != x) return false;
+              return Comm(b, "stablehlo.multiply", [&](int pp, int qq) {
+                if (pp != x || qq != x) return false;
+                xr = x;
+                return true;
+              });
+            });
+          });
+        });
+      });
+      return xr;
+    };
+    int res = -1;
+    Comm(v, "stablehlo.multiply", [&](int x, int h) {  // x * (0.5 (1 + t))
+      return Comm(h, "stablehlo.multiply", [&](int half, int t1) {
+        if (!IsConstNear(half, 0.5)) return false;
+        return Comm(t1, "stablehlo.add", [&](int one, int t) {
+          if (!IsConstNear(one, 1.0) || tanh_input(t) != x) return false;
+          res = x;
+          return true;
+        });
+      });
+    });
+    if (res >= 0) return res;
+    Comm(v, "stablehlo.multiply", [&](int hx, int t1) {  // (0.5 x) (1 + t)
+      int x = -1;
+      if (!Comm(hx, "stablehlo.multiply", [&](int half, int xx) {
+            if (!IsConstNear(half, 0.5)) return false;
+            x = xx;
+            return true;
+          }))
+        return false;
+      return Comm(t1, "stablehlo.add", [&](int one, int t) {
+        if (!IsConstNear(one, 1.0) || tanh_input(t) != x) return false;
+        res = x;
+        return true;
+      });
+    });
+    return res;
+  }
+
+  // A product with a matched bias whose fp32 result x feeds gelu_tanh(x)
+  // rounded to bf16 for the next product (the MLP's up-projection): the
+  // GEMM's epilogue writes that bf16 value as a side output
+  // (mk_gemm_bias_gelu, mk_gelu_tanh's function of the stored x), so the
+  // forward chain is never materialised.  Its ops stay: the backward reads x
+  // (and recomputes from it whatever else it needs).  Whether the side
+  // output is taken is decided at lowering, where the operand layouts are
+  // known (LowerDot); otherwise the convert lowers as before.
+  void TryMatchGemmGelu(int cv) {
+    const Op& c = ops_[cv];
+    if (c.operands.size() != 1 || c.results.size() != 1) return;
+    const int M = c.operands[0], CV = c.results[0];
+    if (m_.types[CV].dtype != DType::kBF16 || m_.types[M].dtype != DType::kF32) return;
+    if (std::count(outputs_.begin(), outputs_.end(), M) || std::count(outputs_.begin(), outputs_.end(), CV)) return;
+    const auto mu = live_users(M);
+    if (mu.empty() || std::any_of(mu.begin(), mu.end(), [&](int u) { return u != cv; })) return;
+    const int X = GeluInput(M);
+    if (X < 0 || m_.types[X].rank() != 2 || m_.types[X].dtype != DType::kF32) return;
+    auto it = fused_.find(producer_[X]);
+    if (it == fused_.end() || it->second.kind != Fused::kGemmEpi || it->second.relu || it->second.gelu_out >= 0) return;
+    it->second.gelu_out = CV;
+    prog_->patterns.push_back("gemm+bias+gelu(bf16 side output)");
+  }
+
   void TryMatchGelu(int mul_idx) {
     const int M = ops_[mul_idx].results[0];
     if (m_.types[M].dtype != DType::kF32) return;
@@ -3259,6 +3342,7 @@ class Lowerer {
   // one shape becomes one batched launch (BatchIndependentEwSteps) instead
   // of a launch in front of every product.
   std::set<int> hoisted_;
+  std::set<int> preset_;  // ops whose result an earlier step already wrote (a GEMM's GELU side output)
   void HoistInputConverts() {
     if (!opts_.fuse_elementwise) return;
     for (size_t i = 0; i < ops_.size(); ++i) {
@@ -3286,7 +3370,7 @@ class Lowerer {
     out_written_.assign(outputs_.size(), false);
     HoistInputConverts();
     for (size_t i = 0; i < ops_.size(); ++i) {
-      if (!live_[i] || hoisted_.count(int(i))) continue;
+      if (!live_[i] || hoisted_.count(int(i)) || preset_.count(int(i))) continue;
       auto f = fused_.find(int(i));
       if (f != fused_.end()) {
         EmitFused(int(i), f->second);
@@ -3890,7 +3974,27 @@ class Lowerer {
             M * N, c_pitch, epilogue};
     st.note = std::to_string(B) + "x" + std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
     if (narrow_out) st.note += " -> bf16";
+    // the GELU side output (TryMatchGemmGelu) where mk_gemm_bias_gelu takes
+    // these layouts: the tiled kernel's operands (bf16, a unit stride, the
+    // other a multiple of 8, 16-byte aligned bases) and fp32 C rows of whole
+    // 16-byte chunks
+    BufRef gelu_buf{};
+    if (epi && epi->gelu_out >= 0 && !narrow_out && pad == 0 && B == 1 && at == DType::kBF16 &&
+        ct == DType::kF32 && M >= 128 && N >= 128 && K >= 64 && N % 4 == 0 && c_pitch == N) {
+      const bool a_ok = (a_ks == 1 && a_ms % 8 == 0 && a_ms >= K) || (a_ms == 1 && a_ks % 8 == 0 && a_ks >= M);
+      const bool b_ok = (b_ks == 1 && b_ns % 8 == 0 && b_ns >= K) || (b_ns == 1 && b_ks % 8 == 0 && b_ks >= N);
+      if (a_ok && b_ok && lv.at().offset % 16 == 0 && rv.at().offset % 16 == 0 && d.offset % 16 == 0) {
+        gelu_buf = NewTemp(size_t(M * N) * 2);
+        st.bufs.push_back(gelu_buf);
+        st.i.push_back(N);
+        st.note += " + gelu side output";
+      }
+    }
     Emit(st);
+    if (gelu_buf.space == Space::kArena) {
+      SetDenseView(epi->gelu_out, gelu_buf);
+      preset_.insert(producer_[epi->gelu_out]);
+    }
     if (narrow_out) {
       View nv;
       nv.buf = d;

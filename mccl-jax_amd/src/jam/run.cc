@@ -58,7 +58,8 @@ void* Resolve(const BufRef& b, const Frame& f) {
 }
 
 // Step encodings (written by lower.cc):
-//   gemm     bufs A,B,C[,bias]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
+//   gemm     bufs A,B,C[,bias[,Y]]  i ab_type,c_type,batch,M,N,K,a_bs,a_ms,a_ks,b_bs,b_ks,b_ns,c_bs,c_ms,epilogue
+//                               [,y_ms]  (Y: bf16 gelu_tanh of C, mk_gemm_bias_gelu)
 //   gemm_blas bufs A,B,C        i as gemm (no epilogue)
 //   gemm_splitk bufs A,B,C,workspace[,bias]  i ab_type,M,N,K,a_ms,a_ks,b_ks,b_ns,c_ms,splits,epilogue
 //   sdpa     bufs Q,K,V,O[,lse] i B,H,Sq,Sk,D,q_bs,q_hs,q_ss,k_bs,k_hs,k_ss,v_bs,v_hs,v_ss,o_bs,o_hs,o_ss,causal  f scale
@@ -91,6 +92,9 @@ int RunStep(const Step& s, const Frame& f, hipStream_t stream) {
   const auto& i = s.i;
   switch (s.kind) {
     case StepKind::kGemm:
+      if (s.bufs.size() > 4)  // + the GELU side output (bufs 4, rows i[15] apart)
+        return mk_gemm_bias_gelu(st, int(i[0]), int(i[1]), i[3], i[4], i[5], P(0), i[7], i[8], P(1), i[10], i[11],
+                                 P(2), i[13], P(3), int(i[14]), P(4), i[15]);
       return mk_gemm(st, int(i[0]), int(i[1]), i[2], i[3], i[4], i[5], P(0), i[6], i[7], i[8], P(1), i[9],
                      i[10], i[11], P(2), i[12], i[13], s.bufs.size() > 3 ? P(3) : nullptr, int(i[14]));
     case StepKind::kSdpa:

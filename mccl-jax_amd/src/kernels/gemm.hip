@@ -285,6 +285,28 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, int64_t batch, bool a_kc, bool
 
 using namespace mk;
 
+extern "C" int mk_gemm_bias_gelu(void* stream, int ab_type, int c_type, int64_t M, int64_t N, int64_t K,
+                                 const void* A, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks,
+                                 int64_t b_ns, void* C, int64_t c_ms, const void* bias, int epilogue, void* Y,
+                                 int64_t y_ms) {
+  clear_error();
+  if (M < 0 || N < 0 || K < 0) return fail(MK_ERR_INVALID, "mk_gemm_bias_gelu: negative shape");
+  if (ab_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_bias_gelu: ab_type must be bf16");
+  if (c_type != MK_BF16 && c_type != MK_F32)
+    return fail(MK_ERR_UNSUPPORTED, "mk_gemm_bias_gelu: c_type must be bf16 or f32");
+  if (epilogue != 0 && epilogue != 1 && epilogue != 5)
+    return fail(MK_ERR_INVALID, "mk_gemm_bias_gelu: epilogue must be 0, 1 or 5");
+  if (epilogue != 0 && !bias) return fail(MK_ERR_INVALID, "mk_gemm_bias_gelu: epilogue needs bias");
+  if (M == 0 || N == 0) return MK_OK;
+  if (!A || !B || !C || !Y) return fail(MK_ERR_INVALID, "mk_gemm_bias_gelu: null pointer");
+  const int r = gemm_tiled(as_stream(stream), c_type, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, C, 0, c_ms,
+                           bias, epilogue | kEpiGeluAux, 0, Y, y_ms);
+  if (r >= 0) return r;
+  return fail(MK_ERR_UNSUPPORTED,
+              "mk_gemm_bias_gelu: needs the tiled kernel (bf16 operands with 16-byte aligned rows, M, N >= 128, "
+              "K >= 64) and C and Y rows of whole 16-byte chunks");
+}
+
 extern "C" int mk_gemm(void* stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N,
                        int64_t K, const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks,
                        const void* B, int64_t b_bs, int64_t b_ks, int64_t b_ns, void* C,

@@ -72,7 +72,10 @@ struct TiledGemm {
   int64_t a_bs, b_bs, c_bs;   // batch strides (elements)
   uint32_t a_bytes, b_bytes;  // bytes addressable from one batch's A / B base
   int tiles_m, tiles_n;
-  int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU; | 4: the bias is fp32
+  int epilogue;               // 0 none, 1 + bias, 2 + bias then ReLU; | 4: the bias is fp32;
+                              // | kEpiGeluAux: aux = bf16 gelu_tanh of each stored value
+  uint16_t* aux;
+  int64_t ld_aux;
   int c_type;
   int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
                               // stored as 16-byte chunks / element by element, 4 / 5 staged fp32 rows
@@ -216,6 +219,19 @@ __device__ inline uint2 pack4(const float (&v)[4]) {
                f32_to_f16(v[2]) | (uint32_t(f32_to_f16(v[3])) << 16)};
 }
 
+// The GELU side output: bf16 gelu_tanh (mk_gelu_tanh's function) of stored
+// values -- a bf16 C chunk of 8 as stored (rounded), fp32 pairs as they are.
+__device__ inline uint32_t gelu2_bf16(float x0, float x1) {
+  return uint32_t(f32_to_bf16(gelu_tanh_f32(x0))) | (uint32_t(f32_to_bf16(gelu_tanh_f32(x1))) << 16);
+}
+__device__ inline u32x4_t gelu8_bf16(const u32x4_t& v) {
+  u32x4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    o[q] = gelu2_bf16(__builtin_bit_cast(float, v[q] << 16), __builtin_bit_cast(float, v[q] & 0xFFFF0000u));
+  return o;
+}
+
 // bias + ReLU on the 4 consecutive columns starting at n (bias read for
 // columns < N only)
 template <int CT>
@@ -298,11 +314,16 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
     const int64_t m = m0 + row, n = n0 + 8 * cn;
     if (m < p.M && n + 8 <= p.N) {
       *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
+      if (p.epilogue & kEpiGeluAux) *reinterpret_cast<u32x4_t*>(p.aux + m * p.ld_aux + n) = gelu8_bf16(v);
     } else if (m < p.M && n < p.N) {  // the chunk that straddles N: its columns below N only
       uint16_t* Ce = reinterpret_cast<uint16_t*>(Cz) + m * p.ldc + n;
+      const u32x4_t gv = gelu8_bf16(v);
 #pragma unroll
       for (int q = 0; q < 8; ++q)
-        if (n + q < p.N) Ce[q] = uint16_t(v[q / 2] >> (16 * (q & 1)));
+        if (n + q < p.N) {
+          Ce[q] = uint16_t(v[q / 2] >> (16 * (q & 1)));
+          if (p.epilogue & kEpiGeluAux) p.aux[m * p.ld_aux + n + q] = uint16_t(gv[q / 2] >> (16 * (q & 1)));
+        }
     }
   }
 }
@@ -364,10 +385,16 @@ __device__ __attribute__((always_inline)) inline void store_staged_f32(const Til
         const int64_t m = m0 + pass * kRP + row, n = n0 + 4 * cn;
         if (m < p.M && n + 4 <= p.N) {
           *reinterpret_cast<f32x4*>(Cz + m * p.ldc + n) = v;
+          if (p.epilogue & kEpiGeluAux)
+            *reinterpret_cast<uint2*>(p.aux + m * p.ld_aux + n) =
+                uint2{gelu2_bf16(v.v[0], v.v[1]), gelu2_bf16(v.v[2], v.v[3])};
         } else if (m < p.M && n < p.N) {  // the chunk that straddles N
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (n + q < p.N) Cz[m * p.ldc + n + q] = v.v[q];
+            if (n + q < p.N) {
+              Cz[m * p.ldc + n + q] = v.v[q];
+              if (p.epilogue & kEpiGeluAux) p.aux[m * p.ld_aux + n + q] = f32_to_bf16(gelu_tanh_f32(v.v[q]));
+            }
         }
       }
     } else {
@@ -612,7 +639,8 @@ int64_t span_bytes(bool kc, int64_t rows, int64_t K, int64_t ld) {
 // not fit the tiled kernel.
 bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
                 const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
-                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem) {
+                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem,
+                void* Y, int64_t y_ms) {
   if (M < 128 || N < 128 || K < 64) return false;
   if (k_rem < 0 || k_rem > K || (k_rem > 0 && (batch < 2 || K % 8 != 0))) return false;
   a_kc = a_ks == 1;
@@ -643,6 +671,16 @@ bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch,
   const bool rows16 = al16(C) && (batch == 1 || c_bs % 8 == 0) && c_ms % 8 == 0;
   const bool rows4 = al16(C) && (batch == 1 || c_bs % 4 == 0) && c_ms % 4 == 0;
   a.c_mode = c_type != MK_F32 ? (rows16 ? 2 : 3) : rows4 ? 5 : 4;
+  a.aux = static_cast<uint16_t*>(Y);
+  a.ld_aux = y_ms;
+  if (epilogue & kEpiGeluAux) {
+    // the side output goes out with C's whole chunks: 8 bf16 per bf16 C
+    // chunk, 4 per fp32 one, rows aligned to match
+    const uintptr_t ya = reinterpret_cast<uintptr_t>(Y);
+    const bool ok16 = c_type == MK_BF16 && a.c_mode == 2 && (ya & 15u) == 0 && y_ms % 8 == 0;
+    const bool ok32 = c_type == MK_F32 && a.c_mode == 5 && (ya & 7u) == 0 && y_ms % 4 == 0;
+    if (batch != 1 || !Y || y_ms < N || !(ok16 || ok32)) return false;
+  }
   return true;
 }
 
@@ -663,11 +701,12 @@ int64_t cu_count() {
 
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
-               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem) {
+               int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem,
+               void* Y, int64_t y_ms) {
   TiledGemm a;
   bool a_kc, b_kc;
   if (!tiled_args(a, a_kc, b_kc, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs, c_ms,
-                  bias, epilogue, k_rem))
+                  bias, epilogue, k_rem, Y, y_ms))
     return -1;
   // Kernel shape: the one with the least estimated time.  Each shape has a
   // throughput per CU measured on a large product (8192 x 8192 x 4096: 1240,

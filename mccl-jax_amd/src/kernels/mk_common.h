@@ -37,11 +37,14 @@ int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t
 // operand convention; returns -1 without launching when the shape, strides or
 // alignment do not fit it, else MK_OK or an MK_ERR_* code.  k_rem > 0: the
 // last batch contracts over its first k_rem k only (the last, shorter slice
-// of a split along K whose slices are K apart).
+// of a split along K whose slices are K apart).  epilogue | kEpiGeluAux: Y
+// (bf16, rows y_ms apart) also receives gelu_tanh of each stored C value
+// (batch 1, bf16 or fp32 C whose rows take whole 16-byte chunks).
+constexpr int kEpiGeluAux = 8;
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue,
-               int64_t k_rem = 0);
+               int64_t k_rem = 0, void* Y = nullptr, int64_t y_ms = 0);
 
 // Flash attention backward behind mk_sdpa_bwd for head_dim 64 / 128
 // (attention_bwd.hip); workspace: the per-row statistics.

@@ -789,6 +789,36 @@ def test_gemm_fp32_bias_bf16_out(K, relu):
         assert torch.equal(got, ref.bfloat16()), (M, N, Kd, splits)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemm_bias_gelu(K, out_dtype):
+    """mk_gemm_bias_gelu: C is mk_gemm's product + bias bit for bit, and Y is
+    mk_gelu_tanh of C as stored, rounded to bf16 (bit for bit), including the
+    chunk that straddles N (N = 1004 in rows padded to 1008)."""
+    rng = np.random.default_rng(77)
+    for (M, N, Kd, pitch) in [(8192, 3072, 768, 3072), (512, 1000, 256, 1000), (384, 1004, 192, 1008)]:
+        print(f"case: gemm_bias_gelu M={M} N={N} K={Kd} pitch={pitch} out={out_dtype}", flush=True)
+        a = dev_bf16(bf16.to_bf16_bits(rng.standard_normal((M, Kd)).astype(np.float32)))
+        # B's rows padded like C's (the tiled kernel's 16-byte aligned rows)
+        b = dev_bf16(bf16.to_bf16_bits((rng.standard_normal((Kd, pitch)) * 0.05).astype(np.float32)))[:, :N]
+        bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).cuda().to(out_dtype)
+        c = torch.full((M, pitch), float("nan"), dtype=out_dtype, device="cuda")
+        y = torch.full((M, pitch), float("nan"), dtype=torch.bfloat16, device="cuda")
+        K.gemm_bias_gelu(a, b, bias, out=c[:, :N], y=y[:, :N])
+        want_c = K.gemm(a, b, out_dtype=out_dtype, bias=bias)
+        assert torch.equal(c[:, :N], want_c)
+        want_y = K.gelu_tanh(want_c.contiguous())
+        assert torch.equal(y[:, :N], want_y.bfloat16())
+        if pitch > N:  # the padding columns stay untouched
+            assert torch.isnan(c[:, N:].float()).all() and torch.isnan(y[:, N:].float()).all()
+
+
+def test_gemm_bias_gelu_needs_the_tiled_kernel(K):
+    a = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
+    b = torch.zeros(64, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(Exception, match="mk_gemm_bias_gelu"):
+        K.gemm_bias_gelu(a, b)
+
+
 # ------------------------------------------------------------------ a6 iota, a12 layout, misc
 def test_iota_convert_fill_copy(K):
     it = K.iota((3, 5, 7), 1).cpu().numpy()

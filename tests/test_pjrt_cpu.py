@@ -155,6 +155,10 @@ def test_compile_jitted_training_step(client):
     # operands): written in bf16 by its epilogue, no conversion pass
     assert plan.count("] gemm (1x256x384x128 -> bf16)") == 2
     assert "convert chain (1 instr, 1 inputs), 3 independent instances" not in plan
+    # the MLP's up-projection (+ bias) writes the bf16 GELU of its result as
+    # a side output: the forward GELU chain is not a step of its own
+    assert plan.count("pattern gemm+bias+gelu(bf16 side output)") == 2
+    assert plan.count("] gemm (1x256x512x128 + gelu side output)") == 2
 
 
 def test_layernorm_train_needs_its_whole_backward(client):
