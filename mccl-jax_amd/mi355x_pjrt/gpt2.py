@@ -337,12 +337,18 @@ class GPT2TrainStep:
                                                  _F(scale), _I(1), P(self.lse[l])], "mk_sdpa_fwd"))
             gemm(BF16, BF16, T, d, d, P(self.att[l]), d, 1, W(p + "w_o"), d, 1, P(self.tmp), d, tag="o")
             add_layernorm(P(self.x[l]), P(self.tmp), W(p + "b_o"), p + "ln2", P(self.xm[l]), P(self.h2[l]))
-            # the up-projection, its bias and the GELU in one launch: f = h2 w_fc + b_fc
-            # (kept for the backward) and g = gelu_tanh(f) from the epilogue
-            calls.append(_Call(lib.mk_gemm_bias_gelu, [st, _I(BF16), _I(BF16), _I64(T), _I64(F), _I64(d),
-                                                       P(self.h2[l]), _I64(d), _I64(1), W(p + "w_fc"), _I64(F),
-                                                       _I64(1), P(self.f[l]), _I64(F), W(p + "b_fc"), _I(1),
-                                                       P(self.g[l]), _I64(F)], "mk_gemm_bias_gelu fc"))
+            if T >= 128 and F >= 128 and d >= 64 and F % 8 == 0 and d % 8 == 0:
+                # the up-projection, its bias and the GELU in one launch (the tiled
+                # kernel's shapes): f = h2 w_fc + b_fc, kept for the backward, and
+                # g = gelu_tanh(f) from the epilogue
+                calls.append(_Call(lib.mk_gemm_bias_gelu, [st, _I(BF16), _I(BF16), _I64(T), _I64(F), _I64(d),
+                                                           P(self.h2[l]), _I64(d), _I64(1), W(p + "w_fc"), _I64(F),
+                                                           _I64(1), P(self.f[l]), _I64(F), W(p + "b_fc"), _I(1),
+                                                           P(self.g[l]), _I64(F)], "mk_gemm_bias_gelu fc"))
+            else:
+                gemm(BF16, BF16, T, F, d, P(self.h2[l]), d, 1, W(p + "w_fc"), F, 1, P(self.f[l]), F, tag="fc")
+                calls.append(_Call(lib.mk_bias_gelu, [st, _I64(T), _I64(F), P(self.f[l]), W(p + "b_fc"),
+                                                      P(self.f[l]), P(self.g[l])], "mk_bias_gelu"))
             gemm(BF16, BF16, T, d, F, P(self.g[l]), F, 1, W(p + "w_pr"), d, 1, P(self.tmp), d, tag="proj")
             nxt, y = (f"h{l + 1}.ln1", P(self.h1[l + 1])) if l + 1 < L else ("lnf", P(self.hf))
             add_layernorm(P(self.xm[l]), P(self.tmp), W(p + "b_pr"), nxt, P(self.x[l + 1]), y)
