@@ -83,6 +83,22 @@ int mk_gemm_bias_gelu(void* stream, int ab_type, int c_type, int64_t M, int64_t 
                       int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* C,
                       int64_t c_ms, const void* bias, int epilogue, void* Y, int64_t y_ms);
 
+/* The MLP's backward through its activation in the product that forms the
+ * incoming gradient: D = A·B (bf16 operands, fp32 accumulate, rounded to
+ * bf16 as mk_gemm stores it), dx = bf16(D * gelu_tanh'(pre)) (the function
+ * of mk_gelu_tanh_bwd) with pre the bf16 pre-activations (rows pre_ms
+ * apart), and dx_colsum[c] = sum_r dx[r][c] over the stored dx (fp32, rows
+ * in a fixed order: deterministic) -- the dot_general, the GELU backward
+ * chain and the bias gradient's reduce (linalg.mm:47-105, elementwise.mm,
+ * reduce.mm:97-106) in one pass plus a small column pass.  Runs only on the
+ * tiled kernel: M, N >= 128, K >= 64, 16-byte aligned operand, dx and pre
+ * rows (MK_ERR_UNSUPPORTED otherwise).  Workspace:
+ * mk_gemm_gelu_bwd_workspace_bytes(M, N). */
+size_t mk_gemm_gelu_bwd_workspace_bytes(int64_t M, int64_t N);
+int mk_gemm_gelu_bwd(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_ms,
+                     int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* dx, int64_t dx_ms,
+                     const void* pre, int64_t pre_ms, float* dx_colsum, void* workspace);
+
 /* Split-K form of mk_gemm for fp32 outputs with few output tiles and a long
  * contraction (the weight gradients dW = Xᵀ dY of the training step: the
  * dot_general of linalg.mm:47-105 with the token axis contracted).  The K

@@ -51,6 +51,8 @@ SIGNATURES = {
     "mk_layernorm_typed": (_I, [_P, _I, _I, _I64, _I64, _P, _P, _P, _F, _P]),
     "mk_gemm_bias_gelu": (_I, [_P, _I, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I, _P,
                                _I64]),
+    "mk_gemm_gelu_bwd_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "mk_gemm_gelu_bwd": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),
     "mk_add_layernorm_typed": (_I, [_P, _I, _I, _I64, _I64, _P, _P, _P, _P, _P, _F, _P, _P]),
     "mk_gelu_tanh": (_I, [_P, _I, _I64, _P, _P]),
     "mk_ew_program": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _I, _I, _I, _P]),

@@ -146,6 +146,13 @@ class GPT2TrainStep:
     # slices; TFLOP/s dw_o 102/179/281/294/260, dw_qkv 304/493/596/462/315,
     # dw_fc and dw_pr 415/593/621/514/367).
     DW_SPLITS = {"dw_o": 8, "dw_qkv": 4, "dw_fc": 4, "dw_pr": 4}
+    # the MLP's GELU forward / backward in the epilogues of its products
+    # (mk_gemm_bias_gelu / mk_gemm_gelu_bwd) rather than separate passes.
+    # Same-process A/B of the step (ms): separate 12.94, forward fused 12.86,
+    # both 12.92, backward only 13.00 -- the backward's epilogue (reading the
+    # pre-activations, the column pass) costs more than the pass it replaces
+    FUSE_GELU_FWD = True
+    FUSE_GELU_BWD = False
     # the hidden-state gradient through the embedding (K = vocabulary): bf16
     # out, split along K in uneven slices (measured: 8 slices 664 us, 2 693,
     # unsplit 910; rocBLAS 682-687)
@@ -241,7 +248,7 @@ class GPT2TrainStep:
         sk.append(lib.mk_gemm_splitk_workspace_bytes(c.d_ff, d, self.DW_SPLITS.get("dw_pr", 1)))
         sk.append(lib.mk_gemm_splitk_workspace_bytes(T, d, self.DHF_SPLITS))
         ws = max(*sk, lib.mk_col_sum_workspace_bytes(T, c.d_ff), lib.mk_col_sum_workspace_bytes(c.batch, c.seq * d),
-                 lib.mk_layernorm_bwd_workspace_bytes(T, d),
+                 lib.mk_layernorm_bwd_workspace_bytes(T, d), lib.mk_gemm_gelu_bwd_workspace_bytes(T, c.d_ff),
                  lib.mk_sdpa_bwd_workspace_bytes(c.batch, c.n_head, c.seq, c.seq, c.d_model // c.n_head),
                  lib.mk_scatter_add_workspace_bytes(c.vocab, T))
         self.ws = torch.empty(int(ws), dtype=torch.uint8, device=dev)
@@ -317,6 +324,9 @@ class GPT2TrainStep:
                                "mk_layernorm_bwd"))
 
         scale = 1.0 / math.sqrt(hd)
+        # the MLP's products can take the GELU in their epilogues where the
+        # tiled kernel takes the shapes (16-byte aligned rows, M, N >= 128, K >= 64)
+        tiled_mlp = T >= 128 and F >= 128 and d >= 64 and F % 8 == 0 and d % 8 == 0
         # ---- forward
         calls.append(_Call(lib.mk_gather_rows, [st, _I64(V), _I64(d * 2), W("wte"), _I(S32), _I64(T),
                                                 P(self.ids), P(self.x[0])], "mk_gather_rows"))
@@ -337,7 +347,7 @@ class GPT2TrainStep:
                                                  _F(scale), _I(1), P(self.lse[l])], "mk_sdpa_fwd"))
             gemm(BF16, BF16, T, d, d, P(self.att[l]), d, 1, W(p + "w_o"), d, 1, P(self.tmp), d, tag="o")
             add_layernorm(P(self.x[l]), P(self.tmp), W(p + "b_o"), p + "ln2", P(self.xm[l]), P(self.h2[l]))
-            if T >= 128 and F >= 128 and d >= 64 and F % 8 == 0 and d % 8 == 0:
+            if tiled_mlp and self.FUSE_GELU_FWD:
                 # the up-projection, its bias and the GELU in one launch (the tiled
                 # kernel's shapes): f = h2 w_fc + b_fc, kept for the backward, and
                 # g = gelu_tanh(f) from the epilogue
@@ -373,10 +383,18 @@ class GPT2TrainStep:
             p = f"h{l}."
             # MLP branch of x[l+1] = xm + proj(gelu(fc(ln2(xm))))
             gemm(BF16, F32, F, d, T, P(self.g[l]), 1, F, P(self.dx), d, 1, G(p + "w_pr"), d, tag="dw_pr")
-            gemm(BF16, BF16, T, F, d, P(self.dx), d, 1, W(p + "w_pr"), 1, d, P(self.dff), F, tag="dg")
-            calls.append(_Call(lib.mk_gelu_tanh_bwd_colsum, [st, _I(BF16), _I64(T), _I64(F), P(self.f[l]),
-                                                             P(self.dff), P(self.dff), G(p + "b_fc"), ws],
-                               "mk_gelu_tanh_bwd_colsum"))
+            if tiled_mlp and self.FUSE_GELU_BWD:
+                # dff = gelu'(f) * (dx w_prᵀ) and the fc bias gradient, the GELU
+                # backward in the product's epilogue
+                calls.append(_Call(lib.mk_gemm_gelu_bwd, [st, _I(BF16), _I64(T), _I64(F), _I64(d), P(self.dx), _I64(d),
+                                                          _I64(1), W(p + "w_pr"), _I64(1), _I64(d), P(self.dff),
+                                                          _I64(F), P(self.f[l]), _I64(F), G(p + "b_fc"), ws],
+                                   "mk_gemm_gelu_bwd dg"))
+            else:
+                gemm(BF16, BF16, T, F, d, P(self.dx), d, 1, W(p + "w_pr"), 1, d, P(self.dff), F, tag="dg")
+                calls.append(_Call(lib.mk_gelu_tanh_bwd_colsum, [st, _I(BF16), _I64(T), _I64(F), P(self.f[l]),
+                                                                 P(self.dff), P(self.dff), G(p + "b_fc"), ws],
+                                   "mk_gelu_tanh_bwd_colsum"))
             gemm(BF16, F32, d, F, T, P(self.h2[l]), 1, d, P(self.dff), F, 1, G(p + "w_fc"), F, tag="dw_fc")
             gemm(BF16, BF16, T, d, F, P(self.dff), F, 1, W(p + "w_fc"), 1, F, P(self.dh), d, tag="dh2")
             ln_bwd(P(self.xm[l]), p + "ln2_g", P(self.dh), P(self.dx), P(self.dx), p + "ln2", G(p + "b_o"))

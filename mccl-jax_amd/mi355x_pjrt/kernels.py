@@ -373,6 +373,23 @@ def gemm_bias_gelu(a, b, bias=None, out_dtype=torch.bfloat16, out=None, y=None, 
     return out, y
 
 
+def gemm_gelu_bwd(a, b, pre, out=None, workspace=None, stream=None):
+    """(dx, dx column sums): dx = bf16(bf16(a @ b) * gelu_tanh'(pre)) and its
+    fp32 column sums, one GEMM launch plus a column pass
+    (mk_gemm_gelu_bwd); a [M, K], b [K, N], pre [M, N] bf16 2-D views."""
+    _require_cuda(a, b, pre)
+    M, Kd = a.shape
+    N = b.shape[1]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device) if out is None else out
+    colsum = torch.empty(N, dtype=torch.float32, device=a.device)
+    ws = _ws(lib().mk_gemm_gelu_bwd_workspace_bytes(M, N), a.device, workspace)
+    rc = lib().mk_gemm_gelu_bwd(_stream(stream), mk_dtype(a.dtype), M, N, Kd, _ptr(a), a.stride(0), a.stride(1),
+                                _ptr(b), b.stride(0), b.stride(1), _ptr(out), out.stride(0), _ptr(pre), pre.stride(0),
+                                _ptr(colsum), _ptr(ws))
+    _check(rc, "mk_gemm_gelu_bwd")
+    return out, colsum
+
+
 def gemm_splitk(a, b, splits, out=None, workspace=None, stream=None, out_dtype=torch.float32, bias=None,
                 relu=False):
     """out = a @ b (+ bias)(ReLU) with the contraction cut into `splits`

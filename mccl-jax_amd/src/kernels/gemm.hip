@@ -269,6 +269,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
 // whatever C's type
 inline bool epilogue_ok(int e) { return e == 0 || e == 1 || e == 2 || e == 5 || e == 6; }
 
+// y[c] = sum of the nrows partial rows of column c, in row order
+__global__ __launch_bounds__(256) void colpart_sum_kernel(const float* __restrict__ part, int64_t nrows, int64_t cols,
+                                                          float* __restrict__ y) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int64_t r = 0; r < nrows; ++r) s += part[r * cols + c];
+  y[c] = s;
+}
+
 template <typename T>
 int launch_gemm(hipStream_t s, const GemmArgs& a, int64_t batch, bool a_kc, bool b_kc) {
   const int64_t tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
@@ -305,6 +315,33 @@ extern "C" int mk_gemm_bias_gelu(void* stream, int ab_type, int c_type, int64_t 
   return fail(MK_ERR_UNSUPPORTED,
               "mk_gemm_bias_gelu: needs the tiled kernel (bf16 operands with 16-byte aligned rows, M, N >= 128, "
               "K >= 64) and C and Y rows of whole 16-byte chunks");
+}
+
+extern "C" size_t mk_gemm_gelu_bwd_workspace_bytes(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  return size_t(((M + 127) / 128) * N * 4 + 255) & ~size_t(255);
+}
+
+extern "C" int mk_gemm_gelu_bwd(void* stream, int ab_type, int64_t M, int64_t N, int64_t K, const void* A,
+                                int64_t a_ms, int64_t a_ks, const void* B, int64_t b_ks, int64_t b_ns, void* dx,
+                                int64_t dx_ms, const void* pre, int64_t pre_ms, float* dx_colsum, void* workspace) {
+  clear_error();
+  if (M < 0 || N < 0 || K < 0) return fail(MK_ERR_INVALID, "mk_gemm_gelu_bwd: negative shape");
+  if (ab_type != MK_BF16) return fail(MK_ERR_UNSUPPORTED, "mk_gemm_gelu_bwd: ab_type must be bf16");
+  if (M == 0 || N == 0) return MK_OK;
+  if (!A || !B || !dx || !pre || !dx_colsum || !workspace) return fail(MK_ERR_INVALID, "mk_gemm_gelu_bwd: null pointer");
+  hipStream_t s = as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+  const int r = gemm_tiled(s, MK_BF16, 1, M, N, K, A, 0, a_ms, a_ks, B, 0, b_ks, b_ns, dx, 0, dx_ms, nullptr,
+                           kEpiGeluBwd, 0, const_cast<void*>(pre), pre_ms, part);
+  if (r < 0)
+    return fail(MK_ERR_UNSUPPORTED,
+                "mk_gemm_gelu_bwd: needs the tiled kernel (bf16 operands with 16-byte aligned rows, M, N >= 128, "
+                "K >= 64) and dx / pre rows of whole 16-byte chunks");
+  if (r != MK_OK) return r;
+  hipLaunchKernelGGL(colpart_sum_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, part, (M + 127) / 128, N,
+                     dx_colsum);
+  return check_launch("mk_gemm_gelu_bwd");
 }
 
 extern "C" int mk_gemm(void* stream, int ab_type, int c_type, int64_t batch, int64_t M, int64_t N,

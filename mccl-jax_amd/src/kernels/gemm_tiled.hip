@@ -76,6 +76,7 @@ struct TiledGemm {
                               // | kEpiGeluAux: aux = bf16 gelu_tanh of each stored value
   uint16_t* aux;
   int64_t ld_aux;
+  float* colpart;             // kEpiGeluBwd: column sums per 128 rows
   int c_type;
   int c_mode;                 // 0 element stores, 1 4-column vector stores, 2 / 3 staged 16-bit rows
                               // stored as 16-byte chunks / element by element, 4 / 5 staged fp32 rows
@@ -306,12 +307,36 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
     }
     return;
   }
+  const bool gelu_bwd = (p.epilogue & kEpiGeluBwd) != 0;
 #pragma unroll
   for (int it = 0; it < TM * kCpr / kThreads; ++it) {
     const int e = it * kThreads + int(threadIdx.x);
     const int row = e / kCpr, cn = e % kCpr;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * pos(row, cn));
+    u32x4_t v = *reinterpret_cast<const u32x4_t*>(st + row * TN + 8 * pos(row, cn));
     const int64_t m = m0 + row, n = n0 + 8 * cn;
+    if (gelu_bwd) {
+      // v (the product as stored) times gelu'(pre), pre read only inside
+      // [M, N); the chunk is written back for the column pass (zeros
+      // outside [M, N))
+      u32x4_t pre = {0u, 0u, 0u, 0u};
+      if (m < p.M && n + 8 <= p.N) {
+        pre = *reinterpret_cast<const u32x4_t*>(p.aux + m * p.ld_aux + n);
+      } else if (m < p.M && n < p.N) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (n + q < p.N) pre[q / 2] |= uint32_t(p.aux[m * p.ld_aux + n + q]) << (16 * (q & 1));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool in0 = m < p.M && n + 2 * q < p.N, in1 = m < p.M && n + 2 * q + 1 < p.N;
+        const float d0 = __builtin_bit_cast(float, v[q] << 16), d1 = __builtin_bit_cast(float, v[q] & 0xFFFF0000u);
+        const float x0 = __builtin_bit_cast(float, pre[q] << 16), x1 = __builtin_bit_cast(float, pre[q] & 0xFFFF0000u);
+        const uint32_t lo = in0 ? f32_to_bf16(d0 * gelu_tanh_grad_f32(x0)) : 0u;
+        const uint32_t hi = in1 ? f32_to_bf16(d1 * gelu_tanh_grad_f32(x1)) : 0u;
+        v[q] = lo | (hi << 16);
+      }
+      *reinterpret_cast<u32x4_t*>(st + row * TN + 8 * pos(row, cn)) = v;
+    }
     if (m < p.M && n + 8 <= p.N) {
       *reinterpret_cast<u32x4_t*>(Cz + 2 * (m * p.ldc + n)) = v;
       if (p.epilogue & kEpiGeluAux) *reinterpret_cast<u32x4_t*>(p.aux + m * p.ld_aux + n) = gelu8_bf16(v);
@@ -324,6 +349,21 @@ __device__ __attribute__((always_inline)) inline void store_staged(const TiledGe
           Ce[q] = uint16_t(v[q / 2] >> (16 * (q & 1)));
           if (p.epilogue & kEpiGeluAux) p.aux[m * p.ld_aux + n + q] = uint16_t(gv[q / 2] >> (16 * (q & 1)));
         }
+    }
+  }
+  if (gelu_bwd) {
+    // column sums of the stored values, 128 rows at a time in row order,
+    // into partial row (m0 + 128 h) / 128
+    lds_barrier();
+    for (int t = int(threadIdx.x); t < TN * (TM / 128); t += kThreads) {
+      const int col = t % TN, h = t / TN;
+      const int64_t n = n0 + col;
+      float sum = 0.f;
+      for (int row = 128 * h; row < 128 * h + 128; ++row) {
+        const uint16_t b = st[row * TN + 8 * pos(row, col >> 3) + (col & 7)];
+        sum += __builtin_bit_cast(float, uint32_t(b) << 16);
+      }
+      if (n < p.N && m0 + 128 * h < p.M) p.colpart[((m0 >> 7) + h) * p.N + n] = sum;
     }
   }
 }
@@ -640,7 +680,7 @@ int64_t span_bytes(bool kc, int64_t rows, int64_t K, int64_t ld) {
 bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K,
                 const void* A, int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
                 int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem,
-                void* Y, int64_t y_ms) {
+                void* Y, int64_t y_ms, float* colpart) {
   if (M < 128 || N < 128 || K < 64) return false;
   if (k_rem < 0 || k_rem > K || (k_rem > 0 && (batch < 2 || K % 8 != 0))) return false;
   a_kc = a_ks == 1;
@@ -681,6 +721,14 @@ bool tiled_args(TiledGemm& a, bool& a_kc, bool& b_kc, int c_type, int64_t batch,
     const bool ok32 = c_type == MK_F32 && a.c_mode == 5 && (ya & 7u) == 0 && y_ms % 4 == 0;
     if (batch != 1 || !Y || y_ms < N || !(ok16 || ok32)) return false;
   }
+  a.colpart = colpart;
+  if (epilogue & kEpiGeluBwd) {
+    // pre read in whole 16-byte chunks beside bf16 C's
+    const uintptr_t ya = reinterpret_cast<uintptr_t>(Y);
+    if ((epilogue & (kEpiGeluAux | 3)) || batch != 1 || c_type != MK_BF16 || a.c_mode != 2 || !Y || !colpart ||
+        (ya & 15u) != 0 || y_ms % 8 != 0 || y_ms < N)
+      return false;
+  }
   return true;
 }
 
@@ -702,11 +750,11 @@ int64_t cu_count() {
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue, int64_t k_rem,
-               void* Y, int64_t y_ms) {
+               void* Y, int64_t y_ms, float* colpart) {
   TiledGemm a;
   bool a_kc, b_kc;
   if (!tiled_args(a, a_kc, b_kc, c_type, batch, M, N, K, A, a_bs, a_ms, a_ks, B, b_bs, b_ks, b_ns, C, c_bs, c_ms,
-                  bias, epilogue, k_rem, Y, y_ms))
+                  bias, epilogue, k_rem, Y, y_ms, colpart))
     return -1;
   // Kernel shape: the one with the least estimated time.  Each shape has a
   // throughput per CU measured on a large product (8192 x 8192 x 4096: 1240,

@@ -40,11 +40,16 @@ int splitk_sum(hipStream_t s, const float* W, int64_t splits, int64_t M, int64_t
 // of a split along K whose slices are K apart).  epilogue | kEpiGeluAux: Y
 // (bf16, rows y_ms apart) also receives gelu_tanh of each stored C value
 // (batch 1, bf16 or fp32 C whose rows take whole 16-byte chunks).
+// epilogue | kEpiGeluBwd (bf16 C, batch 1): C = bf16(stored product *
+// gelu_tanh'(Y)) with Y the bf16 pre-activations (rows y_ms apart), and
+// colpart row r (N floats) = the column sums of rows 128 r .. 128 r + 127 of
+// the stored C (ceil(M / 128) rows).
 constexpr int kEpiGeluAux = 8;
+constexpr int kEpiGeluBwd = 16;
 int gemm_tiled(hipStream_t s, int c_type, int64_t batch, int64_t M, int64_t N, int64_t K, const void* A,
                int64_t a_bs, int64_t a_ms, int64_t a_ks, const void* B, int64_t b_bs, int64_t b_ks,
                int64_t b_ns, void* C, int64_t c_bs, int64_t c_ms, const void* bias, int epilogue,
-               int64_t k_rem = 0, void* Y = nullptr, int64_t y_ms = 0);
+               int64_t k_rem = 0, void* Y = nullptr, int64_t y_ms = 0, float* colpart = nullptr);
 
 // Flash attention backward behind mk_sdpa_bwd for head_dim 64 / 128
 // (attention_bwd.hip); workspace: the per-row statistics.
@@ -159,6 +164,17 @@ __device__ inline float gelu_tanh_f32(float x) {
   const float t = x * fmaf(x * x, kC1, kC0);
   const float e = exp2f(t);
   return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// gelu(x) = x * s, s = 1 / (1 + exp(-2u)), u = c (x + k x^3) (the forward's
+// form); gelu'(x) = s + x s (1 - s) 2c (1 + 3k x^2).
+__device__ inline float gelu_tanh_grad_f32(float x) {
+  constexpr float kC = 0.7978845608028654f, kK = 0.044715f;
+  constexpr float kC0 = -2.0f * kC * 1.4426950408889634f;
+  const float x2 = x * x;
+  const float e = exp2f(x * fmaf(x2, kC0 * kK, kC0));
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);
+  return s * fmaf(x * (1.0f - s), (2.0f * kC) * fmaf(3.0f * kK, x2, 1.0f), 1.0f);
 }
 
 // ---------------------------------------------------------------- wave64

@@ -36,16 +36,7 @@ template <> __device__ inline void stf<uint16_t>(uint16_t* p, int64_t i, float v
 inline int64_t align256(int64_t n) { return (n + 255) & ~int64_t(255); }
 
 // ---------------------------------------------------------------- GELU bwd
-// gelu(x) = x * s, s = 1 / (1 + exp(-2u)), u = c (x + k x^3) (the forward's
-// form); gelu'(x) = s + x s (1 - s) 2c (1 + 3k x^2).
-__device__ inline float gelu_tanh_grad_f32(float x) {
-  constexpr float kC = 0.7978845608028654f, kK = 0.044715f;
-  constexpr float kC0 = -2.0f * kC * 1.4426950408889634f;
-  const float x2 = x * x;
-  const float e = exp2f(x * fmaf(x2, kC0 * kK, kC0));
-  const float s = __builtin_amdgcn_rcpf(1.0f + e);
-  return s * fmaf(x * (1.0f - s), (2.0f * kC) * fmaf(3.0f * kK, x2, 1.0f), 1.0f);
-}
+// (gelu_tanh_grad_f32 in mk_common.h)
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void gelu_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,

@@ -812,6 +812,35 @@ def test_gemm_bias_gelu(K, out_dtype):
             assert torch.isnan(c[:, N:].float()).all() and torch.isnan(y[:, N:].float()).all()
 
 
+def test_gemm_gelu_bwd(K):
+    """mk_gemm_gelu_bwd: dx is mk_gelu_tanh_bwd(pre, mk_gemm's bf16 product)
+    bit for bit, including the chunk that straddles N (rows padded to 1008)
+    and the rows past the last whole tile; the column sums equal the float64
+    sums of the stored dx to fp32 rounding, bit for bit on repeat."""
+    rng = np.random.default_rng(78)
+    for (M, N, Kd, pitch, tb) in [(8192, 3072, 768, 3072, True), (300, 1000, 256, 1000, False),
+                                  (384, 1004, 192, 1008, True)]:
+        print(f"case: gemm_gelu_bwd M={M} N={N} K={Kd} pitch={pitch} b_kc={tb}", flush=True)
+        a = dev_bf16(bf16.to_bf16_bits(rng.standard_normal((M, Kd)).astype(np.float32)))
+        if tb:  # B read k-contiguous (the transposed weight of the step)
+            b = dev_bf16(bf16.to_bf16_bits((rng.standard_normal((pitch, Kd)) * 0.05).astype(np.float32)))[:N].t()
+        else:
+            b = dev_bf16(bf16.to_bf16_bits((rng.standard_normal((Kd, pitch)) * 0.05).astype(np.float32)))[:, :N]
+        pre = dev_bf16(bf16.to_bf16_bits((rng.standard_normal((M, pitch)) * 2).astype(np.float32)))[:, :N]
+        dx = torch.full((M, pitch), float("nan"), dtype=torch.bfloat16, device="cuda")
+        got, cs = K.gemm_gelu_bwd(a, b, pre, out=dx[:, :N])
+        dy = K.gemm(a, b, out_dtype=torch.bfloat16)
+        want = K.gelu_tanh_bwd(pre.contiguous(), dy.contiguous())
+        assert torch.equal(dx[:, :N], want)
+        if pitch > N:
+            assert torch.isnan(dx[:, N:].float()).all()
+        ref = dx[:, :N].double().sum(0)
+        scale = dx[:, :N].double().abs().sum(0)
+        assert float(((cs.double() - ref).abs() / (scale + 1e-30)).max()) < 1e-5
+        _, cs2 = K.gemm_gelu_bwd(a, b, pre, out=dx[:, :N])
+        assert torch.equal(cs, cs2)
+
+
 def test_gemm_bias_gelu_needs_the_tiled_kernel(K):
     a = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
     b = torch.zeros(64, 128, dtype=torch.bfloat16, device="cuda")
