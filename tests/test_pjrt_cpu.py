@@ -182,6 +182,24 @@ def test_layernorm_train_needs_its_whole_backward(client):
     assert plan.count("] layernorm (f32 -> bf16") == 2
 
 
+def test_gemm_gelu_side_output_needs_the_gelu(client):
+    """The up-projection's GELU side output is taken only for gelu_tanh
+    itself: with the cubic coefficient changed (0.044715 -> 0.05) in one
+    layer, that layer's product is written alone and its chain stays an
+    elementwise step; the other layer keeps the side output."""
+    from mi355x_pjrt import gpt2, train_hlo
+
+    cfg = gpt2.GPT2Config(n_layer=2, d_model=128, n_head=2, seq=128, batch=2, vocab=257)
+    text = train_hlo.gpt2_train_step(cfg)
+    cst = "dense<4.471500000e-02>"
+    assert text.count(cst) == 2
+    i = text.index(cst)
+    bad = text[:i] + "dense<5.000000000e-02>" + text[i + len(cst):]
+    plan, _, _ = _plan(client, bad)
+    assert plan.count("+ gelu side output") == 1
+    assert plan.count("pattern gemm+bias+gelu(bf16 side output)") == 1
+
+
 def test_sdpa_backward_needs_the_row_broadcast(client):
     """The attention backward matcher follows the row sums sum(dP * P) back to
     [B,H,Sq,Sk]: only a broadcast of the [B,H,Sq] axes onto dims {0,1,2}
