@@ -52,7 +52,7 @@ struct GemmArgs {
 // Stage one operand tile (ROWS x BK, element (row, k) = src[row*rs + k*ks])
 // into registers.  KC: the operand is k-contiguous (ks == 1); otherwise it
 // is row-contiguous (rs == 1).
-template <typename T, bool KC, int ROWS>
+template <typename T, bool KC, int ROWS, int NT = kThreads>
 struct TileLoader {
   using C = Cfg<T>;
   static constexpr int BK = C::BK, VEC = C::VEC;
@@ -60,8 +60,8 @@ struct TileLoader {
   // at one k, taken in pairs of k (bf16) so LDS writes are 32-bit.
   static constexpr int KPAIR = sizeof(T) == 2 ? 2 : 1;
   static constexpr int CHUNKS = KC ? ROWS * BK / VEC : (ROWS / VEC) * (BK / KPAIR);
-  static constexpr int PER_T = CHUNKS / kThreads;
-  static_assert(CHUNKS % kThreads == 0, "chunks must divide evenly");
+  static constexpr int PER_T = CHUNKS / NT;
+  static_assert(CHUNKS % NT == 0, "chunks must divide evenly");
   u32x4_t reg[PER_T][KPAIR];
 
   __device__ inline void load(const T* src, int64_t rs, int64_t ks, int64_t row0, int64_t rows,
@@ -73,7 +73,7 @@ struct TileLoader {
     if (vec && row0 + ROWS <= rows && k0 + BK <= K) {
 #pragma unroll
       for (int i = 0; i < PER_T; ++i) {
-        const int ch = threadIdx.x + i * kThreads;
+        const int ch = threadIdx.x + i * NT;
         if constexpr (KC) {
           const int r = ch / (BK / VEC), kc = (ch % (BK / VEC)) * VEC;
           reg[i][0] = *reinterpret_cast<const u32x4_t*>(src + (row0 + r) * rs + (k0 + kc));
@@ -88,7 +88,7 @@ struct TileLoader {
     }
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
-      const int ch = threadIdx.x + i * kThreads;
+      const int ch = threadIdx.x + i * NT;
       if constexpr (KC) {
         const int r = ch / (BK / VEC), kc = (ch % (BK / VEC)) * VEC;
         const int64_t gr = row0 + r, gk = k0 + kc;
@@ -131,7 +131,7 @@ struct TileLoader {
     constexpr int LS = C::LDS_STRIDE;
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
-      const int ch = threadIdx.x + i * kThreads;
+      const int ch = threadIdx.x + i * NT;
       if constexpr (KC) {
         const int r = ch / (BK / VEC), kc = (ch % (BK / VEC)) * VEC;
         if constexpr (sizeof(T) == 2) {
@@ -159,9 +159,14 @@ struct TileLoader {
   }
 };
 
-template <typename T, bool A_KC, bool B_KC>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
+// NW waves in an (NW / 2) x 2 arrangement: 4 waves of 64 x 64, or 8 waves of
+// 32 x 64 (the fp32 products, where one 4-wave workgroup per CU left each
+// SIMD a single wave to hide the loads behind).
+template <typename T, bool A_KC, bool B_KC, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_kernel(const GemmArgs p) {
   using C = Cfg<T>;
+  constexpr int NT = 64 * NW;
+  constexpr int MI = NW == 8 ? 1 : 2;  // 32-row MFMA blocks per wave
   constexpr int BK = C::BK, LS = C::LDS_STRIDE, KSTEP = C::KSTEP;
   __shared__ __attribute__((aligned(16))) T As[2][kBM * LS];
   __shared__ __attribute__((aligned(16))) T Bs[2][kBN * LS];
@@ -177,15 +182,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
   const int c = lane & 31, g = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
 
-  TileLoader<T, A_KC, kBM> la;
-  TileLoader<T, B_KC, kBN> lb;
+  TileLoader<T, A_KC, kBM, NT> la;
+  TileLoader<T, B_KC, kBN, NT> lb;
   // B element (n, k) = B[k*b_ks + n*b_ns]: rows are n
   const int64_t a_rs = p.a_ms, a_ks = p.a_ks;
   const int64_t b_rs = p.b_ns, b_ks = p.b_ks;
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -208,10 +213,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
 #pragma unroll
     for (int ks = 0; ks < BK; ks += KSTEP) {
       if constexpr (sizeof(T) == 2) {
-        bf16x8_t af[2], bfv[2];
+        bf16x8_t af[MI], bfv[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          u32x4_t v = *reinterpret_cast<const u32x4_t*>(&As[buf][(wm * 64 + i * 32 + c) * LS + ks + 8 * g]);
+        for (int i = 0; i < MI; ++i) {
+          u32x4_t v = *reinterpret_cast<const u32x4_t*>(&As[buf][(wm * 32 * MI + i * 32 + c) * LS + ks + 8 * g]);
           __builtin_memcpy(&af[i], &v, 16);
         }
 #pragma unroll
@@ -220,18 +225,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
           __builtin_memcpy(&bfv[j], &v, 16);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfv[j], acc[i][j], 0, 0, 0);
       } else {
-        float af[2], bfv[2];
+        float af[MI], bfv[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) af[i] = As[buf][(wm * 64 + i * 32 + c) * LS + ks + g];
+        for (int i = 0; i < MI; ++i) af[i] = As[buf][(wm * 32 * MI + i * 32 + c) * LS + ks + g];
 #pragma unroll
         for (int j = 0; j < 2; ++j) bfv[j] = Bs[buf][(wn * 64 + j * 32 + c) * LS + ks + g];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bfv[j], acc[i][j], 0, 0, 0);
@@ -249,10 +254,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const GemmArgs p) {
     float bias = 0.f;
     if (p.epilogue != 0) bias = load_as_f32(p.bias, n, (p.epilogue & 4) ? MK_F32 : p.c_type);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MI; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * g + (r % 4);
+        const int64_t m = m0 + wm * 32 * MI + i * 32 + 8 * (r / 4) + 4 * g + (r % 4);
         if (m >= p.M) continue;
         float v = acc[i][j][r];
         if (p.epilogue != 0) v += bias;
@@ -279,14 +284,17 @@ __global__ __launch_bounds__(256) void colpart_sum_kernel(const float* __restric
   y[c] = s;
 }
 
+// fp32 operands: 8 waves per workgroup (two per SIMD when one workgroup
+// holds a CU); bf16: 4
 template <typename T>
 int launch_gemm(hipStream_t s, const GemmArgs& a, int64_t batch, bool a_kc, bool b_kc) {
+  constexpr int NW = sizeof(T) == 4 ? 8 : 4;
   const int64_t tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
-  const dim3 g{unsigned(tiles), unsigned(batch)}, b{unsigned(kThreads)};
-  if (a_kc && b_kc) hipLaunchKernelGGL((gemm_kernel<T, true, true>), g, b, 0, s, a);
-  else if (a_kc && !b_kc) hipLaunchKernelGGL((gemm_kernel<T, true, false>), g, b, 0, s, a);
-  else if (!a_kc && b_kc) hipLaunchKernelGGL((gemm_kernel<T, false, true>), g, b, 0, s, a);
-  else hipLaunchKernelGGL((gemm_kernel<T, false, false>), g, b, 0, s, a);
+  const dim3 g{unsigned(tiles), unsigned(batch)}, b{unsigned(64 * NW)};
+  if (a_kc && b_kc) hipLaunchKernelGGL((gemm_kernel<T, true, true, NW>), g, b, 0, s, a);
+  else if (a_kc && !b_kc) hipLaunchKernelGGL((gemm_kernel<T, true, false, NW>), g, b, 0, s, a);
+  else if (!a_kc && b_kc) hipLaunchKernelGGL((gemm_kernel<T, false, true, NW>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((gemm_kernel<T, false, false, NW>), g, b, 0, s, a);
   return check_launch("mk_gemm");
 }
 
