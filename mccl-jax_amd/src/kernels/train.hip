@@ -889,14 +889,18 @@ __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_vec_ker
 #pragma unroll
     for (int j = 0; j < 4; ++j) m = fmaxf(m, x[i].v[j]);
   const float M = block_reduce(m, true);
+  // the exponentials are kept (in place of the logits) for the gradient
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sum += __builtin_amdgcn_exp2f((x[i].v[j] - M) * kL2e);
+    for (int j = 0; j < 4; ++j) {
+      x[i].v[j] = __builtin_amdgcn_exp2f((x[i].v[j] - M) * kL2e);
+      sum += x[i].v[j];
+    }
   const float S = block_reduce(sum, false);
   const float lse = M + __logf(S);
-  const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
+  const float inv_s = 1.f / S;
   if (t == 0 && loss) loss[row] = lab_ok ? lse - xlab : lse;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -905,7 +909,7 @@ __global__ __launch_bounds__(kXentF32Threads) void softmax_xent_f32_bf16_vec_ker
     float g[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float pr = __builtin_amdgcn_exp2f(fmaf(x[i].v[j] - M, kL2e, -ls2));
+      const float pr = x[i].v[j] * inv_s;
       g[j] = (4 * v + j == lab ? pr - 1.f : pr) * grad_scale;
     }
     if (v < nfull) {
