@@ -671,15 +671,21 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
   // exponents from x - max (exact at the max), so a row's largest p is
   // exactly 1 / S and a one-class row has p = 1, gradient 0
   const float M = block_reduce(m, true);
-  float sum = ej >= 0 ? __builtin_amdgcn_exp2f((ex - M) * kL2e) : 0.f;
+  // the exponentials are kept for the gradient (one exp per element)
+  const float eex = ej >= 0 ? __builtin_amdgcn_exp2f((ex - M) * kL2e) : 0.f;
+  float e[NVT][8];
+  float sum = eex;
 #pragma unroll
   for (int i = 0; i < NVT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      sum += __builtin_amdgcn_exp2f((lo16(v[i][j]) - M) * kL2e) + __builtin_amdgcn_exp2f((hi16(v[i][j]) - M) * kL2e);
+    for (int j = 0; j < 4; ++j) {
+      e[i][2 * j] = __builtin_amdgcn_exp2f((lo16(v[i][j]) - M) * kL2e);
+      e[i][2 * j + 1] = __builtin_amdgcn_exp2f((hi16(v[i][j]) - M) * kL2e);
+      sum += e[i][2 * j] + e[i][2 * j + 1];
+    }
   const float S = block_reduce(sum, false);
   const float lse = M + __logf(S);
-  const float ls2 = __builtin_amdgcn_logf(S);  // log2 S
+  const float inv_s = 1.f / S;
   if (t == 0 && loss) loss[row] = lab_ok ? lse - bf16_to_f32(xlab_bits) : lse;
   // gradient, from the registers (every read of the row is done: in place is safe)
   u32x4_t* dv = reinterpret_cast<u32x4_t*>(dr + head);
@@ -689,25 +695,19 @@ __global__ __launch_bounds__(kXentThreads) void softmax_xent_bf16_kernel(const u
     if (idx < nv) {
       u32x4_t o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(lo16(v[i][j]) - M, kL2e, -ls2));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(hi16(v[i][j]) - M, kL2e, -ls2));
-        o[j] = pack_bf16(p0 * grad_scale, p1 * grad_scale);
-      }
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack_bf16(e[i][2 * j] * inv_s * grad_scale, e[i][2 * j + 1] * inv_s * grad_scale);
       dv[idx] = o;
     }
   }
-  if (ej >= 0) {
-    const float p = __builtin_amdgcn_exp2f(fmaf(ex - M, kL2e, -ls2));
-    dr[ej] = f32_to_bf16(p * grad_scale);
-  }
+  if (ej >= 0) dr[ej] = f32_to_bf16(eex * inv_s * grad_scale);
   // the one-hot term touches one element: after every store above, thread 0
   // rewrites it as (p - 1) * grad_scale, p from the label's logit (the same
   // value and rounding as the element's own store)
   if (lab_ok) {
     __syncthreads();
     if (t == 0) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(bf16_to_f32(xlab_bits) - M, kL2e, -ls2)) - 1.f;
+      const float p = __builtin_amdgcn_exp2f((bf16_to_f32(xlab_bits) - M) * kL2e) * inv_s - 1.f;
       dr[lab] = f32_to_bf16(p * grad_scale);
     }
   }
